@@ -1,0 +1,837 @@
+/*
+ * aic_oracle.c -- CPU restatement of the AutonomousAICore TransformerLM training step.
+ *
+ * TEST INFRASTRUCTURE ONLY (see aic_oracle.h).  Built with -ffp-contract=off so that the
+ * only fused multiply-adds are the explicit AVX2 ones of the GEMM microkernel, as in the
+ * reference (src/ops/cpu_gemm.cpp:20-62).  Reductions accumulate in double where the
+ * reference does (src/ops/cpu_ops.cpp:152-269, src/loss/cross_entropy.cpp:214-222,
+ * src/optim/clip_grad.cpp:25-32).
+ */
+#define _GNU_SOURCE
+#include "aic_oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+#include <unistd.h>
+
+static int g_threads = 0;
+
+void orc_set_threads(int n) { g_threads = n; }
+
+int orc_get_threads(void) {
+    if (g_threads > 0) return g_threads;
+    long hw = sysconf(_SC_NPROCESSORS_ONLN);
+    int n = hw <= 0 ? 4 : (int)hw;
+    if (n > 24) n = 24;  /* src/ops/cpu_gemm.cpp:143-146 */
+    return n;
+}
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+static void* xcalloc(size_t n, size_t sz) {
+    void* p = calloc(n ? n : 1, sz);
+    if (!p) abort();
+    return p;
+}
+
+/* ======================================================================================
+ * GEMM (src/ops/cpu_gemm.cpp)
+ * ====================================================================================== */
+
+/* 4x16 AVX2+FMA microkernel, accumulating into C (src/ops/cpu_gemm.cpp:20-62). */
+static void mk_4x16(int64_t kl, const float* a, int64_t lda, const float* b, int64_t ldb, float* c, int64_t ldc) {
+    __m256 c00 = _mm256_loadu_ps(c + 0 * ldc + 0), c01 = _mm256_loadu_ps(c + 0 * ldc + 8);
+    __m256 c10 = _mm256_loadu_ps(c + 1 * ldc + 0), c11 = _mm256_loadu_ps(c + 1 * ldc + 8);
+    __m256 c20 = _mm256_loadu_ps(c + 2 * ldc + 0), c21 = _mm256_loadu_ps(c + 2 * ldc + 8);
+    __m256 c30 = _mm256_loadu_ps(c + 3 * ldc + 0), c31 = _mm256_loadu_ps(c + 3 * ldc + 8);
+    for (int64_t p = 0; p < kl; ++p) {
+        __m256 b0 = _mm256_loadu_ps(b + p * ldb), b1 = _mm256_loadu_ps(b + p * ldb + 8);
+        __m256 a0 = _mm256_set1_ps(a[0 * lda + p]);
+        __m256 a1 = _mm256_set1_ps(a[1 * lda + p]);
+        __m256 a2 = _mm256_set1_ps(a[2 * lda + p]);
+        __m256 a3 = _mm256_set1_ps(a[3 * lda + p]);
+        c00 = _mm256_fmadd_ps(a0, b0, c00); c01 = _mm256_fmadd_ps(a0, b1, c01);
+        c10 = _mm256_fmadd_ps(a1, b0, c10); c11 = _mm256_fmadd_ps(a1, b1, c11);
+        c20 = _mm256_fmadd_ps(a2, b0, c20); c21 = _mm256_fmadd_ps(a2, b1, c21);
+        c30 = _mm256_fmadd_ps(a3, b0, c30); c31 = _mm256_fmadd_ps(a3, b1, c31);
+    }
+    _mm256_storeu_ps(c + 0 * ldc, c00); _mm256_storeu_ps(c + 0 * ldc + 8, c01);
+    _mm256_storeu_ps(c + 1 * ldc, c10); _mm256_storeu_ps(c + 1 * ldc + 8, c11);
+    _mm256_storeu_ps(c + 2 * ldc, c20); _mm256_storeu_ps(c + 2 * ldc + 8, c21);
+    _mm256_storeu_ps(c + 3 * ldc, c30); _mm256_storeu_ps(c + 3 * ldc + 8, c31);
+}
+
+/* 64x64 K/N tiling over rows [m0, m1) (src/ops/cpu_gemm.cpp:65-115). */
+static void block_tiled(int64_t m0, int64_t m1, int64_t N, int64_t K, const float* A, const float* B, float* C) {
+    const int64_t TN = 64, TK = 64;
+    for (int64_t kb = 0; kb < K; kb += TK) {
+        int64_t kl = (kb + TK <= K) ? TK : (K - kb);
+        for (int64_t nb = 0; nb < N; nb += TN) {
+            int64_t nl = (nb + TN <= N) ? TN : (N - nb);
+            int64_t m = m0;
+            for (; m + 4 <= m1; m += 4) {
+                int64_t n = nb;
+                for (; n + 16 <= nb + nl; n += 16)
+                    mk_4x16(kl, A + m * K + kb, K, B + kb * N + n, N, C + m * N + n, N);
+                for (; n < nb + nl; ++n) {
+                    for (int64_t sm = 0; sm < 4; ++sm) {
+                        float sum = 0.0f;
+                        for (int64_t p = 0; p < kl; ++p) sum += A[(m + sm) * K + kb + p] * B[(kb + p) * N + n];
+                        C[(m + sm) * N + n] += sum;
+                    }
+                }
+            }
+            for (; m < m1; ++m) {
+                for (int64_t n = nb; n < nb + nl; ++n) {
+                    float sum = 0.0f;
+                    for (int64_t p = 0; p < kl; ++p) sum += A[m * K + kb + p] * B[(kb + p) * N + n];
+                    C[m * N + n] += sum;
+                }
+            }
+        }
+    }
+}
+
+typedef struct {
+    int64_t m0, m1, N, K;
+    const float *A, *B;
+    float* C;
+} gemm_job;
+
+static void* gemm_worker(void* arg) {
+    gemm_job* j = (gemm_job*)arg;
+    block_tiled(j->m0, j->m1, j->N, j->K, j->A, j->B, j->C);
+    return NULL;
+}
+
+/* gemm_2d (src/ops/cpu_gemm.cpp:119-177): C zero-initialised, then a row split over
+ * min(hw, 24) threads, single-threaded for small problems. */
+void orc_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K) {
+    memset(C, 0, sizeof(float) * (size_t)(M * N));
+    if (M == 0 || N == 0 || K == 0) return;
+    int nt = orc_get_threads();
+    int64_t work = M * N * K;
+    if (M < (int64_t)nt * 4 || work < 64 * 64 * 64) nt = 1;
+    if (nt == 1) {
+        block_tiled(0, M, N, K, A, B, C);
+        return;
+    }
+    int64_t rpt = (M + nt - 1) / nt;
+    rpt = ((rpt + 3) / 4) * 4;
+    pthread_t th[64];
+    gemm_job jobs[64];
+    int launched = 0;
+    for (int t = 0; t < nt; ++t) {
+        int64_t m0 = t * rpt;
+        if (m0 >= M) break;
+        int64_t m1 = (m0 + rpt <= M) ? m0 + rpt : M;
+        jobs[t] = (gemm_job){m0, m1, N, K, A, B, C};
+        pthread_create(&th[t], NULL, gemm_worker, &jobs[t]);
+        ++launched;
+    }
+    for (int t = 0; t < launched; ++t) pthread_join(th[t], NULL);
+}
+
+static void transpose(const float* src, float* dst, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) dst[c * rows + r] = src[r * cols + c];
+}
+
+/* Linear forward: matmul(x, W^T) with W^T made contiguous, one gemm_2d per batch
+ * (include/nn/linear.hpp:31-41, src/ops/cpu_gemm.cpp:180-254). */
+void orc_linear_fwd(const float* x, const float* W, float* y, int64_t B, int64_t S, int64_t in, int64_t out) {
+    float* Wt = (float*)xcalloc((size_t)(in * out), sizeof(float));
+    transpose(W, Wt, out, in);
+    for (int64_t b = 0; b < B; ++b) orc_gemm(x + b * S * in, Wt, y + b * S * out, S, out, in);
+    free(Wt);
+}
+
+/* MatMulBackward of y = x . W^T (src/autograd/functions.cpp:254-273):
+ *   grad_a = matmul(g, W)            -> dx_b = dy_b . W            (per batch)
+ *   grad_b = matmul(x^T, g)          -> P_b = x_b^T . dy_b  [in,out]
+ *   reduce_gradient_for_broadcast    -> sum over b in double      (src/ops/cpu_ops.cpp:195-262)
+ *   TransposeBackward                -> dW = (sum_b P_b)^T [out,in]
+ * dW is accumulated (+=) into the caller's buffer, as AccumulateGrad adds to an existing
+ * gradient (src/autograd/node.cpp:31-46). */
+void orc_linear_bwd(const float* x, const float* W, const float* dy, float* dx, float* dW,
+                    int64_t B, int64_t S, int64_t in, int64_t out) {
+    if (dx) {
+        for (int64_t b = 0; b < B; ++b) orc_gemm(dy + b * S * out, W, dx + b * S * in, S, in, out);
+    }
+    if (dW) {
+        float* xt = (float*)xcalloc((size_t)(in * S), sizeof(float));
+        float* Pb = (float*)xcalloc((size_t)(in * out), sizeof(float));
+        double* acc = (double*)xcalloc((size_t)(in * out), sizeof(double));
+        for (int64_t b = 0; b < B; ++b) {
+            transpose(x + b * S * in, xt, S, in);
+            orc_gemm(xt, dy + b * S * out, Pb, in, out, S);
+            for (int64_t i = 0; i < in * out; ++i) acc[i] += (double)Pb[i];
+        }
+        for (int64_t i = 0; i < in; ++i)
+            for (int64_t o = 0; o < out; ++o) dW[o * in + i] += (float)acc[i * out + o];
+        free(acc);
+        free(Pb);
+        free(xt);
+    }
+}
+
+/* ======================================================================================
+ * RMSNorm (include/nn/rms_norm.hpp:18-34)
+ *   x2 = x*x; mean(x2,-1) in double -> float; rms = sqrt(mean + eps); y = (x / rms) * w
+ * ====================================================================================== */
+void orc_rmsnorm_fwd(const float* x, const float* w, float* y, float* rms, int64_t rows, int64_t d, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * d;
+        double acc = 0.0;
+        for (int64_t j = 0; j < d; ++j) {
+            float sq = xr[j] * xr[j];
+            acc += (double)sq;
+        }
+        float mean = (float)(acc / (double)d);
+        float rr = sqrtf(mean + eps);
+        if (rms) rms[r] = rr;
+        for (int64_t j = 0; j < d; ++j) {
+            float n = xr[j] / rr;
+            y[r * d + j] = n * w[j];
+        }
+    }
+}
+
+/* Closed-form gradient of the graph above (MulBackward, DivBackward, SqrtBackward,
+ * MeanBackward, src/autograd/functions.cpp:60-78,150-200):
+ *   dn = dy*w;  dx_j = dn_j/rms - x_j * sum_i(dn_i x_i) / (d rms^3);  dw_j += sum_rows dy_j x_j/rms
+ * dx is written (not accumulated); dw is accumulated. */
+void orc_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rms,
+                     float* dx, float* dw, int64_t rows, int64_t d) {
+    double* dwacc = dw ? (double*)xcalloc((size_t)d, sizeof(double)) : NULL;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * d;
+        const float* gr = dy + r * d;
+        float rr = rms[r];
+        double dot = 0.0;
+        for (int64_t j = 0; j < d; ++j) dot += (double)(gr[j] * w[j]) * (double)xr[j];
+        float coef = (float)(dot / ((double)d * (double)rr * (double)rr * (double)rr));
+        if (dx)
+            for (int64_t j = 0; j < d; ++j) dx[r * d + j] = (gr[j] * w[j]) / rr - xr[j] * coef;
+        if (dwacc)
+            for (int64_t j = 0; j < d; ++j) dwacc[j] += (double)(gr[j] * (xr[j] / rr));
+    }
+    if (dw) {
+        for (int64_t j = 0; j < d; ++j) dw[j] += (float)dwacc[j];
+        free(dwacc);
+    }
+}
+
+/* ======================================================================================
+ * RoPE (include/nn/rope.hpp)
+ * ====================================================================================== */
+void orc_rope_tables(float* cos_t, float* sin_t, int64_t max_seq, int64_t hd, float base) {
+    int64_t half = hd / 2;
+    float* freqs = (float*)xcalloc((size_t)half, sizeof(float));
+    for (int64_t i = 0; i < half; ++i) {
+        float exponent = (float)(2 * i) / (float)hd;
+        freqs[i] = 1.0f / powf(base, exponent);
+    }
+    for (int64_t pos = 0; pos < max_seq; ++pos)
+        for (int64_t i = 0; i < half; ++i) {
+            float angle = (float)pos * freqs[i];
+            cos_t[pos * half + i] = cosf(angle);
+            sin_t[pos * half + i] = sinf(angle);
+        }
+    free(freqs);
+}
+
+/* x1' = x1*c - x2*s ; x2' = x1*s + x2*c (include/nn/rope.hpp:97-99). */
+void orc_rope_fwd(float* x, const float* cos_t, const float* sin_t, int64_t B, int64_t S, int64_t H,
+                  int64_t hd, int64_t start_pos) {
+    int64_t half = hd / 2;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s < S; ++s)
+            for (int64_t h = 0; h < H; ++h) {
+                float* row = x + ((b * S + s) * H + h) * hd;
+                const float* c = cos_t + (start_pos + s) * half;
+                const float* sn = sin_t + (start_pos + s) * half;
+                for (int64_t i = 0; i < half; ++i) {
+                    float x1 = row[i], x2 = row[i + half];
+                    float a = x1 * c[i], bb = x2 * sn[i];
+                    float r1 = a - bb;
+                    float e = x1 * sn[i], f = x2 * c[i];
+                    float r2 = e + f;
+                    row[i] = r1;
+                    row[i + half] = r2;
+                }
+            }
+}
+
+/* dx1 = g1*c + g2*s ; dx2 = g2*c - g1*s (include/nn/rope.hpp:23-39). */
+void orc_rope_bwd(float* g, const float* cos_t, const float* sin_t, int64_t B, int64_t S, int64_t H,
+                  int64_t hd, int64_t start_pos) {
+    int64_t half = hd / 2;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s < S; ++s)
+            for (int64_t h = 0; h < H; ++h) {
+                float* row = g + ((b * S + s) * H + h) * hd;
+                const float* c = cos_t + (start_pos + s) * half;
+                const float* sn = sin_t + (start_pos + s) * half;
+                for (int64_t i = 0; i < half; ++i) {
+                    float g1 = row[i], g2 = row[i + half];
+                    float a = g1 * c[i], bb = g2 * sn[i];
+                    float d1 = a + bb;
+                    float e = g2 * c[i], f = g1 * sn[i];
+                    float d2 = e - f;
+                    row[i] = d1;
+                    row[i + half] = d2;
+                }
+            }
+}
+
+/* ======================================================================================
+ * Attention core (include/nn/attention.hpp:84-119), per (b, h) head slice:
+ *   scores = gemm(q [S,hd], k^T [hd,S]); scores *= 1/sqrt(hd); scores += mask(-1e9, j > i);
+ *   softmax: m = rowmax; e = exp(s - m); sum in double -> float; P = e / sum;  o = gemm(P, v)
+ * ====================================================================================== */
+static void gather_head(const float* x, float* dst, int64_t b, int64_t h, int64_t S, int64_t H, int64_t hd) {
+    for (int64_t s = 0; s < S; ++s) memcpy(dst + s * hd, x + ((b * S + s) * H + h) * hd, sizeof(float) * (size_t)hd);
+}
+static void scatter_head(float* x, const float* src, int64_t b, int64_t h, int64_t S, int64_t H, int64_t hd) {
+    for (int64_t s = 0; s < S; ++s) memcpy(x + ((b * S + s) * H + h) * hd, src + s * hd, sizeof(float) * (size_t)hd);
+}
+
+void orc_attention_fwd(const float* q, const float* k, const float* v, float* o, float* E, float* rowsum,
+                       int64_t B, int64_t S, int64_t H, int64_t hd, int causal) {
+    float scale = 1.0f / sqrtf((float)hd);
+    float* qh = (float*)xcalloc((size_t)(S * hd), sizeof(float));
+    float* kh = (float*)xcalloc((size_t)(S * hd), sizeof(float));
+    float* kt = (float*)xcalloc((size_t)(S * hd), sizeof(float));
+    float* vh = (float*)xcalloc((size_t)(S * hd), sizeof(float));
+    float* oh = (float*)xcalloc((size_t)(S * hd), sizeof(float));
+    float* sc = (float*)xcalloc((size_t)(S * S), sizeof(float));
+    float* P = (float*)xcalloc((size_t)(S * S), sizeof(float));
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < H; ++h) {
+            gather_head(q, qh, b, h, S, H, hd);
+            gather_head(k, kh, b, h, S, H, hd);
+            gather_head(v, vh, b, h, S, H, hd);
+            transpose(kh, kt, S, hd);
+            orc_gemm(qh, kt, sc, S, S, hd);
+            float* Ebh = E ? E + (b * H + h) * S * S : NULL;
+            for (int64_t i = 0; i < S; ++i) {
+                float* row = sc + i * S;
+                for (int64_t j = 0; j < S; ++j) {
+                    row[j] = row[j] * scale;
+                    if (causal && S > 1 && j > i) row[j] = row[j] + (-1e9f);
+                }
+                float mx = row[0];
+                for (int64_t j = 1; j < S; ++j)
+                    if (row[j] > mx) mx = row[j];
+                double acc = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    float e = expf(row[j] - mx);
+                    row[j] = e;
+                    acc += (double)e;
+                }
+                float sm = (float)acc;
+                if (rowsum) rowsum[(b * H + h) * S + i] = sm;
+                for (int64_t j = 0; j < S; ++j) {
+                    if (Ebh) Ebh[i * S + j] = row[j];
+                    P[i * S + j] = row[j] / sm;
+                }
+            }
+            orc_gemm(P, vh, oh, S, hd, S);
+            scatter_head(o, oh, b, h, S, H, hd);
+        }
+    free(qh); free(kh); free(kt); free(vh); free(oh); free(sc); free(P);
+}
+
+/* Backward of the graph above.  For out = e / s (DivBackward then SumBackward then ExpBackward):
+ *   t_j = g_j / s ;  c = sum_k(-g_k e_k / (s*s)) in double ;  dscore_j = (t_j + c) * e_j
+ * then *scale, and the two MatMulBackwards. */
+void orc_attention_bwd(const float* q, const float* k, const float* v, const float* E, const float* rowsum,
+                       const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t S, int64_t H,
+                       int64_t hd) {
+    float scale = 1.0f / sqrtf((float)hd);
+    size_t sh = (size_t)(S * hd), ss = (size_t)(S * S);
+    float* qh = (float*)xcalloc(sh, sizeof(float));
+    float* qt = (float*)xcalloc(sh, sizeof(float));
+    float* kh = (float*)xcalloc(sh, sizeof(float));
+    float* vh = (float*)xcalloc(sh, sizeof(float));
+    float* vt = (float*)xcalloc(sh, sizeof(float));
+    float* gh = (float*)xcalloc(sh, sizeof(float));
+    float* tmp = (float*)xcalloc(sh, sizeof(float));
+    float* P = (float*)xcalloc(ss, sizeof(float));
+    float* Pt = (float*)xcalloc(ss, sizeof(float));
+    float* dP = (float*)xcalloc(ss, sizeof(float));
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < H; ++h) {
+            const float* Ebh = E + (b * H + h) * S * S;
+            const float* sbh = rowsum + (b * H + h) * S;
+            gather_head(q, qh, b, h, S, H, hd);
+            gather_head(k, kh, b, h, S, H, hd);
+            gather_head(v, vh, b, h, S, H, hd);
+            gather_head(dout, gh, b, h, S, H, hd);
+            for (int64_t i = 0; i < S; ++i)
+                for (int64_t j = 0; j < S; ++j) P[i * S + j] = Ebh[i * S + j] / sbh[i];
+            /* context = matmul(P, v): dP = g . v^T ; dv = P^T . g */
+            transpose(vh, vt, S, hd);
+            orc_gemm(gh, vt, dP, S, S, hd);
+            transpose(P, Pt, S, S);
+            orc_gemm(Pt, gh, tmp, S, hd, S);
+            scatter_head(dv, tmp, b, h, S, H, hd);
+            /* softmax backward */
+            for (int64_t i = 0; i < S; ++i) {
+                float s = sbh[i];
+                const float* e = Ebh + i * S;
+                float* g = dP + i * S;
+                double acc = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    float t = (-g[j]) * e[j];
+                    acc += (double)(t / (s * s));
+                }
+                float c = (float)acc;
+                for (int64_t j = 0; j < S; ++j) {
+                    float t = g[j] / s;
+                    g[j] = ((t + c) * e[j]) * scale;
+                }
+            }
+            /* scores = matmul(q, k^T): dq = dS . k ; d(k^T) = q^T . dS ; dk = transpose */
+            orc_gemm(dP, kh, tmp, S, hd, S);
+            scatter_head(dq, tmp, b, h, S, H, hd);
+            transpose(qh, qt, S, hd);
+            float* dkt = (float*)xcalloc(sh, sizeof(float));
+            orc_gemm(qt, dP, dkt, hd, S, S);
+            transpose(dkt, tmp, hd, S);
+            free(dkt);
+            scatter_head(dk, tmp, b, h, S, H, hd);
+        }
+    free(qh); free(qt); free(kh); free(vh); free(vt); free(gh); free(tmp); free(P); free(Pt); free(dP);
+}
+
+/* ======================================================================================
+ * SwiGLU activation
+ * ====================================================================================== */
+void orc_swiglu_fwd(const float* g, const float* u, float* h, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float x = g[i];
+        float a = x / (1.0f + expf(-x)); /* silu, src/ops/cpu_ops.cpp:143-146 */
+        h[i] = a * u[i];
+    }
+}
+
+void orc_swiglu_bwd(const float* g, const float* u, const float* dh, float* dg, float* du, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float x = g[i];
+        float a = x / (1.0f + expf(-x));
+        float s = 1.0f / (1.0f + expf(-x)); /* sigmoid, src/ops/cpu_ops.cpp:139-141 */
+        float dsilu = s * (1.0f + x * (1.0f - s));
+        du[i] = dh[i] * a;
+        dg[i] = (dh[i] * u[i]) * dsilu;
+    }
+}
+
+/* ======================================================================================
+ * Cross-entropy (src/loss/cross_entropy.cpp)
+ * ====================================================================================== */
+float orc_ce_fwd(const float* logits, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                 float* losses, float* lse_out, int64_t* valid_count) {
+    int64_t valid = 0;
+    double total = 0.0; /* sum(sample_losses) in double, src/ops/cpu_ops.cpp:152-162 */
+    for (int64_t i = 0; i < N; ++i) {
+        const float* z = logits + i * C;
+        float mx = z[0];
+        for (int64_t j = 1; j < C; ++j)
+            if (z[j] > mx) mx = z[j];
+        double se = 0.0;
+        for (int64_t j = 0; j < C; ++j) se += exp((double)(z[j] - mx));
+        float lse = (float)((double)mx + log(se > 1e-12 ? se : 1e-12));
+        if (lse_out) lse_out[i] = lse;
+        float li = 0.0f;
+        int64_t t = targets[i];
+        if (t != ignore_index) {
+            li = lse - z[t];
+            ++valid;
+        }
+        if (losses) losses[i] = li;
+        total += (double)li;
+    }
+    if (valid_count) *valid_count = valid;
+    if (valid == 0) return 0.0f;
+    float tot = (float)total;
+    return tot / (float)valid;
+}
+
+void orc_ce_bwd(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                int64_t ignore_index, int64_t valid_count, float g, float* dlogits) {
+    float scale = valid_count > 0 ? g / (float)valid_count : 0.0f;
+    for (int64_t i = 0; i < N; ++i) {
+        float* gz = dlogits + i * C;
+        int64_t t = targets[i];
+        if (t == ignore_index) {
+            memset(gz, 0, sizeof(float) * (size_t)C);
+            continue;
+        }
+        const float* z = logits + i * C;
+        for (int64_t j = 0; j < C; ++j) {
+            float prob = expf(z[j] - lse[i]);
+            float ind = (j == t) ? 1.0f : 0.0f;
+            gz[j] = (prob - ind) * scale;
+        }
+    }
+}
+
+/* ======================================================================================
+ * Embedding
+ * ====================================================================================== */
+void orc_embedding_fwd(const int64_t* ids, const float* W, float* out, int64_t N, int64_t D, int64_t V) {
+    for (int64_t i = 0; i < N; ++i) {
+        int64_t t = ids[i];
+        if (t >= 0 && t < V) memcpy(out + i * D, W + t * D, sizeof(float) * (size_t)D);
+        else memset(out + i * D, 0, sizeof(float) * (size_t)D);
+    }
+}
+
+/* Scatter-add in token order; accumulates into dW. */
+void orc_embedding_bwd(const int64_t* ids, const float* dout, float* dW, int64_t N, int64_t D, int64_t V) {
+    for (int64_t i = 0; i < N; ++i) {
+        int64_t t = ids[i];
+        if (t < 0 || t >= V) continue;
+        float* row = dW + t * D;
+        const float* g = dout + i * D;
+        for (int64_t d = 0; d < D; ++d) row[d] += g[d];
+    }
+}
+
+/* ======================================================================================
+ * Optimizer tail
+ * ====================================================================================== */
+void orc_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+               float eps, float wd, int64_t step) {
+    float bc1 = 1.0f - powf(beta1, (float)step);
+    float bc2 = 1.0f - powf(beta2, (float)step);
+    for (int64_t i = 0; i < n; ++i) {
+        float grad = g[i];
+        float param = p[i];
+        param -= lr * wd * param;
+        float mm = beta1 * m[i] + (1.0f - beta1) * grad;
+        float vv = beta2 * v[i] + (1.0f - beta2) * grad * grad;
+        m[i] = mm;
+        v[i] = vv;
+        float m_hat = mm / bc1;
+        float v_hat = vv / bc2;
+        param -= lr * (m_hat / (sqrtf(v_hat) + eps));
+        p[i] = param;
+    }
+}
+
+float orc_clip_grad_norm(float* const* grads, const int64_t* sizes, int64_t count, float max_norm) {
+    double tot = 0.0;
+    for (int64_t t = 0; t < count; ++t) {
+        double s = 0.0;
+        for (int64_t i = 0; i < sizes[t]; ++i) s += (double)grads[t][i] * (double)grads[t][i];
+        tot += s;
+    }
+    float norm = (float)sqrt(tot);
+    float coef = max_norm / (norm + 1e-6f);
+    if (coef < 1.0f)
+        for (int64_t t = 0; t < count; ++t)
+            for (int64_t i = 0; i < sizes[t]; ++i) grads[t][i] *= coef;
+    return norm;
+}
+
+void orc_scaler_init(orc_scaler* s, float initial_scale, float growth_factor, float backoff_factor,
+                     int growth_interval, float min_scale, float max_scale) {
+    s->initial_scale = initial_scale;
+    s->growth_factor = growth_factor;
+    s->backoff_factor = backoff_factor;
+    s->growth_interval = growth_interval;
+    s->min_scale = min_scale;
+    s->max_scale = max_scale;
+    s->scale = initial_scale;
+    s->good_steps = 0;
+    s->skipped_steps = 0;
+}
+
+int orc_scaler_unscale_and_update(orc_scaler* s, float* const* grads, const int64_t* sizes, int64_t count) {
+    for (int64_t t = 0; t < count; ++t)
+        for (int64_t i = 0; i < sizes[t]; ++i)
+            if (isnan(grads[t][i]) || isinf(grads[t][i])) {
+                float ns = s->scale * s->backoff_factor;
+                s->scale = ns > s->min_scale ? ns : s->min_scale;
+                s->good_steps = 0;
+                s->skipped_steps++;
+                return 0;
+            }
+    float inv = 1.0f / s->scale;
+    for (int64_t t = 0; t < count; ++t)
+        for (int64_t i = 0; i < sizes[t]; ++i) grads[t][i] *= inv;
+    s->good_steps++;
+    if (s->good_steps >= s->growth_interval) {
+        float ns = s->scale * s->growth_factor;
+        s->scale = ns < s->max_scale ? ns : s->max_scale;
+        s->good_steps = 0;
+    }
+    return 1;
+}
+
+/* ======================================================================================
+ * TransformerLM step (src/models/transformer_lm.cpp:50-62, include/nn/transformer_block.hpp:26-36,
+ * src/train/trainer.cpp:37-118 without the scheduler: lr is fixed)
+ * ====================================================================================== */
+typedef struct {
+    float *wq, *wk, *wv, *wo, *wg, *wu, *wd, *n1, *n2;
+} layer_ptrs;
+
+typedef struct {
+    float* emb;
+    layer_ptrs* layers;
+    float* normf;
+    float* head;
+} lm_ptrs;
+
+int64_t orc_lm_num_params(const orc_lm_config* c) {
+    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab;
+    int64_t per_layer = 4 * d * d + 3 * d * f + 2 * d;
+    return V * d + c->n_layers * per_layer + d + (c->tied ? 0 : V * d);
+}
+
+static lm_ptrs map_params(const orc_lm_config* c, float* base) {
+    lm_ptrs p;
+    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab;
+    float* cur = base;
+    p.emb = cur; cur += V * d;
+    p.layers = (layer_ptrs*)xcalloc((size_t)c->n_layers, sizeof(layer_ptrs));
+    for (int64_t l = 0; l < c->n_layers; ++l) {
+        layer_ptrs* L = &p.layers[l];
+        L->wq = cur; cur += d * d;
+        L->wk = cur; cur += d * d;
+        L->wv = cur; cur += d * d;
+        L->wo = cur; cur += d * d;
+        L->wg = cur; cur += f * d;
+        L->wu = cur; cur += f * d;
+        L->wd = cur; cur += d * f;
+        L->n1 = cur; cur += d;
+        L->n2 = cur; cur += d;
+    }
+    p.normf = cur; cur += d;
+    p.head = c->tied ? p.emb : cur;
+    return p;
+}
+
+typedef struct {
+    float *x, *h1, *r1, *q, *k, *v, *E, *rs, *ctx, *x1, *h2, *r2, *g, *u, *hm;
+} layer_acts;
+
+static void add_into(float* dst, const float* a, const float* b, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = a[i] + b[i];
+}
+
+/* Forward; returns logits [T, V] (caller frees) and fills acts when non-NULL. */
+static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t* ids, int64_t B, int64_t S,
+                         layer_acts* acts, float** hf_out, float** rf_out, float** xf_out,
+                         const float* cos_t, const float* sin_t, orc_step_result* res) {
+    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, H = c->n_heads, hd = d / H, T = B * S;
+    size_t Td = (size_t)(T * d), Tf = (size_t)(T * f);
+    double t0 = now_s();
+    float* x = (float*)xcalloc(Td, sizeof(float));
+    orc_embedding_fwd(ids, P->emb, x, T, d, V);
+    double t1 = now_s();
+    for (int64_t l = 0; l < c->n_layers; ++l) {
+        layer_ptrs* L = &P->layers[l];
+        float* h1 = (float*)xcalloc(Td, sizeof(float));
+        float* r1 = (float*)xcalloc((size_t)T, sizeof(float));
+        float* q = (float*)xcalloc(Td, sizeof(float));
+        float* k = (float*)xcalloc(Td, sizeof(float));
+        float* v = (float*)xcalloc(Td, sizeof(float));
+        float* ctx = (float*)xcalloc(Td, sizeof(float));
+        float* att = (float*)xcalloc(Td, sizeof(float));
+        float* x1 = (float*)xcalloc(Td, sizeof(float));
+        float* h2 = (float*)xcalloc(Td, sizeof(float));
+        float* r2 = (float*)xcalloc((size_t)T, sizeof(float));
+        float* g = (float*)xcalloc(Tf, sizeof(float));
+        float* u = (float*)xcalloc(Tf, sizeof(float));
+        float* hm = (float*)xcalloc(Tf, sizeof(float));
+        float* ffo = (float*)xcalloc(Td, sizeof(float));
+        float* E = acts ? (float*)xcalloc((size_t)(B * H * S * S), sizeof(float)) : NULL;
+        float* rs = acts ? (float*)xcalloc((size_t)(B * H * S), sizeof(float)) : NULL;
+
+        orc_rmsnorm_fwd(x, L->n1, h1, r1, T, d, c->norm_eps);
+        orc_linear_fwd(h1, L->wq, q, B, S, d, d);
+        orc_linear_fwd(h1, L->wk, k, B, S, d, d);
+        orc_linear_fwd(h1, L->wv, v, B, S, d, d);
+        orc_rope_fwd(q, cos_t, sin_t, B, S, H, hd, 0);
+        orc_rope_fwd(k, cos_t, sin_t, B, S, H, hd, 0);
+        orc_attention_fwd(q, k, v, ctx, E, rs, B, S, H, hd, 1);
+        orc_linear_fwd(ctx, L->wo, att, B, S, d, d);
+        add_into(x1, x, att, (int64_t)Td);
+        orc_rmsnorm_fwd(x1, L->n2, h2, r2, T, d, c->norm_eps);
+        orc_linear_fwd(h2, L->wg, g, B, S, d, f);
+        orc_linear_fwd(h2, L->wu, u, B, S, d, f);
+        orc_swiglu_fwd(g, u, hm, (int64_t)Tf);
+        orc_linear_fwd(hm, L->wd, ffo, B, S, f, d);
+        float* x2 = (float*)xcalloc(Td, sizeof(float));
+        add_into(x2, x1, ffo, (int64_t)Td);
+        free(att);
+        free(ffo);
+        if (acts) {
+            layer_acts* A = &acts[l];
+            A->x = x; A->h1 = h1; A->r1 = r1; A->q = q; A->k = k; A->v = v; A->E = E; A->rs = rs;
+            A->ctx = ctx; A->x1 = x1; A->h2 = h2; A->r2 = r2; A->g = g; A->u = u; A->hm = hm;
+        } else {
+            free(x); free(h1); free(r1); free(q); free(k); free(v); free(ctx); free(x1); free(h2);
+            free(r2); free(g); free(u); free(hm);
+        }
+        x = x2;
+    }
+    double t2 = now_s();
+    float* hf = (float*)xcalloc(Td, sizeof(float));
+    float* rf = (float*)xcalloc((size_t)T, sizeof(float));
+    orc_rmsnorm_fwd(x, P->normf, hf, rf, T, d, c->norm_eps);
+    float* logits = (float*)xcalloc((size_t)(T * V), sizeof(float));
+    orc_linear_fwd(hf, P->head, logits, B, S, d, V);
+    double t3 = now_s();
+    if (res) {
+        res->t_embed = t1 - t0;
+        res->t_blocks_fwd = t2 - t1;
+        res->t_head_fwd = t3 - t2;
+    }
+    if (hf_out) *hf_out = hf; else free(hf);
+    if (rf_out) *rf_out = rf; else free(rf);
+    if (xf_out) *xf_out = x; else free(x);
+    return logits;
+}
+
+float orc_lm_loss(const orc_lm_config* c, const float* params, const int64_t* ids, const int64_t* targets,
+                  int64_t B, int64_t S) {
+    lm_ptrs P = map_params(c, (float*)params);
+    int64_t hd = c->d_model / c->n_heads;
+    float* cos_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    orc_rope_tables(cos_t, sin_t, S, hd, c->rope_base);
+    float* logits = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL);
+    float loss = orc_ce_fwd(logits, targets, B * S, c->vocab, -100, NULL, NULL, NULL);
+    free(logits); free(cos_t); free(sin_t); free(P.layers);
+    return loss;
+}
+
+int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, float* v, int64_t* step_count,
+                const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* o,
+                orc_scaler* scaler, orc_step_result* res) {
+    orc_step_result local;
+    if (!res) res = &local;
+    memset(res, 0, sizeof(*res));
+    if (S > c->max_seq_len) return -1;
+    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, H = c->n_heads, hd = d / H, T = B * S;
+    size_t Td = (size_t)(T * d), Tf = (size_t)(T * f);
+    int64_t np = orc_lm_num_params(c);
+    lm_ptrs P = map_params(c, params);
+    memset(grads, 0, sizeof(float) * (size_t)np);
+    lm_ptrs G = map_params(c, grads);
+
+    float* cos_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    orc_rope_tables(cos_t, sin_t, S, hd, c->rope_base);
+
+    layer_acts* acts = (layer_acts*)xcalloc((size_t)c->n_layers, sizeof(layer_acts));
+    float *hf, *rf, *xf;
+    float* logits = lm_forward(c, &P, ids, B, S, acts, &hf, &rf, &xf, cos_t, sin_t, res);
+
+    /* loss */
+    double tl0 = now_s();
+    float* lse = (float*)xcalloc((size_t)T, sizeof(float));
+    int64_t valid = 0;
+    float loss = orc_ce_fwd(logits, targets, T, V, -100, NULL, lse, &valid);
+    res->loss = loss;
+    float gscale = 1.0f;
+    if (o->use_scaler && scaler) gscale = scaler->scale; /* scaler.scale(loss) = mul(loss, scale) */
+    res->loss_scale_used = gscale;
+    float* dlogits = (float*)xcalloc((size_t)(T * V), sizeof(float));
+    orc_ce_bwd(logits, targets, lse, T, V, -100, valid, gscale, dlogits);
+    free(logits);
+    double tl1 = now_s();
+    res->t_loss = tl1 - tl0;
+
+    /* head + final norm backward */
+    float* dh = (float*)xcalloc(Td, sizeof(float));
+    orc_linear_bwd(hf, P.head, dlogits, dh, G.head, B, S, d, V);
+    free(dlogits);
+    float* dx = (float*)xcalloc(Td, sizeof(float));
+    orc_rmsnorm_bwd(dh, xf, P.normf, rf, dx, G.normf, T, d);
+    double tl2 = now_s();
+    res->t_head_bwd = tl2 - tl1;
+
+    /* blocks backward */
+    float* tmp = (float*)xcalloc(Td, sizeof(float));
+    float* tmp2 = (float*)xcalloc(Td, sizeof(float));
+    float* dhm = (float*)xcalloc(Tf, sizeof(float));
+    float* dg = (float*)xcalloc(Tf, sizeof(float));
+    float* du = (float*)xcalloc(Tf, sizeof(float));
+    float* dq = (float*)xcalloc(Td, sizeof(float));
+    float* dk = (float*)xcalloc(Td, sizeof(float));
+    float* dv = (float*)xcalloc(Td, sizeof(float));
+    for (int64_t l = c->n_layers - 1; l >= 0; --l) {
+        layer_ptrs* L = &P.layers[l];
+        layer_ptrs* GL = &G.layers[l];
+        layer_acts* A = &acts[l];
+        /* x2 = x1 + down(hm): dx is grad of x2 */
+        orc_linear_bwd(A->hm, L->wd, dx, dhm, GL->wd, B, S, f, d);
+        orc_swiglu_bwd(A->g, A->u, dhm, dg, du, (int64_t)Tf);
+        orc_linear_bwd(A->h2, L->wg, dg, tmp, GL->wg, B, S, d, f);
+        orc_linear_bwd(A->h2, L->wu, du, tmp2, GL->wu, B, S, d, f);
+        add_into(tmp, tmp, tmp2, (int64_t)Td); /* grad of h2 (engine accumulation) */
+        orc_rmsnorm_bwd(tmp, A->x1, L->n2, A->r2, tmp2, GL->n2, T, d);
+        add_into(dx, dx, tmp2, (int64_t)Td); /* grad of x1 = residual + norm path */
+        /* x1 = x + out_proj(ctx) */
+        orc_linear_bwd(A->ctx, L->wo, dx, tmp, GL->wo, B, S, d, d);
+        orc_attention_bwd(A->q, A->k, A->v, A->E, A->rs, tmp, dq, dk, dv, B, S, H, hd);
+        orc_rope_bwd(dq, cos_t, sin_t, B, S, H, hd, 0);
+        orc_rope_bwd(dk, cos_t, sin_t, B, S, H, hd, 0);
+        orc_linear_bwd(A->h1, L->wq, dq, tmp, GL->wq, B, S, d, d);
+        orc_linear_bwd(A->h1, L->wk, dk, tmp2, GL->wk, B, S, d, d);
+        add_into(tmp, tmp, tmp2, (int64_t)Td);
+        orc_linear_bwd(A->h1, L->wv, dv, tmp2, GL->wv, B, S, d, d);
+        add_into(tmp, tmp, tmp2, (int64_t)Td);
+        orc_rmsnorm_bwd(tmp, A->x, L->n1, A->r1, tmp2, GL->n1, T, d);
+        add_into(dx, dx, tmp2, (int64_t)Td);
+        free(A->x); free(A->h1); free(A->r1); free(A->q); free(A->k); free(A->v); free(A->E); free(A->rs);
+        free(A->ctx); free(A->x1); free(A->h2); free(A->r2); free(A->g); free(A->u); free(A->hm);
+    }
+    double tl3 = now_s();
+    res->t_blocks_bwd = tl3 - tl2;
+    orc_embedding_bwd(ids, dx, G.emb, T, d, V);
+    double tl4 = now_s();
+    res->t_embed_bwd = tl4 - tl3;
+    free(tmp); free(tmp2); free(dhm); free(dg); free(du); free(dq); free(dk); free(dv); free(dx); free(dh);
+    free(hf); free(rf); free(xf); free(lse); free(acts); free(cos_t); free(sin_t);
+
+    /* optimizer tail: [scaler] -> clip -> AdamW (src/train/trainer.cpp:70-95) */
+    double to0 = now_s();
+    float* gp[1] = {grads};
+    int64_t gs[1] = {np};
+    int ok = 1;
+    if (o->use_scaler && scaler) ok = orc_scaler_unscale_and_update(scaler, gp, gs, 1);
+    res->found_inf = !ok;
+    if (ok) {
+        if (o->max_grad_norm > 0.0f) {
+            res->grad_norm = orc_clip_grad_norm(gp, gs, 1, o->max_grad_norm);
+        } else {
+            double s = 0.0;
+            for (int64_t i = 0; i < np; ++i) s += (double)grads[i] * (double)grads[i];
+            res->grad_norm = (float)sqrt(s);
+        }
+        if (o->do_update) {
+            *step_count += 1;
+            orc_adamw(params, grads, m, v, np, o->lr, o->beta1, o->beta2, o->eps, o->weight_decay, *step_count);
+        }
+    }
+    res->t_optim = now_s() - to0;
+    free(P.layers);
+    free(G.layers);
+    return 0;
+}

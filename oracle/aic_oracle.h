@@ -1,0 +1,169 @@
+/*
+ * aic_oracle.h -- CPU restatement of the AutonomousAICore TransformerLM training step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (autonomousaicore_amd/) links,
+ * imports or calls this library.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, and only as the checker or as the timed CPU
+ * baseline, never as the measured GPU path.
+ *
+ * Every function restates the reference's CPU algorithm (fp32 storage, fp32 GEMM with
+ * the AVX2 4x16 FMA microkernel, double-precision reductions) and cites the reference
+ * file:line it follows.  Paths are relative to /root/reference/AutonomousAICore/.
+ *
+ * Pinning (what checks each function against something other than itself):
+ *   orc_gemm              reference known answers (tests/unit/test_matmul.cpp:17-68)
+ *                         + numpy float64 matmul on random inputs
+ *   orc_rmsnorm_*         unit-RMS invariant (tests/unit/test_nn.cpp:58-81)
+ *                         + torch.nn.functional.rms_norm float64 fwd/autograd bwd
+ *   orc_rope_*            norm preservation + start_pos offset (tests/unit/test_nn.cpp:83-112),
+ *                         pos 0 == identity, bwd == inverse rotation, adjoint identity
+ *   orc_attention_*       torch scaled_dot_product_attention(is_causal) float64 + autograd
+ *   orc_swiglu_*          closed form silu(g)*u + torch autograd float64
+ *   orc_ce_*              0.407606 known answer (tests/unit/test_optim.cpp:16-36),
+ *                         +-1000 stability (:38-65), ignore_index zero rows (:101-129),
+ *                         torch cross_entropy float64 + autograd
+ *   orc_embedding_*       gather bit-equal + scatter counts (tests/unit/test_model.cpp:15-48)
+ *   orc_adamw             0.989 one-step answer (tests/unit/test_optim.cpp:209-237)
+ *                         + torch.optim.AdamW float64
+ *   orc_clip_grad_norm    sqrt(91) -> 5 (tests/unit/test_optim.cpp:191-207)
+ *   orc_scaler_*          sequences of tests/unit/test_amp.cpp:56-142
+ *   orc_lm_step           whole step vs an independent torch float64 model built from
+ *                         library routines (F.embedding, F.linear, F.rms_norm, SDPA,
+ *                         F.silu, F.cross_entropy, clip_grad_norm_, torch.optim.AdamW)
+ * The reference itself cannot be compiled here (include/tensor/tensor.hpp:135 is rejected
+ * by g++ 11 and clang 22), so no function is pinned against a reference binary.
+ */
+#ifndef AIC_ORACLE_H
+#define AIC_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- threading of the GEMM row split (src/ops/cpu_gemm.cpp:143-175: min(hw, 24)) ---- */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* ---- GEMM: C[M,N] = A[M,K] . B[K,N], all row-major contiguous (src/ops/cpu_gemm.cpp:119-177) ---- */
+void orc_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
+
+/* Linear y[T,out] = x[T,in] . W[out,in]^T, run per batch of S rows (include/nn/linear.hpp:31-41,
+ * src/ops/cpu_gemm.cpp:180-254). */
+void orc_linear_fwd(const float* x, const float* W, float* y, int64_t B, int64_t S, int64_t in, int64_t out);
+/* MatMulBackward (src/autograd/functions.cpp:254-273): dx = dy . W ; dW = sum_b x_b^T dy_b
+ * (batch sum in double, src/ops/cpu_ops.cpp:195-262).  Either output may be NULL. */
+void orc_linear_bwd(const float* x, const float* W, const float* dy, float* dx, float* dW,
+                    int64_t B, int64_t S, int64_t in, int64_t out);
+
+/* ---- RMSNorm (include/nn/rms_norm.hpp:18-34) ---- */
+void orc_rmsnorm_fwd(const float* x, const float* w, float* y, float* rms, int64_t rows, int64_t d, float eps);
+/* dx = dy*w/rms - x * sum(dy*w*x) / (d*rms^3); dw += sum_rows dy*x/rms (double). */
+void orc_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rms,
+                     float* dx, float* dw, int64_t rows, int64_t d);
+
+/* ---- RoPE, half-split, tables built like include/nn/rope.hpp:122-144 ---- */
+void orc_rope_tables(float* cos_t, float* sin_t, int64_t max_seq, int64_t hd, float base);
+/* x laid out [B, S, H, hd] (the [B,S,d] projection output); rotated in place,
+ * position of row s is start_pos + s (include/nn/rope.hpp:66-112). */
+void orc_rope_fwd(float* x, const float* cos_t, const float* sin_t, int64_t B, int64_t S, int64_t H,
+                  int64_t hd, int64_t start_pos);
+/* Adjoint rotation (include/nn/rope.hpp:23-39), in place. */
+void orc_rope_bwd(float* g, const float* cos_t, const float* sin_t, int64_t B, int64_t S, int64_t H,
+                  int64_t hd, int64_t start_pos);
+
+/* ---- causal self-attention core, default (materialised) path (include/nn/attention.hpp:84-119) ----
+ * q, k, v, o in [B, S, H, hd] layout.  E ([B,H,S,S]) receives exp(score - rowmax) and
+ * rowsum ([B,H,S]) the float row sums, which the backward needs (softmax = E / rowsum,
+ * src/ops/ops.cpp:460-471).  Both may be NULL when no backward follows. */
+void orc_attention_fwd(const float* q, const float* k, const float* v, float* o, float* E, float* rowsum,
+                       int64_t B, int64_t S, int64_t H, int64_t hd, int causal);
+/* Backward of the same graph: matmul, mul(scale), add(mask), max/sub/exp/sum/div, matmul
+ * (src/autograd/functions.cpp:60-78 Div, :150-170 Exp/Sum, :254-273 MatMul). */
+void orc_attention_bwd(const float* q, const float* k, const float* v, const float* E, const float* rowsum,
+                       const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t S, int64_t H,
+                       int64_t hd);
+
+/* ---- SwiGLU activation h = silu(g) * u (include/nn/swiglu.hpp:21-33, src/ops/cpu_ops.cpp:143-146) ---- */
+void orc_swiglu_fwd(const float* g, const float* u, float* h, int64_t n);
+/* SiluBackward s*(1+x*(1-s)) (src/autograd/functions.cpp:167-175) and MulBackward. */
+void orc_swiglu_bwd(const float* g, const float* u, const float* dh, float* dg, float* du, int64_t n);
+
+/* ---- cross-entropy with index targets (src/loss/cross_entropy.cpp:149-290) ----
+ * Returns the reduced loss ("mean" over valid rows); losses/lse may be NULL. */
+float orc_ce_fwd(const float* logits, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                 float* losses, float* lse, int64_t* valid_count);
+/* grad = (exp(z - lse) - onehot) * g / valid (src/loss/cross_entropy.cpp:77-127). */
+void orc_ce_bwd(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                int64_t ignore_index, int64_t valid_count, float g, float* dlogits);
+
+/* ---- Embedding (src/nn/embedding.cpp:96-156, :26-82) ---- */
+void orc_embedding_fwd(const int64_t* ids, const float* W, float* out, int64_t N, int64_t D, int64_t V);
+void orc_embedding_bwd(const int64_t* ids, const float* dout, float* dW, int64_t N, int64_t D, int64_t V);
+
+/* ---- optimizer tail ---- */
+/* AdamW::step for one tensor (src/optim/adamw.cpp:14-90); step = the incremented count. */
+void orc_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+               float eps, float wd, int64_t step);
+/* clip_grad_norm_ (src/optim/clip_grad.cpp:11-53) over `count` gradient buffers. */
+float orc_clip_grad_norm(float* const* grads, const int64_t* sizes, int64_t count, float max_norm);
+
+/* DynamicLossScaler (src/train/amp.cpp:50-152). */
+typedef struct {
+    float initial_scale, growth_factor, backoff_factor;
+    int growth_interval;
+    float min_scale, max_scale;
+    float scale;
+    int good_steps, skipped_steps;
+} orc_scaler;
+void orc_scaler_init(orc_scaler* s, float initial_scale, float growth_factor, float backoff_factor,
+                     int growth_interval, float min_scale, float max_scale);
+/* Returns 1 and unscales in place if every gradient is finite, else backs off and returns 0. */
+int orc_scaler_unscale_and_update(orc_scaler* s, float* const* grads, const int64_t* sizes, int64_t count);
+
+/* ---- whole TransformerLM training step ----
+ * Parameter layout of `params` (and of grads / m / v), one flat float buffer:
+ *   tok_embeddings.weight [V, d]
+ *   for each layer l: attn.q_proj [d,d], attn.k_proj [d,d], attn.v_proj [d,d], attn.out_proj [d,d],
+ *                     ffn.gate_proj [f,d], ffn.up_proj [f,d], ffn.down_proj [d,f],
+ *                     norm1.weight [d], norm2.weight [d]
+ *   norm.weight [d]
+ *   lm_head.weight [V, d]      (absent when tied: the head reuses tok_embeddings.weight)
+ */
+typedef struct {
+    int64_t vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len;
+    float norm_eps, rope_base;
+    int tied;
+} orc_lm_config;
+
+typedef struct {
+    float lr, beta1, beta2, eps, weight_decay;
+    float max_grad_norm;   /* <= 0: no clipping */
+    int use_scaler;        /* 1: loss scaling as Trainer::step with AMP (src/train/trainer.cpp:37-118) */
+    int do_update;         /* 0: stop after backward (grads only) */
+} orc_train_opts;
+
+typedef struct {
+    float loss;
+    float grad_norm;       /* pre-clip global L2 norm of the (unscaled) gradients */
+    int found_inf;         /* scaler found a non-finite gradient; the update was skipped */
+    float loss_scale_used;
+    double t_embed, t_blocks_fwd, t_head_fwd, t_loss, t_head_bwd, t_blocks_bwd, t_embed_bwd, t_optim; /* seconds */
+} orc_step_result;
+
+int64_t orc_lm_num_params(const orc_lm_config* cfg);
+/* Loss only (no grad), used for finite-difference checks. */
+float orc_lm_loss(const orc_lm_config* cfg, const float* params, const int64_t* ids, const int64_t* targets,
+                  int64_t B, int64_t S);
+/* One step: forward, cross_entropy(mean, ignore -100), backward, [scaler], clip, AdamW.
+ * grads receives the gradients seen by the optimizer (unscaled, post-clip).
+ * m/v/step_count: AdamW state; scaler may be NULL when opts->use_scaler == 0. */
+int orc_lm_step(const orc_lm_config* cfg, float* params, float* grads, float* m, float* v, int64_t* step_count,
+                const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* opts,
+                orc_scaler* scaler, orc_step_result* res);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,314 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The product
+package never imports it.  Each wrapper names the C function it calls; the C functions
+cite the reference file:line they restate.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+f32p = C.POINTER(C.c_float)
+i64p = C.POINTER(C.c_int64)
+
+
+class LMConfig(C.Structure):
+    _fields_ = [("vocab", C.c_int64), ("d_model", C.c_int64), ("n_layers", C.c_int64),
+                ("n_heads", C.c_int64), ("d_ffn", C.c_int64), ("max_seq_len", C.c_int64),
+                ("norm_eps", C.c_float), ("rope_base", C.c_float), ("tied", C.c_int)]
+
+
+class TrainOpts(C.Structure):
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("weight_decay", C.c_float), ("max_grad_norm", C.c_float), ("use_scaler", C.c_int),
+                ("do_update", C.c_int)]
+
+
+class StepResult(C.Structure):
+    _fields_ = [("loss", C.c_float), ("grad_norm", C.c_float), ("found_inf", C.c_int),
+                ("loss_scale_used", C.c_float), ("t_embed", C.c_double), ("t_blocks_fwd", C.c_double),
+                ("t_head_fwd", C.c_double), ("t_loss", C.c_double), ("t_head_bwd", C.c_double),
+                ("t_blocks_bwd", C.c_double), ("t_embed_bwd", C.c_double), ("t_optim", C.c_double)]
+
+
+class Scaler(C.Structure):
+    _fields_ = [("initial_scale", C.c_float), ("growth_factor", C.c_float), ("backoff_factor", C.c_float),
+                ("growth_interval", C.c_int), ("min_scale", C.c_float), ("max_scale", C.c_float),
+                ("scale", C.c_float), ("good_steps", C.c_int), ("skipped_steps", C.c_int)]
+
+
+def build() -> str:
+    """Compile liboracle.so with oracle/Makefile (gcc, AVX2+FMA)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        L.orc_ce_fwd.restype = C.c_float
+        L.orc_clip_grad_norm.restype = C.c_float
+        L.orc_lm_loss.restype = C.c_float
+        L.orc_lm_num_params.restype = C.c_int64
+        L.orc_get_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(f32p)
+
+
+def _i(a):
+    assert a.dtype == np.int64 and a.flags.c_contiguous
+    return a.ctypes.data_as(i64p)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def threads() -> int:
+    return lib().orc_get_threads()
+
+
+def gemm(A, B):
+    """orc_gemm: C = A @ B (fp32, reference AVX2 microkernel order)."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2
+    Cm = np.empty((M, N), np.float32)
+    lib().orc_gemm(_f(A), _f(B), _f(Cm), C.c_int64(M), C.c_int64(N), C.c_int64(K))
+    return Cm
+
+
+def linear_fwd(x, W, B, S):
+    x = np.ascontiguousarray(x, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    out, inn = W.shape
+    y = np.empty((B * S, out), np.float32)
+    lib().orc_linear_fwd(_f(x), _f(W), _f(y), C.c_int64(B), C.c_int64(S), C.c_int64(inn), C.c_int64(out))
+    return y
+
+
+def linear_bwd(x, W, dy, B, S):
+    x = np.ascontiguousarray(x, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    dy = np.ascontiguousarray(dy, np.float32)
+    out, inn = W.shape
+    dx = np.empty((B * S, inn), np.float32)
+    dW = np.zeros((out, inn), np.float32)
+    lib().orc_linear_bwd(_f(x), _f(W), _f(dy), _f(dx), _f(dW), C.c_int64(B), C.c_int64(S), C.c_int64(inn),
+                         C.c_int64(out))
+    return dx, dW
+
+
+def rmsnorm_fwd(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    rows, d = x.shape
+    y = np.empty_like(x)
+    rms = np.empty(rows, np.float32)
+    lib().orc_rmsnorm_fwd(_f(x), _f(w), _f(y), _f(rms), C.c_int64(rows), C.c_int64(d), C.c_float(eps))
+    return y, rms
+
+
+def rmsnorm_bwd(dy, x, w, rms):
+    dy = np.ascontiguousarray(dy, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, d = x.shape
+    dx = np.empty_like(x)
+    dw = np.zeros(d, np.float32)
+    lib().orc_rmsnorm_bwd(_f(dy), _f(x), _f(np.ascontiguousarray(w, np.float32)), _f(rms), _f(dx), _f(dw),
+                          C.c_int64(rows), C.c_int64(d))
+    return dx, dw
+
+
+def rope_tables(max_seq, hd, base=10000.0):
+    c = np.empty((max_seq, hd // 2), np.float32)
+    s = np.empty((max_seq, hd // 2), np.float32)
+    lib().orc_rope_tables(_f(c), _f(s), C.c_int64(max_seq), C.c_int64(hd), C.c_float(base))
+    return c, s
+
+
+def rope_fwd(x, B, S, H, hd, start_pos=0, base=10000.0):
+    """x: [B*S, H*hd]; returns the rotated copy."""
+    x = np.array(x, np.float32, copy=True, order="C")
+    c, s = rope_tables(start_pos + S, hd, base)
+    lib().orc_rope_fwd(_f(x), _f(c), _f(s), C.c_int64(B), C.c_int64(S), C.c_int64(H), C.c_int64(hd),
+                       C.c_int64(start_pos))
+    return x
+
+
+def rope_bwd(g, B, S, H, hd, start_pos=0, base=10000.0):
+    g = np.array(g, np.float32, copy=True, order="C")
+    c, s = rope_tables(start_pos + S, hd, base)
+    lib().orc_rope_bwd(_f(g), _f(c), _f(s), C.c_int64(B), C.c_int64(S), C.c_int64(H), C.c_int64(hd),
+                       C.c_int64(start_pos))
+    return g
+
+
+def attention_fwd(q, k, v, B, S, H, hd, causal=True, keep=True):
+    """q,k,v: [B*S, H*hd] (= [B,S,H,hd]).  Returns o and (E, rowsum) for the backward."""
+    q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+    o = np.empty_like(q)
+    E = np.empty((B, H, S, S), np.float32) if keep else None
+    rs = np.empty((B, H, S), np.float32) if keep else None
+    lib().orc_attention_fwd(_f(q), _f(k), _f(v), _f(o), _f(E) if keep else None, _f(rs) if keep else None,
+                            C.c_int64(B), C.c_int64(S), C.c_int64(H), C.c_int64(hd), C.c_int(1 if causal else 0))
+    return o, E, rs
+
+
+def attention_bwd(q, k, v, E, rs, do, B, S, H, hd):
+    q, k, v, do = (np.ascontiguousarray(t, np.float32) for t in (q, k, v, do))
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    lib().orc_attention_bwd(_f(q), _f(k), _f(v), _f(E), _f(rs), _f(do), _f(dq), _f(dk), _f(dv),
+                            C.c_int64(B), C.c_int64(S), C.c_int64(H), C.c_int64(hd))
+    return dq, dk, dv
+
+
+def swiglu_fwd(g, u):
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    h = np.empty_like(g)
+    lib().orc_swiglu_fwd(_f(g), _f(u), _f(h), C.c_int64(g.size))
+    return h
+
+
+def swiglu_bwd(g, u, dh):
+    g, u, dh = (np.ascontiguousarray(t, np.float32) for t in (g, u, dh))
+    dg, du = np.empty_like(g), np.empty_like(u)
+    lib().orc_swiglu_bwd(_f(g), _f(u), _f(dh), _f(dg), _f(du), C.c_int64(g.size))
+    return dg, du
+
+
+def ce_fwd(logits, targets, ignore_index=-100):
+    logits = np.ascontiguousarray(logits, np.float32)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, Cn = logits.shape
+    losses = np.empty(N, np.float32)
+    lse = np.empty(N, np.float32)
+    valid = C.c_int64(0)
+    loss = lib().orc_ce_fwd(_f(logits), _i(targets), C.c_int64(N), C.c_int64(Cn), C.c_int64(ignore_index),
+                            _f(losses), _f(lse), C.byref(valid))
+    return float(loss), losses, lse, int(valid.value)
+
+
+def ce_bwd(logits, targets, lse, valid, g=1.0, ignore_index=-100):
+    logits = np.ascontiguousarray(logits, np.float32)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, Cn = logits.shape
+    d = np.empty_like(logits)
+    lib().orc_ce_bwd(_f(logits), _i(targets), _f(np.ascontiguousarray(lse, np.float32)), C.c_int64(N),
+                     C.c_int64(Cn), C.c_int64(ignore_index), C.c_int64(valid), C.c_float(g), _f(d))
+    return d
+
+
+def embedding_fwd(ids, W):
+    ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
+    W = np.ascontiguousarray(W, np.float32)
+    V, D = W.shape
+    out = np.empty((ids.size, D), np.float32)
+    lib().orc_embedding_fwd(_i(ids), _f(W), _f(out), C.c_int64(ids.size), C.c_int64(D), C.c_int64(V))
+    return out
+
+
+def embedding_bwd(ids, dout, V):
+    ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
+    dout = np.ascontiguousarray(dout, np.float32)
+    D = dout.shape[1]
+    dW = np.zeros((V, D), np.float32)
+    lib().orc_embedding_bwd(_i(ids), _f(dout), _f(dW), C.c_int64(ids.size), C.c_int64(D), C.c_int64(V))
+    return dW
+
+
+def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step):
+    """In place on p, m, v (float32 arrays)."""
+    lib().orc_adamw(_f(p), _f(g), _f(m), _f(v), C.c_int64(p.size), C.c_float(lr), C.c_float(beta1),
+                    C.c_float(beta2), C.c_float(eps), C.c_float(wd), C.c_int64(step))
+
+
+def clip_grad_norm(grads, max_norm):
+    """In place on the list of float32 arrays; returns the pre-clip norm."""
+    n = len(grads)
+    ptrs = (f32p * n)(*[_f(g) for g in grads])
+    sizes = (C.c_int64 * n)(*[g.size for g in grads])
+    return float(lib().orc_clip_grad_norm(ptrs, sizes, C.c_int64(n), C.c_float(max_norm)))
+
+
+class LossScaler:
+    """orc_scaler_*: the reference DynamicLossScaler state machine."""
+
+    def __init__(self, initial_scale=65536.0, growth_factor=2.0, backoff_factor=0.5, growth_interval=1000,
+                 min_scale=1.0, max_scale=16777216.0):
+        self.s = Scaler()
+        lib().orc_scaler_init(C.byref(self.s), C.c_float(initial_scale), C.c_float(growth_factor),
+                              C.c_float(backoff_factor), C.c_int(growth_interval), C.c_float(min_scale),
+                              C.c_float(max_scale))
+
+    def unscale_and_update(self, grads):
+        n = len(grads)
+        ptrs = (f32p * n)(*[_f(g) for g in grads])
+        sizes = (C.c_int64 * n)(*[g.size for g in grads])
+        return bool(lib().orc_scaler_unscale_and_update(C.byref(self.s), ptrs, sizes, C.c_int64(n)))
+
+    @property
+    def scale(self):
+        return self.s.scale
+
+    @property
+    def good_steps(self):
+        return self.s.good_steps
+
+    @property
+    def skipped_steps(self):
+        return self.s.skipped_steps
+
+
+def make_config(vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len, norm_eps=1e-6, rope_base=10000.0,
+                tied=False):
+    return LMConfig(vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len, norm_eps, rope_base, 1 if tied else 0)
+
+
+def num_params(cfg: LMConfig) -> int:
+    return int(lib().orc_lm_num_params(C.byref(cfg)))
+
+
+def lm_loss(cfg, params, ids, targets, B, S):
+    return float(lib().orc_lm_loss(C.byref(cfg), _f(params), _i(np.ascontiguousarray(ids, np.int64)),
+                                   _i(np.ascontiguousarray(targets, np.int64)), C.c_int64(B), C.c_int64(S)))
+
+
+def lm_step(cfg, params, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1,
+            max_grad_norm=1.0, m=None, v=None, step=0, scaler: LossScaler | None = None, do_update=True):
+    """One training step in place on `params` (float32 flat).  Returns (result, grads, m, v, step)."""
+    n = num_params(cfg)
+    assert params.size == n and params.dtype == np.float32
+    grads = np.zeros(n, np.float32)
+    m = np.zeros(n, np.float32) if m is None else m
+    v = np.zeros(n, np.float32) if v is None else v
+    stepc = C.c_int64(step)
+    opts = TrainOpts(lr, beta1, beta2, eps, weight_decay, max_grad_norm, 1 if scaler else 0, 1 if do_update else 0)
+    res = StepResult()
+    rc = lib().orc_lm_step(C.byref(cfg), _f(params), _f(grads), _f(m), _f(v), C.byref(stepc),
+                           _i(np.ascontiguousarray(ids, np.int64)), _i(np.ascontiguousarray(targets, np.int64)),
+                           C.c_int64(B), C.c_int64(S), C.byref(opts), C.byref(scaler.s) if scaler else None,
+                           C.byref(res))
+    if rc != 0:
+        raise RuntimeError(f"orc_lm_step failed with {rc}")
+    return res, grads, m, v, int(stepc.value)

@@ -1,0 +1,346 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before any GPU result is compared with it.
+
+Each check compares the oracle with something other than itself: the reference's own
+known-answer tests (cited file:line under /root/reference/AutonomousAICore), a closed
+form or invariant, or an independent torch float64 implementation built from library
+routines.  CPU only.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests import torch_ref
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    nb = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (nb if nb > 0 else 1.0))
+
+
+# --------------------------------------------------------------------------- GEMM
+def test_gemm_known_answers(orc):
+    # tests/unit/test_matmul.cpp:17-37
+    a = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    b = np.array([[7, 8], [9, 1], [2, 3]], np.float32)
+    np.testing.assert_array_equal(orc.gemm(a, b), np.array([[31, 19], [85, 55]], np.float32))
+    # tests/unit/test_matmul.cpp:39-53 (SIMD remainders)
+    c = orc.gemm(np.ones((67, 79), np.float32), np.full((79, 83), 2.0, np.float32))
+    assert np.all(c == 158.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (5, 17, 3), (64, 128, 64), (130, 70, 200), (257, 33, 129)])
+def test_gemm_vs_float64(orc, M, N, K):
+    rng = np.random.default_rng(M * 1000 + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert rel(orc.gemm(A, B), ref) < 1e-6
+
+
+def test_gemm_threads_do_not_change_rows(orc):
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((256, 96)).astype(np.float32)
+    B = rng.standard_normal((96, 80)).astype(np.float32)
+    orc.set_threads(1)
+    c1 = orc.gemm(A, B)
+    orc.set_threads(8)
+    c8 = orc.gemm(A, B)
+    orc.set_threads(0)
+    np.testing.assert_array_equal(c1, c8)
+
+
+def test_linear_fwd_bwd_vs_torch(orc):
+    rng = np.random.default_rng(7)
+    B, S, i, o = 3, 20, 48, 36
+    x = rng.standard_normal((B * S, i)).astype(np.float32)
+    W = rng.standard_normal((o, i)).astype(np.float32)
+    dy = rng.standard_normal((B * S, o)).astype(np.float32)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    Wt = torch.tensor(W, dtype=torch.float64, requires_grad=True)
+    y = F.linear(xt, Wt)
+    y.backward(torch.tensor(dy, dtype=torch.float64))
+    assert rel(orc.linear_fwd(x, W, B, S), y.detach().numpy()) < 1e-6
+    dx, dW = orc.linear_bwd(x, W, dy, B, S)
+    assert rel(dx, xt.grad.numpy()) < 1e-6
+    assert rel(dW, Wt.grad.numpy()) < 1e-6
+
+
+# --------------------------------------------------------------------------- RMSNorm
+def test_rmsnorm_unit_rms(orc):
+    # tests/unit/test_nn.cpp:58-81
+    rng = np.random.default_rng(0)
+    x = (2.5 * rng.standard_normal((64, 64))).astype(np.float32)
+    y, _ = orc.rmsnorm_fwd(x, np.ones(64, np.float32), 1e-6)
+    assert np.allclose((y.astype(np.float64) ** 2).mean(-1), 1.0, atol=1e-3)
+
+
+def test_rmsnorm_vs_torch(orc):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((33, 96)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(96)).astype(np.float32)
+    dy = rng.standard_normal((33, 96)).astype(np.float32)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    yt = F.rms_norm(xt, (96,), wt, 1e-6)
+    yt.backward(torch.tensor(dy, dtype=torch.float64))
+    y, rms = orc.rmsnorm_fwd(x, w, 1e-6)
+    assert rel(y, yt.detach().numpy()) < 1e-6
+    dx, dw = orc.rmsnorm_bwd(dy, x, w, rms)
+    assert rel(dx, xt.grad.numpy()) < 1e-5
+    assert rel(dw, wt.grad.numpy()) < 1e-5
+
+
+# --------------------------------------------------------------------------- RoPE
+def test_rope_invariants(orc):
+    # tests/unit/test_nn.cpp:83-112: norm preservation and start_pos offset
+    rng = np.random.default_rng(2)
+    B, S, H, hd = 1, 8, 1, 16
+    x = rng.standard_normal((B * S, H * hd)).astype(np.float32)
+    xr = orc.rope_fwd(x, B, S, H, hd)
+    np.testing.assert_allclose((xr.astype(np.float64) ** 2).sum(-1), (x.astype(np.float64) ** 2).sum(-1), rtol=1e-5)
+    one = orc.rope_fwd(x[3:4], 1, 1, 1, hd, start_pos=3)
+    np.testing.assert_allclose(one[0], xr[3], atol=1e-6)
+    # position 0 is the identity rotation
+    np.testing.assert_array_equal(xr[0], x[0])
+    # backward is the inverse rotation, and the adjoint: <R x, g> == <x, R^T g>
+    np.testing.assert_allclose(orc.rope_bwd(xr, B, S, H, hd), x, atol=1e-5)
+    g = rng.standard_normal(x.shape).astype(np.float32)
+    lhs = float((xr.astype(np.float64) * g).sum())
+    rhs = float((x.astype(np.float64) * orc.rope_bwd(g, B, S, H, hd)).sum())
+    assert abs(lhs - rhs) < 1e-4 * (abs(lhs) + 1)
+
+
+def test_rope_pairs_are_half_split(orc):
+    # a vector with only element i set rotates into elements i and i + hd/2 only
+    hd, S = 8, 5
+    x = np.zeros((S, hd), np.float32)
+    x[:, 1] = 1.0
+    xr = orc.rope_fwd(x, 1, S, 1, hd)
+    cos, sin = torch_ref.rope_tables_np(S, hd)
+    np.testing.assert_allclose(xr[:, 1], cos[:, 1], atol=1e-7)
+    np.testing.assert_allclose(xr[:, 1 + hd // 2], sin[:, 1], atol=1e-7)
+    assert np.count_nonzero(np.delete(xr, [1, 1 + hd // 2], axis=1)) == 0
+
+
+# --------------------------------------------------------------------------- attention
+@pytest.mark.parametrize("B,S,H,hd", [(2, 16, 2, 8), (1, 64, 4, 32), (2, 33, 3, 16)])
+def test_attention_vs_sdpa(orc, B, S, H, hd):
+    rng = np.random.default_rng(B * 100 + S)
+    q, k, v, do = (rng.standard_normal((B * S, H * hd)).astype(np.float32) for _ in range(4))
+
+    def t(a):
+        return torch.tensor(a.reshape(B, S, H, hd), dtype=torch.float64).transpose(1, 2).requires_grad_(True)
+
+    qt, kt, vt = t(q), t(k), t(v)
+    ot = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+    ot.backward(torch.tensor(do.reshape(B, S, H, hd), dtype=torch.float64).transpose(1, 2))
+    o, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd)
+
+    def back(x):
+        return x.detach().transpose(1, 2).reshape(B * S, H * hd).numpy()
+
+    assert rel(o, back(ot)) < 1e-5
+    dq, dk, dv = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
+    assert rel(dq, qt.grad.transpose(1, 2).reshape(B * S, H * hd).numpy()) < 1e-5
+    assert rel(dk, kt.grad.transpose(1, 2).reshape(B * S, H * hd).numpy()) < 1e-5
+    assert rel(dv, vt.grad.transpose(1, 2).reshape(B * S, H * hd).numpy()) < 1e-5
+
+
+def test_attention_first_row_copies_v(orc):
+    # causal: query 0 sees only key 0, so o[0] == v[0] exactly
+    rng = np.random.default_rng(5)
+    B, S, H, hd = 1, 12, 2, 8
+    q, k, v = (rng.standard_normal((B * S, H * hd)).astype(np.float32) for _ in range(3))
+    o, _, _ = orc.attention_fwd(q, k, v, B, S, H, hd)
+    np.testing.assert_array_equal(o[0], v[0])
+
+
+# --------------------------------------------------------------------------- SwiGLU
+def test_swiglu_vs_torch(orc):
+    rng = np.random.default_rng(9)
+    g, u, dh = (rng.standard_normal(1000).astype(np.float32) * 3 for _ in range(3))
+    gt = torch.tensor(g, dtype=torch.float64, requires_grad=True)
+    ut = torch.tensor(u, dtype=torch.float64, requires_grad=True)
+    ht = F.silu(gt) * ut
+    ht.backward(torch.tensor(dh, dtype=torch.float64))
+    assert rel(orc.swiglu_fwd(g, u), ht.detach().numpy()) < 1e-6
+    dg, du = orc.swiglu_bwd(g, u, dh)
+    assert rel(dg, gt.grad.numpy()) < 1e-6
+    assert rel(du, ut.grad.numpy()) < 1e-6
+
+
+# --------------------------------------------------------------------------- cross-entropy
+def test_ce_known_answer(orc):
+    # tests/unit/test_optim.cpp:16-36
+    z = np.array([[1, 2, 3], [1, -1, 0]], np.float32)
+    loss, losses, lse, valid = orc.ce_fwd(z, np.array([2, 0]))
+    assert abs(loss - 0.407606) < 1e-4 and valid == 2
+    assert abs(losses.sum() - 2 * 0.407606) < 1e-4
+
+
+def test_ce_stability_and_ignore(orc):
+    # tests/unit/test_optim.cpp:38-65 and :101-129
+    z = np.array([[1000, 1001, 999, 998], [-1000, -999, -1001, -1002]], np.float32)
+    loss, _, lse, valid = orc.ce_fwd(z, np.array([1, 1]))
+    d = orc.ce_bwd(z, np.array([1, 1]), lse, valid)
+    assert math.isfinite(loss) and loss > 0 and np.all(np.isfinite(d))
+    rng = np.random.default_rng(4)
+    z = rng.standard_normal((6, 5)).astype(np.float32)
+    t = np.array([0, 2, -100, -100, 4, 1])
+    loss, _, lse, valid = orc.ce_fwd(z, t)
+    d = orc.ce_bwd(z, t, lse, valid)
+    assert valid == 4
+    assert np.all(d[2] == 0) and np.all(d[3] == 0) and np.any(np.abs(d[0]) > 1e-6)
+
+
+def test_ce_vs_torch(orc):
+    rng = np.random.default_rng(11)
+    z = (3 * rng.standard_normal((40, 77))).astype(np.float32)
+    t = rng.integers(0, 77, 40)
+    t[[3, 17]] = -100
+    zt = torch.tensor(z, dtype=torch.float64, requires_grad=True)
+    lt = F.cross_entropy(zt, torch.tensor(t), ignore_index=-100)
+    lt.backward(torch.tensor(2.0, dtype=torch.float64))
+    loss, _, lse, valid = orc.ce_fwd(z, t)
+    assert abs(loss - float(lt)) < 1e-6 * abs(float(lt))
+    assert rel(orc.ce_bwd(z, t, lse, valid, g=2.0), zt.grad.numpy()) < 1e-6
+
+
+# --------------------------------------------------------------------------- embedding
+def test_embedding_known_answer(orc):
+    # tests/unit/test_model.cpp:15-48
+    rng = np.random.default_rng(6)
+    W = rng.standard_normal((16, 8)).astype(np.float32)
+    ids = np.array([0, 5, 12, 3, 5, 1])
+    out = orc.embedding_fwd(ids, W)
+    np.testing.assert_array_equal(out, W[ids])
+    dW = orc.embedding_bwd(ids, np.ones((6, 8), np.float32), 16)
+    assert np.all(dW[5] == 2.0) and np.all(dW[0] == 1.0) and np.all(dW[7] == 0.0)
+    # out-of-range ids give zero rows and no gradient
+    out = orc.embedding_fwd(np.array([-1, 16, 2]), W)
+    assert np.all(out[:2] == 0) and np.array_equal(out[2], W[2])
+
+
+# --------------------------------------------------------------------------- optimizer tail
+def test_adamw_known_answer(orc):
+    # tests/unit/test_optim.cpp:209-237
+    p = np.ones(2, np.float32)
+    m = np.zeros(2, np.float32)
+    v = np.zeros(2, np.float32)
+    orc.adamw(p, np.full(2, 0.1, np.float32), m, v, 0.01, 0.9, 0.999, 1e-8, 0.1, 1)
+    np.testing.assert_allclose(p, 0.989, atol=1e-4)
+
+
+def test_adamw_vs_torch(orc):
+    rng = np.random.default_rng(12)
+    p0 = rng.standard_normal(500).astype(np.float32)
+    p = p0.copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    pt = torch.tensor(p0, dtype=torch.float64, requires_grad=True)
+    opt = torch.optim.AdamW([pt], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    for step in range(1, 4):
+        g = rng.standard_normal(500).astype(np.float32)
+        orc.adamw(p, g, m, v, 3e-4, 0.9, 0.95, 1e-8, 0.1, step)
+        pt.grad = torch.tensor(g, dtype=torch.float64)
+        opt.step()
+    assert np.max(np.abs(p - pt.detach().numpy())) < 1e-6
+
+
+def test_clip_known_answer(orc):
+    # tests/unit/test_optim.cpp:191-207
+    g1 = np.full(3, 3.0, np.float32)
+    g2 = np.full(4, 4.0, np.float32)
+    n = orc.clip_grad_norm([g1, g2], 5.0)
+    assert abs(n - math.sqrt(91)) < 1e-3
+    assert abs(orc.clip_grad_norm([g1, g2], 100.0) - 5.0) < 1e-3
+
+
+def test_scaler_sequences(orc):
+    # tests/unit/test_amp.cpp:56-84
+    s = orc.LossScaler(initial_scale=1024.0)
+    g = np.array([1024, 2048, -512, 0], np.float32)
+    assert s.unscale_and_update([g]) and s.good_steps == 1 and s.skipped_steps == 0
+    np.testing.assert_allclose(g, [1, 2, -0.5, 0])
+    # :86-116 backoff on NaN then Inf
+    for bad, expect in ((np.nan, 512.0), (np.inf, 256.0)):
+        g = np.array([1, bad, 2, 3], np.float32)
+        assert not s.unscale_and_update([g])
+        assert s.scale == expect and s.good_steps == 0
+    assert s.skipped_steps == 2
+    # :118-142 growth every 3 good steps, capped at max
+    s = orc.LossScaler(initial_scale=128.0, growth_interval=3, max_scale=1024.0)
+    seen = []
+    for _ in range(6):
+        assert s.unscale_and_update([np.array([1, 2], np.float32)])
+        seen.append(s.scale)
+    assert seen == [128, 128, 256, 256, 256, 512]
+
+
+# --------------------------------------------------------------------------- whole step
+def _tiny_case(seed=1234, tied=True, vocab=512, d=128, L=2, H=4, f=352, B=8, S=64):
+    rng = np.random.default_rng(seed)
+    lay = torch_ref.layout(vocab, d, L, f, tied)
+    params = []
+    for name, shape in lay:
+        if name.endswith("norm1.weight") or name.endswith("norm2.weight") or name == "norm.weight":
+            params.append(np.ones(shape, np.float32).reshape(-1))
+        else:
+            params.append((0.02 * rng.standard_normal(shape)).astype(np.float32).reshape(-1))
+    params = np.concatenate(params)
+    seq = rng.integers(0, vocab, (B, S + 1))
+    return params, seq[:, :S].copy(), seq[:, 1:].copy()
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_lm_step_vs_torch(orc, tied):
+    vocab, d, L, H, f, B, S = 512, 128, 2, 4, 352, 8, 64
+    params, ids, tgt = _tiny_case(tied=tied)
+    cfg = orc.make_config(vocab, d, L, H, f, S, tied=tied)
+    assert orc.num_params(cfg) == params.size
+    loss_t, norm_t, grads_t, new_t = torch_ref.lm_step(vocab, d, L, H, f, tied, params, ids, tgt, B, S)
+    p = params.copy()
+    res, grads, m, v, step = orc.lm_step(cfg, p, ids, tgt, B, S)
+    assert abs(res.loss - loss_t) / abs(loss_t) < 1e-5
+    assert abs(res.grad_norm - norm_t) / norm_t < 1e-4
+    off = 0
+    for name, shape in torch_ref.layout(vocab, d, L, f, tied):
+        n = int(np.prod(shape))
+        assert rel(grads[off:off + n], grads_t[off:off + n]) < 1e-4, name
+        assert rel(p[off:off + n], new_t[off:off + n]) < 1e-4, name
+        off += n
+    assert step == 1
+
+
+def test_lm_loss_matches_step_and_fd(orc):
+    """orc_lm_loss equals the step's loss; a finite difference along the analytic gradient
+    direction matches the directional derivative."""
+    vocab, d, L, H, f, B, S = 64, 32, 1, 2, 48, 2, 8
+    params, ids, tgt = _tiny_case(seed=5, tied=False, vocab=vocab, d=d, L=L, H=H, f=f, B=B, S=S)
+    cfg = orc.make_config(vocab, d, L, H, f, S, tied=False)
+    l0 = orc.lm_loss(cfg, params, ids, tgt, B, S)
+    res, grads, _, _, _ = orc.lm_step(cfg, params.copy(), ids, tgt, B, S, max_grad_norm=1e9, do_update=False)
+    assert l0 == res.loss
+    u = grads / np.linalg.norm(grads)
+    h = 1e-2
+    lp = orc.lm_loss(cfg, (params + h * u).astype(np.float32), ids, tgt, B, S)
+    lm = orc.lm_loss(cfg, (params - h * u).astype(np.float32), ids, tgt, B, S)
+    fd = (lp - lm) / (2 * h)
+    assert abs(fd - float(np.linalg.norm(grads))) < 2e-2 * float(np.linalg.norm(grads))
+
+
+def test_lm_step_scaler_is_exact_power_of_two(orc):
+    """With loss scaling the optimizer sees the same gradients (scale is a power of two)."""
+    vocab, d, L, H, f, B, S = 64, 32, 1, 2, 48, 2, 8
+    params, ids, tgt = _tiny_case(seed=8, tied=False, vocab=vocab, d=d, L=L, H=H, f=f, B=B, S=S)
+    cfg = orc.make_config(vocab, d, L, H, f, S, tied=False)
+    r0, g0, _, _, _ = orc.lm_step(cfg, params.copy(), ids, tgt, B, S, do_update=False)
+    sc = orc.LossScaler()
+    r1, g1, _, _, _ = orc.lm_step(cfg, params.copy(), ids, tgt, B, S, do_update=False, scaler=sc)
+    assert r1.loss_scale_used == 65536.0 and not r1.found_inf
+    np.testing.assert_array_equal(g0, g1)
