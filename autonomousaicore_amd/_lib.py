@@ -1,0 +1,135 @@
+"""ctypes binding of the native library libaic_hip.so (include/aic_hip.h).
+
+Loading never compiles and never falls back: if the library is missing, `load()` raises
+with the command that builds it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libaic_hip.so")
+
+AIC_F32, AIC_F16, AIC_BF16, AIC_I32, AIC_I64, AIC_U8, AIC_U16 = 0, 1, 2, 3, 4, 5, 6
+
+vp = C.c_void_p
+i64 = C.c_int64
+f32 = C.c_float
+i32 = C.c_int
+i64p = C.POINTER(C.c_int64)
+f32p = C.POINTER(C.c_float)
+
+
+class OptimCtl(C.Structure):
+    _fields_ = [("scale", f32), ("good_steps", i32), ("skipped_steps", i32), ("use_scaler", i32),
+                ("growth_factor", f32), ("backoff_factor", f32), ("growth_interval", i32), ("min_scale", f32),
+                ("max_scale", f32), ("max_grad_norm", f32), ("grad_norm", f32), ("grad_mult", f32), ("skip", i32),
+                ("step", i32)]
+
+
+class LMConfig(C.Structure):
+    _fields_ = [("vocab", i64), ("d_model", i64), ("n_layers", i64), ("n_heads", i64), ("d_ffn", i64),
+                ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32)]
+
+
+class TrainConfig(C.Structure):
+    _fields_ = [("lr", f32), ("beta1", f32), ("beta2", f32), ("eps", f32), ("weight_decay", f32),
+                ("max_grad_norm", f32), ("use_loss_scaler", i32), ("init_scale", f32), ("growth_factor", f32),
+                ("backoff_factor", f32), ("growth_interval", i32), ("min_scale", f32), ("max_scale", f32)]
+
+
+class KernelStat(C.Structure):
+    _fields_ = [("name", C.c_char * 32), ("launches", i64), ("total_ms", C.c_double), ("flops", C.c_double),
+                ("bytes", C.c_double), ("mfma_bound", i32)]
+
+
+class StepStats(C.Structure):
+    _fields_ = [("loss", f32), ("grad_norm", f32), ("found_inf", i32), ("loss_scale", f32), ("step", i64)]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "aic_hip_last_error": (C.c_char_p, []),
+    "aic_hip_device_count": (i32, []),
+    "aic_hip_version": (C.c_char_p, []),
+    "aic_hip_mem_alloc_async": (i32, [C.POINTER(vp), C.c_size_t, vp]),
+    "aic_hip_mem_free_async": (i32, [vp, vp]),
+    "aic_hip_mem_stats": (i32, [i64p, i64p]),
+    "aic_hip_gemm": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp, i64, i32, i32, vp]),
+    "aic_hip_rmsnorm_fwd": (i32, [vp, i64, vp, vp, i64, vp, i64, i64, f32, i32, vp]),
+    "aic_hip_rmsnorm_bwd": (i32, [vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, i32, i64, i64, i32, vp]),
+    "aic_hip_rope": (i32, [vp, i64, i64, i64, i64, i64, i64, vp, vp, i32, i32, vp]),
+    "aic_hip_rope_tables": (i32, [vp, vp, i64, i64, f32]),
+    "aic_hip_attn_fwd": (i32, [vp, vp, vp, i64, vp, i64, vp, i64, i64, i64, i64, i32, f32, i32, vp]),
+    "aic_hip_attn_bwd": (i32, [vp, vp, vp, i64, vp, vp, i64, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, f32, i32,
+                               vp]),
+    "aic_hip_swiglu_fwd": (i32, [vp, vp, i64, vp, i64, i64, i64, i32, vp]),
+    "aic_hip_swiglu_bwd": (i32, [vp, vp, i64, vp, i64, vp, vp, i64, i64, i64, i32, vp]),
+    "aic_hip_ce_fwd": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, vp, i32, vp]),
+    "aic_hip_ce_bwd": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, vp, vp, i64, i32, vp]),
+    "aic_hip_embed_fwd": (i32, [vp, i64, vp, i64, i64, vp, i32, vp]),
+    "aic_hip_embed_bwd": (i32, [vp, i64, vp, i64, i64, vp, i32, i32, vp]),
+    "aic_hip_grad_sqnorm_multi": (i32, [C.POINTER(vp), i64p, i32, vp, vp, vp]),
+    "aic_hip_scale_multi": (i32, [C.POINTER(vp), i64p, i32, vp, vp]),
+    "aic_hip_optim_finalize": (i32, [vp, vp, vp, vp]),
+    "aic_hip_adamw_multi": (i32, [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i64p,
+                                  i32, f32, f32, f32, f32, f32, i64, vp, vp]),
+    "aic_hip_cast_f32_bf16": (i32, [vp, vp, i64, vp]),
+    "aic_lm_create": (i32, [C.POINTER(LMConfig), C.POINTER(TrainConfig), C.POINTER(vp)]),
+    "aic_lm_destroy": (i32, [vp]),
+    "aic_lm_num_params": (i64, [vp]),
+    "aic_lm_num_tensors": (i32, [vp]),
+    "aic_lm_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
+    "aic_lm_set_params": (i32, [vp, vp]),
+    "aic_lm_get_params": (i32, [vp, vp]),
+    "aic_lm_get_grads": (i32, [vp, vp]),
+    "aic_lm_get_adam_state": (i32, [vp, vp, vp, i64p]),
+    "aic_lm_init_normal": (i32, [vp, C.c_uint64, f32, i32]),
+    "aic_lm_train_step": (i32, [vp, vp, vp, i64, i64, i32, C.POINTER(StepStats)]),
+    "aic_lm_eval_loss": (i32, [vp, vp, vp, i64, i64, i32, f32p]),
+    "aic_lm_stream": (i32, [vp, C.POINTER(vp)]),
+    "aic_lm_synchronize": (i32, [vp]),
+    "aic_lm_last_stats": (i32, [vp, C.POINTER(StepStats)]),
+    "aic_lm_profile": (i32, [vp, i32]),
+    "aic_lm_profile_stats": (i32, [vp, C.POINTER(KernelStat), i32, C.POINTER(i32)]),
+    "aic_synth_uniform_ids": (i32, [C.c_uint64, i64, i64, vp]),
+    "aic_synth_zipf_ids": (i32, [C.c_uint64, i64, i64, C.c_double, vp]),
+    "aic_synth_normal": (i32, [C.c_uint64, i64, f32, f32, vp]),
+}
+
+
+class AicError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"aic error {code}: {message}")
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """Load libaic_hip.so (built by `python -m autonomousaicore_amd.build`)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m autonomousaicore_amd.build` "
+                           "(or __graft_entry__.build()); there is no fallback path")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = load().aic_hip_last_error()
+        raise AicError(rc, msg.decode() if msg else "")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

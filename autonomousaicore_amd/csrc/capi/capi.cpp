@@ -1,0 +1,440 @@
+// extern "C" boundary of the library (declared in include/aic_hip.h).  Every entry catches
+// aic::Error / std::exception, records the message for aic_hip_last_error() and returns
+// the error code; nothing throws across the ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+
+#include "../../../include/aic_hip.h"
+#include "../data/synthetic.hpp"
+#include "../kernels/gemm.hpp"
+#include "../kernels/kernels.hpp"
+#include "../model/transformer_lm.hpp"
+#include "../runtime/error.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic {
+
+const char* error_code_name(ErrorCode c) noexcept {
+    switch (c) {
+        case ErrorCode::Ok: return "Ok";
+        case ErrorCode::InvalidArgument: return "InvalidArgument";
+        case ErrorCode::OutOfRange: return "OutOfRange";
+        case ErrorCode::ShapeMismatch: return "ShapeMismatch";
+        case ErrorCode::DTypeMismatch: return "DTypeMismatch";
+        case ErrorCode::DeviceMismatch: return "DeviceMismatch";
+        case ErrorCode::OutOfMemory: return "OutOfMemory";
+        case ErrorCode::HipError: return "HipError";
+        case ErrorCode::NotImplemented: return "NotImplemented";
+        case ErrorCode::BackendUnavailable: return "BackendUnavailable";
+        case ErrorCode::IOError: return "IOError";
+        case ErrorCode::FormatError: return "FormatError";
+        case ErrorCode::Overflow: return "Overflow";
+        case ErrorCode::InvalidState: return "InvalidState";
+        case ErrorCode::RuntimeError: return "RuntimeError";
+        case ErrorCode::Internal: return "Internal";
+    }
+    return "Unknown";
+}
+
+const char* dtype_name(DType d) noexcept {
+    switch (d) {
+        case DType::Float32: return "float32";
+        case DType::Float16: return "float16";
+        case DType::BFloat16: return "bfloat16";
+        case DType::Int32: return "int32";
+        case DType::Int64: return "int64";
+        case DType::UInt8: return "uint8";
+        case DType::UInt16: return "uint16";
+    }
+    return "unknown";
+}
+
+}  // namespace aic
+
+struct aic_lm {
+    aic::models::TransformerLM* model;
+};
+
+namespace {
+
+thread_local std::string t_last_error;
+
+template <typename F>
+int guard(F&& f) {
+    try {
+        f();
+        t_last_error.clear();
+        return 0;
+    } catch (const aic::Error& e) {
+        t_last_error = e.what();
+        return static_cast<int>(e.code());
+    } catch (const std::bad_alloc& e) {
+        t_last_error = std::string("host allocation failed: ") + e.what();
+        return static_cast<int>(aic::ErrorCode::OutOfMemory);
+    } catch (const std::exception& e) {
+        t_last_error = e.what();
+        return static_cast<int>(aic::ErrorCode::RuntimeError);
+    } catch (...) {
+        t_last_error = "unknown error";
+        return static_cast<int>(aic::ErrorCode::Internal);
+    }
+}
+
+aic::DType dt(aic_dtype d) { return static_cast<aic::DType>(static_cast<int>(d)); }
+hipStream_t st(aic_stream s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char* aic_hip_last_error(void) { return t_last_error.c_str(); }
+
+int aic_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+const char* aic_hip_version(void) { return "autonomousaicore_amd 0.1.0 (gfx950)"; }
+
+int aic_hip_mem_alloc_async(void** ptr, size_t bytes, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(ptr, InvalidArgument, "null output pointer");
+        *ptr = aic::pool_alloc(bytes, st(stream));
+    });
+}
+
+int aic_hip_mem_free_async(void* ptr, aic_stream stream) { return guard([&] { aic::pool_free(ptr, st(stream)); }); }
+
+int aic_hip_mem_stats(int64_t* allocated_bytes, int64_t* peak_bytes) {
+    return guard([&] {
+        const aic::MemoryStats s = aic::pool_stats();
+        if (allocated_bytes) *allocated_bytes = s.allocated_bytes;
+        if (peak_bytes) *peak_bytes = s.peak_bytes;
+    });
+}
+
+int aic_hip_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                 const void* B, int64_t ldb, float beta, void* C, int64_t ldc, const void* R, int64_t ldr,
+                 aic_dtype ab_type, aic_dtype c_type, aic_stream stream) {
+    return guard([&] {
+        aic::hip::GemmArgs a;
+        a.transA = transA;
+        a.transB = transB;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.alpha = alpha;
+        a.beta = beta;
+        a.A = A;
+        a.lda = lda;
+        a.B = B;
+        a.ldb = ldb;
+        a.C = C;
+        a.ldc = ldc;
+        a.R = R;
+        a.ldr = ldr;
+        a.ab = dt(ab_type);
+        a.c = dt(c_type);
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
+int aic_hip_rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows,
+                        int64_t dim, float eps, aic_dtype d, aic_stream stream) {
+    return guard([&] { aic::hip::rmsnorm_fwd(x, ldx, w, y, ldy, rms, rows, dim, eps, dt(d), st(stream)); });
+}
+
+int aic_hip_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                        const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, int accumulate, int64_t rows,
+                        int64_t dim, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::rmsnorm_bwd(dy, lddy, x, ldx, w, rms, dres, ldres, dx, lddx, dw, accumulate != 0, rows, dim, dt(d),
+                              st(stream));
+    });
+}
+
+int aic_hip_rope(void* x, int64_t ld, int64_t B, int64_t S, int64_t heads, int64_t hd, int64_t start_pos,
+                 const float* cos_t, const float* sin_t, int inverse, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::rope(x, ld, B, S, heads, hd, start_pos, cos_t, sin_t, inverse != 0, dt(d), st(stream));
+    });
+}
+
+int aic_hip_rope_tables(float* cos_host, float* sin_host, int64_t max_seq, int64_t hd, float base) {
+    return guard([&] {
+        AIC_CHECK(cos_host && sin_host && max_seq >= 0 && hd > 0 && hd % 2 == 0, InvalidArgument, "bad rope table args");
+        aic::hip::rope_tables_host(cos_host, sin_host, max_seq, hd, base);
+    });
+}
+
+int aic_hip_attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
+                     int64_t B, int64_t H, int64_t S, int64_t hd, int causal, float scale, aic_dtype d,
+                     aic_stream stream) {
+    return guard([&] {
+        aic::hip::attn_fwd(q, k, v, ld_qkv, o, ld_o, lse, B, H, S, hd, causal != 0, scale, dt(d), st(stream));
+    });
+}
+
+int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
+                     int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
+                     int64_t S, int64_t hd, int causal, float scale, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::attn_bwd(q, k, v, ld_qkv, o, dout, ld_o, lse, dq, dk, dv, ld_d, B, H, S, hd, causal != 0, scale,
+                           dt(d), st(stream));
+    });
+}
+
+int aic_hip_swiglu_fwd(const void* g, const void* u, int64_t ld_gu, void* h, int64_t ld_h, int64_t T, int64_t f,
+                       aic_dtype d, aic_stream stream) {
+    return guard([&] { aic::hip::swiglu_fwd(g, u, ld_gu, h, ld_h, T, f, dt(d), st(stream)); });
+}
+
+int aic_hip_swiglu_bwd(const void* g, const void* u, int64_t ld_gu, const void* dh, int64_t ld_h, void* dg, void* du,
+                       int64_t ld_d, int64_t T, int64_t f, aic_dtype d, aic_stream stream) {
+    return guard([&] { aic::hip::swiglu_bwd(g, u, ld_gu, dh, ld_h, dg, du, ld_d, T, f, dt(d), st(stream)); });
+}
+
+int aic_hip_ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                   float* losses, float* lse, float* loss_mean, int64_t* valid, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::ce_fwd(logits, ld, targets, N, C, ignore_index, losses, lse, loss_mean, valid, dt(d), st(stream));
+    });
+}
+
+int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                   int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d,
+                   aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::ce_bwd(logits, ld, targets, lse, N, C, ignore_index, grad, valid, dlogits, ld_d, dt(d), st(stream));
+    });
+}
+
+int aic_hip_embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, aic_dtype d,
+                      aic_stream stream) {
+    return guard([&] { aic::hip::embed_fwd(ids, N, W, V, D, out, dt(d), st(stream)); });
+}
+
+int aic_hip_embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, int accumulate,
+                      aic_dtype d, aic_stream stream) {
+    return guard([&] { aic::hip::embed_bwd(ids, N, dout, V, D, dW, accumulate != 0, dt(d), st(stream)); });
+}
+
+int aic_hip_grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                              int* nonfinite, aic_stream stream) {
+    return guard([&] { aic::hip::grad_sqnorm_multi(grads, sizes, count, sqnorm, nonfinite, st(stream)); });
+}
+
+int aic_hip_scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, aic_stream stream) {
+    return guard([&] { aic::hip::scale_multi(grads, sizes, count, scale, st(stream)); });
+}
+
+int aic_hip_optim_finalize(const double* sqnorm, const int* nonfinite, aic_optim_ctl* ctl, aic_stream stream) {
+    return guard([&] { aic::hip::optim_finalize(sqnorm, nonfinite, ctl, st(stream)); });
+}
+
+int aic_hip_adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
+                        const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int64_t step, const aic_optim_ctl* ctl, aic_stream stream) {
+    return guard([&] {
+        aic::hip::adamw_multi(p, g, m, v, p_bf16, sizes, count, lr, beta1, beta2, eps, weight_decay, step, ctl,
+                              st(stream));
+    });
+}
+
+int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream) {
+    return guard([&] { aic::hip::cast_f32_bf16(src, dst, n, st(stream)); });
+}
+
+// ------------------------------------------------------------------ TransformerLM
+int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm** out) {
+    return guard([&] {
+        AIC_CHECK(cfg && tcfg && out, InvalidArgument, "null argument");
+        aic::models::TransformerLMConfig c;
+        c.vocab_size = cfg->vocab;
+        c.hidden_dim = cfg->d_model;
+        c.num_layers = cfg->n_layers;
+        c.num_heads = cfg->n_heads;
+        c.intermediate_dim = cfg->d_ffn;
+        c.max_seq_len = cfg->max_seq_len;
+        c.rms_norm_eps = cfg->norm_eps;
+        c.rope_theta = cfg->rope_base;
+        c.tie_word_embeddings = cfg->tied != 0;
+        c.compute = dt(cfg->compute);
+        aic::models::TrainOptions o;
+        o.adamw = {tcfg->lr, tcfg->beta1, tcfg->beta2, tcfg->eps, tcfg->weight_decay};
+        o.max_grad_norm = tcfg->max_grad_norm;
+        o.use_loss_scaler = tcfg->use_loss_scaler != 0;
+        o.scaler = {tcfg->init_scale, tcfg->growth_factor, tcfg->backoff_factor, tcfg->growth_interval,
+                    tcfg->min_scale, tcfg->max_scale};
+        auto* h = new aic_lm{nullptr};
+        try {
+            h->model = new aic::models::TransformerLM(c, o);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int aic_lm_destroy(aic_lm* lm) {
+    return guard([&] {
+        if (!lm) return;
+        delete lm->model;
+        delete lm;
+    });
+}
+
+int64_t aic_lm_num_params(const aic_lm* lm) { return lm ? lm->model->num_params() : -1; }
+
+int aic_lm_num_tensors(const aic_lm* lm) { return lm ? static_cast<int>(lm->model->params().size()) : -1; }
+
+int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        const auto& ps = lm->model->params();
+        AIC_CHECK(i >= 0 && i < static_cast<int>(ps.size()), OutOfRange, "tensor index ", i);
+        const auto& p = ps[static_cast<size_t>(i)];
+        if (name && name_cap > 0) {
+            std::strncpy(name, p.name.c_str(), static_cast<size_t>(name_cap) - 1);
+            name[name_cap - 1] = '\0';
+        }
+        if (rank) *rank = static_cast<int>(p.shape.size());
+        if (dims)
+            for (size_t k = 0; k < p.shape.size() && k < 2; ++k) dims[k] = p.shape[k];
+        if (offset) {
+            int64_t o = 0;
+            for (int j = 0; j < i; ++j) o += ps[static_cast<size_t>(j)].numel;
+            *offset = o;  // offset in the packed (unpadded) host layout
+        }
+    });
+}
+
+int aic_lm_set_params(aic_lm* lm, const float* host) { return guard([&] { lm->model->set_params(host); }); }
+int aic_lm_get_params(const aic_lm* lm, float* host) { return guard([&] { lm->model->get_params(host); }); }
+int aic_lm_get_grads(const aic_lm* lm, float* host) { return guard([&] { lm->model->get_grads(host); }); }
+int aic_lm_get_adam_state(const aic_lm* lm, float* m, float* v, int64_t* step) {
+    return guard([&] { lm->model->get_adam_state(m, v, step); });
+}
+
+int aic_lm_init_normal(aic_lm* lm, uint64_t seed, float std, int residual_scaling) {
+    return guard([&] { lm->model->init_normal(seed, std, residual_scaling != 0); });
+}
+
+namespace {
+struct IdsOnDevice {
+    const int64_t* ids = nullptr;
+    const int64_t* tgt = nullptr;
+    aic::DeviceBuffer buf;
+    IdsOnDevice(const int64_t* i, const int64_t* t, int64_t n, int on_device, hipStream_t s) {
+        if (on_device) {
+            ids = i;
+            tgt = t;
+            return;
+        }
+        buf = aic::DeviceBuffer(sizeof(int64_t) * 2 * static_cast<size_t>(n), s);
+        int64_t* d = buf.as<int64_t>();
+        AIC_HIP_CHECK(hipMemcpyAsync(d, i, sizeof(int64_t) * n, hipMemcpyHostToDevice, s));
+        AIC_HIP_CHECK(hipMemcpyAsync(d + n, t, sizeof(int64_t) * n, hipMemcpyHostToDevice, s));
+        AIC_HIP_CHECK(hipStreamSynchronize(s));
+        ids = d;
+        tgt = d + n;
+    }
+};
+
+void fill_stats(const aic::models::StepStats& s, aic_step_stats* out) {
+    out->loss = s.loss;
+    out->grad_norm = s.grad_norm;
+    out->found_inf = s.found_inf ? 1 : 0;
+    out->loss_scale = s.loss_scale;
+    out->step = s.step;
+}
+}  // namespace
+
+int aic_lm_train_step(aic_lm* lm, const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, int on_device,
+                      aic_step_stats* stats) {
+    return guard([&] {
+        AIC_CHECK(lm && ids && targets, InvalidArgument, "null argument");
+        IdsOnDevice in(ids, targets, B * S, on_device, lm->model->stream());
+        lm->model->train_step(in.ids, in.tgt, B, S);
+        if (stats) fill_stats(lm->model->last_stats(), stats);
+    });
+}
+
+int aic_lm_eval_loss(aic_lm* lm, const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, int on_device,
+                     float* loss) {
+    return guard([&] {
+        AIC_CHECK(lm && ids && targets && loss, InvalidArgument, "null argument");
+        IdsOnDevice in(ids, targets, B * S, on_device, lm->model->stream());
+        *loss = lm->model->eval_loss(in.ids, in.tgt, B, S);
+    });
+}
+
+int aic_lm_stream(const aic_lm* lm, aic_stream* stream) {
+    return guard([&] { *stream = static_cast<aic_stream>(lm->model->stream()); });
+}
+
+int aic_lm_synchronize(aic_lm* lm) { return guard([&] { lm->model->synchronize(); }); }
+
+int aic_lm_last_stats(aic_lm* lm, aic_step_stats* stats) {
+    return guard([&] { fill_stats(lm->model->last_stats(), stats); });
+}
+
+int aic_lm_profile(aic_lm* lm, int enable) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        lm->model->set_profiling(enable != 0);
+    });
+}
+
+int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n) {
+    return guard([&] {
+        AIC_CHECK(lm && n, InvalidArgument, "null argument");
+        const auto st = lm->model->profile_stats();
+        int k = 0;
+        for (const auto& c : st) {
+            if (k >= cap || !out) break;
+            aic_kernel_stat& o = out[k++];
+            std::memset(&o, 0, sizeof(o));
+            std::strncpy(o.name, c.name.c_str(), sizeof(o.name) - 1);
+            o.launches = c.launches;
+            o.total_ms = c.total_ms;
+            o.flops = c.flops;
+            o.bytes = c.bytes;
+            o.mfma_bound = c.mfma_bound ? 1 : 0;
+        }
+        *n = out ? k : static_cast<int>(st.size());
+    });
+}
+
+// ------------------------------------------------------------------ synthetic data
+int aic_synth_uniform_ids(uint64_t seed, int64_t n, int64_t vocab, int64_t* out_host) {
+    return guard([&] {
+        AIC_CHECK(out_host && n >= 0 && vocab > 0, InvalidArgument, "bad arguments");
+        aic::data::uniform_ids(seed, n, vocab, out_host);
+    });
+}
+
+int aic_synth_zipf_ids(uint64_t seed, int64_t n, int64_t vocab, double s, int64_t* out_host) {
+    return guard([&] {
+        AIC_CHECK(out_host && n >= 0 && vocab > 0 && s > 0, InvalidArgument, "bad arguments");
+        aic::data::zipf_ids(seed, n, vocab, s, out_host);
+    });
+}
+
+int aic_synth_normal(uint64_t seed, int64_t n, float mean, float std, float* out_host) {
+    return guard([&] {
+        AIC_CHECK(out_host && n >= 0, InvalidArgument, "bad arguments");
+        aic::data::normal(seed, n, mean, std, out_host);
+    });
+}
+
+}  // extern "C"

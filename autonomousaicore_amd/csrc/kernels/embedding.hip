@@ -1,0 +1,164 @@
+// Token embedding gather and its deterministic scatter-add backward.
+// Replaces cuda_embedding_forward/backward (src/cuda/cuda_embedding.cu:21-61), whose
+// backward uses fp32 atomicAdd (order-dependent results).  Here the backward sorts the
+// (id, position) pairs once in LDS (bitonic, one block) and then sums each id's rows in
+// token order, so repeated runs are bit-identical and ids that repeat often (Zipf-
+// distributed text) are summed by four waves instead of serialising on one address.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void embed_fwd_k(const int64_t* __restrict__ ids, int64_t N, const T* __restrict__ W,
+                                                   int64_t V, int64_t D, T* __restrict__ out) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= N * D) return;
+    const int64_t i = idx / D, d = idx % D;
+    const int64_t t = ids[i];
+    out[idx] = (t >= 0 && t < V) ? W[t * D + d] : T(0.0f);
+}
+
+// 16-byte copies (D*sizeof(T) % 16 == 0).
+__global__ __launch_bounds__(256) void embed_fwd_v(const int64_t* __restrict__ ids, int64_t N,
+                                                   const uint4* __restrict__ W, int64_t V, int64_t Dv,
+                                                   uint4* __restrict__ out) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= N * Dv) return;
+    const int64_t i = idx / Dv, d = idx % Dv;
+    const int64_t t = ids[i];
+    out[idx] = (t >= 0 && t < V) ? W[t * Dv + d] : make_uint4(0, 0, 0, 0);
+}
+
+constexpr int kSortMax = 16384;  // tokens per step sortable in one block's LDS (128 KB)
+
+// Bitonic sort of keys (id << 32 | position); ids outside [0, V) sort last.
+__global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__ ids, int N, int64_t V,
+                                                     int* __restrict__ sorted_pos, int* __restrict__ sorted_id) {
+    extern __shared__ unsigned long long key[];
+    int P = 1;
+    while (P < N) P <<= 1;
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        unsigned long long k = ~0ull;
+        if (i < N) {
+            const int64_t t = ids[i];
+            const unsigned long long id = (t >= 0 && t < V) ? static_cast<unsigned long long>(t) : 0x7fffffffull;
+            k = (id << 32) | static_cast<unsigned long long>(i);
+        }
+        key[i] = k;
+    }
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < P; i += blockDim.x) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const unsigned long long a = key[i], b = key[j];
+                    if ((a > b) == up) {
+                        key[i] = b;
+                        key[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < N; i += blockDim.x) {
+        const unsigned long long k = key[i];
+        sorted_pos[i] = static_cast<int>(k & 0xffffffffull);
+        const int id = static_cast<int>(k >> 32);
+        sorted_id[i] = id;
+    }
+}
+
+// One block per (sorted position p, column chunk of 256).  The block does work only if p
+// starts a run of equal ids; its 4 waves take every 4th token of the run, then combine in
+// a fixed order.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_seg_k(const int* __restrict__ sorted_pos, const int* __restrict__ sorted_id,
+                                                   int N, int64_t V, const T* __restrict__ dout, int64_t D,
+                                                   float* __restrict__ dW, int accumulate) {
+    __shared__ float part[4][64];
+    const int p = blockIdx.x;
+    const int id = sorted_id[p];
+    if (id >= V) return;
+    if (p > 0 && sorted_id[p - 1] == id) return;
+    int end = p + 1;
+    while (end < N && sorted_id[end] == id) ++end;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int64_t c0 = static_cast<int64_t>(blockIdx.y) * 64; c0 < D; c0 += static_cast<int64_t>(gridDim.y) * 64) {
+        const int64_t c = c0 + lane;
+        float acc = 0.0f;
+        if (c < D)
+            for (int q = p + wave; q < end; q += 4) acc += ld(dout, static_cast<int64_t>(sorted_pos[q]) * D + c);
+        part[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0 && c < D) {
+            const float s = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+            float* o = dW + static_cast<int64_t>(id) * D + c;
+            *o = accumulate ? *o + s : s;
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, DType dt, hipStream_t s) {
+    AIC_CHECK(N >= 0 && V > 0 && D > 0, InvalidArgument, "embed_fwd: bad shape");
+    if (N == 0) return;
+    const size_t es = dtype_size(dt);
+    AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "embed_fwd: dtype must be f32 or bf16");
+    const bool vec = (D * es) % 16 == 0 && (reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+    if (vec) {
+        const int64_t Dv = D * static_cast<int64_t>(es) / 16;
+        hipLaunchKernelGGL(embed_fwd_v, dim3(grid_for(N * Dv, 256, 1LL << 31)), dim3(256), 0, s, ids, N,
+                           static_cast<const uint4*>(W), V, Dv, static_cast<uint4*>(out));
+    } else if (dt == DType::Float32) {
+        hipLaunchKernelGGL(embed_fwd_k<float>, dim3(grid_for(N * D, 256, 1LL << 31)), dim3(256), 0, s, ids, N,
+                           static_cast<const float*>(W), V, D, static_cast<float*>(out));
+    } else {
+        hipLaunchKernelGGL(embed_fwd_k<bf16>, dim3(grid_for(N * D, 256, 1LL << 31)), dim3(256), 0, s, ids, N,
+                           static_cast<const bf16*>(W), V, D, static_cast<bf16*>(out));
+    }
+    AIC_LAUNCH_CHECK("embed_fwd");
+}
+
+void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, bool accumulate,
+               DType dt, hipStream_t s) {
+    AIC_CHECK(N >= 0 && V > 0 && D > 0, InvalidArgument, "embed_bwd: bad shape");
+    AIC_CHECK(N <= kSortMax, InvalidArgument, "embed_bwd: at most ", kSortMax, " tokens per call, got ", N);
+    AIC_CHECK(V < 0x7fffffffLL, InvalidArgument, "embed_bwd: vocabulary too large");
+    AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "embed_bwd: dtype must be f32 or bf16");
+    if (!accumulate) AIC_HIP_CHECK(hipMemsetAsync(dW, 0, sizeof(float) * V * D, s));
+    if (N == 0) return;
+    DeviceBuffer buf(sizeof(int) * 2 * N, s);
+    int* spos = buf.as<int>();
+    int* sid = spos + N;
+    int P = 1;
+    while (P < N) P <<= 1;
+    const size_t lds = sizeof(unsigned long long) * P;
+    if (lds > 65536)
+        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&embed_sort_k),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    hipLaunchKernelGGL(embed_sort_k, dim3(1), dim3(1024), lds, s, ids,
+                       static_cast<int>(N), V, spos, sid);
+    AIC_LAUNCH_CHECK("embed_sort");
+    const unsigned gy = static_cast<unsigned>(std::min<int64_t>((D + 63) / 64, 32));
+    if (dt == DType::Float32)
+        hipLaunchKernelGGL(embed_seg_k<float>, dim3(static_cast<unsigned>(N), gy), dim3(256), 0, s, spos, sid,
+                           static_cast<int>(N), V, static_cast<const float*>(dout), D, dW, accumulate ? 1 : 0);
+    else
+        hipLaunchKernelGGL(embed_seg_k<bf16>, dim3(static_cast<unsigned>(N), gy), dim3(256), 0, s, spos, sid,
+                           static_cast<int>(N), V, static_cast<const bf16*>(dout), D, dW, accumulate ? 1 : 0);
+    AIC_LAUNCH_CHECK("embed_seg");
+}
+
+}  // namespace aic::hip

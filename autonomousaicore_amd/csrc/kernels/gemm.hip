@@ -1,0 +1,348 @@
+// GEMM for the Linear layers: C = alpha * op(A) op(B) + beta * C + R.
+//
+// Replaces the reference's GEMM backend (src/cuda/cuda_gemm.cu:241-398, called from
+// src/ops/matmul.cpp:25-52): one launch per product instead of one per batch slice, no
+// weight transpose copy (op() reads either layout), fp32 accumulation, and the residual add
+// of TransformerBlock (include/nn/transformer_block.hpp:26-36) fused into the epilogue.
+//
+// bf16 path: hand-written CDNA4 kernel on v_mfma_f32_32x32x16_bf16.
+//   * 256 threads = 4 waves arranged 2x2; macro tile BM x BN x 64, each wave BM/2 x BN/2
+//     built from 32x32 MFMA blocks; fp32 accumulators live in AGPRs.
+//   * LDS holds both operands K-contiguous ([row][64] bf16 = 128 B per row), double
+//     buffered, 16-byte chunks XOR-swizzled by (r ^ r>>3) & 7 so that both 8-row and
+//     16-row lane groups of a ds_read_b128 hit distinct banks.
+//   * Operands stored M/N-contiguous in HBM (the dW = dY^T X and dX = dY W orientations)
+//     are transposed in registers on the way into LDS: each thread loads an 8(k) x 8(m)
+//     block with 8 coalesced 16-byte loads and writes 8 K-contiguous 16-byte chunks.
+//   * Blocks are remapped so that each XCD (hardware dispatches block b to XCD b % 8)
+//     works on a contiguous, M-grouped range of tiles and shares A/B panels in its L2.
+// fp32 path (the fp32 reference configuration) and odd shapes: a plain SIMT tiled kernel.
+#include "gemm.hpp"
+
+#include "common.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+constexpr int kBK = 64;
+
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+struct MfmaParams {
+    const bf16* A;
+    const bf16* B;
+    void* C;
+    const void* R;
+    int64_t lda, ldb, ldc, ldr;
+    int M, N, K;
+    float alpha, beta;
+};
+
+// Map the hardware block id to a tile so that consecutive tiles (same A row panel,
+// neighbouring B panels) land on the same XCD.
+__device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int q = nb / 8, r = nb % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    const int id = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+    constexpr int G = 8;
+    const int per_group = G * tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * G;
+    const int gsize = min(tiles_m - first_m, G);
+    const int inner = id % per_group;
+    tm = first_m + inner % gsize;
+    tn = inner / gsize;
+}
+
+// Loads one ROWS x 64 operand tile whose K dimension is contiguous in HBM.
+template <int ROWS>
+struct KContigLoader {
+    static constexpr int CH = ROWS * kBK / 8 / 256;  // 16-byte chunks per thread
+    uint4 r[CH];
+    __device__ __forceinline__ void load(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, int k0, int K) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
+            const int row = c >> 3, kc = c & 7;
+            const int gr = row0 + row, gk = k0 + kc * 8;
+            if (gr < nrows && gk < K)
+                r[i] = *reinterpret_cast<const uint4*>(g + static_cast<int64_t>(gr) * ld + gk);
+            else
+                r[i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    __device__ __forceinline__ void store(bf16* s) const {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
+            const int row = c >> 3, kc = c & 7;
+            *reinterpret_cast<uint4*>(s + row * kBK + ((kc ^ swz(row)) << 3)) = r[i];
+        }
+    }
+};
+
+// Loads one ROWS x 64 operand tile stored [K][ld] (rows contiguous in HBM) and transposes
+// it in registers: thread t < ROWS owns the 8(k) x 8(row) block (kg = t % 8, rc = t / 8).
+template <int ROWS>
+struct RowContigLoader {
+    uint4 r[8];
+    __device__ __forceinline__ void load(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, int k0, int K) {
+        const int t = threadIdx.x;
+        if (t >= ROWS) return;
+        const int kg = t & 7, rc = t >> 3;
+        const int gr = row0 + rc * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int gk = k0 + kg * 8 + i;
+            if (gk < K && gr < nrows)
+                r[i] = *reinterpret_cast<const uint4*>(g + static_cast<int64_t>(gk) * ld + gr);
+            else
+                r[i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    __device__ __forceinline__ static uint32_t w(const uint4& v, int i) {
+        return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+    }
+    __device__ __forceinline__ void store(bf16* s) const {
+        const int t = threadIdx.x;
+        if (t >= ROWS) return;
+        const int kg = t & 7, rc = t >> 3;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            uint4 o;
+            o.x = __builtin_amdgcn_perm(w(r[1], j >> 1), w(r[0], j >> 1), sel);
+            o.y = __builtin_amdgcn_perm(w(r[3], j >> 1), w(r[2], j >> 1), sel);
+            o.z = __builtin_amdgcn_perm(w(r[5], j >> 1), w(r[4], j >> 1), sel);
+            o.w = __builtin_amdgcn_perm(w(r[7], j >> 1), w(r[6], j >> 1), sel);
+            const int row = rc * 8 + j;
+            *reinterpret_cast<uint4*>(s + row * kBK + ((kg ^ swz(row)) << 3)) = o;
+        }
+    }
+};
+
+template <int BM, int BN, bool TA, bool TB, typename CT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_mfma(const MfmaParams p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int STAGE = (BM + BN) * kBK;
+    __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
+
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    using ALoader = typename std::conditional<TA, RowContigLoader<BM>, KContigLoader<BM>>::type;
+    using BLoader = typename std::conditional<TB, KContigLoader<BN>, RowContigLoader<BN>>::type;
+    ALoader la;
+    BLoader lb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nk = (p.K + kBK - 1) / kBK;
+    la.load(p.A, p.lda, m0, p.M, 0, p.K);
+    lb.load(p.B, p.ldb, n0, p.N, 0, p.K);
+    la.store(smem);
+    lb.store(smem + BM * kBK);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const bf16* As = smem + (kt & 1) * STAGE;
+        const bf16* Bs = As + BM * kBK;
+        if (kt + 1 < nk) {
+            la.load(p.A, p.lda, m0, p.M, (kt + 1) * kBK, p.K);
+            lb.load(p.B, p.ldb, n0, p.N, (kt + 1) * kBK, p.K);
+        }
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int c = 2 * kk + (lane >> 5);
+            bf16x8 af[FM], bfr[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int row = wm * WM + i * 32 + (lane & 31);
+                af[i] = *reinterpret_cast<const bf16x8*>(As + row * kBK + ((c ^ swz(row)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int row = wn * WN + j * 32 + (lane & 31);
+                bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + row * kBK + ((c ^ swz(row)) << 3));
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
+            la.store(nxt);
+            lb.store(nxt + BM * kBK);
+        }
+        __syncthreads();
+    }
+
+    CT* C = static_cast<CT*>(p.C);
+    const CT* R = static_cast<const CT*>(p.R);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WN + j * 32 + (lane & 31);
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (m >= p.M) continue;
+                float v = p.alpha * acc[i][j][e];
+                const int64_t ci = static_cast<int64_t>(m) * p.ldc + n;
+                if (p.beta != 0.0f) v += p.beta * ld(C, ci);
+                if (R) v += ld(R, static_cast<int64_t>(m) * p.ldr + n);
+                st(C, ci, v);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------
+// SIMT tiled GEMM (fp32 configuration, odd shapes).  64x64 tile, 256 threads, 4x4 each.
+// ---------------------------------------------------------------------------------------
+template <typename T, typename CT>
+__global__ __launch_bounds__(256) void gemm_simt(const T* __restrict__ A, const T* __restrict__ B, CT* C,
+                                                  const CT* R, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr,
+                                                  int M, int N, int K, int ta, int tb, float alpha, float beta) {
+    constexpr int TS = 64, TK = 16;
+    __shared__ float As[TK][TS + 4];
+    __shared__ float Bs[TK][TS + 4];
+    const int m0 = blockIdx.y * TS, n0 = blockIdx.x * TS;
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += TK) {
+        for (int e = threadIdx.x; e < TS * TK; e += 256) {
+            const int r = e / TK, kk = e % TK;
+            const int m = m0 + r, k = k0 + kk;
+            float a = 0.0f;
+            if (m < M && k < K) a = ld(A, ta ? static_cast<int64_t>(k) * lda + m : static_cast<int64_t>(m) * lda + k);
+            As[kk][r] = a;
+            const int n = n0 + r;
+            float b = 0.0f;
+            if (n < N && k < K) b = ld(B, tb ? static_cast<int64_t>(n) * ldb + k : static_cast<int64_t>(k) * ldb + n);
+            Bs[kk][r] = b;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < TK; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx * 4 + j;
+            if (n >= N) continue;
+            const int64_t ci = static_cast<int64_t>(m) * ldc + n;
+            float v = alpha * acc[i][j];
+            if (beta != 0.0f) v += beta * ld(C, ci);
+            if (R) v += ld(R, static_cast<int64_t>(m) * ldr + n);
+            st(C, ci, v);
+        }
+    }
+}
+
+template <int BM, int BN, bool TA, bool TB, typename CT>
+void launch_mfma(const GemmArgs& a, hipStream_t s) {
+    MfmaParams p;
+    p.A = static_cast<const bf16*>(a.A);
+    p.B = static_cast<const bf16*>(a.B);
+    p.C = a.C;
+    p.R = a.R;
+    p.lda = a.lda; p.ldb = a.ldb; p.ldc = a.ldc; p.ldr = a.ldr;
+    p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
+    p.alpha = a.alpha; p.beta = a.beta;
+    const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
+    hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, TA, TB, CT>), dim3(tiles), dim3(256), 0, s, p);
+    AIC_LAUNCH_CHECK("gemm_bf16_mfma");
+}
+
+template <int BM, int BN, typename CT>
+void dispatch_trans(const GemmArgs& a, hipStream_t s) {
+    if (!a.transA && a.transB) launch_mfma<BM, BN, false, true, CT>(a, s);
+    else if (!a.transA && !a.transB) launch_mfma<BM, BN, false, false, CT>(a, s);
+    else if (a.transA && !a.transB) launch_mfma<BM, BN, true, false, CT>(a, s);
+    else launch_mfma<BM, BN, true, true, CT>(a, s);
+}
+
+template <typename T, typename CT>
+void launch_simt(const GemmArgs& a, hipStream_t s) {
+    dim3 grid(static_cast<unsigned>((a.N + 63) / 64), static_cast<unsigned>((a.M + 63) / 64));
+    hipLaunchKernelGGL((gemm_simt<T, CT>), grid, dim3(256), 0, s, static_cast<const T*>(a.A),
+                       static_cast<const T*>(a.B), static_cast<CT*>(a.C), static_cast<const CT*>(a.R), a.lda, a.ldb,
+                       a.ldc, a.ldr, static_cast<int>(a.M), static_cast<int>(a.N), static_cast<int>(a.K), a.transA,
+                       a.transB, a.alpha, a.beta);
+    AIC_LAUNCH_CHECK("gemm_simt");
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+bool gemm_mfma_eligible(const GemmArgs& a) {
+    if (a.ab != DType::BFloat16) return false;
+    if (a.K % 8 || a.lda % 8 || a.ldb % 8 || !aligned16(a.A) || !aligned16(a.B)) return false;
+    if (a.transA && a.M % 8) return false;
+    if (!a.transB && a.N % 8) return false;
+    return true;
+}
+
+void gemm(const GemmArgs& a, hipStream_t s) {
+    AIC_CHECK(a.M >= 0 && a.N >= 0 && a.K >= 0, InvalidArgument, "negative GEMM size");
+    AIC_CHECK(a.M < (1LL << 31) && a.N < (1LL << 31) && a.K < (1LL << 31), InvalidArgument, "GEMM size too large");
+    AIC_CHECK(a.A && a.B && a.C, InvalidArgument, "null GEMM operand");
+    AIC_CHECK(a.ab == DType::Float32 || a.ab == DType::BFloat16, DTypeMismatch, "GEMM inputs must be f32 or bf16");
+    AIC_CHECK(a.c == DType::Float32 || a.c == DType::BFloat16, DTypeMismatch, "GEMM output must be f32 or bf16");
+    const int64_t amin = a.transA ? a.M : a.K, bmin = a.transB ? a.K : a.N;
+    AIC_CHECK(a.lda >= (amin > 0 ? amin : 1) && a.ldb >= (bmin > 0 ? bmin : 1) && a.ldc >= (a.N > 0 ? a.N : 1),
+              InvalidArgument, "leading dimension smaller than the row length");
+    if (a.M == 0 || a.N == 0) return;
+    if (gemm_mfma_eligible(a)) {
+        const bool big = a.M >= 2048 && a.N >= 2048 && ((a.M / 256) * (a.N / 256) >= 256);
+        if (a.c == DType::Float32) {
+            if (big) dispatch_trans<256, 256, float>(a, s);
+            else dispatch_trans<128, 128, float>(a, s);
+        } else {
+            if (big) dispatch_trans<256, 256, bf16>(a, s);
+            else dispatch_trans<128, 128, bf16>(a, s);
+        }
+        return;
+    }
+    if (a.ab == DType::Float32) {
+        if (a.c == DType::Float32) launch_simt<float, float>(a, s);
+        else launch_simt<float, bf16>(a, s);
+    } else {
+        if (a.c == DType::Float32) launch_simt<bf16, float>(a, s);
+        else launch_simt<bf16, bf16>(a, s);
+    }
+}
+
+}  // namespace aic::hip

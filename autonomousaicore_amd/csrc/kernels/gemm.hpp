@@ -1,0 +1,37 @@
+// Host interface of the GEMM kernels (see gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../runtime/dtype.hpp"
+
+namespace aic::hip {
+
+// Row-major C[M,N] = alpha * op(A) . op(B) + beta * C + R, fp32 accumulation.
+//   op(A) is M x K: A[m*lda + k], or A[k*lda + m] when transA.
+//   op(B) is K x N: B[k*ldb + n], or B[n*ldb + k] when transB.
+// Linear forward y = x W^T is (transA=0, transB=1); dx = dy W is (0, 0); dW = dy^T x is (1, 0).
+// R (optional, same dtype as C, leading dimension ldr) is added after scaling; beta == 0
+// never reads C.
+struct GemmArgs {
+    int transA = 0, transB = 0;
+    int64_t M = 0, N = 0, K = 0;
+    float alpha = 1.0f, beta = 0.0f;
+    const void* A = nullptr;
+    int64_t lda = 0;
+    const void* B = nullptr;
+    int64_t ldb = 0;
+    void* C = nullptr;
+    int64_t ldc = 0;
+    const void* R = nullptr;
+    int64_t ldr = 0;
+    DType ab = DType::BFloat16;
+    DType c = DType::BFloat16;
+};
+
+bool gemm_mfma_eligible(const GemmArgs& a);
+void gemm(const GemmArgs& a, hipStream_t stream);
+
+}  // namespace aic::hip

@@ -1,0 +1,63 @@
+// Host launchers of the non-GEMM kernels.  All take explicit leading dimensions (elements),
+// enqueue on `s` and throw aic::Error on invalid arguments or launch failure.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../runtime/dtype.hpp"
+
+namespace aic::hip {
+
+// RMSNorm (norm.hip)
+void rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows,
+                 int64_t dim, float eps, DType dt, hipStream_t s);
+void rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                 const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
+                 int64_t dim, DType dt, hipStream_t s);
+
+// RoPE (rope.hip)
+void rope(void* x, int64_t ld, int64_t B, int64_t S, int64_t heads, int64_t hd, int64_t start_pos, const float* cos_t,
+          const float* sin_t, bool inverse, DType dt, hipStream_t s);
+void rope_tables_host(float* cos_t, float* sin_t, int64_t max_seq, int64_t hd, float base);
+
+// SwiGLU activation (swiglu.hip)
+void swiglu_fwd(const void* g, const void* u, int64_t ld_gu, void* h, int64_t ld_h, int64_t T, int64_t f, DType dt,
+                hipStream_t s);
+void swiglu_bwd(const void* g, const void* u, int64_t ld_gu, const void* dh, int64_t ld_h, void* dg, void* du,
+                int64_t ld_d, int64_t T, int64_t f, DType dt, hipStream_t s);
+
+// Cross-entropy (loss.hip)
+void ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+            float* losses, float* lse, float* loss_mean, int64_t* valid, DType dt, hipStream_t s);
+void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+            int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d, DType dt,
+            hipStream_t s);
+
+// Embedding (embedding.hip)
+void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, DType dt, hipStream_t s);
+void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, bool accumulate,
+               DType dt, hipStream_t s);
+
+// Attention (attention.hip)
+void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
+              int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);
+void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
+              int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
+              int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);
+
+// Optimizer tail (optim.hip)
+struct OptimCtl;  // = aic_optim_ctl (include/aic_hip.h)
+void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm, int* nonfinite,
+                       hipStream_t s);
+void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s);
+void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipStream_t s);
+void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
+                 const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps, float wd,
+                 int64_t step, const void* ctl, hipStream_t s);
+void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s);
+void fill_normal(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t s);
+void fill_const(float* dst, int64_t n, float v, hipStream_t s);
+
+}  // namespace aic::hip

@@ -1,0 +1,234 @@
+// Fused log-sum-exp cross-entropy with index targets.
+// Replaces cuda_cross_entropy_forward/backward (src/cuda/cuda_loss.cu:68-190) and the CPU
+// path of src/loss/cross_entropy.cpp:149-290.  One block per row; the mean over valid rows
+// is reduced by a single block in a fixed order (deterministic), and the valid-row count
+// stays on the device (the reference synchronises the host for it, cuda_loss.cu:228-234).
+// A target outside [0, C) that is not ignore_index yields a NaN row loss (the reference
+// throws OutOfRange on the host).
+#include <cmath>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+template <bool PRECISE>
+__device__ __forceinline__ float ex(float x) {
+    if constexpr (PRECISE) return expf(x);
+    else return __expf(x);
+}
+
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(256) void ce_fwd_k(const T* __restrict__ logits, int64_t ldl,
+                                                const int64_t* __restrict__ targets, int C, int64_t ignore_index,
+                                                float* __restrict__ losses, float* __restrict__ lse_out) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    const T* z = logits + row * ldl;
+    float m = -INFINITY, s = 0.0f;
+    for (int j = threadIdx.x; j < C; j += 256) {
+        const float v = ld(z, j);
+        if (v > m) {
+            s = s * ex<PRECISE>(m - v) + 1.0f;
+            m = v;
+        } else {
+            s += ex<PRECISE>(v - m);
+        }
+    }
+    const float M = block_max(m, red);
+    const float part = (m == -INFINITY) ? 0.0f : s * ex<PRECISE>(m - M);
+    const float S = block_sum(part, red);
+    if (threadIdx.x == 0) {
+        const float lse = M + logf(fmaxf(S, 1e-12f));
+        if (lse_out) lse_out[row] = lse;
+        const int64_t t = targets[row];
+        float li = 0.0f;
+        if (t != ignore_index) li = (t >= 0 && t < C) ? lse - ld(z, t) : NAN;
+        if (losses) losses[row] = li;
+    }
+}
+
+// Single block: recomputes the row losses' sum in a fixed order from `losses`.
+__global__ __launch_bounds__(1024) void ce_mean_k(const float* __restrict__ losses,
+                                                  const int64_t* __restrict__ targets, int64_t N,
+                                                  int64_t ignore_index, float* loss_mean, int64_t* valid) {
+    __shared__ double sd[1024];
+    __shared__ long long sc[1024];
+    double acc = 0.0;
+    long long cnt = 0;
+    for (int64_t i = threadIdx.x; i < N; i += 1024) {
+        acc += static_cast<double>(losses[i]);
+        cnt += (targets[i] != ignore_index) ? 1 : 0;
+    }
+    sd[threadIdx.x] = acc;
+    sc[threadIdx.x] = cnt;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            sd[threadIdx.x] += sd[threadIdx.x + o];
+            sc[threadIdx.x] += sc[threadIdx.x + o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const long long v = sc[0];
+        if (valid) *valid = v;
+        if (loss_mean) *loss_mean = v > 0 ? static_cast<float>(sd[0]) / static_cast<float>(v) : 0.0f;
+    }
+}
+
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(256) void ce_bwd_k(const T* logits, int64_t ldl, const int64_t* __restrict__ targets,
+                                                const float* __restrict__ lse, int C, int64_t ignore_index,
+                                                const float* __restrict__ grad, const int64_t* __restrict__ valid,
+                                                T* dl, int64_t ldd) {
+    const int64_t row = blockIdx.x;
+    const int64_t t = targets[row];
+    const T* z = logits + row * ldl;
+    T* d = dl + row * ldd;
+    if (t == ignore_index) {
+        for (int j = threadIdx.x; j < C; j += 256) st(d, j, 0.0f);
+        return;
+    }
+    const int64_t v = *valid;
+    const float scale = v > 0 ? (*grad) / static_cast<float>(v) : 0.0f;
+    const float l = lse[row];
+    for (int j = threadIdx.x; j < C; j += 256) {
+        const float p = ex<PRECISE>(ld(z, j) - l);
+        st(d, j, (p - (j == t ? 1.0f : 0.0f)) * scale);
+    }
+}
+
+// bf16 rows with C % 8 == 0 and 16-byte aligned rows: 8 logits per access.
+__global__ __launch_bounds__(256) void ce_fwd_bf16v(const bf16* __restrict__ logits, int64_t ldl,
+                                                    const int64_t* __restrict__ targets, int C,
+                                                    int64_t ignore_index, float* __restrict__ losses,
+                                                    float* __restrict__ lse_out) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    const bf16* z = logits + row * ldl;
+    float m = -INFINITY, s = 0.0f;
+    for (int j = threadIdx.x * 8; j < C; j += 256 * 8) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(z + j);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+        float mx = v[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, v[i]);
+        if (mx > m) {
+            s *= __expf(m - mx);
+            m = mx;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += __expf(v[i] - m);
+    }
+    const float M = block_max(m, red);
+    const float part = (m == -INFINITY) ? 0.0f : s * __expf(m - M);
+    const float S = block_sum(part, red);
+    if (threadIdx.x == 0) {
+        const float lse = M + logf(fmaxf(S, 1e-12f));
+        if (lse_out) lse_out[row] = lse;
+        const int64_t t = targets[row];
+        float li = 0.0f;
+        if (t != ignore_index) li = (t >= 0 && t < C) ? lse - bf2f(z[t]) : NAN;
+        if (losses) losses[row] = li;
+    }
+}
+
+__global__ __launch_bounds__(256) void ce_bwd_bf16v(const bf16* logits, int64_t ldl,
+                                                    const int64_t* __restrict__ targets, const float* __restrict__ lse,
+                                                    int C, int64_t ignore_index, const float* __restrict__ grad,
+                                                    const int64_t* __restrict__ valid, bf16* dl, int64_t ldd) {
+    const int64_t row = blockIdx.x;
+    const int64_t t = targets[row];
+    const bf16* z = logits + row * ldl;
+    bf16* d = dl + row * ldd;
+    const int64_t v = *valid;
+    const bool ign = (t == ignore_index);
+    const float scale = (v > 0 && !ign) ? (*grad) / static_cast<float>(v) : 0.0f;
+    const float l = ign ? 0.0f : lse[row];
+    for (int j = threadIdx.x * 8; j < C; j += 256 * 8) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(z + j);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xffff0000u);
+            float ga = (__expf(a - l) - (j + 2 * i == t ? 1.0f : 0.0f)) * scale;
+            float gb = (__expf(b - l) - (j + 2 * i + 1 == t ? 1.0f : 0.0f)) * scale;
+            if (ign) ga = gb = 0.0f;
+            o[i] = static_cast<uint32_t>(f2bf_bits(ga)) | (static_cast<uint32_t>(f2bf_bits(gb)) << 16);
+        }
+        *reinterpret_cast<uint4*>(d + j) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+void ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+            float* losses, float* lse, float* loss_mean, int64_t* valid, DType dt, hipStream_t s) {
+    AIC_CHECK(N >= 0 && C > 0 && ld >= C && C < (1LL << 31), InvalidArgument, "ce_fwd: bad shape");
+    AIC_CHECK(N < (1LL << 31), InvalidArgument, "ce_fwd: too many rows");
+    float* tmp = nullptr;
+    DeviceBuffer hold;
+    if (N > 0) {
+        if (!losses && (loss_mean || valid)) {
+            hold = DeviceBuffer(sizeof(float) * N, s);
+            tmp = hold.as<float>();
+        }
+        float* lp = losses ? losses : tmp;
+        const dim3 grid(static_cast<unsigned>(N));
+        if (dt == DType::BFloat16 && C % 8 == 0 && ld % 8 == 0 && a16(logits))
+            hipLaunchKernelGGL(ce_fwd_bf16v, grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld, targets,
+                               static_cast<int>(C), ignore_index, lp, lse);
+        else if (dt == DType::BFloat16)
+            hipLaunchKernelGGL((ce_fwd_k<bf16, false>), grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld,
+                               targets, static_cast<int>(C), ignore_index, lp, lse);
+        else if (dt == DType::Float32)
+            hipLaunchKernelGGL((ce_fwd_k<float, true>), grid, dim3(256), 0, s, static_cast<const float*>(logits), ld,
+                               targets, static_cast<int>(C), ignore_index, lp, lse);
+        else
+            AIC_THROW(DTypeMismatch, "ce_fwd: dtype must be f32 or bf16");
+        AIC_LAUNCH_CHECK("ce_fwd");
+    }
+    if (loss_mean || valid) {
+        const float* lp = losses ? losses : tmp;
+        hipLaunchKernelGGL(ce_mean_k, dim3(1), dim3(1024), 0, s, lp, targets, N, ignore_index, loss_mean, valid);
+        AIC_LAUNCH_CHECK("ce_mean");
+    }
+}
+
+void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+            int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d, DType dt,
+            hipStream_t s) {
+    AIC_CHECK(N >= 0 && C > 0 && ld >= C && ld_d >= C && C < (1LL << 31), InvalidArgument, "ce_bwd: bad shape");
+    AIC_CHECK(grad && valid && lse, InvalidArgument, "ce_bwd: grad, valid and lse are required");
+    if (N == 0) return;
+    const dim3 grid(static_cast<unsigned>(N));
+    if (dt == DType::BFloat16 && C % 8 == 0 && ld % 8 == 0 && ld_d % 8 == 0 && a16(logits) && a16(dlogits))
+        hipLaunchKernelGGL(ce_bwd_bf16v, grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld, targets, lse,
+                           static_cast<int>(C), ignore_index, grad, valid, static_cast<bf16*>(dlogits), ld_d);
+    else if (dt == DType::BFloat16)
+        hipLaunchKernelGGL((ce_bwd_k<bf16, false>), grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld,
+                           targets, lse, static_cast<int>(C), ignore_index, grad, valid, static_cast<bf16*>(dlogits),
+                           ld_d);
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL((ce_bwd_k<float, true>), grid, dim3(256), 0, s, static_cast<const float*>(logits), ld,
+                           targets, lse, static_cast<int>(C), ignore_index, grad, valid, static_cast<float*>(dlogits),
+                           ld_d);
+    else
+        AIC_THROW(DTypeMismatch, "ce_bwd: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("ce_bwd");
+}
+
+}  // namespace aic::hip

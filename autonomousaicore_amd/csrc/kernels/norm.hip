@@ -1,0 +1,219 @@
+// RMSNorm forward/backward as single fused kernels (the reference builds RMSNorm from six
+// primitive ops plus their backward nodes, include/nn/rms_norm.hpp:18-34).
+// HBM-bound: one wave per row, 16-byte vector loads; the weight gradient is reduced
+// per block into per-wave LDS slices and then across blocks in a fixed order
+// (deterministic, no atomics).
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+template <typename T> struct Vec;
+template <> struct Vec<float> { static constexpr int N = 4; };
+template <> struct Vec<bf16> { static constexpr int N = 8; };
+
+// Loads VN consecutive elements as fp32.
+template <typename T, int VN>
+__device__ __forceinline__ void load_vec(const T* p, float* out) {
+    if constexpr (VN == 1) {
+        out[0] = ld(p, 0);
+    } else if constexpr (sizeof(T) == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = __uint_as_float(w[i] << 16);
+            out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+template <typename T, int VN>
+__device__ __forceinline__ void store_vec(T* p, const float* in) {
+    if constexpr (VN == 1) {
+        st(p, 0, in[0]);
+    } else if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(in[0], in[1], in[2], in[3]);
+    } else {
+        uint4 v;
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = static_cast<uint32_t>(f2bf_bits(in[2 * i])) | (static_cast<uint32_t>(f2bf_bits(in[2 * i + 1])) << 16);
+        v.x = w[0]; v.y = w[1]; v.z = w[2]; v.w = w[3];
+        *reinterpret_cast<uint4*>(p) = v;
+    }
+}
+
+template <typename T, int VN>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_k(const T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
+                                                     T* __restrict__ y, int64_t ldy, float* __restrict__ rms,
+                                                     int64_t rows, int dim, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T* xr = x + row * ldx;
+    float ss = 0.0f;
+    for (int j = lane * VN; j < dim; j += 64 * VN) {
+        float v[VN];
+        load_vec<T, VN>(xr + j, v);
+#pragma unroll
+        for (int i = 0; i < VN; ++i) ss += v[i] * v[i];
+    }
+    ss = wave_sum(ss);
+    const float r = sqrtf(ss / static_cast<float>(dim) + eps);
+    const float inv = 1.0f / r;
+    if (lane == 0 && rms) rms[row] = r;
+    T* yr = y + row * ldy;
+    for (int j = lane * VN; j < dim; j += 64 * VN) {
+        float v[VN], o[VN];
+        load_vec<T, VN>(xr + j, v);
+#pragma unroll
+        for (int i = 0; i < VN; ++i) o[i] = (v[i] * inv) * w[j + i];
+        store_vec<T, VN>(yr + j, o);
+    }
+}
+
+constexpr int kBwdRowsPerWave = 4;
+
+// dx and per-block dw partials.  Block = 4 waves; wave w handles rows
+// blockIdx*16 + w*4 .. +3.  dw partial of the block -> part[blockIdx][dim].
+template <typename T, int VN>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_k(const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x,
+                                                     int64_t ldx, const float* __restrict__ w,
+                                                     const float* __restrict__ rms, const T* dres, int64_t ldres,
+                                                     T* dx, int64_t lddx, float* __restrict__ part, int64_t rows,
+                                                     int dim) {
+    extern __shared__ float sdw[];  // [4][dim] when part != nullptr
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (part)
+        for (int j = threadIdx.x; j < 4 * dim; j += 256) sdw[j] = 0.0f;
+    __syncthreads();
+    for (int rr = 0; rr < kBwdRowsPerWave; ++rr) {
+        const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kBwdRowsPerWave + rr;
+        if (row >= rows) break;
+        const T* gr = dy + row * lddy;
+        const T* xr = x + row * ldx;
+        const float r = rms[row];
+        const float inv = 1.0f / r;
+        float dot = 0.0f;
+        for (int j = lane * VN; j < dim; j += 64 * VN) {
+            float gv[VN], xv[VN];
+            load_vec<T, VN>(gr + j, gv);
+            load_vec<T, VN>(xr + j, xv);
+#pragma unroll
+            for (int i = 0; i < VN; ++i) dot += (gv[i] * w[j + i]) * xv[i];
+        }
+        dot = wave_sum(dot);
+        const float coef = dot / (static_cast<float>(dim) * r * r * r);
+        for (int j = lane * VN; j < dim; j += 64 * VN) {
+            float gv[VN], xv[VN], o[VN];
+            load_vec<T, VN>(gr + j, gv);
+            load_vec<T, VN>(xr + j, xv);
+            if (dres) {
+                float rv[VN];
+                load_vec<T, VN>(dres + row * ldres + j, rv);
+#pragma unroll
+                for (int i = 0; i < VN; ++i) o[i] = rv[i] + ((gv[i] * w[j + i]) * inv - xv[i] * coef);
+            } else {
+#pragma unroll
+                for (int i = 0; i < VN; ++i) o[i] = (gv[i] * w[j + i]) * inv - xv[i] * coef;
+            }
+            if (part) {
+#pragma unroll
+                for (int i = 0; i < VN; ++i) sdw[wave * dim + j + i] += gv[i] * (xv[i] * inv);
+            }
+            store_vec<T, VN>(dx + row * lddx + j, o);
+        }
+    }
+    if (!part) return;
+    __syncthreads();
+    for (int j = threadIdx.x; j < dim; j += 256)
+        part[static_cast<int64_t>(blockIdx.x) * dim + j] = ((sdw[j] + sdw[dim + j]) + sdw[2 * dim + j]) + sdw[3 * dim + j];
+}
+
+__global__ void reduce_parts_k(const float* __restrict__ part, int nparts, int dim, float* dw, int accumulate) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= dim) return;
+    float s = 0.0f;
+    for (int b = 0; b < nparts; ++b) s += part[static_cast<int64_t>(b) * dim + j];
+    dw[j] = accumulate ? dw[j] + s : s;
+}
+
+bool vec_ok(const void* p, int64_t ld, int64_t dim, int vn, size_t es) {
+    return (reinterpret_cast<uintptr_t>(p) % (vn * es)) == 0 && ld % vn == 0 && dim % vn == 0;
+}
+
+template <typename T>
+void fwd_t(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows, int64_t dim,
+           float eps, hipStream_t s) {
+    constexpr int VN = Vec<T>::N;
+    const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
+    if (vec_ok(x, ldx, dim, VN, sizeof(T)) && vec_ok(y, ldy, dim, VN, sizeof(T)))
+        hipLaunchKernelGGL((rmsnorm_fwd_k<T, VN>), dim3(grid), dim3(256), 0, s, static_cast<const T*>(x), ldx, w,
+                           static_cast<T*>(y), ldy, rms, rows, static_cast<int>(dim), eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_fwd_k<T, 1>), dim3(grid), dim3(256), 0, s, static_cast<const T*>(x), ldx, w,
+                           static_cast<T*>(y), ldy, rms, rows, static_cast<int>(dim), eps);
+    AIC_LAUNCH_CHECK("rmsnorm_fwd");
+}
+
+template <typename T>
+void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+           const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
+           int64_t dim, hipStream_t s) {
+    constexpr int VN = Vec<T>::N;
+    const int64_t rows_per_block = 4 * kBwdRowsPerWave;
+    const unsigned grid = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
+    float* part = nullptr;
+    if (dw) part = static_cast<float*>(pool_alloc(sizeof(float) * grid * dim, s));
+    const size_t lds = dw ? sizeof(float) * 4 * dim : 0;
+    AIC_CHECK(lds <= 160 * 1024, InvalidArgument, "rmsnorm_bwd: dim too large for the LDS weight-gradient slices");
+    const bool vec = vec_ok(dy, lddy, dim, VN, sizeof(T)) && vec_ok(x, ldx, dim, VN, sizeof(T)) &&
+                     vec_ok(dx, lddx, dim, VN, sizeof(T)) && (!dres || vec_ok(dres, ldres, dim, VN, sizeof(T)));
+    if (vec)
+        hipLaunchKernelGGL((rmsnorm_bwd_k<T, VN>), dim3(grid), dim3(256), lds, s, static_cast<const T*>(dy), lddy,
+                           static_cast<const T*>(x), ldx, w, rms, static_cast<const T*>(dres), ldres,
+                           static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
+    else
+        hipLaunchKernelGGL((rmsnorm_bwd_k<T, 1>), dim3(grid), dim3(256), lds, s, static_cast<const T*>(dy), lddy,
+                           static_cast<const T*>(x), ldx, w, rms, static_cast<const T*>(dres), ldres,
+                           static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
+    AIC_LAUNCH_CHECK("rmsnorm_bwd");
+    if (dw) {
+        hipLaunchKernelGGL(reduce_parts_k, dim3(static_cast<unsigned>((dim + 255) / 256)), dim3(256), 0, s, part,
+                           static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
+        AIC_LAUNCH_CHECK("rmsnorm_bwd reduce");
+        pool_free(part, s);
+    }
+}
+
+}  // namespace
+
+void rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows,
+                 int64_t dim, float eps, DType dt, hipStream_t s) {
+    AIC_CHECK(rows >= 0 && dim > 0 && ldx >= dim && ldy >= dim, InvalidArgument, "rmsnorm_fwd: bad shape");
+    if (rows == 0) return;
+    if (dt == DType::Float32) fwd_t<float>(x, ldx, w, y, ldy, rms, rows, dim, eps, s);
+    else if (dt == DType::BFloat16) fwd_t<bf16>(x, ldx, w, y, ldy, rms, rows, dim, eps, s);
+    else AIC_THROW(DTypeMismatch, "rmsnorm_fwd: dtype must be f32 or bf16");
+}
+
+void rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                 const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
+                 int64_t dim, DType dt, hipStream_t s) {
+    AIC_CHECK(rows >= 0 && dim > 0 && lddy >= dim && ldx >= dim && lddx >= dim, InvalidArgument,
+              "rmsnorm_bwd: bad shape");
+    if (rows == 0) return;
+    if (dt == DType::Float32) bwd_t<float>(dy, lddy, x, ldx, w, rms, dres, ldres, dx, lddx, dw, accumulate, rows, dim, s);
+    else if (dt == DType::BFloat16)
+        bwd_t<bf16>(dy, lddy, x, ldx, w, rms, dres, ldres, dx, lddx, dw, accumulate, rows, dim, s);
+    else AIC_THROW(DTypeMismatch, "rmsnorm_bwd: dtype must be f32 or bf16");
+}
+
+}  // namespace aic::hip

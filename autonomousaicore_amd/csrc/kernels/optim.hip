@@ -1,0 +1,298 @@
+// Optimizer tail of the training step, kept entirely on the device:
+//   grad_sqnorm_multi  global sum of squares (fp64 partials, fixed-order final reduction)
+//                      fused with the non-finite scan of the loss scaler
+//   optim_finalize     one thread: loss-scaler skip/backoff/growth + clip coefficient
+//   adamw_multi        fused AdamW (+ bf16 shadow copy of the updated weights)
+// Replaces clip_grad_norm_ (src/optim/clip_grad.cpp:11-53, one host sync per parameter on
+// the GPU path), DynamicLossScaler::unscale_and_update (src/train/amp.cpp:68-152,
+// cudaMalloc + sync per parameter) and cuda_adamw_step (src/cuda/cuda_adamw.cu:22-89,
+// one launch per parameter).  No host synchronisation is needed between backward and the
+// update.
+#include <cmath>
+
+#include "../../../include/aic_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+constexpr int kNormBlocks = 1024;
+
+__device__ __forceinline__ bool finite_(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
+
+__global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int64_t n, double* part, int* part_nf) {
+    __shared__ double sd[256];
+    __shared__ int sn[256];
+    double acc = 0.0;
+    int nf = 0;
+    const int64_t n4 = ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) ? n / 4 : 0;
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float4 v = g4[i];
+        nf |= !finite_(v.x) | !finite_(v.y) | !finite_(v.z) | !finite_(v.w);
+        acc += static_cast<double>(v.x * v.x + v.y * v.y) + static_cast<double>(v.z * v.z + v.w * v.w);
+    }
+    for (int64_t i = n4 * 4 + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float v = g[i];
+        nf |= !finite_(v);
+        acc += static_cast<double>(v) * static_cast<double>(v);
+    }
+    sd[threadIdx.x] = acc;
+    sn[threadIdx.x] = nf;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            sd[threadIdx.x] += sd[threadIdx.x + o];
+            sn[threadIdx.x] |= sn[threadIdx.x + o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part[blockIdx.x] = sd[0];
+        part_nf[blockIdx.x] = sn[0];
+    }
+}
+
+__global__ __launch_bounds__(1024) void sqnorm_final_k(const double* __restrict__ part, const int* __restrict__ part_nf,
+                                                       int nparts, double* out, int* out_nf) {
+    __shared__ double sd[1024];
+    __shared__ int sn[1024];
+    double acc = 0.0;
+    int nf = 0;
+    for (int i = threadIdx.x; i < nparts; i += 1024) {
+        acc += part[i];
+        nf |= part_nf[i];
+    }
+    sd[threadIdx.x] = acc;
+    sn[threadIdx.x] = nf;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            sd[threadIdx.x] += sd[threadIdx.x + o];
+            sn[threadIdx.x] |= sn[threadIdx.x + o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        *out = sd[0];
+        *out_nf = sn[0];
+    }
+}
+
+__global__ void scale_k(float* g, int64_t n, const float* scale) {
+    const float s = *scale;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        g[i] *= s;
+}
+
+// DynamicLossScaler::unscale_and_update (src/train/amp.cpp:118-152), then clip_grad_norm_
+// (src/optim/clip_grad.cpp:40-50), folded into one multiplier for AdamW.
+__global__ void finalize_k(const double* sqnorm, const int* nonfinite, aic_optim_ctl* c) {
+    const float scale = c->use_scaler ? c->scale : 1.0f;
+    if (c->use_scaler && *nonfinite) {
+        c->skip = 1;
+        c->scale = fmaxf(c->min_scale, c->scale * c->backoff_factor);
+        c->good_steps = 0;
+        c->skipped_steps += 1;
+        c->grad_norm = NAN;
+        c->grad_mult = 0.0f;
+        return;
+    }
+    c->skip = 0;
+    const float inv = 1.0f / scale;
+    const float norm = static_cast<float>(sqrt(*sqnorm) * static_cast<double>(inv));
+    c->grad_norm = norm;
+    float mult = inv;
+    if (c->max_grad_norm > 0.0f) {
+        const float coef = c->max_grad_norm / (norm + 1e-6f);
+        if (coef < 1.0f) mult = inv * coef;
+    }
+    c->grad_mult = mult;
+    c->step += 1;
+    if (c->use_scaler) {
+        c->good_steps += 1;
+        if (c->good_steps >= c->growth_interval) {
+            c->scale = fminf(c->max_scale, c->scale * c->growth_factor);
+            c->good_steps = 0;
+        }
+    }
+}
+
+template <bool BF16COPY>
+__global__ __launch_bounds__(256) void adamw_k(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                                               float* __restrict__ v, bf16* __restrict__ pb, int64_t n, float lr,
+                                               float beta1, float beta2, float eps, float wd, int64_t host_step,
+                                               const aic_optim_ctl* __restrict__ ctl) {
+    float mult = 1.0f;
+    int64_t step = host_step;
+    if (ctl) {
+        if (ctl->skip) return;
+        mult = ctl->grad_mult;
+        step = ctl->step;
+    }
+    const float bc1 = 1.0f - powf(beta1, static_cast<float>(step));
+    const float bc2 = 1.0f - powf(beta2, static_cast<float>(step));
+    const float ob1 = 1.0f - beta1, ob2 = 1.0f - beta2, lrwd = lr * wd;
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(m) |
+                       reinterpret_cast<uintptr_t>(v)) & 15u) == 0 &&
+                     (!BF16COPY || (reinterpret_cast<uintptr_t>(pb) & 7u) == 0);
+    const int64_t n4 = vec ? n / 4 : 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 pp = reinterpret_cast<float4*>(p)[i];
+        const float4 gg = reinterpret_cast<const float4*>(g)[i];
+        float4 mm = reinterpret_cast<float4*>(m)[i];
+        float4 vv = reinterpret_cast<float4*>(v)[i];
+        float* pa = &pp.x;
+        const float* ga = &gg.x;
+        float* ma = &mm.x;
+        float* va = &vv.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float gr = ga[j] * mult;
+            float par = pa[j];
+            par -= lrwd * par;
+            const float m1 = beta1 * ma[j] + ob1 * gr;
+            const float v1 = beta2 * va[j] + ob2 * gr * gr;
+            ma[j] = m1;
+            va[j] = v1;
+            par -= lr * ((m1 / bc1) / (sqrtf(v1 / bc2) + eps));
+            pa[j] = par;
+        }
+        reinterpret_cast<float4*>(p)[i] = pp;
+        reinterpret_cast<float4*>(m)[i] = mm;
+        reinterpret_cast<float4*>(v)[i] = vv;
+        if (BF16COPY) {
+            const uint32_t w0 = static_cast<uint32_t>(f2bf_bits(pp.x)) | (static_cast<uint32_t>(f2bf_bits(pp.y)) << 16);
+            const uint32_t w1 = static_cast<uint32_t>(f2bf_bits(pp.z)) | (static_cast<uint32_t>(f2bf_bits(pp.w)) << 16);
+            reinterpret_cast<uint2*>(pb)[i] = make_uint2(w0, w1);
+        }
+    }
+    for (int64_t i = n4 * 4 + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float gr = g[i] * mult;
+        float par = p[i];
+        par -= lrwd * par;
+        const float m1 = beta1 * m[i] + ob1 * gr;
+        const float v1 = beta2 * v[i] + ob2 * gr * gr;
+        m[i] = m1;
+        v[i] = v1;
+        par -= lr * ((m1 / bc1) / (sqrtf(v1 / bc2) + eps));
+        p[i] = par;
+        if (BF16COPY) pb[i] = f2bf(par);
+    }
+}
+
+__global__ void cast_k(const float* __restrict__ src, bf16* __restrict__ dst, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        dst[i] = f2bf(src[i]);
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__global__ void fill_normal_k(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std) {
+    const uint64_t key = splitmix64(seed);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t c = offset + static_cast<uint64_t>(i);
+        const uint64_t r1 = splitmix64(key ^ (2 * c)), r2 = splitmix64(key ^ (2 * c + 1));
+        const double u1 = (static_cast<double>(r1 >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        const double u2 = static_cast<double>(r2 >> 11) * (1.0 / 9007199254740992.0);
+        const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        dst[i] = mean + std * static_cast<float>(z);
+    }
+}
+
+__global__ void fill_const_k(float* dst, int64_t n, float v) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        dst[i] = v;
+}
+
+}  // namespace
+
+void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm, int* nonfinite,
+                       hipStream_t s) {
+    AIC_CHECK(count >= 0 && sqnorm && nonfinite, InvalidArgument, "grad_sqnorm_multi: bad arguments");
+    int total_blocks = 0;
+    int blocks[4096];
+    AIC_CHECK(count <= 4096, InvalidArgument, "grad_sqnorm_multi: at most 4096 tensors");
+    for (int t = 0; t < count; ++t) {
+        const int64_t nb = (sizes[t] + 256 * 16 - 1) / (256 * 16);
+        blocks[t] = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nb, kNormBlocks)));
+        total_blocks += blocks[t];
+    }
+    DeviceBuffer part(sizeof(double) * std::max(total_blocks, 1) + sizeof(int) * std::max(total_blocks, 1), s);
+    double* pd = part.as<double>();
+    int* pn = reinterpret_cast<int*>(pd + std::max(total_blocks, 1));
+    int off = 0;
+    for (int t = 0; t < count; ++t) {
+        hipLaunchKernelGGL(sqnorm_k, dim3(blocks[t]), dim3(256), 0, s, grads[t], sizes[t], pd + off, pn + off);
+        AIC_LAUNCH_CHECK("grad_sqnorm");
+        off += blocks[t];
+    }
+    hipLaunchKernelGGL(sqnorm_final_k, dim3(1), dim3(1024), 0, s, pd, pn, total_blocks, sqnorm, nonfinite);
+    AIC_LAUNCH_CHECK("grad_sqnorm_final");
+}
+
+void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s) {
+    for (int t = 0; t < count; ++t) {
+        if (sizes[t] == 0) continue;
+        hipLaunchKernelGGL(scale_k, dim3(grid_for(sizes[t], 256, 8192)), dim3(256), 0, s, grads[t], sizes[t], scale);
+        AIC_LAUNCH_CHECK("scale_multi");
+    }
+}
+
+void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipStream_t s) {
+    AIC_CHECK(sqnorm && nonfinite && ctl, InvalidArgument, "optim_finalize: null argument");
+    hipLaunchKernelGGL(finalize_k, dim3(1), dim3(1), 0, s, sqnorm, nonfinite, static_cast<aic_optim_ctl*>(ctl));
+    AIC_LAUNCH_CHECK("optim_finalize");
+}
+
+void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
+                 const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps, float wd,
+                 int64_t step, const void* ctl, hipStream_t s) {
+    for (int t = 0; t < count; ++t) {
+        if (sizes[t] == 0) continue;
+        const unsigned grid = grid_for((sizes[t] + 3) / 4, 256, 16384);
+        const auto* c = static_cast<const aic_optim_ctl*>(ctl);
+        bf16* pb = p_bf16 ? static_cast<bf16*>(p_bf16[t]) : nullptr;
+        if (pb)
+            hipLaunchKernelGGL(adamw_k<true>, dim3(grid), dim3(256), 0, s, p[t], g[t], m[t], v[t], pb, sizes[t], lr,
+                               beta1, beta2, eps, wd, step, c);
+        else
+            hipLaunchKernelGGL(adamw_k<false>, dim3(grid), dim3(256), 0, s, p[t], g[t], m[t], v[t], pb, sizes[t], lr,
+                               beta1, beta2, eps, wd, step, c);
+        AIC_LAUNCH_CHECK("adamw");
+    }
+}
+
+void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(cast_k, dim3(grid_for(n, 256, 16384)), dim3(256), 0, s, src, static_cast<bf16*>(dst), n);
+    AIC_LAUNCH_CHECK("cast_f32_bf16");
+}
+
+void fill_normal(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(fill_normal_k, dim3(grid_for(n, 256, 16384)), dim3(256), 0, s, dst, n, seed, offset, mean, std);
+    AIC_LAUNCH_CHECK("fill_normal");
+}
+
+void fill_const(float* dst, int64_t n, float v, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(fill_const_k, dim3(grid_for(n, 256, 16384)), dim3(256), 0, s, dst, n, v);
+    AIC_LAUNCH_CHECK("fill_const");
+}
+
+}  // namespace aic::hip

@@ -1,0 +1,430 @@
+#include "transformer_lm.hpp"
+
+#include <cmath>
+#include <cstring>
+
+#include "../kernels/gemm.hpp"
+#include "../kernels/kernels.hpp"
+#include "../runtime/error.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::models {
+
+// Device-resident scalars of a step, read back with one copy.
+struct TransformerLM::DevScalars {
+    float loss;
+    float scale_used;
+    int64_t valid;
+    double sqnorm;
+    int nonfinite;
+    int pad;
+    aic_optim_ctl ctl;
+};
+
+namespace {
+
+constexpr int64_t kAlign = 64;  // arena offsets are multiples of 64 elements (256 bytes)
+
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+          const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
+          int64_t ldr = 0, float beta = 0.0f) {
+    const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
+    auto scope = prof.scope(ta ? kGemmWgrad : (tb ? kGemmFwd : kGemmDgrad), 2.0 * M * N * K, es * (M * K + N * K) + ec * M * N * (R ? 2 : 1), s);
+    hip::GemmArgs a;
+    a.transA = ta;
+    a.transB = tb;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.A = A;
+    a.lda = lda;
+    a.B = B;
+    a.ldb = ldb;
+    a.C = C;
+    a.ldc = ldc;
+    a.R = R;
+    a.ldr = ldr;
+    a.beta = beta;
+    a.ab = ab;
+    a.c = c;
+    hip::gemm(a, s);
+}
+
+}  // namespace
+
+TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions& opt) : cfg_(cfg), opt_(opt) {
+    const int64_t V = cfg.vocab_size, d = cfg.hidden_dim, L = cfg.num_layers, H = cfg.num_heads,
+                  f = cfg.intermediate_dim;
+    AIC_CHECK(V > 0 && d > 0 && L > 0 && H > 0 && f > 0 && cfg.max_seq_len > 0, InvalidArgument,
+              "TransformerLM: all sizes must be positive");
+    AIC_CHECK(d % H == 0, InvalidArgument, "d_model (", d, ") must be divisible by n_heads (", H, ")");
+    AIC_CHECK((d / H) % 2 == 0, InvalidArgument, "head_dim must be even for RoPE");
+    AIC_CHECK(cfg.compute == DType::Float32 || cfg.compute == DType::BFloat16, DTypeMismatch,
+              "compute dtype must be f32 or bf16");
+
+    int64_t off = 0;
+    auto add = [&](const std::string& name, std::vector<int64_t> shape) {
+        ParamInfo p;
+        p.name = name;
+        p.shape = shape;
+        p.numel = 1;
+        for (auto s : shape) p.numel *= s;
+        p.offset = off;
+        off = align_up(off + p.numel);
+        params_.push_back(p);
+        return p.offset;
+    };
+    emb_ = add("tok_embeddings.weight", {V, d});
+    for (int64_t l = 0; l < L; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        Layer ly;
+        // q, k, v are adjacent rows of one [3d, d] matrix; gate, up of one [2f, d] matrix.
+        // The alignment padding is zero here because d*d and f*d are multiples of 64 for
+        // d % 8 == 0; otherwise the fused GEMMs below are split.
+        ly.wqkv = add(pre + "attn.q_proj.weight", {d, d});
+        add(pre + "attn.k_proj.weight", {d, d});
+        add(pre + "attn.v_proj.weight", {d, d});
+        ly.wo = add(pre + "attn.out_proj.weight", {d, d});
+        ly.wgu = add(pre + "ffn.gate_proj.weight", {f, d});
+        add(pre + "ffn.up_proj.weight", {f, d});
+        ly.wd = add(pre + "ffn.down_proj.weight", {d, f});
+        ly.n1 = add(pre + "norm1.weight", {d});
+        ly.n2 = add(pre + "norm2.weight", {d});
+        layers_.push_back(ly);
+    }
+    normf_ = add("norm.weight", {d});
+    head_ = cfg.tie_word_embeddings ? emb_ : add("lm_head.weight", {V, d});
+    arena_ = off;
+    AIC_CHECK((d * d) % kAlign == 0 && (f * d) % kAlign == 0, InvalidArgument,
+              "d_model*d_model and d_ffn*d_model must be multiples of 64 (fused q/k/v and gate/up projections)");
+
+    AIC_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    const size_t bytes = sizeof(float) * static_cast<size_t>(arena_);
+    AIC_HIP_CHECK(hipMalloc(&params_dev_, bytes));
+    AIC_HIP_CHECK(hipMalloc(&grads_dev_, bytes));
+    AIC_HIP_CHECK(hipMalloc(&m_dev_, bytes));
+    AIC_HIP_CHECK(hipMalloc(&v_dev_, bytes));
+    AIC_HIP_CHECK(hipMemsetAsync(params_dev_, 0, bytes, stream_));
+    AIC_HIP_CHECK(hipMemsetAsync(grads_dev_, 0, bytes, stream_));
+    AIC_HIP_CHECK(hipMemsetAsync(m_dev_, 0, bytes, stream_));
+    AIC_HIP_CHECK(hipMemsetAsync(v_dev_, 0, bytes, stream_));
+    if (cfg.compute == DType::BFloat16) {
+        AIC_HIP_CHECK(hipMalloc(&low_dev_, sizeof(uint16_t) * static_cast<size_t>(arena_)));
+        AIC_HIP_CHECK(hipMemsetAsync(low_dev_, 0, sizeof(uint16_t) * static_cast<size_t>(arena_), stream_));
+    }
+
+    const int64_t hd = d / H, half = hd / 2;
+    std::vector<float> c(static_cast<size_t>(cfg.max_seq_len * half)), s(c.size());
+    hip::rope_tables_host(c.data(), s.data(), cfg.max_seq_len, hd, cfg.rope_theta);
+    AIC_HIP_CHECK(hipMalloc(&cos_dev_, sizeof(float) * c.size()));
+    AIC_HIP_CHECK(hipMalloc(&sin_dev_, sizeof(float) * s.size()));
+    AIC_HIP_CHECK(hipMemcpy(cos_dev_, c.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice));
+    AIC_HIP_CHECK(hipMemcpy(sin_dev_, s.data(), sizeof(float) * s.size(), hipMemcpyHostToDevice));
+
+    DevScalars init{};
+    init.ctl.scale = opt.use_loss_scaler ? opt.scaler.initial_scale : 1.0f;
+    init.ctl.use_scaler = opt.use_loss_scaler ? 1 : 0;
+    init.ctl.growth_factor = opt.scaler.growth_factor;
+    init.ctl.backoff_factor = opt.scaler.backoff_factor;
+    init.ctl.growth_interval = opt.scaler.growth_interval;
+    init.ctl.min_scale = opt.scaler.min_scale;
+    init.ctl.max_scale = opt.scaler.max_scale;
+    init.ctl.max_grad_norm = opt.max_grad_norm;
+    init.scale_used = init.ctl.scale;
+    AIC_HIP_CHECK(hipMalloc(&dev_, sizeof(DevScalars)));
+    AIC_HIP_CHECK(hipMemcpy(dev_, &init, sizeof(DevScalars), hipMemcpyHostToDevice));
+    const float one = 1.0f;
+    AIC_HIP_CHECK(hipMalloc(&one_dev_, sizeof(float)));
+    AIC_HIP_CHECK(hipMemcpy(one_dev_, &one, sizeof(float), hipMemcpyHostToDevice));
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+TransformerLM::~TransformerLM() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (void* p : {static_cast<void*>(params_dev_), static_cast<void*>(grads_dev_), static_cast<void*>(m_dev_),
+                    static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
+                    static_cast<void*>(dev_), static_cast<void*>(one_dev_)})
+        if (p) (void)hipFree(p);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+int64_t TransformerLM::num_params() const {
+    int64_t n = 0;
+    for (const auto& p : params_) n += p.numel;
+    return n;
+}
+
+void TransformerLM::refresh_low_precision() {
+    if (low_dev_) hip::cast_f32_bf16(params_dev_, low_dev_, arena_, stream_);
+}
+
+const void* TransformerLM::W(int64_t off) const {
+    if (low_dev_) return static_cast<const uint16_t*>(low_dev_) + off;
+    return params_dev_ + off;
+}
+
+void TransformerLM::set_params(const float* host) {
+    // host holds the tensors back to back in arena order, without the alignment padding
+    std::vector<float> full(static_cast<size_t>(arena_), 0.0f);
+    int64_t src = 0;
+    for (const auto& p : params_) {
+        std::memcpy(full.data() + p.offset, host + src, sizeof(float) * static_cast<size_t>(p.numel));
+        src += p.numel;
+    }
+    AIC_HIP_CHECK(hipMemcpyAsync(params_dev_, full.data(), sizeof(float) * full.size(), hipMemcpyHostToDevice, stream_));
+    refresh_low_precision();
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+namespace {
+void gather_host(const float* dev, const std::vector<ParamInfo>& ps, int64_t arena, float* host, hipStream_t s) {
+    std::vector<float> full(static_cast<size_t>(arena));
+    AIC_HIP_CHECK(hipMemcpyAsync(full.data(), dev, sizeof(float) * full.size(), hipMemcpyDeviceToHost, s));
+    AIC_HIP_CHECK(hipStreamSynchronize(s));
+    int64_t dst = 0;
+    for (const auto& p : ps) {
+        std::memcpy(host + dst, full.data() + p.offset, sizeof(float) * static_cast<size_t>(p.numel));
+        dst += p.numel;
+    }
+}
+}  // namespace
+
+void TransformerLM::get_params(float* host) const { gather_host(params_dev_, params_, arena_, host, stream_); }
+void TransformerLM::get_grads(float* host) const { gather_host(grads_dev_, params_, arena_, host, stream_); }
+
+void TransformerLM::get_adam_state(float* m, float* v, int64_t* step) const {
+    if (m) gather_host(m_dev_, params_, arena_, m, stream_);
+    if (v) gather_host(v_dev_, params_, arena_, v, stream_);
+    if (step) {
+        DevScalars h{};
+        AIC_HIP_CHECK(hipMemcpyAsync(&h, dev_, sizeof(h), hipMemcpyDeviceToHost, stream_));
+        AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+        *step = h.ctl.step;
+    }
+}
+
+void TransformerLM::init_normal(uint64_t seed, float std, bool residual_scaling) {
+    const float rs = residual_scaling ? 1.0f / std::sqrt(2.0f * static_cast<float>(cfg_.num_layers)) : 1.0f;
+    uint64_t off = 0;
+    for (const auto& p : params_) {
+        const bool is_norm = p.shape.size() == 1;
+        if (is_norm) {
+            hip::fill_const(params_dev_ + p.offset, p.numel, 1.0f, stream_);
+        } else {
+            const bool resid = p.name.find("out_proj") != std::string::npos ||
+                               p.name.find("down_proj") != std::string::npos;
+            hip::fill_normal(params_dev_ + p.offset, p.numel, seed, off, 0.0f, std * (resid ? rs : 1.0f), stream_);
+        }
+        off += static_cast<uint64_t>(p.numel);
+    }
+    refresh_low_precision();
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, bool backward,
+                                     float* loss_out) {
+    AIC_CHECK(B > 0 && S > 0, InvalidArgument, "batch and sequence must be positive");
+    AIC_CHECK(S <= cfg_.max_seq_len, OutOfRange, "sequence length ", S, " exceeds max_seq_len ", cfg_.max_seq_len);
+    const hipStream_t s = stream_;
+    const DType dt = cfg_.compute;
+    const size_t es = dtype_size(dt);
+    const int64_t T = B * S, d = cfg_.hidden_dim, f = cfg_.intermediate_dim, V = cfg_.vocab_size,
+                  H = cfg_.num_heads, hd = d / H, L = cfg_.num_layers;
+    const float eps = cfg_.rms_norm_eps;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    // causal attention: S(S+1)/2 (query, key) pairs per head, 2 products of 2*hd FLOPs each
+    const double attn_flops = 2.0 * static_cast<double>(B * H) * static_cast<double>(S) * (S + 1) * hd;
+
+    auto act = [&](int64_t elems) { return DeviceBuffer(es * static_cast<size_t>(elems), s); };
+    auto f32 = [&](int64_t elems) { return DeviceBuffer(sizeof(float) * static_cast<size_t>(elems), s); };
+
+    // ---- activations kept for the backward ----
+    DeviceBuffer xs = act((L + 1) * T * d);  // residual stream x_0 .. x_L
+    DeviceBuffer h1 = act(L * T * d), qkv = act(L * T * 3 * d), ob = act(L * T * d), x1 = act(L * T * d),
+                 h2 = act(L * T * d), gu = act(L * T * 2 * f), am = act(L * T * f);
+    DeviceBuffer r1 = f32(L * T), r2 = f32(L * T), lse = f32(L * T * H);
+    DeviceBuffer hf = act(T * d), rf = f32(T), logits = act(T * V), lse_ce = f32(T);
+    auto at = [&](const DeviceBuffer& b, int64_t elem) {
+        return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
+    };
+    auto atf = [&](const DeviceBuffer& b, int64_t elem) { return b.as<float>() + elem; };
+
+    // ---- forward (TransformerLM::forward, src/models/transformer_lm.cpp:50-62) ----
+    {
+        auto _p = prof_.scope(kEmbedFwd, 0.0, 2.0 * es * T * d + 8.0 * T, s);
+        hip::embed_fwd(ids, T, W(emb_), V, d, at(xs, 0), dt, s);
+    }
+    for (int64_t l = 0; l < L; ++l) {
+        const Layer& ly = layers_[l];
+        void* x = at(xs, l * T * d);
+        void* xn = at(xs, (l + 1) * T * d);
+        void* h1l = at(h1, l * T * d);
+        void* qkvl = at(qkv, l * T * 3 * d);
+        void* ol = at(ob, l * T * d);
+        void* x1l = at(x1, l * T * d);
+        void* h2l = at(h2, l * T * d);
+        void* gul = at(gu, l * T * 2 * f);
+        void* aml = at(am, l * T * f);
+        {
+            auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
+            hip::rmsnorm_fwd(x, d, P(ly.n1), h1l, d, atf(r1, l * T), T, d, eps, dt, s);
+        }
+        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, W(ly.wqkv), d, qkvl, 3 * d, dt, dt, s);
+        {
+            auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
+            hip::rope(qkvl, 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, false, dt, s);
+        }
+        {
+            auto _p = prof_.scope(kAttnFwd, attn_flops, 4.0 * es * T * d, s);
+            hip::attn_fwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
+                          d, atf(lse, l * T * H), B, H, S, hd, true, scale, dt, s);
+        }
+        gemm(prof_, 0, 1, T, d, d, ol, d, W(ly.wo), d, x1l, d, dt, dt, s, x, d);
+        {
+            auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
+            hip::rmsnorm_fwd(x1l, d, P(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
+        }
+        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, W(ly.wgu), d, gul, 2 * f, dt, dt, s);
+        {
+            auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
+            hip::swiglu_fwd(gul, static_cast<char*>(gul) + es * f, 2 * f, aml, f, T, f, dt, s);
+        }
+        gemm(prof_, 0, 1, T, d, f, aml, f, W(ly.wd), f, xn, d, dt, dt, s, x1l, d);
+    }
+    void* xL = at(xs, L * T * d);
+    {
+        auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
+        hip::rmsnorm_fwd(xL, d, P(normf_), hf.get(), d, rf.as<float>(), T, d, eps, dt, s);
+    }
+    gemm(prof_, 0, 1, T, V, d, hf.get(), d, W(head_), d, logits.get(), V, dt, dt, s);
+
+    // ---- loss (cross_entropy mean, ignore_index -100, src/loss/cross_entropy.cpp:149-290) ----
+    {
+        auto _p = prof_.scope(kCeFwd, 0.0, es * T * V + 16.0 * T, s);
+        hip::ce_fwd(logits.get(), V, targets, T, V, -100, nullptr, lse_ce.as<float>(), &dev_->loss, &dev_->valid, dt,
+                    s);
+    }
+    if (!backward) {
+        if (loss_out) {
+            AIC_HIP_CHECK(hipMemcpyAsync(loss_out, &dev_->loss, sizeof(float), hipMemcpyDeviceToHost, s));
+            AIC_HIP_CHECK(hipStreamSynchronize(s));
+        }
+        return;
+    }
+
+    // ---- backward (autograd::backward, src/autograd/engine.cpp:116-189, as a fixed schedule) ----
+    AIC_HIP_CHECK(hipMemcpyAsync(&dev_->scale_used, &dev_->ctl.scale, sizeof(float), hipMemcpyDeviceToDevice, s));
+    const float* gscale = opt_.use_loss_scaler ? &dev_->ctl.scale : one_dev_;
+    {
+        auto _p = prof_.scope(kCeBwd, 0.0, 2.0 * es * T * V + 12.0 * T, s);
+        hip::ce_bwd(logits.get(), V, targets, lse_ce.as<float>(), T, V, -100, gscale, &dev_->valid, logits.get(), V, dt,
+                    s);
+    }
+    void* dl = logits.get();
+    DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(T * 2 * f), da = act(T * f);
+    gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
+    gemm(prof_, 0, 0, T, d, V, dl, V, W(head_), d, dh.get(), d, dt, dt, s);
+    {
+        auto _p = prof_.scope(kNormBwd, 0.0, 3.0 * es * T * d + 4.0 * T, s);
+        hip::rmsnorm_bwd(dh.get(), d, xL, d, P(normf_), rf.as<float>(), nullptr, 0, dx.get(), d, G(normf_), false, T,
+                         d, dt, s);
+    }
+    for (int64_t l = L - 1; l >= 0; --l) {
+        const Layer& ly = layers_[l];
+        void* x = at(xs, l * T * d);
+        void* h1l = at(h1, l * T * d);
+        void* qkvl = at(qkv, l * T * 3 * d);
+        void* ol = at(ob, l * T * d);
+        void* x1l = at(x1, l * T * d);
+        void* h2l = at(h2, l * T * d);
+        void* gul = at(gu, l * T * 2 * f);
+        void* aml = at(am, l * T * f);
+        // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
+        gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, f, d, dx.get(), d, W(ly.wd), f, da.get(), f, dt, dt, s);
+        {
+            auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
+            hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
+                            static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
+        }
+        gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, W(ly.wgu), d, dh.get(), d, dt, dt, s);
+        {
+            auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
+            hip::rmsnorm_bwd(dh.get(), d, x1l, d, P(ly.n2), atf(r2, l * T), dx.get(), d, dx.get(), d, G(ly.n2), false,
+                             T, d, dt, s);
+        }
+        // x1 = x + out_proj(attn(rope(q), rope(k), v))
+        gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, d, d, dx.get(), d, W(ly.wo), d, dh.get(), d, dt, dt, s);
+        {
+            auto _p = prof_.scope(kAttnBwd, 2.5 * attn_flops, 8.0 * es * T * d, s);
+            hip::attn_bwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
+                          dh.get(), d, atf(lse, l * T * H), dqkv.get(), static_cast<char*>(dqkv.get()) + es * d,
+                          static_cast<char*>(dqkv.get()) + es * 2 * d, 3 * d, B, H, S, hd, true, scale, dt, s);
+        }
+        {
+            auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
+            hip::rope(dqkv.get(), 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, true, dt, s);
+        }
+        gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, W(ly.wqkv), d, dh.get(), d, dt, dt, s);
+        {
+            auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
+            hip::rmsnorm_bwd(dh.get(), d, x, d, P(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, G(ly.n1), false,
+                             T, d, dt, s);
+        }
+    }
+    {
+        auto _p = prof_.scope(kEmbedBwd, 0.0, es * T * d + 4.0 * V * d + 8.0 * T, s);
+        hip::embed_bwd(ids, T, dx.get(), V, d, G(emb_), cfg_.tie_word_embeddings, dt, s);
+    }
+
+    // ---- optimizer tail: scaler -> clip_grad_norm_ -> AdamW (src/train/trainer.cpp:70-95) ----
+    const float* gp[1] = {grads_dev_};
+    const int64_t sizes[1] = {arena_};
+    {
+        auto _p = prof_.scope(kGradNorm, 0.0, 4.0 * arena_, s);
+        hip::grad_sqnorm_multi(gp, sizes, 1, &dev_->sqnorm, &dev_->nonfinite, s);
+        hip::optim_finalize(&dev_->sqnorm, &dev_->nonfinite, &dev_->ctl, s);
+    }
+    float* pp[1] = {params_dev_};
+    float* mp[1] = {m_dev_};
+    float* vp[1] = {v_dev_};
+    void* lp[1] = {low_dev_};
+    const auto& a = opt_.adamw;
+    {
+        auto _p = prof_.scope(kAdamW, 0.0, (28.0 + (low_dev_ ? 2.0 : 0.0)) * arena_, s);
+        hip::adamw_multi(pp, gp, mp, vp, low_dev_ ? lp : nullptr, sizes, 1, a.lr, a.beta1, a.beta2, a.eps,
+                         a.weight_decay, 0, &dev_->ctl, s);
+    }
+}
+
+void TransformerLM::train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S) {
+    forward_backward(ids, targets, B, S, true, nullptr);
+}
+
+float TransformerLM::eval_loss(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S) {
+    float loss = 0.0f;
+    forward_backward(ids, targets, B, S, false, &loss);
+    return loss;
+}
+
+StepStats TransformerLM::last_stats() {
+    DevScalars h{};
+    AIC_HIP_CHECK(hipMemcpyAsync(&h, dev_, sizeof(h), hipMemcpyDeviceToHost, stream_));
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    StepStats st;
+    st.loss = h.loss;
+    st.grad_norm = h.ctl.grad_norm;
+    st.found_inf = h.ctl.skip != 0;
+    st.loss_scale = h.scale_used;
+    st.step = h.ctl.step;
+    return st;
+}
+
+void TransformerLM::synchronize() { AIC_HIP_CHECK(hipStreamSynchronize(stream_)); }
+
+}  // namespace aic::models

@@ -1,0 +1,136 @@
+// TransformerLM training step on one GPU.
+//
+// Mirrors the reference's model and trainer API (models::TransformerLMConfig and
+// TransformerLM, include/models/transformer_lm.hpp:19-76; optim::AdamWOptions,
+// include/optim/adamw.hpp:12-18; train::DynamicLossScalerOptions,
+// include/train/amp.hpp:34-41; Trainer::step, src/train/trainer.cpp:37-118) and runs the
+// whole step -- forward, cross-entropy, backward, loss scaling, clip_grad_norm_ and AdamW --
+// as one stream of fused HIP kernels:
+//   * parameters, gradients and AdamW moments live in flat fp32 device arenas, one tensor
+//     after another (q/k/v and gate/up adjacent so each pair/triple is one GEMM), with a
+//     bf16 shadow copy of the weights refreshed by the AdamW kernel in AMP mode;
+//   * the residual adds are fused into the out_proj/down_proj GEMM epilogues and the
+//     residual-stream gradient adds into the RMSNorm backward;
+//   * the loss scaler, the clip decision and the AdamW step count stay on the device, so a
+//     step needs no host synchronisation (the reference syncs per parameter).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../../include/aic_hip.h"
+#include "../runtime/dtype.hpp"
+#include "../runtime/profiler.hpp"
+
+namespace aic::models {
+
+struct TransformerLMConfig {
+    int64_t vocab_size = 320;
+    int64_t hidden_dim = 128;
+    int64_t num_layers = 4;
+    int64_t num_heads = 4;
+    int64_t intermediate_dim = 384;
+    int64_t max_seq_len = 512;
+    float rms_norm_eps = 1e-5f;
+    float rope_theta = 10000.0f;
+    bool tie_word_embeddings = false;
+    DType compute = DType::Float32;  // Float32 (reference precision) or BFloat16 (AMP)
+};
+
+struct AdamWOptions {
+    float lr = 1e-3f, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, weight_decay = 0.01f;
+};
+
+struct DynamicLossScalerOptions {
+    float initial_scale = 65536.0f, growth_factor = 2.0f, backoff_factor = 0.5f;
+    int growth_interval = 1000;
+    float min_scale = 1.0f, max_scale = 16777216.0f;
+};
+
+struct TrainOptions {
+    AdamWOptions adamw;
+    float max_grad_norm = 1.0f;
+    bool use_loss_scaler = false;
+    DynamicLossScalerOptions scaler;
+};
+
+struct ParamInfo {
+    std::string name;
+    std::vector<int64_t> shape;
+    int64_t offset = 0;  // elements into the arena
+    int64_t numel = 0;
+};
+
+struct StepStats {
+    float loss = 0.0f;
+    float grad_norm = 0.0f;
+    bool found_inf = false;
+    float loss_scale = 1.0f;
+    int64_t step = 0;
+};
+
+class TransformerLM {
+public:
+    TransformerLM(const TransformerLMConfig& cfg, const TrainOptions& opt);
+    ~TransformerLM();
+    TransformerLM(const TransformerLM&) = delete;
+    TransformerLM& operator=(const TransformerLM&) = delete;
+
+    const TransformerLMConfig& config() const { return cfg_; }
+    const std::vector<ParamInfo>& params() const { return params_; }
+    int64_t arena_elems() const { return arena_; }
+    int64_t num_params() const;
+    hipStream_t stream() const { return stream_; }
+
+    void set_params(const float* host);
+    void get_params(float* host) const;
+    void get_grads(float* host) const;
+    void get_adam_state(float* m, float* v, int64_t* step) const;
+    void init_normal(uint64_t seed, float std, bool residual_scaling);
+
+    // ids/targets: device pointers to [B, S] int64.
+    void train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
+    float eval_loss(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
+    StepStats last_stats();
+    void synchronize();
+
+    // Per-kernel-class HIP-event timing of the following steps (resets when enabled).
+    void set_profiling(bool on) { prof_.enable(on); }
+    std::vector<KernelClassStats> profile_stats() { return prof_.collect(); }
+
+private:
+    struct Layer {
+        int64_t wqkv, wo, wgu, wd, n1, n2;  // arena offsets
+    };
+    struct DevScalars;
+
+    void refresh_low_precision();
+    const void* W(int64_t off) const;  // compute-precision weight at arena offset
+    float* P(int64_t off) const { return params_dev_ + off; }
+    float* G(int64_t off) const { return grads_dev_ + off; }
+    void forward_backward(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, bool backward,
+                          float* loss_out);
+
+    TransformerLMConfig cfg_;
+    TrainOptions opt_;
+    std::vector<ParamInfo> params_;
+    std::vector<Layer> layers_;
+    int64_t emb_ = 0, normf_ = 0, head_ = 0;
+    int64_t arena_ = 0;
+    hipStream_t stream_ = nullptr;
+    float* params_dev_ = nullptr;
+    float* grads_dev_ = nullptr;
+    float* m_dev_ = nullptr;
+    float* v_dev_ = nullptr;
+    void* low_dev_ = nullptr;  // bf16 shadow weights (AMP)
+    float* cos_dev_ = nullptr;
+    float* sin_dev_ = nullptr;
+    DevScalars* dev_ = nullptr;
+    float* one_dev_ = nullptr;
+    Profiler prof_;
+};
+
+}  // namespace aic::models

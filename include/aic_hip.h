@@ -1,0 +1,299 @@
+/*
+ * aic_hip.h -- C-ABI of the MI355X (gfx950) backend for the AutonomousAICore TransformerLM
+ * training step.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, else an aic error code (the numbering of the reference's
+ *     aic::ErrorCode, include/core/error.hpp:13-29; 7 = HIP error); no exception crosses
+ *     the ABI.  aic_hip_last_error() gives the message of the calling thread's last error.
+ *   - pointers are device pointers unless the name says host; sizes are int64_t; row-major
+ *     layouts with explicit leading dimensions (in elements).
+ *   - the caller allocates outputs (as the reference's raw-pointer launchers do,
+ *     e.g. src/ops/flash_attention.cpp:299-300); internal scratch comes from the library's
+ *     stream-ordered pool.
+ *   - `stream` is a hipStream_t (NULL = the null stream); every call is asynchronous with
+ *     respect to the host unless stated.
+ * Each declaration names the reference interface it replaces (paths relative to
+ * AutonomousAICore/ of the reference repository).
+ */
+#ifndef AIC_HIP_H
+#define AIC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types; values equal the reference's aic::DType (include/core/dtype.hpp:18-26). */
+typedef enum {
+    AIC_F32 = 0,
+    AIC_F16 = 1,
+    AIC_BF16 = 2,
+    AIC_I32 = 3,
+    AIC_I64 = 4,
+    AIC_U8 = 5,
+    AIC_U16 = 6
+} aic_dtype;
+
+typedef void* aic_stream; /* hipStream_t */
+
+/* ---------------------------------------------------------------- runtime ---------- */
+/* Message of this thread's last failed call ("" if none).
+ * Replaces: aic::Error::what() of AIC_THROW(CudaError, ...) (include/core/error.hpp:31-48). */
+const char* aic_hip_last_error(void);
+/* Number of visible GPUs (0 without a GPU; never fails).
+ * Replaces: get_cuda_device_count (src/runtime/cuda_info.cpp:15-33). */
+int aic_hip_device_count(void);
+/* Library version string. */
+const char* aic_hip_version(void);
+
+/* Stream-ordered caching allocator over hipMallocAsync on the device's default pool, with
+ * the release threshold raised so freed blocks stay cached.
+ * Replaces: DeviceMemoryPool::allocate_on_stream / deallocate_on_stream
+ * (include/memory/memory_pool.hpp:120-155, src/memory/memory_pool.cpp:182-286). */
+int aic_hip_mem_alloc_async(void** ptr, size_t bytes, aic_stream stream);
+int aic_hip_mem_free_async(void* ptr, aic_stream stream);
+/* Bytes currently allocated through the pool and the high-water mark
+ * (replaces MemoryStats, include/memory/allocator.hpp:14-50). */
+int aic_hip_mem_stats(int64_t* allocated_bytes, int64_t* peak_bytes);
+
+/* ---------------------------------------------------------------- GEMM ------------- */
+/* C[M,N] = alpha * op(A) . op(B) + beta * C + R  (fp32 accumulation).
+ *   op(A): M x K, stored A[m*lda + k], or A[k*lda + m] when transA.
+ *   op(B): K x N, stored B[k*ldb + n], or B[n*ldb + k] when transB.
+ *   ab_type: AIC_BF16 (MFMA path) or AIC_F32; c_type: AIC_BF16 or AIC_F32; R (nullable)
+ *   has c_type and leading dimension ldr; beta == 0 never reads C.
+ * Linear forward y = x W^T is (0, 1); dx = dy W is (0, 0); dW = dy^T x is (1, 0).
+ * Replaces: aic::cuda::gemm_2d / matmul (src/cuda/cuda_gemm.cuh:11-14) and the
+ * MatMulBackward products (src/autograd/functions.cpp:254-273). */
+int aic_hip_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                 const void* B, int64_t ldb, float beta, void* C, int64_t ldc, const void* R, int64_t ldr,
+                 aic_dtype ab_type, aic_dtype c_type, aic_stream stream);
+
+/* ---------------------------------------------------------------- RMSNorm ---------- */
+/* y = x / rms * w with rms = sqrt(mean(x^2) + eps) per row; rms[rows] (fp32) is saved.
+ * x/y have dtype dt (F32 or BF16), leading dimensions ldx/ldy; w is fp32 [dim].
+ * Replaces: the RMSNorm composite (include/nn/rms_norm.hpp:18-34). */
+int aic_hip_rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows,
+                        int64_t dim, float eps, aic_dtype dt, aic_stream stream);
+/* dx = dy*w/rms - x * sum(dy*w*x)/(dim*rms^3) (+ dres if non-NULL, the residual-stream
+ * gradient, fused);  dw (fp32 [dim]) = sum_rows dy*x/rms, overwritten (accumulate = 0) or
+ * added to (accumulate = 1).  dw may be NULL.  dx may alias dres.
+ * Replaces: the backward of the same composite (src/autograd/functions.cpp:60-200). */
+int aic_hip_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                        const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, int accumulate, int64_t rows,
+                        int64_t dim, aic_dtype dt, aic_stream stream);
+
+/* ---------------------------------------------------------------- RoPE ------------- */
+/* In-place half-split rotation of `heads` heads of width hd per row:
+ *   row t = b*S + s (position start_pos + s), head h at x[t*ld + h*hd + i].
+ * inverse = 0: x1' = x1 c - x2 s, x2' = x1 s + x2 c; inverse = 1: the adjoint (backward).
+ * cos_t/sin_t: fp32 [>= start_pos+S, hd/2], as built by aic_hip_rope_tables.
+ * q and k of a fused [T, 3d] projection are rotated by one call with heads = 2*n_heads.
+ * Replaces: RotaryPositionEmbedding::forward and RoPEBackward (include/nn/rope.hpp:23-112). */
+int aic_hip_rope(void* x, int64_t ld, int64_t B, int64_t S, int64_t heads, int64_t hd, int64_t start_pos,
+                 const float* cos_t, const float* sin_t, int inverse, aic_dtype dt, aic_stream stream);
+/* Host: fill host arrays cos_t/sin_t [max_seq, hd/2] exactly as the reference builds its
+ * cache in float (include/nn/rope.hpp:122-144). */
+int aic_hip_rope_tables(float* cos_host, float* sin_host, int64_t max_seq, int64_t hd, float base);
+
+/* ---------------------------------------------------------------- attention -------- */
+/* Causal flash attention forward.  q/k/v rows are tokens t = b*S + s with head h at
+ * column h*hd (leading dimension ld_qkv, e.g. 3*d for a fused QKV projection); o has
+ * leading dimension ld_o; lse [B, H, S] fp32 (natural-log row log-sum-exp of the scaled
+ * scores).  hd in {32, 64, 128}; dt F32 or BF16.
+ * Replaces: launch_flash_attention_forward_gpu (src/cuda/cuda_flash_attention.cuh:12-28)
+ * and the default materialised path (include/nn/attention.hpp:84-119). */
+int aic_hip_attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
+                     int64_t B, int64_t H, int64_t S, int64_t hd, int causal, float scale, aic_dtype dt,
+                     aic_stream stream);
+/* Backward: dq/dk/dv (leading dimension ld_d) from o, do (leading dimension ld_o) and lse.
+ * Deterministic (no atomics).
+ * Replaces: launch_flash_attention_backward_gpu (src/cuda/cuda_flash_attention.cuh:30-46). */
+int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
+                     int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
+                     int64_t S, int64_t hd, int causal, float scale, aic_dtype dt, aic_stream stream);
+
+/* ---------------------------------------------------------------- SwiGLU ----------- */
+/* h = silu(g) * u, silu(x) = x / (1 + exp(-x)); g, u, h [T, f] with leading dims ld_gu, ld_h.
+ * Replaces: silu + mul of SwiGLU::forward (include/nn/swiglu.hpp:21-33). */
+int aic_hip_swiglu_fwd(const void* g, const void* u, int64_t ld_gu, void* h, int64_t ld_h, int64_t T, int64_t f,
+                       aic_dtype dt, aic_stream stream);
+/* dg = dh*u*silu'(g), du = dh*silu(g), silu'(x) = s(1+x(1-s)).
+ * Replaces: SiluBackward + MulBackward (src/autograd/functions.cpp:60-68,167-175). */
+int aic_hip_swiglu_bwd(const void* g, const void* u, int64_t ld_gu, const void* dh, int64_t ld_h, void* dg, void* du,
+                       int64_t ld_d, int64_t T, int64_t f, aic_dtype dt, aic_stream stream);
+
+/* ---------------------------------------------------------------- cross-entropy ---- */
+/* Per-row LSE loss with index targets; losses[N], lse[N] (fp32, may be NULL except lse
+ * when a backward follows); *loss_mean (device fp32) = sum(losses)/valid, *valid (device
+ * int64) = rows with target != ignore_index.  Deterministic.
+ * Replaces: cuda_cross_entropy_forward (src/cuda/cuda_loss.cuh:17-33). */
+int aic_hip_ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                   float* losses, float* lse, float* loss_mean, int64_t* valid, aic_dtype dt, aic_stream stream);
+/* dlogits = (exp(z - lse) - onehot(t)) * (*grad) / (*valid); ignored rows are 0.
+ * grad and valid are device scalars; dlogits may alias logits.
+ * Replaces: cuda_cross_entropy_backward (src/cuda/cuda_loss.cuh:35-52). */
+int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                   int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d,
+                   aic_dtype dt, aic_stream stream);
+
+/* ---------------------------------------------------------------- embedding -------- */
+/* out[i,:] = W[ids[i],:] (zero row for ids outside [0, V)); W/out dtype dt.
+ * Replaces: cuda_embedding_forward (src/cuda/cuda_embedding.cuh:10-18). */
+int aic_hip_embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, aic_dtype dt,
+                      aic_stream stream);
+/* dW[v,:] (fp32) = sum over i with ids[i] == v of dout[i,:], summed in token order
+ * (deterministic; no atomics); overwrite (accumulate = 0: rows of absent ids become 0)
+ * or add (accumulate = 1).
+ * Replaces: cuda_embedding_backward (src/cuda/cuda_embedding.cuh:20-28). */
+int aic_hip_embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, int accumulate,
+                      aic_dtype dt, aic_stream stream);
+
+/* ---------------------------------------------------------------- optimizer -------- */
+/* Sum of squares (fp64) of `count` fp32 gradient buffers, and a non-finite flag, written to
+ * the device scalars *sqnorm and *nonfinite.  grads/sizes are host arrays of device
+ * pointers / element counts.
+ * Replaces: the per-parameter mul + sum + .item() of clip_grad_norm_
+ * (src/optim/clip_grad.cpp:33-37) and launch_has_nan_or_inf_gpu (src/train/amp.cpp:12-15). */
+int aic_hip_grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                              int* nonfinite, aic_stream stream);
+/* grads[i] *= (*scale) for every buffer (device scalar).
+ * Replaces: launch_unscale_gpu (src/train/amp.cpp:12-15) and mul_ of clip_grad_norm_
+ * (src/optim/clip_grad.cpp:45-50). */
+int aic_hip_scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, aic_stream stream);
+
+/* Device-resident optimizer control block: loss scaler state (src/train/amp.cpp:50-152)
+ * and the outputs of the clip decision.  Lives in device memory. */
+typedef struct {
+    float scale;           /* current loss scale (1 when scaling is off) */
+    int good_steps;
+    int skipped_steps;
+    int use_scaler;
+    float growth_factor, backoff_factor;
+    int growth_interval;
+    float min_scale, max_scale;
+    float max_grad_norm;   /* <= 0: no clipping */
+    float grad_norm;       /* out: pre-clip L2 norm of the unscaled gradients */
+    float grad_mult;       /* out: multiplier AdamW applies to the raw gradient (clip/scale) */
+    int skip;              /* out: 1 when a non-finite gradient was found (step skipped) */
+    int step;              /* AdamW step count; finalize increments it when the step is applied */
+} aic_optim_ctl;
+
+/* One thread: from *sqnorm/*nonfinite decide skip / backoff / growth exactly as
+ * DynamicLossScaler::unscale_and_update, then norm = sqrt(sqnorm)/scale and the clip
+ * coefficient max/(norm + 1e-6) when < 1 (clip_grad_norm_), leaving grad_mult =
+ * coef/scale for AdamW, and increments step unless the step is skipped.  The scale used
+ * for this step is the one on entry.
+ * Replaces: the host logic of src/train/amp.cpp:118-152 and src/optim/clip_grad.cpp:40-50. */
+int aic_hip_optim_finalize(const double* sqnorm, const int* nonfinite, aic_optim_ctl* ctl, aic_stream stream);
+
+/* Fused AdamW over `count` tensors (host arrays of device pointers / sizes):
+ *   g' = g * ctl->grad_mult (or g when ctl is NULL); skip everything when ctl->skip;
+ *   the step count is ctl->step when ctl is non-NULL, else `step`;
+ *   p -= lr*wd*p; m = b1 m + (1-b1) g'; v = b2 v + (1-b2) g'^2;
+ *   p -= lr * (m/bc1) / (sqrt(v/bc2) + eps), bc_i = 1 - beta_i^step (float).
+ * p_bf16[i] (nullable entries) receive the bf16 copy of the updated parameter.
+ * Replaces: cuda_adamw_step (src/cuda/cuda_adamw.cuh:10-24), one launch for all tensors. */
+int aic_hip_adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
+                        const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int64_t step, const aic_optim_ctl* ctl, aic_stream stream);
+
+/* fp32 -> bf16 (round to nearest even) copy of n elements. */
+int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream);
+
+/* ---------------------------------------------------------------- TransformerLM ---- */
+/* The whole training step behind the reference's C++ API (TransformerLM::forward,
+ * cross_entropy, Tensor::backward, DynamicLossScaler, clip_grad_norm_, AdamW::step;
+ * src/train/trainer.cpp:37-118), with parameters, gradients and AdamW state in flat
+ * device arenas. */
+typedef struct aic_lm aic_lm;
+
+typedef struct {
+    int64_t vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len;
+    float norm_eps, rope_base;
+    int tied;              /* lm_head shares tok_embeddings.weight */
+    aic_dtype compute;     /* AIC_F32 (reference precision) or AIC_BF16 (AMP: bf16 compute,
+                              fp32 master weights, gradients and AdamW state) */
+} aic_lm_config;
+
+typedef struct {
+    float lr, beta1, beta2, eps, weight_decay;
+    float max_grad_norm;   /* <= 0: no clipping */
+    int use_loss_scaler;
+    float init_scale, growth_factor, backoff_factor;
+    int growth_interval;
+    float min_scale, max_scale;
+} aic_train_config;
+
+typedef struct {
+    float loss;
+    float grad_norm;
+    int found_inf;
+    float loss_scale;      /* scale used by this step */
+    int64_t step;          /* AdamW step count after this step */
+} aic_step_stats;
+
+/* Creates the model on the current device; parameters are zero until set or initialised. */
+int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm** out);
+int aic_lm_destroy(aic_lm* lm);
+int64_t aic_lm_num_params(const aic_lm* lm);
+int aic_lm_num_tensors(const aic_lm* lm);
+/* Name, shape and flat offset of parameter tensor i in named_parameters() order of the
+ * arena (name buffer of name_cap bytes, dims of 2 entries). */
+int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset);
+/* Host <-> device copies of the flat fp32 arenas (synchronous). */
+int aic_lm_set_params(aic_lm* lm, const float* host);
+int aic_lm_get_params(const aic_lm* lm, float* host);
+int aic_lm_get_grads(const aic_lm* lm, float* host);
+int aic_lm_get_adam_state(const aic_lm* lm, float* m_host, float* v_host, int64_t* step);
+/* Synthetic initialisation on the device: N(0, std) for weight matrices and embeddings,
+ * ones for norms; residual projections (out_proj, down_proj) times 1/sqrt(2 L) when
+ * residual_scaling.  Counter-based (splitmix64 + Box-Muller), seed-determined. */
+int aic_lm_init_normal(aic_lm* lm, uint64_t seed, float std, int residual_scaling);
+/* One training step on token ids / targets ([B, S] int64, device pointers when
+ * on_device, else host).  stats (host, nullable): when non-NULL the call synchronises and
+ * fills it; otherwise the step stays asynchronous on the model's stream.
+ * Replaces: Trainer::step (src/train/trainer.cpp:37-118) with a fixed learning rate. */
+int aic_lm_train_step(aic_lm* lm, const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, int on_device,
+                      aic_step_stats* stats);
+/* Loss only (no gradient, no update); synchronous. */
+int aic_lm_eval_loss(aic_lm* lm, const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, int on_device,
+                     float* loss);
+/* The model's HIP stream and a full synchronisation of it. */
+int aic_lm_stream(const aic_lm* lm, aic_stream* stream);
+int aic_lm_synchronize(aic_lm* lm);
+/* Statistics of the last step (synchronises). */
+int aic_lm_last_stats(aic_lm* lm, aic_step_stats* stats);
+
+/* Per-kernel-class timing of the steps run while profiling is enabled: a pair of HIP events
+ * brackets every launch on the model's stream, and each class accumulates its algorithmic
+ * FLOPs (MFMA-bound classes) or HBM bytes (bandwidth-bound classes).  Enabling resets the
+ * accumulators.  No counterpart in the reference (it times only whole steps with
+ * std::chrono, src/train/trainer.cpp:39,100-102). */
+typedef struct {
+    char name[32];
+    int64_t launches;
+    double total_ms;
+    double flops;          /* algorithmic FLOPs summed over launches */
+    double bytes;          /* algorithmic HBM bytes summed over launches */
+    int mfma_bound;        /* 1: judge against the bf16 MFMA peak, 0: against HBM bandwidth */
+} aic_kernel_stat;
+int aic_lm_profile(aic_lm* lm, int enable);
+/* Synchronises, then writes up to cap classes with at least one launch; *n = count. */
+int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n);
+
+/* ---------------------------------------------------------------- synthetic data ---- */
+/* Host-side counter-based generators (splitmix64), shared by the tests and the bench.
+ * Uniform ids in [0, vocab); Zipf(s) ids (P(k) ~ k^-s over ranks k = 1..vocab, id = k-1,
+ * inverse-CDF); N(mean, std) floats via Box-Muller. */
+int aic_synth_uniform_ids(uint64_t seed, int64_t n, int64_t vocab, int64_t* out_host);
+int aic_synth_zipf_ids(uint64_t seed, int64_t n, int64_t vocab, double s, int64_t* out_host);
+int aic_synth_normal(uint64_t seed, int64_t n, float mean, float std, float* out_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,367 @@
+"""GPU parity of each HIP kernel, called through the C-ABI, against the CPU oracle (fp32
+kernels) or the oracle / float64 on bf16-rounded inputs (bf16 kernels).  Tolerances are
+stated per test: fp32 paths at reference precision, bf16 paths at the bf16 rounding level."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+from autonomousaicore_amd import _lib  # noqa: E402
+from tests.gpu_util import bf16_round, call, dev, host, ptr, rel, stream  # noqa: E402
+
+F32, BF16 = _lib.AIC_F32, _lib.AIC_BF16
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.set_device(0)
+
+
+def _gemm(ta, tb, M, N, K, A, B, ab, ct, R=None, alpha=1.0, beta=0.0, C0=None):
+    lda = A.shape[1]
+    ldb = B.shape[1]
+    Cout = C0.clone() if C0 is not None else torch.empty((M, N), dtype=ct, device="cuda")
+    call("aic_hip_gemm", ta, tb, M, N, K, alpha, ptr(A), lda, ptr(B), ldb, beta, ptr(Cout), N, ptr(R),
+         N if R is not None else 0, ab, F32 if ct == torch.float32 else BF16, stream())
+    return Cout
+
+
+def _ref_gemm(ta, tb, A, B):
+    a = A.astype(np.float64)
+    b = B.astype(np.float64)
+    return (a.T if ta else a) @ (b.T if tb else b)
+
+
+# ----------------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 384, 320), (136, 200, 72), (4096, 4096, 128)])
+def test_gemm_bf16_mfma(ta, tb, M, N, K):
+    rng = np.random.default_rng(M + 7 * N + 13 * K + 2 * ta + tb)
+    A = bf16_round(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = bf16_round(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    ref = _ref_gemm(ta, tb, A, B)
+    Ad, Bd = dev(A, torch.bfloat16), dev(B, torch.bfloat16)
+    c32 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32)
+    assert rel(host(c32), ref) < 1e-5  # fp32 accumulation of exact bf16 products
+    c16 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.bfloat16)
+    assert rel(host(c16), ref) < 4e-3  # one bf16 rounding of the result
+
+
+def test_gemm_epilogue_residual_alpha_beta():
+    rng = np.random.default_rng(3)
+    M, N, K = 384, 256, 128
+    A = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    B = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    R = bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    ref = 0.5 * _ref_gemm(0, 1, A, B) + 2.0 * C0 + R
+    out = _gemm(0, 1, M, N, K, dev(A, torch.bfloat16), dev(B, torch.bfloat16), BF16, torch.float32,
+                R=dev(R), alpha=0.5, beta=2.0, C0=dev(C0))
+    assert rel(host(out), ref) < 1e-5
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0)])
+def test_gemm_fp32_matches_oracle(orc, ta, tb):
+    rng = np.random.default_rng(10 + ta + 2 * tb)
+    M, N, K = 96, 160, 136
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    ref = orc.gemm(np.ascontiguousarray(A.T) if ta else A, np.ascontiguousarray(B.T) if tb else B)
+    out = _gemm(ta, tb, M, N, K, dev(A), dev(B), F32, torch.float32)
+    assert rel(host(out), ref) < 1e-6
+
+
+# ----------------------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("dt", [F32, BF16])
+@pytest.mark.parametrize("rows,dim", [(64, 128), (257, 768), (33, 2048), (5, 100)])
+def test_rmsnorm(orc, dt, rows, dim):
+    rng = np.random.default_rng(rows * dim)
+    x = rng.standard_normal((rows, dim)).astype(np.float32) * 1.7
+    w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    dy = rng.standard_normal((rows, dim)).astype(np.float32)
+    dres = rng.standard_normal((rows, dim)).astype(np.float32)
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    if dt == BF16:
+        x, dy, dres = bf16_round(x), bf16_round(dy), bf16_round(dres)
+    y_ref, rms_ref = orc.rmsnorm_fwd(x, w, 1e-6)
+    dx_ref, dw_ref = orc.rmsnorm_bwd(dy, x, w, rms_ref)
+    xd, wd = dev(x, tdt), dev(w)
+    y = torch.empty_like(xd)
+    rms = torch.empty(rows, dtype=torch.float32, device="cuda")
+    call("aic_hip_rmsnorm_fwd", ptr(xd), dim, ptr(wd), ptr(y), dim, ptr(rms), rows, dim, 1e-6, dt, stream())
+    tol = 1e-6 if dt == F32 else 4e-3
+    assert rel(host(y), y_ref) < tol
+    assert rel(host(rms), rms_ref) < 1e-6
+    dyd, dresd = dev(dy, tdt), dev(dres, tdt)
+    dx = torch.empty_like(xd)
+    dw = torch.full((dim,), 7.0, dtype=torch.float32, device="cuda")
+    call("aic_hip_rmsnorm_bwd", ptr(dyd), dim, ptr(xd), dim, ptr(wd), ptr(rms), ptr(dresd), dim, ptr(dx), dim,
+         ptr(dw), 0, rows, dim, dt, stream())
+    assert rel(host(dx), dx_ref + dres) < (1e-5 if dt == F32 else 4e-3)
+    assert rel(host(dw), dw_ref) < 1e-5
+    # accumulate = 1 adds to the existing weight gradient
+    call("aic_hip_rmsnorm_bwd", ptr(dyd), dim, ptr(xd), dim, ptr(wd), ptr(rms), None, 0, ptr(dx), dim, ptr(dw), 1,
+         rows, dim, dt, stream())
+    assert rel(host(dw), 2 * dw_ref) < 1e-5
+    assert rel(host(dx), dx_ref) < (1e-5 if dt == F32 else 4e-3)
+
+
+# ----------------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("dt", [F32, BF16])
+@pytest.mark.parametrize("B,S,H,hd", [(2, 64, 4, 32), (1, 300, 3, 64), (2, 128, 2, 128)])
+def test_rope_on_fused_qkv(orc, dt, B, S, H, hd):
+    rng = np.random.default_rng(S + hd)
+    d = H * hd
+    qkv = rng.standard_normal((B * S, 3 * d)).astype(np.float32)
+    if dt == BF16:
+        qkv = bf16_round(qkv)
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    cos, sin = orc.rope_tables(S + 5, hd)
+    cosd, sind = dev(cos), dev(sin)  # keep both alive: a freed temporary's block is reused
+    x = dev(qkv, tdt)
+    call("aic_hip_rope", ptr(x), 3 * d, B, S, 2 * H, hd, 0, ptr(cosd), ptr(sind), 0, dt, stream())
+    got = host(x)
+    q_ref = orc.rope_fwd(qkv[:, :d], B, S, H, hd)
+    k_ref = orc.rope_fwd(qkv[:, d:2 * d], B, S, H, hd)
+    tol = 1e-6 if dt == F32 else 4e-3
+    assert rel(got[:, :d], q_ref) < tol and rel(got[:, d:2 * d], k_ref) < tol
+    np.testing.assert_array_equal(got[:, 2 * d:], qkv[:, 2 * d:])  # v untouched
+    # inverse rotation restores the input
+    call("aic_hip_rope", ptr(x), 3 * d, B, S, 2 * H, hd, 0, ptr(cosd), ptr(sind), 1, dt, stream())
+    assert rel(host(x), qkv) < (1e-6 if dt == F32 else 8e-3)
+
+
+# ----------------------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_swiglu(orc, dt):
+    rng = np.random.default_rng(21)
+    T, f = 96, 352
+    gu = (3 * rng.standard_normal((T, 2 * f))).astype(np.float32)
+    dh = rng.standard_normal((T, f)).astype(np.float32)
+    if dt == BF16:
+        gu, dh = bf16_round(gu), bf16_round(dh)
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    g, u = np.ascontiguousarray(gu[:, :f]), np.ascontiguousarray(gu[:, f:])
+    gud, dhd = dev(gu, tdt), dev(dh, tdt)
+    h = torch.empty((T, f), dtype=tdt, device="cuda")
+    es = gud.element_size()
+    call("aic_hip_swiglu_fwd", ptr(gud), ptr(gud) + es * f, 2 * f, ptr(h), f, T, f, dt, stream())
+    tol = 1e-6 if dt == F32 else 4e-3
+    assert rel(host(h), orc.swiglu_fwd(g, u)) < tol
+    dgu = torch.empty_like(gud)
+    call("aic_hip_swiglu_bwd", ptr(gud), ptr(gud) + es * f, 2 * f, ptr(dhd), f, ptr(dgu), ptr(dgu) + es * f, 2 * f,
+         T, f, dt, stream())
+    dg_ref, du_ref = orc.swiglu_bwd(g, u, dh)
+    out = host(dgu)
+    assert rel(out[:, :f], dg_ref) < tol * 2 and rel(out[:, f:], du_ref) < tol * 2
+
+
+# ----------------------------------------------------------------------------- cross-entropy
+@pytest.mark.parametrize("dt", [F32, BF16])
+@pytest.mark.parametrize("N,Cn", [(64, 512), (37, 32000), (8, 77)])
+def test_cross_entropy(orc, dt, N, Cn):
+    rng = np.random.default_rng(N + Cn)
+    z = (2 * rng.standard_normal((N, Cn))).astype(np.float32)
+    t = rng.integers(0, Cn, N).astype(np.int64)
+    t[::7] = -100
+    if dt == BF16:
+        z = bf16_round(z)
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    loss_ref, losses_ref, lse_ref, valid_ref = orc.ce_fwd(z, t)
+    zd, td = dev(z, tdt), dev(t)
+    lse = torch.empty(N, dtype=torch.float32, device="cuda")
+    losses = torch.empty(N, dtype=torch.float32, device="cuda")
+    mean = torch.empty(1, dtype=torch.float32, device="cuda")
+    valid = torch.empty(1, dtype=torch.int64, device="cuda")
+    call("aic_hip_ce_fwd", ptr(zd), Cn, ptr(td), N, Cn, -100, ptr(losses), ptr(lse), ptr(mean), ptr(valid), dt,
+         stream())
+    assert int(host(valid)[0]) == valid_ref
+    assert abs(float(host(mean)[0]) - loss_ref) < 1e-5 * abs(loss_ref)
+    assert rel(host(lse), lse_ref) < 1e-6
+    g = torch.tensor([3.0], dtype=torch.float32, device="cuda")
+    d = torch.empty_like(zd)
+    call("aic_hip_ce_bwd", ptr(zd), Cn, ptr(td), ptr(lse), N, Cn, -100, ptr(g), ptr(valid), ptr(d), Cn, dt, stream())
+    d_ref = orc.ce_bwd(z, t, lse_ref, valid_ref, g=3.0)
+    assert rel(host(d), d_ref) < (1e-5 if dt == F32 else 4e-3)
+    assert np.all(host(d)[t == -100] == 0)
+    # in place (dlogits aliases logits)
+    call("aic_hip_ce_bwd", ptr(zd), Cn, ptr(td), ptr(lse), N, Cn, -100, ptr(g), ptr(valid), ptr(zd), Cn, dt,
+         stream())
+    assert rel(host(zd), d_ref) < (1e-5 if dt == F32 else 4e-3)
+
+
+# ----------------------------------------------------------------------------- embedding
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_embedding_gather_bit_exact_and_scatter(orc, dt):
+    rng = np.random.default_rng(31)
+    V, D, N = 1000, 136, 4096
+    W = rng.standard_normal((V, D)).astype(np.float32)
+    if dt == BF16:
+        W = bf16_round(W)
+    ids = np.minimum(rng.zipf(1.1, N) - 1, V - 1).astype(np.int64)
+    ids[5] = -1
+    ids[9] = V  # out of range: zero row, no gradient
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    Wd, idd = dev(W, tdt), dev(ids)
+    out = torch.empty((N, D), dtype=tdt, device="cuda")
+    call("aic_hip_embed_fwd", ptr(idd), N, ptr(Wd), V, D, ptr(out), dt, stream())
+    np.testing.assert_array_equal(host(out), orc.embedding_fwd(ids, W))  # bit-exact gather
+    dout = rng.standard_normal((N, D)).astype(np.float32)
+    if dt == BF16:
+        dout = bf16_round(dout)
+    dd = dev(dout, tdt)
+    dW = torch.full((V, D), 5.0, dtype=torch.float32, device="cuda")
+    call("aic_hip_embed_bwd", ptr(idd), N, ptr(dd), V, D, ptr(dW), 0, dt, stream())
+    ref = orc.embedding_bwd(ids, dout, V)
+    got = host(dW)
+    assert rel(got, ref) < 1e-6
+    assert np.all(got[np.setdiff1d(np.arange(V), ids)] == 0)
+    # deterministic: a second run is bit-identical
+    dW2 = torch.zeros_like(dW)
+    call("aic_hip_embed_bwd", ptr(idd), N, ptr(dd), V, D, ptr(dW2), 0, dt, stream())
+    np.testing.assert_array_equal(host(dW2), got)
+    # accumulate adds to what is there
+    call("aic_hip_embed_bwd", ptr(idd), N, ptr(dd), V, D, ptr(dW2), 1, dt, stream())
+    assert rel(host(dW2), 2 * ref) < 1e-6
+
+
+# ----------------------------------------------------------------------------- attention
+@pytest.mark.parametrize("B,S,H,hd", [(2, 64, 4, 32), (1, 100, 2, 64), (1, 128, 2, 16)])
+def test_attention_fp32_matches_oracle(orc, B, S, H, hd):
+    rng = np.random.default_rng(S * hd)
+    d = H * hd
+    qkv = rng.standard_normal((B * S, 3 * d)).astype(np.float32)
+    q, k, v = (np.ascontiguousarray(qkv[:, i * d:(i + 1) * d]) for i in range(3))
+    do = rng.standard_normal((B * S, d)).astype(np.float32)
+    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd)
+    dq_ref, dk_ref, dv_ref = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
+    x = dev(qkv)
+    o = torch.empty((B * S, d), dtype=torch.float32, device="cuda")
+    lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    sc = 1.0 / np.sqrt(hd)
+    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 4 * d, ptr(x) + 8 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, 1, sc,
+         F32, stream())
+    assert rel(host(o), o_ref) < 1e-5
+    dqkv = torch.empty_like(x)
+    dod = dev(do)
+    call("aic_hip_attn_bwd", ptr(x), ptr(x) + 4 * d, ptr(x) + 8 * d, 3 * d, ptr(o), ptr(dod), d, ptr(lse),
+         ptr(dqkv), ptr(dqkv) + 4 * d, ptr(dqkv) + 8 * d, 3 * d, B, H, S, hd, 1, sc, F32, stream())
+    g = host(dqkv)
+    assert rel(g[:, :d], dq_ref) < 1e-4
+    assert rel(g[:, d:2 * d], dk_ref) < 1e-4
+    assert rel(g[:, 2 * d:], dv_ref) < 1e-4
+
+
+@pytest.mark.parametrize("B,S,H,hd", [(1, 256, 2, 128), (2, 192, 3, 64), (1, 1024, 2, 128), (1, 72, 1, 64)])
+def test_attention_bf16_mfma(orc, B, S, H, hd):
+    rng = np.random.default_rng(S + hd + H)
+    d = H * hd
+    qkv = bf16_round(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+    do = bf16_round(rng.standard_normal((B * S, d)).astype(np.float32))
+    q, k, v = (np.ascontiguousarray(qkv[:, i * d:(i + 1) * d]) for i in range(3))
+    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd)
+    dq_ref, dk_ref, dv_ref = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
+    x = dev(qkv, torch.bfloat16)
+    o = torch.empty((B * S, d), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    sc = 1.0 / np.sqrt(hd)
+    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, 1, sc,
+         BF16, stream())
+    # bf16 P and a bf16 output: errors at the bf16 rounding level
+    assert rel(host(o), o_ref) < 1e-2
+    dqkv = torch.empty_like(x)
+    dod = dev(do, torch.bfloat16)
+    call("aic_hip_attn_bwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
+         ptr(lse), ptr(dqkv), ptr(dqkv) + 2 * d, ptr(dqkv) + 4 * d, 3 * d, B, H, S, hd, 1, sc, BF16, stream())
+    g = host(dqkv)
+    assert rel(g[:, :d], dq_ref) < 2e-2
+    assert rel(g[:, d:2 * d], dk_ref) < 2e-2
+    assert rel(g[:, 2 * d:], dv_ref) < 2e-2
+    # deterministic backward
+    dqkv2 = torch.empty_like(x)
+    call("aic_hip_attn_bwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
+         ptr(lse), ptr(dqkv2), ptr(dqkv2) + 2 * d, ptr(dqkv2) + 4 * d, 3 * d, B, H, S, hd, 1, sc, BF16, stream())
+    np.testing.assert_array_equal(host(dqkv2), g)
+
+
+# ----------------------------------------------------------------------------- optimizer tail
+def test_grad_sqnorm_and_nonfinite():
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal(1_000_003).astype(np.float32)
+    b = rng.standard_normal(77).astype(np.float32)
+    ad, bd = dev(a), dev(b)
+    sq = torch.empty(1, dtype=torch.float64, device="cuda")
+    nf = torch.empty(1, dtype=torch.int32, device="cuda")
+    import ctypes as C
+    ptrs = (C.c_void_p * 2)(ptr(ad), ptr(bd))
+    sizes = (C.c_int64 * 2)(a.size, b.size)
+    call("aic_hip_grad_sqnorm_multi", ptrs, sizes, 2, ptr(sq), ptr(nf), stream())
+    ref = float((a.astype(np.float64) ** 2).sum() + (b.astype(np.float64) ** 2).sum())
+    assert abs(float(host(sq)[0]) - ref) < 1e-9 * ref and int(host(nf)[0]) == 0
+    bd[13] = float("inf")
+    call("aic_hip_grad_sqnorm_multi", ptrs, sizes, 2, ptr(sq), ptr(nf), stream())
+    assert int(host(nf)[0]) == 1
+
+
+def test_adamw_matches_oracle(orc):
+    import ctypes as C
+    rng = np.random.default_rng(42)
+    n = 100_001
+    p = rng.standard_normal(n).astype(np.float32)
+    pm, m, v = p.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    pd, md, vd = dev(p), dev(np.zeros(n, np.float32)), dev(np.zeros(n, np.float32))
+    low = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    for step in (1, 2, 3):
+        g = rng.standard_normal(n).astype(np.float32)
+        orc.adamw(pm, g, m, v, 3e-4, 0.9, 0.95, 1e-8, 0.1, step)
+        gd = dev(g)
+        args = [(C.c_void_p * 1)(ptr(t)) for t in (pd, gd, md, vd, low)]
+        call("aic_hip_adamw_multi", *args, (C.c_int64 * 1)(n), 1, 3e-4, 0.9, 0.95, 1e-8, 0.1, step, None, stream())
+    assert np.max(np.abs(host(pd) - pm)) < 1e-6
+    assert rel(host(md), m) < 1e-6 and rel(host(vd), v) < 1e-6
+    np.testing.assert_array_equal(host(low), bf16_round(host(pd)))
+
+
+def _ctl(**kw):
+    c = _lib.OptimCtl()
+    c.scale, c.use_scaler, c.growth_factor, c.backoff_factor = 1024.0, 1, 2.0, 0.5
+    c.growth_interval, c.min_scale, c.max_scale, c.max_grad_norm = 1000, 1.0, 16777216.0, 0.0
+    for k, val in kw.items():
+        setattr(c, k, val)
+    return c
+
+
+def _finalize(c, sq, nf):
+    import ctypes as C
+    buf = torch.tensor(np.frombuffer(bytes(c), np.uint8).copy(), device="cuda")
+    sqd = torch.tensor([sq], dtype=torch.float64, device="cuda")
+    nfd = torch.tensor([nf], dtype=torch.int32, device="cuda")
+    call("aic_hip_optim_finalize", ptr(sqd), ptr(nfd), ptr(buf), stream())
+    out = _lib.OptimCtl()
+    C.memmove(C.addressof(out), host(buf).astype(np.uint8).tobytes(), C.sizeof(out))
+    return out
+
+
+def test_optim_finalize_scaler_and_clip_semantics(orc):
+    # backoff on non-finite (tests/unit/test_amp.cpp:86-116)
+    c = _finalize(_ctl(), 1.0, 1)
+    assert c.skip == 1 and c.scale == 512.0 and c.skipped_steps == 1 and c.step == 0
+    # growth after growth_interval good steps (tests/unit/test_amp.cpp:118-142)
+    c = _ctl(scale=128.0, growth_interval=3, max_scale=1024.0)
+    seen = []
+    for _ in range(6):
+        c = _finalize(c, 4.0, 0)
+        seen.append(c.scale)
+    assert seen == [128, 128, 256, 256, 256, 512] and c.step == 6
+    # clip: unscaled norm sqrt(91) -> coefficient 5/sqrt(91) (tests/unit/test_optim.cpp:191-207)
+    scale = 4.0
+    c = _finalize(_ctl(scale=scale, max_grad_norm=5.0), 91.0 * scale * scale, 0)
+    assert abs(c.grad_norm - np.sqrt(91)) < 1e-4
+    assert abs(c.grad_mult - (5.0 / (np.sqrt(91) + 1e-6)) / scale) < 1e-7
+    # below the threshold only the unscale remains
+    c = _finalize(_ctl(scale=scale, max_grad_norm=100.0), 91.0 * scale * scale, 0)
+    assert c.grad_mult == 1.0 / scale
