@@ -15,18 +15,19 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// float -> bf16 round-to-nearest-even, NaN -> 0x7FC0 (the reference's float_to_bf16,
-// include/core/dtype.hpp:118-126).
-__device__ __forceinline__ uint16_t f2bf_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+// float -> bf16, round to nearest even: the hardware conversion (v_cvt_pk_bf16_f32 on
+// gfx950), equal to the reference's float_to_bf16 (include/core/dtype.hpp:118-126) for every
+// non-NaN input; a NaN stays a NaN.
+__device__ __forceinline__ bf16 f2bf(float f) { return static_cast<bf16>(f); }
+__device__ __forceinline__ uint16_t f2bf_bits(float f) { return __builtin_bit_cast(uint16_t, f2bf(f)); }
+// Two floats -> packed bf16 pair (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return static_cast<uint32_t>(f2bf_bits(a)) | (static_cast<uint32_t>(f2bf_bits(b)) << 16);
 }
-__device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, f2bf_bits(f)); }
 __device__ __forceinline__ float bf2f(bf16 h) {
     return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
 }

@@ -5,17 +5,21 @@
 // weight transpose copy (op() reads either layout), fp32 accumulation, and the residual add
 // of TransformerBlock (include/nn/transformer_block.hpp:26-36) fused into the epilogue.
 //
-// bf16 path: hand-written CDNA4 kernel on v_mfma_f32_32x32x16_bf16.
+// bf16 path: hand-written CDNA4 kernel on v_mfma_f32_32x32x16_bf16 (gemm_bf16_dma).
 //   * 256 threads = 4 waves arranged 2x2; macro tile BM x BN x 64, each wave BM/2 x BN/2
 //     built from 32x32 MFMA blocks; fp32 accumulators live in AGPRs.
-//   * LDS holds both operands K-contiguous ([row][64] bf16 = 128 B per row), double
-//     buffered, 16-byte chunks XOR-swizzled by (r ^ r>>3) & 7 so that both 8-row and
-//     16-row lane groups of a ds_read_b128 hit distinct banks.
-//   * Operands stored M/N-contiguous in HBM (the dW = dY^T X and dX = dY W orientations)
-//     are transposed in registers on the way into LDS: each thread loads an 8(k) x 8(m)
-//     block with 8 coalesced 16-byte loads and writes 8 K-contiguous 16-byte chunks.
+//   * Operand tiles go from HBM straight into LDS with global_load_lds_dwordx4 (no VGPR
+//     staging), S stages deep; a wave waits only for its own copies of the tile it is about
+//     to read (s_waitcnt vmcnt(N)) and one s_barrier per K step publishes all waves' copies.
+//   * An operand whose K dimension is contiguous in HBM is kept as [rows][64] in LDS with
+//     16-byte chunks XOR-swizzled per row and read with ds_read_b128.  An operand whose
+//     rows are contiguous (dgrad's weight, both wgrad operands) is kept untransposed as
+//     [64][rows] and read with ds_read_b64_tr_b16, which transposes 4x4 blocks of 16-bit
+//     values across each group of 16 lanes; its chunks are XOR-swizzled by 4*(k & 3).
 //   * Blocks are remapped so that each XCD (hardware dispatches block b to XCD b % 8)
 //     works on a contiguous, M-grouped range of tiles and shares A/B panels in its L2.
+// Shapes the DMA kernel cannot take (K % 64 != 0) use gemm_bf16_mfma, which stages tiles
+// through registers (and transposes row-contiguous operands there).
 // fp32 path (the fp32 reference configuration) and odd shapes: a plain SIMT tiled kernel.
 #include "gemm.hpp"
 
@@ -214,6 +218,200 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_mfma(const MfmaParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Direct-to-LDS MFMA kernel.
+// ---------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+__device__ __forceinline__ int swz_rc(int k) { return 4 * (k & 3); }
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt[3:0] in
+// bits 3:0, expcnt 6:4, lgkmcnt 11:8, vmcnt[5:4] in 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One wave's share of a ROWS x 64 tile, copied HBM -> LDS with 1 KB per instruction.
+// KC: K contiguous in HBM, LDS [ROWS][64].  RC: rows contiguous in HBM, LDS [64][ROWS].
+template <int ROWS, bool KC>
+__device__ __forceinline__ void dma_tile(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, int k0, bf16* s) {
+    constexpr int SEGS = ROWS * kBK / 512;  // 512 bf16 = 1 KB per segment
+    constexpr int PER_WAVE = SEGS / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int seg = wave * PER_WAVE + i;
+        const bf16* src;
+        if constexpr (KC) {
+            const int row = seg * 8 + (lane >> 3);
+            const int lc = (lane & 7) ^ swz(row);
+            const int gr = min(row0 + row, nrows - 1);
+            src = g + static_cast<int64_t>(gr) * ld + k0 + lc * 8;
+        } else {
+            constexpr int CPR = ROWS / 8;       // 16-byte chunks per k row
+            constexpr int RPS = 64 / CPR;       // k rows per segment
+            const int k = seg * RPS + lane / CPR;
+            const int lc = (lane % CPR) ^ swz_rc(k);
+            const int gr = min(row0 + lc * 8, nrows - 8);
+            src = g + static_cast<int64_t>(k0 + k) * ld + gr;
+        }
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(s + seg * 512), 16, 0, 0);
+    }
+}
+
+// MFMA operand fragment (8 bf16 along k) for rows rb .. rb+31 of a tile, k step kk.
+template <int ROWS, bool KC>
+__device__ __forceinline__ bf16x8 frag(const bf16* t, int rb, int kk) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (KC) {
+        const int row = rb + (lane & 31);
+        const int c = 2 * kk + (lane >> 5);
+        return *reinterpret_cast<const bf16x8*>(t + row * kBK + ((c ^ swz(row)) << 3));
+    } else {
+        // ds_read_b64_tr_b16: within a group of 16 lanes, output lane i, slot j receives
+        // element i % 4 of the 4 values addressed by source lane 4j + i / 4.  Source lane
+        // s = 4j + q points at k row (kbase + j), columns m0 + 4q .. +3, so output lane i
+        // holds column m0 + i for k rows kbase .. kbase+3.
+        const int g = lane >> 4, s_ = lane & 15, j = s_ >> 2, q = s_ & 3;
+        const int m = rb + 16 * (g & 1) + 4 * q;
+        v4i16_t r[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 16 * kk + 8 * (g >> 1) + 4 * h + j;
+            const bf16* p = t + k * ROWS + (((m >> 3) ^ swz_rc(k)) << 3) + (m & 7);
+            r[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
+        }
+        const uint2 a = __builtin_bit_cast(uint2, r[0]), b = __builtin_bit_cast(uint2, r[1]);
+        return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+    }
+}
+
+// Wait until at most `tiles` later tiles' copies (LPT instructions each) are in flight.
+template <int LPT>
+__device__ __forceinline__ void wait_tiles(int tiles) {
+    if (tiles >= 2) wait_vmcnt<2 * LPT>();
+    else if (tiles == 1) wait_vmcnt<LPT>();
+    else wait_vmcnt<0>();
+}
+
+__device__ __forceinline__ void wait_lds() {
+    // lgkmcnt(0), vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+// Main loop schedule (per wave): fragments are double-buffered in registers; the reads of
+// k step kk+1 are interleaved with the MFMAs of step kk (sched_group_barrier hints).  The
+// barrier that publishes tile kt+1 sits between the MFMAs of steps 2 and 3, so the MFMA
+// pipe keeps working across it; right after it the freed stage receives tile kt+S and the
+// first fragments of tile kt+1 are read while step 3's MFMAs issue.
+template <int BM, int BN, int S, bool TA, bool TB, typename CT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int STAGE = (BM + BN) * kBK;
+    constexpr bool AKC = !TA, BKC = TB;
+    constexpr int LPT = (BM + BN) * kBK / 512 / 4;  // copy instructions per wave per K step
+    constexpr int NREAD = (AKC ? FM : 2 * FM) + (BKC ? FN : 2 * FN);  // LDS reads per k step
+    constexpr int NMF = FM * FN;
+    constexpr int MF_PER_READ = (NMF + NREAD - 1) / NREAD;
+    static_assert(S >= 2 && S <= 4, "stages");
+    extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    auto copy = [&](int tile, int stage) {
+        bf16* dst = smem + stage * STAGE;
+        dma_tile<BM, AKC>(p.A, p.lda, m0, p.M, tile * kBK, dst);
+        dma_tile<BN, BKC>(p.B, p.ldb, n0, p.N, tile * kBK, dst + BM * kBK);
+    };
+    auto read = [&](int stage, int kk, bf16x8* af, bf16x8* bfr) {
+        const bf16* As = smem + stage * STAGE;
+        const bf16* Bs = As + BM * kBK;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = frag<BM, AKC>(As, wm * WM + i * 32, kk);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[j] = frag<BN, BKC>(Bs, wn * WN + j * 32, kk);
+    };
+    auto mma = [&](const bf16x8* af, const bf16x8* bfr) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    };
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < NREAD; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, MF_PER_READ, 0);  // then MFMAs
+        }
+    };
+
+    const int nk = p.K / kBK;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+        if (st < nk) copy(st, st);
+    wait_tiles<LPT>(min(S, nk) - 1);
+    __builtin_amdgcn_s_barrier();
+    bf16x8 fa[2][FM], fb[2][FN];
+    read(0, 0, fa[0], fb[0]);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt % S;
+        read(cur, 1, fa[1], fb[1]);
+        mma(fa[0], fb[0]);
+        interleave();
+        read(cur, 2, fa[0], fb[0]);
+        mma(fa[1], fb[1]);
+        interleave();
+        read(cur, 3, fa[1], fb[1]);
+        mma(fa[0], fb[0]);
+        interleave();
+        wait_lds();  // this wave's reads of stage `cur` are complete
+        if (kt + 1 < nk) wait_tiles<LPT>(min(S - 2, nk - 1 - (kt + 1)));  // tile kt+1 has landed
+        __builtin_amdgcn_s_barrier();
+        if (kt + S < nk) copy(kt + S, cur);
+        if (kt + 1 < nk) read((kt + 1) % S, 0, fa[0], fb[0]);
+        mma(fa[1], fb[1]);
+        interleave();
+    }
+
+    CT* C = static_cast<CT*>(p.C);
+    const CT* R = static_cast<const CT*>(p.R);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WN + j * 32 + (lane & 31);
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (m >= p.M) continue;
+                float v = p.alpha * acc[i][j][e];
+                const int64_t ci = static_cast<int64_t>(m) * p.ldc + n;
+                if (p.beta != 0.0f) v += p.beta * ld(C, ci);
+                if (R) v += ld(R, static_cast<int64_t>(m) * p.ldr + n);
+                st(C, ci, v);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------
 // SIMT tiled GEMM (fp32 configuration, odd shapes).  64x64 tile, 256 threads, 4x4 each.
 // ---------------------------------------------------------------------------------------
 template <typename T, typename CT>
@@ -285,6 +483,36 @@ void launch_mfma(const GemmArgs& a, hipStream_t s) {
     AIC_LAUNCH_CHECK("gemm_bf16_mfma");
 }
 
+template <int BM, int BN, int S, bool TA, bool TB, typename CT>
+void launch_dma(const GemmArgs& a, hipStream_t s) {
+    MfmaParams p;
+    p.A = static_cast<const bf16*>(a.A);
+    p.B = static_cast<const bf16*>(a.B);
+    p.C = a.C;
+    p.R = a.R;
+    p.lda = a.lda; p.ldb = a.ldb; p.ldc = a.ldc; p.ldr = a.ldr;
+    p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
+    p.alpha = a.alpha; p.beta = a.beta;
+    const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
+    constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * kBK * sizeof(uint16_t);
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_dma<BM, BN, S, TA, TB, CT>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        configured = true;
+    }
+    hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, S, TA, TB, CT>), dim3(tiles), dim3(256), lds, s, p);
+    AIC_LAUNCH_CHECK("gemm_bf16_dma");
+}
+
+template <int BM, int BN, int S, typename CT>
+void dispatch_dma(const GemmArgs& a, hipStream_t s) {
+    if (!a.transA && a.transB) launch_dma<BM, BN, S, false, true, CT>(a, s);
+    else if (!a.transA && !a.transB) launch_dma<BM, BN, S, false, false, CT>(a, s);
+    else if (a.transA && !a.transB) launch_dma<BM, BN, S, true, false, CT>(a, s);
+    else launch_dma<BM, BN, S, true, true, CT>(a, s);
+}
+
 template <int BM, int BN, typename CT>
 void dispatch_trans(const GemmArgs& a, hipStream_t s) {
     if (!a.transA && a.transB) launch_mfma<BM, BN, false, true, CT>(a, s);
@@ -315,6 +543,12 @@ bool gemm_mfma_eligible(const GemmArgs& a) {
     return true;
 }
 
+bool gemm_dma_eligible(const GemmArgs& a) {
+    if (!gemm_mfma_eligible(a)) return false;
+    if (a.K % kBK || a.M < 8 || a.N < 8) return false;
+    return true;
+}
+
 void gemm(const GemmArgs& a, hipStream_t s) {
     AIC_CHECK(a.M >= 0 && a.N >= 0 && a.K >= 0, InvalidArgument, "negative GEMM size");
     AIC_CHECK(a.M < (1LL << 31) && a.N < (1LL << 31) && a.K < (1LL << 31), InvalidArgument, "GEMM size too large");
@@ -325,6 +559,17 @@ void gemm(const GemmArgs& a, hipStream_t s) {
     AIC_CHECK(a.lda >= (amin > 0 ? amin : 1) && a.ldb >= (bmin > 0 ? bmin : 1) && a.ldc >= (a.N > 0 ? a.N : 1),
               InvalidArgument, "leading dimension smaller than the row length");
     if (a.M == 0 || a.N == 0) return;
+    if (gemm_dma_eligible(a)) {
+        const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+        if (a.c == DType::Float32) {
+            if (t256 >= 192) dispatch_dma<256, 256, 2, float>(a, s);
+            else dispatch_dma<128, 128, 4, float>(a, s);
+        } else {
+            if (t256 >= 192) dispatch_dma<256, 256, 2, bf16>(a, s);
+            else dispatch_dma<128, 128, 4, bf16>(a, s);
+        }
+        return;
+    }
     if (gemm_mfma_eligible(a)) {
         const bool big = a.M >= 2048 && a.N >= 2048 && ((a.M / 256) * (a.N / 256) >= 256);
         if (a.c == DType::Float32) {

@@ -32,6 +32,7 @@ struct GemmArgs {
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);
+bool gemm_dma_eligible(const GemmArgs& a);
 void gemm(const GemmArgs& a, hipStream_t stream);
 
 }  // namespace aic::hip

@@ -137,12 +137,24 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_k(const T* __restrict__ dy, i
         part[static_cast<int64_t>(blockIdx.x) * dim + j] = ((sdw[j] + sdw[dim + j]) + sdw[2 * dim + j]) + sdw[3 * dim + j];
 }
 
-__global__ void reduce_parts_k(const float* __restrict__ part, int nparts, int dim, float* dw, int accumulate) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= dim) return;
+// dw[j] = sum over partial rows b of part[b][j], in a fixed order: block = 64 columns x 16
+// waves, wave w sums rows w, w+16, ...; the 16 wave sums are then added in wave order.
+__global__ __launch_bounds__(1024) void reduce_parts_k(const float* __restrict__ part, int nparts, int dim, float* dw,
+                                                       int accumulate) {
+    __shared__ float red[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
     float s = 0.0f;
-    for (int b = 0; b < nparts; ++b) s += part[static_cast<int64_t>(b) * dim + j];
-    dw[j] = accumulate ? dw[j] + s : s;
+    if (j < dim)
+        for (int b = wave; b < nparts; b += 16) s += part[static_cast<int64_t>(b) * dim + j];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && j < dim) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += red[w][lane];
+        dw[j] = accumulate ? dw[j] + t : t;
+    }
 }
 
 bool vec_ok(const void* p, int64_t ld, int64_t dim, int vn, size_t es) {
@@ -186,7 +198,7 @@ void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float
                            static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
     AIC_LAUNCH_CHECK("rmsnorm_bwd");
     if (dw) {
-        hipLaunchKernelGGL(reduce_parts_k, dim3(static_cast<unsigned>((dim + 255) / 256)), dim3(256), 0, s, part,
+        hipLaunchKernelGGL(reduce_parts_k, dim3(static_cast<unsigned>((dim + 63) / 64)), dim3(1024), 0, s, part,
                            static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
         AIC_LAUNCH_CHECK("rmsnorm_bwd reduce");
         pool_free(part, s);
