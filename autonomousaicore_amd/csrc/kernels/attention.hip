@@ -6,17 +6,22 @@
 // mathematics: softmax(Q K^T * scale + causal mask) V with the row log-sum-exp saved.
 //
 // bf16 path (head_dim 64 / 128), v_mfma_f32_32x32x16_bf16, wave64:
-//   forward   one block = 128 queries (4 waves x 32), K/V tiles of 64 keys double-buffered
-//             in LDS.  Each wave computes S^T = K Q^T so that a lane owns one query: the row
-//             max/sum need one cross-half exchange (lane ^ 32) and the rescale of the
-//             output accumulator O^T is per lane.  P^T feeds O^T += V^T P^T straight from
-//             the accumulator registers: the MFMA k-order is permuted identically on the A
-//             side (V^T read from a transposed LDS tile with two 8-byte reads).
-//   backward  two kernels, no atomics (deterministic):
-//             dK/dV: one block = 128 keys (4 waves x 32) looping over 64-query tiles; S and
-//             dP are computed as [query x key] so a lane owns a key and P / dS feed
-//             dV^T += dO^T P and dK^T += Q^T dS from registers.
-//             dQ:   one block = 128 queries looping over 64-key tiles (dQ^T += K^T dS^T).
+//   * Q/K/V/dO tiles travel HBM -> LDS with global_load_lds_dwordx4 (no register staging)
+//     into [rows][head_dim] tiles whose 16-byte chunks are XOR-swizzled per row.  Row
+//     operands are read with ds_read_b128; transposed operands (V^T, K^T, Q^T, dO^T) are read
+//     from the same tiles with ds_read_b64_tr_b16, so no transposed copy is kept.
+//   * forward  one block = 128 queries (4 waves x 32).  A wave computes S^T = K Q^T so a
+//              lane owns one query: the row max/sum need one exchange with lane ^ 32 and the
+//              rescale of the output accumulator O^T is per lane.  P^T feeds
+//              O^T += V^T P^T from the accumulator registers (the MFMA k order is permuted
+//              identically on the V^T side).  Masking runs only on diagonal tiles; the scale
+//              is folded into one FMA before exp2; O is rescaled only when a row max grows by
+//              more than 2^8 (values stay below 2^8 otherwise, exactly as rescaling would).
+//   * backward two kernels, no atomics (deterministic):
+//              dK/dV: one block = 128 keys (4 waves x 32) over 64-query tiles; S and dP are
+//              [query x key] so a lane owns a key and P / dS feed dV^T += dO^T P and
+//              dK^T += Q^T dS from registers.
+//              dQ:   one block = 128 queries over 64-key tiles (dQ^T += K^T dS^T).
 // fp32 path (the fp32 reference configuration, head_dim <= 64): SIMT kernels, fp32 math.
 #include <algorithm>
 #include <cmath>
@@ -31,226 +36,224 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazyRescale = 8.0f;  // log2 units
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 // ---------------------------------------------------------------------------------------
-// LDS layouts
-//   row-major "K-contiguous" tile [rows][HD]: 16-byte chunks XOR-swizzled per row
-//   transposed tile [HD][64]: 8-byte chunks XOR-swizzled per row
+// [rows][HD] bf16 tiles in LDS.  Chunk swizzle: 16 consecutive rows map one logical chunk
+// to 16 distinct 16-byte bank slots (ds_read_b128, lane = row), and 4 consecutive rows map
+// a chunk pair to 4 distinct 32-byte slots (ds_read_b64_tr_b16).
 // ---------------------------------------------------------------------------------------
 template <int HD>
-__device__ __forceinline__ int swz16(int row) {
-    constexpr int NC = HD / 8;
-    constexpr int SH = NC == 16 ? 4 : (NC == 8 ? 3 : 2);
-    return (row ^ (row >> SH)) & (NC - 1);
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (HD == 128) return 2 * (row & 7) | ((row >> 3) & 1);
+    else return 2 * ((row >> 1) & 3) | ((row >> 3) & 1);
 }
-__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 4)) & 15; }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// This wave's quarter of a 64 x HD tile: rows [row0, row0 + 64) of a [tokens][ld] matrix
+// (head offset applied by the caller), rows >= nrows clamped (their values are never used).
 template <int HD>
-__device__ __forceinline__ bf16x8 read_row_frag(const bf16* t, int row, int chunk) {
-    return *reinterpret_cast<const bf16x8*>(t + row * HD + ((chunk ^ swz16<HD>(row)) << 3));
-}
-// A-operand fragment from a transposed [HD][64] tile for the permuted 16-wide k-step ks:
-// elements 0..3 = columns 16ks + 4h + (0..3), elements 4..7 = columns 16ks + 8 + 4h + (0..3).
-__device__ __forceinline__ bf16x8 read_t_frag(const bf16* t, int row, int ks, int h) {
-    const int ca = 4 * ks + h, cb = 4 * ks + 2 + h;
-    const int sw = swz8(row);
-    const uint2 a = *reinterpret_cast<const uint2*>(t + row * 64 + ((ca ^ sw) << 2));
-    const uint2 b = *reinterpret_cast<const uint2*>(t + row * 64 + ((cb ^ sw) << 2));
-    uint4 r = make_uint4(a.x, a.y, b.x, b.y);
-    return __builtin_bit_cast(bf16x8, r);
-}
-
-__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
-// 8 rows x 8 columns (16 bytes per row) held as r[0..7] -> write column block into a
-// transposed [HD][64] tile: output row (col0 + j) gets the 8 values r[0..7][j] at tile
-// columns row0 .. row0+7.
-__device__ __forceinline__ void store_transposed8(bf16* t, const uint4* r, int col0, int row0) {
+__device__ __forceinline__ void dma_rows64(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, bf16* s) {
+    constexpr int NC = HD / 8, RPS = 64 / NC;  // chunks per row, rows per 1 KB segment
+    constexpr int PER_WAVE = 64 * HD / 512 / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t w0 = __builtin_amdgcn_perm(word(r[1], j >> 1), word(r[0], j >> 1), sel);
-        const uint32_t w1 = __builtin_amdgcn_perm(word(r[3], j >> 1), word(r[2], j >> 1), sel);
-        const uint32_t w2 = __builtin_amdgcn_perm(word(r[5], j >> 1), word(r[4], j >> 1), sel);
-        const uint32_t w3 = __builtin_amdgcn_perm(word(r[7], j >> 1), word(r[6], j >> 1), sel);
-        const int row = col0 + j;
-        const int sw = swz8(row);
-        const int c = row0 >> 2;  // 8-byte chunk index of the first 4 columns
-        *reinterpret_cast<uint2*>(t + row * 64 + ((c ^ sw) << 2)) = make_uint2(w0, w1);
-        *reinterpret_cast<uint2*>(t + row * 64 + (((c + 1) ^ sw) << 2)) = make_uint2(w2, w3);
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int seg = wave * PER_WAVE + i;
+        const int row = seg * RPS + lane / NC;
+        const int lc = (lane % NC) ^ swz<HD>(row);
+        const int gr = min(row0 + row, nrows - 1);
+        __builtin_amdgcn_global_load_lds(g + static_cast<int64_t>(gr) * ld + lc * 8, (lds_void_t*)(s + seg * 512), 16,
+                                         0, 0);
     }
 }
 
-__device__ __forceinline__ bf16x8 pack_bf16x8(const f32x16& a, int off) {
-    bf16x8 r;
+// Row operand (lane = row rb + lane%32, 8 values of k step kk along head_dim).
+template <int HD>
+__device__ __forceinline__ bf16x8 row_frag(const bf16* t, int rb, int kk) {
+    const int lane = threadIdx.x & 63;
+    const int row = rb + (lane & 31);
+    const int c = 2 * kk + (lane >> 5);
+    return *reinterpret_cast<const bf16x8*>(t + row * HD + ((c ^ swz<HD>(row)) << 3));
+}
+
+// Transposed operand: lane = head_dim column cb + lane%32, 8 values along rows in the
+// permuted order of a 16-row step ks (elements 0..3: rows 16ks + 4h + 0..3, elements 4..7:
+// rows 16ks + 8 + 4h + 0..3, h = lane / 32), read with ds_read_b64_tr_b16: within a group
+// of 16 lanes, output lane i slot j takes element i % 4 of the 4 values at source lane
+// 4j + i / 4, so source lane s = 4j + q addresses row (base + j), columns cb' + 4q .. +3.
+template <int HD>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* t, int cb, int ks) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, h = lane >> 5, s = lane & 15, j = s >> 2, q = s & 3;
+    const int col = cb + 16 * (g & 1) + 4 * q;
+    v4i16_t r[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = f2bf(a[off + i]);
-    return r;
+    for (int u = 0; u < 2; ++u) {
+        const int row = 16 * ks + 8 * u + 4 * h + j;
+        const bf16* p = t + row * HD + (((col >> 3) ^ swz<HD>(row)) << 3) + (col & 7);
+        r[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
+    }
+    const uint2 a = __builtin_bit_cast(uint2, r[0]), b = __builtin_bit_cast(uint2, r[1]);
+    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+__device__ __forceinline__ bf16x8 pack_bf16x8(const f32x16& a, int off) {
+    return __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(a[off], a[off + 1]), pack_bf16x2(a[off + 2], a[off + 3]),
+                                                 pack_bf16x2(a[off + 4], a[off + 5]),
+                                                 pack_bf16x2(a[off + 6], a[off + 7])));
 }
 
 __device__ __forceinline__ uint4 ldg16(const bf16* p, bool ok) {
     return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
 }
 
+__device__ __forceinline__ void zero(f32x16& a) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) a[e] = 0.0f;
+}
+
+// Writes a [32 rows of head_dim] x [lane = token] accumulator block as token rows.
+__device__ __forceinline__ void store_t(bf16* row_ptr, const f32x16& acc, int ob, float mul) {
+    const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int d0 = ob * 32 + 8 * g + 4 * h;
+        *reinterpret_cast<uint2*>(row_ptr + d0) =
+            make_uint2(pack_bf16x2(acc[4 * g] * mul, acc[4 * g + 1] * mul),
+                       pack_bf16x2(acc[4 * g + 2] * mul, acc[4 * g + 3] * mul));
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------
 template <int HD>
-__global__ __launch_bounds__(256, 1) void attn_fwd_mfma(const bf16* __restrict__ q, const bf16* __restrict__ k,
+__global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                         const bf16* __restrict__ v, int64_t ldq, bf16* __restrict__ o,
-                                                        int64_t ldo, float* __restrict__ lse, int H, int S,
-                                                        float scale_log2, int causal) {
-    constexpr int BQ = 128, BKV = 64, NC = HD / 8, KS = HD / 16, OB = HD / 32;
-    __shared__ __attribute__((aligned(16))) bf16 sK[2][BKV * HD];
-    __shared__ __attribute__((aligned(16))) bf16 sVt[2][HD * BKV];
+                                                        int64_t ldo, float* __restrict__ lse, int H, int S, float c,
+                                                        int causal) {
+    constexpr int BQ = 128, BKV = 64, KS = HD / 16, OB = HD / 32, TILE = BKV * HD;
+    constexpr int LPT = 2 * (64 * HD / 512 / 4);  // K and V copy instructions per wave per tile
+    __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];  // per stage: K then V
 
     const int nq = (S + BQ - 1) / BQ;
     const int qb = nq - 1 - static_cast<int>(blockIdx.x);
     const int h = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
-    const int q0 = qb * BQ;
-    const int qw = q0 + wave * 32;
-    const int myq = qw + (lane & 31);
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
-    const bf16* kb = k + tok0 * ldq + static_cast<int64_t>(h) * HD;
-    const bf16* vb = v + tok0 * ldq + static_cast<int64_t>(h) * HD;
+    const int q0 = qb * BQ, qw = q0 + wave * 32, myq = qw + (lane & 31);
+    const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
+    const bf16* kb = k + tok0 * ldq + hoff;
+    const bf16* vb = v + tok0 * ldq + hoff;
 
     bf16x8 qf[KS];
     {
-        const bf16* qp = q + (tok0 + myq) * ldq + static_cast<int64_t>(h) * HD + 8 * hl;
+        const bf16* qp = q + (tok0 + myq) * ldq + hoff + 8 * hl;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, ldg16(qp + 16 * kk, myq < S));
     }
-
     f32x16 oacc[OB];
 #pragma unroll
-    for (int i = 0; i < OB; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[i][e] = 0.0f;
+    for (int i = 0; i < OB; ++i) zero(oacc[i]);
     float m_run = -INFINITY, l_run = 0.0f;
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
     const int ntiles = (kv_end + BKV - 1) / BKV;
-
-    // loaders: K rows (NC/4 chunks per thread); V 8x8 blocks (threads < 8*NC)
-    constexpr int KCH = BKV * NC / 256;
-    uint4 rk[KCH], rv[8];
-    auto gload = [&](int t) {
-        const int k0 = t * BKV;
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = threadIdx.x + 256 * i;
-            const int row = c / NC, ch = c % NC;
-            rk[i] = ldg16(kb + static_cast<int64_t>(k0 + row) * ldq + ch * 8, k0 + row < S);
-        }
-        if (threadIdx.x < 8 * NC) {
-            const int kg = threadIdx.x & 7, hc = threadIdx.x >> 3;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int key = k0 + kg * 8 + i;
-                rv[i] = ldg16(vb + static_cast<int64_t>(key) * ldq + hc * 8, key < S);
-            }
-        }
+    auto copy = [&](int t, int st) {
+        dma_rows64<HD>(kb, ldq, t * BKV, S, sm[st]);
+        dma_rows64<HD>(vb, ldq, t * BKV, S, sm[st] + TILE);
     };
-    auto sstore = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = threadIdx.x + 256 * i;
-            const int row = c / NC, ch = c % NC;
-            *reinterpret_cast<uint4*>(&sK[st][row * HD + ((ch ^ swz16<HD>(row)) << 3)]) = rk[i];
-        }
-        if (threadIdx.x < 8 * NC) {
-            const int kg = threadIdx.x & 7, hc = threadIdx.x >> 3;
-            store_transposed8(sVt[st], rv, hc * 8, kg * 8);
-        }
-    };
-
-    if (ntiles > 0) {
-        gload(0);
-        sstore(0);
-    }
-    __syncthreads();
+    if (ntiles > 0) copy(0, 0);
+    if (ntiles > 1) copy(1, 1);
 
     for (int t = 0; t < ntiles; ++t) {
         const int st = t & 1;
-        if (t + 1 < ntiles) gload(t + 1);
+        if (t + 1 < ntiles) wait_vmcnt<LPT>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
         const int k0 = t * BKV;
-        const bool active = !causal || (k0 <= qw + 31);
-        if (active) {
+        const bf16* Ks = sm[st];
+        const bf16* Vs = sm[st] + TILE;
+        if (!causal || k0 <= qw + 31) {
             f32x16 s[2];
+            zero(s[0]);
+            zero(s[1]);
 #pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
+            for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) s[jb][e] = 0.0f;
+                for (int jb = 0; jb < 2; ++jb)
+                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Ks, jb * 32, kk), qf[kk], s[jb], 0, 0,
+                                                                     0);
+            // s[jb][e]: raw score of key k0 + 32jb + 8(e/4) + 4hl + e%4 and query myq
+            const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S;
+            if (diag) {
 #pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
+                for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-                for (int jb = 0; jb < 2; ++jb) {
-                    const bf16x8 kf = read_row_frag<HD>(sK[st], jb * 32 + (lane & 31), 2 * kk + hl);
-                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[jb], 0, 0, 0);
-                }
+                    for (int e = 0; e < 16; ++e) {
+                        const int key = k0 + jb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
+                        if ((causal && key > myq) || key >= S) s[jb][e] = -INFINITY;
+                    }
             }
-            float mx = -INFINITY;
+            float mx = s[0][0];
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + jb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-                    float x = s[jb][e] * scale_log2;
-                    if ((causal && key > myq) || key >= S) x = -INFINITY;
-                    s[jb][e] = x;
-                    mx = fmaxf(mx, x);
-                }
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[jb][e]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            // lazy rescale: move the reference max only when it grows by more than 2^8
+            const bool grow = (mx - m_run) * c > kLazyRescale;
+            if (__any(grow)) {
+                const float m_new = grow ? mx : m_run;
+                const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * c);
+                l_run *= alpha;
+#pragma unroll
+                for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) oacc[ob][e] *= alpha;
+                m_run = m_new;
+            }
+            const float moff = -m_run * c;
             float rs = 0.0f;
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = (s[jb][e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[jb][e] - m_new);
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, moff));
                     s[jb][e] = p;
                     rs += p;
                 }
             rs += __shfl_xor(rs, 32, 64);
-            l_run = l_run * alpha + rs;
-            m_run = m_new;
-#pragma unroll
-            for (int ob = 0; ob < OB; ++ob)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) oacc[ob][e] *= alpha;
+            l_run += rs;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 pf = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
 #pragma unroll
-                for (int ob = 0; ob < OB; ++ob) {
-                    const bf16x8 vf = read_t_frag(sVt[st], ob * 32 + (lane & 31), ks, hl);
-                    oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[ob], 0, 0, 0);
-                }
+                for (int ob = 0; ob < OB; ++ob)
+                    oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Vs, ob * 32, ks), pf, oacc[ob], 0, 0,
+                                                                        0);
             }
         }
-        if (t + 1 < ntiles) sstore(st ^ 1);
-        __syncthreads();
+        wait_lds();
+        __builtin_amdgcn_s_barrier();  // everyone is done with stage st
+        if (t + 2 < ntiles) copy(t + 2, st);
     }
 
     if (myq < S) {
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-        bf16* op = o + (tok0 + myq) * ldo + static_cast<int64_t>(h) * HD;
+        bf16* op = o + (tok0 + myq) * ldo + hoff;
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = ob * 32 + 8 * g + 4 * hl;
-                const uint32_t w0 = static_cast<uint32_t>(f2bf_bits(oacc[ob][4 * g] * inv)) |
-                                    (static_cast<uint32_t>(f2bf_bits(oacc[ob][4 * g + 1] * inv)) << 16);
-                const uint32_t w1 = static_cast<uint32_t>(f2bf_bits(oacc[ob][4 * g + 2] * inv)) |
-                                    (static_cast<uint32_t>(f2bf_bits(oacc[ob][4 * g + 3] * inv)) << 16);
-                *reinterpret_cast<uint2*>(op + d0) = make_uint2(w0, w1);
-            }
-        if (hl == 0) lse[(static_cast<int64_t>(b) * H + h) * S + myq] = (m_run + log2f(l_run)) * kLn2;
+        for (int ob = 0; ob < OB; ++ob) store_t(op, oacc[ob], ob, inv);
+        if (hl == 0) lse[(static_cast<int64_t>(b) * H + h) * S + myq] = (m_run * c + log2f(l_run)) * kLn2;
     }
 }
 
@@ -276,37 +279,26 @@ __global__ __launch_bounds__(256) void attn_dot_k(const T* __restrict__ o, const
 }
 
 // ---------------------------------------------------------------------------------------
-// Backward: dK, dV
+// Backward: dK, dV.  Stage = Q tile, dO tile (64 x HD each), lse and D of the 64 queries.
 // ---------------------------------------------------------------------------------------
-template <int HD>
-struct BwdKVSmem {
-    bf16 q[64 * HD];
-    bf16 qt[HD * 64];
-    bf16 dO[64 * HD];
-    bf16 dOt[HD * 64];
-    float lse2[64];
-    float D[64];
-};
-
 template <int HD>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ldq,
     const bf16* __restrict__ dout, int64_t ldo, const float* __restrict__ lse, const float* __restrict__ Dg,
-    bf16* __restrict__ dk, bf16* __restrict__ dv, int64_t ldd, int H, int S, float scale_log2, float scale,
-    int causal) {
-    constexpr int BQ = 64, BKV = 128, NC = HD / 8, KS = HD / 16, OB = HD / 32;
-    __shared__ __attribute__((aligned(16))) BwdKVSmem<HD> sm[2];
+    bf16* __restrict__ dk, bf16* __restrict__ dv, int64_t ldd, int H, int S, float c, float scale, int causal) {
+    constexpr int BQ = 64, BKV = 128, KS = HD / 16, OB = HD / 32, TILE = BQ * HD;
+    constexpr int LPT = 2 * (64 * HD / 512 / 4);
+    constexpr int STAGE = 2 * TILE + 2 * 64 * 2;  // Q, dO, then lse and D as fp32 (2 x 64 x 4 B)
+    __shared__ __attribute__((aligned(16))) bf16 sm[2][STAGE];
 
     const int nkv = (S + BKV - 1) / BKV;
-    const int kb_ = nkv - 1 - static_cast<int>(blockIdx.x);  // kv tiles with most work first (lowest keys)
-    const int kblk = causal ? (nkv - 1 - kb_) : kb_;
+    const int kblk = causal ? static_cast<int>(blockIdx.x) : nkv - 1 - static_cast<int>(blockIdx.x);
     const int h = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
-    const int k0 = kblk * BKV;
-    const int kw = k0 + wave * 32;
-    const int mykey = kw + (lane & 31);
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
-    const int64_t hoff = static_cast<int64_t>(h) * HD;
+    const int k0 = kblk * BKV, kw = k0 + wave * 32, mykey = kw + (lane & 31);
+    const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
+    const float* lse_bh = lse + (static_cast<int64_t>(b) * H + h) * S;
+    const float* D_bh = Dg + (static_cast<int64_t>(b) * H + h) * S;
 
     bf16x8 kf[KS], vf[KS];
     {
@@ -320,98 +312,76 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
     }
     f32x16 dvt[OB], dkt[OB];
 #pragma unroll
-    for (int i = 0; i < OB; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            dvt[i][e] = 0.0f;
-            dkt[i][e] = 0.0f;
-        }
+    for (int i = 0; i < OB; ++i) {
+        zero(dvt[i]);
+        zero(dkt[i]);
+    }
 
     const int nq = (S + BQ - 1) / BQ;
-    const int qt_begin = causal ? (k0 / BQ) : 0;
-    const float* lse_bh = lse + (static_cast<int64_t>(b) * H + h) * S;
-    const float* D_bh = Dg + (static_cast<int64_t>(b) * H + h) * S;
-
-    // loader: threads [0, 8NC) load Q 8x8 blocks, threads [128, 128 + 8NC) load dO blocks.
-    uint4 r[8];
-    float rl = 0.0f, rd = 0.0f;
-    const int half = threadIdx.x >> 7, tl = threadIdx.x & 127;
-    auto gload = [&](int qt) {
-        const int qs = qt * BQ;
-        if (tl < 8 * NC) {
-            const int rg = tl & 7, hc = tl >> 3;
-            const bf16* src = half == 0 ? q : dout;
-            const int64_t lds = half == 0 ? ldq : ldo;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int row = qs + rg * 8 + i;
-                r[i] = ldg16(src + (tok0 + row) * lds + hoff + hc * 8, row < S);
-            }
-        }
-        if (threadIdx.x < 64) {
-            const int row = qs + threadIdx.x;
-            rl = row < S ? lse_bh[row] * kLog2e : 0.0f;
-            rd = row < S ? D_bh[row] : 0.0f;
+    const int qt0 = causal ? (k0 / BQ) : 0;
+    // waves 0 and 1 also copy the 64 lse / D values of the tile (4 bytes per lane)
+    auto copy = [&](int qt, int st) {
+        dma_rows64<HD>(q + tok0 * ldq + hoff, ldq, qt * BQ, S, sm[st]);
+        dma_rows64<HD>(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
+        if (wave < 2) {
+            const float* src = (wave == 0 ? lse_bh : D_bh) + min(qt * BQ + lane, S - 1);
+            __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(sm[st] + 2 * TILE + wave * 128), 4, 0, 0);
         }
     };
-    auto sstore = [&](int st) {
-        if (tl < 8 * NC) {
-            const int rg = tl & 7, hc = tl >> 3;
-            bf16* rowt = half == 0 ? sm[st].q : sm[st].dO;
-            bf16* trt = half == 0 ? sm[st].qt : sm[st].dOt;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int row = rg * 8 + i;
-                *reinterpret_cast<uint4*>(rowt + row * HD + ((hc ^ swz16<HD>(row)) << 3)) = r[i];
-            }
-            store_transposed8(trt, r, hc * 8, rg * 8);
-        }
-        if (threadIdx.x < 64) {
-            sm[st].lse2[threadIdx.x] = rl;
-            sm[st].D[threadIdx.x] = rd;
-        }
-    };
+    if (qt0 < nq) copy(qt0, 0);
+    if (qt0 + 1 < nq) copy(qt0 + 1, 1);
 
-    if (qt_begin < nq) {
-        gload(qt_begin);
-        sstore(0);
-    }
-    __syncthreads();
-
-    for (int qt = qt_begin; qt < nq; ++qt) {
-        const int st = (qt - qt_begin) & 1;
-        if (qt + 1 < nq) gload(qt + 1);
+    for (int qt = qt0; qt < nq; ++qt) {
+        const int st = (qt - qt0) & 1;
+        if (qt + 1 < nq) {
+            if (wave < 2) wait_vmcnt<LPT + 1>();
+            else wait_vmcnt<LPT>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_barrier();
         const int qs = qt * BQ;
-        const bool active = !causal || (qs + BQ - 1 >= kw);
-        if (active) {
+        const bf16* Qs = sm[st];
+        const bf16* Os = sm[st] + TILE;
+        const float* Ls = reinterpret_cast<const float*>(sm[st] + 2 * TILE);
+        const float* Ds = Ls + 64;
+        if (!causal || qs + BQ - 1 >= kw) {
             f32x16 s[2], dp[2];
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    s[mb][e] = 0.0f;
-                    dp[mb][e] = 0.0f;
-                }
+            for (int mb = 0; mb < 2; ++mb) {
+                zero(s[mb]);
+                zero(dp[mb]);
+            }
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
-                    const bf16x8 qa = read_row_frag<HD>(sm[st].q, mb * 32 + (lane & 31), 2 * kk + hl);
-                    s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kf[kk], s[mb], 0, 0, 0);
-                    const bf16x8 da = read_row_frag<HD>(sm[st].dO, mb * 32 + (lane & 31), 2 * kk + hl);
-                    dp[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vf[kk], dp[mb], 0, 0, 0);
+                    s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Qs, mb * 32, kk), kf[kk], s[mb], 0, 0,
+                                                                     0);
+                    dp[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Os, mb * 32, kk), vf[kk], dp[mb], 0,
+                                                                      0, 0);
                 }
             // s[mb][e]: query qs + 32mb + 8(e/4) + 4hl + e%4, key mykey
+            const bool diag = (causal && qs < kw + 31) || qs + BQ > S || kw + 32 > S;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int qi = mb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-                    const int qq = qs + qi;
-                    const bool valid = (qq < S) && (mykey < S) && (!causal || mykey <= qq);
-                    const float p = valid ? __builtin_amdgcn_exp2f(s[mb][e] * scale_log2 - sm[st].lse2[qi]) : 0.0f;
-                    s[mb][e] = p;
-                    dp[mb][e] = p * (dp[mb][e] - sm[st].D[qi]);
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int qi = mb * 32 + 8 * g4 + 4 * hl;
+                    const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);
+                    const float4 d4 = *reinterpret_cast<const float4*>(Ds + qi);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int e = 4 * g4 + u;
+                        float p = __builtin_amdgcn_exp2f(fmaf(s[mb][e], c, -lv[u] * kLog2e));
+                        if (diag) {
+                            const int qq = qs + qi + u;
+                            if (qq >= S || mykey >= S || (causal && mykey > qq)) p = 0.0f;
+                        }
+                        s[mb][e] = p;
+                        dp[mb][e] = p * (dp[mb][e] - dvv[u]);
+                    }
                 }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
@@ -419,69 +389,48 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
                 for (int ob = 0; ob < OB; ++ob) {
-                    const int hrow = ob * 32 + (lane & 31);
-                    const bf16x8 doa = read_t_frag(sm[st].dOt, hrow, ks, hl);
-                    dvt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(doa, pf, dvt[ob], 0, 0, 0);
-                    const bf16x8 qa = read_t_frag(sm[st].qt, hrow, ks, hl);
-                    dkt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, dsf, dkt[ob], 0, 0, 0);
+                    dvt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Os, ob * 32, ks), pf, dvt[ob], 0, 0, 0);
+                    dkt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Qs, ob * 32, ks), dsf, dkt[ob], 0, 0,
+                                                                       0);
                 }
             }
         }
-        if (qt + 1 < nq) sstore(st ^ 1);
-        __syncthreads();
+        wait_lds();
+        __builtin_amdgcn_s_barrier();
+        if (qt + 2 < nq) copy(qt + 2, st);
     }
 
     if (mykey < S) {
         bf16* dkp = dk + (tok0 + mykey) * ldd + hoff;
         bf16* dvp = dv + (tok0 + mykey) * ldd + hoff;
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = ob * 32 + 8 * g + 4 * hl;
-                uint32_t wk[2], wv[2];
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    wk[u] = static_cast<uint32_t>(f2bf_bits(dkt[ob][4 * g + 2 * u] * scale)) |
-                            (static_cast<uint32_t>(f2bf_bits(dkt[ob][4 * g + 2 * u + 1] * scale)) << 16);
-                    wv[u] = static_cast<uint32_t>(f2bf_bits(dvt[ob][4 * g + 2 * u])) |
-                            (static_cast<uint32_t>(f2bf_bits(dvt[ob][4 * g + 2 * u + 1])) << 16);
-                }
-                *reinterpret_cast<uint2*>(dkp + d0) = make_uint2(wk[0], wk[1]);
-                *reinterpret_cast<uint2*>(dvp + d0) = make_uint2(wv[0], wv[1]);
-            }
+        for (int ob = 0; ob < OB; ++ob) {
+            store_t(dkp, dkt[ob], ob, scale);
+            store_t(dvp, dvt[ob], ob, 1.0f);
+        }
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// Backward: dQ
+// Backward: dQ.  Stage = K tile, V tile.
 // ---------------------------------------------------------------------------------------
 template <int HD>
-struct BwdQSmem {
-    bf16 k[64 * HD];
-    bf16 kt[HD * 64];
-    bf16 v[64 * HD];
-};
-
-template <int HD>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_mfma(const bf16* __restrict__ q, const bf16* __restrict__ k,
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                            const bf16* __restrict__ v, int64_t ldq,
                                                            const bf16* __restrict__ dout, int64_t ldo,
                                                            const float* __restrict__ lse, const float* __restrict__ Dg,
-                                                           bf16* __restrict__ dq, int64_t ldd, int H, int S,
-                                                           float scale_log2, float scale, int causal) {
-    constexpr int BQ = 128, BKV = 64, NC = HD / 8, KS = HD / 16, OB = HD / 32;
-    __shared__ __attribute__((aligned(16))) BwdQSmem<HD> sm[2];
+                                                           bf16* __restrict__ dq, int64_t ldd, int H, int S, float c,
+                                                           float scale, int causal) {
+    constexpr int BQ = 128, BKV = 64, KS = HD / 16, OB = HD / 32, TILE = BKV * HD;
+    constexpr int LPT = 2 * (64 * HD / 512 / 4);
+    __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];
 
     const int nq = (S + BQ - 1) / BQ;
     const int qb = nq - 1 - static_cast<int>(blockIdx.x);
     const int h = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
-    const int q0 = qb * BQ;
-    const int qw = q0 + wave * 32;
-    const int myq = qw + (lane & 31);
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
-    const int64_t hoff = static_cast<int64_t>(h) * HD;
+    const int q0 = qb * BQ, qw = q0 + wave * 32, myq = qw + (lane & 31);
+    const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
 
     bf16x8 qf[KS], df[KS];
     {
@@ -493,128 +442,75 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_mfma(const bf16* __restric
             df[kk] = __builtin_bit_cast(bf16x8, ldg16(dp_ + 16 * kk, myq < S));
         }
     }
-    const float my_lse2 = myq < S ? lse[(static_cast<int64_t>(b) * H + h) * S + myq] * kLog2e : 0.0f;
+    const float my_l2 = myq < S ? lse[(static_cast<int64_t>(b) * H + h) * S + myq] * kLog2e : 0.0f;
     const float my_D = myq < S ? Dg[(static_cast<int64_t>(b) * H + h) * S + myq] : 0.0f;
-
     f32x16 dqt[OB];
 #pragma unroll
-    for (int i = 0; i < OB; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) dqt[i][e] = 0.0f;
+    for (int i = 0; i < OB; ++i) zero(dqt[i]);
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
     const int ntiles = (kv_end + BKV - 1) / BKV;
-
-    // loader: threads [0, 8NC) load K as 8x8 blocks (both layouts); threads [128, 256) load V rows
-    uint4 r[8];
-    const int half = threadIdx.x >> 7, tl = threadIdx.x & 127;
-    constexpr int VCH = BKV * NC / 128;
-    auto gload = [&](int t) {
-        const int k0 = t * BKV;
-        if (half == 0) {
-            if (tl < 8 * NC) {
-                const int rg = tl & 7, hc = tl >> 3;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int row = k0 + rg * 8 + i;
-                    r[i] = ldg16(k + (tok0 + row) * ldq + hoff + hc * 8, row < S);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < VCH; ++i) {
-                const int c = tl + 128 * i;
-                const int row = c / NC, ch = c % NC;
-                r[i] = ldg16(v + (tok0 + k0 + row) * ldq + hoff + ch * 8, k0 + row < S);
-            }
-        }
+    auto copy = [&](int t, int st) {
+        dma_rows64<HD>(k + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st]);
+        dma_rows64<HD>(v + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st] + TILE);
     };
-    auto sstore = [&](int st) {
-        if (half == 0) {
-            if (tl < 8 * NC) {
-                const int rg = tl & 7, hc = tl >> 3;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int row = rg * 8 + i;
-                    *reinterpret_cast<uint4*>(sm[st].k + row * HD + ((hc ^ swz16<HD>(row)) << 3)) = r[i];
-                }
-                store_transposed8(sm[st].kt, r, hc * 8, rg * 8);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < VCH; ++i) {
-                const int c = tl + 128 * i;
-                const int row = c / NC, ch = c % NC;
-                *reinterpret_cast<uint4*>(sm[st].v + row * HD + ((ch ^ swz16<HD>(row)) << 3)) = r[i];
-            }
-        }
-    };
-
-    if (ntiles > 0) {
-        gload(0);
-        sstore(0);
-    }
-    __syncthreads();
+    if (ntiles > 0) copy(0, 0);
+    if (ntiles > 1) copy(1, 1);
 
     for (int t = 0; t < ntiles; ++t) {
         const int st = t & 1;
-        if (t + 1 < ntiles) gload(t + 1);
+        if (t + 1 < ntiles) wait_vmcnt<LPT>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
         const int k0 = t * BKV;
-        const bool active = !causal || (k0 <= qw + 31);
-        if (active) {
+        const bf16* Ks = sm[st];
+        const bf16* Vs = sm[st] + TILE;
+        if (!causal || k0 <= qw + 31) {
             f32x16 s[2], dp[2];
 #pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    s[jb][e] = 0.0f;
-                    dp[jb][e] = 0.0f;
-                }
+            for (int jb = 0; jb < 2; ++jb) {
+                zero(s[jb]);
+                zero(dp[jb]);
+            }
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb) {
-                    const bf16x8 ka = read_row_frag<HD>(sm[st].k, jb * 32 + (lane & 31), 2 * kk + hl);
-                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[kk], s[jb], 0, 0, 0);
-                    const bf16x8 va = read_row_frag<HD>(sm[st].v, jb * 32 + (lane & 31), 2 * kk + hl);
-                    dp[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, df[kk], dp[jb], 0, 0, 0);
+                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Ks, jb * 32, kk), qf[kk], s[jb], 0, 0,
+                                                                     0);
+                    dp[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Vs, jb * 32, kk), df[kk], dp[jb], 0,
+                                                                      0, 0);
                 }
+            const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S || myq >= S;
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + jb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-                    const bool valid = (key < S) && (myq < S) && (!causal || key <= myq);
-                    const float p = valid ? __builtin_amdgcn_exp2f(s[jb][e] * scale_log2 - my_lse2) : 0.0f;
+                    float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
+                    if (diag) {
+                        const int key = k0 + jb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
+                        if (key >= S || myq >= S || (causal && key > myq)) p = 0.0f;
+                    }
                     dp[jb][e] = p * (dp[jb][e] - my_D);
                 }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
-                for (int ob = 0; ob < OB; ++ob) {
-                    const bf16x8 ka = read_t_frag(sm[st].kt, ob * 32 + (lane & 31), ks, hl);
-                    dqt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, dsf, dqt[ob], 0, 0, 0);
-                }
+                for (int ob = 0; ob < OB; ++ob)
+                    dqt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Ks, ob * 32, ks), dsf, dqt[ob], 0, 0,
+                                                                       0);
             }
         }
-        if (t + 1 < ntiles) sstore(st ^ 1);
-        __syncthreads();
+        wait_lds();
+        __builtin_amdgcn_s_barrier();
+        if (t + 2 < ntiles) copy(t + 2, st);
     }
 
     if (myq < S) {
         bf16* dqp = dq + (tok0 + myq) * ldd + hoff;
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = ob * 32 + 8 * g + 4 * hl;
-                const uint32_t w0 = static_cast<uint32_t>(f2bf_bits(dqt[ob][4 * g] * scale)) |
-                                    (static_cast<uint32_t>(f2bf_bits(dqt[ob][4 * g + 1] * scale)) << 16);
-                const uint32_t w1 = static_cast<uint32_t>(f2bf_bits(dqt[ob][4 * g + 2] * scale)) |
-                                    (static_cast<uint32_t>(f2bf_bits(dqt[ob][4 * g + 3] * scale)) << 16);
-                *reinterpret_cast<uint2*>(dqp + d0) = make_uint2(w0, w1);
-            }
+        for (int ob = 0; ob < OB; ++ob) store_t(dqp, dqt[ob], ob, scale);
     }
 }
 
