@@ -75,6 +75,7 @@ SIGNATURES = {
     "aic_hip_optim_finalize": (i32, [vp, vp, vp, vp]),
     "aic_hip_adamw_multi": (i32, [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i64p,
                                   i32, f32, f32, f32, f32, f32, i64, vp, vp]),
+    "aic_hip_adamw_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, vp]),
     "aic_hip_cast_f32_bf16": (i32, [vp, vp, i64, vp]),
     "aic_lm_create": (i32, [C.POINTER(LMConfig), C.POINTER(TrainConfig), C.POINTER(vp)]),
     "aic_lm_destroy": (i32, [vp]),

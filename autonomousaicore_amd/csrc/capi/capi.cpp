@@ -249,6 +249,15 @@ int aic_hip_adamw_multi(float* const* p, const float* const* g, float* const* m,
     });
 }
 
+int aic_hip_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                       float eps, float weight_decay, float bias_correction1, float bias_correction2,
+                       aic_stream stream) {
+    return guard([&] {
+        aic::hip::adamw_step(p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2,
+                             st(stream));
+    });
+}
+
 int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream) {
     return guard([&] { aic::hip::cast_f32_bf16(src, dst, n, st(stream)); });
 }

@@ -22,7 +22,7 @@
 //              [query x key] so a lane owns a key and P / dS feed dV^T += dO^T P and
 //              dK^T += Q^T dS from registers.
 //              dQ:   one block = 128 queries over 64-key tiles (dQ^T += K^T dS^T).
-// fp32 path (the fp32 reference configuration, head_dim <= 64): SIMT kernels, fp32 math.
+// fp32 path (the fp32 reference configuration, head_dim 16/32/64/128): SIMT kernels, fp32 math.
 #include <algorithm>
 #include <cmath>
 
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
 }
 
 // ---------------------------------------------------------------------------------------
-// SIMT path (fp32 configuration, any dtype, head_dim <= 64): one thread per query row
+// SIMT path (fp32 configuration, any dtype, head_dim 16/32/64/128): one thread per query row
 // (forward, dQ) or key row (dK, dV); fp32 math; K/V or Q/dO tiles staged in LDS.
 // ---------------------------------------------------------------------------------------
 constexpr int kSimtTile = 64;
@@ -697,6 +697,7 @@ void fwd_simt(const void* q, const void* k, const void* v, int64_t ldq, void* o,
     if (hd == 16) AIC_FWD_SIMT(16);
     else if (hd == 32) AIC_FWD_SIMT(32);
     else if (hd == 64) AIC_FWD_SIMT(64);
+    else if (hd == 128) AIC_FWD_SIMT(128);
     else AIC_THROW(NotImplemented, "attention: head_dim ", hd, " is not supported on this path");
 #undef AIC_FWD_SIMT
     AIC_LAUNCH_CHECK("attn_fwd_simt");
@@ -722,6 +723,7 @@ void bwd_simt(const void* q, const void* k, const void* v, int64_t ldq, const vo
     if (hd == 16) AIC_BWD_SIMT(16);
     else if (hd == 32) AIC_BWD_SIMT(32);
     else if (hd == 64) AIC_BWD_SIMT(64);
+    else if (hd == 128) AIC_BWD_SIMT(128);
     else AIC_THROW(NotImplemented, "attention: head_dim ", hd, " is not supported on this path");
 #undef AIC_BWD_SIMT
     AIC_LAUNCH_CHECK("attn_bwd_simt");

@@ -56,6 +56,9 @@ void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipSt
 void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
                  const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps, float wd,
                  int64_t step, const void* ctl, hipStream_t s);
+// Single-tensor AdamW with caller-computed bias corrections bc1 = 1 - beta1^t, bc2 = 1 - beta2^t.
+void adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
+                float wd, float bc1, float bc2, hipStream_t s);
 void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s);
 void fill_normal(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t s);
 void fill_const(float* dst, int64_t n, float v, hipStream_t s);

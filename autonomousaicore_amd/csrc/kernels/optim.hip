@@ -127,7 +127,9 @@ template <bool BF16COPY>
 __global__ __launch_bounds__(256) void adamw_k(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
                                                float* __restrict__ v, bf16* __restrict__ pb, int64_t n, float lr,
                                                float beta1, float beta2, float eps, float wd, int64_t host_step,
-                                               const aic_optim_ctl* __restrict__ ctl) {
+                                               float host_bc1, float host_bc2, const aic_optim_ctl* __restrict__ ctl) {
+    // bias corrections: from the device step count (ctl), from a host step count, or as
+    // given by the caller (host_step == 0), which is how AdamW::step passes them
     float mult = 1.0f;
     int64_t step = host_step;
     if (ctl) {
@@ -135,8 +137,8 @@ __global__ __launch_bounds__(256) void adamw_k(float* __restrict__ p, const floa
         mult = ctl->grad_mult;
         step = ctl->step;
     }
-    const float bc1 = 1.0f - powf(beta1, static_cast<float>(step));
-    const float bc2 = 1.0f - powf(beta2, static_cast<float>(step));
+    const float bc1 = step > 0 ? 1.0f - powf(beta1, static_cast<float>(step)) : host_bc1;
+    const float bc2 = step > 0 ? 1.0f - powf(beta2, static_cast<float>(step)) : host_bc2;
     const float ob1 = 1.0f - beta1, ob2 = 1.0f - beta2, lrwd = lr * wd;
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(m) |
                        reinterpret_cast<uintptr_t>(v)) & 15u) == 0 &&
@@ -262,6 +264,7 @@ void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipSt
 void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
                  const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps, float wd,
                  int64_t step, const void* ctl, hipStream_t s) {
+    AIC_CHECK(ctl || step > 0, InvalidArgument, "adamw_multi: step must be >= 1 without a control block");
     for (int t = 0; t < count; ++t) {
         if (sizes[t] == 0) continue;
         const unsigned grid = grid_for((sizes[t] + 3) / 4, 256, 16384);
@@ -269,12 +272,23 @@ void adamw_multi(float* const* p, const float* const* g, float* const* m, float*
         bf16* pb = p_bf16 ? static_cast<bf16*>(p_bf16[t]) : nullptr;
         if (pb)
             hipLaunchKernelGGL(adamw_k<true>, dim3(grid), dim3(256), 0, s, p[t], g[t], m[t], v[t], pb, sizes[t], lr,
-                               beta1, beta2, eps, wd, step, c);
+                               beta1, beta2, eps, wd, step, 0.0f, 0.0f, c);
         else
             hipLaunchKernelGGL(adamw_k<false>, dim3(grid), dim3(256), 0, s, p[t], g[t], m[t], v[t], pb, sizes[t], lr,
-                               beta1, beta2, eps, wd, step, c);
+                               beta1, beta2, eps, wd, step, 0.0f, 0.0f, c);
         AIC_LAUNCH_CHECK("adamw");
     }
+}
+
+void adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
+                float wd, float bc1, float bc2, hipStream_t s) {
+    AIC_CHECK(n >= 0 && (n == 0 || (p && g && m && v)), InvalidArgument, "adamw_step: bad arguments");
+    AIC_CHECK(bc1 > 0.0f && bc2 > 0.0f, InvalidArgument, "adamw_step: bias corrections must be positive");
+    if (n == 0) return;
+    const unsigned grid = grid_for((n + 3) / 4, 256, 16384);
+    hipLaunchKernelGGL(adamw_k<false>, dim3(grid), dim3(256), 0, s, p, g, m, v, nullptr, n, lr, beta1, beta2, eps, wd,
+                       int64_t{0}, bc1, bc2, nullptr);
+    AIC_LAUNCH_CHECK("adamw_step");
 }
 
 void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s) {

@@ -360,7 +360,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
         gemm(prof_, 0, 0, T, d, d, dx.get(), d, W(ly.wo), d, dh.get(), d, dt, dt, s);
         {
-            auto _p = prof_.scope(kAttnBwd, 2.5 * attn_flops, 8.0 * es * T * d, s);
+            // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
+            auto _p = prof_.scope(kAttnBwd, 2.0 * attn_flops, 8.0 * es * T * d, s);
             hip::attn_bwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
                           dh.get(), d, atf(lse, l * T * H), dqkv.get(), static_cast<char*>(dqkv.get()) + es * d,
                           static_cast<char*>(dqkv.get()) + es * 2 * d, 3 * d, B, H, S, hd, true, scale, dt, s);

@@ -1,0 +1,158 @@
+"""Summarise rocprofv3 output of bench.py by kernel class.
+
+    python -m autonomousaicore_amd.rocprof_summary --stats DIR/run_kernel_stats.csv \
+        [--fetch DIR/run_counter_collection.csv --write DIR/run_counter_collection.csv \
+         --copy-probe-mib 1024] [--steps N]
+
+Kernel symbols map to the same classes as the library's event profiler (the class a launch
+is timed under inside TransformerLM::train_step), so the per-class average launch time here
+can be compared with bench.py's `kernel_classes[...].avg_ms`.
+
+Traffic: FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are summed per class and divided by the
+class's dispatch count.  Each counter is scaled by expected/measured on the copy kernel that
+`bench.py --copy-probe-mib M` runs before the model (a device-to-device copy of M MiB reads
+and writes exactly M MiB).  The scaled per-launch byte counts are printed as
+`traffic <class> <bytes>` lines, which bench.py reads back for its `roofline.traffic`.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import re
+from collections import defaultdict
+
+# (regex on the demangled or mangled symbol, class); first match wins.
+_RULES = [
+    (r"gemm_bf16_dma(<\d+, \d+, \d+, false, true|ILi\d+ELi\d+ELi\d+ELb0ELb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma(<\d+, \d+, \d+, false, false|ILi\d+ELi\d+ELi\d+ELb0ELb0E)", "gemm_dgrad"),
+    (r"gemm_bf16_dma(<\d+, \d+, \d+, true, false|ILi\d+ELi\d+ELi\d+ELb1ELb0E)", "gemm_wgrad"),
+    (r"attn_fwd", "attn_fwd"),
+    (r"attn_bwd|attn_dot", "attn_bwd"),
+    (r"rmsnorm_fwd", "rmsnorm_fwd"),
+    (r"rmsnorm_bwd|reduce_parts", "rmsnorm_bwd"),
+    (r"rope_k", "rope"),
+    (r"swiglu_fwd", "swiglu_fwd"),
+    (r"swiglu_bwd", "swiglu_bwd"),
+    (r"ce_fwd|ce_mean", "ce_fwd"),
+    (r"ce_bwd", "ce_bwd"),
+    (r"embed_fwd", "embed_fwd"),
+    (r"embed_sort|embed_seg", "embed_bwd"),
+    (r"sqnorm|finalize", "grad_norm"),
+    (r"adamw", "adamw"),
+]
+
+
+# Classes timed as one event scope around several kernels: the kernel launched once per
+# scope, so per-launch figures here are per scope, as in bench.py.
+_ANCHOR = {
+    "attn_bwd": r"attn_bwd_dq",
+    "rmsnorm_bwd": r"rmsnorm_bwd",
+    "grad_norm": r"sqnorm_k",
+    "ce_fwd": r"ce_fwd",
+    "embed_bwd": r"embed_seg",
+}
+
+
+def is_anchor(cls: str, name: str) -> bool:
+    pat = _ANCHOR.get(cls)
+    return pat is None or re.search(pat, name) is not None
+
+
+def kernel_class(name: str) -> str:
+    for pat, cls in _RULES:
+        if re.search(pat, name):
+            return cls
+    return "other"
+
+
+def read_stats(path):
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((r["Name"], int(r["Calls"]), float(r["TotalDurationNs"])))
+    return rows
+
+
+def read_counter(path, counter):
+    """Per-dispatch values of one counter: list of (kernel name, KiB)."""
+    out = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                out.append((r["Kernel_Name"], float(r["Counter_Value"])))
+    return out
+
+
+def copy_factor(disp, mib):
+    """expected / measured for the largest device copy in the run."""
+    copies = [v for n, v in disp if "copyBuffer" in n]
+    if not copies or mib <= 0:
+        return None
+    return (mib * 1024.0) / max(copies)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--stats", required=True)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-probe-mib", type=int, default=0)
+    ap.add_argument("--steps", type=int, default=0, help="train steps in the profiled run (for ms/step)")
+    args = ap.parse_args(argv)
+
+    per = defaultdict(lambda: [0, 0.0])
+    kernels = []
+    for name, calls, tot in read_stats(args.stats):
+        cls = kernel_class(name)
+        if is_anchor(cls, name):
+            per[cls][0] += calls
+        per[cls][1] += tot
+        kernels.append((tot, calls, cls, name))
+    grand = sum(v[1] for v in per.values())
+    print("# kernel classes (rocprofv3 --kernel-trace --stats); launches = event scopes, avg = per scope")
+    print(f"{'class':<13} {'launches':>8} {'total_ms':>10} {'avg_us':>9} {'share':>6}" +
+          (f" {'ms/step':>8}" if args.steps else ""))
+    for cls, (calls, tot) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+        line = f"{cls:<13} {calls:>8} {tot / 1e6:>10.3f} {tot / max(calls, 1) / 1e3:>9.1f} {100 * tot / grand:>5.1f}%"
+        if args.steps:
+            line += f" {tot / 1e6 / args.steps:>8.3f}"
+        print(line)
+    print("\n# kernels (top 20 by total time)")
+    for tot, calls, cls, name in sorted(kernels, reverse=True)[:20]:
+        short = name if len(name) <= 110 else name[:107] + "..."
+        print(f"{cls:<13} {calls:>6} {tot / calls / 1e3:>9.1f} us  {short}")
+
+    if args.fetch and args.write:
+        fd = read_counter(args.fetch, "FETCH_SIZE")
+        wd = read_counter(args.write, "WRITE_SIZE")
+        ff = copy_factor(fd, args.copy_probe_mib)
+        wf = copy_factor(wd, args.copy_probe_mib)
+        print("\n# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)")
+        print(f"copy probe {args.copy_probe_mib} MiB: FETCH_SIZE scale {ff:.4f}, WRITE_SIZE scale {wf:.4f}")
+        acc = defaultdict(lambda: [0, 0.0, 0, 0.0])
+        for n, v in fd:
+            c = kernel_class(n)
+            a = acc[c]
+            a[0] += is_anchor(c, n)
+            a[1] += v
+        for n, v in wd:
+            c = kernel_class(n)
+            a = acc[c]
+            a[2] += is_anchor(c, n)
+            a[3] += v
+        print(f"{'class':<13} {'launches':>8} {'fetch_MB':>10} {'write_MB':>10}")
+        for cls, (nf, sf, nw, sw) in sorted(acc.items()):
+            if cls == "other" or nf == 0 or nw == 0:
+                continue
+            fb = sf * 1024.0 * ff / nf
+            wb = sw * 1024.0 * wf / nw
+            print(f"{cls:<13} {nf:>8} {fb / 1e6:>10.2f} {wb / 1e6:>10.2f}")
+        print()
+        for cls, (nf, sf, nw, sw) in sorted(acc.items()):
+            if cls == "other" or nf == 0 or nw == 0:
+                continue
+            print(f"traffic {cls} {int(round(sf * 1024.0 * ff / nf + sw * 1024.0 * wf / nw))}")
+
+
+if __name__ == "__main__":
+    main()

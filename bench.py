@@ -42,10 +42,27 @@ def matmul_params(c):
 
 
 def step_flops(c):
-    """Algorithmic FLOPs per step: 6 T P_mm + causal attention (fwd 2 products, bwd 5)."""
+    """Algorithmic FLOPs per step: 6 T P_mm + 6 L T S d (causal attention: forward Q K^T and
+    P V at 2 S d per token per layer on the causal average, backward twice that)."""
     T = c["B"] * c["S"]
-    attn_fwd = 2.0 * c["B"] * c["H"] * c["S"] * (c["S"] + 1) * (c["d"] // c["H"])
-    return 6.0 * T * matmul_params(c) + c["L"] * 3.5 * attn_fwd
+    return 6.0 * T * matmul_params(c) + 6.0 * c["L"] * T * c["S"] * c["d"]
+
+
+def profiled_traffic(kernel_class):
+    """HBM bytes per launch of a kernel class, from the committed rocprofv3 PMC summaries
+    (lines `traffic <class> <bytes>` written by autonomousaicore_amd.rocprof_summary), or None."""
+    pdir = os.path.join(HERE, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    for fn in sorted(os.listdir(pdir)):
+        if not fn.endswith(".txt"):
+            continue
+        with open(os.path.join(pdir, fn)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel_class:
+                    return int(parts[2])
+    return None
 
 
 def cpu_baseline(c, seed=1234):
@@ -69,13 +86,18 @@ def cpu_baseline(c, seed=1234):
     params[off:off + 2 * d] = 1.0
     params[off + 2 * d:off + 3 * d] = 1.0
     ids, tgt = aic.batch(seed, 1, S, c["vocab"], dist="zipf")
-    t0 = time.perf_counter()
-    res, *_ = orc.lm_step(cfg, params, ids, tgt, 1, S)
-    wall = time.perf_counter() - t0
-    per_token = (res.t_embed + res.t_embed_bwd + res.t_head_fwd + res.t_loss + res.t_head_bwd)
-    blocks = res.t_blocks_fwd + res.t_blocks_bwd
     full_params = matmul_params(c) + c["vocab"] * d + c["L"] * 2 * d + d
-    t_step = c["B"] * (per_token + c["L"] * blocks) + res.t_optim * (full_params / n)
+    # one untimed warm-up, then the median of three sample steps (each from the same weights)
+    orc.lm_step(cfg, params.copy(), ids, tgt, 1, S)
+    t0 = time.perf_counter()
+    est = []
+    for _ in range(3):
+        res, *_ = orc.lm_step(cfg, params.copy(), ids, tgt, 1, S)
+        per_token = (res.t_embed + res.t_embed_bwd + res.t_head_fwd + res.t_loss + res.t_head_bwd)
+        blocks = res.t_blocks_fwd + res.t_blocks_bwd
+        est.append(c["B"] * (per_token + c["L"] * blocks) + res.t_optim * (full_params / n))
+    wall = time.perf_counter() - t0
+    t_step = sorted(est)[1]
     tokens = c["B"] * S
     return {
         "value": round(tokens / t_step, 2),
@@ -83,7 +105,7 @@ def cpu_baseline(c, seed=1234):
         "cores": threads,
         "kind": "port",
         "sample": (f"oracle fp32 step (restatement of the reference AVX2 CPU path) on 1 layer at the "
-                   f"config widths, B=1 x S={S}, measured {wall:.1f} s; extrapolated to {c['L']} layers, "
+                   f"config widths, B=1 x S={S}, median of 3 after 1 warm-up ({wall:.1f} s timed); extrapolated to {c['L']} layers, "
                    f"B={c['B']} and AdamW over {full_params / 1e6:.0f}M parameters: {t_step:.1f} s/step"),
     }
 
@@ -95,6 +117,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="1b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="before the model, copy a buffer of this many MiB once (a known-size kernel that calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -109,6 +134,14 @@ def main():
         sys.exit(1)
     c = CONFIGS[args.config]
     B, S = c["B"], c["S"]
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     model = aic.TransformerLM(
         aic.TransformerLMConfig(vocab_size=c["vocab"], hidden_dim=c["d"], num_layers=c["L"], num_heads=c["H"],
                                 intermediate_dim=c["f"], max_seq_len=S, rms_norm_eps=1e-6, compute="bfloat16"),
@@ -157,7 +190,7 @@ def main():
     d = kc[dom["name"]]
     roofline = {"kernel": dom["name"], "bound": d["bound"], "achieved": d["achieved"],
                 "peak": PEAK_BF16_TFLOPS if d["bound"] == "mfma" else PEAK_HBM_GBS, "unit": d["unit"],
-                "frac": d["frac"], "avg_launch_ms": d["avg_ms"], "traffic": None}
+                "frac": d["frac"], "avg_launch_ms": d["avg_ms"], "traffic": profiled_traffic(dom["name"])}
 
     cpu = None
     if not args.no_cpu_baseline:

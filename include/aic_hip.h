@@ -201,6 +201,14 @@ int aic_hip_adamw_multi(float* const* p, const float* const* g, float* const* m,
                         const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps,
                         float weight_decay, int64_t step, const aic_optim_ctl* ctl, aic_stream stream);
 
+/* AdamW on one tensor with the caller's bias corrections bc1 = 1 - beta1^t and
+ * bc2 = 1 - beta2^t (computed in float on the host, as AdamW::step does,
+ * src/optim/adamw.cpp:28-29); same update order as aic_hip_adamw_multi.
+ * Replaces: cuda_adamw_step (src/cuda/cuda_adamw.cuh:10-24), argument for argument. */
+int aic_hip_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                       float eps, float weight_decay, float bias_correction1, float bias_correction2,
+                       aic_stream stream);
+
 /* fp32 -> bf16 (round to nearest even) copy of n elements. */
 int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream);
 

@@ -230,7 +230,7 @@ def test_embedding_gather_bit_exact_and_scatter(orc, dt):
 
 
 # ----------------------------------------------------------------------------- attention
-@pytest.mark.parametrize("B,S,H,hd", [(2, 64, 4, 32), (1, 100, 2, 64), (1, 128, 2, 16)])
+@pytest.mark.parametrize("B,S,H,hd", [(2, 64, 4, 32), (1, 100, 2, 64), (1, 128, 2, 16), (1, 96, 2, 128)])
 def test_attention_fp32_matches_oracle(orc, B, S, H, hd):
     rng = np.random.default_rng(S * hd)
     d = H * hd
@@ -324,6 +324,28 @@ def test_adamw_matches_oracle(orc):
     assert np.max(np.abs(host(pd) - pm)) < 1e-6
     assert rel(host(md), m) < 1e-6 and rel(host(vd), v) < 1e-6
     np.testing.assert_array_equal(host(low), bf16_round(host(pd)))
+
+
+def test_adamw_step_with_caller_bias_corrections(orc):
+    # the reference's cuda_adamw_step contract: bias corrections computed by the caller
+    rng = np.random.default_rng(43)
+    n = 50_003
+    p = rng.standard_normal(n).astype(np.float32)
+    pm, m, v = p.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    pd, md, vd = dev(p), dev(np.zeros(n, np.float32)), dev(np.zeros(n, np.float32))
+    for step in (1, 2, 3, 10):
+        g = rng.standard_normal(n).astype(np.float32)
+        orc.adamw(pm, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01, step)
+        gd = dev(g)
+        bc1 = float(np.float32(1) - np.float32(0.9) ** np.float32(step))
+        bc2 = float(np.float32(1) - np.float32(0.999) ** np.float32(step))
+        call("aic_hip_adamw_step", ptr(pd), ptr(gd), ptr(md), ptr(vd), n, 1e-3, 0.9, 0.999, 1e-8, 0.01, bc1, bc2,
+             stream())
+    assert np.max(np.abs(host(pd) - pm)) < 1e-6
+    assert rel(host(md), m) < 1e-6 and rel(host(vd), v) < 1e-5
+    # a zero bias correction is an argument error, not a division by zero
+    assert _lib.load().aic_hip_adamw_step(ptr(pd), ptr(gd), ptr(md), ptr(vd), n, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.0,
+                                          bc2, stream()) != 0
 
 
 def _ctl(**kw):
