@@ -72,8 +72,7 @@ __device__ __forceinline__ void dma_rows64(const bf16* __restrict__ g, int64_t l
         const int row = seg * RPS + lane / NC;
         const int lc = (lane % NC) ^ swz<HD>(row);
         const int gr = min(row0 + row, nrows - 1);
-        __builtin_amdgcn_global_load_lds(g + static_cast<int64_t>(gr) * ld + lc * 8, (lds_void_t*)(s + seg * 512), 16,
-                                         0, 0);
+        dma16(g + static_cast<int64_t>(gr) * ld + lc * 8, s + seg * 512);
     }
 }
 
@@ -325,7 +324,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
         dma_rows64<HD>(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
         if (wave < 2) {
             const float* src = (wave == 0 ? lse_bh : D_bh) + min(qt * BQ + lane, S - 1);
-            __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(sm[st] + 2 * TILE + wave * 128), 4, 0, 0);
+            dma4(src, sm[st] + 2 * TILE + wave * 128);
         }
     };
     if (qt0 < nq) copy(qt0, 0);

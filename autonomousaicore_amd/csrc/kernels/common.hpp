@@ -82,6 +82,26 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return red[0];
 }
 
+// Direct global -> LDS copy of 16 (dma16) or 4 (dma4) bytes per lane: lane i's bytes land at
+// lds + i * size (lds must be the same for the whole wave).  Issued as inline assembly so the
+// compiler does not track it: the caller orders it with explicit s_waitcnt vmcnt(N) before the
+// data is read (the compiler's own tracking would otherwise put a vmcnt(0) in front of every
+// ds_read_b64_tr_b16, which carries no memory operand, and expose the whole copy latency).
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+    const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, const void* lds) {
+    const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(g)
+                 : "memory", "m0");
+}
+
 inline unsigned grid_for(int64_t n, int block, int64_t cap = 65535LL * 8) {
     int64_t g = (n + block - 1) / block;
     if (g < 1) g = 1;

@@ -23,6 +23,8 @@
 // fp32 path (the fp32 reference configuration) and odd shapes: a plain SIMT tiled kernel.
 #include "gemm.hpp"
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace aic::hip {
@@ -41,7 +43,25 @@ struct MfmaParams {
     int64_t lda, ldb, ldc, ldr;
     int M, N, K;
     float alpha, beta;
+    int vec;  // C (and R) rows allow 4-element vector access: ld % 4 == 0, 16-byte aligned base
 };
+
+// Four consecutive elements of a C / R row, as floats.
+__device__ __forceinline__ void ld4(const float* p, float v[4]) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+__device__ __forceinline__ void ld4(const bf16* p, float v[4]) {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+    v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+}
+__device__ __forceinline__ void st4(float* p, const float v[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4(bf16* p, const float v[4]) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
 
 // Map the hardware block id to a tile so that consecutive tiles (same A row panel,
 // neighbouring B panels) land on the same XCD.
@@ -233,11 +253,19 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// One wave's share of a ROWS x 64 tile, copied HBM -> LDS with 1 KB per instruction.
-// KC: K contiguous in HBM, LDS [ROWS][64].  RC: rows contiguous in HBM, LDS [64][ROWS].
-template <int ROWS, bool KC>
+// Chunk swizzle of a K-contiguous [rows][BK] tile: the 16-byte chunk c of row r is stored
+// at c ^ swz_kc(r), so the 16 rows read by one ds_read_b128 phase hit distinct banks.
+template <int BK>
+__device__ __forceinline__ int swz_kc(int r) {
+    if constexpr (BK == 64) return (r ^ (r >> 3)) & 7;
+    else return (r >> 2) & 3;  // BK == 32: four chunks per 64-byte row
+}
+
+// One wave's share of a ROWS x BK tile, copied HBM -> LDS with 1 KB per instruction.
+// KC: K contiguous in HBM, LDS [ROWS][BK].  RC: rows contiguous in HBM, LDS [BK][ROWS].
+template <int ROWS, int BK, bool KC>
 __device__ __forceinline__ void dma_tile(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, int k0, bf16* s) {
-    constexpr int SEGS = ROWS * kBK / 512;  // 512 bf16 = 1 KB per segment
+    constexpr int SEGS = ROWS * BK / 512;  // 512 bf16 = 1 KB per segment
     constexpr int PER_WAVE = SEGS / 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -245,30 +273,32 @@ __device__ __forceinline__ void dma_tile(const bf16* __restrict__ g, int64_t ld,
         const int seg = wave * PER_WAVE + i;
         const bf16* src;
         if constexpr (KC) {
-            const int row = seg * 8 + (lane >> 3);
-            const int lc = (lane & 7) ^ swz(row);
+            constexpr int CPR = BK / 8;    // 16-byte chunks per row
+            constexpr int RPS = 64 / CPR;  // rows per segment
+            const int row = seg * RPS + lane / CPR;
+            const int lc = (lane % CPR) ^ swz_kc<BK>(row);
             const int gr = min(row0 + row, nrows - 1);
             src = g + static_cast<int64_t>(gr) * ld + k0 + lc * 8;
         } else {
-            constexpr int CPR = ROWS / 8;       // 16-byte chunks per k row
-            constexpr int RPS = 64 / CPR;       // k rows per segment
+            constexpr int CPR = ROWS / 8;  // 16-byte chunks per k row
+            constexpr int RPS = 64 / CPR;  // k rows per segment
             const int k = seg * RPS + lane / CPR;
             const int lc = (lane % CPR) ^ swz_rc(k);
             const int gr = min(row0 + lc * 8, nrows - 8);
             src = g + static_cast<int64_t>(k0 + k) * ld + gr;
         }
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(s + seg * 512), 16, 0, 0);
+        dma16(src, s + seg * 512);
     }
 }
 
 // MFMA operand fragment (8 bf16 along k) for rows rb .. rb+31 of a tile, k step kk.
-template <int ROWS, bool KC>
+template <int ROWS, int BK, bool KC>
 __device__ __forceinline__ bf16x8 frag(const bf16* t, int rb, int kk) {
     const int lane = threadIdx.x & 63;
     if constexpr (KC) {
         const int row = rb + (lane & 31);
         const int c = 2 * kk + (lane >> 5);
-        return *reinterpret_cast<const bf16x8*>(t + row * kBK + ((c ^ swz(row)) << 3));
+        return *reinterpret_cast<const bf16x8*>(t + row * BK + ((c ^ swz_kc<BK>(row)) << 3));
     } else {
         // ds_read_b64_tr_b16: within a group of 16 lanes, output lane i, slot j receives
         // element i % 4 of the 4 values addressed by source lane 4j + i / 4.  Source lane
@@ -291,7 +321,8 @@ __device__ __forceinline__ bf16x8 frag(const bf16* t, int rb, int kk) {
 // Wait until at most `tiles` later tiles' copies (LPT instructions each) are in flight.
 template <int LPT>
 __device__ __forceinline__ void wait_tiles(int tiles) {
-    if (tiles >= 2) wait_vmcnt<2 * LPT>();
+    if (tiles >= 3) wait_vmcnt<3 * LPT>();
+    else if (tiles == 2) wait_vmcnt<2 * LPT>();
     else if (tiles == 1) wait_vmcnt<LPT>();
     else wait_vmcnt<0>();
 }
@@ -302,21 +333,27 @@ __device__ __forceinline__ void wait_lds() {
 }
 
 // Main loop schedule (per wave): fragments are double-buffered in registers; the reads of
-// k step kk+1 are interleaved with the MFMAs of step kk (sched_group_barrier hints).  The
-// barrier that publishes tile kt+1 sits between the MFMAs of steps 2 and 3, so the MFMA
-// pipe keeps working across it; right after it the freed stage receives tile kt+S and the
-// first fragments of tile kt+1 are read while step 3's MFMAs issue.
-template <int BM, int BN, int S, bool TA, bool TB, typename CT>
+// k step ks+1 are interleaved with the MFMAs of step ks (sched_group_barrier hints).  The
+// barrier that publishes tile kt+1 sits before the MFMAs of the tile's last k step, so the
+// MFMA pipe keeps working across it; right after it the freed stage receives tile kt+S and
+// the first fragments of tile kt+1 are read while the last step's MFMAs issue.
+template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
 __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int STAGE = (BM + BN) * kBK;
+    constexpr int KS = BK / 16;
+    constexpr int STAGE = (BM + BN) * BK;
     constexpr bool AKC = !TA, BKC = TB;
-    constexpr int LPT = (BM + BN) * kBK / 512 / 4;  // copy instructions per wave per K step
+    constexpr int LPT = (BM + BN) * BK / 512 / 4;  // copy instructions per wave per K step
     constexpr int NREAD = (AKC ? FM : 2 * FM) + (BKC ? FN : 2 * FN);  // LDS reads per k step
     constexpr int NMF = FM * FN;
-    constexpr int MF_PER_READ = (NMF + NREAD - 1) / NREAD;
-    static_assert(S >= 2 && S <= 4, "stages");
+    // the next step's fragment reads go out with the first half of this step's MFMAs, so
+    // they have landed (no lgkmcnt stall) when the next step starts
+    constexpr int HALF = NMF / 2 > 0 ? NMF / 2 : 1;
+    constexpr int READS_PER_MF = (NREAD + HALF - 1) / HALF;
+    constexpr int FRONT = (NREAD + READS_PER_MF - 1) / READS_PER_MF;  // MFMAs that carry reads
+    static_assert(S >= 2 && S <= 5 && KS % 2 == 0, "stages / k steps");
+    static_assert((S - 2) * LPT < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) bf16 smem[];
 
     const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
@@ -336,33 +373,39 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
 
     auto copy = [&](int tile, int stage) {
         bf16* dst = smem + stage * STAGE;
-        dma_tile<BM, AKC>(p.A, p.lda, m0, p.M, tile * kBK, dst);
-        dma_tile<BN, BKC>(p.B, p.ldb, n0, p.N, tile * kBK, dst + BM * kBK);
+        dma_tile<BM, BK, AKC>(p.A, p.lda, m0, p.M, tile * BK, dst);
+        dma_tile<BN, BK, BKC>(p.B, p.ldb, n0, p.N, tile * BK, dst + BM * BK);
     };
     auto read = [&](int stage, int kk, bf16x8* af, bf16x8* bfr) {
         const bf16* As = smem + stage * STAGE;
-        const bf16* Bs = As + BM * kBK;
+        const bf16* Bs = As + BM * BK;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = frag<BM, AKC>(As, wm * WM + i * 32, kk);
+        for (int i = 0; i < FM; ++i) af[i] = frag<BM, BK, AKC>(As, wm * WM + i * 32, kk);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) bfr[j] = frag<BN, BKC>(Bs, wn * WN + j * 32, kk);
+        for (int j = 0; j < FN; ++j) bfr[j] = frag<BN, BK, BKC>(Bs, wn * WN + j * 32, kk);
     };
+    // B operand first: acc[i][j] accumulates the transposed 32x32 block (rows n, columns m),
+    // so each lane ends up owning runs of four consecutive n of one output row m.
     auto mma = [&](const bf16x8* af, const bf16x8* bfr) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     };
     auto interleave = [&]() {
+        // an MFMA leads each pair: no read is in flight ahead of the step's first MFMA,
+        // whose operands were read a half step earlier
 #pragma unroll
-        for (int i = 0; i < NREAD; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // one LDS read
-            __builtin_amdgcn_sched_group_barrier(0x008, MF_PER_READ, 0);  // then MFMAs
+        for (int i = 0; i < FRONT; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, READS_PER_MF, 0);  // LDS reads
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF - FRONT, 0);  // the rest of the MFMAs
+        __builtin_amdgcn_sched_barrier(0);  // nothing moves across k steps
     };
 
-    const int nk = p.K / kBK;
+    const int nk = p.K / BK;
 #pragma unroll
     for (int st = 0; st < S; ++st)
         if (st < nk) copy(st, st);
@@ -372,15 +415,12 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     read(0, 0, fa[0], fb[0]);
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt % S;
-        read(cur, 1, fa[1], fb[1]);
-        mma(fa[0], fb[0]);
-        interleave();
-        read(cur, 2, fa[0], fb[0]);
-        mma(fa[1], fb[1]);
-        interleave();
-        read(cur, 3, fa[1], fb[1]);
-        mma(fa[0], fb[0]);
-        interleave();
+#pragma unroll
+        for (int ks = 0; ks + 1 < KS; ++ks) {
+            read(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+            mma(fa[ks & 1], fb[ks & 1]);
+            interleave();
+        }
         wait_lds();  // this wave's reads of stage `cur` are complete
         if (kt + 1 < nk) wait_tiles<LPT>(min(S - 2, nk - 1 - (kt + 1)));  // tile kt+1 has landed
         __builtin_amdgcn_s_barrier();
@@ -390,25 +430,116 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
         interleave();
     }
 
+    // Epilogue.  Lane owns output row m = mb + lane % 32 and, in block (i, j), the columns
+    // n = nb + 8g + 4h + 0..3 (g = 0..3, h = lane / 32) in acc[i][j][4g .. 4g+3].
     CT* C = static_cast<CT*>(p.C);
     const CT* R = static_cast<const CT*>(p.R);
+    const int h = lane >> 5;
+    if (p.vec && m0 + BM <= p.M && n0 + BN <= p.N) {
+        // Full tile: each wave stages its WM x WN sub-tile through its quarter of the (now
+        // idle) LDS, so that every global store (and residual load) moves 16 contiguous
+        // bytes per lane, whole rows per instruction.  After the loop's last barrier no wave
+        // reads operand stages any more and no copy is in flight.
+        constexpr int E = sizeof(CT);
+        constexpr int RB = WN * E;                                       // bytes per sub-tile row
+        constexpr int CPR = RB / 16;                                     // 16-byte chunks per row
+        constexpr int REGION = S * STAGE * 2 / 4;                        // LDS bytes per wave
+        constexpr int FIT = REGION / RB < WM ? REGION / RB : WM;  // rows that fit the region
+        constexpr int IB = FIT / 32;                                // 32-row blocks per pass
+        constexpr int PASS_ROWS = IB * 32;                          // rows staged per pass
+        constexpr int VE = 16 / E;     // elements per chunk
+        constexpr int RPI = 64 / CPR;  // rows per 64-lane instruction
+        static_assert(IB >= 1 && FM % IB == 0 && (CPR & (CPR - 1)) == 0 && PASS_ROWS % RPI == 0,
+                      "epilogue staging");
+        char* region = reinterpret_cast<char*>(smem) + wave * REGION;
+        const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int i0 = 0; i0 < FM; i0 += IB) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int n = n0 + wn * WN + j * 32 + (lane & 31);
-            if (n >= p.N) continue;
+            for (int ii = 0; ii < IB; ++ii) {
+                const int r = ii * 32 + (lane & 31);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int byte = (32 * j + 8 * g + 4 * h) * E;
+                        char* d = region + r * RB + (((byte >> 4) ^ (r & (CPR - 1))) << 4) + (byte & 15);
+                        const f32x16& a = acc[i0 + ii][j];
+                        const float v0 = p.alpha * a[4 * g], v1 = p.alpha * a[4 * g + 1];
+                        const float v2 = p.alpha * a[4 * g + 2], v3 = p.alpha * a[4 * g + 3];
+                        if constexpr (E == 2)
+                            *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+                        else
+                            *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
+                    }
+            }
+            wait_lds();
+#pragma unroll
+            for (int t = 0; t < PASS_ROWS / RPI; ++t) {
+                const int r = t * RPI + lane / CPR, c = lane % CPR;
+                const uint4 raw = *reinterpret_cast<const uint4*>(region + r * RB + ((c ^ (r & (CPR - 1))) << 4));
+                const int64_t gm = wrow0 + i0 * 32 + r;
+                const int gn = wcol0 + c * VE;
+                CT* dst = C + gm * p.ldc + gn;
+                float v[VE];
+                if constexpr (E == 2) {
+                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        v[2 * q] = __uint_as_float(w[q] << 16);
+                        v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+                    }
+                } else {
+                    v[0] = __uint_as_float(raw.x); v[1] = __uint_as_float(raw.y);
+                    v[2] = __uint_as_float(raw.z); v[3] = __uint_as_float(raw.w);
+                }
+                if (p.beta != 0.0f) {
+#pragma unroll
+                    for (int q = 0; q < VE; q += 4) {
+                        float c4[4];
+                        ld4(dst + q, c4);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[q + u] += p.beta * c4[u];
+                    }
+                }
+                if (R) {
+#pragma unroll
+                    for (int q = 0; q < VE; q += 4) {
+                        float r4[4];
+                        ld4(R + gm * p.ldr + gn + q, r4);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[q + u] += r4[u];
+                    }
+                }
+                if constexpr (E == 2) {
+                    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+                } else {
+                    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+            wait_lds();  // the next pass overwrites the region
+        }
+        return;
+    }
+    const int nw = n0 + wn * WN + 4 * h;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (m >= p.M) continue;
+                const int n = nw + j * 32 + 8 * (e >> 2) + (e & 3);
+                if (n >= p.N) continue;
                 float v = p.alpha * acc[i][j][e];
                 const int64_t ci = static_cast<int64_t>(m) * p.ldc + n;
                 if (p.beta != 0.0f) v += p.beta * ld(C, ci);
                 if (R) v += ld(R, static_cast<int64_t>(m) * p.ldr + n);
                 st(C, ci, v);
             }
-        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -468,6 +599,8 @@ __global__ __launch_bounds__(256) void gemm_simt(const T* __restrict__ A, const 
     }
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 template <int BM, int BN, bool TA, bool TB, typename CT>
 void launch_mfma(const GemmArgs& a, hipStream_t s) {
     MfmaParams p;
@@ -478,12 +611,13 @@ void launch_mfma(const GemmArgs& a, hipStream_t s) {
     p.lda = a.lda; p.ldb = a.ldb; p.ldc = a.ldc; p.ldr = a.ldr;
     p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
     p.alpha = a.alpha; p.beta = a.beta;
+    p.vec = 0;
     const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, TA, TB, CT>), dim3(tiles), dim3(256), 0, s, p);
     AIC_LAUNCH_CHECK("gemm_bf16_mfma");
 }
 
-template <int BM, int BN, int S, bool TA, bool TB, typename CT>
+template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
 void launch_dma(const GemmArgs& a, hipStream_t s) {
     MfmaParams p;
     p.A = static_cast<const bf16*>(a.A);
@@ -493,24 +627,26 @@ void launch_dma(const GemmArgs& a, hipStream_t s) {
     p.lda = a.lda; p.ldb = a.ldb; p.ldc = a.ldc; p.ldr = a.ldr;
     p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
     p.alpha = a.alpha; p.beta = a.beta;
+    p.vec = a.ldc % 4 == 0 && aligned16(a.C) && (!a.R || (a.ldr % 4 == 0 && aligned16(a.R)));
     const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
-    constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * kBK * sizeof(uint16_t);
+    constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * BK * sizeof(uint16_t);
+    static_assert(lds <= 160 * 1024, "LDS per block");
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_dma<BM, BN, S, TA, TB, CT>),
+        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_dma<BM, BN, BK, S, TA, TB, CT>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         configured = true;
     }
-    hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, S, TA, TB, CT>), dim3(tiles), dim3(256), lds, s, p);
+    hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, BK, S, TA, TB, CT>), dim3(tiles), dim3(256), lds, s, p);
     AIC_LAUNCH_CHECK("gemm_bf16_dma");
 }
 
-template <int BM, int BN, int S, typename CT>
+template <int BM, int BN, int BK, int S, typename CT>
 void dispatch_dma(const GemmArgs& a, hipStream_t s) {
-    if (!a.transA && a.transB) launch_dma<BM, BN, S, false, true, CT>(a, s);
-    else if (!a.transA && !a.transB) launch_dma<BM, BN, S, false, false, CT>(a, s);
-    else if (a.transA && !a.transB) launch_dma<BM, BN, S, true, false, CT>(a, s);
-    else launch_dma<BM, BN, S, true, true, CT>(a, s);
+    if (!a.transA && a.transB) launch_dma<BM, BN, BK, S, false, true, CT>(a, s);
+    else if (!a.transA && !a.transB) launch_dma<BM, BN, BK, S, false, false, CT>(a, s);
+    else if (a.transA && !a.transB) launch_dma<BM, BN, BK, S, true, false, CT>(a, s);
+    else launch_dma<BM, BN, BK, S, true, true, CT>(a, s);
 }
 
 template <int BM, int BN, typename CT>
@@ -531,8 +667,6 @@ void launch_simt(const GemmArgs& a, hipStream_t s) {
     AIC_LAUNCH_CHECK("gemm_simt");
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 }  // namespace
 
 bool gemm_mfma_eligible(const GemmArgs& a) {
@@ -545,7 +679,7 @@ bool gemm_mfma_eligible(const GemmArgs& a) {
 
 bool gemm_dma_eligible(const GemmArgs& a) {
     if (!gemm_mfma_eligible(a)) return false;
-    if (a.K % kBK || a.M < 8 || a.N < 8) return false;
+    if (a.K % 64 || a.M < 8 || a.N < 8) return false;
     return true;
 }
 
@@ -562,11 +696,11 @@ void gemm(const GemmArgs& a, hipStream_t s) {
     if (gemm_dma_eligible(a)) {
         const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
         if (a.c == DType::Float32) {
-            if (t256 >= 192) dispatch_dma<256, 256, 2, float>(a, s);
-            else dispatch_dma<128, 128, 4, float>(a, s);
+            if (t256 >= 192) dispatch_dma<256, 256, 64, 2, float>(a, s);
+            else dispatch_dma<128, 128, 64, 4, float>(a, s);
         } else {
-            if (t256 >= 192) dispatch_dma<256, 256, 2, bf16>(a, s);
-            else dispatch_dma<128, 128, 4, bf16>(a, s);
+            if (t256 >= 192) dispatch_dma<256, 256, 64, 2, bf16>(a, s);
+            else dispatch_dma<128, 128, 64, 4, bf16>(a, s);
         }
         return;
     }
