@@ -42,14 +42,15 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 // ---------------------------------------------------------------------------------------
-// [rows][HD] bf16 tiles in LDS.  Chunk swizzle: 16 consecutive rows map one logical chunk
-// to 16 distinct 16-byte bank slots (ds_read_b128, lane = row), and 4 consecutive rows map
-// a chunk pair to 4 distinct 32-byte slots (ds_read_b64_tr_b16).
+// [rows][HD] bf16 tiles in LDS, 16-byte chunks XOR-swizzled per row.  The swizzle depends
+// on row % 16 only and makes both read patterns bank-conflict free: a ds_read_b128 phase
+// (16 consecutive rows, one logical chunk) touches 16 distinct bank slots, and each half of
+// a ds_read_b64_tr_b16 (4 consecutive rows x 64 bytes) covers the banks exactly once.
 // ---------------------------------------------------------------------------------------
 template <int HD>
 __device__ __forceinline__ int swz(int row) {
-    if constexpr (HD == 128) return 2 * (row & 7) | ((row >> 3) & 1);
-    else return 2 * ((row >> 1) & 3) | ((row >> 3) & 1);
+    if constexpr (HD == 128) return 4 * (row & 3) | ((row >> 2) & 3);
+    else return 4 * ((row >> 1) & 1) | ((row >> 2) & 3);
 }
 
 template <int N>
@@ -76,35 +77,46 @@ __device__ __forceinline__ void dma_rows64(const bf16* __restrict__ g, int64_t l
     }
 }
 
-// Row operand (lane = row rb + lane%32, 8 values of k step kk along head_dim).
+// MFMA operand fragments of a swizzled [rows][HD] tile, addressed through per-lane byte
+// offsets computed once per kernel (every read is then a register base plus an immediate).
+//   row(t, rb, kk): lane = row rb + lane%32 (rb a multiple of 32), 8 values of k step kk
+//                   along head_dim (ds_read_b128).
+//   tr(t, ob, ks):  lane = head_dim column 32ob + lane%32, 8 values along rows in the
+//                   permuted order of a 16-row step ks (elements 0..3: rows 16ks + 4h + 0..3,
+//                   elements 4..7: rows 16ks + 8 + 4h + 0..3, h = lane / 32), read with two
+//                   ds_read_b64_tr_b16: within a group of 16 lanes, output lane i slot j takes
+//                   element i % 4 of the 4 values at source lane 4j + i / 4, so source lane
+//                   s = 4j + q addresses row (base + j), columns cb' + 4q .. +3.
 template <int HD>
-__device__ __forceinline__ bf16x8 row_frag(const bf16* t, int rb, int kk) {
-    const int lane = threadIdx.x & 63;
-    const int row = rb + (lane & 31);
-    const int c = 2 * kk + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(t + row * HD + ((c ^ swz<HD>(row)) << 3));
-}
-
-// Transposed operand: lane = head_dim column cb + lane%32, 8 values along rows in the
-// permuted order of a 16-row step ks (elements 0..3: rows 16ks + 4h + 0..3, elements 4..7:
-// rows 16ks + 8 + 4h + 0..3, h = lane / 32), read with ds_read_b64_tr_b16: within a group
-// of 16 lanes, output lane i slot j takes element i % 4 of the 4 values at source lane
-// 4j + i / 4, so source lane s = 4j + q addresses row (base + j), columns cb' + 4q .. +3.
-template <int HD>
-__device__ __forceinline__ bf16x8 tr_frag(const bf16* t, int cb, int ks) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, h = lane >> 5, s = lane & 15, j = s >> 2, q = s & 3;
-    const int col = cb + 16 * (g & 1) + 4 * q;
-    v4i16_t r[2];
+struct Frags {
+    static constexpr int KS = HD / 16, OB = HD / 32, RB = HD * 2;  // RB: bytes per row
+    int row_off[KS];
+    int tr_off[OB][2];
+    __device__ __forceinline__ void init() {
+        const int lane = threadIdx.x & 63;
+        const int h = lane >> 5, r = lane & 31;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int row = 16 * ks + 8 * u + 4 * h + j;
-        const bf16* p = t + row * HD + (((col >> 3) ^ swz<HD>(row)) << 3) + (col & 7);
-        r[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
+        for (int kk = 0; kk < KS; ++kk) row_off[kk] = r * RB + (((2 * kk + h) ^ swz<HD>(r)) << 4);
+        const int g = lane >> 4, s = lane & 15, j = s >> 2, q = s & 3;
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int row = 8 * u + 4 * h + j;
+                const int col = 32 * ob + 16 * (g & 1) + 4 * q;
+                tr_off[ob][u] = row * RB + (((col >> 3) ^ swz<HD>(row)) << 4) + (col & 7) * 2;
+            }
     }
-    const uint2 a = __builtin_bit_cast(uint2, r[0]), b = __builtin_bit_cast(uint2, r[1]);
-    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
-}
+    __device__ __forceinline__ bf16x8 row(const char* t, int rb, int kk) const {
+        return *reinterpret_cast<const bf16x8*>(t + rb * RB + row_off[kk]);
+    }
+    __device__ __forceinline__ bf16x8 tr(const char* t, int ob, int ks) const {
+        const v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + 16 * ks * RB + tr_off[ob][0]));
+        const v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + 16 * ks * RB + tr_off[ob][1]));
+        const uint2 x = __builtin_bit_cast(uint2, a), y = __builtin_bit_cast(uint2, b);
+        return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+    }
+};
 
 __device__ __forceinline__ bf16x8 pack_bf16x8(const f32x16& a, int off) {
     return __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(a[off], a[off + 1]), pack_bf16x2(a[off + 2], a[off + 3]),
@@ -145,9 +157,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__
     constexpr int LPT = 2 * (64 * HD / 512 / 4);  // K and V copy instructions per wave per tile
     __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];  // per stage: K then V
 
+    // 1-D grid, heaviest blocks first over all (batch, head) pairs: block id -> (tile, bh)
     const int nq = (S + BQ - 1) / BQ;
-    const int qb = nq - 1 - static_cast<int>(blockIdx.x);
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int BH = static_cast<int>(gridDim.x) / nq;
+    const int qb = nq - 1 - static_cast<int>(blockIdx.x) / BH;
+    const int bh = static_cast<int>(blockIdx.x) % BH, h = bh % H, b = bh / H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
     const int q0 = qb * BQ, qw = q0 + wave * 32, myq = qw + (lane & 31);
     const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
@@ -160,6 +174,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, ldg16(qp + 16 * kk, myq < S));
     }
+    Frags<HD> F;
+    F.init();
     f32x16 oacc[OB];
 #pragma unroll
     for (int i = 0; i < OB; ++i) zero(oacc[i]);
@@ -180,8 +196,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         const int k0 = t * BKV;
-        const bf16* Ks = sm[st];
-        const bf16* Vs = sm[st] + TILE;
+        const char* Kb = reinterpret_cast<const char*>(sm[st]);
+        const char* Vb = reinterpret_cast<const char*>(sm[st] + TILE);
         if (!causal || k0 <= qw + 31) {
             f32x16 s[2];
             zero(s[0]);
@@ -190,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__
             for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb)
-                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Ks, jb * 32, kk), qf[kk], s[jb], 0, 0,
+                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Kb, jb * 32, kk), qf[kk], s[jb], 0, 0,
                                                                      0);
             // s[jb][e]: raw score of key k0 + 32jb + 8(e/4) + 4hl + e%4 and query myq
             const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S;
@@ -238,7 +254,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(const bf16* __restrict__
                 const bf16x8 pf = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
 #pragma unroll
                 for (int ob = 0; ob < OB; ++ob)
-                    oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Vs, ob * 32, ks), pf, oacc[ob], 0, 0,
+                    oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Vb, ob, ks), pf, oacc[ob], 0, 0,
                                                                         0);
             }
         }
@@ -290,9 +306,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
     constexpr int STAGE = 2 * TILE + 2 * 64 * 2;  // Q, dO, then lse and D as fp32 (2 x 64 x 4 B)
     __shared__ __attribute__((aligned(16))) bf16 sm[2][STAGE];
 
+    // 1-D grid, heaviest blocks first (causal: key block 0 sees every query tile)
     const int nkv = (S + BKV - 1) / BKV;
-    const int kblk = causal ? static_cast<int>(blockIdx.x) : nkv - 1 - static_cast<int>(blockIdx.x);
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int BH = static_cast<int>(gridDim.x) / nkv;
+    const int kblk = static_cast<int>(blockIdx.x) / BH;
+    const int bh = static_cast<int>(blockIdx.x) % BH, h = bh % H, b = bh / H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
     const int k0 = kblk * BKV, kw = k0 + wave * 32, mykey = kw + (lane & 31);
     const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
@@ -309,6 +327,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
             vf[kk] = __builtin_bit_cast(bf16x8, ldg16(vp + 16 * kk, mykey < S));
         }
     }
+    Frags<HD> F;
+    F.init();
     f32x16 dvt[OB], dkt[OB];
 #pragma unroll
     for (int i = 0; i < OB; ++i) {
@@ -340,8 +360,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
         }
         __builtin_amdgcn_s_barrier();
         const int qs = qt * BQ;
-        const bf16* Qs = sm[st];
-        const bf16* Os = sm[st] + TILE;
+        const char* Qb = reinterpret_cast<const char*>(sm[st]);
+        const char* Ob = reinterpret_cast<const char*>(sm[st] + TILE);
         const float* Ls = reinterpret_cast<const float*>(sm[st] + 2 * TILE);
         const float* Ds = Ls + 64;
         if (!causal || qs + BQ - 1 >= kw) {
@@ -355,9 +375,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
             for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
-                    s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Qs, mb * 32, kk), kf[kk], s[mb], 0, 0,
+                    s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Qb, mb * 32, kk), kf[kk], s[mb], 0, 0,
                                                                      0);
-                    dp[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Os, mb * 32, kk), vf[kk], dp[mb], 0,
+                    dp[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Ob, mb * 32, kk), vf[kk], dp[mb], 0,
                                                                       0, 0);
                 }
             // s[mb][e]: query qs + 32mb + 8(e/4) + 4hl + e%4, key mykey
@@ -388,8 +408,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
                 for (int ob = 0; ob < OB; ++ob) {
-                    dvt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Os, ob * 32, ks), pf, dvt[ob], 0, 0, 0);
-                    dkt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Qs, ob * 32, ks), dsf, dkt[ob], 0, 0,
+                    dvt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Ob, ob, ks), pf, dvt[ob], 0, 0, 0);
+                    dkt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Qb, ob, ks), dsf, dkt[ob], 0, 0,
                                                                        0);
                 }
             }
@@ -424,9 +444,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
     constexpr int LPT = 2 * (64 * HD / 512 / 4);
     __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];
 
+    // 1-D grid, heaviest blocks first over all (batch, head) pairs: block id -> (tile, bh)
     const int nq = (S + BQ - 1) / BQ;
-    const int qb = nq - 1 - static_cast<int>(blockIdx.x);
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int BH = static_cast<int>(gridDim.x) / nq;
+    const int qb = nq - 1 - static_cast<int>(blockIdx.x) / BH;
+    const int bh = static_cast<int>(blockIdx.x) % BH, h = bh % H, b = bh / H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
     const int q0 = qb * BQ, qw = q0 + wave * 32, myq = qw + (lane & 31);
     const int64_t tok0 = static_cast<int64_t>(b) * S, hoff = static_cast<int64_t>(h) * HD;
@@ -443,6 +465,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
     }
     const float my_l2 = myq < S ? lse[(static_cast<int64_t>(b) * H + h) * S + myq] * kLog2e : 0.0f;
     const float my_D = myq < S ? Dg[(static_cast<int64_t>(b) * H + h) * S + myq] : 0.0f;
+    Frags<HD> F;
+    F.init();
     f32x16 dqt[OB];
 #pragma unroll
     for (int i = 0; i < OB; ++i) zero(dqt[i]);
@@ -462,8 +486,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         const int k0 = t * BKV;
-        const bf16* Ks = sm[st];
-        const bf16* Vs = sm[st] + TILE;
+        const char* Kb = reinterpret_cast<const char*>(sm[st]);
+        const char* Vb = reinterpret_cast<const char*>(sm[st] + TILE);
         if (!causal || k0 <= qw + 31) {
             f32x16 s[2], dp[2];
 #pragma unroll
@@ -475,9 +499,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
             for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb) {
-                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Ks, jb * 32, kk), qf[kk], s[jb], 0, 0,
+                    s[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Kb, jb * 32, kk), qf[kk], s[jb], 0, 0,
                                                                      0);
-                    dp[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<HD>(Vs, jb * 32, kk), df[kk], dp[jb], 0,
+                    dp[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Vb, jb * 32, kk), df[kk], dp[jb], 0,
                                                                       0, 0);
                 }
             const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S || myq >= S;
@@ -497,7 +521,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
                 for (int ob = 0; ob < OB; ++ob)
-                    dqt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(Ks, ob * 32, ks), dsf, dqt[ob], 0, 0,
+                    dqt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Kb, ob, ks), dsf, dqt[ob], 0, 0,
                                                                        0);
             }
         }
@@ -734,10 +758,11 @@ void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void*
               int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s) {
     AIC_CHECK(B >= 0 && H > 0 && S >= 0 && hd > 0 && ld_qkv >= H * hd && ld_o >= H * hd, InvalidArgument,
               "attn_fwd: bad shape");
-    AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31), InvalidArgument, "attn_fwd: sequence too long");
+    AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31) && ((S + 127) / 128) * H * B < (1LL << 31), InvalidArgument,
+              "attn_fwd: sequence too long");
     if (B == 0 || S == 0) return;
     if (dt == DType::BFloat16 && mfma_ok(q, k, v, ld_qkv, o, ld_o, hd)) {
-        const dim3 grid(static_cast<unsigned>((S + 127) / 128), static_cast<unsigned>(H), static_cast<unsigned>(B));
+        const dim3 grid(static_cast<unsigned>(((S + 127) / 128) * H * B));
         const float sl2 = scale * kLog2e;
         if (hd == 128)
             hipLaunchKernelGGL(attn_fwd_mfma<128>, grid, dim3(256), 0, s, static_cast<const bf16*>(q),
@@ -760,7 +785,8 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
               int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s) {
     AIC_CHECK(B >= 0 && H > 0 && S >= 0 && hd > 0 && ld_qkv >= H * hd && ld_o >= H * hd && ld_d >= H * hd,
               InvalidArgument, "attn_bwd: bad shape");
-    AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31), InvalidArgument, "attn_bwd: sequence too long");
+    AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31) && ((S + 127) / 128) * H * B < (1LL << 31), InvalidArgument,
+              "attn_bwd: sequence too long");
     if (B == 0 || S == 0) return;
     DeviceBuffer Dbuf(sizeof(float) * B * H * S, s);
     float* D = Dbuf.as<float>();
@@ -781,8 +807,8 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
     if (dt == DType::BFloat16 && mfma_ok(q, k, v, ld_qkv, dout, ld_o, hd) && ld_d % 8 == 0 && a16(dq) && a16(dk) &&
         a16(dv)) {
         const float sl2 = scale * kLog2e;
-        const dim3 gkv(static_cast<unsigned>((S + 127) / 128), static_cast<unsigned>(H), static_cast<unsigned>(B));
-        const dim3 gq(static_cast<unsigned>((S + 127) / 128), static_cast<unsigned>(H), static_cast<unsigned>(B));
+        const dim3 gkv(static_cast<unsigned>(((S + 127) / 128) * H * B));
+        const dim3 gq(static_cast<unsigned>(((S + 127) / 128) * H * B));
 #define AIC_BWD_MFMA(HD_)                                                                                        \
     do {                                                                                                          \
         hipLaunchKernelGGL(attn_bwd_dkdv_mfma<HD_>, gkv, dim3(256), 0, s, static_cast<const bf16*>(q),            \

@@ -291,6 +291,32 @@ __device__ __forceinline__ void dma_tile(const bf16* __restrict__ g, int64_t ld,
     }
 }
 
+// Instruction i (0 <= i < ROWS * BK / 2048) of this wave's share of a dma_tile copy.
+template <int ROWS, int BK, bool KC>
+__device__ __forceinline__ void dma_one(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, int k0, bf16* s,
+                                        int i) {
+    constexpr int PER_WAVE = ROWS * BK / 512 / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int seg = wave * PER_WAVE + i;
+    const bf16* src;
+    if constexpr (KC) {
+        constexpr int CPR = BK / 8;
+        constexpr int RPS = 64 / CPR;
+        const int row = seg * RPS + lane / CPR;
+        const int lc = (lane % CPR) ^ swz_kc<BK>(row);
+        const int gr = min(row0 + row, nrows - 1);
+        src = g + static_cast<int64_t>(gr) * ld + k0 + lc * 8;
+    } else {
+        constexpr int CPR = ROWS / 8;
+        constexpr int RPS = 64 / CPR;
+        const int k = seg * RPS + lane / CPR;
+        const int lc = (lane % CPR) ^ swz_rc(k);
+        const int gr = min(row0 + lc * 8, nrows - 8);
+        src = g + static_cast<int64_t>(k0 + k) * ld + gr;
+    }
+    dma16(src, s + seg * 512);
+}
+
 // MFMA operand fragment (8 bf16 along k) for rows rb .. rb+31 of a tile, k step kk.
 template <int ROWS, int BK, bool KC>
 __device__ __forceinline__ bf16x8 frag(const bf16* t, int rb, int kk) {
@@ -384,6 +410,18 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) bfr[j] = frag<BN, BK, BKC>(Bs, wn * WN + j * 32, kk);
     };
+    constexpr int PA = BM * BK / 512 / 4;  // A-tile copy instructions per wave
+    auto copy_one = [&](int tile, int stage, int q) {
+        bf16* dst = smem + stage * STAGE;
+        if (q < PA) dma_one<BM, BK, AKC>(p.A, p.lda, m0, p.M, tile * BK, dst, q);
+        else dma_one<BN, BK, BKC>(p.B, p.ldb, n0, p.N, tile * BK, dst + BM * BK, q - PA);
+    };
+    auto read_one = [&](int stage, int kk, int f, bf16x8* af, bf16x8* bfr) {
+        const bf16* As = smem + stage * STAGE;
+        const bf16* Bs = As + BM * BK;
+        if (f < FM) af[f] = frag<BM, BK, AKC>(As, wm * WM + f * 32, kk);
+        else bfr[f - FM] = frag<BN, BK, BKC>(Bs, wn * WN + (f - FM) * 32, kk);
+    };
     // B operand first: acc[i][j] accumulates the transposed 32x32 block (rows n, columns m),
     // so each lane ends up owning runs of four consecutive n of one output row m.
     auto mma = [&](const bf16x8* af, const bf16x8* bfr) {
@@ -424,10 +462,21 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
         wait_lds();  // this wave's reads of stage `cur` are complete
         if (kt + 1 < nk) wait_tiles<LPT>(min(S - 2, nk - 1 - (kt + 1)));  // tile kt+1 has landed
         __builtin_amdgcn_s_barrier();
-        if (kt + S < nk) copy(kt + S, cur);
-        if (kt + 1 < nk) read((kt + 1) % S, 0, fa[0], fb[0]);
-        mma(fa[1], fb[1]);
-        interleave();
+        // Last k step: its MFMAs, the copy of tile kt+S into the freed stage and the first
+        // fragment reads of tile kt+1 go out interleaved one by one, so the copy issue never
+        // holds back the MFMA pipe.
+        const int nxt = (kt + 1) % S;
+        const bool more_copies = kt + S < nk, more_tiles = kt + 1 < nk;
+#pragma unroll
+        for (int q = 0; q < NMF; ++q) {
+            acc[q / FN][q % FN] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][q % FN], fa[1][q / FN], acc[q / FN][q % FN], 0, 0, 0);
+            if (more_copies) {
+#pragma unroll
+                for (int c = q * LPT / NMF; c < (q + 1) * LPT / NMF; ++c) copy_one(kt + S, cur, c);
+            }
+            if (q < FM + FN && more_tiles) read_one(nxt, 0, q, fa[0], fb[0]);
+        }
     }
 
     // Epilogue.  Lane owns output row m = mb + lane % 32 and, in block (i, j), the columns
