@@ -77,6 +77,16 @@ SIGNATURES = {
                                   i32, f32, f32, f32, f32, f32, i64, vp, vp]),
     "aic_hip_adamw_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, vp]),
     "aic_hip_cast_f32_bf16": (i32, [vp, vp, i64, vp]),
+    "aic_hip_moe_route": (i32, [vp, i64, i64, i64, f32, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "aic_hip_moe_max_rows": (i64, [i64, i64, i64]),
+    "aic_hip_moe_permute": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp]),
+    "aic_hip_moe_gather": (i32, [vp, i64, vp, i64, i64, i64, vp, i32, vp]),
+    "aic_hip_moe_combine": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, i64, vp, i64, i32, vp]),
+    "aic_moe_ffn_create": (i32, [i64, i64, i64, i64, f32, i32, C.POINTER(vp)]),
+    "aic_moe_ffn_destroy": (i32, [vp]),
+    "aic_moe_ffn_forward": (i32, [vp, vp, i64, vp, vp, vp, vp, vp, vp]),
+    "aic_moe_ffn_backward": (i32, [vp, vp, f32, vp, vp, vp, vp]),
+    "aic_moe_ffn_routing": (i32, [vp, vp, vp, vp]),
     "aic_lm_create": (i32, [C.POINTER(LMConfig), C.POINTER(TrainConfig), C.POINTER(vp)]),
     "aic_lm_destroy": (i32, [vp]),
     "aic_lm_num_params": (i64, [vp]),

@@ -12,6 +12,7 @@
 #include "../data/synthetic.hpp"
 #include "../kernels/gemm.hpp"
 #include "../kernels/kernels.hpp"
+#include "../model/moe_ffn.hpp"
 #include "../model/transformer_lm.hpp"
 #include "../runtime/error.hpp"
 #include "../runtime/memory_pool.hpp"
@@ -54,6 +55,10 @@ const char* dtype_name(DType d) noexcept {
 }
 
 }  // namespace aic
+
+struct aic_moe_ffn {
+    aic::models::MoEFFN* ffn;
+};
 
 struct aic_lm {
     aic::models::TransformerLM* model;
@@ -443,6 +448,91 @@ int aic_synth_normal(uint64_t seed, int64_t n, float mean, float std, float* out
     return guard([&] {
         AIC_CHECK(out_host && n >= 0, InvalidArgument, "bad arguments");
         aic::data::normal(seed, n, mean, std, out_host);
+    });
+}
+
+
+// ---------------------------------------------------------------------------------------
+// Mixture of experts
+// ---------------------------------------------------------------------------------------
+int aic_hip_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx, float* gsel,
+                      float* probs, float* rweights, int64_t* counts, float* mean_probs, float* aux, aic_stream stream) {
+    return guard([&] {
+        aic::hip::moe_route(logits, T, E, k, aux_coef, idx, gsel, probs, rweights, counts, mean_probs, aux, st(stream));
+    });
+}
+
+int64_t aic_hip_moe_max_rows(int64_t T, int64_t E, int64_t k) { return aic::hip::moe_max_rows(T, E, k); }
+
+int aic_hip_moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k, int64_t E, int64_t* offsets,
+                        int32_t* dst_row, int32_t* src_ent, aic_stream stream) {
+    return guard([&] { aic::hip::moe_permute(idx, counts, T, k, E, offsets, dst_row, src_ent, st(stream)); });
+}
+
+int aic_hip_moe_gather(const void* x, int64_t ldx, const int32_t* src_ent, int64_t k, int64_t rows, int64_t d,
+                       void* xp, aic_dtype dtype, aic_stream stream) {
+    return guard([&] { aic::hip::moe_gather(x, ldx, src_ent, k, rows, d, xp, dt(dtype), st(stream)); });
+}
+
+int aic_hip_moe_combine(const void* ye, const int64_t* idx, const int32_t* dst_row, const float* gsel, int64_t T,
+                        int64_t k, int64_t d, const void* residual, int64_t ldr, void* out, int64_t ldo, aic_dtype dtype,
+                        aic_stream stream) {
+    return guard([&] {
+        aic::hip::moe_combine(ye, idx, dst_row, gsel, T, k, d, residual, ldr, out, ldo, dt(dtype), st(stream));
+    });
+}
+
+int aic_moe_ffn_create(int64_t d_model, int64_t d_hidden, int64_t num_experts, int64_t top_k, float aux_loss_coef,
+                       aic_dtype dtype, aic_moe_ffn** out) {
+    return guard([&] {
+        AIC_CHECK(out, InvalidArgument, "null argument");
+        auto* h = new aic_moe_ffn{nullptr};
+        try {
+            h->ffn = new aic::models::MoEFFN(d_model, d_hidden, num_experts, top_k, aux_loss_coef, dt(dtype));
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int aic_moe_ffn_destroy(aic_moe_ffn* m) {
+    return guard([&] {
+        if (!m) return;
+        delete m->ffn;
+        delete m;
+    });
+}
+
+int aic_moe_ffn_forward(aic_moe_ffn* m, const void* h, int64_t T, const void* router_w, const void* experts,
+                        const void* residual, void* y, float* aux, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(m, InvalidArgument, "null handle");
+        m->ffn->forward(h, T, router_w, experts, residual, y, aux, st(stream));
+    });
+}
+
+int aic_moe_ffn_backward(aic_moe_ffn* m, const void* dy, float daux, void* dh, float* drouter_w, float* dexperts,
+                         aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(m, InvalidArgument, "null handle");
+        m->ffn->backward(dy, daux, dh, drouter_w, dexperts, st(stream));
+    });
+}
+
+int aic_moe_ffn_routing(aic_moe_ffn* m, int64_t* idx_host, int64_t* counts_host, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(m && idx_host && counts_host, InvalidArgument, "null argument");
+        (void)stream;
+        AIC_HIP_CHECK(hipDeviceSynchronize());
+        const auto& ch = m->ffn->counts_host();
+        int64_t T = 0;
+        for (size_t e = 0; e < ch.size(); ++e) {
+            counts_host[e] = ch[e];
+            T += ch[e];
+        }
+        AIC_HIP_CHECK(hipMemcpy(idx_host, m->ffn->idx(), sizeof(int64_t) * T, hipMemcpyDeviceToHost));
     });
 }
 

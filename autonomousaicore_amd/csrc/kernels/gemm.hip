@@ -358,6 +358,126 @@ __device__ __forceinline__ void wait_lds() {
     __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
+// Epilogue of the MFMA kernels: C = alpha * acc (+ beta * C) (+ R) for this block's tile.
+// acc[i][j] holds the transposed 32x32 block (rows n, columns m) of wave (wm, wn).
+template <int BM, int BN, int LDS_BYTES, typename CT>
+__device__ __forceinline__ void gemm_epilogue(const MfmaParams& p, const f32x16 (&acc)[BM / 64][BN / 64], bf16* smem,
+                                              int m0, int n0) {
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // Epilogue.  Lane owns output row m = mb + lane % 32 and, in block (i, j), the columns
+    // n = nb + 8g + 4h + 0..3 (g = 0..3, h = lane / 32) in acc[i][j][4g .. 4g+3].
+    CT* C = static_cast<CT*>(p.C);
+    const CT* R = static_cast<const CT*>(p.R);
+    const int h = lane >> 5;
+    if (p.vec && m0 + BM <= p.M && n0 + BN <= p.N) {
+        // Full tile: each wave stages its WM x WN sub-tile through its quarter of the (now
+        // idle) LDS, so that every global store (and residual load) moves 16 contiguous
+        // bytes per lane, whole rows per instruction.  After the loop's last barrier no wave
+        // reads operand stages any more and no copy is in flight.
+        constexpr int E = sizeof(CT);
+        constexpr int RB = WN * E;                                       // bytes per sub-tile row
+        constexpr int CPR = RB / 16;                                     // 16-byte chunks per row
+        constexpr int REGION = LDS_BYTES / 4;  // LDS bytes per wave
+        constexpr int FIT = REGION / RB < WM ? REGION / RB : WM;  // rows that fit the region
+        constexpr int IB = FIT / 32;                                // 32-row blocks per pass
+        constexpr int PASS_ROWS = IB * 32;                          // rows staged per pass
+        constexpr int VE = 16 / E;     // elements per chunk
+        constexpr int RPI = 64 / CPR;  // rows per 64-lane instruction
+        static_assert(IB >= 1 && FM % IB == 0 && (CPR & (CPR - 1)) == 0 && PASS_ROWS % RPI == 0,
+                      "epilogue staging");
+        char* region = reinterpret_cast<char*>(smem) + wave * REGION;
+        const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
+#pragma unroll
+        for (int i0 = 0; i0 < FM; i0 += IB) {
+#pragma unroll
+            for (int ii = 0; ii < IB; ++ii) {
+                const int r = ii * 32 + (lane & 31);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int byte = (32 * j + 8 * g + 4 * h) * E;
+                        char* d = region + r * RB + (((byte >> 4) ^ (r & (CPR - 1))) << 4) + (byte & 15);
+                        const f32x16& a = acc[i0 + ii][j];
+                        const float v0 = p.alpha * a[4 * g], v1 = p.alpha * a[4 * g + 1];
+                        const float v2 = p.alpha * a[4 * g + 2], v3 = p.alpha * a[4 * g + 3];
+                        if constexpr (E == 2)
+                            *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+                        else
+                            *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
+                    }
+            }
+            wait_lds();
+#pragma unroll
+            for (int t = 0; t < PASS_ROWS / RPI; ++t) {
+                const int r = t * RPI + lane / CPR, c = lane % CPR;
+                const uint4 raw = *reinterpret_cast<const uint4*>(region + r * RB + ((c ^ (r & (CPR - 1))) << 4));
+                const int64_t gm = wrow0 + i0 * 32 + r;
+                const int gn = wcol0 + c * VE;
+                CT* dst = C + gm * p.ldc + gn;
+                float v[VE];
+                if constexpr (E == 2) {
+                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        v[2 * q] = __uint_as_float(w[q] << 16);
+                        v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+                    }
+                } else {
+                    v[0] = __uint_as_float(raw.x); v[1] = __uint_as_float(raw.y);
+                    v[2] = __uint_as_float(raw.z); v[3] = __uint_as_float(raw.w);
+                }
+                if (p.beta != 0.0f) {
+#pragma unroll
+                    for (int q = 0; q < VE; q += 4) {
+                        float c4[4];
+                        ld4(dst + q, c4);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[q + u] += p.beta * c4[u];
+                    }
+                }
+                if (R) {
+#pragma unroll
+                    for (int q = 0; q < VE; q += 4) {
+                        float r4[4];
+                        ld4(R + gm * p.ldr + gn + q, r4);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[q + u] += r4[u];
+                    }
+                }
+                if constexpr (E == 2) {
+                    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+                } else {
+                    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+            wait_lds();  // the next pass overwrites the region
+        }
+        return;
+    }
+    const int nw = n0 + wn * WN + 4 * h;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int n = nw + j * 32 + 8 * (e >> 2) + (e & 3);
+                if (n >= p.N) continue;
+                float v = p.alpha * acc[i][j][e];
+                const int64_t ci = static_cast<int64_t>(m) * p.ldc + n;
+                if (p.beta != 0.0f) v += p.beta * ld(C, ci);
+                if (R) v += ld(R, static_cast<int64_t>(m) * p.ldr + n);
+                st(C, ci, v);
+            }
+    }
+}
+
 // Main loop schedule (per wave): fragments are double-buffered in registers; the reads of
 // k step ks+1 are interleaved with the MFMAs of step ks (sched_group_barrier hints).  The
 // barrier that publishes tile kt+1 sits before the MFMAs of the tile's last k step, so the
@@ -479,116 +599,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
         }
     }
 
-    // Epilogue.  Lane owns output row m = mb + lane % 32 and, in block (i, j), the columns
-    // n = nb + 8g + 4h + 0..3 (g = 0..3, h = lane / 32) in acc[i][j][4g .. 4g+3].
-    CT* C = static_cast<CT*>(p.C);
-    const CT* R = static_cast<const CT*>(p.R);
-    const int h = lane >> 5;
-    if (p.vec && m0 + BM <= p.M && n0 + BN <= p.N) {
-        // Full tile: each wave stages its WM x WN sub-tile through its quarter of the (now
-        // idle) LDS, so that every global store (and residual load) moves 16 contiguous
-        // bytes per lane, whole rows per instruction.  After the loop's last barrier no wave
-        // reads operand stages any more and no copy is in flight.
-        constexpr int E = sizeof(CT);
-        constexpr int RB = WN * E;                                       // bytes per sub-tile row
-        constexpr int CPR = RB / 16;                                     // 16-byte chunks per row
-        constexpr int REGION = S * STAGE * 2 / 4;                        // LDS bytes per wave
-        constexpr int FIT = REGION / RB < WM ? REGION / RB : WM;  // rows that fit the region
-        constexpr int IB = FIT / 32;                                // 32-row blocks per pass
-        constexpr int PASS_ROWS = IB * 32;                          // rows staged per pass
-        constexpr int VE = 16 / E;     // elements per chunk
-        constexpr int RPI = 64 / CPR;  // rows per 64-lane instruction
-        static_assert(IB >= 1 && FM % IB == 0 && (CPR & (CPR - 1)) == 0 && PASS_ROWS % RPI == 0,
-                      "epilogue staging");
-        char* region = reinterpret_cast<char*>(smem) + wave * REGION;
-        const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
-#pragma unroll
-        for (int i0 = 0; i0 < FM; i0 += IB) {
-#pragma unroll
-            for (int ii = 0; ii < IB; ++ii) {
-                const int r = ii * 32 + (lane & 31);
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int byte = (32 * j + 8 * g + 4 * h) * E;
-                        char* d = region + r * RB + (((byte >> 4) ^ (r & (CPR - 1))) << 4) + (byte & 15);
-                        const f32x16& a = acc[i0 + ii][j];
-                        const float v0 = p.alpha * a[4 * g], v1 = p.alpha * a[4 * g + 1];
-                        const float v2 = p.alpha * a[4 * g + 2], v3 = p.alpha * a[4 * g + 3];
-                        if constexpr (E == 2)
-                            *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
-                        else
-                            *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
-                    }
-            }
-            wait_lds();
-#pragma unroll
-            for (int t = 0; t < PASS_ROWS / RPI; ++t) {
-                const int r = t * RPI + lane / CPR, c = lane % CPR;
-                const uint4 raw = *reinterpret_cast<const uint4*>(region + r * RB + ((c ^ (r & (CPR - 1))) << 4));
-                const int64_t gm = wrow0 + i0 * 32 + r;
-                const int gn = wcol0 + c * VE;
-                CT* dst = C + gm * p.ldc + gn;
-                float v[VE];
-                if constexpr (E == 2) {
-                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        v[2 * q] = __uint_as_float(w[q] << 16);
-                        v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-                    }
-                } else {
-                    v[0] = __uint_as_float(raw.x); v[1] = __uint_as_float(raw.y);
-                    v[2] = __uint_as_float(raw.z); v[3] = __uint_as_float(raw.w);
-                }
-                if (p.beta != 0.0f) {
-#pragma unroll
-                    for (int q = 0; q < VE; q += 4) {
-                        float c4[4];
-                        ld4(dst + q, c4);
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) v[q + u] += p.beta * c4[u];
-                    }
-                }
-                if (R) {
-#pragma unroll
-                    for (int q = 0; q < VE; q += 4) {
-                        float r4[4];
-                        ld4(R + gm * p.ldr + gn + q, r4);
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) v[q + u] += r4[u];
-                    }
-                }
-                if constexpr (E == 2) {
-                    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
-                } else {
-                    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-            wait_lds();  // the next pass overwrites the region
-        }
-        return;
-    }
-    const int nw = n0 + wn * WN + 4 * h;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int m = m0 + wm * WM + i * 32 + (lane & 31);
-        if (m >= p.M) continue;
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int n = nw + j * 32 + 8 * (e >> 2) + (e & 3);
-                if (n >= p.N) continue;
-                float v = p.alpha * acc[i][j][e];
-                const int64_t ci = static_cast<int64_t>(m) * p.ldc + n;
-                if (p.beta != 0.0f) v += p.beta * ld(C, ci);
-                if (R) v += ld(R, static_cast<int64_t>(m) * p.ldr + n);
-                st(C, ci, v);
-            }
-    }
+    gemm_epilogue<BM, BN, S * STAGE * 2, CT>(p, acc, smem, m0, n0);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -40,6 +40,23 @@ void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t 
 void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, bool accumulate,
                DType dt, hipStream_t s);
 
+// Mixture of experts (moe.hip).  Expert row blocks start at multiples of 64 rows.
+int64_t moe_max_rows(int64_t T, int64_t E, int64_t k);
+void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx, float* gsel,
+               float* probs, float* rweights, int64_t* counts, float* mean_probs, float* aux, hipStream_t s);
+void moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k, int64_t E, int64_t* offsets,
+                 int* dst_row, int* src_ent, hipStream_t s);
+void moe_gather(const void* x, int64_t ldx, const int* src_ent, int64_t k, int64_t rows, int64_t d, void* xp, DType dt,
+                hipStream_t s);
+void moe_combine(const void* ye, const int64_t* idx, const int* dst_row, const float* gsel, int64_t T, int64_t k,
+                 int64_t d, const void* R, int64_t ldr, void* out, int64_t ldo, DType dt, hipStream_t s);
+void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* src_ent, const float* gsel, int64_t rows,
+                     int64_t k, int64_t d, void* dye, float* dgsel, DType dt, hipStream_t s);
+void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_t T, int64_t k, int64_t d, void* dx,
+                 int64_t ldx, bool accumulate, DType dt, hipStream_t s);
+void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
+                    int64_t E, int64_t k, float aux_coef, float daux, float* dlogits, hipStream_t s);
+
 // Attention (attention.hip)
 void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
               int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);

@@ -1,0 +1,423 @@
+// Mixture-of-experts routing, dispatch and combine (the MoE FFN of MoETransformerBlock).
+//
+// Replaces MoERouter::route (src/nn/moe.cpp:33-129), which copies the gate logits to the
+// host, partial-sorts every token there and copies indices, weights and counts back, and the
+// dense dispatch of MoELayer::forward (moe.cpp:155-253), which runs every active expert on
+// every token and multiplies by a zero gate for the tokens it does not own.  Here routing,
+// counts and the auxiliary loss stay on the device, tokens are permuted into contiguous
+// per-expert row blocks (a stable counting sort), each expert's SwiGLU runs only on its own
+// rows, and the weighted combine gathers them back.  Nothing uses atomics: every reduction
+// has a fixed order, so routing and gradients are bit-reproducible.
+//
+// Semantics shared with the reference (and the CPU oracle):
+//   probs = softmax(logits) (max-shift, exp, sum, divide); top-k by logit, descending, ties to
+//   the lower expert index (the reference's partial_sort leaves ties unspecified);
+//   gates = probs * mask / (sum(probs * mask) + 1e-9) (moe.cpp:202-204);
+//   aux = sum_e mean_t(probs[t, e]) * counts[e] * E * coef / (T * k) when coef > 0 and E > 1
+//   (moe.cpp:84-101), the counts entering as constants.
+#include <cstring>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace aic::hip {
+
+namespace {
+
+constexpr int kMaxE = 64;  // experts per layer handled by the per-token kernels
+constexpr int kMaxK = 8;   // experts per token
+
+// One thread per token: softmax over E, top-k selection, normalised gates of the selected.
+__global__ __launch_bounds__(256) void moe_route_k(const float* __restrict__ logits, int T, int E, int k,
+                                                   int64_t* __restrict__ idx, float* __restrict__ gsel,
+                                                   float* __restrict__ probs, float* __restrict__ rweights) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const float* row = logits + static_cast<int64_t>(t) * E;
+    float x[kMaxE];
+    float m = row[0];
+    for (int e = 0; e < E; ++e) {
+        x[e] = row[e];
+        m = fmaxf(m, x[e]);
+    }
+    double s = 0.0;
+    float p[kMaxE];
+    for (int e = 0; e < E; ++e) {
+        p[e] = expf(x[e] - m);
+        s += static_cast<double>(p[e]);
+    }
+    const float sf = static_cast<float>(s);
+    for (int e = 0; e < E; ++e) {
+        p[e] = p[e] / sf;
+        probs[static_cast<int64_t>(t) * E + e] = p[e];
+    }
+    // selection: repeatedly the largest remaining logit, the lowest index among equals
+    uint64_t used = 0;
+    int sel[kMaxK];
+    for (int j = 0; j < k; ++j) {
+        int best = -1;
+        for (int e = 0; e < E; ++e)
+            if (!((used >> e) & 1) && (best < 0 || x[e] > x[best])) best = e;
+        used |= 1ull << best;
+        sel[j] = best;
+        idx[static_cast<int64_t>(t) * k + j] = best;
+    }
+    double den = 0.0;
+    for (int e = 0; e < E; ++e)
+        if ((used >> e) & 1) den += static_cast<double>(p[e]);
+    const float denf = static_cast<float>(den) + 1e-9f;
+    for (int j = 0; j < k; ++j) gsel[static_cast<int64_t>(t) * k + j] = p[sel[j]] / denf;
+    if (rweights) {  // route()'s routing_weights: softmax over the selected logits (moe.cpp:67-77)
+        const float mx = x[sel[0]];
+        float se = 0.0f;
+        for (int j = 0; j < k; ++j) se += expf(x[sel[j]] - mx);
+        for (int j = 0; j < k; ++j) rweights[static_cast<int64_t>(t) * k + j] = expf(x[sel[j]] - mx) / (se + 1e-9f);
+    }
+}
+
+// One block: per-expert counts, mean probabilities (double, fixed order) and the aux loss.
+__global__ __launch_bounds__(256) void moe_stats_k(const int64_t* __restrict__ idx, const float* __restrict__ probs,
+                                                   int T, int E, int k, float aux_coef, int64_t* __restrict__ counts,
+                                                   float* __restrict__ mean_probs, float* __restrict__ aux) {
+    __shared__ double sp[256];
+    __shared__ long long sc[256];
+    __shared__ float mp_s[kMaxE];
+    __shared__ long long cnt_s[kMaxE];
+    for (int e = 0; e < E; ++e) {
+        double a = 0.0;
+        long long c = 0;
+        for (int t = threadIdx.x; t < T; t += blockDim.x) {
+            a += static_cast<double>(probs[static_cast<int64_t>(t) * E + e]);
+            for (int j = 0; j < k; ++j) c += idx[static_cast<int64_t>(t) * k + j] == e;
+        }
+        sp[threadIdx.x] = a;
+        sc[threadIdx.x] = c;
+        __syncthreads();
+        for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+            if (threadIdx.x < w) {
+                sp[threadIdx.x] += sp[threadIdx.x + w];
+                sc[threadIdx.x] += sc[threadIdx.x + w];
+            }
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) {
+            mp_s[e] = static_cast<float>(sp[0] / static_cast<double>(T));
+            cnt_s[e] = sc[0];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        double a = 0.0;
+        const float scale = (static_cast<float>(E) * aux_coef) / (static_cast<float>(T) * static_cast<float>(k));
+        for (int e = 0; e < E; ++e) {
+            if (mean_probs) mean_probs[e] = mp_s[e];
+            counts[e] = cnt_s[e];
+            a += static_cast<double>(mp_s[e] * (static_cast<float>(cnt_s[e]) * scale));
+        }
+        if (aux) *aux = (aux_coef > 0.0f && E > 1) ? static_cast<float>(a) : 0.0f;
+    }
+}
+
+constexpr int kRowAlign = 64;  // each expert's row block starts at a multiple of 64 rows
+__device__ __forceinline__ long long align_rows(long long n) { return (n + kRowAlign - 1) / kRowAlign * kRowAlign; }
+
+// One block per expert: stable positions of its (token, slot) entries in token order, in a
+// row block that starts at offsets[e] (a multiple of 64; the block is padded to 64 rows).
+// dst_row[t * k + j] = row of that entry; src_ent[row] = t * k + j, or -1 for a padding row.
+__global__ __launch_bounds__(256) void moe_permute_k(const int64_t* __restrict__ idx, const int64_t* __restrict__ counts,
+                                                     int T, int k, int E, int64_t* __restrict__ offsets,
+                                                     int* __restrict__ dst_row, int* __restrict__ src_ent) {
+    const int e = blockIdx.x;
+    __shared__ int scan[256];
+    __shared__ int base_s, start_s;
+    if (threadIdx.x == 0) {
+        long long off = 0;
+        for (int i = 0; i < e; ++i) off += align_rows(counts[i]);
+        base_s = static_cast<int>(off);
+        start_s = static_cast<int>(off);
+        if (e == 0) {
+            long long o = 0;
+            for (int i = 0; i < E; ++i) {
+                offsets[i] = o;
+                o += align_rows(counts[i]);
+            }
+            offsets[E] = o;
+        }
+    }
+    __syncthreads();
+    const int n = T * k;
+    for (int c0 = 0; c0 < n; c0 += blockDim.x) {
+        const int i = c0 + threadIdx.x;
+        const int hit = (i < n && idx[i] == e) ? 1 : 0;
+        scan[threadIdx.x] = hit;
+        __syncthreads();
+        for (int w = 1; w < static_cast<int>(blockDim.x); w <<= 1) {  // inclusive Hillis-Steele scan
+            const int v = threadIdx.x >= w ? scan[threadIdx.x - w] : 0;
+            __syncthreads();
+            scan[threadIdx.x] += v;
+            __syncthreads();
+        }
+        if (hit) {
+            const int row = base_s + scan[threadIdx.x] - 1;
+            dst_row[i] = row;
+            src_ent[row] = i;
+        }
+        const int total = scan[blockDim.x - 1];
+        __syncthreads();
+        if (threadIdx.x == 0) base_s += total;
+        __syncthreads();
+    }
+    const int end = start_s + static_cast<int>(align_rows(base_s - start_s));
+    for (int r = base_s + threadIdx.x; r < end; r += blockDim.x) src_ent[r] = -1;
+}
+
+// xp[r, :] = x[token of entry src_ent[r], :], zero for padding rows
+template <typename T>
+__global__ __launch_bounds__(256) void moe_gather_k(const T* __restrict__ x, int64_t ldx, const int* __restrict__ src,
+                                                    int k, int d, T* __restrict__ xp) {
+    const int r = blockIdx.x;
+    const int ent = src[r];
+    T* o = xp + static_cast<int64_t>(r) * d;
+    if (ent < 0) {
+        for (int c = threadIdx.x; c < d; c += blockDim.x) st(o, c, 0.0f);
+        return;
+    }
+    const T* s = x + static_cast<int64_t>(ent / k) * ldx;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) o[c] = s[c];
+}
+
+// The token's slots in increasing expert order (the order the reference accumulates experts).
+__device__ __forceinline__ void slot_order(const int64_t* idx_t, int k, int* ord) {
+    for (int j = 0; j < k; ++j) ord[j] = j;
+    for (int a = 1; a < k; ++a)
+        for (int b = a; b > 0 && idx_t[ord[b]] < idx_t[ord[b - 1]]; --b) {
+            const int tmp = ord[b];
+            ord[b] = ord[b - 1];
+            ord[b - 1] = tmp;
+        }
+}
+
+// out[t, :] = R[t, :] + sum over slots (increasing expert) of gsel[t, j] * ye[dst_row[t, j], :]
+template <typename T>
+__global__ __launch_bounds__(256) void moe_combine_k(const T* __restrict__ ye, const int64_t* __restrict__ idx,
+                                                     const int* __restrict__ dst_row, const float* __restrict__ gsel,
+                                                     int k, int d, const T* __restrict__ R, int64_t ldr,
+                                                     T* __restrict__ out, int64_t ldo) {
+    const int t = blockIdx.x;
+    int ord[kMaxK];
+    slot_order(idx + static_cast<int64_t>(t) * k, k, ord);
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        float y = 0.0f;
+        for (int q = 0; q < k; ++q) {
+            const int j = ord[q];
+            const int r = dst_row[static_cast<int64_t>(t) * k + j];
+            y += ld(ye, static_cast<int64_t>(r) * d + c) * gsel[static_cast<int64_t>(t) * k + j];
+        }
+        const float base = R ? ld(R, static_cast<int64_t>(t) * ldr + c) : 0.0f;
+        st(out, static_cast<int64_t>(t) * ldo + c, base + y);
+    }
+}
+
+// Per expert row r (entry t * k + j): dye[r] = gsel[t, j] * dout[t] and
+// dgsel[t, j] = sum_c dout[t, c] * ye[r, c] (double, fixed order); padding rows get dye = 0.
+template <typename T>
+__global__ __launch_bounds__(256) void moe_combine_bwd_k(const T* __restrict__ dout, int64_t ldo, const T* __restrict__ ye,
+                                                         const int* __restrict__ src_ent, const float* __restrict__ gsel,
+                                                         int k, int d, T* __restrict__ dye, float* __restrict__ dgsel) {
+    const int r = blockIdx.x;
+    const int ent = src_ent[r];
+    T* dr = dye + static_cast<int64_t>(r) * d;
+    if (ent < 0) {
+        for (int c = threadIdx.x; c < d; c += blockDim.x) st(dr, c, 0.0f);
+        return;
+    }
+    const int t = ent / k;
+    const float g = gsel[ent];
+    __shared__ double red[256];
+    double acc = 0.0;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        const float go = ld(dout, static_cast<int64_t>(t) * ldo + c);
+        acc += static_cast<double>(go * ld(ye, static_cast<int64_t>(r) * d + c));
+        st(dr, c, go * g);
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dgsel[ent] = static_cast<float>(red[0]);
+}
+
+// dx[t, :] (+)= sum over slots (increasing expert) of dxp[dst_row[t, j], :]
+template <typename T>
+__global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, const int64_t* __restrict__ idx,
+                                                     const int* __restrict__ dst_row, int k, int d, T* __restrict__ dx,
+                                                     int64_t ldx, int accumulate) {
+    const int t = blockIdx.x;
+    int ord[kMaxK];
+    slot_order(idx + static_cast<int64_t>(t) * k, k, ord);
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        float s = 0.0f;
+        for (int q = 0; q < k; ++q) {
+            const int r = dst_row[static_cast<int64_t>(t) * k + ord[q]];
+            s += ld(dxp, static_cast<int64_t>(r) * d + c);
+        }
+        const int64_t o = static_cast<int64_t>(t) * ldx + c;
+        st(dx, o, accumulate ? ld(dx, o) + s : s);
+    }
+}
+
+// Router backward, one thread per token: gradient of the gates (normalisation and mask) and of
+// the aux loss through both softmaxes into dlogits [T, E] (overwritten).
+__global__ __launch_bounds__(256) void moe_router_bwd_k(const float* __restrict__ probs, const int64_t* __restrict__ idx,
+                                                        const float* __restrict__ dgsel,
+                                                        const int64_t* __restrict__ counts, int T, int E, int k,
+                                                        float aux_coef, float daux, float* __restrict__ dlogits) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const float* p = probs + static_cast<int64_t>(t) * E;
+    float dg[kMaxE];
+    uint64_t used = 0;
+    for (int e = 0; e < E; ++e) dg[e] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        const int e = static_cast<int>(idx[static_cast<int64_t>(t) * k + j]);
+        used |= 1ull << e;
+        dg[e] = dgsel[static_cast<int64_t>(t) * k + j];
+    }
+    double den = 0.0;
+    for (int e = 0; e < E; ++e)
+        if ((used >> e) & 1) den += static_cast<double>(p[e]);
+    const float denf = static_cast<float>(den) + 1e-9f;
+    double sb = 0.0;
+    for (int e = 0; e < E; ++e)
+        if ((used >> e) & 1) sb += static_cast<double>(-dg[e] * p[e] / (denf * denf));
+    float dp[kMaxE];
+    for (int e = 0; e < E; ++e) dp[e] = ((used >> e) & 1) ? (dg[e] / denf + static_cast<float>(sb)) : 0.0f;
+    float dl[kMaxE];
+    double s = 0.0;
+    for (int e = 0; e < E; ++e) s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
+    float sf = static_cast<float>(s);
+    for (int e = 0; e < E; ++e) dl[e] = p[e] * (dp[e] - sf);
+    if (aux_coef > 0.0f && E > 1) {
+        const float fscale = (static_cast<float>(E) * aux_coef) / (static_cast<float>(T) * static_cast<float>(k));
+        s = 0.0;
+        for (int e = 0; e < E; ++e) {
+            dp[e] = (daux * (static_cast<float>(counts[e]) * fscale)) / static_cast<float>(T);
+            s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
+        }
+        sf = static_cast<float>(s);
+        for (int e = 0; e < E; ++e) dl[e] += p[e] * (dp[e] - sf);
+    }
+    for (int e = 0; e < E; ++e) dlogits[static_cast<int64_t>(t) * E + e] = dl[e];
+}
+
+void check_moe(int64_t T, int64_t E, int64_t k) {
+    AIC_CHECK(T >= 1 && T < (1LL << 28), InvalidArgument, "moe: token count out of range");
+    AIC_CHECK(E >= 1 && E <= kMaxE, InvalidArgument, "moe: experts must be in [1, ", kMaxE, "]");
+    AIC_CHECK(k >= 1 && k <= kMaxK && k <= E, InvalidArgument, "moe: top_k must be in [1, min(E, ", kMaxK, ")]");
+}
+
+}  // namespace
+
+void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx, float* gsel,
+               float* probs, float* rweights, int64_t* counts, float* mean_probs, float* aux, hipStream_t s) {
+    check_moe(T, E, k);
+    AIC_CHECK(logits && idx && gsel && probs && counts, InvalidArgument, "moe_route: null argument");
+    hipLaunchKernelGGL(moe_route_k, dim3(grid_for(T, 256)), dim3(256), 0, s, logits, static_cast<int>(T),
+                       static_cast<int>(E), static_cast<int>(k), idx, gsel, probs, rweights);
+    AIC_LAUNCH_CHECK("moe_route");
+    hipLaunchKernelGGL(moe_stats_k, dim3(1), dim3(256), 0, s, idx, probs, static_cast<int>(T), static_cast<int>(E),
+                       static_cast<int>(k), aux_coef, counts, mean_probs, aux);
+    AIC_LAUNCH_CHECK("moe_stats");
+}
+
+int64_t moe_max_rows(int64_t T, int64_t E, int64_t k) { return T * k + E * (kRowAlign - 1); }
+
+void moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k, int64_t E, int64_t* offsets,
+                 int* dst_row, int* src_ent, hipStream_t s) {
+    check_moe(T, E, k);
+    AIC_CHECK(idx && counts && offsets && dst_row && src_ent, InvalidArgument, "moe_permute: null argument");
+    hipLaunchKernelGGL(moe_permute_k, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, idx, counts,
+                       static_cast<int>(T), static_cast<int>(k), static_cast<int>(E), offsets, dst_row, src_ent);
+    AIC_LAUNCH_CHECK("moe_permute");
+}
+
+void moe_gather(const void* x, int64_t ldx, const int* src_ent, int64_t k, int64_t rows, int64_t d, void* xp, DType dt,
+                hipStream_t s) {
+    AIC_CHECK(rows >= 0 && d > 0 && ldx >= d && k >= 1, InvalidArgument, "moe_gather: bad shape");
+    if (rows == 0) return;
+    if (dt == DType::BFloat16)
+        hipLaunchKernelGGL(moe_gather_k<bf16>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                           static_cast<const bf16*>(x), ldx, src_ent, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<bf16*>(xp));
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL(moe_gather_k<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                           static_cast<const float*>(x), ldx, src_ent, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<float*>(xp));
+    else
+        AIC_THROW(DTypeMismatch, "moe_gather: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("moe_gather");
+}
+
+void moe_combine(const void* ye, const int64_t* idx, const int* dst_row, const float* gsel, int64_t T, int64_t k,
+                 int64_t d, const void* R, int64_t ldr, void* out, int64_t ldo, DType dt, hipStream_t s) {
+    AIC_CHECK(T >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldo >= d, InvalidArgument, "moe_combine: bad shape");
+    if (T == 0) return;
+    if (dt == DType::BFloat16)
+        hipLaunchKernelGGL(moe_combine_k<bf16>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
+                           static_cast<const bf16*>(ye), idx, dst_row, gsel, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<const bf16*>(R), ldr, static_cast<bf16*>(out), ldo);
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL(moe_combine_k<float>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
+                           static_cast<const float*>(ye), idx, dst_row, gsel, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<const float*>(R), ldr, static_cast<float*>(out), ldo);
+    else
+        AIC_THROW(DTypeMismatch, "moe_combine: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("moe_combine");
+}
+
+void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* src_ent, const float* gsel, int64_t rows,
+                     int64_t k, int64_t d, void* dye, float* dgsel, DType dt, hipStream_t s) {
+    AIC_CHECK(rows >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldo >= d, InvalidArgument, "moe_combine_bwd: bad shape");
+    if (rows == 0) return;
+    const dim3 g(static_cast<unsigned>(rows));
+    if (dt == DType::BFloat16)
+        hipLaunchKernelGGL(moe_combine_bwd_k<bf16>, g, dim3(256), 0, s, static_cast<const bf16*>(dout), ldo,
+                           static_cast<const bf16*>(ye), src_ent, gsel, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<bf16*>(dye), dgsel);
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL(moe_combine_bwd_k<float>, g, dim3(256), 0, s, static_cast<const float*>(dout), ldo,
+                           static_cast<const float*>(ye), src_ent, gsel, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<float*>(dye), dgsel);
+    else
+        AIC_THROW(DTypeMismatch, "moe_combine_bwd: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("moe_combine_bwd");
+}
+
+void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_t T, int64_t k, int64_t d, void* dx,
+                 int64_t ldx, bool accumulate, DType dt, hipStream_t s) {
+    AIC_CHECK(T >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldx >= d, InvalidArgument, "moe_scatter: bad shape");
+    if (T == 0) return;
+    if (dt == DType::BFloat16)
+        hipLaunchKernelGGL(moe_scatter_k<bf16>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
+                           static_cast<const bf16*>(dxp), idx, dst_row, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<bf16*>(dx), ldx, accumulate ? 1 : 0);
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL(moe_scatter_k<float>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
+                           static_cast<const float*>(dxp), idx, dst_row, static_cast<int>(k), static_cast<int>(d),
+                           static_cast<float*>(dx), ldx, accumulate ? 1 : 0);
+    else
+        AIC_THROW(DTypeMismatch, "moe_scatter: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("moe_scatter");
+}
+
+void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
+                    int64_t E, int64_t k, float aux_coef, float daux, float* dlogits, hipStream_t s) {
+    check_moe(T, E, k);
+    hipLaunchKernelGGL(moe_router_bwd_k, dim3(grid_for(T, 256)), dim3(256), 0, s, probs, idx, dgsel, counts,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), aux_coef, daux, dlogits);
+    AIC_LAUNCH_CHECK("moe_router_bwd");
+}
+
+}  // namespace aic::hip

@@ -1,0 +1,47 @@
+// Mixture-of-experts feed-forward block of MoETransformerBlock (src/nn/moe.cpp:155-253):
+// router Linear(d, E) -> top-k routing with normalised gates and the load-balancing aux loss,
+// E SwiGLU experts (gate [f,d], up [f,d], down [d,f], no bias) on the tokens routed to them,
+// gate-weighted combine; and the backward of all of it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "../runtime/dtype.hpp"
+#include "../runtime/memory_pool.hpp"
+
+namespace aic::models {
+
+class MoEFFN {
+public:
+    MoEFFN(int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, DType dt);
+
+    // h [T, d] (dt, leading dimension d); router wr [E, d] (dt); experts: E consecutive blocks of
+    // gate [f, d], up [f, d], down [d, f] (dt).  y [T, d] (dt) = R + MoE(h) (R nullable);
+    // *aux (device fp32) = the aux loss.  The inputs stay referenced until backward.
+    void forward(const void* h, int64_t T, const void* wr, const void* experts, const void* R, void* y, float* aux,
+                 hipStream_t s);
+    // dy [T, d] (dt), daux = dL/daux.  dh [T, d] (dt) is overwritten; dwr [E, d] and dexperts (the
+    // experts layout, fp32) are overwritten (zero for an expert that received no token).
+    void backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s);
+
+    // Routing of the last forward: idx [T, k] and counts [E] (device pointers).
+    const int64_t* idx() const { return idx_.as<int64_t>(); }
+    const int64_t* counts() const { return counts_.as<int64_t>(); }
+    const std::vector<int64_t>& counts_host() const { return counts_h_; }
+
+private:
+    int64_t d_, f_, E_, k_;
+    float coef_;
+    DType dt_;
+    int64_t T_ = 0;
+    const void* h_ = nullptr;
+    const void* wr_ = nullptr;
+    const void* ex_ = nullptr;
+    std::vector<int64_t> counts_h_, offsets_h_;
+    DeviceBuffer logits_, idx_, gsel_, probs_, counts_, offsets_, dst_row_, src_ent_, xp_, gu_, a_, ye_;
+};
+
+}  // namespace aic::models

@@ -212,6 +212,56 @@ int aic_hip_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, 
 /* fp32 -> bf16 (round to nearest even) copy of n elements. */
 int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream);
 
+/* ---------------------------------------------------------------- mixture of experts */
+/* Routing on fp32 gate logits [T,E] (E <= 64, top_k <= min(E, 8)): probs = softmax(logits)
+ * [T,E]; idx [T,k] = the k largest logits per token, descending, ties to the lower expert
+ * index; gsel [T,k] = probs of the selected experts divided by their sum + 1e-9 (the
+ * normalised gates of MoELayer::forward); rweights [T,k] (nullable) = softmax over the
+ * selected logits (route()'s routing_weights); counts [E] (int64); mean_probs [E] (nullable);
+ * *aux = sum_e mean_probs[e] * counts[e] * E * coef / (T * k) (0 when coef <= 0 or E == 1).
+ * All outputs in device memory; deterministic (no atomics).
+ * Replaces: MoERouter::route (src/nn/moe.cpp:33-129) and the gate normalisation of
+ * MoELayer::forward (src/nn/moe.cpp:170-204). */
+int aic_hip_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx, float* gsel,
+                      float* probs, float* rweights, int64_t* counts, float* mean_probs, float* aux, aic_stream stream);
+/* Rows needed by the expert-sorted layout: T*k entries plus padding to 64-row expert blocks. */
+int64_t aic_hip_moe_max_rows(int64_t T, int64_t E, int64_t k);
+/* Stable dispatch order: expert e owns rows [offsets[e], offsets[e+1]) (offsets [E+1], int64,
+ * multiples of 64); dst_row [T*k] = row of entry t*k+j; src_ent [max_rows] = entry of a row,
+ * -1 for padding.  Tokens keep their order inside an expert.
+ * Replaces: the host-side mask and per-expert dense dispatch of MoELayer::forward
+ * (src/nn/moe.cpp:177-246). */
+int aic_hip_moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k, int64_t E, int64_t* offsets,
+                        int32_t* dst_row, int32_t* src_ent, aic_stream stream);
+/* xp[r,:] = x[token of src_ent[r],:] (zero rows for padding). */
+int aic_hip_moe_gather(const void* x, int64_t ldx, const int32_t* src_ent, int64_t k, int64_t rows, int64_t d,
+                       void* xp, aic_dtype dt, aic_stream stream);
+/* Un-permute: out[t,:] = residual[t,:] (nullable) + sum over the token's experts, in increasing
+ * expert index, of gsel[t,j] * ye[dst_row[t*k+j],:].
+ * Replaces: the gate-weighted accumulation of MoELayer::forward (src/nn/moe.cpp:214-246). */
+int aic_hip_moe_combine(const void* ye, const int64_t* idx, const int32_t* dst_row, const float* gsel, int64_t T,
+                        int64_t k, int64_t d, const void* residual, int64_t ldr, void* out, int64_t ldo, aic_dtype dt,
+                        aic_stream stream);
+
+/* The whole MoE feed-forward block (router Linear(d, E), top-k routing with normalised gates
+ * and aux loss, E SwiGLU experts on their own tokens, gate-weighted combine) and its backward.
+ * Weights: router [E, d]; experts = E consecutive blocks of gate [f,d], up [f,d], down [d,f];
+ * all in dt.  Forward: y [T,d] = residual + MoE(h) (residual nullable), *aux (device fp32).
+ * The forward keeps h and the weights referenced for the backward.  Backward: dh [T,d] (dt)
+ * overwritten; drouter [E,d] and dexperts (fp32, experts layout) overwritten, zero for an
+ * expert with no token.
+ * Replaces: MoELayer::forward and its autograd graph (src/nn/moe.cpp:155-253). */
+typedef struct aic_moe_ffn aic_moe_ffn;
+int aic_moe_ffn_create(int64_t d_model, int64_t d_hidden, int64_t num_experts, int64_t top_k, float aux_loss_coef,
+                       aic_dtype dt, aic_moe_ffn** out);
+int aic_moe_ffn_destroy(aic_moe_ffn* m);
+int aic_moe_ffn_forward(aic_moe_ffn* m, const void* h, int64_t T, const void* router_w, const void* experts,
+                        const void* residual, void* y, float* aux, aic_stream stream);
+int aic_moe_ffn_backward(aic_moe_ffn* m, const void* dy, float daux, void* dh, float* drouter_w, float* dexperts,
+                         aic_stream stream);
+/* Routing of the last forward, copied to the host: idx [T,k], counts [E] (synchronous). */
+int aic_moe_ffn_routing(aic_moe_ffn* m, int64_t* idx_host, int64_t* counts_host, aic_stream stream);
+
 /* ---------------------------------------------------------------- TransformerLM ---- */
 /* The whole training step behind the reference's C++ API (TransformerLM::forward,
  * cross_entropy, Tensor::backward, DynamicLossScaler, clip_grad_norm_, AdamW::step;

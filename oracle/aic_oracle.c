@@ -835,3 +835,221 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
     free(G.layers);
     return 0;
 }
+
+/* ======================================================================================
+ * Mixture of experts (src/nn/moe.cpp)
+ * ====================================================================================== */
+
+/* Row softmax as the reference composes it (src/ops/ops.cpp:460-471): m = max (no gradient),
+ * ex = exp(x - m), s = sum(ex) accumulated in double, p = ex / s. */
+static void softmax_row(const float* x, float* p, int64_t n) {
+    float m = x[0];
+    for (int64_t i = 1; i < n; ++i) m = x[i] > m ? x[i] : m;
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        p[i] = expf(x[i] - m);
+        s += (double)p[i];
+    }
+    const float sf = (float)s;
+    for (int64_t i = 0; i < n; ++i) p[i] = p[i] / sf;
+}
+
+/* Backward of softmax_row through its div / sum / exp ops (src/autograd/functions.cpp):
+ * dx = p * (dp - sum(dp * p)), the reduction in double.  Adds into dx. */
+static void softmax_row_bwd(const float* p, const float* dp, float* dx, int64_t n) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) s += (double)dp[i] * (double)p[i];
+    const float sf = (float)s;
+    for (int64_t i = 0; i < n; ++i) dx[i] += p[i] * (dp[i] - sf);
+}
+
+/* MoERouter::route (moe.cpp:33-129) and the gate normalisation of MoELayer::forward
+ * (moe.cpp:170-204) on precomputed gate logits [T,E]:
+ *   probs = softmax(logits); idx[t, 0..k) = the k largest logits, descending, ties broken by the
+ *   lower expert index (the reference's std::partial_sort leaves tie order unspecified; this
+ *   explicit rule is the one the kernel implements); rweights = softmax over the selected logits
+ *   with the 1e-9 of moe.cpp:74; counts[e] = tokens routed to e; mean_probs = mean_t probs (double
+ *   sum); aux = sum_e mean_probs[e] * counts[e] * E * coef / (T * k) when coef > 0 and E > 1,
+ *   else 0; gates = probs * mask / (sum(probs * mask) + 1e-9).  Any output may be NULL. */
+void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx,
+                   float* rweights, float* gates, float* probs, int64_t* counts, float* mean_probs, float* aux) {
+    float* p = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    int64_t* cnt = (int64_t*)xcalloc((size_t)E, sizeof(int64_t));
+    int64_t* sel = (int64_t*)xcalloc((size_t)k, sizeof(int64_t));
+    char* used = (char*)xcalloc((size_t)E, 1);
+    for (int64_t t = 0; t < T; ++t) {
+        const float* row = logits + t * E;
+        softmax_row(row, p + t * E, E);
+        memset(used, 0, (size_t)E);
+        for (int64_t j = 0; j < k; ++j) { /* selection: largest remaining logit, lowest index on ties */
+            int64_t best = -1;
+            for (int64_t e = 0; e < E; ++e)
+                if (!used[e] && (best < 0 || row[e] > row[best])) best = e;
+            used[best] = 1;
+            sel[j] = best;
+            cnt[best]++;
+            if (idx) idx[t * k + j] = best;
+        }
+        if (rweights) {
+            const float mx = row[sel[0]];
+            float se = 0.0f;
+            for (int64_t j = 0; j < k; ++j) se += expf(row[sel[j]] - mx);
+            for (int64_t j = 0; j < k; ++j) rweights[t * k + j] = expf(row[sel[j]] - mx) / (se + 1e-9f);
+        }
+        if (gates) {
+            /* masked = probs * mask; denom = sum(masked, -1) + 1e-9 (sum in double) */
+            double s = 0.0;
+            for (int64_t e = 0; e < E; ++e) s += used[e] ? (double)p[t * E + e] : 0.0;
+            const float den = (float)s + 1e-9f;
+            for (int64_t e = 0; e < E; ++e) gates[t * E + e] = (used[e] ? p[t * E + e] : 0.0f) / den;
+        }
+    }
+    double auxd = 0.0;
+    const float scale = ((float)E * aux_coef) / ((float)T * (float)k);
+    for (int64_t e = 0; e < E; ++e) {
+        double s = 0.0;
+        for (int64_t t = 0; t < T; ++t) s += (double)p[t * E + e];
+        const float mp = (float)(s / (double)T);
+        if (mean_probs) mean_probs[e] = mp;
+        if (counts) counts[e] = cnt[e];
+        auxd += (double)(mp * ((float)cnt[e] * scale));
+    }
+    if (aux) *aux = (aux_coef > 0.0f && E > 1) ? (float)auxd : 0.0f;
+    if (probs) memcpy(probs, p, sizeof(float) * (size_t)(T * E));
+    free(used);
+    free(sel);
+    free(cnt);
+    free(p);
+}
+
+/* Tokens routed to expert e, in token order. */
+static int64_t moe_rows(const int64_t* idx, int64_t T, int64_t k, int64_t e, int64_t* rows) {
+    int64_t n = 0;
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t j = 0; j < k; ++j)
+            if (idx[t * k + j] == e) rows[n++] = t;
+    return n;
+}
+
+/* MoELayer::forward (moe.cpp:155-253) on the normalised input h [T,d]: router weights wr [E,d],
+ * experts e: gate wg[e] [f,d], up wu[e] [f,d], down wd[e] [d,f] (SwiGLU, include/nn/swiglu.hpp).
+ * y[t] = sum over the selected experts in increasing e of gates[t,e] * SwiGLU_e(h[t]); the
+ * reference evaluates every active expert on all tokens and multiplies by a zero gate for the
+ * unrouted ones, which adds exact zeros, so the sparse sum is the same.  Outputs idx [T,k],
+ * gates [T,E] and aux may be NULL. */
+void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx_out,
+                     float* gates_out) {
+    float* logits = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    orc_linear_fwd(h, wr, logits, 1, T, d, E);
+    int64_t* idx = (int64_t*)xcalloc((size_t)(T * k), sizeof(int64_t));
+    float* gates = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    orc_moe_route(logits, T, E, k, aux_coef, idx, NULL, gates, NULL, NULL, NULL, aux);
+    memset(y, 0, sizeof(float) * (size_t)(T * d));
+    int64_t* rows = (int64_t*)xcalloc((size_t)T, sizeof(int64_t));
+    float* xe = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    float* g = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* u = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* a = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* ye = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    for (int64_t e = 0; e < E; ++e) {
+        const int64_t n = moe_rows(idx, T, k, e, rows);
+        if (n == 0) continue;
+        for (int64_t r = 0; r < n; ++r) memcpy(xe + r * d, h + rows[r] * d, sizeof(float) * (size_t)d);
+        orc_linear_fwd(xe, wg + e * f * d, g, 1, n, d, f);
+        orc_linear_fwd(xe, wu + e * f * d, u, 1, n, d, f);
+        orc_swiglu_fwd(g, u, a, n * f);
+        orc_linear_fwd(a, wd + e * d * f, ye, 1, n, f, d);
+        for (int64_t r = 0; r < n; ++r) {
+            const float gt = gates[rows[r] * E + e];
+            for (int64_t c = 0; c < d; ++c) y[rows[r] * d + c] += ye[r * d + c] * gt;
+        }
+    }
+    if (idx_out) memcpy(idx_out, idx, sizeof(int64_t) * (size_t)(T * k));
+    if (gates_out) memcpy(gates_out, gates, sizeof(float) * (size_t)(T * E));
+    free(ye); free(a); free(u); free(g); free(xe); free(rows); free(gates); free(idx); free(logits);
+}
+
+/* Backward of orc_moe_ffn_fwd for dL/dy = dy and dL/daux = daux, through the reference's graph:
+ * mul (expert output x gate column, the broadcast reduction in double), the expert SwiGLUs, the
+ * gate normalisation (div / sum / add 1e-9), the mask, both router softmaxes (the one of route()
+ * feeding mean_probs and the aux loss, the one of forward() feeding the gates) and both gate
+ * Linear applications.  Gradients are added into dh [T,d], dwr [E,d], dwg/dwu [E,f,d], dwd [E,d,f]. */
+void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
+                     float* dwr, float* dwg, float* dwu, float* dwd) {
+    float* logits = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    orc_linear_fwd(h, wr, logits, 1, T, d, E);
+    int64_t* idx = (int64_t*)xcalloc((size_t)(T * k), sizeof(int64_t));
+    float* gates = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    float* probs = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    int64_t* counts = (int64_t*)xcalloc((size_t)E, sizeof(int64_t));
+    orc_moe_route(logits, T, E, k, aux_coef, idx, NULL, gates, probs, counts, NULL, NULL);
+    float* dgates = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    int64_t* rows = (int64_t*)xcalloc((size_t)T, sizeof(int64_t));
+    float* xe = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    float* g = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* u = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* a = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* ye = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    float* dye = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    float* da = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* dg = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* du = (float*)xcalloc((size_t)(T * f), sizeof(float));
+    float* dxe = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    float* dxe2 = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    for (int64_t e = 0; e < E; ++e) {
+        const int64_t n = moe_rows(idx, T, k, e, rows);
+        if (n == 0) continue; /* inactive experts are skipped: no gradient at all */
+        for (int64_t r = 0; r < n; ++r) memcpy(xe + r * d, h + rows[r] * d, sizeof(float) * (size_t)d);
+        orc_linear_fwd(xe, wg + e * f * d, g, 1, n, d, f);
+        orc_linear_fwd(xe, wu + e * f * d, u, 1, n, d, f);
+        orc_swiglu_fwd(g, u, a, n * f);
+        orc_linear_fwd(a, wd + e * d * f, ye, 1, n, f, d);
+        for (int64_t r = 0; r < n; ++r) {
+            const int64_t t = rows[r];
+            const float gt = gates[t * E + e];
+            double s = 0.0;
+            for (int64_t c = 0; c < d; ++c) {
+                dye[r * d + c] = dy[t * d + c] * gt;
+                s += (double)(dy[t * d + c] * ye[r * d + c]);
+            }
+            dgates[t * E + e] = (float)s;
+        }
+        orc_linear_bwd(a, wd + e * d * f, dye, da, dwd + e * d * f, 1, n, f, d);
+        orc_swiglu_bwd(g, u, da, dg, du, n * f);
+        orc_linear_bwd(xe, wg + e * f * d, dg, dxe, dwg + e * f * d, 1, n, d, f);
+        orc_linear_bwd(xe, wu + e * f * d, du, dxe2, dwu + e * f * d, 1, n, d, f);
+        for (int64_t r = 0; r < n; ++r)
+            for (int64_t c = 0; c < d; ++c) dh[rows[r] * d + c] += dxe[r * d + c] + dxe2[r * d + c];
+    }
+    /* router: gates = masked / (sum(masked) + 1e-9), masked = probs * mask */
+    float* dlogits = (float*)xcalloc((size_t)(T * E), sizeof(float));
+    float* dp = (float*)xcalloc((size_t)E, sizeof(float));
+    const float fscale = ((float)E * aux_coef) / ((float)T * (float)k);
+    const int aux_on = aux_coef > 0.0f && E > 1;
+    for (int64_t t = 0; t < T; ++t) {
+        double den_d = 0.0;
+        char used[256] = {0};
+        for (int64_t j = 0; j < k; ++j) used[idx[t * k + j]] = 1;
+        for (int64_t e = 0; e < E; ++e) den_d += used[e] ? (double)probs[t * E + e] : 0.0;
+        const float den = (float)den_d + 1e-9f;
+        double sb = 0.0; /* grad of the denominator: sum_e -dg * masked / den^2 */
+        for (int64_t e = 0; e < E; ++e) {
+            const float masked = used[e] ? probs[t * E + e] : 0.0f;
+            sb += (double)(-dgates[t * E + e] * masked / (den * den));
+        }
+        for (int64_t e = 0; e < E; ++e) dp[e] = used[e] ? (dgates[t * E + e] / den + (float)sb) : 0.0f;
+        softmax_row_bwd(probs + t * E, dp, dlogits + t * E, E);
+        if (aux_on) { /* route()'s softmax: d mean_probs[e] = daux * f_e, mean over T */
+            for (int64_t e = 0; e < E; ++e) dp[e] = (daux * ((float)counts[e] * fscale)) / (float)T;
+            softmax_row_bwd(probs + t * E, dp, dlogits + t * E, E);
+        }
+    }
+    float* dhr = (float*)xcalloc((size_t)(T * d), sizeof(float));
+    orc_linear_bwd(h, wr, dlogits, dhr, dwr, 1, T, d, E);
+    for (int64_t i = 0; i < T * d; ++i) dh[i] += dhr[i];
+    free(dhr); free(dp); free(dlogits);
+    free(dxe2); free(dxe); free(du); free(dg); free(da); free(dye); free(ye); free(a); free(u); free(g); free(xe);
+    free(rows); free(dgates); free(counts); free(probs); free(gates); free(idx); free(logits);
+}

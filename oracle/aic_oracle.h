@@ -163,6 +163,20 @@ int orc_lm_step(const orc_lm_config* cfg, float* params, float* grads, float* m,
                 const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* opts,
                 orc_scaler* scaler, orc_step_result* res);
 
+/* ---- Mixture of experts (src/nn/moe.cpp) ---- */
+/* Router on gate logits [T,E] (moe.cpp:33-129) plus the gate normalisation of MoELayer::forward
+ * (moe.cpp:170-204); top-k ties go to the lower expert index.  Any output may be NULL. */
+void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx,
+                   float* rweights, float* gates, float* probs, int64_t* counts, float* mean_probs, float* aux);
+/* MoELayer::forward on h [T,d]: router wr [E,d]; experts wg/wu [E,f,d], wd [E,d,f]. */
+void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx,
+                     float* gates);
+/* Its backward for dL/dy and dL/daux; gradients are added into dh, dwr, dwg, dwu, dwd (E <= 256). */
+void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
+                     float* dwr, float* dwg, float* dwu, float* dwd);
+
 #ifdef __cplusplus
 }
 #endif

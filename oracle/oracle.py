@@ -312,3 +312,53 @@ def lm_step(cfg, params, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps
     if rc != 0:
         raise RuntimeError(f"orc_lm_step failed with {rc}")
     return res, grads, m, v, int(stepc.value)
+
+
+# ----------------------------------------------------------------------------- mixture of experts
+def moe_route(logits, k, aux_coef):
+    """orc_moe_route: returns idx [T,k] int64, rweights [T,k], gates [T,E], probs [T,E],
+    counts [E] int64, mean_probs [E], aux (float)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    assert E <= 256
+    idx = np.empty((T, k), np.int64)
+    rw = np.empty((T, k), np.float32)
+    gates = np.empty((T, E), np.float32)
+    probs = np.empty((T, E), np.float32)
+    counts = np.empty(E, np.int64)
+    mp = np.empty(E, np.float32)
+    aux = C.c_float(0.0)
+    lib().orc_moe_route(_f(logits), C.c_int64(T), C.c_int64(E), C.c_int64(k), C.c_float(aux_coef), _i(idx), _f(rw),
+                        _f(gates), _f(probs), _i(counts), _f(mp), C.byref(aux))
+    return idx, rw, gates, probs, counts, mp, aux.value
+
+
+def moe_ffn_fwd(h, wr, wg, wu, wd, k, aux_coef):
+    """orc_moe_ffn_fwd: h [T,d], wr [E,d], wg/wu [E,f,d], wd [E,d,f] -> y [T,d], aux, idx, gates."""
+    h, wr, wg, wu, wd = (np.ascontiguousarray(t, np.float32) for t in (h, wr, wg, wu, wd))
+    T, d = h.shape
+    E, f, _ = wg.shape
+    assert E <= 256
+    y = np.empty((T, d), np.float32)
+    idx = np.empty((T, k), np.int64)
+    gates = np.empty((T, E), np.float32)
+    aux = C.c_float(0.0)
+    lib().orc_moe_ffn_fwd(_f(h), _f(wr), _f(wg), _f(wu), _f(wd), C.c_int64(T), C.c_int64(d), C.c_int64(f),
+                          C.c_int64(E), C.c_int64(k), C.c_float(aux_coef), _f(y), C.byref(aux), _i(idx), _f(gates))
+    return y, aux.value, idx, gates
+
+
+def moe_ffn_bwd(h, wr, wg, wu, wd, k, aux_coef, dy, daux):
+    """orc_moe_ffn_bwd: returns dh, dwr, dwg, dwu, dwd for dL/dy = dy and dL/daux = daux."""
+    h, wr, wg, wu, wd, dy = (np.ascontiguousarray(t, np.float32) for t in (h, wr, wg, wu, wd, dy))
+    T, d = h.shape
+    E, f, _ = wg.shape
+    dh = np.zeros((T, d), np.float32)
+    dwr = np.zeros_like(wr)
+    dwg = np.zeros_like(wg)
+    dwu = np.zeros_like(wu)
+    dwd = np.zeros_like(wd)
+    lib().orc_moe_ffn_bwd(_f(h), _f(wr), _f(wg), _f(wu), _f(wd), C.c_int64(T), C.c_int64(d), C.c_int64(f),
+                          C.c_int64(E), C.c_int64(k), C.c_float(aux_coef), _f(dy), C.c_float(daux), _f(dh), _f(dwr),
+                          _f(dwg), _f(dwu), _f(dwd))
+    return dh, dwr, dwg, dwu, dwd

@@ -344,3 +344,75 @@ def test_lm_step_scaler_is_exact_power_of_two(orc):
     r1, g1, _, _, _ = orc.lm_step(cfg, params.copy(), ids, tgt, B, S, do_update=False, scaler=sc)
     assert r1.loss_scale_used == 65536.0 and not r1.found_inf
     np.testing.assert_array_equal(g0, g1)
+
+
+# ----------------------------------------------------------------------------- mixture of experts
+def test_moe_route_topk_brute_force_and_invariants(orc):
+    # invariants of tests/unit/test_moe.cpp:25-76 (RouterTopKMath) plus a brute-force top-k
+    rng = np.random.default_rng(11)
+    T, E, k = 200, 8, 2
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    idx, rw, gates, probs, counts, mp, aux = orc.moe_route(logits, k, 0.01)
+    np.testing.assert_array_equal(idx, torch_ref.moe_topk(logits, k))
+    assert counts.sum() == T * k
+    np.testing.assert_array_equal(counts, np.bincount(idx.ravel(), minlength=E))
+    assert np.all(idx[:, 0] != idx[:, 1])
+    assert np.all(rw > 0) and np.all(rw <= 1) and np.allclose(rw.sum(1), 1.0, atol=1e-4)
+    np.testing.assert_allclose(gates.sum(1), 1.0, atol=1e-5)
+    assert np.all(gates[np.arange(T)[:, None], idx] > 0) and np.count_nonzero(gates) == T * k
+
+
+def test_moe_route_tie_rule(orc):
+    # equal logits go to the lower expert index
+    logits = np.array([[1, 1, 1, 0], [0, 2, 2, 2], [3, 0, 3, 3], [0.5, 0.5, 0.5, 0.5]], np.float32)
+    idx, *_ = orc.moe_route(logits, 2, 0.0)
+    np.testing.assert_array_equal(idx, [[0, 1], [1, 2], [0, 2], [0, 1]])
+    idx3, *_ = orc.moe_route(logits, 3, 0.0)
+    np.testing.assert_array_equal(idx3, [[0, 1, 2], [1, 2, 3], [0, 2, 3], [0, 1, 2]])
+
+
+def test_moe_route_values_vs_float64(orc):
+    import torch
+    rng = np.random.default_rng(12)
+    T, E, k, coef = 64, 8, 2, 0.05
+    logits = (2 * rng.standard_normal((T, E))).astype(np.float32)
+    idx, rw, gates, probs, counts, mp, aux = orc.moe_route(logits, k, coef)
+    L = torch.tensor(logits, dtype=torch.float64)
+    p = torch.softmax(L, -1).numpy()
+    np.testing.assert_allclose(probs, p, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(mp, p.mean(0), rtol=1e-6)
+    mask = np.zeros((T, E))
+    np.put_along_axis(mask, idx, 1.0, axis=1)
+    g = p * mask / ((p * mask).sum(1, keepdims=True) + 1e-9)
+    np.testing.assert_allclose(gates, g, rtol=1e-6, atol=1e-7)
+    sel = np.take_along_axis(logits.astype(np.float64), idx, axis=1)
+    w = np.exp(sel - sel[:, :1])
+    np.testing.assert_allclose(rw, w / w.sum(1, keepdims=True), rtol=1e-6)
+    # aux = alpha * E / (T k) * sum_e count_e * mean_probs_e  (moe.cpp:84-101)
+    assert abs(aux - coef * E / (T * k) * (counts * p.mean(0)).sum()) < 1e-7
+    assert aux > 0
+    # aux_coef = 0 gives a zero loss (tests/unit/test_moe.cpp:104-108)
+    assert orc.moe_route(logits, k, 0.0)[6] == 0.0
+
+
+@pytest.mark.parametrize("T,d,f,E,k", [(24, 16, 32, 4, 2), (40, 32, 48, 8, 2), (16, 16, 24, 4, 1)])
+def test_moe_ffn_fwd_bwd_vs_float64(orc, T, d, f, E, k):
+    rng = np.random.default_rng(T + d + E)
+    h = rng.standard_normal((T, d)).astype(np.float32)
+    wr = (0.3 * rng.standard_normal((E, d))).astype(np.float32)
+    wg = (0.2 * rng.standard_normal((E, f, d))).astype(np.float32)
+    wu = (0.2 * rng.standard_normal((E, f, d))).astype(np.float32)
+    wd = (0.2 * rng.standard_normal((E, d, f))).astype(np.float32)
+    dy = rng.standard_normal((T, d)).astype(np.float32)
+    coef, daux = 0.02, 1.7
+    y, aux, idx, gates = orc.moe_ffn_fwd(h, wr, wg, wu, wd, k, coef)
+    y_ref, aux_ref, grads = torch_ref.moe_ffn_torch(h, wr, wg, wu, wd, k, coef, dy=dy, daux=daux)
+    assert np.linalg.norm(y - y_ref) / np.linalg.norm(y_ref) < 1e-5
+    assert abs(aux - aux_ref) <= 1e-6 * abs(aux_ref)
+    got = orc.moe_ffn_bwd(h, wr, wg, wu, wd, k, coef, dy, daux)
+    for name, gv, rv in zip(["dh", "dwr", "dwg", "dwu", "dwd"], got, grads):
+        rv = np.zeros_like(gv) if rv is None else rv
+        # top-1: the gate p / (p + 1e-9) has a derivative ~1e-9 relative, below fp32 resolution,
+        # so the router gradient's gate part is fp32 rounding noise (the aux part dominates)
+        tol = 1e-2 if (k == 1 and name == "dwr") else 1e-4
+        assert np.linalg.norm(gv - rv) / max(np.linalg.norm(rv), 1e-12) < tol, name

@@ -89,3 +89,48 @@ def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, 
     opt.step()
     new_params = np.concatenate([P[name].detach().numpy().reshape(-1) for name, _ in lay])
     return float(loss), float(norm), grads, new_params
+
+
+# ----------------------------------------------------------------------------- mixture of experts
+def moe_topk(logits, k):
+    """Top-k expert indices per row: larger logit first, ties to the lower index (numpy)."""
+    T, E = logits.shape
+    order = np.lexsort((np.broadcast_to(np.arange(E), (T, E)), -logits.astype(np.float64)), axis=1)
+    return order[:, :k].astype(np.int64)
+
+
+def moe_ffn_torch(h, wr, wg, wu, wd, k, aux_coef, dy=None, daux=1.0):
+    """float64 MoE layer built like the reference graph (src/nn/moe.cpp:33-253): every active
+    expert runs on all tokens and is weighted by the normalised, masked gate; aux uses the
+    route() softmax.  Returns y, aux and, when dy is given, the gradients of
+    sum(y * dy) + daux * aux wrt (h, wr, wg, wu, wd)."""
+    import torch
+    import torch.nn.functional as F
+
+    t = [torch.tensor(np.asarray(a, np.float64), requires_grad=True) for a in (h, wr, wg, wu, wd)]
+    th, twr, twg, twu, twd = t
+    T, d = th.shape
+    E = twr.shape[0]
+    logits = th @ twr.T
+    idx = torch.tensor(moe_topk(logits.detach().numpy(), k))
+    probs_r = torch.softmax(th @ twr.T, dim=-1)            # route()'s own gate evaluation
+    counts = torch.bincount(idx.reshape(-1), minlength=E).to(torch.float64)
+    f_e = counts * (E * aux_coef) / (T * k)
+    aux = (probs_r.mean(0) * f_e).sum() if (aux_coef > 0 and E > 1) else torch.zeros((), dtype=torch.float64)
+    probs = torch.softmax(logits, dim=-1)
+    mask = torch.zeros(T, E, dtype=torch.float64)
+    mask.scatter_(1, idx, 1.0)
+    masked = probs * mask
+    gates = masked / (masked.sum(-1, keepdim=True) + 1e-9)
+    y = torch.zeros(T, d, dtype=torch.float64)
+    for e in range(E):
+        if counts[e] == 0:
+            continue
+        a = F.silu(th @ twg[e].T) * (th @ twu[e].T)
+        y = y + (a @ twd[e].T) * gates[:, e:e + 1]
+    out = [y.detach().numpy(), float(aux.detach())]
+    if dy is not None:
+        loss = (y * torch.tensor(np.asarray(dy, np.float64))).sum() + daux * aux
+        loss.backward()
+        out.append([None if x.grad is None else x.grad.numpy() for x in t])
+    return out
