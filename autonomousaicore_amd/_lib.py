@@ -87,6 +87,15 @@ SIGNATURES = {
     "aic_moe_ffn_forward": (i32, [vp, vp, i64, vp, vp, vp, vp, vp, vp]),
     "aic_moe_ffn_backward": (i32, [vp, vp, f32, vp, vp, vp, vp]),
     "aic_moe_ffn_routing": (i32, [vp, vp, vp, vp]),
+    "aic_hip_int4_quantize": (i32, [vp, i64, i64, vp, vp, i32, vp]),
+    "aic_hip_int4_dequantize": (i32, [vp, vp, i32, i64, i64, vp, i32, vp]),
+    "aic_hip_int4_dequant_gemm": (i32, [i32, i64, i64, i64, f32, vp, i64, vp, vp, i32, i64, f32, vp, i64, vp, i64,
+                                        i32, i32, vp]),
+    "aic_hip_lora_merge": (i32, [vp, vp, vp, i64, i64, i64, f32, i32, i32, vp]),
+    "aic_qlora_linear_create": (i32, [i64, i64, i64, f32, i64, i32, i32, vp]),
+    "aic_qlora_linear_destroy": (i32, [vp]),
+    "aic_qlora_linear_forward": (i32, [vp, vp, i64, vp, vp, vp, vp, vp, vp, vp]),
+    "aic_qlora_linear_backward": (i32, [vp, vp, vp, vp, vp, i32, vp]),
     "aic_lm_create": (i32, [C.POINTER(LMConfig), C.POINTER(TrainConfig), C.POINTER(vp)]),
     "aic_lm_destroy": (i32, [vp]),
     "aic_lm_num_params": (i64, [vp]),

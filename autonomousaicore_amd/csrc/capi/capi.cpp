@@ -13,6 +13,7 @@
 #include "../kernels/gemm.hpp"
 #include "../kernels/kernels.hpp"
 #include "../model/moe_ffn.hpp"
+#include "../model/qlora_linear.hpp"
 #include "../model/transformer_lm.hpp"
 #include "../runtime/error.hpp"
 #include "../runtime/memory_pool.hpp"
@@ -58,6 +59,10 @@ const char* dtype_name(DType d) noexcept {
 
 struct aic_moe_ffn {
     aic::models::MoEFFN* ffn;
+};
+
+struct aic_qlora_linear {
+    aic::models::QLoRALinear* lin;
 };
 
 struct aic_lm {
@@ -533,6 +538,88 @@ int aic_moe_ffn_routing(aic_moe_ffn* m, int64_t* idx_host, int64_t* counts_host,
             T += ch[e];
         }
         AIC_HIP_CHECK(hipMemcpy(idx_host, m->ffn->idx(), sizeof(int64_t) * T, hipMemcpyDeviceToHost));
+    });
+}
+
+// ------------------------------------------------------------------ INT4 + LoRA
+int aic_hip_int4_quantize(const float* x, int64_t n, int64_t group, uint8_t* packed, void* scales,
+                          aic_dtype scale_type, aic_stream stream) {
+    return guard([&] { aic::hip::int4_quantize(x, n, group, packed, scales, dt(scale_type), st(stream)); });
+}
+
+int aic_hip_int4_dequantize(const uint8_t* packed, const void* scales, aic_dtype scale_type, int64_t n, int64_t group,
+                            void* out, aic_dtype out_type, aic_stream stream) {
+    return guard([&] { aic::hip::int4_dequant(packed, scales, dt(scale_type), n, group, out, dt(out_type), st(stream)); });
+}
+
+int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx,
+                              const uint8_t* Wq, const void* scales, aic_dtype scale_type, int64_t group, float beta,
+                              void* C, int64_t ldc, const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type,
+                              aic_stream stream) {
+    return guard([&] {
+        aic::models::int4_dequant_gemm(transW, M, N, K, alpha, X, ldx, Wq, scales, dt(scale_type), group, beta, C, ldc,
+                                       R, ldr, dt(ab_type), dt(c_type), st(stream));
+    });
+}
+
+int aic_hip_lora_merge(void* W, const void* A, const void* B, int64_t in_features, int64_t out_features, int64_t rank,
+                       float scaling, int sign, aic_dtype dtype, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(W && A && B && in_features > 0 && out_features > 0 && rank > 0, InvalidArgument, "bad lora_merge args");
+        aic::hip::GemmArgs a;
+        a.M = out_features;
+        a.N = in_features;
+        a.K = rank;
+        a.alpha = sign >= 0 ? scaling : -scaling;
+        a.A = B;
+        a.lda = rank;
+        a.B = A;
+        a.ldb = in_features;
+        a.beta = 1.0f;
+        a.C = W;
+        a.ldc = in_features;
+        a.ab = dt(dtype);
+        a.c = dt(dtype);
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
+int aic_qlora_linear_create(int64_t in_features, int64_t out_features, int64_t rank, float alpha, int64_t group,
+                            aic_dtype scale_type, aic_dtype dtype, aic_qlora_linear** out) {
+    return guard([&] {
+        AIC_CHECK(out, InvalidArgument, "null argument");
+        auto* h = new aic_qlora_linear{nullptr};
+        try {
+            h->lin = new aic::models::QLoRALinear(in_features, out_features, rank, alpha, group, dt(scale_type), dt(dtype));
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int aic_qlora_linear_destroy(aic_qlora_linear* m) {
+    return guard([&] {
+        if (!m) return;
+        delete m->lin;
+        delete m;
+    });
+}
+
+int aic_qlora_linear_forward(aic_qlora_linear* m, const void* x, int64_t T, const uint8_t* Wq, const void* scales,
+                             const void* A, const void* B, const void* R, void* y, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(m, InvalidArgument, "null module");
+        m->lin->forward(x, T, Wq, scales, A, B, R, y, st(stream));
+    });
+}
+
+int aic_qlora_linear_backward(aic_qlora_linear* m, const void* dy, void* dx, float* dA, float* dB, int accumulate,
+                              aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(m, InvalidArgument, "null module");
+        m->lin->backward(dy, dx, dA, dB, accumulate != 0, st(stream));
     });
 }
 

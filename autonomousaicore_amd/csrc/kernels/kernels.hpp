@@ -57,6 +57,13 @@ void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_
 void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
                     int64_t E, int64_t k, float aux_coef, float daux, float* dlogits, hipStream_t s);
 
+// INT4 symmetric quantization (int4.hip).  Scales are f32 or f16; the dequantized output f32 or
+// bf16.  int4_group returns the effective group size (G <= 0 or G > n: n) and rejects an odd one.
+int64_t int4_group(int64_t n, int64_t G);
+void int4_quantize(const float* x, int64_t n, int64_t G, uint8_t* packed, void* scales, DType scale_t, hipStream_t s);
+void int4_dequant(const uint8_t* packed, const void* scales, DType scale_t, int64_t n, int64_t G, void* out, DType out_t,
+                  hipStream_t s);
+
 // Attention (attention.hip)
 void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
               int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);

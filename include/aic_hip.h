@@ -262,6 +262,55 @@ int aic_moe_ffn_backward(aic_moe_ffn* m, const void* dy, float daux, void* dh, f
 /* Routing of the last forward, copied to the host: idx [T,k], counts [E] (synchronous). */
 int aic_moe_ffn_routing(aic_moe_ffn* m, int64_t* idx_host, int64_t* counts_host, aic_stream stream);
 
+/* ---------------------------------------------------------------- INT4 + LoRA ------ */
+/* INT4-symmetric weights: groups of `group` consecutive elements of the flat row-major weight
+ * (group <= 0 or > n: one group; an odd group with more than one group is rejected);
+ * s = max(absmax/7, 1e-8); q = clamp(round_half_away(x/s), -7, 7); packed[(n+1)/2] holds element
+ * 2i in the low nibble and 2i+1 in the high nibble (4-bit two's complement); scales[ceil(n/group)]
+ * are AIC_F32 or AIC_F16 (fp16 rounding of the fp32 s, which q always uses).
+ * Replaces: QuantizedTensor::quantize, INT4_SYMMETRIC (src/nn/quantization.cpp:197-295), which
+ * runs on the host. */
+int aic_hip_int4_quantize(const float* x, int64_t n, int64_t group, uint8_t* packed, void* scales,
+                          aic_dtype scale_type, aic_stream stream);
+/* out[i] = q_i * s_{i/group}, written as out_type (AIC_F32 or AIC_BF16, round to nearest even).
+ * Replaces: QuantizedTensor::dequantize (src/nn/quantization.cpp:359-474) and
+ * launch_dequantize_int4 (src/cuda/cuda_quantize.cuh; src/cuda/cuda_quantize.cu:141-159). */
+int aic_hip_int4_dequantize(const uint8_t* packed, const void* scales, aic_dtype scale_type, int64_t n, int64_t group,
+                            void* out, aic_dtype out_type, aic_stream stream);
+/* C[M,N] = alpha * X[M,K] . op(deq(Wq)) + beta * C + R with Wq an INT4 weight as above:
+ * transW = 1: Wq holds W [N,K] and op(W) = W^T (forward y = x W^T); transW = 0: Wq holds W [K,N]
+ * (input gradient dx = dy W).  The weight is dequantized into library scratch in ab_type
+ * (AIC_BF16 or AIC_F32) and multiplied there; X, C and R as in aic_hip_gemm.
+ * Replaces: QuantizedLinear::forward (src/nn/quantization.cpp:669-679: dequantize, transpose,
+ * matmul) and its MatMulBackward input gradient (src/autograd/functions.cpp:254-273). */
+int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx,
+                              const uint8_t* Wq, const void* scales, aic_dtype scale_type, int64_t group, float beta,
+                              void* C, int64_t ldc, const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type,
+                              aic_stream stream);
+/* W[out,in] += sign * scaling * B[out,rank] . A[rank,in]  (sign >= 0: merge, < 0: unmerge);
+ * W, A, B of `dtype` (AIC_F32 or AIC_BF16).
+ * Replaces: LoRALinear::merge / unmerge (src/nn/lora.cpp:95-108). */
+int aic_hip_lora_merge(void* W, const void* A, const void* B, int64_t in_features, int64_t out_features, int64_t rank,
+                       float scaling, int sign, aic_dtype dtype, aic_stream stream);
+
+/* A QLoRA projection: frozen INT4 base plus LoRA adapter,
+ *   y = x . deq(Wq)^T + ((x . A^T) . B^T) * (alpha / rank)  [+ R],
+ * with A [rank,in], B [out,rank]; rank 0 is the plain QuantizedLinear.  dtype (AIC_F32 or
+ * AIC_BF16) is the type of x, y, R, dx, A and B; adapter gradients are fp32.
+ * Replaces: LoRALinear::forward (src/nn/lora.cpp:75-93) over QuantizedLinear::forward
+ * (src/nn/quantization.cpp:669-679), with the base frozen as LoRALinear does (lora.cpp:54-56). */
+typedef struct aic_qlora_linear aic_qlora_linear;
+int aic_qlora_linear_create(int64_t in_features, int64_t out_features, int64_t rank, float alpha, int64_t group,
+                            aic_dtype scale_type, aic_dtype dtype, aic_qlora_linear** out);
+int aic_qlora_linear_destroy(aic_qlora_linear* m);
+/* x [T,in], y / R [T,out] (R nullable).  x, Wq, scales, A and B stay referenced until backward. */
+int aic_qlora_linear_forward(aic_qlora_linear* m, const void* x, int64_t T, const uint8_t* Wq, const void* scales,
+                             const void* A, const void* B, const void* R, void* y, aic_stream stream);
+/* dy [T,out] -> dx [T,in] (overwritten; NULL skips it), dA [rank,in] and dB [out,rank] (fp32,
+ * overwritten, or added to when accumulate != 0, as AccumulateGrad adds). */
+int aic_qlora_linear_backward(aic_qlora_linear* m, const void* dy, void* dx, float* dA, float* dB, int accumulate,
+                              aic_stream stream);
+
 /* ---------------------------------------------------------------- TransformerLM ---- */
 /* The whole training step behind the reference's C++ API (TransformerLM::forward,
  * cross_entropy, Tensor::backward, DynamicLossScaler, clip_grad_norm_, AdamW::step;

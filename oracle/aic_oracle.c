@@ -1053,3 +1053,141 @@ void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const flo
     free(dxe2); free(dxe); free(du); free(dg); free(da); free(dye); free(ye); free(a); free(u); free(g); free(xe);
     free(rows); free(dgates); free(counts); free(probs); free(gates); free(idx); free(logits);
 }
+
+/* ======================================================================================
+ * INT4 symmetric quantization (src/nn/quantization.cpp:197-295 quantize, :359-474 dequantize,
+ * include/nn/quantization.hpp:41-56 nibble packing)
+ * ====================================================================================== */
+
+/* IEEE binary32 -> binary16, round to nearest even, subnormals kept (the fp16 scale storage
+ * of the QLoRA configuration; the reference stores fp32 scales). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to infinity */
+    const int e = (int)(ax >> 23) - 127;
+    if (e >= -14) {
+        const uint32_t m = ax & 0x7fffffu, rem = m & 0x1fffu;
+        uint32_t h = ((uint32_t)(e + 15) << 10) | (m >> 13);
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* a carry bumps the exponent */
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return (uint16_t)sign;
+    const uint32_t m = (ax & 0x7fffffu) | 0x800000u; /* |f| = m * 2^(e-23); unit 2^-24 */
+    const int sh = -(e + 1);                         /* 14..24 */
+    const uint32_t rem = m & ((1u << sh) - 1u), halfw = 1u << (sh - 1);
+    uint32_t h = m >> sh;
+    if (rem > halfw || (rem == halfw && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    float v;
+    if (e == 0) v = ldexpf((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexpf((float)(m | 0x400u), (int)e - 25);
+    return (h & 0x8000u) ? -v : v;
+}
+
+static float int4_scale(const void* scales, int scale_f16, int64_t g) {
+    return scale_f16 ? orc_f16_to_f32(((const uint16_t*)scales)[g]) : ((const float*)scales)[g];
+}
+
+int orc_int4_quantize(const float* x, int64_t n, int64_t G, int scale_f16, uint8_t* packed, void* scales) {
+    if (n < 0) return 1;
+    if (n == 0) return 0;
+    if (G <= 0 || G > n) G = n; /* group_size <= 0: one group over the tensor (quantization.cpp:202-205) */
+    const int64_t ng = (n + G - 1) / G;
+    if (ng > 1 && (G & 1)) return 2; /* odd groups would share a byte between two groups */
+    memset(packed, 0, (size_t)((n + 1) / 2));
+    for (int64_t g = 0; g < ng; ++g) {
+        const int64_t start = g * G, end = start + G < n ? start + G : n;
+        float amax = fabsf(x[start]);
+        for (int64_t i = start + 1; i < end; ++i) {
+            const float av = fabsf(x[i]);
+            if (av > amax) amax = av;
+        }
+        float s = amax / 7.0f;
+        if (s < 1e-8f) s = 1e-8f;
+        if (scale_f16) ((uint16_t*)scales)[g] = orc_f32_to_f16(s);
+        else ((float*)scales)[g] = s;
+        for (int64_t i = start; i < end; i += 2) {
+            float q0 = roundf(x[i] / s); /* std::round: halves away from zero */
+            q0 = q0 < -7.0f ? -7.0f : (q0 > 7.0f ? 7.0f : q0);
+            int q1i = 0;
+            if (i + 1 < end) {
+                float q1 = roundf(x[i + 1] / s);
+                q1 = q1 < -7.0f ? -7.0f : (q1 > 7.0f ? 7.0f : q1);
+                q1i = (int)q1;
+            }
+            packed[i / 2] = (uint8_t)(((unsigned)(q1i & 0x0f) << 4) | ((unsigned)((int)q0) & 0x0fu));
+        }
+    }
+    return 0;
+}
+
+int orc_int4_dequantize(const uint8_t* packed, const void* scales, int scale_f16, int64_t n, int64_t G, float* out) {
+    if (n < 0) return 1;
+    if (n == 0) return 0;
+    if (G <= 0 || G > n) G = n;
+    if ((n + G - 1) / G > 1 && (G & 1)) return 2;
+    for (int64_t i = 0; i < n; ++i) {
+        const unsigned b = packed[i / 2], u = (i & 1) ? (b >> 4) : (b & 0x0fu);
+        const int q = u >= 8 ? (int)u - 16 : (int)u;
+        out[i] = (float)q * int4_scale(scales, scale_f16, i / G);
+    }
+    return 0;
+}
+
+/* ======================================================================================
+ * LoRA (src/nn/lora.cpp:31-108)
+ * ====================================================================================== */
+
+void orc_lora_fwd(const float* x, const float* W, const float* A, const float* Bm, float scaling, int64_t Bt,
+                  int64_t S, int64_t in, int64_t out, int64_t r, float* y, float* xa_out) {
+    const int64_t T = Bt * S;
+    float* xa = (float*)xcalloc((size_t)(T * r), sizeof(float));
+    float* lo = (float*)xcalloc((size_t)(T * out), sizeof(float));
+    orc_linear_fwd(x, W, y, Bt, S, in, out);
+    orc_linear_fwd(x, A, xa, Bt, S, in, r);
+    orc_linear_fwd(xa, Bm, lo, Bt, S, r, out);
+    for (int64_t i = 0; i < T * out; ++i) y[i] = y[i] + lo[i] * scaling;
+    if (xa_out) memcpy(xa_out, xa, sizeof(float) * (size_t)(T * r));
+    free(lo);
+    free(xa);
+}
+
+void orc_lora_bwd(const float* x, const float* W, const float* A, const float* Bm, float scaling, const float* dy,
+                  int64_t Bt, int64_t S, int64_t in, int64_t out, int64_t r, float* dx, float* dA, float* dB) {
+    const int64_t T = Bt * S;
+    float* xa = (float*)xcalloc((size_t)(T * r), sizeof(float));
+    float* dl = (float*)xcalloc((size_t)(T * out), sizeof(float));
+    float* dxa = (float*)xcalloc((size_t)(T * r), sizeof(float));
+    float* dxl = (float*)xcalloc((size_t)(T * in), sizeof(float));
+    orc_linear_fwd(x, A, xa, Bt, S, in, r);
+    for (int64_t i = 0; i < T * out; ++i) dl[i] = dy[i] * scaling; /* MulBackward of lora_out * scaling */
+    orc_linear_bwd(xa, Bm, dl, dxa, dB, Bt, S, r, out);
+    orc_linear_bwd(x, A, dxa, dx ? dxl : NULL, dA, Bt, S, in, r);
+    if (dx) {
+        orc_linear_bwd(x, W, dy, dx, NULL, Bt, S, in, out); /* frozen base: no dW */
+        for (int64_t i = 0; i < T * in; ++i) dx[i] = dx[i] + dxl[i];
+    }
+    free(dxl);
+    free(dxa);
+    free(dl);
+    free(xa);
+}
+
+void orc_lora_merge(float* W, const float* A, const float* Bm, float scaling, int64_t in, int64_t out, int64_t r,
+                    int sign) {
+    float* dw = (float*)xcalloc((size_t)(out * in), sizeof(float));
+    orc_gemm(Bm, A, dw, out, in, r);
+    for (int64_t i = 0; i < out * in; ++i) {
+        const float d = dw[i] * scaling;
+        W[i] = sign >= 0 ? W[i] + d : W[i] - d;
+    }
+    free(dw);
+}

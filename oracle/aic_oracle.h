@@ -27,6 +27,13 @@
  *                         + torch.optim.AdamW float64
  *   orc_clip_grad_norm    sqrt(91) -> 5 (tests/unit/test_optim.cpp:191-207)
  *   orc_scaler_*          sequences of tests/unit/test_amp.cpp:56-142
+ *   orc_moe_*             brute-force top-k, routing invariants (tests/unit/test_moe.cpp),
+ *                         float64 autograd restatement of src/nn/moe.cpp
+ *   orc_int4_*            exhaustive 16 nibble values and known bytes, half-away rounding,
+ *                         packing count / compression / cosine (tests/unit/test_quantization.cpp:47-67),
+ *                         |deq - x| <= s/2, byte idempotence; fp16 scales vs numpy float16
+ *   orc_lora_*            B = 0 identity (tests/unit/test_lora.cpp:58-73), merge == unmerged
+ *                         forward (:107-143), torch float64 autograd
  *   orc_lm_step           whole step vs an independent torch float64 model built from
  *                         library routines (F.embedding, F.linear, F.rms_norm, SDPA,
  *                         F.silu, F.cross_entropy, clip_grad_norm_, torch.optim.AdamW)
@@ -176,6 +183,34 @@ void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const flo
 void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
                      int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
                      float* dwr, float* dwg, float* dwu, float* dwd);
+
+/* ---- INT4 symmetric quantization (src/nn/quantization.cpp) ---- */
+/* IEEE binary32 <-> binary16 (round to nearest even; subnormals kept). */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+/* QuantizedTensor::quantize, INT4_SYMMETRIC (quantization.cpp:197-295): groups of G consecutive
+ * elements of the flat row-major x[n] (G <= 0 or G > n: one group); s = max(absmax/7, 1e-8);
+ * q = clamp(round_half_away(x/s), -7, 7); packed[(n+1)/2] holds element 2i in the low nibble
+ * (include/nn/quantization.hpp:41-44).  scales[ceil(n/G)]: fp32, or (scale_f16) the fp16 bits
+ * of s; q always uses the fp32 s, so the packed bytes equal the reference's either way.
+ * Returns 0, 1 for n < 0, 2 for an odd G with more than one group. */
+int orc_int4_quantize(const float* x, int64_t n, int64_t G, int scale_f16, uint8_t* packed, void* scales);
+/* QuantizedTensor::dequantize (quantization.cpp:433-443): out[i] = q_i * s_{i/G}. */
+int orc_int4_dequantize(const uint8_t* packed, const void* scales, int scale_f16, int64_t n, int64_t G, float* out);
+
+/* ---- LoRA (src/nn/lora.cpp) ---- */
+/* LoRALinear::forward (lora.cpp:75-93) on base weight W [out,in] (a Linear, or the dequantized
+ * INT4 weight of QuantizedLinear::forward, quantization.cpp:669-679), A [r,in], Bm [out,r]:
+ * y = x W^T + ((x A^T) Bm^T) * scaling, each product per batch of S rows.  xa [T,r] may be NULL. */
+void orc_lora_fwd(const float* x, const float* W, const float* A, const float* Bm, float scaling, int64_t Bt,
+                  int64_t S, int64_t in, int64_t out, int64_t r, float* y, float* xa);
+/* Its backward with W frozen (lora.cpp:54-56): dl = dy*scaling; dxa = dl Bm; dBm += dl^T xa;
+ * dA += dxa^T x; dx = dy W + dxa A (overwritten).  Any output may be NULL. */
+void orc_lora_bwd(const float* x, const float* W, const float* A, const float* Bm, float scaling, const float* dy,
+                  int64_t Bt, int64_t S, int64_t in, int64_t out, int64_t r, float* dx, float* dA, float* dB);
+/* LoRALinear::merge / unmerge (lora.cpp:95-108): W = W +- (Bm A) * scaling (sign >= 0: merge). */
+void orc_lora_merge(float* W, const float* A, const float* Bm, float scaling, int64_t in, int64_t out, int64_t r,
+                    int sign);
 
 #ifdef __cplusplus
 }

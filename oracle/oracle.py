@@ -362,3 +362,77 @@ def moe_ffn_bwd(h, wr, wg, wu, wd, k, aux_coef, dy, daux):
                           C.c_int64(E), C.c_int64(k), C.c_float(aux_coef), _f(dy), C.c_float(daux), _f(dh), _f(dwr),
                           _f(dwg), _f(dwu), _f(dwd))
     return dh, dwr, dwg, dwu, dwd
+
+
+# ----------------------------------------------------------------------------- INT4 + LoRA
+def f32_to_f16_bits(x):
+    """orc_f32_to_f16 over an array: uint16 bits of fp16(x), round to nearest even."""
+    L = lib()
+    L.orc_f32_to_f16.restype = C.c_uint16
+    L.orc_f32_to_f16.argtypes = [C.c_float]
+    x = np.asarray(x, np.float32).ravel()
+    return np.array([L.orc_f32_to_f16(float(v)) for v in x], np.uint16)
+
+
+def int4_quantize(x, G, scale_f16=False):
+    """orc_int4_quantize of the flat x: returns packed uint8 [(n+1)/2] and scales
+    (float32, or float16 when scale_f16) [ceil(n/G)]."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    n = x.size
+    g = n if (G <= 0 or G > n) else G
+    ng = (n + g - 1) // g if n else 0
+    packed = np.zeros((n + 1) // 2, np.uint8)
+    scales = np.zeros(ng, np.float16 if scale_f16 else np.float32)
+    rc = lib().orc_int4_quantize(_f(x), C.c_int64(n), C.c_int64(G), C.c_int(1 if scale_f16 else 0),
+                                 packed.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p))
+    if rc != 0:
+        raise ValueError(f"orc_int4_quantize failed with {rc}")
+    return packed, scales
+
+
+def int4_dequantize(packed, scales, n, G):
+    """orc_int4_dequantize: float32 [n]; scales may be float32 or float16."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales)
+    out = np.empty(n, np.float32)
+    rc = lib().orc_int4_dequantize(packed.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p),
+                                   C.c_int(1 if scales.dtype == np.float16 else 0), C.c_int64(n), C.c_int64(G),
+                                   _f(out))
+    if rc != 0:
+        raise ValueError(f"orc_int4_dequantize failed with {rc}")
+    return out
+
+
+def lora_fwd(x, W, A, Bm, scaling, Bt, S):
+    """orc_lora_fwd: x [Bt*S,in], W [out,in], A [r,in], Bm [out,r] -> y [Bt*S,out], xa [Bt*S,r]."""
+    x, W, A, Bm = (np.ascontiguousarray(t, np.float32) for t in (x, W, A, Bm))
+    out, inn = W.shape
+    r = A.shape[0]
+    y = np.empty((Bt * S, out), np.float32)
+    xa = np.empty((Bt * S, r), np.float32)
+    lib().orc_lora_fwd(_f(x), _f(W), _f(A), _f(Bm), C.c_float(scaling), C.c_int64(Bt), C.c_int64(S), C.c_int64(inn),
+                       C.c_int64(out), C.c_int64(r), _f(y), _f(xa))
+    return y, xa
+
+
+def lora_bwd(x, W, A, Bm, scaling, dy, Bt, S):
+    """orc_lora_bwd: returns dx, dA, dB."""
+    x, W, A, Bm, dy = (np.ascontiguousarray(t, np.float32) for t in (x, W, A, Bm, dy))
+    out, inn = W.shape
+    r = A.shape[0]
+    dx = np.empty((Bt * S, inn), np.float32)
+    dA = np.zeros((r, inn), np.float32)
+    dB = np.zeros((out, r), np.float32)
+    lib().orc_lora_bwd(_f(x), _f(W), _f(A), _f(Bm), C.c_float(scaling), _f(dy), C.c_int64(Bt), C.c_int64(S),
+                       C.c_int64(inn), C.c_int64(out), C.c_int64(r), _f(dx), _f(dA), _f(dB))
+    return dx, dA, dB
+
+
+def lora_merge(W, A, Bm, scaling, sign=1):
+    """orc_lora_merge: returns W +- (Bm A) * scaling (a new array)."""
+    W = np.array(W, np.float32, copy=True, order="C")
+    A, Bm = (np.ascontiguousarray(t, np.float32) for t in (A, Bm))
+    out, inn = W.shape
+    lib().orc_lora_merge(_f(W), _f(A), _f(Bm), C.c_float(scaling), C.c_int64(inn), C.c_int64(out),
+                         C.c_int64(A.shape[0]), C.c_int(sign))
+    return W

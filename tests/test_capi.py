@@ -46,6 +46,11 @@ def test_argument_errors_are_codes():
     assert rc == 1 and b"even" in lib.aic_hip_last_error()
     rc = lib.aic_hip_embed_bwd(None, 20000, None, 10, 4, None, 0, _lib.AIC_F32, None)
     assert rc == 1 and b"tokens per call" in lib.aic_hip_last_error()
+    # an odd INT4 group size over several groups is refused before anything is launched
+    rc = lib.aic_hip_int4_quantize(None, 100, 7, None, None, _lib.AIC_F16, None)
+    assert rc == 1 and b"even" in lib.aic_hip_last_error()
+    rc = lib.aic_hip_int4_dequantize(None, None, _lib.AIC_BF16, 64, 32, None, _lib.AIC_F32, None)
+    assert rc != 0 and b"scales" in lib.aic_hip_last_error()
     with pytest.raises(aic.AicError):
         _lib.call("aic_synth_uniform_ids", C.c_uint64(1), 4, 0, None)
 

@@ -416,3 +416,153 @@ def test_moe_ffn_fwd_bwd_vs_float64(orc, T, d, f, E, k):
         # so the router gradient's gate part is fp32 rounding noise (the aux part dominates)
         tol = 1e-2 if (k == 1 and name == "dwr") else 1e-4
         assert np.linalg.norm(gv - rv) / max(np.linalg.norm(rv), 1e-12) < tol, name
+
+
+# --------------------------------------------------------------------------- INT4 quantization
+_NIBBLE = [0, 1, 2, 3, 4, 5, 6, 7, -8, -7, -6, -5, -4, -3, -2, -1]   # two's complement of 4 bits
+
+
+def test_int4_every_byte_decodes_to_its_two_nibbles(orc):
+    # all 256 bytes, scale 1: element 2i is the low nibble, 2i+1 the high nibble
+    # (include/nn/quantization.hpp:41-56), both signed
+    packed = np.arange(256, dtype=np.uint8)
+    out = orc.int4_dequantize(packed, np.ones(1, np.float32), 512, 512)
+    np.testing.assert_array_equal(out[0::2], np.array([_NIBBLE[b & 15] for b in range(256)], np.float32))
+    np.testing.assert_array_equal(out[1::2], np.array([_NIBBLE[b >> 4] for b in range(256)], np.float32))
+
+
+def test_int4_known_bytes_and_exact_grid(orc):
+    # a group whose absmax is 3.5 has s = 0.5 exactly, so x = q*s round-trips for q = -7..7
+    q = np.arange(-7, 8, dtype=np.float32)
+    x = np.concatenate([q * 0.5, [0.0]]).astype(np.float32)
+    packed, s = orc.int4_quantize(x, 16)
+    assert s.tolist() == [0.5]
+    # pairs (-7,-6) (-5,-4) (-3,-2) (-1,0) (1,2) (3,4) (5,6) (7,0)
+    assert packed.tolist() == [0xA9, 0xCB, 0xED, 0x0F, 0x21, 0x43, 0x65, 0x07]
+    np.testing.assert_array_equal(orc.int4_dequantize(packed, s, 16, 16), x)
+
+
+def test_int4_rounds_halves_away_from_zero(orc):
+    # std::round, not round-half-even: 2.5 -> 3, -2.5 -> -3, 0.5 -> 1, 3.5 -> 4
+    x = np.array([7.0, 2.5, -2.5, 0.5, -0.5, 3.5, -3.5, 1.4999], np.float32)
+    packed, s = orc.int4_quantize(x, 8)
+    assert s.tolist() == [1.0]
+    np.testing.assert_array_equal(orc.int4_dequantize(packed, s, 8, 8), [7, 3, -3, 1, -1, 4, -4, 1])
+
+
+def test_int4_scale_floor_and_group_layout(orc):
+    x = np.zeros(10, np.float32)
+    x[4:8] = [1.0, -2.0, 0.5, 0.25]
+    packed, s = orc.int4_quantize(x, 4)           # groups [0:4] [4:8] [8:10]; the last one partial
+    assert s.dtype == np.float32 and s.size == 3 and packed.size == 5
+    assert s[0] == np.float32(1e-8) and s[2] == np.float32(1e-8)
+    assert s[1] == np.float32(2.0) / np.float32(7.0)
+    assert packed[0] == 0 and packed[1] == 0 and packed[4] == 0
+    # G <= 0 or G > n: one group over the whole tensor (quantization.cpp:202-205)
+    for G in (0, -1, 99):
+        p1, s1 = orc.int4_quantize(x, G)
+        assert s1.size == 1 and s1[0] == np.float32(2.0) / np.float32(7.0)
+    # an odd group size with more than one group would split a byte between two groups
+    with pytest.raises(ValueError):
+        orc.int4_quantize(x, 3)
+
+
+def test_int4_reference_packing_compression_and_cosine(orc):
+    # tests/unit/test_quantization.cpp:47-67: 64x128 uniform(-2.5, 2.5), G = 32
+    rng = np.random.default_rng(47)
+    x = rng.uniform(-2.5, 2.5, (64, 128)).astype(np.float32)
+    packed, s = orc.int4_quantize(x, 32)
+    assert packed.size == 4096 and s.size == 256
+    assert x.size * 4 / (packed.nbytes + s.nbytes) > 3.5
+    deq = orc.int4_dequantize(packed, s, x.size, 32).astype(np.float64)
+    xd = x.ravel().astype(np.float64)
+    assert deq @ xd / (np.linalg.norm(deq) * np.linalg.norm(xd)) > 0.99
+
+
+@pytest.mark.parametrize("n,G", [(4096, 128), (1000, 32), (777, 64), (513, 512)])
+def test_int4_error_bound_and_idempotence(orc, n, G):
+    rng = np.random.default_rng(n + G)
+    x = (rng.standard_normal(n) * rng.uniform(0.01, 3.0)).astype(np.float32)
+    packed, s = orc.int4_quantize(x, G)
+    deq = orc.int4_dequantize(packed, s, n, G)
+    sg = np.repeat(s, G)[:n].astype(np.float64)
+    assert np.all(np.abs(deq - x) <= 0.5 * sg * (1 + 1e-6))          # round to nearest level
+    # every group's absmax lands on +-7
+    amax = np.array([np.abs(deq[i:i + G]).max() for i in range(0, n, G)])
+    np.testing.assert_allclose(amax, 7 * s, rtol=0)
+    p2, s2 = orc.int4_quantize(deq, G)                                # re-quantizing is a fixed point
+    np.testing.assert_array_equal(p2, packed)
+    np.testing.assert_allclose(s2, s, rtol=2e-7)
+
+
+def test_f16_conversion_matches_numpy(orc):
+    rng = np.random.default_rng(3)
+    special = np.array([0.0, -0.0, 1e-8, 5.96e-8, 2.0 ** -25, 2.0 ** -25 * 1.0000001, 2.0 ** -24 * 1.5,
+                        2.0 ** -24 * 2.5, 6.1e-5, 2.0 ** -14, 65504.0, 65519.0, 65520.0, 1e6, np.inf, -np.inf,
+                        1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 1.0 + 2.0 ** -11 + 2.0 ** -23], np.float32)
+    x = np.concatenate([special, -special, np.float32(2.0) ** rng.uniform(-30, 17, 4000).astype(np.float32),
+                        rng.standard_normal(2000).astype(np.float32) * 1e-6]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(orc.f32_to_f16_bits(x), ref)
+
+
+def test_int4_fp16_scales(orc):
+    # fp16 scale storage (the QLoRA configuration): the bytes are those of the fp32-scale run, the
+    # scales are the fp16 rounding of the fp32 ones, dequantization multiplies by the widened fp16
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(8192) * 0.02).astype(np.float32)
+    x[128:256] *= 1e-6                                                # an fp16-subnormal scale
+    p32, s32 = orc.int4_quantize(x, 128)
+    p16, s16 = orc.int4_quantize(x, 128, scale_f16=True)
+    np.testing.assert_array_equal(p16, p32)
+    np.testing.assert_array_equal(s16, s32.astype(np.float16))
+    deq = orc.int4_dequantize(p16, s16, x.size, 128)
+    q = orc.int4_dequantize(p32, np.ones_like(s32), x.size, 128)
+    np.testing.assert_array_equal(deq, q * np.repeat(s16.astype(np.float32), 128))
+
+
+# --------------------------------------------------------------------------- LoRA
+def _lora_inputs(rng, Bt, S, inn, out, r):
+    x = rng.standard_normal((Bt * S, inn)).astype(np.float32)
+    W = (rng.standard_normal((out, inn)) / math.sqrt(inn)).astype(np.float32)
+    A = rng.uniform(-1 / math.sqrt(inn), 1 / math.sqrt(inn), (r, inn)).astype(np.float32)
+    Bm = rng.uniform(-0.5, 0.5, (out, r)).astype(np.float32)
+    return x, W, A, Bm
+
+
+def test_lora_zero_b_is_the_base_linear(orc):
+    # tests/unit/test_lora.cpp:58-73: B = 0 at initialisation, so the output equals the base
+    rng = np.random.default_rng(1)
+    x, W, A, _ = _lora_inputs(rng, 2, 16, 64, 128, 8)
+    y, _ = orc.lora_fwd(x, W, A, np.zeros((128, 8), np.float32), 16.0 / 8, 2, 16)
+    np.testing.assert_array_equal(y, orc.linear_fwd(x, W, 2, 16))
+
+
+def test_lora_merge_matches_unmerged_forward(orc):
+    # tests/unit/test_lora.cpp:107-143 at its tolerance (1e-4), and unmerge restores W
+    rng = np.random.default_rng(2)
+    x, W, A, Bm = _lora_inputs(rng, 2, 8, 32, 48, 4)
+    y, _ = orc.lora_fwd(x, W, A, Bm, 8.0 / 4, 2, 8)
+    Wm = orc.lora_merge(W, A, Bm, 8.0 / 4)
+    assert np.max(np.abs(orc.linear_fwd(x, Wm, 2, 8) - y)) < 1e-4
+    assert np.max(np.abs(orc.lora_merge(Wm, A, Bm, 8.0 / 4, sign=-1) - W)) < 1e-6
+
+
+@pytest.mark.parametrize("Bt,S,inn,out,r", [(2, 16, 64, 48, 8), (1, 40, 96, 32, 16), (3, 5, 17, 23, 3)])
+def test_lora_fwd_bwd_vs_float64(orc, Bt, S, inn, out, r):
+    rng = np.random.default_rng(Bt * S + inn + r)
+    x, W, A, Bm = _lora_inputs(rng, Bt, S, inn, out, r)
+    dy = rng.standard_normal((Bt * S, out)).astype(np.float32)
+    scaling = 32.0 / r
+    y, xa = orc.lora_fwd(x, W, A, Bm, scaling, Bt, S)
+    dx, dA, dB = orc.lora_bwd(x, W, A, Bm, scaling, dy, Bt, S)
+    xt, At, Bt_ = (torch.tensor(t, dtype=torch.float64, requires_grad=True) for t in (x, A, Bm))
+    Wt = torch.tensor(W, dtype=torch.float64)
+    yt = F.linear(xt, Wt) + F.linear(F.linear(xt, At), Bt_) * scaling
+    yt.backward(torch.tensor(dy, dtype=torch.float64))
+    assert rel(y, yt.detach().numpy()) < 1e-6
+    assert rel(xa, F.linear(xt, At).detach().numpy()) < 1e-6
+    assert rel(dx, xt.grad.numpy()) < 1e-5
+    assert rel(dA, At.grad.numpy()) < 1e-5
+    assert rel(dB, Bt_.grad.numpy()) < 1e-5
