@@ -23,9 +23,10 @@ from collections import defaultdict
 
 # (regex on the demangled or mangled symbol, class); first match wins.
 _RULES = [
-    (r"gemm_bf16_dma(<\d+, \d+, \d+, false, true|ILi\d+ELi\d+ELi\d+ELb0ELb1E)", "gemm_fwd"),
-    (r"gemm_bf16_dma(<\d+, \d+, \d+, false, false|ILi\d+ELi\d+ELi\d+ELb0ELb0E)", "gemm_dgrad"),
-    (r"gemm_bf16_dma(<\d+, \d+, \d+, true, false|ILi\d+ELi\d+ELi\d+ELb1ELb0E)", "gemm_wgrad"),
+    # gemm_bf16_dma<BM, BN, BK, STAGES, transA, transB, C>, demangled or mangled
+    (r"gemm_bf16_dma(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
+    (r"gemm_bf16_dma(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
     (r"attn_fwd", "attn_fwd"),
     (r"attn_bwd|attn_dot", "attn_bwd"),
     (r"rmsnorm_fwd", "rmsnorm_fwd"),
