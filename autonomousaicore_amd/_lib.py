@@ -96,6 +96,14 @@ SIGNATURES = {
     "aic_qlora_linear_destroy": (i32, [vp]),
     "aic_qlora_linear_forward": (i32, [vp, vp, i64, vp, vp, vp, vp, vp, vp, vp]),
     "aic_qlora_linear_backward": (i32, [vp, vp, vp, vp, vp, i32, vp]),
+    "aic_hip_strided_copy": (i32, [vp, i64, i32, i64p, i64p, i64, vp, vp]),
+    "aic_hip_cast": (i32, [vp, i32, vp, i32, i64, vp]),
+    "aic_hip_binary": (i32, [i32, vp, i64, i32, i64p, i64p, vp, i64, i32, i64p, i64p, vp, vp]),
+    "aic_hip_unary": (i32, [i32, vp, vp, i64, vp]),
+    "aic_hip_reduce_all": (i32, [i32, vp, i64, vp, vp]),
+    "aic_hip_reduce_dim": (i32, [i32, vp, i32, i64p, i32, vp, vp]),
+    "aic_hip_cat": (i32, [C.POINTER(vp), i64p, i32, i64, i64, i64, vp, vp]),
+    "aic_hip_sum_to_shape": (i32, [vp, i32, i64p, i32, i64p, vp, vp]),
     "aic_lm_create": (i32, [C.POINTER(LMConfig), C.POINTER(TrainConfig), C.POINTER(vp)]),
     "aic_lm_destroy": (i32, [vp]),
     "aic_lm_num_params": (i64, [vp]),

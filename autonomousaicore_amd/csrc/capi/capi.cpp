@@ -623,4 +623,45 @@ int aic_qlora_linear_backward(aic_qlora_linear* m, const void* dy, void* dx, flo
     });
 }
 
+// ------------------------------------------------------------------ tensor primitives
+int aic_hip_strided_copy(const void* src, int64_t offset, int ndim, const int64_t* shape, const int64_t* strides,
+                         int64_t elem_size, void* dst, aic_stream stream) {
+    return guard([&] { aic::hip::strided_copy(src, offset, ndim, shape, strides, elem_size, dst, st(stream)); });
+}
+
+int aic_hip_cast(const void* src, aic_dtype from, void* dst, aic_dtype to, int64_t n, aic_stream stream) {
+    return guard([&] { aic::hip::cast(src, dt(from), dst, dt(to), n, st(stream)); });
+}
+
+int aic_hip_binary(int op, const float* a, int64_t a_offset, int a_ndim, const int64_t* a_shape,
+                   const int64_t* a_strides, const float* b, int64_t b_offset, int b_ndim, const int64_t* b_shape,
+                   const int64_t* b_strides, float* out, aic_stream stream) {
+    return guard([&] {
+        aic::hip::binary(op, a, a_offset, a_ndim, a_shape, a_strides, b, b_offset, b_ndim, b_shape, b_strides, out,
+                         st(stream));
+    });
+}
+
+int aic_hip_unary(int op, const float* x, float* y, int64_t n, aic_stream stream) {
+    return guard([&] { aic::hip::unary(op, x, y, n, st(stream)); });
+}
+
+int aic_hip_reduce_all(int op, const float* x, int64_t n, float* out, aic_stream stream) {
+    return guard([&] { aic::hip::reduce_all(op, x, n, out, st(stream)); });
+}
+
+int aic_hip_reduce_dim(int op, const float* x, int ndim, const int64_t* shape, int dim, float* out, aic_stream stream) {
+    return guard([&] { aic::hip::reduce_dim(op, x, ndim, shape, dim, out, st(stream)); });
+}
+
+int aic_hip_cat(const void* const* srcs, const int64_t* mids, int count, int64_t outer, int64_t inner,
+                int64_t elem_size, void* dst, aic_stream stream) {
+    return guard([&] { aic::hip::cat(srcs, mids, count, outer, inner, elem_size, dst, st(stream)); });
+}
+
+int aic_hip_sum_to_shape(const float* grad, int ndim, const int64_t* shape, int target_ndim,
+                         const int64_t* target_shape, float* out, aic_stream stream) {
+    return guard([&] { aic::hip::sum_to_shape(grad, ndim, shape, target_ndim, target_shape, out, st(stream)); });
+}
+
 }  // extern "C"

@@ -64,6 +64,24 @@ void int4_quantize(const float* x, int64_t n, int64_t G, uint8_t* packed, void* 
 void int4_dequant(const uint8_t* packed, const void* scales, DType scale_t, int64_t n, int64_t G, void* out, DType out_t,
                   hipStream_t s);
 
+// Tensor primitives (tensor_ops.hip).  Views are (offset, rank <= 8, shape, strides) in elements;
+// binary ops broadcast NumPy-style into a contiguous output.  op codes: binary 0 add, 1 sub,
+// 2 mul, 3 div; unary 0 neg, 1 abs, 2 exp, 3 log, 4 sqrt, 5 tanh, 6 sigmoid, 7 gelu, 8 silu;
+// reductions 0 sum, 1 mean, 2 max, 3 min.
+void strided_copy(const void* src, int64_t offset, int ndim, const int64_t* shape, const int64_t* strides,
+                  int64_t elem_size, void* dst, hipStream_t s);
+void cast(const void* src, DType from, void* dst, DType to, int64_t n, hipStream_t s);
+void binary(int op, const float* a, int64_t a_off, int ra, const int64_t* a_shape, const int64_t* a_strides,
+            const float* b, int64_t b_off, int rb, const int64_t* b_shape, const int64_t* b_strides, float* out,
+            hipStream_t s);
+void unary(int op, const float* x, float* y, int64_t n, hipStream_t s);
+void reduce_all(int op, const float* x, int64_t n, float* out, hipStream_t s);
+void reduce_dim(int op, const float* x, int ndim, const int64_t* shape, int dim, float* out, hipStream_t s);
+void cat(const void* const* srcs, const int64_t* mids, int count, int64_t outer, int64_t inner, int64_t elem_size,
+         void* dst, hipStream_t s);
+void sum_to_shape(const float* g, int ndim, const int64_t* shape, int tr, const int64_t* target, float* out,
+                  hipStream_t s);
+
 // Attention (attention.hip)
 void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
               int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);

@@ -311,6 +311,48 @@ int aic_qlora_linear_forward(aic_qlora_linear* m, const void* x, int64_t T, cons
 int aic_qlora_linear_backward(aic_qlora_linear* m, const void* dy, void* dx, float* dA, float* dB, int accumulate,
                               aic_stream stream);
 
+/* ---------------------------------------------------------------- tensor primitives */
+/* fp32 primitives of the reference's tensor backend.  A view is (offset, ndim <= 8, shape,
+ * strides), all in elements, with shape/strides host arrays; outputs are contiguous. */
+/* Contiguous copy of a strided view (elem_size 1, 2, 4 or 8 bytes).
+ * Replaces: Tensor::clone / contiguous (src/tensor/tensor.cpp:248-304), whose GPU path goes
+ * through the host. */
+int aic_hip_strided_copy(const void* src, int64_t offset, int ndim, const int64_t* shape, const int64_t* strides,
+                         int64_t elem_size, void* dst, aic_stream stream);
+/* n elements from -> to for the reference's cast table (f32<->f16, f32<->bf16, f32<->i64,
+ * f32<->i32, i64<->i32), with its rounding and NaN encodings (include/core/dtype.hpp:65-133);
+ * any other pair fails with NotImplemented (8).
+ * Replaces: Tensor::to(DType) (src/tensor/tensor.cpp:359-410), a host round trip on the GPU. */
+int aic_hip_cast(const void* src, aic_dtype from, void* dst, aic_dtype to, int64_t n, aic_stream stream);
+/* out = a (op) b with NumPy broadcasting (op 0 add, 1 sub, 2 mul, 3 div); out has the
+ * broadcast shape.  Incompatible shapes fail with ShapeMismatch (3).
+ * Replaces: aic::cuda::add/sub/mul/div (src/cuda/cuda_elementwise.cuh:9-12; semantics of
+ * src/ops/cpu_ops.cpp:14-101 and src/core/shape.cpp:138-195). */
+int aic_hip_binary(int op, const float* a, int64_t a_offset, int a_ndim, const int64_t* a_shape,
+                   const int64_t* a_strides, const float* b, int64_t b_offset, int b_ndim, const int64_t* b_shape,
+                   const int64_t* b_strides, float* out, aic_stream stream);
+/* y = f(x) over n contiguous elements: 0 neg, 1 abs, 2 exp, 3 log, 4 sqrt, 5 tanh, 6 sigmoid,
+ * 7 gelu (tanh form), 8 silu.
+ * Replaces: aic::cuda::neg ... silu (src/cuda/cuda_elementwise.cuh:14-22; src/ops/cpu_ops.cpp:105-146). */
+int aic_hip_unary(int op, const float* x, float* y, int64_t n, aic_stream stream);
+/* *out = sum / mean / max / min (op 0..3) of n contiguous elements; sums in double.
+ * Replaces: aic::cuda::sum/mean/max/min(a) (src/cuda/cuda_reductions.cuh:10-14; src/ops/cpu_ops.cpp:151-197). */
+int aic_hip_reduce_all(int op, const float* x, int64_t n, float* out, aic_stream stream);
+/* Reduction of a contiguous tensor along dim (negative counts from the end); out holds the
+ * shape without dim (keepdim only changes the shape).
+ * Replaces: aic::cuda::sum/mean/max/min(a, dim, keepdim) (src/cuda/cuda_reductions.cuh:15-18;
+ * src/ops/cpu_ops.cpp:203-287). */
+int aic_hip_reduce_dim(int op, const float* x, int ndim, const int64_t* shape, int dim, float* out, aic_stream stream);
+/* Concatenation of count contiguous [outer, mids[i], inner] tensors (device pointers in a host
+ * array) into [outer, sum(mids), inner].  Replaces: cat (src/ops/ops.cpp:473-530). */
+int aic_hip_cat(const void* const* srcs, const int64_t* mids, int count, int64_t outer, int64_t inner,
+                int64_t elem_size, void* dst, aic_stream stream);
+/* Sums a broadcast gradient back to target_shape: leading dims, then dims where the target is 1,
+ * one float-rounded sum per dim as the reference does.
+ * Replaces: reduce_gradient_for_broadcast (src/autograd/functions.cpp:10-41). */
+int aic_hip_sum_to_shape(const float* grad, int ndim, const int64_t* shape, int target_ndim,
+                         const int64_t* target_shape, float* out, aic_stream stream);
+
 /* ---------------------------------------------------------------- TransformerLM ---- */
 /* The whole training step behind the reference's C++ API (TransformerLM::forward,
  * cross_entropy, Tensor::backward, DynamicLossScaler, clip_grad_norm_, AdamW::step;

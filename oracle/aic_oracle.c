@@ -1191,3 +1191,283 @@ void orc_lora_merge(float* W, const float* A, const float* Bm, float scaling, in
     }
     free(dw);
 }
+
+/* ======================================================================================
+ * Tensor primitives (src/ops/cpu_ops.cpp, src/tensor/tensor.cpp, src/core/shape.cpp,
+ * src/ops/ops.cpp cat, src/autograd/functions.cpp reduce_gradient_for_broadcast)
+ * ====================================================================================== */
+
+/* Shape::broadcast (src/core/shape.cpp:138-166); returns the output rank or -1. */
+int orc_broadcast_shape(const int64_t* a, int ra, const int64_t* b, int rb, int64_t* out) {
+    const int r = ra > rb ? ra : rb;
+    for (int i = 0; i < r; ++i) {
+        const int64_t da = i < ra ? a[ra - 1 - i] : 1, db = i < rb ? b[rb - 1 - i] : 1;
+        if (da != db && da != 1 && db != 1) return -1;
+        out[r - 1 - i] = da > db ? da : db;
+    }
+    return r;
+}
+
+/* Shape::broadcast_strides (src/core/shape.cpp:168-195); returns 0 or -1. */
+static int bcast_strides(const int64_t* shape, const int64_t* strides, int r, const int64_t* target, int tr,
+                         int64_t* out) {
+    if (r > tr) return -1;
+    for (int i = 0; i < tr; ++i) {
+        const int oi = r - 1 - i, ti = tr - 1 - i;
+        if (oi >= 0) {
+            if (shape[oi] == target[ti]) out[ti] = strides[oi];
+            else if (shape[oi] == 1) out[ti] = 0;
+            else return -1;
+        } else {
+            out[ti] = 0;
+        }
+    }
+    return 0;
+}
+
+/* Tensor::clone of a strided view (src/tensor/tensor.cpp:255-297): row-major multi-index walk. */
+void orc_strided_copy(const void* src, int64_t offset, int ndim, const int64_t* shape, const int64_t* strides,
+                      int64_t elem_size, void* dst) {
+    int64_t total = 1, coords[16] = {0};
+    for (int i = 0; i < ndim; ++i) total *= shape[i];
+    const char* s = (const char*)src;
+    char* d = (char*)dst;
+    for (int64_t lin = 0; lin < total; ++lin) {
+        int64_t off = offset;
+        for (int i = 0; i < ndim; ++i) off += coords[i] * strides[i];
+        memcpy(d + lin * elem_size, s + off * elem_size, (size_t)elem_size);
+        for (int i = ndim - 1; i >= 0; --i) {
+            if (++coords[i] < shape[i]) break;
+            coords[i] = 0;
+        }
+    }
+}
+
+/* float_to_half / half_to_float / float_to_bf16 (include/core/dtype.hpp:65-133), restated. */
+static uint16_t ref_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t mant = x & 0x007FFFFFu;
+    const int32_t exp = (int32_t)((x >> 23) & 0xFFu);
+    if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (mant ? (0x200u | (mant >> 13)) : 0u));
+    const int32_t e = exp - 127 + 15;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        mant |= 0x00800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t hm = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (hm & 1u))) ++hm;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)h;
+}
+
+static uint16_t ref_f32_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x007FFFFFu) != 0) return (uint16_t)(((x >> 16) & 0x8000u) | 0x7FC0u);
+    return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+static float ref_f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x3FFu, bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do {
+                ++e;
+                mant <<= 1;
+            } while ((mant & 0x400u) == 0);
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((mant & 0x3FFu) << 13);
+        }
+    } else if (exp == 0x1F) {
+        bits = sign | 0x7F800000u | (mant << 13);  /* NaN payloads are kept as they are */
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static float ref_bf16_to_f32(uint16_t b) {
+    const uint32_t x = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* Tensor::to(DType) cast table (src/tensor/tensor.cpp:359-410).  dtype codes as aic::DType:
+ * 0 f32, 1 f16, 2 bf16, 3 i32, 4 i64.  Returns 0, or 1 for a pair the reference rejects. */
+int orc_cast(const void* src, int from, void* dst, int to, int64_t n) {
+    if (from == to) {
+        const int64_t es = (from == 4) ? 8 : ((from == 0 || from == 3) ? 4 : 2);
+        memcpy(dst, src, (size_t)(n * es));
+        return 0;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        if (from == 0 && to == 1) ((uint16_t*)dst)[i] = ref_f32_to_f16(((const float*)src)[i]);
+        else if (from == 0 && to == 2) ((uint16_t*)dst)[i] = ref_f32_to_bf16(((const float*)src)[i]);
+        else if (from == 1 && to == 0) ((float*)dst)[i] = ref_f16_to_f32(((const uint16_t*)src)[i]);
+        else if (from == 2 && to == 0) ((float*)dst)[i] = ref_bf16_to_f32(((const uint16_t*)src)[i]);
+        else if (from == 0 && to == 4) ((int64_t*)dst)[i] = (int64_t)((const float*)src)[i];
+        else if (from == 4 && to == 0) ((float*)dst)[i] = (float)((const int64_t*)src)[i];
+        else if (from == 0 && to == 3) ((int32_t*)dst)[i] = (int32_t)((const float*)src)[i];
+        else if (from == 3 && to == 0) ((float*)dst)[i] = (float)((const int32_t*)src)[i];
+        else if (from == 4 && to == 3) ((int32_t*)dst)[i] = (int32_t)((const int64_t*)src)[i];
+        else if (from == 3 && to == 4) ((int64_t*)dst)[i] = (int64_t)((const int32_t*)src)[i];
+        else return 1;
+    }
+    return 0;
+}
+
+/* binary_broadcast_cpu (src/ops/cpu_ops.cpp:14-60); op 0 add, 1 sub, 2 mul, 3 div.  Views are
+ * (offset, shape, strides) in elements; out is contiguous of the broadcast shape.  Returns 0 or -1. */
+int orc_binary(int op, const float* a, int64_t a_off, const int64_t* a_shape, const int64_t* a_strides, int ra,
+               const float* b, int64_t b_off, const int64_t* b_shape, const int64_t* b_strides, int rb, float* out) {
+    int64_t oshape[16], sa[16], sb[16], coords[16] = {0};
+    const int r = orc_broadcast_shape(a_shape, ra, b_shape, rb, oshape);
+    if (r < 0 || bcast_strides(a_shape, a_strides, ra, oshape, r, sa) || bcast_strides(b_shape, b_strides, rb, oshape, r, sb))
+        return -1;
+    int64_t total = 1;
+    for (int i = 0; i < r; ++i) total *= oshape[i];
+    for (int64_t lin = 0; lin < total; ++lin) {
+        int64_t oa = a_off, ob = b_off;
+        for (int k = 0; k < r; ++k) {
+            oa += coords[k] * sa[k];
+            ob += coords[k] * sb[k];
+        }
+        const float x = a[oa], y = b[ob];
+        out[lin] = op == 0 ? x + y : (op == 1 ? x - y : (op == 2 ? x * y : x / y));
+        for (int k = r - 1; k >= 0; --k) {
+            if (++coords[k] < oshape[k]) break;
+            coords[k] = 0;
+        }
+    }
+    return 0;
+}
+
+/* unary_cpu functions (src/ops/cpu_ops.cpp:105-146): 0 neg, 1 abs, 2 exp, 3 log, 4 sqrt, 5 tanh,
+ * 6 sigmoid, 7 gelu (tanh form), 8 silu. */
+void orc_unary(int op, const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        float r;
+        switch (op) {
+            case 0: r = -v; break;
+            case 1: r = fabsf(v); break;
+            case 2: r = expf(v); break;
+            case 3: r = logf(v); break;
+            case 4: r = sqrtf(v); break;
+            case 5: r = tanhf(v); break;
+            case 6: r = 1.0f / (1.0f + expf(-v)); break;
+            case 7: {
+                const float inner = 0.7978845608f * (v + 0.044715f * v * v * v);
+                r = 0.5f * v * (1.0f + tanhf(inner));
+                break;
+            }
+            default: r = v / (1.0f + expf(-v)); break;
+        }
+        y[i] = r;
+    }
+}
+
+/* Full reductions (src/ops/cpu_ops.cpp:151-197): 0 sum (double), 1 mean (sum / (float)n),
+ * 2 max, 3 min (NaN never replaces the running value). */
+float orc_reduce_all(int op, const float* x, int64_t n) {
+    if (op == 0 || op == 1) {
+        double acc = 0.0;
+        for (int64_t i = 0; i < n; ++i) acc += (double)x[i];
+        float s = (float)acc;
+        if (op == 1) s /= (float)n;
+        return s;
+    }
+    float m = op == 2 ? -INFINITY : INFINITY;
+    for (int64_t i = 0; i < n; ++i)
+        if (op == 2 ? x[i] > m : x[i] < m) m = x[i];
+    return m;
+}
+
+/* reduce_dim_cpu (src/ops/cpu_ops.cpp:203-271) on a contiguous x of `shape`: out has the shape
+ * without `dim` (keepdim only changes the shape).  Mean is (float)(sum / size) in double. */
+void orc_reduce_dim(int op, const float* x, int ndim, const int64_t* shape, int dim, float* out) {
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < dim; ++i) outer *= shape[i];
+    for (int i = dim + 1; i < ndim; ++i) inner *= shape[i];
+    const int64_t rs = shape[dim];
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t in = 0; in < inner; ++in) {
+            const float* p = x + o * rs * inner + in;
+            double acc = 0.0;
+            float mx = -INFINITY, mn = INFINITY;
+            for (int64_t k = 0; k < rs; ++k) {
+                const float v = p[k * inner];
+                if (op <= 1) acc += (double)v;
+                else if (op == 2) { if (v > mx) mx = v; }
+                else if (v < mn) mn = v;
+            }
+            out[o * inner + in] = op == 0 ? (float)acc : (op == 1 ? (float)(acc / (double)rs) : (op == 2 ? mx : mn));
+        }
+}
+
+/* cat along `dim` of `count` contiguous inputs that agree outside dim (src/ops/ops.cpp:473-530):
+ * out = [outer, sum(mid_i), inner]. */
+void orc_cat(const void* const* srcs, const int64_t* mids, int count, int64_t outer, int64_t inner, int64_t elem_size,
+             void* dst) {
+    int64_t total_mid = 0;
+    for (int i = 0; i < count; ++i) total_mid += mids[i];
+    int64_t off = 0;
+    for (int i = 0; i < count; ++i) {
+        const int64_t row = mids[i] * inner * elem_size;
+        for (int64_t o = 0; o < outer; ++o)
+            memcpy((char*)dst + (o * total_mid + off) * inner * elem_size, (const char*)srcs[i] + o * row, (size_t)row);
+        off += mids[i];
+    }
+}
+
+/* reduce_gradient_for_broadcast (src/autograd/functions.cpp:10-41): sum over leading dims, then
+ * over the dims where the target has size 1 (each a reduce_dim sum, rounded to float between
+ * steps).  out has the target's element count.  Returns 0 or -1. */
+int orc_sum_to_shape(const float* g, int ndim, const int64_t* shape, int tr, const int64_t* target, float* out) {
+    int64_t cur[16], n = 1;
+    int r = ndim;
+    for (int i = 0; i < ndim; ++i) { cur[i] = shape[i]; n *= shape[i]; }
+    float* buf = (float*)xcalloc((size_t)(n > 0 ? n : 1), sizeof(float));
+    float* tmp = (float*)xcalloc((size_t)(n > 0 ? n : 1), sizeof(float));
+    memcpy(buf, g, sizeof(float) * (size_t)n);
+    if (tr == 0) {
+        out[0] = orc_reduce_all(0, buf, n);
+        free(tmp); free(buf);
+        return 0;
+    }
+    while (r > tr) {
+        orc_reduce_dim(0, buf, r, cur, 0, tmp);
+        n /= cur[0];
+        for (int i = 0; i + 1 < r; ++i) cur[i] = cur[i + 1];
+        --r;
+        float* t = buf; buf = tmp; tmp = t;
+    }
+    for (int i = 0; i < tr; ++i) {
+        if (target[i] == 1 && cur[i] > 1) {
+            orc_reduce_dim(0, buf, r, cur, i, tmp);
+            n /= cur[i];
+            cur[i] = 1;
+            float* t = buf; buf = tmp; tmp = t;
+        }
+    }
+    for (int i = 0; i < tr; ++i)
+        if (cur[i] != target[i]) { free(tmp); free(buf); return -1; }
+    memcpy(out, buf, sizeof(float) * (size_t)n);
+    free(tmp);
+    free(buf);
+    return 0;
+}

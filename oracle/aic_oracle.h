@@ -34,6 +34,9 @@
  *                         |deq - x| <= s/2, byte idempotence; fp16 scales vs numpy float16
  *   orc_lora_*            B = 0 identity (tests/unit/test_lora.cpp:58-73), merge == unmerged
  *                         forward (:107-143), torch float64 autograd
+ *   orc_binary/unary/...  reference known answers (tests/unit/test_ops.cpp, test_tensor.cpp:45-98,
+ *                         test_shape.cpp:49-72), numpy broadcasting / as_strided / float64
+ *                         reductions / float16 casts, torch bfloat16 casts
  *   orc_lm_step           whole step vs an independent torch float64 model built from
  *                         library routines (F.embedding, F.linear, F.rms_norm, SDPA,
  *                         F.silu, F.cross_entropy, clip_grad_norm_, torch.optim.AdamW)
@@ -211,6 +214,31 @@ void orc_lora_bwd(const float* x, const float* W, const float* A, const float* B
 /* LoRALinear::merge / unmerge (lora.cpp:95-108): W = W +- (Bm A) * scaling (sign >= 0: merge). */
 void orc_lora_merge(float* W, const float* A, const float* Bm, float scaling, int64_t in, int64_t out, int64_t r,
                     int sign);
+
+/* ---- Tensor primitives (fp32 compute; src/ops/cpu_ops.cpp, src/tensor/tensor.cpp) ---- */
+/* Shape::broadcast (src/core/shape.cpp:138-166): output rank, or -1 if incompatible. */
+int orc_broadcast_shape(const int64_t* a, int ra, const int64_t* b, int rb, int64_t* out);
+/* Tensor::clone of a strided view (src/tensor/tensor.cpp:255-297); ndim <= 16. */
+void orc_strided_copy(const void* src, int64_t offset, int ndim, const int64_t* shape, const int64_t* strides,
+                      int64_t elem_size, void* dst);
+/* Tensor::to(DType) (src/tensor/tensor.cpp:359-410); codes 0 f32, 1 f16, 2 bf16, 3 i32, 4 i64.
+ * Returns 1 for a pair the reference does not implement. */
+int orc_cast(const void* src, int from, void* dst, int to, int64_t n);
+/* binary_broadcast_cpu (src/ops/cpu_ops.cpp:14-60): op 0 add, 1 sub, 2 mul, 3 div. */
+int orc_binary(int op, const float* a, int64_t a_off, const int64_t* a_shape, const int64_t* a_strides, int ra,
+               const float* b, int64_t b_off, const int64_t* b_shape, const int64_t* b_strides, int rb, float* out);
+/* unary_cpu (src/ops/cpu_ops.cpp:105-146): 0 neg, 1 abs, 2 exp, 3 log, 4 sqrt, 5 tanh, 6 sigmoid,
+ * 7 gelu, 8 silu. */
+void orc_unary(int op, const float* x, float* y, int64_t n);
+/* sum / mean / max / min over all elements (src/ops/cpu_ops.cpp:151-197): op 0..3. */
+float orc_reduce_all(int op, const float* x, int64_t n);
+/* reduce_dim_cpu (src/ops/cpu_ops.cpp:203-271) of a contiguous tensor along dim. */
+void orc_reduce_dim(int op, const float* x, int ndim, const int64_t* shape, int dim, float* out);
+/* cat (src/ops/ops.cpp:473-530) of contiguous [outer, mid_i, inner] inputs. */
+void orc_cat(const void* const* srcs, const int64_t* mids, int count, int64_t outer, int64_t inner, int64_t elem_size,
+             void* dst);
+/* reduce_gradient_for_broadcast (src/autograd/functions.cpp:10-41). */
+int orc_sum_to_shape(const float* g, int ndim, const int64_t* shape, int tr, const int64_t* target, float* out);
 
 #ifdef __cplusplus
 }

@@ -436,3 +436,118 @@ def lora_merge(W, A, Bm, scaling, sign=1):
     lib().orc_lora_merge(_f(W), _f(A), _f(Bm), C.c_float(scaling), C.c_int64(inn), C.c_int64(out),
                          C.c_int64(A.shape[0]), C.c_int(sign))
     return W
+
+
+# ----------------------------------------------------------------------------- tensor primitives
+DT_CODES = {np.dtype(np.float32): 0, np.dtype(np.float16): 1, np.dtype(np.int32): 3, np.dtype(np.int64): 4}
+BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+UNARY = {"neg": 0, "abs": 1, "exp": 2, "log": 3, "sqrt": 4, "tanh": 5, "sigmoid": 6, "gelu": 7, "silu": 8}
+REDUCE = {"sum": 0, "mean": 1, "max": 2, "min": 3}
+
+
+def _i64arr(v):
+    return np.ascontiguousarray(np.asarray(v, np.int64))
+
+
+def broadcast_shape(a, b):
+    out = np.zeros(max(len(a), len(b), 1), np.int64)
+    r = lib().orc_broadcast_shape(_i(_i64arr(a)), C.c_int(len(a)), _i(_i64arr(b)), C.c_int(len(b)), _i(out))
+    if r < 0:
+        raise ValueError("shapes do not broadcast")
+    return tuple(int(v) for v in out[:r])
+
+
+def strided_copy(base, offset, shape, strides):
+    """orc_strided_copy of the view (offset, shape, strides) (in elements) of a flat array."""
+    base = np.ascontiguousarray(base)
+    out = np.empty(int(np.prod(shape)) if len(shape) else 1, base.dtype)
+    lib().orc_strided_copy(base.ctypes.data_as(C.c_void_p), C.c_int64(offset), C.c_int(len(shape)),
+                           _i(_i64arr(shape)), _i(_i64arr(strides)), C.c_int64(base.itemsize),
+                           out.ctypes.data_as(C.c_void_p))
+    return out.reshape(shape)
+
+
+def cast(x, to, bf16_from=False):
+    """orc_cast: x (float32 / float16 / int32 / int64, or uint16 bf16 bits with bf16_from) -> `to`
+    ("f32", "f16", "bf16", "i32", "i64"); 16-bit results are returned as uint16 bits."""
+    x = np.ascontiguousarray(x)
+    fr = 2 if bf16_from else DT_CODES[x.dtype] if x.dtype != np.uint16 else 1
+    code = {"f32": 0, "f16": 1, "bf16": 2, "i32": 3, "i64": 4}[to]
+    odt = {0: np.float32, 1: np.uint16, 2: np.uint16, 3: np.int32, 4: np.int64}[code]
+    out = np.empty(x.shape, odt)
+    rc = lib().orc_cast(x.ctypes.data_as(C.c_void_p), C.c_int(fr), out.ctypes.data_as(C.c_void_p), C.c_int(code),
+                        C.c_int64(x.size))
+    if rc != 0:
+        raise NotImplementedError(f"cast {fr} -> {code}")
+    return out
+
+
+def binary(op, a, b, a_view=None, b_view=None):
+    """orc_binary.  a / b are arrays (contiguous views) or flat bases with views (offset, shape, strides)."""
+    def view(x, v):
+        x = np.ascontiguousarray(x, np.float32)
+        if v is None:
+            st = [s // 4 for s in x.strides] if x.ndim else []
+            return x.ravel(), 0, list(x.shape), st
+        return x.ravel(), v[0], list(v[1]), list(v[2])
+    xa, oa, sa, ta = view(a, a_view)
+    xb, ob, sb, tb = view(b, b_view)
+    shape = broadcast_shape(sa, sb)
+    out = np.empty(shape, np.float32)
+    rc = lib().orc_binary(C.c_int(BINARY[op]), _f(xa), C.c_int64(oa), _i(_i64arr(sa)), _i(_i64arr(ta)),
+                          C.c_int(len(sa)), _f(xb), C.c_int64(ob), _i(_i64arr(sb)), _i(_i64arr(tb)), C.c_int(len(sb)),
+                          _f(out))
+    if rc != 0:
+        raise ValueError("shapes do not broadcast")
+    return out
+
+
+def unary(op, x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_unary(C.c_int(UNARY[op]), _f(x), _f(y), C.c_int64(x.size))
+    return y
+
+
+def reduce_all(op, x):
+    L = lib()
+    L.orc_reduce_all.restype = C.c_float
+    x = np.ascontiguousarray(x, np.float32)
+    return np.float32(L.orc_reduce_all(C.c_int(REDUCE[op]), _f(x), C.c_int64(x.size)))
+
+
+def reduce_dim(op, x, dim, keepdim=False):
+    x = np.ascontiguousarray(x, np.float32)
+    d = dim + x.ndim if dim < 0 else dim
+    oshape = [s for i, s in enumerate(x.shape) if i != d]
+    out = np.empty(oshape, np.float32)
+    lib().orc_reduce_dim(C.c_int(REDUCE[op]), _f(x), C.c_int(x.ndim), _i(_i64arr(x.shape)), C.c_int(d), _f(out))
+    if keepdim:
+        out = out.reshape([1 if i == d else s for i, s in enumerate(x.shape)])
+    return out
+
+
+def cat(arrays, dim):
+    arrays = [np.ascontiguousarray(a) for a in arrays]
+    r = arrays[0].ndim
+    d = dim + r if dim < 0 else dim
+    outer = int(np.prod(arrays[0].shape[:d]))
+    inner = int(np.prod(arrays[0].shape[d + 1:]))
+    mids = _i64arr([a.shape[d] for a in arrays])
+    shape = list(arrays[0].shape)
+    shape[d] = int(mids.sum())
+    out = np.empty(shape, arrays[0].dtype)
+    ptrs = (C.c_void_p * len(arrays))(*[a.ctypes.data for a in arrays])
+    lib().orc_cat(ptrs, _i(mids), C.c_int(len(arrays)), C.c_int64(outer), C.c_int64(inner),
+                  C.c_int64(arrays[0].itemsize), out.ctypes.data_as(C.c_void_p))
+    return out
+
+
+def sum_to_shape(g, target):
+    g = np.ascontiguousarray(g, np.float32)
+    out = np.empty(target, np.float32)
+    rc = lib().orc_sum_to_shape(_f(g), C.c_int(g.ndim), _i(_i64arr(g.shape)), C.c_int(len(target)),
+                                _i(_i64arr(target)), _f(out))
+    if rc != 0:
+        raise ValueError("cannot reduce to the target shape")
+    return out

@@ -64,6 +64,31 @@ def test_gemm_epilogue_residual_alpha_beta():
     assert rel(host(out), ref) < 1e-5
 
 
+# Weight-gradient shapes of the 1B step (o_proj, gate/up) over the full K = 8192, partial
+# tiles with long K, each with residual / alpha / beta epilogues; runs must be bit-identical.
+LONG_K_CASES = [(1, 0, 2048, 2048, 8192), (1, 0, 11264, 2048, 8192), (0, 1, 600, 520, 8192),
+                (0, 0, 1000, 1000, 4096), (1, 1, 264, 1032, 8192)]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K", LONG_K_CASES)
+def test_gemm_long_k_and_epilogues(ta, tb, M, N, K):
+    rng = np.random.default_rng(M + N + K + ta)
+    A = bf16_round(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = bf16_round(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    R = bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    ref = _ref_gemm(ta, tb, A, B)
+    Ad, Bd, Rd = dev(A, torch.bfloat16), dev(B, torch.bfloat16), dev(R)
+    c1 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32)
+    c2 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32)
+    assert rel(host(c1), ref) < 1e-5
+    np.testing.assert_array_equal(host(c1), host(c2))   # deterministic
+    c16 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.bfloat16, R=dev(R, torch.bfloat16), alpha=0.5)
+    assert rel(host(c16), 0.5 * ref + R) < 4e-3
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    cb = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32, R=Rd, alpha=0.25, beta=-1.5, C0=dev(C0))
+    assert rel(host(cb), 0.25 * ref - 1.5 * C0 + R) < 1e-5
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0)])
 def test_gemm_fp32_matches_oracle(orc, ta, tb):
     rng = np.random.default_rng(10 + ta + 2 * tb)

@@ -566,3 +566,139 @@ def test_lora_fwd_bwd_vs_float64(orc, Bt, S, inn, out, r):
     assert rel(dx, xt.grad.numpy()) < 1e-5
     assert rel(dA, At.grad.numpy()) < 1e-5
     assert rel(dB, Bt_.grad.numpy()) < 1e-5
+
+
+# --------------------------------------------------------------------------- tensor primitives
+def test_ops_reference_known_answers(orc):
+    # tests/unit/test_ops.cpp:12-131
+    a, b = np.full((2, 3), 4.0, np.float32), np.full((2, 3), 2.0, np.float32)
+    for op, v in (("add", 6), ("sub", 2), ("mul", 8), ("div", 2)):
+        assert np.all(orc.binary(op, a, b) == v)
+    np.testing.assert_array_equal(orc.binary("add", np.arange(6, dtype=np.float32).reshape(2, 3),
+                                             np.full((1, 3), 10.0, np.float32)),
+                                  np.arange(10, 16, dtype=np.float32).reshape(2, 3))
+    a5 = np.full((2, 2), 5.0, np.float32)                           # scalar operands are [1] tensors
+    for op, sc, v in (("add", 3, 8), ("sub", 2, 3), ("div", 2, 2.5)):
+        assert np.all(orc.binary(op, a5, np.full((1,), sc, np.float32)) == v)
+    assert np.all(orc.binary("mul", np.full((1,), 2.0, np.float32), a5) == 10)
+    x = np.arange(-2, 3, dtype=np.float32)
+    assert orc.unary("sigmoid", x)[2] == 0.5 and orc.unary("tanh", x)[2] == 0
+    assert orc.unary("gelu", x)[2] == 0 and orc.unary("silu", x)[2] == 0 and orc.unary("exp", np.zeros(1, np.float32))[0] == 1
+    r = np.arange(1, 6, dtype=np.float32)
+    assert [orc.reduce_all(op, r) for op in ("sum", "mean", "max", "min")] == [15, 3, 5, 1]
+    m = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    np.testing.assert_array_equal(orc.reduce_dim("sum", m, 0), [5, 7, 9])
+    np.testing.assert_array_equal(orc.reduce_dim("sum", m, 1, keepdim=True), [[6], [15]])
+    np.testing.assert_array_equal(orc.reduce_dim("max", m, 1), [3, 6])
+
+
+def test_shape_and_view_known_answers(orc):
+    # tests/unit/test_shape.cpp:49-72 and tests/unit/test_tensor.cpp:45-69, 88-98
+    assert orc.broadcast_shape((2, 1, 4), (3, 4)) == (2, 3, 4)
+    with pytest.raises(ValueError):
+        orc.broadcast_shape((2, 3, 4), (5, 4))
+    t = orc.strided_copy(np.arange(6, dtype=np.float32), 0, [3, 2], [1, 3])   # transpose(0, 1) of [2, 3]
+    np.testing.assert_array_equal(t.ravel(), [0, 3, 1, 4, 2, 5])
+    f16 = orc.cast(np.arange(4, dtype=np.float32), "f16")
+    np.testing.assert_array_equal(orc.cast(f16.view(np.float16), "f32"), np.arange(4, dtype=np.float32))
+
+
+def test_binary_broadcast_and_strided_views_vs_numpy(orc):
+    rng = np.random.default_rng(1)
+    for sa, sb in [((4, 1, 5), (3, 1)), ((2, 3, 4), (4,)), ((1,), (7, 6)), ((5, 1), (1, 6)), ((2, 3), (2, 3))]:
+        a = rng.standard_normal(sa).astype(np.float32)
+        b = (rng.standard_normal(sb) + 3).astype(np.float32)
+        for op, f in (("add", np.add), ("sub", np.subtract), ("mul", np.multiply), ("div", np.divide)):
+            np.testing.assert_array_equal(orc.binary(op, a, b), f(a, b))
+    # non-contiguous views: a transposed [3, 4] view of a [4, 3] base with an offset, and a slice
+    base = rng.standard_normal(40).astype(np.float32)
+    va = (2, [3, 4], [1, 3])
+    ref_a = np.lib.stride_tricks.as_strided(base[2:], (3, 4), (4, 12))
+    vb = (5, [4], [2])
+    ref_b = base[5::2][:4]
+    np.testing.assert_array_equal(orc.binary("mul", base, base, va, vb), ref_a * ref_b)
+    np.testing.assert_array_equal(orc.strided_copy(base, 2, [3, 4], [1, 3]), ref_a)
+    # a 4-D permute
+    x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)
+    p = x.transpose(2, 0, 3, 1)
+    np.testing.assert_array_equal(orc.strided_copy(x.ravel(), 0, list(p.shape), [s // 4 for s in p.strides]), p)
+
+
+def test_unary_vs_float64(orc):
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(4000) * 3).astype(np.float32)
+    xd = x.astype(np.float64)
+    ref = {"neg": -xd, "abs": np.abs(xd), "exp": np.exp(xd), "tanh": np.tanh(xd), "sigmoid": 1 / (1 + np.exp(-xd)),
+           "gelu": 0.5 * xd * (1 + np.tanh(np.sqrt(2 / np.pi) * (xd + 0.044715 * xd ** 3))),
+           "silu": xd / (1 + np.exp(-xd))}
+    for op, r in ref.items():
+        np.testing.assert_allclose(orc.unary(op, x), r, rtol=3e-6, atol=1e-6, err_msg=op)
+    xp = np.abs(x) + 1e-3
+    np.testing.assert_allclose(orc.unary("log", xp), np.log(xp.astype(np.float64)), rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(orc.unary("sqrt", xp), np.sqrt(xp))   # correctly rounded
+
+
+def test_reductions_vs_numpy(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((6, 50, 7)).astype(np.float32)
+    assert orc.reduce_all("sum", x) == np.float32(x.astype(np.float64).sum())
+    assert orc.reduce_all("mean", x) == np.float32(np.float32(x.astype(np.float64).sum()) / np.float32(x.size))
+    assert orc.reduce_all("max", x) == x.max() and orc.reduce_all("min", x) == x.min()
+    for d in range(3):
+        np.testing.assert_array_equal(orc.reduce_dim("sum", x, d), x.astype(np.float64).sum(d).astype(np.float32))
+        np.testing.assert_array_equal(orc.reduce_dim("mean", x, d), x.astype(np.float64).mean(d).astype(np.float32))
+        np.testing.assert_array_equal(orc.reduce_dim("max", x, d), x.max(d))
+        np.testing.assert_array_equal(orc.reduce_dim("min", x, d), x.min(d))
+    y = x.copy()
+    y[0, 0, 0] = np.nan                                                  # NaN never wins a comparison
+    assert orc.reduce_all("max", y) == np.nanmax(y)
+
+
+def test_cat_and_sum_to_shape_vs_numpy(orc):
+    rng = np.random.default_rng(4)
+    parts = [rng.standard_normal((2, k, 3)).astype(np.float32) for k in (1, 4, 2)]
+    for d in (0, 1, 2, -1):
+        ps = parts if d in (1,) else [rng.standard_normal((2, 3, 3)).astype(np.float32) for _ in range(3)]
+        np.testing.assert_array_equal(orc.cat(ps, d), np.concatenate(ps, d))
+    ids = [np.arange(5, dtype=np.int64), np.arange(3, dtype=np.int64)]
+    np.testing.assert_array_equal(orc.cat(ids, 0), np.concatenate(ids))
+    g = rng.standard_normal((4, 2, 3, 5)).astype(np.float32)
+    for target in [(3, 5), (1, 5), (3, 1), (2, 1, 5), (1, 1), ()]:
+        tgt = target if target else ()
+        ref = g.astype(np.float64)
+        lead = g.ndim - len(tgt)
+        ref = ref.sum(tuple(range(lead))) if lead else ref
+        for i, t in enumerate(tgt):
+            if t == 1 and ref.shape[i] > 1:
+                ref = ref.sum(i, keepdims=True)
+        np.testing.assert_allclose(orc.sum_to_shape(g, tgt), ref.astype(np.float32).reshape(tgt), rtol=1e-6, atol=1e-6)
+
+
+def test_casts_vs_numpy_and_torch(orc):
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 3000),
+                        np.array([0.0, -0.0, 65504, 65519, 65520, 1e9, -1e9, 2.0 ** -25, 2.0 ** -24 * 1.5,
+                                  np.inf, -np.inf], np.float32)]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        np.testing.assert_array_equal(orc.cast(x, "f16"), x.astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(orc.cast(x, "bf16"), torch.from_numpy(x).to(torch.bfloat16).view(torch.int16)
+                                  .numpy().view(np.uint16))
+    nan = np.array([np.nan, -np.nan], np.float32)
+    assert orc.cast(nan, "bf16").tolist() == [0x7FC0, 0xFFC0]          # the reference's canonical NaN
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)            # every f16 bit pattern
+    fin = np.isfinite(h.view(np.float16))
+    np.testing.assert_array_equal(orc.cast(h, "f32")[fin], h.view(np.float16)[fin].astype(np.float32))
+    hb = h[~fin].astype(np.uint32)                                      # inf / NaN keep their payload
+    np.testing.assert_array_equal(orc.cast(h[~fin], "f32").view(np.uint32),
+                                  ((hb & 0x8000) << 16) | 0x7F800000 | ((hb & 0x3FF) << 13))
+    bb = np.arange(0, 65536, 7, dtype=np.uint32).astype(np.uint16)
+    np.testing.assert_array_equal(orc.cast(bb, "f32", bf16_from=True).view(np.uint32), bb.astype(np.uint32) << 16)
+    xi = (rng.standard_normal(1000) * 1e4).astype(np.float32)
+    np.testing.assert_array_equal(orc.cast(xi, "i64"), xi.astype(np.int64))    # truncation toward zero
+    np.testing.assert_array_equal(orc.cast(xi, "i32"), xi.astype(np.int32))
+    iv = rng.integers(-2 ** 40, 2 ** 40, 1000)
+    np.testing.assert_array_equal(orc.cast(iv, "f32"), iv.astype(np.float32))
+    np.testing.assert_array_equal(orc.cast(iv, "i32"), iv.astype(np.int32))
+    np.testing.assert_array_equal(orc.cast(iv.astype(np.int32), "i64"), iv.astype(np.int32).astype(np.int64))
+    with pytest.raises(NotImplementedError):
+        orc.cast(h, "bf16")                                            # f16 -> bf16 is not in the table
