@@ -788,8 +788,7 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
     AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31) && ((S + 127) / 128) * H * B < (1LL << 31), InvalidArgument,
               "attn_bwd: sequence too long");
     if (B == 0 || S == 0) return;
-    DeviceBuffer Dbuf(sizeof(float) * B * H * S, s);
-    float* D = Dbuf.as<float>();
+    float* D = static_cast<float*>(stream_scratch(sizeof(float) * B * H * S, s));
     const int64_t waves = B * S * H;
     const unsigned dgrid = static_cast<unsigned>((waves * 64 + 255) / 256);
     if (dt == DType::BFloat16)

@@ -39,7 +39,8 @@ constexpr int kSortMax = 16384;  // tokens per step sortable in one block's LDS 
 
 // Bitonic sort of keys (id << 32 | position); ids outside [0, V) sort last.
 __global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__ ids, int N, int64_t V,
-                                                     int* __restrict__ sorted_pos, int* __restrict__ sorted_id) {
+                                                     int* __restrict__ sorted_pos, int* __restrict__ sorted_id,
+                                                     int* __restrict__ run_start, int* __restrict__ nruns) {
     extern __shared__ unsigned long long key[];
     int P = 1;
     while (P < N) P <<= 1;
@@ -74,6 +75,92 @@ __global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__
         sorted_pos[i] = static_cast<int>(k & 0xffffffffull);
         const int id = static_cast<int>(k >> 32);
         sorted_id[i] = id;
+    }
+    if (!run_start) return;
+    // Compact the starts of the runs of equal in-range ids: thread t owns sorted positions
+    // [t * per, (t + 1) * per); an exclusive scan of the per-thread counts gives the offsets.
+    __shared__ int cnt[1024];
+    const int per = (N + blockDim.x - 1) / blockDim.x;
+    const int b0 = threadIdx.x * per, b1 = min(N, b0 + per);
+    auto is_start = [&](int i) {
+        const unsigned long long id = key[i] >> 32;
+        return id < static_cast<unsigned long long>(V) && (i == 0 || (key[i - 1] >> 32) != id);
+    };
+    int c = 0;
+    for (int i = b0; i < b1; ++i) c += is_start(i);
+    cnt[threadIdx.x] = c;
+    __syncthreads();
+    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {  // inclusive Hillis-Steele scan
+        const int v = threadIdx.x >= static_cast<unsigned>(off) ? cnt[threadIdx.x - off] : 0;
+        __syncthreads();
+        cnt[threadIdx.x] += v;
+        __syncthreads();
+    }
+    int o = cnt[threadIdx.x] - c;
+    for (int i = b0; i < b1; ++i)
+        if (is_start(i)) run_start[o++] = i;
+    if (threadIdx.x == blockDim.x - 1) *nruns = cnt[threadIdx.x];
+}
+
+// One block of 16 waves per (run of equal ids, chunk of 8 * 64 columns), grid-striding over
+// all of them.  Wave w adds the rows of tokens p + w, p + w + 16, ... in order, eight rows'
+// 16-byte loads in flight at a time; the 16 partial sums are then added in wave order, so the
+// result is the same on every run.
+template <typename T>
+__global__ __launch_bounds__(1024) void embed_run_k(const int* __restrict__ sorted_pos, const int* __restrict__ sorted_id,
+                                                    const int* __restrict__ run_start, const int* __restrict__ nruns,
+                                                    int N, const T* __restrict__ dout, int64_t D,
+                                                    float* __restrict__ dW, int accumulate) {
+    constexpr int VE = 16 / sizeof(T);  // elements per 16-byte load
+    constexpr int U = 8;
+    __shared__ float part[16][64 * VE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunks = static_cast<int>(D / (64 * VE));
+    const int items = *nruns * chunks;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int r = it / chunks, ch = it % chunks;
+        const int p = run_start[r], id = sorted_id[p];
+        int end = r + 1 < *nruns ? run_start[r + 1] : N;
+        while (end > p + 1 && sorted_id[end - 1] != id) --end;  // trailing out-of-range ids
+        const int64_t col = static_cast<int64_t>(ch) * 64 * VE + lane * VE;
+        float acc[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[e] = 0.0f;
+        for (int q0 = p + wave; q0 < end; q0 += 16 * U) {
+            uint4 raw[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int q = q0 + 16 * u;
+                raw[u] = q < end ? *reinterpret_cast<const uint4*>(dout + static_cast<int64_t>(sorted_pos[q]) * D + col)
+                                 : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (q0 + 16 * u >= end) break;
+                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+                if constexpr (sizeof(T) == 2) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        acc[2 * k] += __uint_as_float(w[k] << 16);
+                        acc[2 * k + 1] += __uint_as_float(w[k] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[k] += __uint_as_float(w[k]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < VE; ++e) part[wave][lane * VE + e] = acc[e];
+        __syncthreads();
+        if (threadIdx.x < 64 * VE) {
+            float sum = part[0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < 16; ++w) sum += part[w][threadIdx.x];
+            float* o = dW + static_cast<int64_t>(id) * D + static_cast<int64_t>(ch) * 64 * VE + threadIdx.x;
+            *o = accumulate ? *o + sum : sum;
+        }
+        __syncthreads();
     }
 }
 
@@ -139,18 +226,33 @@ void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64
     AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "embed_bwd: dtype must be f32 or bf16");
     if (!accumulate) AIC_HIP_CHECK(hipMemsetAsync(dW, 0, sizeof(float) * V * D, s));
     if (N == 0) return;
-    DeviceBuffer buf(sizeof(int) * 2 * N, s);
-    int* spos = buf.as<int>();
+    const size_t es = dtype_size(dt);
+    const bool runs = (D * static_cast<int64_t>(es)) % (64 * 16) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15u) == 0;
+    int* spos = static_cast<int*>(stream_scratch(sizeof(int) * (3 * N + 1), s));
     int* sid = spos + N;
+    int* rstart = sid + N;
+    int* nruns = rstart + N;
     int P = 1;
     while (P < N) P <<= 1;
     const size_t lds = sizeof(unsigned long long) * P;
     if (lds > 65536)
         AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&embed_sort_k),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    hipLaunchKernelGGL(embed_sort_k, dim3(1), dim3(1024), lds, s, ids,
-                       static_cast<int>(N), V, spos, sid);
+    hipLaunchKernelGGL(embed_sort_k, dim3(1), dim3(1024), lds, s, ids, static_cast<int>(N), V, spos, sid,
+                       runs ? rstart : nullptr, nruns);
     AIC_LAUNCH_CHECK("embed_sort");
+    if (runs) {
+        // one block of 16 waves per (run, 8 * 64-column chunk), at most 2048 blocks striding
+        const unsigned g = static_cast<unsigned>(std::min<int64_t>(2048, N * (D * static_cast<int64_t>(es) / 1024)));
+        if (dt == DType::Float32)
+            hipLaunchKernelGGL(embed_run_k<float>, dim3(g), dim3(1024), 0, s, spos, sid, rstart, nruns,
+                               static_cast<int>(N), static_cast<const float*>(dout), D, dW, accumulate ? 1 : 0);
+        else
+            hipLaunchKernelGGL(embed_run_k<bf16>, dim3(g), dim3(1024), 0, s, spos, sid, rstart, nruns,
+                               static_cast<int>(N), static_cast<const bf16*>(dout), D, dW, accumulate ? 1 : 0);
+        AIC_LAUNCH_CHECK("embed_run");
+        return;
+    }
     const unsigned gy = static_cast<unsigned>(std::min<int64_t>((D + 63) / 64, 32));
     if (dt == DType::Float32)
         hipLaunchKernelGGL(embed_seg_k<float>, dim3(static_cast<unsigned>(N), gy), dim3(256), 0, s, spos, sid,

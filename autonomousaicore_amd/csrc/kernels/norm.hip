@@ -79,6 +79,47 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_k(const T* __restrict__ x, in
     }
 }
 
+// Register-resident forms for dim <= 64 * VN * CH: a lane holds its CH chunks of the row, so
+// all of a row's loads are in flight at once and the row is read once.  Same arithmetic, in
+// the same order, as the loop forms above and below (results are bit-identical).
+template <typename T, int VN, int CH>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_r(const T* __restrict__ x, int64_t ldx, const float* __restrict__ w,
+                                                     T* __restrict__ y, int64_t ldy, float* __restrict__ rms,
+                                                     int64_t rows, int dim, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T* xr = x + row * ldx;
+    float v[CH][VN];
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+        const int c = (t * 64 + lane) * VN;
+        if (c < dim) load_vec<T, VN>(xr + c, v[t]);
+        else
+#pragma unroll
+            for (int i = 0; i < VN; ++i) v[t][i] = 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < CH; ++t)
+#pragma unroll
+        for (int i = 0; i < VN; ++i) ss += v[t][i] * v[t][i];
+    ss = wave_sum(ss);
+    const float r = sqrtf(ss / static_cast<float>(dim) + eps);
+    const float inv = 1.0f / r;
+    if (lane == 0 && rms) rms[row] = r;
+    T* yr = y + row * ldy;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+        const int c = (t * 64 + lane) * VN;
+        if (c >= dim) continue;
+        float o[VN];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) o[i] = (v[t][i] * inv) * w[c + i];
+        store_vec<T, VN>(yr + c, o);
+    }
+}
+
 constexpr int kBwdRowsPerWave = 4;
 
 // dx and per-block dw partials.  Block = 4 waves; wave w handles rows
@@ -139,6 +180,127 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_k(const T* __restrict__ dy, i
 
 // dw[j] = sum over partial rows b of part[b][j], in a fixed order: block = 64 columns x 16
 // waves, wave w sums rows w, w+16, ...; the 16 wave sums are then added in wave order.
+// Register-resident backward: wave w of block b handles rows (4b + w) * R .. +R-1 (R = 2, so
+// twice as many waves are in flight as in the loop form); the lane's
+// dw contributions accumulate in registers over its rows, then the four waves' sums are
+// added in wave order, as the loop form does through LDS.
+constexpr int kBwdRegRowsPerWave = 2;
+
+template <typename T, int VN, int CH>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_r(const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x,
+                                                     int64_t ldx, const float* __restrict__ w,
+                                                     const float* __restrict__ rms, const T* dres, int64_t ldres,
+                                                     T* dx, int64_t lddx, float* __restrict__ part, int64_t rows,
+                                                     int dim) {
+    extern __shared__ float sdw[];  // [4][dim] when part != nullptr
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float wv[CH][VN], dwa[CH][VN];
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+        const int c = (t * 64 + lane) * VN;
+#pragma unroll
+        for (int i = 0; i < VN; ++i) {
+            wv[t][i] = c < dim ? w[c + i] : 0.0f;
+            dwa[t][i] = 0.0f;
+        }
+    }
+    for (int rr = 0; rr < kBwdRegRowsPerWave; ++rr) {
+        const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kBwdRegRowsPerWave + rr;
+        if (row >= rows) break;
+        const T* gr = dy + row * lddy;
+        const T* xr = x + row * ldx;
+        float gv[CH][VN], xv[CH][VN], rv[CH][VN];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            const int c = (t * 64 + lane) * VN;
+            if (c < dim) {
+                load_vec<T, VN>(gr + c, gv[t]);
+                load_vec<T, VN>(xr + c, xv[t]);
+                if (dres) load_vec<T, VN>(dres + row * ldres + c, rv[t]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < VN; ++i) gv[t][i] = xv[t][i] = rv[t][i] = 0.0f;
+            }
+        }
+        const float r = rms[row];
+        const float inv = 1.0f / r;
+        float dot = 0.0f;
+#pragma unroll
+        for (int t = 0; t < CH; ++t)
+#pragma unroll
+            for (int i = 0; i < VN; ++i) dot += (gv[t][i] * wv[t][i]) * xv[t][i];
+        dot = wave_sum(dot);
+        const float coef = dot / (static_cast<float>(dim) * r * r * r);
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            const int c = (t * 64 + lane) * VN;
+            if (c >= dim) continue;
+            float o[VN];
+#pragma unroll
+            for (int i = 0; i < VN; ++i) {
+                const float g = (gv[t][i] * wv[t][i]) * inv - xv[t][i] * coef;
+                o[i] = dres ? rv[t][i] + g : g;
+                if (part) dwa[t][i] += gv[t][i] * (xv[t][i] * inv);
+            }
+            store_vec<T, VN>(dx + row * lddx + c, o);
+        }
+    }
+    if (!part) return;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+        const int c = (t * 64 + lane) * VN;
+        if (c < dim)
+#pragma unroll
+            for (int i = 0; i < VN; ++i) sdw[wave * dim + c + i] = dwa[t][i];
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < dim; j += 256)
+        part[static_cast<int64_t>(blockIdx.x) * dim + j] = ((sdw[j] + sdw[dim + j]) + sdw[2 * dim + j]) + sdw[3 * dim + j];
+}
+
+// dw = sum of the per-block partials, 8 columns per block so the whole chip takes part: thread t
+// adds partials t, t + 256, ... of its column pair in order, then a fixed-order block tree.
+__global__ __launch_bounds__(256) void reduce_parts8_k(const float* __restrict__ part, int nparts, int dim,
+                                                       float* dw, int accumulate) {
+    __shared__ float red[256][9];
+    const int c0 = blockIdx.x * 8;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    // four partial rows' loads in flight per thread, added in order
+    for (int b0 = threadIdx.x; b0 < nparts; b0 += 4 * 256) {
+        float4 u[4], v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int b = b0 + k * 256;
+            if (b < nparts) {
+                u[k] = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(b) * dim + c0);
+                v[k] = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(b) * dim + c0 + 4);
+            } else {
+                u[k] = v[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc[0] += u[k].x; acc[1] += u[k].y; acc[2] += u[k].z; acc[3] += u[k].w;
+            acc[4] += v[k].x; acc[5] += v[k].y; acc[6] += v[k].z; acc[7] += v[k].w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) red[threadIdx.x][i] = acc[i];
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (threadIdx.x < h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red[threadIdx.x][i] += red[threadIdx.x + h][i];
+        __syncthreads();
+    }
+    if (threadIdx.x < 8) {
+        const int j = c0 + threadIdx.x;
+        dw[j] = accumulate ? dw[j] + red[0][threadIdx.x] : red[0][threadIdx.x];
+    }
+}
+
 __global__ __launch_bounds__(1024) void reduce_parts_k(const float* __restrict__ part, int nparts, int dim, float* dw,
                                                        int accumulate) {
     __shared__ float red[16][64];
@@ -157,6 +319,15 @@ __global__ __launch_bounds__(1024) void reduce_parts_k(const float* __restrict__
     }
 }
 
+// Chunks of vn elements per lane for a row of dim, rounded up to a power of two (0: too long
+// for the register forms).
+int chunks_for(int64_t dim, int vn) {
+    const int64_t need = (dim + 64 * vn - 1) / (64 * vn);
+    for (int c = 1; c <= 8; c *= 2)
+        if (need <= c) return c;
+    return 0;
+}
+
 bool vec_ok(const void* p, int64_t ld, int64_t dim, int vn, size_t es) {
     return (reinterpret_cast<uintptr_t>(p) % (vn * es)) == 0 && ld % vn == 0 && dim % vn == 0;
 }
@@ -166,7 +337,17 @@ void fwd_t(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, flo
            float eps, hipStream_t s) {
     constexpr int VN = Vec<T>::N;
     const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
-    if (vec_ok(x, ldx, dim, VN, sizeof(T)) && vec_ok(y, ldy, dim, VN, sizeof(T)))
+    const int ch = chunks_for(dim, VN);
+    const bool vec = vec_ok(x, ldx, dim, VN, sizeof(T)) && vec_ok(y, ldy, dim, VN, sizeof(T));
+#define AIC_FWD_R(CH)                                                                                            \
+    hipLaunchKernelGGL((rmsnorm_fwd_r<T, VN, CH>), dim3(grid), dim3(256), 0, s, static_cast<const T*>(x), ldx, w, \
+                       static_cast<T*>(y), ldy, rms, rows, static_cast<int>(dim), eps)
+    if (vec && ch == 1) AIC_FWD_R(1);
+    else if (vec && ch == 2) AIC_FWD_R(2);
+    else if (vec && ch == 4) AIC_FWD_R(4);
+    else if (vec && ch == 8) AIC_FWD_R(8);
+#undef AIC_FWD_R
+    else if (vec)
         hipLaunchKernelGGL((rmsnorm_fwd_k<T, VN>), dim3(grid), dim3(256), 0, s, static_cast<const T*>(x), ldx, w,
                            static_cast<T*>(y), ldy, rms, rows, static_cast<int>(dim), eps);
     else
@@ -180,15 +361,26 @@ void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float
            const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
            int64_t dim, hipStream_t s) {
     constexpr int VN = Vec<T>::N;
-    const int64_t rows_per_block = 4 * kBwdRowsPerWave;
-    const unsigned grid = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
-    float* part = nullptr;
-    if (dw) part = static_cast<float*>(pool_alloc(sizeof(float) * grid * dim, s));
-    const size_t lds = dw ? sizeof(float) * 4 * dim : 0;
-    AIC_CHECK(lds <= 160 * 1024, InvalidArgument, "rmsnorm_bwd: dim too large for the LDS weight-gradient slices");
     const bool vec = vec_ok(dy, lddy, dim, VN, sizeof(T)) && vec_ok(x, ldx, dim, VN, sizeof(T)) &&
                      vec_ok(dx, lddx, dim, VN, sizeof(T)) && (!dres || vec_ok(dres, ldres, dim, VN, sizeof(T)));
-    if (vec)
+    const int ch = chunks_for(dim, VN);
+    const bool reg = vec && ch > 0;
+    const int64_t rows_per_block = 4 * (reg ? kBwdRegRowsPerWave : kBwdRowsPerWave);
+    const unsigned grid = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
+    float* part = nullptr;
+    if (dw) part = static_cast<float*>(stream_scratch(sizeof(float) * grid * dim, s));
+    const size_t lds = dw ? sizeof(float) * 4 * dim : 0;
+    AIC_CHECK(lds <= 160 * 1024, InvalidArgument, "rmsnorm_bwd: dim too large for the LDS weight-gradient slices");
+#define AIC_BWD_R(CH)                                                                                         \
+    hipLaunchKernelGGL((rmsnorm_bwd_r<T, VN, CH>), dim3(grid), dim3(256), lds, s, static_cast<const T*>(dy), \
+                       lddy, static_cast<const T*>(x), ldx, w, rms, static_cast<const T*>(dres), ldres,        \
+                       static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim))
+    if (vec && ch == 1) AIC_BWD_R(1);
+    else if (vec && ch == 2) AIC_BWD_R(2);
+    else if (vec && ch == 4) AIC_BWD_R(4);
+    else if (vec && ch == 8) AIC_BWD_R(8);
+#undef AIC_BWD_R
+    else if (vec)
         hipLaunchKernelGGL((rmsnorm_bwd_k<T, VN>), dim3(grid), dim3(256), lds, s, static_cast<const T*>(dy), lddy,
                            static_cast<const T*>(x), ldx, w, rms, static_cast<const T*>(dres), ldres,
                            static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
@@ -198,10 +390,13 @@ void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float
                            static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
     AIC_LAUNCH_CHECK("rmsnorm_bwd");
     if (dw) {
-        hipLaunchKernelGGL(reduce_parts_k, dim3(static_cast<unsigned>((dim + 63) / 64)), dim3(1024), 0, s, part,
-                           static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
+        if (dim % 8 == 0)
+            hipLaunchKernelGGL(reduce_parts8_k, dim3(static_cast<unsigned>(dim / 8)), dim3(256), 0, s, part,
+                               static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
+        else
+            hipLaunchKernelGGL(reduce_parts_k, dim3(static_cast<unsigned>((dim + 63) / 64)), dim3(1024), 0, s, part,
+                               static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
         AIC_LAUNCH_CHECK("rmsnorm_bwd reduce");
-        pool_free(part, s);
     }
 }
 

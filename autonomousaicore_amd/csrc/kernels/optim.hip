@@ -145,34 +145,45 @@ __global__ __launch_bounds__(256) void adamw_k(float* __restrict__ p, const floa
                      (!BF16COPY || (reinterpret_cast<uintptr_t>(pb) & 7u) == 0);
     const int64_t n4 = vec ? n / 4 : 0;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 pp = reinterpret_cast<float4*>(p)[i];
-        const float4 gg = reinterpret_cast<const float4*>(g)[i];
-        float4 mm = reinterpret_cast<float4*>(m)[i];
-        float4 vv = reinterpret_cast<float4*>(v)[i];
-        float* pa = &pp.x;
-        const float* ga = &gg.x;
-        float* ma = &mm.x;
-        float* va = &vv.x;
+    // Streaming pass: two float4 groups per thread per iteration (8 loads in flight), all
+    // accesses non-temporal, since nothing here is read again before the next step.
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * 2 + threadIdx.x; base < n4; base += 2 * stride) {
+        f32x4 pp[2], gg[2], mm[2], vv[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float gr = ga[j] * mult;
-            float par = pa[j];
-            par -= lrwd * par;
-            const float m1 = beta1 * ma[j] + ob1 * gr;
-            const float v1 = beta2 * va[j] + ob2 * gr * gr;
-            ma[j] = m1;
-            va[j] = v1;
-            par -= lr * ((m1 / bc1) / (sqrtf(v1 / bc2) + eps));
-            pa[j] = par;
+        for (int u = 0; u < 2; ++u) {
+            const int64_t i = base + u * blockDim.x;
+            if (i < n4) {
+                pp[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + i);
+                gg[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g) + i);
+                mm[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(m) + i);
+                vv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(v) + i);
+            }
         }
-        reinterpret_cast<float4*>(p)[i] = pp;
-        reinterpret_cast<float4*>(m)[i] = mm;
-        reinterpret_cast<float4*>(v)[i] = vv;
-        if (BF16COPY) {
-            const uint32_t w0 = static_cast<uint32_t>(f2bf_bits(pp.x)) | (static_cast<uint32_t>(f2bf_bits(pp.y)) << 16);
-            const uint32_t w1 = static_cast<uint32_t>(f2bf_bits(pp.z)) | (static_cast<uint32_t>(f2bf_bits(pp.w)) << 16);
-            reinterpret_cast<uint2*>(pb)[i] = make_uint2(w0, w1);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t i = base + u * blockDim.x;
+            if (i >= n4) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float gr = gg[u][j] * mult;
+                float par = pp[u][j];
+                par -= lrwd * par;
+                const float m1 = beta1 * mm[u][j] + ob1 * gr;
+                const float v1 = beta2 * vv[u][j] + ob2 * gr * gr;
+                mm[u][j] = m1;
+                vv[u][j] = v1;
+                par -= lr * ((m1 / bc1) / (sqrtf(v1 / bc2) + eps));
+                pp[u][j] = par;
+            }
+            __builtin_nontemporal_store(pp[u], reinterpret_cast<f32x4*>(p) + i);
+            __builtin_nontemporal_store(mm[u], reinterpret_cast<f32x4*>(m) + i);
+            __builtin_nontemporal_store(vv[u], reinterpret_cast<f32x4*>(v) + i);
+            if (BF16COPY) {
+                u32x2 w;
+                w[0] = static_cast<uint32_t>(f2bf_bits(pp[u][0])) | (static_cast<uint32_t>(f2bf_bits(pp[u][1])) << 16);
+                w[1] = static_cast<uint32_t>(f2bf_bits(pp[u][2])) | (static_cast<uint32_t>(f2bf_bits(pp[u][3])) << 16);
+                __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(pb) + i);
+            }
         }
     }
     for (int64_t i = n4 * 4 + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -234,8 +245,8 @@ void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int coun
         blocks[t] = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nb, kNormBlocks)));
         total_blocks += blocks[t];
     }
-    DeviceBuffer part(sizeof(double) * std::max(total_blocks, 1) + sizeof(int) * std::max(total_blocks, 1), s);
-    double* pd = part.as<double>();
+    double* pd = static_cast<double*>(
+        stream_scratch(sizeof(double) * std::max(total_blocks, 1) + sizeof(int) * std::max(total_blocks, 1), s));
     int* pn = reinterpret_cast<int*>(pd + std::max(total_blocks, 1));
     int off = 0;
     for (int t = 0; t < count; ++t) {
@@ -267,7 +278,7 @@ void adamw_multi(float* const* p, const float* const* g, float* const* m, float*
     AIC_CHECK(ctl || step > 0, InvalidArgument, "adamw_multi: step must be >= 1 without a control block");
     for (int t = 0; t < count; ++t) {
         if (sizes[t] == 0) continue;
-        const unsigned grid = grid_for((sizes[t] + 3) / 4, 256, 16384);
+        const unsigned grid = grid_for((sizes[t] + 7) / 8, 256, 262144);
         const auto* c = static_cast<const aic_optim_ctl*>(ctl);
         bf16* pb = p_bf16 ? static_cast<bf16*>(p_bf16[t]) : nullptr;
         if (pb)
@@ -285,7 +296,7 @@ void adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float l
     AIC_CHECK(n >= 0 && (n == 0 || (p && g && m && v)), InvalidArgument, "adamw_step: bad arguments");
     AIC_CHECK(bc1 > 0.0f && bc2 > 0.0f, InvalidArgument, "adamw_step: bias corrections must be positive");
     if (n == 0) return;
-    const unsigned grid = grid_for((n + 3) / 4, 256, 16384);
+    const unsigned grid = grid_for((n + 7) / 8, 256, 262144);
     hipLaunchKernelGGL(adamw_k<false>, dim3(grid), dim3(256), 0, s, p, g, m, v, nullptr, n, lr, beta1, beta2, eps, wd,
                        int64_t{0}, bc1, bc2, nullptr);
     AIC_LAUNCH_CHECK("adamw_step");

@@ -423,10 +423,9 @@ void reduce_all(int op, const float* x, int64_t n, float* out, hipStream_t s) {
     if (parts < 1) parts = 1;
     if (parts > 1024) parts = 1024;
     const int64_t chunk = (n + parts - 1) / parts;
-    DeviceBuffer part(sizeof(Acc) * static_cast<size_t>(parts), s);
-    hipLaunchKernelGGL(reduce_part_k, dim3(static_cast<unsigned>(parts)), dim3(256), 0, s, op, x, n, chunk,
-                       part.as<Acc>());
-    hipLaunchKernelGGL(reduce_final_k, dim3(1), dim3(256), 0, s, op, part.as<Acc>(), static_cast<int>(parts), n, out);
+    Acc* part = static_cast<Acc*>(stream_scratch(sizeof(Acc) * static_cast<size_t>(parts), s));
+    hipLaunchKernelGGL(reduce_part_k, dim3(static_cast<unsigned>(parts)), dim3(256), 0, s, op, x, n, chunk, part);
+    hipLaunchKernelGGL(reduce_final_k, dim3(1), dim3(256), 0, s, op, part, static_cast<int>(parts), n, out);
     AIC_LAUNCH_CHECK("reduce_all");
 }
 

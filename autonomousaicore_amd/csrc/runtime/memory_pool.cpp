@@ -1,6 +1,8 @@
 #include "memory_pool.hpp"
 
 #include <atomic>
+#include <map>
+#include <tuple>
 #include <cstdint>
 #include <mutex>
 #include <unordered_map>
@@ -66,6 +68,29 @@ void pool_free(void* ptr, hipStream_t stream) {
 MemoryStats pool_stats() {
     std::lock_guard<std::mutex> lk(g_mu);
     return g_stats;
+}
+
+void* stream_scratch(size_t bytes, hipStream_t stream, int slot) {
+    struct Entry {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    static std::mutex mu;
+    static std::map<std::tuple<int, hipStream_t, int>, Entry> cache;
+    if (bytes == 0) return nullptr;
+    int dev = 0;
+    AIC_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(mu);
+    Entry& e = cache[std::make_tuple(dev, stream, slot)];
+    if (e.bytes < bytes) {
+        if (e.ptr) pool_free(e.ptr, stream);  // stream-ordered: earlier launches finish first
+        e.ptr = nullptr;
+        e.bytes = 0;
+        const size_t grow = bytes + bytes / 4;  // headroom so slowly growing sizes do not churn
+        e.ptr = pool_alloc(grow, stream);
+        e.bytes = grow;
+    }
+    return e.ptr;
 }
 
 void DeviceBuffer::reset() noexcept {

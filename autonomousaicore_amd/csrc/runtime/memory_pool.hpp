@@ -61,4 +61,12 @@ private:
     hipStream_t stream_ = nullptr;
 };
 
+// Scratch memory owned by the library, one growing buffer per (device, stream, slot): work
+// on one stream runs in order, so a kernel's scratch can be reused by the next call on the
+// same stream without a free and a new allocation (each of which costs a few microseconds of
+// stream time).  The pointer stays valid until the next call with the same key asks for more
+// bytes; callers use it only for the duration of their own launches.  Slots let one call hold
+// several buffers at once.
+void* stream_scratch(size_t bytes, hipStream_t stream, int slot = 0);
+
 }  // namespace aic

@@ -221,9 +221,11 @@ def test_cross_entropy(orc, dt, N, Cn):
 
 # ----------------------------------------------------------------------------- embedding
 @pytest.mark.parametrize("dt", [F32, BF16])
-def test_embedding_gather_bit_exact_and_scatter(orc, dt):
-    rng = np.random.default_rng(31)
-    V, D, N = 1000, 136, 4096
+@pytest.mark.parametrize("V,D,N", [(1000, 136, 4096), (1500, 1024, 8192), (32000, 2048, 2048)])
+def test_embedding_gather_bit_exact_and_scatter(orc, dt, V, D, N):
+    # D = 136: the per-column path; D * element size a multiple of 1 KB: the run-list path (the
+    # 1B shape among them), Zipf ids so one id repeats hundreds of times
+    rng = np.random.default_rng(31 + D)
     W = rng.standard_normal((V, D)).astype(np.float32)
     if dt == BF16:
         W = bf16_round(W)
