@@ -30,7 +30,8 @@ class OptimCtl(C.Structure):
 
 class LMConfig(C.Structure):
     _fields_ = [("vocab", i64), ("d_model", i64), ("n_layers", i64), ("n_heads", i64), ("d_ffn", i64),
-                ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32)]
+                ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32),
+                ("n_experts", i64), ("top_k", i64), ("aux_loss_coef", f32)]
 
 
 class TrainConfig(C.Structure):
@@ -45,7 +46,8 @@ class KernelStat(C.Structure):
 
 
 class StepStats(C.Structure):
-    _fields_ = [("loss", f32), ("grad_norm", f32), ("found_inf", i32), ("loss_scale", f32), ("step", i64)]
+    _fields_ = [("loss", f32), ("grad_norm", f32), ("found_inf", i32), ("loss_scale", f32), ("step", i64),
+                ("aux_loss", f32)]
 
 
 # name -> (restype, argtypes)

@@ -287,6 +287,9 @@ int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm
         c.rope_theta = cfg->rope_base;
         c.tie_word_embeddings = cfg->tied != 0;
         c.compute = dt(cfg->compute);
+        c.num_experts = cfg->n_experts;
+        c.top_k = cfg->top_k;
+        c.aux_loss_coef = cfg->aux_loss_coef;
         aic::models::TrainOptions o;
         o.adamw = {tcfg->lr, tcfg->beta1, tcfg->beta2, tcfg->eps, tcfg->weight_decay};
         o.max_grad_norm = tcfg->max_grad_norm;
@@ -375,6 +378,7 @@ void fill_stats(const aic::models::StepStats& s, aic_step_stats* out) {
     out->found_inf = s.found_inf ? 1 : 0;
     out->loss_scale = s.loss_scale;
     out->step = s.step;
+    out->aux_loss = s.aux_loss;
 }
 }  // namespace
 

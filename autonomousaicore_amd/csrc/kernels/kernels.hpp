@@ -54,8 +54,12 @@ void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* s
                      int64_t k, int64_t d, void* dye, float* dgsel, DType dt, hipStream_t s);
 void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_t T, int64_t k, int64_t d, void* dx,
                  int64_t ldx, bool accumulate, DType dt, hipStream_t s);
+// daux_scale (device, nullable) multiplies daux: the loss scale of an AMP step.
 void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
-                    int64_t E, int64_t k, float aux_coef, float daux, float* dlogits, hipStream_t s);
+                    int64_t E, int64_t k, float aux_coef, float daux, const float* daux_scale, float* dlogits,
+                    hipStream_t s);
+// *total = aux[0] + aux[1] + ... (layer order); *loss += *total.  MoETransformerLM::total_aux_loss.
+void moe_aux_total(const float* aux, int64_t L, float* loss, float* total, hipStream_t s);
 
 // INT4 symmetric quantization (int4.hip).  Scales are f32 or f16; the dequantized output f32 or
 // bf16.  int4_group returns the effective group size (G <= 0 or G > n: n) and rejects an odd one.

@@ -273,9 +273,11 @@ __global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, 
 __global__ __launch_bounds__(256) void moe_router_bwd_k(const float* __restrict__ probs, const int64_t* __restrict__ idx,
                                                         const float* __restrict__ dgsel,
                                                         const int64_t* __restrict__ counts, int T, int E, int k,
-                                                        float aux_coef, float daux, float* __restrict__ dlogits) {
+                                                        float aux_coef, float daux, const float* __restrict__ daux_scale,
+                                                        float* __restrict__ dlogits) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
+    if (daux_scale) daux *= *daux_scale;
     const float* p = probs + static_cast<int64_t>(t) * E;
     float dg[kMaxE];
     uint64_t used = 0;
@@ -413,11 +415,28 @@ void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_
 }
 
 void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
-                    int64_t E, int64_t k, float aux_coef, float daux, float* dlogits, hipStream_t s) {
+                    int64_t E, int64_t k, float aux_coef, float daux, const float* daux_scale, float* dlogits,
+                    hipStream_t s) {
     check_moe(T, E, k);
     hipLaunchKernelGGL(moe_router_bwd_k, dim3(grid_for(T, 256)), dim3(256), 0, s, probs, idx, dgsel, counts,
-                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), aux_coef, daux, dlogits);
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), aux_coef, daux, daux_scale,
+                       dlogits);
     AIC_LAUNCH_CHECK("moe_router_bwd");
+}
+
+namespace {
+__global__ void moe_aux_total_k(const float* __restrict__ aux, int L, float* __restrict__ loss, float* __restrict__ total) {
+    float t = aux[0];
+    for (int l = 1; l < L; ++l) t = t + aux[l];  // add(add(aux_0, aux_1), ...) in layer order
+    *total = t;
+    *loss = *loss + t;
+}
+}  // namespace
+
+void moe_aux_total(const float* aux, int64_t L, float* loss, float* total, hipStream_t s) {
+    AIC_CHECK(L >= 1 && aux && loss && total, InvalidArgument, "moe_aux_total: bad arguments");
+    hipLaunchKernelGGL(moe_aux_total_k, dim3(1), dim3(1), 0, s, aux, static_cast<int>(L), loss, total);
+    AIC_LAUNCH_CHECK("moe_aux_total");
 }
 
 }  // namespace aic::hip

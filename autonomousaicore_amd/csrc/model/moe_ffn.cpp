@@ -91,7 +91,8 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
                      s);
 }
 
-void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s) {
+void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s,
+                      const float* daux_scale) {
     AIC_CHECK(T_ > 0 && dy && dh && dwr && dexperts, InvalidArgument, "MoEFFN::backward: forward first, no nulls");
     const size_t es = dtype_size(dt_);
     const int64_t T = T_, f2 = 2 * f_, ex = 3 * f_ * d_, used = offsets_h_[E_];
@@ -125,7 +126,7 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
     hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
     // router: dlogits from the gates and the aux loss, then both router products
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,
-                        coef_, daux, dlog.as<float>(), s);
+                        coef_, daux, daux_scale, dlog.as<float>(), s);
     if (dt_ == DType::Float32) {
         gemm(1, 0, E_, d_, T, dlog.get(), E_, h_, d_, dwr, d_, DType::Float32, DType::Float32, s);
         gemm(0, 0, T, d_, E_, dlog.get(), E_, wr_, d_, dh, d_, DType::Float32, DType::Float32, s, 1.0f);

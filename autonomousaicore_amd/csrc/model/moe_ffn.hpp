@@ -25,7 +25,9 @@ public:
                  hipStream_t s);
     // dy [T, d] (dt), daux = dL/daux.  dh [T, d] (dt) is overwritten; dwr [E, d] and dexperts (the
     // experts layout, fp32) are overwritten (zero for an expert that received no token).
-    void backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s);
+    // daux_scale (device, nullable) multiplies daux (the loss scale of an AMP step).
+    void backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s,
+                  const float* daux_scale = nullptr);
 
     // Routing of the last forward: idx [T, k] and counts [E] (device pointers).
     const int64_t* idx() const { return idx_.as<int64_t>(); }

@@ -19,6 +19,8 @@ struct TransformerLM::DevScalars {
     int nonfinite;
     int pad;
     aic_optim_ctl ctl;
+    float aux;  // sum of the MoE layers' aux losses of the last forward
+    int pad2;
 };
 
 namespace {
@@ -63,6 +65,9 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     AIC_CHECK((d / H) % 2 == 0, InvalidArgument, "head_dim must be even for RoPE");
     AIC_CHECK(cfg.compute == DType::Float32 || cfg.compute == DType::BFloat16, DTypeMismatch,
               "compute dtype must be f32 or bf16");
+    const int64_t E = cfg.num_experts;
+    AIC_CHECK(E == 0 || (E >= 1 && E <= 64 && cfg.top_k >= 1 && cfg.top_k <= 8 && cfg.top_k <= E), InvalidArgument,
+              "MoE: need 1 <= num_experts <= 64 and 1 <= top_k <= min(num_experts, 8)");
 
     int64_t off = 0;
     auto add = [&](const std::string& name, std::vector<int64_t> shape) {
@@ -87,9 +92,23 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
         add(pre + "attn.k_proj.weight", {d, d});
         add(pre + "attn.v_proj.weight", {d, d});
         ly.wo = add(pre + "attn.out_proj.weight", {d, d});
-        ly.wgu = add(pre + "ffn.gate_proj.weight", {f, d});
-        add(pre + "ffn.up_proj.weight", {f, d});
-        ly.wd = add(pre + "ffn.down_proj.weight", {d, f});
+        if (E == 0) {
+            ly.wgu = add(pre + "ffn.gate_proj.weight", {f, d});
+            add(pre + "ffn.up_proj.weight", {f, d});
+            ly.wd = add(pre + "ffn.down_proj.weight", {d, f});
+        } else {
+            // MoETransformerBlock (src/nn/moe.cpp:140-160, 270-280): router Linear(d, E), then
+            // expert e's gate [f, d], up [f, d], down [d, f] back to back
+            ly.wgu = ly.wd = 0;
+            ly.wr = add(pre + "moe.router.gate.weight", {E, d});
+            for (int64_t e = 0; e < E; ++e) {
+                const std::string ep = pre + "moe.experts." + std::to_string(e) + ".";
+                const int64_t g = add(ep + "gate_proj.weight", {f, d});
+                if (e == 0) ly.wex = g;
+                add(ep + "up_proj.weight", {f, d});
+                add(ep + "down_proj.weight", {d, f});
+            }
+        }
         ly.n1 = add(pre + "norm1.weight", {d});
         ly.n2 = add(pre + "norm2.weight", {d});
         layers_.push_back(ly);
@@ -138,14 +157,21 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     const float one = 1.0f;
     AIC_HIP_CHECK(hipMalloc(&one_dev_, sizeof(float)));
     AIC_HIP_CHECK(hipMemcpy(one_dev_, &one, sizeof(float), hipMemcpyHostToDevice));
+    if (E > 0) {
+        AIC_HIP_CHECK(hipMalloc(&aux_dev_, sizeof(float) * static_cast<size_t>(L)));
+        AIC_HIP_CHECK(hipMemset(aux_dev_, 0, sizeof(float) * static_cast<size_t>(L)));
+        for (int64_t l = 0; l < L; ++l)
+            moe_.push_back(std::make_unique<MoEFFN>(d, f, E, cfg.top_k, cfg.aux_loss_coef, cfg.compute));
+    }
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 TransformerLM::~TransformerLM() {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    moe_.clear();  // their buffers are freed on stream_, so before it is destroyed
     for (void* p : {static_cast<void*>(params_dev_), static_cast<void*>(grads_dev_), static_cast<void*>(m_dev_),
                     static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
-                    static_cast<void*>(dev_), static_cast<void*>(one_dev_)})
+                    static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
         if (p) (void)hipFree(p);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
@@ -242,8 +268,9 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
 
     // ---- activations kept for the backward ----
     DeviceBuffer xs = act((L + 1) * T * d);  // residual stream x_0 .. x_L
+    const bool moe = cfg_.num_experts > 0;
     DeviceBuffer h1 = act(L * T * d), qkv = act(L * T * 3 * d), ob = act(L * T * d), x1 = act(L * T * d),
-                 h2 = act(L * T * d), gu = act(L * T * 2 * f), am = act(L * T * f);
+                 h2 = act(L * T * d), gu = act(moe ? 0 : L * T * 2 * f), am = act(moe ? 0 : L * T * f);
     DeviceBuffer r1 = f32(L * T), r2 = f32(L * T), lse = f32(L * T * H);
     DeviceBuffer hf = act(T * d), rf = f32(T), logits = act(T * V), lse_ce = f32(T);
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
@@ -265,8 +292,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         void* ol = at(ob, l * T * d);
         void* x1l = at(x1, l * T * d);
         void* h2l = at(h2, l * T * d);
-        void* gul = at(gu, l * T * 2 * f);
-        void* aml = at(am, l * T * f);
+        void* gul = moe ? nullptr : at(gu, l * T * 2 * f);
+        void* aml = moe ? nullptr : at(am, l * T * f);
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_fwd(x, d, P(ly.n1), h1l, d, atf(r1, l * T), T, d, eps, dt, s);
@@ -285,6 +312,11 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_fwd(x1l, d, P(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
+        }
+        if (moe) {
+            // MoELayer::forward (src/nn/moe.cpp:155-253) with the residual x1 added by the combine
+            moe_[l]->forward(h2l, T, W(ly.wr), W(ly.wex), x1l, xn, aux_dev_ + l, s);
+            continue;
         }
         gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, W(ly.wgu), d, gul, 2 * f, dt, dt, s);
         {
@@ -306,6 +338,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         hip::ce_fwd(logits.get(), V, targets, T, V, -100, nullptr, lse_ce.as<float>(), &dev_->loss, &dev_->valid, dt,
                     s);
     }
+    // total_loss = cross_entropy + total_aux_loss (tests/unit/test_moe.cpp:224-228)
+    if (moe) hip::moe_aux_total(aux_dev_, L, &dev_->loss, &dev_->aux, s);
     if (!backward) {
         if (loss_out) {
             AIC_HIP_CHECK(hipMemcpyAsync(loss_out, &dev_->loss, sizeof(float), hipMemcpyDeviceToHost, s));
@@ -323,7 +357,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                     s);
     }
     void* dl = logits.get();
-    DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(T * 2 * f), da = act(T * f);
+    DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(moe ? 0 : T * 2 * f),
+                 da = act(moe ? 0 : T * f);
     gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
     gemm(prof_, 0, 0, T, d, V, dl, V, W(head_), d, dh.get(), d, dt, dt, s);
     {
@@ -339,18 +374,23 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         void* ol = at(ob, l * T * d);
         void* x1l = at(x1, l * T * d);
         void* h2l = at(h2, l * T * d);
-        void* gul = at(gu, l * T * 2 * f);
-        void* aml = at(am, l * T * f);
-        // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
-        gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, f, d, dx.get(), d, W(ly.wd), f, da.get(), f, dt, dt, s);
-        {
-            auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
-            hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
-                            static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
+        if (moe) {
+            // x_{l+1} = x1 + moe(h2); d total_loss / d aux_l = 1 (times the loss scale)
+            moe_[l]->backward(dx.get(), 1.0f, dh.get(), G(ly.wr), G(ly.wex), s, gscale);
+        } else {
+            void* gul = at(gu, l * T * 2 * f);
+            void* aml = at(am, l * T * f);
+            // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
+            gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, f, d, dx.get(), d, W(ly.wd), f, da.get(), f, dt, dt, s);
+            {
+                auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
+                hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
+                                static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
+            }
+            gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, W(ly.wgu), d, dh.get(), d, dt, dt, s);
         }
-        gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, W(ly.wgu), d, dh.get(), d, dt, dt, s);
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_bwd(dh.get(), d, x1l, d, P(ly.n2), atf(r2, l * T), dx.get(), d, dx.get(), d, G(ly.n2), false,
@@ -419,6 +459,7 @@ StepStats TransformerLM::last_stats() {
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
     StepStats st;
     st.loss = h.loss;
+    st.aux_loss = cfg_.num_experts > 0 ? h.aux : 0.0f;
     st.grad_norm = h.ctl.grad_norm;
     st.found_inf = h.ctl.skip != 0;
     st.loss_scale = h.scale_used;

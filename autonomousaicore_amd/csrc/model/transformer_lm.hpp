@@ -18,12 +18,14 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
 #include "../../../include/aic_hip.h"
 #include "../runtime/dtype.hpp"
 #include "../runtime/profiler.hpp"
+#include "moe_ffn.hpp"
 
 namespace aic::models {
 
@@ -38,6 +40,12 @@ struct TransformerLMConfig {
     float rope_theta = 10000.0f;
     bool tie_word_embeddings = false;
     DType compute = DType::Float32;  // Float32 (reference precision) or BFloat16 (AMP)
+    // Mixture of experts (MoETransformerLMConfig, include/models/moe_transformer_lm.hpp): with
+    // num_experts > 0 every FFN is a routed MoE layer of num_experts SwiGLU experts of
+    // intermediate_dim, top_k per token, and the training loss adds each layer's aux loss.
+    int64_t num_experts = 0;
+    int64_t top_k = 2;
+    float aux_loss_coef = 0.01f;
 };
 
 struct AdamWOptions {
@@ -65,7 +73,8 @@ struct ParamInfo {
 };
 
 struct StepStats {
-    float loss = 0.0f;
+    float loss = 0.0f;      // cross-entropy + the MoE aux losses (total_aux_loss)
+    float aux_loss = 0.0f;  // sum of the MoE layers' aux losses (0 for a dense model)
     float grad_norm = 0.0f;
     bool found_inf = false;
     float loss_scale = 1.0f;
@@ -103,7 +112,8 @@ public:
 
 private:
     struct Layer {
-        int64_t wqkv, wo, wgu, wd, n1, n2;  // arena offsets
+        int64_t wqkv, wo, wgu, wd, n1, n2;  // arena offsets (wgu / wd: dense FFN)
+        int64_t wr = 0, wex = 0;            // MoE: router [E, d]; experts, each gate, up, down
     };
     struct DevScalars;
 
@@ -130,6 +140,8 @@ private:
     float* sin_dev_ = nullptr;
     DevScalars* dev_ = nullptr;
     float* one_dev_ = nullptr;
+    float* aux_dev_ = nullptr;  // per-layer MoE aux losses [L]
+    std::vector<std::unique_ptr<MoEFFN>> moe_;
     Profiler prof_;
 };
 

@@ -28,6 +28,16 @@ class TransformerLMConfig:
     rope_theta: float = 10000.0
     tie_word_embeddings: bool = False
     compute: str = "float32"  # "float32" (reference precision) or "bfloat16" (AMP)
+    num_experts: int = 0      # > 0: MoE FFNs (MoETransformerLMConfig)
+    top_k: int = 2
+    aux_loss_coef: float = 0.01
+
+
+@dataclass
+class MoETransformerLMConfig(TransformerLMConfig):
+    """models::MoETransformerLMConfig (include/models/moe_transformer_lm.hpp): the dense
+    configuration plus the expert count, router top-k and aux-loss coefficient."""
+    num_experts: int = 8
 
 
 @dataclass
@@ -64,6 +74,7 @@ class StepMetrics:
     found_inf: bool
     loss_scale: float
     step: int
+    aux_loss: float = 0.0
 
 
 class TransformerLM:
@@ -75,7 +86,8 @@ class TransformerLM:
         self.train_cfg = train
         c = _lib.LMConfig(cfg.vocab_size, cfg.hidden_dim, cfg.num_layers, cfg.num_heads, cfg.intermediate_dim,
                           cfg.max_seq_len, cfg.rms_norm_eps, cfg.rope_theta, 1 if cfg.tie_word_embeddings else 0,
-                          AIC_BF16 if cfg.compute == "bfloat16" else AIC_F32)
+                          AIC_BF16 if cfg.compute == "bfloat16" else AIC_F32, cfg.num_experts, cfg.top_k,
+                          cfg.aux_loss_coef)
         a, s = train.adamw, train.scaler
         t = _lib.TrainConfig(a.lr, a.beta1, a.beta2, a.eps, a.weight_decay, train.max_grad_norm,
                              1 if train.use_amp else 0, s.initial_scale, s.growth_factor, s.backoff_factor,
@@ -156,7 +168,7 @@ class TransformerLM:
                   C.byref(st) if st is not None else None)
         if st is None:
             return None
-        return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step))
+        return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step), float(st.aux_loss))
 
     def eval_loss(self, ids, targets, B: int, S: int) -> float:
         on_dev = isinstance(ids, int)
@@ -176,7 +188,7 @@ class TransformerLM:
     def last_stats(self) -> StepMetrics:
         st = _lib.StepStats()
         _lib.call("aic_lm_last_stats", self._h, C.byref(st))
-        return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step))
+        return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step), float(st.aux_loss))
 
     def set_profiling(self, on: bool) -> None:
         """Time every kernel launch of the following steps with HIP events (resets)."""

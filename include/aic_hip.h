@@ -366,6 +366,11 @@ typedef struct {
     int tied;              /* lm_head shares tok_embeddings.weight */
     aic_dtype compute;     /* AIC_F32 (reference precision) or AIC_BF16 (AMP: bf16 compute,
                               fp32 master weights, gradients and AdamW state) */
+    int64_t n_experts;     /* 0: dense SwiGLU FFN; > 0: MoETransformerLM (src/models/moe_transformer_lm.cpp):
+                              every FFN is n_experts SwiGLU experts of d_ffn with a top_k router,
+                              and the loss is cross_entropy + total_aux_loss (<= 64 experts) */
+    int64_t top_k;
+    float aux_loss_coef;
 } aic_lm_config;
 
 typedef struct {
@@ -383,6 +388,7 @@ typedef struct {
     int found_inf;
     float loss_scale;      /* scale used by this step */
     int64_t step;          /* AdamW step count after this step */
+    float aux_loss;        /* MoE: total_aux_loss, included in loss (0 for a dense model) */
 } aic_step_stats;
 
 /* Creates the model on the current device; parameters are zero until set or initialised. */
@@ -390,8 +396,8 @@ int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm
 int aic_lm_destroy(aic_lm* lm);
 int64_t aic_lm_num_params(const aic_lm* lm);
 int aic_lm_num_tensors(const aic_lm* lm);
-/* Name, shape and flat offset of parameter tensor i in named_parameters() order of the
- * arena (name buffer of name_cap bytes, dims of 2 entries). */
+/* Name (the reference's parameter name), shape and flat offset of parameter tensor i, in
+ * arena order (layer-major; name buffer of name_cap bytes, dims of 2 entries). */
 int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset);
 /* Host <-> device copies of the flat fp32 arenas (synchronous). */
 int aic_lm_set_params(aic_lm* lm, const float* host);

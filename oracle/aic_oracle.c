@@ -586,6 +586,7 @@ int orc_scaler_unscale_and_update(orc_scaler* s, float* const* grads, const int6
  * ====================================================================================== */
 typedef struct {
     float *wq, *wk, *wv, *wo, *wg, *wu, *wd, *n1, *n2;
+    float *wr, *wex; /* MoE: router [E,d]; experts, each gate [f,d], up [f,d], down [d,f] */
 } layer_ptrs;
 
 typedef struct {
@@ -596,8 +597,8 @@ typedef struct {
 } lm_ptrs;
 
 int64_t orc_lm_num_params(const orc_lm_config* c) {
-    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab;
-    int64_t per_layer = 4 * d * d + 3 * d * f + 2 * d;
+    int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, E = c->n_experts;
+    int64_t per_layer = 4 * d * d + (E > 0 ? E * d + E * 3 * d * f : 3 * d * f) + 2 * d;
     return V * d + c->n_layers * per_layer + d + (c->tied ? 0 : V * d);
 }
 
@@ -613,9 +614,14 @@ static lm_ptrs map_params(const orc_lm_config* c, float* base) {
         L->wk = cur; cur += d * d;
         L->wv = cur; cur += d * d;
         L->wo = cur; cur += d * d;
-        L->wg = cur; cur += f * d;
-        L->wu = cur; cur += f * d;
-        L->wd = cur; cur += d * f;
+        if (c->n_experts > 0) {
+            L->wr = cur; cur += c->n_experts * d;
+            L->wex = cur; cur += c->n_experts * 3 * f * d;
+        } else {
+            L->wg = cur; cur += f * d;
+            L->wu = cur; cur += f * d;
+            L->wd = cur; cur += d * f;
+        }
         L->n1 = cur; cur += d;
         L->n2 = cur; cur += d;
     }
@@ -632,10 +638,40 @@ static void add_into(float* dst, const float* a, const float* b, int64_t n) {
     for (int64_t i = 0; i < n; ++i) dst[i] = a[i] + b[i];
 }
 
+/* Experts stored back to back (gate, up, down per expert) <-> the [E,f,d] / [E,d,f] stacks
+ * the MoE restatement takes. */
+static void experts_split(const float* wex, int64_t E, int64_t d, int64_t f, float* wg, float* wu, float* wd) {
+    const int64_t fd = f * d;
+    for (int64_t e = 0; e < E; ++e) {
+        memcpy(wg + e * fd, wex + e * 3 * fd, sizeof(float) * (size_t)fd);
+        memcpy(wu + e * fd, wex + e * 3 * fd + fd, sizeof(float) * (size_t)fd);
+        memcpy(wd + e * fd, wex + e * 3 * fd + 2 * fd, sizeof(float) * (size_t)fd);
+    }
+}
+static void experts_merge_add(float* wex, int64_t E, int64_t d, int64_t f, const float* wg, const float* wu,
+                              const float* wd) {
+    const int64_t fd = f * d;
+    for (int64_t e = 0; e < E; ++e)
+        for (int64_t i = 0; i < fd; ++i) {
+            wex[e * 3 * fd + i] += wg[e * fd + i];
+            wex[e * 3 * fd + fd + i] += wu[e * fd + i];
+            wex[e * 3 * fd + 2 * fd + i] += wd[e * fd + i];
+        }
+}
+
+void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx,
+                     float* gates);
+void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
+                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
+                     float* dwr, float* dwg, float* dwu, float* dwd);
+
 /* Forward; returns logits [T, V] (caller frees) and fills acts when non-NULL. */
 static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t* ids, int64_t B, int64_t S,
                          layer_acts* acts, float** hf_out, float** rf_out, float** xf_out,
-                         const float* cos_t, const float* sin_t, orc_step_result* res) {
+                         const float* cos_t, const float* sin_t, orc_step_result* res, float* aux_total) {
+    float aux_sum = 0.0f;
+    int have_aux = 0;
     int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, H = c->n_heads, hd = d / H, T = B * S;
     size_t Td = (size_t)(T * d), Tf = (size_t)(T * f);
     double t0 = now_s();
@@ -671,10 +707,24 @@ static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t
         orc_linear_fwd(ctx, L->wo, att, B, S, d, d);
         add_into(x1, x, att, (int64_t)Td);
         orc_rmsnorm_fwd(x1, L->n2, h2, r2, T, d, c->norm_eps);
-        orc_linear_fwd(h2, L->wg, g, B, S, d, f);
-        orc_linear_fwd(h2, L->wu, u, B, S, d, f);
-        orc_swiglu_fwd(g, u, hm, (int64_t)Tf);
-        orc_linear_fwd(hm, L->wd, ffo, B, S, f, d);
+        if (c->n_experts > 0) {
+            /* MoETransformerBlock: x2 = x1 + MoELayer(norm2(x1)) (src/nn/moe.cpp:155-253, 283-300) */
+            const int64_t E = c->n_experts;
+            float* wg = (float*)xcalloc((size_t)(E * f * d), sizeof(float));
+            float* wu = (float*)xcalloc((size_t)(E * f * d), sizeof(float));
+            float* wd = (float*)xcalloc((size_t)(E * f * d), sizeof(float));
+            experts_split(L->wex, E, d, f, wg, wu, wd);
+            float aux = 0.0f;
+            orc_moe_ffn_fwd(h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef, ffo, &aux, NULL, NULL);
+            aux_sum = have_aux ? aux_sum + aux : aux; /* total_aux_loss: add in layer order */
+            have_aux = 1;
+            free(wg); free(wu); free(wd);
+        } else {
+            orc_linear_fwd(h2, L->wg, g, B, S, d, f);
+            orc_linear_fwd(h2, L->wu, u, B, S, d, f);
+            orc_swiglu_fwd(g, u, hm, (int64_t)Tf);
+            orc_linear_fwd(hm, L->wd, ffo, B, S, f, d);
+        }
         float* x2 = (float*)xcalloc(Td, sizeof(float));
         add_into(x2, x1, ffo, (int64_t)Td);
         free(att);
@@ -704,6 +754,7 @@ static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t
     if (hf_out) *hf_out = hf; else free(hf);
     if (rf_out) *rf_out = rf; else free(rf);
     if (xf_out) *xf_out = x; else free(x);
+    if (aux_total) *aux_total = aux_sum;
     return logits;
 }
 
@@ -714,8 +765,10 @@ float orc_lm_loss(const orc_lm_config* c, const float* params, const int64_t* id
     float* cos_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
     float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
     orc_rope_tables(cos_t, sin_t, S, hd, c->rope_base);
-    float* logits = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL);
+    float aux = 0.0f;
+    float* logits = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL, &aux);
     float loss = orc_ce_fwd(logits, targets, B * S, c->vocab, -100, NULL, NULL, NULL);
+    if (c->n_experts > 0) loss = loss + aux;
     free(logits); free(cos_t); free(sin_t); free(P.layers);
     return loss;
 }
@@ -740,14 +793,17 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
 
     layer_acts* acts = (layer_acts*)xcalloc((size_t)c->n_layers, sizeof(layer_acts));
     float *hf, *rf, *xf;
-    float* logits = lm_forward(c, &P, ids, B, S, acts, &hf, &rf, &xf, cos_t, sin_t, res);
+    float aux = 0.0f;
+    float* logits = lm_forward(c, &P, ids, B, S, acts, &hf, &rf, &xf, cos_t, sin_t, res, &aux);
 
-    /* loss */
+    /* loss (+ total_aux_loss for MoE, tests/unit/test_moe.cpp:224-228) */
     double tl0 = now_s();
     float* lse = (float*)xcalloc((size_t)T, sizeof(float));
     int64_t valid = 0;
     float loss = orc_ce_fwd(logits, targets, T, V, -100, NULL, lse, &valid);
+    if (c->n_experts > 0) loss = loss + aux;
     res->loss = loss;
+    res->aux_loss = c->n_experts > 0 ? aux : 0.0f;
     float gscale = 1.0f;
     if (o->use_scaler && scaler) gscale = scaler->scale; /* scaler.scale(loss) = mul(loss, scale) */
     res->loss_scale_used = gscale;
@@ -779,12 +835,29 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
         layer_ptrs* L = &P.layers[l];
         layer_ptrs* GL = &G.layers[l];
         layer_acts* A = &acts[l];
-        /* x2 = x1 + down(hm): dx is grad of x2 */
-        orc_linear_bwd(A->hm, L->wd, dx, dhm, GL->wd, B, S, f, d);
-        orc_swiglu_bwd(A->g, A->u, dhm, dg, du, (int64_t)Tf);
-        orc_linear_bwd(A->h2, L->wg, dg, tmp, GL->wg, B, S, d, f);
-        orc_linear_bwd(A->h2, L->wu, du, tmp2, GL->wu, B, S, d, f);
-        add_into(tmp, tmp, tmp2, (int64_t)Td); /* grad of h2 (engine accumulation) */
+        if (c->n_experts > 0) {
+            /* x2 = x1 + moe(h2); d loss / d aux_l = 1 (scaled with the loss) */
+            const int64_t E = c->n_experts, efd = E * f * d;
+            float* wg = (float*)xcalloc((size_t)efd, sizeof(float));
+            float* wu = (float*)xcalloc((size_t)efd, sizeof(float));
+            float* wd = (float*)xcalloc((size_t)efd, sizeof(float));
+            float* dwg = (float*)xcalloc((size_t)efd, sizeof(float));
+            float* dwu = (float*)xcalloc((size_t)efd, sizeof(float));
+            float* dwd = (float*)xcalloc((size_t)efd, sizeof(float));
+            experts_split(L->wex, E, d, f, wg, wu, wd);
+            memset(tmp, 0, sizeof(float) * Td);
+            orc_moe_ffn_bwd(A->h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef, dx, gscale, tmp, GL->wr, dwg,
+                            dwu, dwd);
+            experts_merge_add(GL->wex, E, d, f, dwg, dwu, dwd);
+            free(wg); free(wu); free(wd); free(dwg); free(dwu); free(dwd);
+        } else {
+            /* x2 = x1 + down(hm): dx is grad of x2 */
+            orc_linear_bwd(A->hm, L->wd, dx, dhm, GL->wd, B, S, f, d);
+            orc_swiglu_bwd(A->g, A->u, dhm, dg, du, (int64_t)Tf);
+            orc_linear_bwd(A->h2, L->wg, dg, tmp, GL->wg, B, S, d, f);
+            orc_linear_bwd(A->h2, L->wu, du, tmp2, GL->wu, B, S, d, f);
+            add_into(tmp, tmp, tmp2, (int64_t)Td); /* grad of h2 (engine accumulation) */
+        }
         orc_rmsnorm_bwd(tmp, A->x1, L->n2, A->r2, tmp2, GL->n2, T, d);
         add_into(dx, dx, tmp2, (int64_t)Td); /* grad of x1 = residual + norm path */
         /* x1 = x + out_proj(ctx) */

@@ -140,11 +140,17 @@ int orc_scaler_unscale_and_update(orc_scaler* s, float* const* grads, const int6
  *                     norm1.weight [d], norm2.weight [d]
  *   norm.weight [d]
  *   lm_head.weight [V, d]      (absent when tied: the head reuses tok_embeddings.weight)
+ * With n_experts = E > 0 (MoETransformerLM, src/models/moe_transformer_lm.cpp) the three ffn
+ * tensors of a layer are replaced by moe.router.gate.weight [E,d] and, for each expert e,
+ * moe.experts.e.gate_proj [f,d], up_proj [f,d], down_proj [d,f]; the loss is cross_entropy +
+ * total_aux_loss (the layers' aux losses added in layer order).
  */
 typedef struct {
     int64_t vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len;
     float norm_eps, rope_base;
     int tied;
+    int64_t n_experts, top_k;
+    float aux_coef;
 } orc_lm_config;
 
 typedef struct {
@@ -160,6 +166,7 @@ typedef struct {
     int found_inf;         /* scaler found a non-finite gradient; the update was skipped */
     float loss_scale_used;
     double t_embed, t_blocks_fwd, t_head_fwd, t_loss, t_head_bwd, t_blocks_bwd, t_embed_bwd, t_optim; /* seconds */
+    float aux_loss;        /* MoE: total_aux_loss (included in loss) */
 } orc_step_result;
 
 int64_t orc_lm_num_params(const orc_lm_config* cfg);

@@ -24,7 +24,8 @@ i64p = C.POINTER(C.c_int64)
 class LMConfig(C.Structure):
     _fields_ = [("vocab", C.c_int64), ("d_model", C.c_int64), ("n_layers", C.c_int64),
                 ("n_heads", C.c_int64), ("d_ffn", C.c_int64), ("max_seq_len", C.c_int64),
-                ("norm_eps", C.c_float), ("rope_base", C.c_float), ("tied", C.c_int)]
+                ("norm_eps", C.c_float), ("rope_base", C.c_float), ("tied", C.c_int), ("n_experts", C.c_int64),
+                ("top_k", C.c_int64), ("aux_coef", C.c_float)]
 
 
 class TrainOpts(C.Structure):
@@ -37,7 +38,8 @@ class StepResult(C.Structure):
     _fields_ = [("loss", C.c_float), ("grad_norm", C.c_float), ("found_inf", C.c_int),
                 ("loss_scale_used", C.c_float), ("t_embed", C.c_double), ("t_blocks_fwd", C.c_double),
                 ("t_head_fwd", C.c_double), ("t_loss", C.c_double), ("t_head_bwd", C.c_double),
-                ("t_blocks_bwd", C.c_double), ("t_embed_bwd", C.c_double), ("t_optim", C.c_double)]
+                ("t_blocks_bwd", C.c_double), ("t_embed_bwd", C.c_double), ("t_optim", C.c_double),
+                ("aux_loss", C.c_float)]
 
 
 class Scaler(C.Structure):
@@ -281,8 +283,9 @@ class LossScaler:
 
 
 def make_config(vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len, norm_eps=1e-6, rope_base=10000.0,
-                tied=False):
-    return LMConfig(vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len, norm_eps, rope_base, 1 if tied else 0)
+                tied=False, n_experts=0, top_k=2, aux_coef=0.01):
+    return LMConfig(vocab, d_model, n_layers, n_heads, d_ffn, max_seq_len, norm_eps, rope_base, 1 if tied else 0,
+                    n_experts, top_k, aux_coef)
 
 
 def num_params(cfg: LMConfig) -> int:

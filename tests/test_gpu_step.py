@@ -171,3 +171,71 @@ def test_eval_loss_equals_step_loss():
     assert l0 == st.loss
     assert model.eval_loss(ids, tgt, 4, 64) < l0  # one AdamW step on the same batch lowers the loss
     model.close()
+
+
+# ----------------------------------------------------------------------------- MoE (configs[3] family)
+def build_moe(cfg, E, k, coef, compute="float32", amp=False):
+    c = aic.MoETransformerLMConfig(vocab_size=cfg["vocab"], hidden_dim=cfg["d"], num_layers=cfg["L"],
+                                   num_heads=cfg["H"], intermediate_dim=cfg["f"], max_seq_len=2048, rms_norm_eps=1e-6,
+                                   compute=compute, num_experts=E, top_k=k, aux_loss_coef=coef)
+    t = aic.TrainingConfig(adamw=aic.AdamWOptions(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1),
+                           max_grad_norm=1.0, use_amp=amp)
+    return aic.TransformerLM(c, t)
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (8, 2), (3, 1)])
+def test_moe_fp32_step_matches_oracle(orc, E, k):
+    """MoETransformerLM step in fp32 (cross_entropy + total_aux_loss, backward through routers
+    and the routed experts, clip, AdamW) against the oracle; router weights N(0, 0.02) as the
+    MoE configuration states."""
+    cfg = dict(vocab=256, d=64, L=2, H=4, f=96, tied=False)
+    B, S, coef = 4, 32, 0.01
+    model = build_moe(cfg, E, k, coef)
+    params = make_params(model, 777 + E)
+    model.set_params(params)
+    assert any("moe.router.gate.weight" in n for n, _, _ in model.layout)
+    ids, tgt = aic.batch(4321, B, S, cfg["vocab"], dist="zipf")
+    st = model.train_step(ids, tgt, B, S)
+    ocfg = orc.make_config(cfg["vocab"], cfg["d"], cfg["L"], cfg["H"], cfg["f"], S, norm_eps=1e-6, n_experts=E,
+                           top_k=k, aux_coef=coef)
+    p = params.copy()
+    res, g_ref, _, _, _ = orc.lm_step(ocfg, p, ids, tgt, B, S)
+    assert abs(st.aux_loss - res.aux_loss) <= 1e-6 * abs(res.aux_loss)
+    assert abs(st.loss - res.loss) / abs(res.loss) < 1e-5
+    assert abs(st.grad_norm - res.grad_norm) / res.grad_norm < 1e-4
+    g = model.get_grads() * min(1.0, 1.0 / (st.grad_norm + 1e-6))
+    for name, shape, off in model.layout:
+        n = int(np.prod(shape))
+        # top-1 router gradients are rounding noise in fp32 (p / (p + 1e-9) cancels)
+        tol = 2e-2 if (k == 1 and "router" in name) else 1e-4
+        assert rel(g[off:off + n], g_ref[off:off + n]) < tol, name
+    check_tensors(model, model.get_params(), p, 1e-4, "param")
+    model.close()
+
+
+def test_moe_bf16_amp_step_close_to_fp32_oracle(orc):
+    """The MoE configuration's widths scaled down (d 1024 -> 256, 16 -> 4 heads of 64, expert
+    SwiGLU 2816 -> 704, 8 experts, top-2, aux 0.01, vocab 32000) at 2 layers, B 2 x S 256,
+    bf16 AMP with loss scaling, against the fp32 oracle; and bit-identical on a second run."""
+    cfg = dict(vocab=32000, d=256, L=2, H=4, f=704, tied=False)
+    B, S = 2, 256
+    outs = []
+    for _ in range(2):
+        model = build_moe(cfg, 8, 2, 0.01, compute="bfloat16", amp=True)
+        params = make_params(model, 2024)
+        model.set_params(params)
+        ids, tgt = aic.batch(99, B, S, cfg["vocab"], dist="zipf")
+        st = model.train_step(ids, tgt, B, S)
+        outs.append((st, model.get_grads(), model.get_params()))
+        model.close()
+    st = outs[0][0]
+    assert outs[1][0].loss == st.loss
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    np.testing.assert_array_equal(outs[0][2], outs[1][2])
+    ocfg = orc.make_config(cfg["vocab"], cfg["d"], cfg["L"], cfg["H"], cfg["f"], S, norm_eps=1e-6, n_experts=8,
+                           top_k=2, aux_coef=0.01)
+    res, _, _, _, _ = orc.lm_step(ocfg, params.copy(), ids, tgt, B, S)
+    assert abs(st.loss - res.loss) / abs(res.loss) < 1e-2
+    assert abs(st.aux_loss - res.aux_loss) < 3e-2 * abs(res.aux_loss)
+    assert st.loss_scale == 65536.0 and not st.found_inf
+    assert abs(st.grad_norm - res.grad_norm) / res.grad_norm < 5e-2

@@ -702,3 +702,33 @@ def test_casts_vs_numpy_and_torch(orc):
     np.testing.assert_array_equal(orc.cast(iv.astype(np.int32), "i64"), iv.astype(np.int32).astype(np.int64))
     with pytest.raises(NotImplementedError):
         orc.cast(h, "bf16")                                            # f16 -> bf16 is not in the table
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (3, 1)])
+def test_moe_lm_step_vs_torch(orc, E, k):
+    # MoETransformerLM: cross_entropy + total_aux_loss, backward through routers and experts,
+    # clip and AdamW, against a float64 torch model (tests/unit/test_moe.cpp:190-240 trains this)
+    vocab, d, L, H, f, B, S, coef = 64, 32, 2, 2, 48, 2, 16, 0.05
+    rng = np.random.default_rng(40 + E)
+    lay = torch_ref.layout(vocab, d, L, f, False, E)
+    params = np.concatenate([(np.ones(s) if len(s) == 1 else rng.standard_normal(s) * 0.2).ravel()
+                             for _, s in lay]).astype(np.float32)
+    ids = rng.integers(0, vocab, B * S).astype(np.int64)
+    tgt = np.roll(ids, -1)
+    cfg = orc.make_config(vocab, d, L, H, f, S, n_experts=E, top_k=k, aux_coef=coef)
+    assert orc.num_params(cfg) == params.size
+    loss_t, norm_t, grads_t, new_t = torch_ref.lm_step(vocab, d, L, H, f, False, params, ids, tgt, B, S,
+                                                        n_experts=E, top_k=k, aux_coef=coef)
+    p = params.copy()
+    res, grads, m, v, step = orc.lm_step(cfg, p, ids, tgt, B, S)
+    assert res.aux_loss > 0
+    assert abs(res.loss - loss_t) / abs(loss_t) < 1e-5
+    assert abs(res.grad_norm - norm_t) / norm_t < 1e-4
+    off = 0
+    for name, shape in lay:
+        n = int(np.prod(shape))
+        # top-1 router gradients are rounding noise in fp32 (p / (p + 1e-9) cancels)
+        tol = 2e-2 if (k == 1 and "router" in name) else 1e-4
+        assert rel(grads[off:off + n], grads_t[off:off + n]) < tol, name
+        off += n
+    assert rel(p, new_t) < 1e-4
