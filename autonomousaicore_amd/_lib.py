@@ -31,7 +31,8 @@ class OptimCtl(C.Structure):
 class LMConfig(C.Structure):
     _fields_ = [("vocab", i64), ("d_model", i64), ("n_layers", i64), ("n_heads", i64), ("d_ffn", i64),
                 ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32),
-                ("n_experts", i64), ("top_k", i64), ("aux_loss_coef", f32)]
+                ("n_experts", i64), ("top_k", i64), ("aux_loss_coef", f32), ("lora_rank", i64),
+                ("lora_alpha", f32), ("quant_group", i64)]
 
 
 class TrainConfig(C.Structure):
@@ -111,6 +112,10 @@ SIGNATURES = {
     "aic_lm_num_params": (i64, [vp]),
     "aic_lm_num_tensors": (i32, [vp]),
     "aic_lm_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
+    "aic_lm_num_base_params": (i64, [vp]),
+    "aic_lm_num_base_tensors": (i32, [vp]),
+    "aic_lm_base_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
+    "aic_lm_set_base_params": (i32, [vp, vp]),
     "aic_lm_set_params": (i32, [vp, vp]),
     "aic_lm_get_params": (i32, [vp, vp]),
     "aic_lm_get_grads": (i32, [vp, vp]),

@@ -290,6 +290,9 @@ int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm
         c.num_experts = cfg->n_experts;
         c.top_k = cfg->top_k;
         c.aux_loss_coef = cfg->aux_loss_coef;
+        c.lora_rank = cfg->lora_rank;
+        c.lora_alpha = cfg->lora_alpha;
+        c.quant_group = cfg->quant_group;
         aic::models::TrainOptions o;
         o.adamw = {tcfg->lr, tcfg->beta1, tcfg->beta2, tcfg->eps, tcfg->weight_decay};
         o.max_grad_norm = tcfg->max_grad_norm;
@@ -319,10 +322,10 @@ int64_t aic_lm_num_params(const aic_lm* lm) { return lm ? lm->model->num_params(
 
 int aic_lm_num_tensors(const aic_lm* lm) { return lm ? static_cast<int>(lm->model->params().size()) : -1; }
 
-int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset) {
+namespace {
+int tensor_info(const std::vector<aic::models::ParamInfo>& ps, int i, char* name, int name_cap, int* rank,
+                int64_t* dims, int64_t* offset) {
     return guard([&] {
-        AIC_CHECK(lm, InvalidArgument, "null model");
-        const auto& ps = lm->model->params();
         AIC_CHECK(i >= 0 && i < static_cast<int>(ps.size()), OutOfRange, "tensor index ", i);
         const auto& p = ps[static_cast<size_t>(i)];
         if (name && name_cap > 0) {
@@ -337,6 +340,36 @@ int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* r
             for (int j = 0; j < i; ++j) o += ps[static_cast<size_t>(j)].numel;
             *offset = o;  // offset in the packed (unpadded) host layout
         }
+    });
+}
+}  // namespace
+
+int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset) {
+    if (!lm) return guard([] { AIC_CHECK(false, InvalidArgument, "null model"); });
+    return tensor_info(lm->model->params(), i, name, name_cap, rank, dims, offset);
+}
+
+int64_t aic_lm_num_base_params(const aic_lm* lm) {
+    if (!lm) return -1;
+    int64_t n = 0;
+    for (const auto& p : lm->model->base_params()) n += p.numel;
+    return n;
+}
+
+int aic_lm_num_base_tensors(const aic_lm* lm) {
+    return lm ? static_cast<int>(lm->model->base_params().size()) : -1;
+}
+
+int aic_lm_base_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims,
+                            int64_t* offset) {
+    if (!lm) return guard([] { AIC_CHECK(false, InvalidArgument, "null model"); });
+    return tensor_info(lm->model->base_params(), i, name, name_cap, rank, dims, offset);
+}
+
+int aic_lm_set_base_params(aic_lm* lm, const float* host) {
+    return guard([&] {
+        AIC_CHECK(lm && host, InvalidArgument, "null argument");
+        lm->model->set_base_params(host);
     });
 }
 

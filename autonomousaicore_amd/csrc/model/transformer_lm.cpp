@@ -31,7 +31,7 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
-          int64_t ldr = 0, float beta = 0.0f) {
+          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     auto scope = prof.scope(ta ? kGemmWgrad : (tb ? kGemmFwd : kGemmDgrad), 2.0 * M * N * K, es * (M * K + N * K) + ec * M * N * (R ? 2 : 1), s);
     hip::GemmArgs a;
@@ -49,6 +49,7 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
     a.R = R;
     a.ldr = ldr;
     a.beta = beta;
+    a.alpha = alpha;
     a.ab = ab;
     a.c = c;
     hip::gemm(a, s);
@@ -68,19 +69,24 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     const int64_t E = cfg.num_experts;
     AIC_CHECK(E == 0 || (E >= 1 && E <= 64 && cfg.top_k >= 1 && cfg.top_k <= 8 && cfg.top_k <= E), InvalidArgument,
               "MoE: need 1 <= num_experts <= 64 and 1 <= top_k <= min(num_experts, 8)");
+    const bool qlora = cfg.lora_rank > 0;
+    AIC_CHECK(cfg.lora_rank >= 0 && (!qlora || E == 0), InvalidArgument, "QLoRA: rank >= 0, and not with MoE FFNs");
 
+    // the model's tensors: the trainable arena, or with QLoRA the frozen base arena
+    std::vector<ParamInfo>& model = qlora ? base_ : params_;
     int64_t off = 0;
-    auto add = [&](const std::string& name, std::vector<int64_t> shape) {
+    auto add_to = [](std::vector<ParamInfo>& list, int64_t& o, const std::string& name, std::vector<int64_t> shape) {
         ParamInfo p;
         p.name = name;
         p.shape = shape;
         p.numel = 1;
-        for (auto s : shape) p.numel *= s;
-        p.offset = off;
-        off = align_up(off + p.numel);
-        params_.push_back(p);
+        for (auto sz : shape) p.numel *= sz;
+        p.offset = o;
+        o = align_up(o + p.numel);
+        list.push_back(p);
         return p.offset;
     };
+    auto add = [&](const std::string& name, std::vector<int64_t> shape) { return add_to(model, off, name, shape); };
     emb_ = add("tok_embeddings.weight", {V, d});
     for (int64_t l = 0; l < L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
@@ -115,7 +121,45 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     }
     normf_ = add("norm.weight", {d});
     head_ = cfg.tie_word_embeddings ? emb_ : add("lm_head.weight", {V, d});
+    base_arena_ = off;
     arena_ = off;
+    int64_t q4_bytes = 0, q4_scales = 0;
+    if (qlora) {
+        // LoRALinear parameters lora_A / lora_B of the seven projections (src/nn/lora.cpp:31-43)
+        const int64_t r = cfg.lora_rank, G = cfg.quant_group;
+        AIC_CHECK(G > 0 && G % 2 == 0 && (d * d) % G == 0 && (f * d) % G == 0, InvalidArgument,
+                  "QLoRA: the group size must be even and divide d*d and d_ffn*d");
+        // A of q, k, v (and of gate, up) must be adjacent to act as one stacked matrix
+        AIC_CHECK((r * d) % kAlign == 0, InvalidArgument, "QLoRA: lora_rank * d_model must be a multiple of 64");
+        int64_t o2 = 0;
+        auto lo = [&](const std::string& name, std::vector<int64_t> shape) { return add_to(params_, o2, name, shape); };
+        for (int64_t l = 0; l < L; ++l) {
+            const std::string pre = "layers." + std::to_string(l) + ".";
+            Layer& ly = layers_[static_cast<size_t>(l)];
+            ly.aqkv = lo(pre + "attn.q_proj.lora_A", {r, d});
+            lo(pre + "attn.k_proj.lora_A", {r, d});
+            lo(pre + "attn.v_proj.lora_A", {r, d});
+            ly.bq = lo(pre + "attn.q_proj.lora_B", {d, r});
+            ly.bk = lo(pre + "attn.k_proj.lora_B", {d, r});
+            ly.bv = lo(pre + "attn.v_proj.lora_B", {d, r});
+            ly.ao = lo(pre + "attn.out_proj.lora_A", {r, d});
+            ly.bo = lo(pre + "attn.out_proj.lora_B", {d, r});
+            ly.agu = lo(pre + "ffn.gate_proj.lora_A", {r, d});
+            lo(pre + "ffn.up_proj.lora_A", {r, d});
+            ly.bg = lo(pre + "ffn.gate_proj.lora_B", {f, r});
+            ly.bu = lo(pre + "ffn.up_proj.lora_B", {f, r});
+            ly.ad = lo(pre + "ffn.down_proj.lora_A", {r, f});
+            ly.bd = lo(pre + "ffn.down_proj.lora_B", {d, r});
+            const int64_t sizes[7] = {d * d, d * d, d * d, d * d, f * d, f * d, d * f};
+            for (int j = 0; j < 7; ++j) {
+                ly.pk[j] = q4_bytes;
+                q4_bytes += (sizes[j] / 2 + 255) / 256 * 256;
+                ly.sc[j] = q4_scales;
+                q4_scales += (sizes[j] / G + 127) / 128 * 128;
+            }
+        }
+        arena_ = o2;
+    }
     AIC_CHECK((d * d) % kAlign == 0 && (f * d) % kAlign == 0, InvalidArgument,
               "d_model*d_model and d_ffn*d_model must be multiples of 64 (fused q/k/v and gate/up projections)");
 
@@ -132,6 +176,21 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     if (cfg.compute == DType::BFloat16) {
         AIC_HIP_CHECK(hipMalloc(&low_dev_, sizeof(uint16_t) * static_cast<size_t>(arena_)));
         AIC_HIP_CHECK(hipMemsetAsync(low_dev_, 0, sizeof(uint16_t) * static_cast<size_t>(arena_), stream_));
+    }
+    if (qlora) {
+        AIC_HIP_CHECK(hipMalloc(&base_dev_, sizeof(float) * static_cast<size_t>(base_arena_)));
+        AIC_HIP_CHECK(hipMemsetAsync(base_dev_, 0, sizeof(float) * static_cast<size_t>(base_arena_), stream_));
+        if (cfg.compute == DType::BFloat16) {
+            AIC_HIP_CHECK(hipMalloc(&base_low_, sizeof(uint16_t) * static_cast<size_t>(base_arena_)));
+            AIC_HIP_CHECK(hipMemsetAsync(base_low_, 0, sizeof(uint16_t) * static_cast<size_t>(base_arena_), stream_));
+        }
+        AIC_HIP_CHECK(hipMalloc(&q4_, static_cast<size_t>(q4_bytes)));
+        AIC_HIP_CHECK(hipMalloc(&q4s_, sizeof(uint16_t) * static_cast<size_t>(q4_scales)));
+        AIC_HIP_CHECK(hipMemsetAsync(q4_, 0, static_cast<size_t>(q4_bytes), stream_));
+        AIC_HIP_CHECK(hipMemsetAsync(q4s_, 0, sizeof(uint16_t) * static_cast<size_t>(q4_scales), stream_));
+    } else {
+        base_dev_ = params_dev_;
+        base_low_ = low_dev_;
     }
 
     const int64_t hd = d / H, half = hd / 2;
@@ -173,6 +232,9 @@ TransformerLM::~TransformerLM() {
                     static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
                     static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
         if (p) (void)hipFree(p);
+    if (lora())
+        for (void* p : {static_cast<void*>(base_dev_), base_low_, static_cast<void*>(q4_), q4s_})
+            if (p) (void)hipFree(p);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -184,6 +246,7 @@ int64_t TransformerLM::num_params() const {
 
 void TransformerLM::refresh_low_precision() {
     if (low_dev_) hip::cast_f32_bf16(params_dev_, low_dev_, arena_, stream_);
+    if (lora() && base_low_) hip::cast_f32_bf16(base_dev_, base_low_, base_arena_, stream_);
 }
 
 const void* TransformerLM::W(int64_t off) const {
@@ -191,15 +254,61 @@ const void* TransformerLM::W(int64_t off) const {
     return params_dev_ + off;
 }
 
-void TransformerLM::set_params(const float* host) {
-    // host holds the tensors back to back in arena order, without the alignment padding
-    std::vector<float> full(static_cast<size_t>(arena_), 0.0f);
+const void* TransformerLM::WB(int64_t off) const {
+    if (base_low_) return static_cast<const uint16_t*>(base_low_) + off;
+    return base_dev_ + off;
+}
+
+namespace {
+// base-arena offset and element count of projection j (q, k, v, o, gate, up, down)
+void proj_of(int64_t wqkv, int64_t wo, int64_t wgu, int64_t wd, int64_t d, int64_t f, int j, int64_t& off, int64_t& n) {
+    const int64_t offs[7] = {wqkv, wqkv + d * d, wqkv + 2 * d * d, wo, wgu, wgu + f * d, wd};
+    const int64_t ns[7] = {d * d, d * d, d * d, d * d, f * d, f * d, d * f};
+    off = offs[j];
+    n = ns[j];
+}
+}  // namespace
+
+void TransformerLM::quantize_base() {
+    const int64_t d = cfg_.hidden_dim, f = cfg_.intermediate_dim;
+    for (const Layer& ly : layers_)
+        for (int j = 0; j < 7; ++j) {
+            int64_t off, n;
+            proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, off, n);
+            hip::int4_quantize(base_dev_ + off, n, cfg_.quant_group, q4_ + ly.pk[j],
+                               static_cast<uint16_t*>(q4s_) + ly.sc[j], DType::Float16, stream_);
+        }
+}
+
+void TransformerLM::dequant(const Layer& ly, int j, int64_t n, void* dst, hipStream_t s) const {
+    hip::int4_dequant(q4_ + ly.pk[j], static_cast<const uint16_t*>(q4s_) + ly.sc[j], DType::Float16, n,
+                      cfg_.quant_group, dst, cfg_.compute, s);
+}
+
+namespace {
+// host holds the tensors back to back in list order, without the alignment padding
+void scatter_to_device(const float* host, const std::vector<ParamInfo>& ps, int64_t arena, float* dev, hipStream_t s) {
+    std::vector<float> full(static_cast<size_t>(arena), 0.0f);
     int64_t src = 0;
-    for (const auto& p : params_) {
+    for (const auto& p : ps) {
         std::memcpy(full.data() + p.offset, host + src, sizeof(float) * static_cast<size_t>(p.numel));
         src += p.numel;
     }
-    AIC_HIP_CHECK(hipMemcpyAsync(params_dev_, full.data(), sizeof(float) * full.size(), hipMemcpyHostToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(dev, full.data(), sizeof(float) * full.size(), hipMemcpyHostToDevice, s));
+    AIC_HIP_CHECK(hipStreamSynchronize(s));
+}
+}  // namespace
+
+void TransformerLM::set_params(const float* host) {
+    scatter_to_device(host, params_, arena_, params_dev_, stream_);
+    refresh_low_precision();
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void TransformerLM::set_base_params(const float* host) {
+    AIC_CHECK(lora(), InvalidState, "set_base_params: the model has no frozen base (lora_rank == 0); use set_params");
+    scatter_to_device(host, base_, base_arena_, base_dev_, stream_);
+    quantize_base();
     refresh_low_precision();
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
 }
@@ -234,16 +343,25 @@ void TransformerLM::get_adam_state(float* m, float* v, int64_t* step) const {
 void TransformerLM::init_normal(uint64_t seed, float std, bool residual_scaling) {
     const float rs = residual_scaling ? 1.0f / std::sqrt(2.0f * static_cast<float>(cfg_.num_layers)) : 1.0f;
     uint64_t off = 0;
-    for (const auto& p : params_) {
+    for (const auto& p : base_params()) {
         const bool is_norm = p.shape.size() == 1;
         if (is_norm) {
-            hip::fill_const(params_dev_ + p.offset, p.numel, 1.0f, stream_);
+            hip::fill_const(base_dev_ + p.offset, p.numel, 1.0f, stream_);
         } else {
             const bool resid = p.name.find("out_proj") != std::string::npos ||
                                p.name.find("down_proj") != std::string::npos;
-            hip::fill_normal(params_dev_ + p.offset, p.numel, seed, off, 0.0f, std * (resid ? rs : 1.0f), stream_);
+            hip::fill_normal(base_dev_ + p.offset, p.numel, seed, off, 0.0f, std * (resid ? rs : 1.0f), stream_);
         }
         off += static_cast<uint64_t>(p.numel);
+    }
+    if (lora()) {
+        // the QLoRA configuration: A ~ N(0, std), B = 0, so the adapted model starts as the base
+        quantize_base();
+        for (const auto& p : params_) {
+            if (p.name.find("lora_B") != std::string::npos) hip::fill_const(params_dev_ + p.offset, p.numel, 0.0f, stream_);
+            else hip::fill_normal(params_dev_ + p.offset, p.numel, seed, off, 0.0f, std, stream_);
+            off += static_cast<uint64_t>(p.numel);
+        }
     }
     refresh_low_precision();
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
@@ -273,15 +391,42 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                  h2 = act(L * T * d), gu = act(moe ? 0 : L * T * 2 * f), am = act(moe ? 0 : L * T * f);
     DeviceBuffer r1 = f32(L * T), r2 = f32(L * T), lse = f32(L * T * H);
     DeviceBuffer hf = act(T * d), rf = f32(T), logits = act(T * V), lse_ce = f32(T);
+    // QLoRA: each layer's adapter inputs x A^T (q/k/v stacked [T,3r], o [T,r], gate/up [T,2r],
+    // down [T,r]) kept for the backward, and one dequantized projection (or stack) at a time
+    const bool ql = lora();
+    const int64_t r = cfg_.lora_rank;
+    const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
+    DeviceBuffer xa_all = act(ql ? L * T * 7 * r : 0);
+    DeviceBuffer wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
         return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
     };
     auto atf = [&](const DeviceBuffer& b, int64_t elem) { return b.as<float>() + elem; };
+    auto xaq = [&](int64_t l) { return at(xa_all, l * T * 7 * r); };
+    auto xao = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 3 * r); };
+    auto xagu = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 4 * r); };
+    auto xad = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 6 * r); };
+    // a projection's base weight: the arena, or with QLoRA the INT4 copy dequantized into wbuf
+    // (QuantizedLinear::forward, src/nn/quantization.cpp:602-615); projections j0..j1 (q, k, v,
+    // o, gate, up, down) stacked
+    auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
+        if (!ql) return WB(off);
+        int64_t o = 0;
+        for (int j = j0; j <= j1; ++j) {
+            int64_t po, n;
+            proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, po, n);
+            dequant(ly, j, n, static_cast<char*>(wbuf.get()) + es * o, s);
+            o += n;
+        }
+        return wbuf.get();
+    };
+    // the frozen model's gradients are not formed with QLoRA
+    auto GB = [&](int64_t off) -> float* { return ql ? nullptr : G(off); };
 
     // ---- forward (TransformerLM::forward, src/models/transformer_lm.cpp:50-62) ----
     {
         auto _p = prof_.scope(kEmbedFwd, 0.0, 2.0 * es * T * d + 8.0 * T, s);
-        hip::embed_fwd(ids, T, W(emb_), V, d, at(xs, 0), dt, s);
+        hip::embed_fwd(ids, T, WB(emb_), V, d, at(xs, 0), dt, s);
     }
     for (int64_t l = 0; l < L; ++l) {
         const Layer& ly = layers_[l];
@@ -296,9 +441,19 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         void* aml = moe ? nullptr : at(am, l * T * f);
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_fwd(x, d, P(ly.n1), h1l, d, atf(r1, l * T), T, d, eps, dt, s);
+            hip::rmsnorm_fwd(x, d, PB(ly.n1), h1l, d, atf(r1, l * T), T, d, eps, dt, s);
         }
-        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, W(ly.wqkv), d, qkvl, 3 * d, dt, dt, s);
+        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s);
+        if (ql) {
+            // LoRA of q, k, v (LoRALinear::forward, src/nn/lora.cpp:75-93): xa = h1 A^T once for
+            // the stacked A [3r, d], then y_j += s * xa_j B_j^T into each column block
+            void* xa = xaq(l);
+            gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xa, 3 * r, dt, dt, s);
+            const int64_t bs[3] = {ly.bq, ly.bk, ly.bv};
+            for (int j = 0; j < 3; ++j)
+                gemm(prof_, 0, 1, T, d, r, static_cast<char*>(xa) + es * j * r, 3 * r, W(bs[j]), r,
+                     static_cast<char*>(qkvl) + es * j * d, 3 * d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+        }
         {
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
             hip::rope(qkvl, 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, false, dt, s);
@@ -308,29 +463,44 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             hip::attn_fwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
                           d, atf(lse, l * T * H), B, H, S, hd, true, scale, dt, s);
         }
-        gemm(prof_, 0, 1, T, d, d, ol, d, W(ly.wo), d, x1l, d, dt, dt, s, x, d);
+        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d);
+        if (ql) {
+            gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s);
+            gemm(prof_, 0, 1, T, d, r, xao(l), r, W(ly.bo), r, x1l, d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+        }
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_fwd(x1l, d, P(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
+            hip::rmsnorm_fwd(x1l, d, PB(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
         }
         if (moe) {
             // MoELayer::forward (src/nn/moe.cpp:155-253) with the residual x1 added by the combine
             moe_[l]->forward(h2l, T, W(ly.wr), W(ly.wex), x1l, xn, aux_dev_ + l, s);
             continue;
         }
-        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, W(ly.wgu), d, gul, 2 * f, dt, dt, s);
+        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s);
+        if (ql) {
+            void* xa = xagu(l);
+            gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xa, 2 * r, dt, dt, s);
+            gemm(prof_, 0, 1, T, f, r, xa, 2 * r, W(ly.bg), r, gul, 2 * f, dt, dt, s, nullptr, 0, 1.0f, lsc);
+            gemm(prof_, 0, 1, T, f, r, static_cast<char*>(xa) + es * r, 2 * r, W(ly.bu), r,
+                 static_cast<char*>(gul) + es * f, 2 * f, dt, dt, s, nullptr, 0, 1.0f, lsc);
+        }
         {
             auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
             hip::swiglu_fwd(gul, static_cast<char*>(gul) + es * f, 2 * f, aml, f, T, f, dt, s);
         }
-        gemm(prof_, 0, 1, T, d, f, aml, f, W(ly.wd), f, xn, d, dt, dt, s, x1l, d);
+        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d);
+        if (ql) {
+            gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s);
+            gemm(prof_, 0, 1, T, d, r, xad(l), r, W(ly.bd), r, xn, d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+        }
     }
     void* xL = at(xs, L * T * d);
     {
         auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
-        hip::rmsnorm_fwd(xL, d, P(normf_), hf.get(), d, rf.as<float>(), T, d, eps, dt, s);
+        hip::rmsnorm_fwd(xL, d, PB(normf_), hf.get(), d, rf.as<float>(), T, d, eps, dt, s);
     }
-    gemm(prof_, 0, 1, T, V, d, hf.get(), d, W(head_), d, logits.get(), V, dt, dt, s);
+    gemm(prof_, 0, 1, T, V, d, hf.get(), d, WB(head_), d, logits.get(), V, dt, dt, s);
 
     // ---- loss (cross_entropy mean, ignore_index -100, src/loss/cross_entropy.cpp:149-290) ----
     {
@@ -358,13 +528,21 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     }
     void* dl = logits.get();
     DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(moe ? 0 : T * 2 * f),
-                 da = act(moe ? 0 : T * f);
-    gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
-    gemm(prof_, 0, 0, T, d, V, dl, V, W(head_), d, dh.get(), d, dt, dt, s);
+                 da = act(moe ? 0 : T * f), dxa = act(ql ? T * 3 * r : 0);
+    // LoRA backward of one projection (LoRALinear, src/nn/lora.cpp:75-93, through autograd):
+    // with y += s * (x A^T) B^T and xa = x A^T kept from the forward,
+    //   dB = s dy^T xa, dxa = s dy B   (then dA = dxa^T x and dx += dxa A by the caller)
+    auto lora_b_bwd = [&](const void* dy, int64_t lddy, int64_t n_out, const void* xa, int64_t ldxa, int64_t boff,
+                          void* dxa_out, int64_t lddxa) {
+        gemm(prof_, 1, 0, n_out, r, T, dy, lddy, xa, ldxa, G(boff), r, dt, DType::Float32, s, nullptr, 0, 0.0f, lsc);
+        gemm(prof_, 0, 0, T, r, n_out, dy, lddy, W(boff), r, dxa_out, lddxa, dt, dt, s, nullptr, 0, 0.0f, lsc);
+    };
+    if (!ql) gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
+    gemm(prof_, 0, 0, T, d, V, dl, V, WB(head_), d, dh.get(), d, dt, dt, s);
     {
         auto _p = prof_.scope(kNormBwd, 0.0, 3.0 * es * T * d + 4.0 * T, s);
-        hip::rmsnorm_bwd(dh.get(), d, xL, d, P(normf_), rf.as<float>(), nullptr, 0, dx.get(), d, G(normf_), false, T,
-                         d, dt, s);
+        hip::rmsnorm_bwd(dh.get(), d, xL, d, PB(normf_), rf.as<float>(), nullptr, 0, dx.get(), d, GB(normf_), false,
+                         T, d, dt, s);
     }
     for (int64_t l = L - 1; l >= 0; --l) {
         const Layer& ly = layers_[l];
@@ -381,24 +559,43 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             void* gul = at(gu, l * T * 2 * f);
             void* aml = at(am, l * T * f);
             // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
-            gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, f, d, dx.get(), d, W(ly.wd), f, da.get(), f, dt, dt, s);
+            if (!ql) gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s);
+            if (ql) {
+                lora_b_bwd(dx.get(), d, d, xad(l), r, ly.bd, dxa.get(), r);
+                gemm(prof_, 1, 0, r, f, T, dxa.get(), r, aml, f, G(ly.ad), f, dt, DType::Float32, s);
+                gemm(prof_, 0, 0, T, f, r, dxa.get(), r, W(ly.ad), f, da.get(), f, dt, dt, s, nullptr, 0, 1.0f);
+            }
             {
                 auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
                 hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
                                 static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
             }
-            gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, W(ly.wgu), d, dh.get(), d, dt, dt, s);
+            if (!ql) gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s);
+            if (ql) {
+                void* xa = xagu(l);
+                lora_b_bwd(dgu.get(), 2 * f, f, xa, 2 * r, ly.bg, dxa.get(), 2 * r);
+                lora_b_bwd(static_cast<char*>(dgu.get()) + es * f, 2 * f, f, static_cast<char*>(xa) + es * r, 2 * r,
+                           ly.bu, static_cast<char*>(dxa.get()) + es * r, 2 * r);
+                gemm(prof_, 1, 0, 2 * r, d, T, dxa.get(), 2 * r, h2l, d, G(ly.agu), d, dt, DType::Float32, s);
+                gemm(prof_, 0, 0, T, d, 2 * r, dxa.get(), 2 * r, W(ly.agu), d, dh.get(), d, dt, dt, s, nullptr, 0,
+                     1.0f);
+            }
         }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x1l, d, P(ly.n2), atf(r2, l * T), dx.get(), d, dx.get(), d, G(ly.n2), false,
-                             T, d, dt, s);
+            hip::rmsnorm_bwd(dh.get(), d, x1l, d, PB(ly.n2), atf(r2, l * T), dx.get(), d, dx.get(), d, GB(ly.n2),
+                             false, T, d, dt, s);
         }
         // x1 = x + out_proj(attn(rope(q), rope(k), v))
-        gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, d, d, dx.get(), d, W(ly.wo), d, dh.get(), d, dt, dt, s);
+        if (!ql) gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s);
+        if (ql) {
+            lora_b_bwd(dx.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
+            gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, d, r, dxa.get(), r, W(ly.ao), d, dh.get(), d, dt, dt, s, nullptr, 0, 1.0f);
+        }
         {
             // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
             auto _p = prof_.scope(kAttnBwd, 2.0 * attn_flops, 8.0 * es * T * d, s);
@@ -410,15 +607,24 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
             hip::rope(dqkv.get(), 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, true, dt, s);
         }
-        gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, W(ly.wqkv), d, dh.get(), d, dt, dt, s);
+        if (!ql) gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
+        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s);
+        if (ql) {
+            const int64_t bs[3] = {ly.bq, ly.bk, ly.bv};
+            for (int j = 0; j < 3; ++j)
+                lora_b_bwd(static_cast<char*>(dqkv.get()) + es * j * d, 3 * d, d,
+                           static_cast<char*>(xaq(l)) + es * j * r, 3 * r, bs[j],
+                           static_cast<char*>(dxa.get()) + es * j * r, 3 * r);
+            gemm(prof_, 1, 0, 3 * r, d, T, dxa.get(), 3 * r, h1l, d, G(ly.aqkv), d, dt, DType::Float32, s);
+            gemm(prof_, 0, 0, T, d, 3 * r, dxa.get(), 3 * r, W(ly.aqkv), d, dh.get(), d, dt, dt, s, nullptr, 0, 1.0f);
+        }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x, d, P(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, G(ly.n1), false,
+            hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, GB(ly.n1), false,
                              T, d, dt, s);
         }
     }
-    {
+    if (!ql) {
         auto _p = prof_.scope(kEmbedBwd, 0.0, es * T * d + 4.0 * V * d + 8.0 * T, s);
         hip::embed_bwd(ids, T, dx.get(), V, d, G(emb_), cfg_.tie_word_embeddings, dt, s);
     }

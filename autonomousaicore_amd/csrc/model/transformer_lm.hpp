@@ -46,6 +46,13 @@ struct TransformerLMConfig {
     int64_t num_experts = 0;
     int64_t top_k = 2;
     float aux_loss_coef = 0.01f;
+    // QLoRA (LoRAAdapter::apply over QuantizedLinear; src/nn/lora.cpp:116-175,
+    // src/nn/quantization.cpp:669-679): lora_rank > 0 freezes every base weight, keeps the seven
+    // projections of each layer as INT4-symmetric groups of quant_group elements with fp16
+    // scales, and trains only the LoRA adapters (A [r, in], B [out, r], scaling alpha / r).
+    int64_t lora_rank = 0;
+    float lora_alpha = 32.0f;
+    int64_t quant_group = 128;
 };
 
 struct AdamWOptions {
@@ -89,12 +96,18 @@ public:
     TransformerLM& operator=(const TransformerLM&) = delete;
 
     const TransformerLMConfig& config() const { return cfg_; }
+    // Trainable tensors (with QLoRA: the LoRA adapters) and the frozen base model's tensors (the
+    // dense layout; the same list as params() without QLoRA).
     const std::vector<ParamInfo>& params() const { return params_; }
+    const std::vector<ParamInfo>& base_params() const { return lora() ? base_ : params_; }
     int64_t arena_elems() const { return arena_; }
     int64_t num_params() const;
     hipStream_t stream() const { return stream_; }
 
     void set_params(const float* host);
+    // QLoRA: the frozen base weights in base_params() order (packed, no padding); the seven
+    // projections of each layer are then quantized to INT4 (QuantizedLinear::from_linear).
+    void set_base_params(const float* host);
     void get_params(float* host) const;
     void get_grads(float* host) const;
     void get_adam_state(float* m, float* v, int64_t* step) const;
@@ -112,13 +125,23 @@ public:
 
 private:
     struct Layer {
-        int64_t wqkv, wo, wgu, wd, n1, n2;  // arena offsets (wgu / wd: dense FFN)
+        int64_t wqkv, wo, wgu, wd, n1, n2;  // base arena offsets (wgu / wd: dense FFN)
         int64_t wr = 0, wex = 0;            // MoE: router [E, d]; experts, each gate, up, down
+        // QLoRA: adapter offsets in the trainable arena (A of q, k, v stacked [3r, d]; A of
+        // gate, up stacked [2r, d]) and each projection's INT4 bytes / fp16 scales
+        int64_t aqkv = 0, bq = 0, bk = 0, bv = 0, ao = 0, bo = 0, agu = 0, bg = 0, bu = 0, ad = 0, bd = 0;
+        int64_t pk[7] = {}, sc[7] = {};  // q, k, v, o, gate, up, down
     };
     struct DevScalars;
 
+    bool lora() const { return cfg_.lora_rank > 0; }
     void refresh_low_precision();
-    const void* W(int64_t off) const;  // compute-precision weight at arena offset
+    void quantize_base();
+    const void* W(int64_t off) const;   // compute-precision trainable weight at arena offset
+    const void* WB(int64_t off) const;  // compute-precision base weight at base arena offset
+    float* PB(int64_t off) const { return base_dev_ + off; }
+    // dequantizes projection j (q, k, v, o, gate, up, down) of layer l into dst (compute dtype)
+    void dequant(const Layer& ly, int j, int64_t n, void* dst, hipStream_t s) const;
     float* P(int64_t off) const { return params_dev_ + off; }
     float* G(int64_t off) const { return grads_dev_ + off; }
     void forward_backward(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, bool backward,
@@ -127,6 +150,8 @@ private:
     TransformerLMConfig cfg_;
     TrainOptions opt_;
     std::vector<ParamInfo> params_;
+    std::vector<ParamInfo> base_;  // QLoRA: the frozen dense model
+    int64_t base_arena_ = 0;
     std::vector<Layer> layers_;
     int64_t emb_ = 0, normf_ = 0, head_ = 0;
     int64_t arena_ = 0;
@@ -141,6 +166,10 @@ private:
     DevScalars* dev_ = nullptr;
     float* one_dev_ = nullptr;
     float* aux_dev_ = nullptr;  // per-layer MoE aux losses [L]
+    float* base_dev_ = nullptr;  // frozen base weights (fp32); the trainable arena without QLoRA
+    void* base_low_ = nullptr;   // their bf16 shadow (AMP)
+    uint8_t* q4_ = nullptr;      // QLoRA: INT4 projections
+    void* q4s_ = nullptr;        //        and their fp16 scales
     std::vector<std::unique_ptr<MoEFFN>> moe_;
     Profiler prof_;
 };

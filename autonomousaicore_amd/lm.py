@@ -31,6 +31,9 @@ class TransformerLMConfig:
     num_experts: int = 0      # > 0: MoE FFNs (MoETransformerLMConfig)
     top_k: int = 2
     aux_loss_coef: float = 0.01
+    lora_rank: int = 0        # > 0: QLoRA (frozen INT4 base, trained LoRA adapters)
+    lora_alpha: float = 32.0
+    quant_group: int = 128
 
 
 @dataclass
@@ -38,6 +41,16 @@ class MoETransformerLMConfig(TransformerLMConfig):
     """models::MoETransformerLMConfig (include/models/moe_transformer_lm.hpp): the dense
     configuration plus the expert count, router top-k and aux-loss coefficient."""
     num_experts: int = 8
+
+
+@dataclass
+class QLoRATransformerLMConfig(TransformerLMConfig):
+    """A TransformerLM fine-tuned the QLoRA way (LoRAAdapter::apply over
+    QuantizedLinear::from_linear; src/nn/lora.cpp:116-175, src/nn/quantization.cpp:669-679):
+    the base model frozen with its seven projections per layer quantized to INT4 (groups of
+    quant_group, fp16 scales), and rank-lora_rank adapters with scaling lora_alpha / lora_rank
+    on all seven projections as the only trained parameters."""
+    lora_rank: int = 16
 
 
 @dataclass
@@ -87,7 +100,7 @@ class TransformerLM:
         c = _lib.LMConfig(cfg.vocab_size, cfg.hidden_dim, cfg.num_layers, cfg.num_heads, cfg.intermediate_dim,
                           cfg.max_seq_len, cfg.rms_norm_eps, cfg.rope_theta, 1 if cfg.tie_word_embeddings else 0,
                           AIC_BF16 if cfg.compute == "bfloat16" else AIC_F32, cfg.num_experts, cfg.top_k,
-                          cfg.aux_loss_coef)
+                          cfg.aux_loss_coef, cfg.lora_rank, cfg.lora_alpha, cfg.quant_group)
         a, s = train.adamw, train.scaler
         t = _lib.TrainConfig(a.lr, a.beta1, a.beta2, a.eps, a.weight_decay, train.max_grad_norm,
                              1 if train.use_amp else 0, s.initial_scale, s.growth_factor, s.backoff_factor,
@@ -95,7 +108,8 @@ class TransformerLM:
         h = C.c_void_p()
         _lib.call("aic_lm_create", C.byref(c), C.byref(t), C.byref(h))
         self._h = h
-        self.layout = self._layout()
+        self.layout = self._layout("aic_lm_num_tensors", "aic_lm_tensor_info")
+        self.base_layout = self._layout("aic_lm_num_base_tensors", "aic_lm_base_tensor_info")
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -108,16 +122,16 @@ class TransformerLM:
         except Exception:
             pass
 
-    def _layout(self):
+    def _layout(self, count: str, info: str):
         lib = _lib.load()
-        n = lib.aic_lm_num_tensors(self._h)
+        n = getattr(lib, count)(self._h)
         out = []
         name = C.create_string_buffer(256)
         rank = C.c_int()
         dims = (C.c_int64 * 2)()
         off = C.c_int64()
         for i in range(n):
-            _lib.check(lib.aic_lm_tensor_info(self._h, i, name, 256, C.byref(rank), dims, C.byref(off)))
+            _lib.check(getattr(lib, info)(self._h, i, name, 256, C.byref(rank), dims, C.byref(off)))
             out.append((name.value.decode(), tuple(dims[: rank.value]), int(off.value)))
         return out
 
@@ -128,6 +142,16 @@ class TransformerLM:
     def named_parameters(self, flat: np.ndarray):
         """Views of a packed flat array as (name, array) pairs in arena order."""
         return [(n, flat[o:o + int(np.prod(s))].reshape(s)) for n, s, o in self.layout]
+
+    @property
+    def num_base_params(self) -> int:
+        return int(_lib.load().aic_lm_num_base_params(self._h))
+
+    def set_base_params(self, flat: np.ndarray) -> None:
+        """QLoRA: the frozen base model (packed, in base_layout order); quantizes its projections."""
+        flat = np.ascontiguousarray(flat, np.float32)
+        assert flat.size == self.num_base_params
+        _lib.call("aic_lm_set_base_params", self._h, flat.ctypes.data)
 
     def set_params(self, flat: np.ndarray) -> None:
         flat = np.ascontiguousarray(flat, np.float32)

@@ -371,6 +371,14 @@ typedef struct {
                               and the loss is cross_entropy + total_aux_loss (<= 64 experts) */
     int64_t top_k;
     float aux_loss_coef;
+    int64_t lora_rank;     /* 0: full fine-tuning; > 0: QLoRA (LoRAAdapter::apply over
+                              QuantizedLinear::from_linear, src/nn/lora.cpp:116-175,
+                              src/nn/quantization.cpp:669-679): the base model is frozen, the seven
+                              projections of each layer are INT4-symmetric groups of quant_group
+                              elements with fp16 scales, and only rank-lora_rank adapters
+                              (scaling lora_alpha / lora_rank) on all seven are trained */
+    float lora_alpha;
+    int64_t quant_group;
 } aic_lm_config;
 
 typedef struct {
@@ -399,7 +407,17 @@ int aic_lm_num_tensors(const aic_lm* lm);
 /* Name (the reference's parameter name), shape and flat offset of parameter tensor i, in
  * arena order (layer-major; name buffer of name_cap bytes, dims of 2 entries). */
 int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset);
-/* Host <-> device copies of the flat fp32 arenas (synchronous). */
+/* QLoRA: the frozen base model's tensors (the dense model's names, shapes and packed order; with
+ * lora_rank == 0 the same list as aic_lm_tensor_info), and setting them, after which the seven
+ * projections of every layer are quantized again.  InvalidState without QLoRA.
+ * Replaces: loading the base weights before LoRAAdapter::apply (src/nn/lora.cpp:116-175). */
+int64_t aic_lm_num_base_params(const aic_lm* lm);
+int aic_lm_num_base_tensors(const aic_lm* lm);
+int aic_lm_base_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims,
+                            int64_t* offset);
+int aic_lm_set_base_params(aic_lm* lm, const float* host);
+/* Host <-> device copies of the flat fp32 arenas (synchronous); with QLoRA the trainable
+ * arena holds the LoRA adapters only. */
 int aic_lm_set_params(aic_lm* lm, const float* host);
 int aic_lm_get_params(const aic_lm* lm, float* host);
 int aic_lm_get_grads(const aic_lm* lm, float* host);

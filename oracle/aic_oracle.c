@@ -596,6 +596,65 @@ typedef struct {
     float* head;
 } lm_ptrs;
 
+/* QLoRA adapters of one layer (LoRALinear lora_A [r,in], lora_B [out,r]; src/nn/lora.cpp:31-43)
+ * in the packed order of the trainable arena: A of q, k, v; B of q, k, v; A, B of out_proj; A of
+ * gate, up; B of gate, up; A, B of down_proj. */
+typedef struct {
+    float *aq, *ak, *av, *bq, *bk, *bv, *ao, *bo, *ag, *au, *bg, *bu, *ad, *bd;
+} lora_layer;
+
+typedef struct {
+    int64_t r;
+    float s;        /* scaling alpha / r */
+    lora_layer* P;  /* adapters */
+    lora_layer* G;  /* their gradients */
+} lora_ctx;
+
+int64_t orc_qlora_num_params(const orc_lm_config* c, int64_t r) {
+    int64_t d = c->d_model, f = c->d_ffn;
+    return c->n_layers * (8 * r * d + 2 * (r * d + f * r) + r * f + d * r);
+}
+
+static lora_layer* map_lora(const orc_lm_config* c, int64_t r, float* base) {
+    int64_t d = c->d_model, f = c->d_ffn;
+    lora_layer* out = (lora_layer*)xcalloc((size_t)c->n_layers, sizeof(lora_layer));
+    float* cur = base;
+    for (int64_t l = 0; l < c->n_layers; ++l) {
+        lora_layer* a = &out[l];
+        a->aq = cur; cur += r * d;
+        a->ak = cur; cur += r * d;
+        a->av = cur; cur += r * d;
+        a->bq = cur; cur += d * r;
+        a->bk = cur; cur += d * r;
+        a->bv = cur; cur += d * r;
+        a->ao = cur; cur += r * d;
+        a->bo = cur; cur += d * r;
+        a->ag = cur; cur += r * d;
+        a->au = cur; cur += r * d;
+        a->bg = cur; cur += f * r;
+        a->bu = cur; cur += f * r;
+        a->ad = cur; cur += r * f;
+        a->bd = cur; cur += d * r;
+    }
+    return out;
+}
+
+/* One projection y = x W^T, with LoRA when lc != NULL (LoRALinear::forward, lora.cpp:75-93). */
+static void proj_fwd(const lora_ctx* lc, const float* x, const float* W, const float* A, const float* Bm, float* y,
+                     int64_t B, int64_t S, int64_t in, int64_t out) {
+    if (lc) orc_lora_fwd(x, W, A, Bm, lc->s, B, S, in, out, lc->r, y, NULL);
+    else orc_linear_fwd(x, W, y, B, S, in, out);
+}
+
+/* Its backward: dW of a trainable base weight, or with LoRA dA/dB of the adapters and no base
+ * gradient (the base is frozen). */
+static void proj_bwd(const lora_ctx* lc, const float* x, const float* W, const float* A, const float* Bm,
+                     const float* dy, float* dx, float* dW, float* dA, float* dB, int64_t B, int64_t S, int64_t in,
+                     int64_t out) {
+    if (lc) orc_lora_bwd(x, W, A, Bm, lc->s, dy, B, S, in, out, lc->r, dx, dA, dB);
+    else orc_linear_bwd(x, W, dy, dx, dW, B, S, in, out);
+}
+
 int64_t orc_lm_num_params(const orc_lm_config* c) {
     int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, E = c->n_experts;
     int64_t per_layer = 4 * d * d + (E > 0 ? E * d + E * 3 * d * f : 3 * d * f) + 2 * d;
@@ -669,7 +728,8 @@ void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const flo
 /* Forward; returns logits [T, V] (caller frees) and fills acts when non-NULL. */
 static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t* ids, int64_t B, int64_t S,
                          layer_acts* acts, float** hf_out, float** rf_out, float** xf_out,
-                         const float* cos_t, const float* sin_t, orc_step_result* res, float* aux_total) {
+                         const float* cos_t, const float* sin_t, orc_step_result* res, float* aux_total,
+                         const lora_ctx* lc) {
     float aux_sum = 0.0f;
     int have_aux = 0;
     int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, H = c->n_heads, hd = d / H, T = B * S;
@@ -697,14 +757,15 @@ static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t
         float* E = acts ? (float*)xcalloc((size_t)(B * H * S * S), sizeof(float)) : NULL;
         float* rs = acts ? (float*)xcalloc((size_t)(B * H * S), sizeof(float)) : NULL;
 
+        const lora_layer* LA = lc ? &lc->P[l] : NULL;
         orc_rmsnorm_fwd(x, L->n1, h1, r1, T, d, c->norm_eps);
-        orc_linear_fwd(h1, L->wq, q, B, S, d, d);
-        orc_linear_fwd(h1, L->wk, k, B, S, d, d);
-        orc_linear_fwd(h1, L->wv, v, B, S, d, d);
+        proj_fwd(lc, h1, L->wq, LA ? LA->aq : NULL, LA ? LA->bq : NULL, q, B, S, d, d);
+        proj_fwd(lc, h1, L->wk, LA ? LA->ak : NULL, LA ? LA->bk : NULL, k, B, S, d, d);
+        proj_fwd(lc, h1, L->wv, LA ? LA->av : NULL, LA ? LA->bv : NULL, v, B, S, d, d);
         orc_rope_fwd(q, cos_t, sin_t, B, S, H, hd, 0);
         orc_rope_fwd(k, cos_t, sin_t, B, S, H, hd, 0);
         orc_attention_fwd(q, k, v, ctx, E, rs, B, S, H, hd, 1);
-        orc_linear_fwd(ctx, L->wo, att, B, S, d, d);
+        proj_fwd(lc, ctx, L->wo, LA ? LA->ao : NULL, LA ? LA->bo : NULL, att, B, S, d, d);
         add_into(x1, x, att, (int64_t)Td);
         orc_rmsnorm_fwd(x1, L->n2, h2, r2, T, d, c->norm_eps);
         if (c->n_experts > 0) {
@@ -720,10 +781,10 @@ static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t
             have_aux = 1;
             free(wg); free(wu); free(wd);
         } else {
-            orc_linear_fwd(h2, L->wg, g, B, S, d, f);
-            orc_linear_fwd(h2, L->wu, u, B, S, d, f);
+            proj_fwd(lc, h2, L->wg, LA ? LA->ag : NULL, LA ? LA->bg : NULL, g, B, S, d, f);
+            proj_fwd(lc, h2, L->wu, LA ? LA->au : NULL, LA ? LA->bu : NULL, u, B, S, d, f);
             orc_swiglu_fwd(g, u, hm, (int64_t)Tf);
-            orc_linear_fwd(hm, L->wd, ffo, B, S, f, d);
+            proj_fwd(lc, hm, L->wd, LA ? LA->ad : NULL, LA ? LA->bd : NULL, ffo, B, S, f, d);
         }
         float* x2 = (float*)xcalloc(Td, sizeof(float));
         add_into(x2, x1, ffo, (int64_t)Td);
@@ -766,26 +827,36 @@ float orc_lm_loss(const orc_lm_config* c, const float* params, const int64_t* id
     float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
     orc_rope_tables(cos_t, sin_t, S, hd, c->rope_base);
     float aux = 0.0f;
-    float* logits = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL, &aux);
+    float* logits = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL, &aux, NULL);
     float loss = orc_ce_fwd(logits, targets, B * S, c->vocab, -100, NULL, NULL, NULL);
     if (c->n_experts > 0) loss = loss + aux;
     free(logits); free(cos_t); free(sin_t); free(P.layers);
     return loss;
 }
 
-int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, float* v, int64_t* step_count,
-                const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* o,
-                orc_scaler* scaler, orc_step_result* res) {
+/* The step on the dense parameters `params`; without LoRA (lc == NULL) the trainable tensors are
+ * params themselves (gradients into grads), with LoRA they are the adapters of lc (trainable /
+ * tgrads of nt elements) and params is the frozen base. */
+static int lm_step_core(const orc_lm_config* c, float* params, float* grads, const lora_ctx* lc, float* trainable,
+                        float* tgrads, int64_t nt, float* m, float* v, int64_t* step_count, const int64_t* ids,
+                        const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* o, orc_scaler* scaler,
+                        orc_step_result* res) {
     orc_step_result local;
     if (!res) res = &local;
     memset(res, 0, sizeof(*res));
     if (S > c->max_seq_len) return -1;
     int64_t d = c->d_model, f = c->d_ffn, V = c->vocab, H = c->n_heads, hd = d / H, T = B * S;
     size_t Td = (size_t)(T * d), Tf = (size_t)(T * f);
-    int64_t np = orc_lm_num_params(c);
+    const int64_t np = nt;
     lm_ptrs P = map_params(c, params);
-    memset(grads, 0, sizeof(float) * (size_t)np);
-    lm_ptrs G = map_params(c, grads);
+    memset(tgrads, 0, sizeof(float) * (size_t)nt);
+    lm_ptrs G;
+    if (grads) {
+        G = map_params(c, grads);
+    } else { /* frozen base: no gradient buffers */
+        memset(&G, 0, sizeof(G));
+        G.layers = (layer_ptrs*)xcalloc((size_t)c->n_layers, sizeof(layer_ptrs));
+    }
 
     float* cos_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
     float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
@@ -794,7 +865,7 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
     layer_acts* acts = (layer_acts*)xcalloc((size_t)c->n_layers, sizeof(layer_acts));
     float *hf, *rf, *xf;
     float aux = 0.0f;
-    float* logits = lm_forward(c, &P, ids, B, S, acts, &hf, &rf, &xf, cos_t, sin_t, res, &aux);
+    float* logits = lm_forward(c, &P, ids, B, S, acts, &hf, &rf, &xf, cos_t, sin_t, res, &aux, lc);
 
     /* loss (+ total_aux_loss for MoE, tests/unit/test_moe.cpp:224-228) */
     double tl0 = now_s();
@@ -835,6 +906,8 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
         layer_ptrs* L = &P.layers[l];
         layer_ptrs* GL = &G.layers[l];
         layer_acts* A = &acts[l];
+        const lora_layer* LA = lc ? &lc->P[l] : NULL;
+        const lora_layer* LG = lc ? &lc->G[l] : NULL;
         if (c->n_experts > 0) {
             /* x2 = x1 + moe(h2); d loss / d aux_l = 1 (scaled with the loss) */
             const int64_t E = c->n_experts, efd = E * f * d;
@@ -852,23 +925,30 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
             free(wg); free(wu); free(wd); free(dwg); free(dwu); free(dwd);
         } else {
             /* x2 = x1 + down(hm): dx is grad of x2 */
-            orc_linear_bwd(A->hm, L->wd, dx, dhm, GL->wd, B, S, f, d);
+            proj_bwd(lc, A->hm, L->wd, LA ? LA->ad : NULL, LA ? LA->bd : NULL, dx, dhm, GL->wd, LG ? LG->ad : NULL,
+                     LG ? LG->bd : NULL, B, S, f, d);
             orc_swiglu_bwd(A->g, A->u, dhm, dg, du, (int64_t)Tf);
-            orc_linear_bwd(A->h2, L->wg, dg, tmp, GL->wg, B, S, d, f);
-            orc_linear_bwd(A->h2, L->wu, du, tmp2, GL->wu, B, S, d, f);
+            proj_bwd(lc, A->h2, L->wg, LA ? LA->ag : NULL, LA ? LA->bg : NULL, dg, tmp, GL->wg, LG ? LG->ag : NULL,
+                     LG ? LG->bg : NULL, B, S, d, f);
+            proj_bwd(lc, A->h2, L->wu, LA ? LA->au : NULL, LA ? LA->bu : NULL, du, tmp2, GL->wu, LG ? LG->au : NULL,
+                     LG ? LG->bu : NULL, B, S, d, f);
             add_into(tmp, tmp, tmp2, (int64_t)Td); /* grad of h2 (engine accumulation) */
         }
         orc_rmsnorm_bwd(tmp, A->x1, L->n2, A->r2, tmp2, GL->n2, T, d);
         add_into(dx, dx, tmp2, (int64_t)Td); /* grad of x1 = residual + norm path */
         /* x1 = x + out_proj(ctx) */
-        orc_linear_bwd(A->ctx, L->wo, dx, tmp, GL->wo, B, S, d, d);
+        proj_bwd(lc, A->ctx, L->wo, LA ? LA->ao : NULL, LA ? LA->bo : NULL, dx, tmp, GL->wo, LG ? LG->ao : NULL,
+                 LG ? LG->bo : NULL, B, S, d, d);
         orc_attention_bwd(A->q, A->k, A->v, A->E, A->rs, tmp, dq, dk, dv, B, S, H, hd);
         orc_rope_bwd(dq, cos_t, sin_t, B, S, H, hd, 0);
         orc_rope_bwd(dk, cos_t, sin_t, B, S, H, hd, 0);
-        orc_linear_bwd(A->h1, L->wq, dq, tmp, GL->wq, B, S, d, d);
-        orc_linear_bwd(A->h1, L->wk, dk, tmp2, GL->wk, B, S, d, d);
+        proj_bwd(lc, A->h1, L->wq, LA ? LA->aq : NULL, LA ? LA->bq : NULL, dq, tmp, GL->wq, LG ? LG->aq : NULL,
+                 LG ? LG->bq : NULL, B, S, d, d);
+        proj_bwd(lc, A->h1, L->wk, LA ? LA->ak : NULL, LA ? LA->bk : NULL, dk, tmp2, GL->wk, LG ? LG->ak : NULL,
+                 LG ? LG->bk : NULL, B, S, d, d);
         add_into(tmp, tmp, tmp2, (int64_t)Td);
-        orc_linear_bwd(A->h1, L->wv, dv, tmp2, GL->wv, B, S, d, d);
+        proj_bwd(lc, A->h1, L->wv, LA ? LA->av : NULL, LA ? LA->bv : NULL, dv, tmp2, GL->wv, LG ? LG->av : NULL,
+                 LG ? LG->bv : NULL, B, S, d, d);
         add_into(tmp, tmp, tmp2, (int64_t)Td);
         orc_rmsnorm_bwd(tmp, A->x, L->n1, A->r1, tmp2, GL->n1, T, d);
         add_into(dx, dx, tmp2, (int64_t)Td);
@@ -877,7 +957,7 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
     }
     double tl3 = now_s();
     res->t_blocks_bwd = tl3 - tl2;
-    orc_embedding_bwd(ids, dx, G.emb, T, d, V);
+    if (G.emb) orc_embedding_bwd(ids, dx, G.emb, T, d, V);
     double tl4 = now_s();
     res->t_embed_bwd = tl4 - tl3;
     free(tmp); free(tmp2); free(dhm); free(dg); free(du); free(dq); free(dk); free(dv); free(dx); free(dh);
@@ -885,7 +965,7 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
 
     /* optimizer tail: [scaler] -> clip -> AdamW (src/train/trainer.cpp:70-95) */
     double to0 = now_s();
-    float* gp[1] = {grads};
+    float* gp[1] = {tgrads};
     int64_t gs[1] = {np};
     int ok = 1;
     if (o->use_scaler && scaler) ok = orc_scaler_unscale_and_update(scaler, gp, gs, 1);
@@ -895,18 +975,75 @@ int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, f
             res->grad_norm = orc_clip_grad_norm(gp, gs, 1, o->max_grad_norm);
         } else {
             double s = 0.0;
-            for (int64_t i = 0; i < np; ++i) s += (double)grads[i] * (double)grads[i];
+            for (int64_t i = 0; i < np; ++i) s += (double)tgrads[i] * (double)tgrads[i];
             res->grad_norm = (float)sqrt(s);
         }
         if (o->do_update) {
             *step_count += 1;
-            orc_adamw(params, grads, m, v, np, o->lr, o->beta1, o->beta2, o->eps, o->weight_decay, *step_count);
+            orc_adamw(trainable, tgrads, m, v, np, o->lr, o->beta1, o->beta2, o->eps, o->weight_decay, *step_count);
         }
     }
     res->t_optim = now_s() - to0;
     free(P.layers);
     free(G.layers);
     return 0;
+}
+
+int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, float* v, int64_t* step_count,
+                const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* o,
+                orc_scaler* scaler, orc_step_result* res) {
+    return lm_step_core(c, params, grads, NULL, params, grads, orc_lm_num_params(c), m, v, step_count, ids, targets,
+                        B, S, o, scaler, res);
+}
+
+/* QuantizedLinear::from_linear then forward's dequantization (src/nn/quantization.cpp:602-615,
+ * 669-679) of the seven projections of every layer of the dense parameters, in place: INT4
+ * symmetric groups of G with fp16 scales. */
+int orc_qlora_dequantize_base(const orc_lm_config* c, int64_t G, float* params) {
+    if (c->n_experts > 0) return -1;
+    lm_ptrs P = map_params(c, params);
+    const int64_t d = c->d_model, f = c->d_ffn;
+    uint8_t* pk = (uint8_t*)xcalloc((size_t)(f * d / 2 + d * d / 2 + 1), 1);
+    uint16_t* sc = (uint16_t*)xcalloc((size_t)((f * d + d * d) / G + 1), sizeof(uint16_t));
+    int rc = 0;
+    for (int64_t l = 0; l < c->n_layers && rc == 0; ++l) {
+        layer_ptrs* L = &P.layers[l];
+        float* w[7] = {L->wq, L->wk, L->wv, L->wo, L->wg, L->wu, L->wd};
+        const int64_t n[7] = {d * d, d * d, d * d, d * d, f * d, f * d, d * f};
+        for (int j = 0; j < 7 && rc == 0; ++j) {
+            rc = orc_int4_quantize(w[j], n[j], G, 1, pk, sc);
+            if (rc == 0) rc = orc_int4_dequantize(pk, sc, 1, n[j], G, w[j]);
+        }
+    }
+    free(pk);
+    free(sc);
+    free(P.layers);
+    return rc;
+}
+
+/* The QLoRA step: base (dense layout) is frozen; its projections are the INT4 round trip of
+ * orc_qlora_dequantize_base, done here on a copy; only the adapters `lora` are trained. */
+int orc_qlora_step(const orc_lm_config* c, int64_t r, float alpha, int64_t G, const float* base, float* lora,
+                   float* grads, float* m, float* v, int64_t* step_count, const int64_t* ids, const int64_t* targets,
+                   int64_t B, int64_t S, const orc_train_opts* o, orc_scaler* scaler, orc_step_result* res) {
+    if (c->n_experts > 0 || r <= 0) return -1;
+    const int64_t np = orc_lm_num_params(c), nl = orc_qlora_num_params(c, r);
+    float* w = (float*)xcalloc((size_t)np, sizeof(float));
+    memcpy(w, base, sizeof(float) * (size_t)np);
+    int rc = orc_qlora_dequantize_base(c, G, w);
+    if (rc == 0) {
+        lora_ctx lc;
+        lc.r = r;
+        lc.s = alpha / (float)r;
+        lc.P = map_lora(c, r, lora);
+        memset(grads, 0, sizeof(float) * (size_t)nl);
+        lc.G = map_lora(c, r, grads);
+        rc = lm_step_core(c, w, NULL, &lc, lora, grads, nl, m, v, step_count, ids, targets, B, S, o, scaler, res);
+        free(lc.P);
+        free(lc.G);
+    }
+    free(w);
+    return rc;
 }
 
 /* ======================================================================================

@@ -180,6 +180,18 @@ int orc_lm_step(const orc_lm_config* cfg, float* params, float* grads, float* m,
                 const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* opts,
                 orc_scaler* scaler, orc_step_result* res);
 
+/* QLoRA TransformerLM step (LoRAAdapter::apply over QuantizedLinear::from_linear,
+ * src/nn/lora.cpp:116-175, src/nn/quantization.cpp:669-679; dense FFN only).  base: the dense
+ * parameters (orc_lm_num_params, frozen); the seven projections of each layer enter as their INT4
+ * round trip (groups of G, fp16 scales).  lora: orc_qlora_num_params adapters, per layer A of
+ * q, k, v [r,d]; B of q, k, v [d,r]; A, B of out_proj; A of gate, up [r,d]; B of gate, up
+ * [f,r]; A of down [r,f]; B of down [d,r]; scaling alpha / r.  grads/m/v: adapter-sized. */
+int64_t orc_qlora_num_params(const orc_lm_config* cfg, int64_t r);
+int orc_qlora_dequantize_base(const orc_lm_config* cfg, int64_t G, float* params);
+int orc_qlora_step(const orc_lm_config* cfg, int64_t r, float alpha, int64_t G, const float* base, float* lora,
+                   float* grads, float* m, float* v, int64_t* step_count, const int64_t* ids, const int64_t* targets,
+                   int64_t B, int64_t S, const orc_train_opts* opts, orc_scaler* scaler, orc_step_result* res);
+
 /* ---- Mixture of experts (src/nn/moe.cpp) ---- */
 /* Router on gate logits [T,E] (moe.cpp:33-129) plus the gate normalisation of MoELayer::forward
  * (moe.cpp:170-204); top-k ties go to the lower expert index.  Any output may be NULL. */

@@ -64,6 +64,7 @@ def lib():
         L.orc_clip_grad_norm.restype = C.c_float
         L.orc_lm_loss.restype = C.c_float
         L.orc_lm_num_params.restype = C.c_int64
+        L.orc_qlora_num_params.restype = C.c_int64
         L.orc_get_threads.restype = C.c_int
         _lib = L
     return _lib
@@ -314,6 +315,44 @@ def lm_step(cfg, params, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps
                            C.byref(res))
     if rc != 0:
         raise RuntimeError(f"orc_lm_step failed with {rc}")
+    return res, grads, m, v, int(stepc.value)
+
+
+def qlora_num_params(cfg: LMConfig, r: int) -> int:
+    return int(lib().orc_qlora_num_params(C.byref(cfg), C.c_int64(r)))
+
+
+def qlora_dequantize_base(cfg, G, params):
+    """The dense parameters with every layer's seven projections replaced by their INT4 round trip
+    (groups of G, fp16 scales)."""
+    out = np.ascontiguousarray(params, np.float32).copy()
+    rc = lib().orc_qlora_dequantize_base(C.byref(cfg), C.c_int64(G), _f(out))
+    if rc != 0:
+        raise RuntimeError(f"orc_qlora_dequantize_base failed with {rc}")
+    return out
+
+
+def qlora_step(cfg, r, alpha, G, base, lora, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+               weight_decay=0.1, max_grad_norm=1.0, m=None, v=None, step=0, scaler: LossScaler | None = None,
+               do_update=True):
+    """One QLoRA step in place on `lora` (float32 flat adapters); base is frozen.
+    Returns (result, grads, m, v, step)."""
+    n = qlora_num_params(cfg, r)
+    assert lora.size == n and lora.dtype == np.float32
+    base = np.ascontiguousarray(base, np.float32)
+    assert base.size == num_params(cfg)
+    grads = np.zeros(n, np.float32)
+    m = np.zeros(n, np.float32) if m is None else m
+    v = np.zeros(n, np.float32) if v is None else v
+    stepc = C.c_int64(step)
+    opts = TrainOpts(lr, beta1, beta2, eps, weight_decay, max_grad_norm, 1 if scaler else 0, 1 if do_update else 0)
+    res = StepResult()
+    rc = lib().orc_qlora_step(C.byref(cfg), C.c_int64(r), C.c_float(alpha), C.c_int64(G), _f(base), _f(lora),
+                              _f(grads), _f(m), _f(v), C.byref(stepc), _i(np.ascontiguousarray(ids, np.int64)),
+                              _i(np.ascontiguousarray(targets, np.int64)), C.c_int64(B), C.c_int64(S),
+                              C.byref(opts), C.byref(scaler.s) if scaler else None, C.byref(res))
+    if rc != 0:
+        raise RuntimeError(f"orc_qlora_step failed with {rc}")
     return res, grads, m, v, int(stepc.value)
 
 

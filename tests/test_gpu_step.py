@@ -239,3 +239,134 @@ def test_moe_bf16_amp_step_close_to_fp32_oracle(orc):
     assert abs(st.aux_loss - res.aux_loss) < 3e-2 * abs(res.aux_loss)
     assert st.loss_scale == 65536.0 and not st.found_inf
     assert abs(st.grad_norm - res.grad_norm) / res.grad_norm < 5e-2
+
+
+# ----------------------------------------------------------------------------- QLoRA
+def build_qlora(cfg, r, alpha, G, compute="float32", amp=False, lr=3e-4):
+    c = aic.QLoRATransformerLMConfig(vocab_size=cfg["vocab"], hidden_dim=cfg["d"], num_layers=cfg["L"],
+                                     num_heads=cfg["H"], intermediate_dim=cfg["f"], max_seq_len=2048,
+                                     rms_norm_eps=1e-6, tie_word_embeddings=cfg["tied"], compute=compute,
+                                     lora_rank=r, lora_alpha=alpha, quant_group=G)
+    t = aic.TrainingConfig(adamw=aic.AdamWOptions(lr=lr, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1),
+                           max_grad_norm=1.0, use_amp=amp)
+    return aic.TransformerLM(c, t)
+
+
+def make_base(model, seed, std=0.05):
+    out = []
+    for i, (name, shape, off) in enumerate(model.base_layout):
+        n = int(np.prod(shape))
+        out.append(np.ones(n, np.float32) if len(shape) == 1 else aic.normal(seed + 7919 * i, n, 0.0, std))
+    return np.concatenate(out)
+
+
+def make_lora(model, seed, b_std):
+    out = []
+    for i, (name, shape, off) in enumerate(model.layout):
+        n = int(np.prod(shape))
+        out.append(aic.normal(seed + 104729 * i, n, 0.0, b_std if "lora_B" in name else 0.05))
+    return np.concatenate(out)
+
+
+QL = dict(vocab=512, d=128, L=2, H=4, f=352, tied=False)
+
+
+@pytest.mark.parametrize("r,alpha,G,tied", [(16, 32.0, 128, False), (8, 16.0, 64, True)])
+def test_qlora_fp32_step_matches_oracle(orc, r, alpha, G, tied):
+    """Frozen INT4 base (fp16 scales), LoRA on all seven projections, only the adapters trained:
+    loss, global norm, adapter gradients, AdamW state and updated adapters against the oracle."""
+    cfg = dict(QL, tied=tied)
+    B, S = 4, 64
+    model = build_qlora(cfg, r, alpha, G)
+    names = [n for n, _, _ in model.layout]
+    assert len(names) == 14 * cfg["L"] and all(".lora_" in n for n in names)
+    base = make_base(model, 31)
+    lora = make_lora(model, 37, 0.02)
+    model.set_base_params(base)
+    model.set_params(lora)
+    ids, tgt = aic.batch(4321, B, S, cfg["vocab"])
+    st = model.train_step(ids, tgt, B, S)
+    ocfg = oracle_cfg(orc, cfg, S)
+    assert orc.qlora_num_params(ocfg, r) == lora.size == model.num_params
+    p = lora.copy()
+    res, g_ref, m_ref, v_ref, step = orc.qlora_step(ocfg, r, alpha, G, base, p, ids, tgt, B, S)
+    assert abs(st.loss - res.loss) / abs(res.loss) < 1e-5
+    assert abs(st.grad_norm - res.grad_norm) / res.grad_norm < 1e-4
+    assert st.step == 1 and not st.found_inf
+    check_tensors(model, model.get_grads() * min(1.0, 1.0 / (st.grad_norm + 1e-6)), g_ref, 1e-4, "grad")
+    check_tensors(model, model.get_params(), p, 1e-4, "param")
+    m, v, s = model.get_adam_state()
+    check_tensors(model, m, m_ref, 1e-4, "exp_avg")
+    check_tensors(model, v, v_ref, 1e-4, "exp_avg_sq")
+    # a second step on the updated adapters
+    ids, tgt = aic.batch(4322, B, S, cfg["vocab"])
+    st = model.train_step(ids, tgt, B, S)
+    res, _, _, _, _ = orc.qlora_step(ocfg, r, alpha, G, base, p, ids, tgt, B, S, m=m_ref, v=v_ref, step=step)
+    assert abs(st.loss - res.loss) / abs(res.loss) < 1e-5
+    check_tensors(model, model.get_params(), p, 1e-4, "param after 2 steps")
+    model.close()
+
+
+def test_qlora_zero_b_equals_dense_model_on_dequantized_base(orc):
+    """B = 0 (the reference's LoRA initialisation): the QLoRA model's loss is bit-identical to
+    the dense model's loss on the INT4 round trip of the base, on the GPU and in the oracle."""
+    cfg = QL
+    B, S, r, G = 4, 64, 16, 128
+    model = build_qlora(cfg, r, 32.0, G)
+    base = make_base(model, 41)
+    model.set_base_params(base)
+    model.set_params(make_lora(model, 43, 0.0))
+    ids, tgt = aic.batch(55, B, S, cfg["vocab"])
+    loss_q = model.eval_loss(ids, tgt, B, S)
+    model.close()
+    ocfg = oracle_cfg(orc, cfg, S)
+    deq = orc.qlora_dequantize_base(ocfg, G, base)
+    dense = build(cfg)
+    dense.set_params(deq)
+    loss_d = dense.eval_loss(ids, tgt, B, S)
+    dense.close()
+    assert loss_q == loss_d
+    assert abs(loss_q - orc.lm_loss(ocfg, deq, ids, tgt, B, S)) / loss_d < 1e-5
+
+
+def test_qlora_bf16_amp_step_close_to_fp32_oracle(orc):
+    """The QLoRA configuration's adapter shape (rank 16, alpha 32, groups of 128) on scaled
+    widths (d 256, 4 heads, SwiGLU 704, vocab 32000, 2 layers), bf16 AMP with loss scaling,
+    against the fp32 oracle; and bit-identical on a second run."""
+    cfg = dict(vocab=32000, d=256, L=2, H=4, f=704, tied=False)
+    B, S, r, alpha, G = 2, 256, 16, 32.0, 128
+    outs = []
+    for _ in range(2):
+        model = build_qlora(cfg, r, alpha, G, compute="bfloat16", amp=True)
+        base = make_base(model, 61, 0.02)
+        lora = make_lora(model, 67, 0.02)
+        model.set_base_params(base)
+        model.set_params(lora)
+        ids, tgt = aic.batch(71, B, S, cfg["vocab"], dist="zipf")
+        st = model.train_step(ids, tgt, B, S)
+        outs.append((st, model.get_grads(), model.get_params()))
+        model.close()
+    st = outs[0][0]
+    assert outs[1][0].loss == st.loss
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    np.testing.assert_array_equal(outs[0][2], outs[1][2])
+    ocfg = oracle_cfg(orc, cfg, S)
+    res, _, _, _, _ = orc.qlora_step(ocfg, r, alpha, G, base, lora.copy(), ids, tgt, B, S)
+    assert abs(st.loss - res.loss) / abs(res.loss) < 1e-2
+    assert st.loss_scale == 65536.0 and not st.found_inf
+    assert abs(st.grad_norm - res.grad_norm) / res.grad_norm < 5e-2
+
+
+def test_qlora_rejects_bad_configurations():
+    with pytest.raises(aic.AicError):
+        build_qlora(dict(QL), 16, 32.0, 127)          # odd group
+    with pytest.raises(aic.AicError):
+        build_qlora(dict(QL), 16, 32.0, 96)           # does not divide d*d
+    c = aic.QLoRATransformerLMConfig(vocab_size=512, hidden_dim=128, num_layers=2, num_heads=4,
+                                     intermediate_dim=352, num_experts=4)
+    with pytest.raises(aic.AicError):
+        aic.TransformerLM(c)
+    dense = build(QL)
+    with pytest.raises(aic.AicError):
+        dense.set_base_params(np.zeros(dense.num_params, np.float32))
+    dense.close()

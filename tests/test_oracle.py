@@ -732,3 +732,80 @@ def test_moe_lm_step_vs_torch(orc, E, k):
         assert rel(grads[off:off + n], grads_t[off:off + n]) < tol, name
         off += n
     assert rel(p, new_t) < 1e-4
+
+
+def _qlora_case(rng, vocab, d, L, f, r, b_std):
+    lay = torch_ref.layout(vocab, d, L, f, False)
+    base = np.concatenate([(np.ones(s) if len(s) == 1 else rng.standard_normal(s) * 0.2).ravel()
+                           for _, s in lay]).astype(np.float32)
+    lora = np.concatenate([(rng.standard_normal(s) * (b_std if "lora_B" in n else 0.2)).ravel()
+                           for n, s in torch_ref.lora_layout(d, L, f, r)]).astype(np.float32)
+    return lay, base, lora
+
+
+def test_qlora_base_round_trip_matches_numpy(orc):
+    # the seven projections of every layer become their INT4 round trip (fp16 scales); embeddings,
+    # norms and the head stay as they are
+    vocab, d, L, f, G = 64, 32, 2, 48, 16
+    rng = np.random.default_rng(77)
+    lay, base, _ = _qlora_case(rng, vocab, d, L, f, 4, 0.0)
+    cfg = orc.make_config(vocab, d, L, 2, f, 16)
+    out = orc.qlora_dequantize_base(cfg, G, base)
+    off = 0
+    for name, shape in lay:
+        n = int(np.prod(shape))
+        want = base[off:off + n]
+        if any(p + ".weight" in name for p in torch_ref.PROJ):
+            want = torch_ref.int4_round_trip(want, G)
+            assert not np.array_equal(want, base[off:off + n])
+        np.testing.assert_array_equal(out[off:off + n], want, err_msg=name)
+        off += n
+
+
+def test_qlora_zero_b_is_the_quantized_dense_model(orc):
+    # LoRA B = 0 (the reference's initialisation, tests/unit/test_lora.cpp:58-73): the loss is the
+    # dense model's on the dequantized base, bit for bit, and every lora_A gradient is zero
+    vocab, d, L, H, f, B, S, r, G = 64, 32, 2, 2, 48, 2, 16, 4, 32
+    rng = np.random.default_rng(78)
+    lay, base, lora = _qlora_case(rng, vocab, d, L, f, r, 0.0)
+    ids = rng.integers(0, vocab, B * S).astype(np.int64)
+    tgt = np.roll(ids, -1)
+    cfg = orc.make_config(vocab, d, L, H, f, S)
+    dense = orc.qlora_dequantize_base(cfg, G, base)
+    want = orc.lm_loss(cfg, dense, ids, tgt, B, S)
+    res, grads, _, _, _ = orc.qlora_step(cfg, r, 8.0, G, base, lora.copy(), ids, tgt, B, S, do_update=False)
+    assert res.loss == want
+    off = 0
+    for name, shape in torch_ref.lora_layout(d, L, f, r):
+        n = int(np.prod(shape))
+        if "lora_A" in name:
+            assert not grads[off:off + n].any(), name
+        else:
+            assert np.abs(grads[off:off + n]).max() > 0, name
+        off += n
+
+
+@pytest.mark.parametrize("r,alpha,G", [(4, 8.0, 32), (8, 32.0, 16)])
+def test_qlora_lm_step_vs_torch(orc, r, alpha, G):
+    # frozen INT4 base + LoRA on all seven projections: loss, global norm, every adapter gradient
+    # and the AdamW update against a float64 torch model with an independent INT4 round trip
+    vocab, d, L, H, f, B, S = 64, 32, 2, 2, 48, 2, 16
+    rng = np.random.default_rng(80 + r)
+    lay, base, lora = _qlora_case(rng, vocab, d, L, f, r, 0.1)
+    ids = rng.integers(0, vocab, B * S).astype(np.int64)
+    tgt = np.roll(ids, -1)
+    cfg = orc.make_config(vocab, d, L, H, f, S)
+    assert orc.qlora_num_params(cfg, r) == lora.size
+    loss_t, norm_t, grads_t, new_t = torch_ref.lm_step(vocab, d, L, H, f, False, base, ids, tgt, B, S,
+                                                        lora=(lora, r, alpha, G))
+    p = lora.copy()
+    res, grads, m, v, step = orc.qlora_step(cfg, r, alpha, G, base, p, ids, tgt, B, S)
+    assert step == 1
+    assert abs(res.loss - loss_t) / abs(loss_t) < 1e-5
+    assert abs(res.grad_norm - norm_t) / norm_t < 1e-4
+    off = 0
+    for name, shape in torch_ref.lora_layout(d, L, f, r):
+        n = int(np.prod(shape))
+        assert rel(grads[off:off + n], grads_t[off:off + n]) < 1e-4, name
+        off += n
+    assert rel(p, new_t) < 1e-4

@@ -37,6 +37,37 @@ def layout(vocab, d, n_layers, f, tied, n_experts=0):
     return out
 
 
+PROJ = ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.out_proj", "ffn.gate_proj", "ffn.up_proj",
+        "ffn.down_proj")
+
+
+def lora_layout(d, n_layers, f, r):
+    """(name, shape) of the LoRA adapters in the packed order of the trainable arena."""
+    out = []
+    for l in range(n_layers):
+        p = f"layers.{l}."
+        out += [(p + "attn.q_proj.lora_A", (r, d)), (p + "attn.k_proj.lora_A", (r, d)),
+                (p + "attn.v_proj.lora_A", (r, d)), (p + "attn.q_proj.lora_B", (d, r)),
+                (p + "attn.k_proj.lora_B", (d, r)), (p + "attn.v_proj.lora_B", (d, r)),
+                (p + "attn.out_proj.lora_A", (r, d)), (p + "attn.out_proj.lora_B", (d, r)),
+                (p + "ffn.gate_proj.lora_A", (r, d)), (p + "ffn.up_proj.lora_A", (r, d)),
+                (p + "ffn.gate_proj.lora_B", (f, r)), (p + "ffn.up_proj.lora_B", (f, r)),
+                (p + "ffn.down_proj.lora_A", (r, f)), (p + "ffn.down_proj.lora_B", (d, r))]
+    return out
+
+
+def int4_round_trip(w, G):
+    """INT4-symmetric quantize + dequantize of a flat float32 array in groups of G, fp16 scales
+    (numpy): s = max(absmax / 7, 1e-8) in float32, q = clamp(round half away(w / s), -7, 7),
+    w' = q * float(fp16(s))."""
+    w = np.asarray(w, np.float32).reshape(-1, G)
+    s = np.maximum(np.abs(w).max(axis=1) / np.float32(7.0), np.float32(1e-8)).astype(np.float32)
+    v = (w / s[:, None]).astype(np.float64)
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) + 0.5), -7, 7)
+    s16 = s.astype(np.float16).astype(np.float32)
+    return (q.astype(np.float32) * s16[:, None]).reshape(-1)
+
+
 def rope_tables_np(S, hd, base=10000.0):
     half = hd // 2
     i = np.arange(half, dtype=np.float32)
@@ -56,16 +87,39 @@ def rope(x, cos, sin):
 
 def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, S, eps=1e-6, lr=3e-4,
             betas=(0.9, 0.95), adam_eps=1e-8, weight_decay=0.1, max_grad_norm=1.0, dtype=torch.float64,
-            n_experts=0, top_k=2, aux_coef=0.01):
-    """Returns loss (cross-entropy + the MoE aux losses), pre-clip grad norm, grads, updated params."""
+            n_experts=0, top_k=2, aux_coef=0.01, lora=None):
+    """Returns loss (cross-entropy + the MoE aux losses), pre-clip grad norm, grads, updated params.
+    lora = (lora_flat, r, alpha, G): params_flat is the frozen base, its projections enter as their
+    INT4 round trip, and the LoRA adapters (y += (x A^T) B^T * alpha / r) are the trained tensors."""
     lay = layout(vocab, d, n_layers, f, tied, n_experts)
     P = {}
     off = 0
     for name, shape in lay:
         n = int(np.prod(shape))
-        P[name] = torch.tensor(params_flat[off:off + n].reshape(shape), dtype=dtype, requires_grad=True)
+        w = params_flat[off:off + n]
+        if lora is not None and any(pr + ".weight" in name for pr in PROJ):
+            w = int4_round_trip(w, lora[3])
+        P[name] = torch.tensor(w.reshape(shape), dtype=dtype, requires_grad=lora is None)
         off += n
     assert off == params_flat.size
+    if lora is not None:
+        lay_t = lora_layout(d, n_layers, f, lora[1])
+        off = 0
+        for name, shape in lay_t:
+            n = int(np.prod(shape))
+            P[name] = torch.tensor(lora[0][off:off + n].reshape(shape), dtype=dtype, requires_grad=True)
+            off += n
+        assert off == lora[0].size
+        scaling = lora[2] / lora[1]
+    else:
+        lay_t = lay
+
+    def lin(x, pre):
+        y = F.linear(x, P[pre + ".weight"])
+        if lora is not None:
+            y = y + F.linear(F.linear(x, P[pre + ".lora_A"]), P[pre + ".lora_B"]) * scaling
+        return y
+
     hd = d // n_heads
     cos_np, sin_np = rope_tables_np(S, hd)
     cos = torch.tensor(cos_np, dtype=dtype)[None, None]
@@ -78,13 +132,13 @@ def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, 
     for l in range(n_layers):
         p = f"layers.{l}."
         h = F.rms_norm(x, (d,), P[p + "norm1.weight"], eps)
-        q = F.linear(h, P[p + "attn.q_proj.weight"]).view(B, S, n_heads, hd).transpose(1, 2)
-        k = F.linear(h, P[p + "attn.k_proj.weight"]).view(B, S, n_heads, hd).transpose(1, 2)
-        v = F.linear(h, P[p + "attn.v_proj.weight"]).view(B, S, n_heads, hd).transpose(1, 2)
+        q = lin(h, p + "attn.q_proj").view(B, S, n_heads, hd).transpose(1, 2)
+        k = lin(h, p + "attn.k_proj").view(B, S, n_heads, hd).transpose(1, 2)
+        v = lin(h, p + "attn.v_proj").view(B, S, n_heads, hd).transpose(1, 2)
         q, k = rope(q, cos, sin), rope(k, cos, sin)
         o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         o = o.transpose(1, 2).reshape(B, S, d)
-        x = x + F.linear(o, P[p + "attn.out_proj.weight"])
+        x = x + lin(o, p + "attn.out_proj")
         h = F.rms_norm(x, (d,), P[p + "norm2.weight"], eps)
         if n_experts:
             ex = [(P[p + f"moe.experts.{e}.gate_proj.weight"], P[p + f"moe.experts.{e}.up_proj.weight"],
@@ -93,8 +147,8 @@ def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, 
             x = x + y.reshape(B, S, d)
             aux_total = aux if aux_total is None else aux_total + aux
         else:
-            a = F.silu(F.linear(h, P[p + "ffn.gate_proj.weight"])) * F.linear(h, P[p + "ffn.up_proj.weight"])
-            x = x + F.linear(a, P[p + "ffn.down_proj.weight"])
+            a = F.silu(lin(h, p + "ffn.gate_proj")) * lin(h, p + "ffn.up_proj")
+            x = x + lin(a, p + "ffn.down_proj")
     x = F.rms_norm(x, (d,), P["norm.weight"], eps)
     head = P["tok_embeddings.weight"] if tied else P["lm_head.weight"]
     logits = F.linear(x, head).reshape(B * S, vocab)
@@ -102,13 +156,13 @@ def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, 
     if aux_total is not None:
         loss = loss + aux_total
     loss.backward()
-    params = [P[name] for name, _ in lay]
+    params = [P[name] for name, _ in lay_t]
     norm = torch.nn.utils.clip_grad_norm_(params, max_grad_norm)
-    grads = np.concatenate([P[name].grad.detach().numpy().reshape(-1) for name, _ in lay])
+    grads = np.concatenate([P[name].grad.detach().numpy().reshape(-1) for name, _ in lay_t])
     opt = torch.optim.AdamW(params, lr=lr, betas=betas, eps=adam_eps, weight_decay=weight_decay)
     opt.step()
-    new_params = np.concatenate([P[name].detach().numpy().reshape(-1) for name, _ in lay])
-    return float(loss), float(norm), grads, new_params
+    new_params = np.concatenate([P[name].detach().numpy().reshape(-1) for name, _ in lay_t])
+    return float(loss.detach()), float(norm), grads, new_params
 
 
 # ----------------------------------------------------------------------------- mixture of experts
