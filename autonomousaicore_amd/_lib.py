@@ -60,6 +60,8 @@ SIGNATURES = {
     "aic_hip_mem_free_async": (i32, [vp, vp]),
     "aic_hip_mem_stats": (i32, [i64p, i64p]),
     "aic_hip_gemm": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp, i64, i32, i32, vp]),
+    "aic_hip_gemm_lowrank": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32,
+                                   f32, vp, i64, vp, i64, i32, i32, vp]),
     "aic_hip_rmsnorm_fwd": (i32, [vp, i64, vp, vp, i64, vp, i64, i64, f32, i32, vp]),
     "aic_hip_rmsnorm_bwd": (i32, [vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, i32, i64, i64, i32, vp]),
     "aic_hip_rope": (i32, [vp, i64, i64, i64, i64, i64, i64, vp, vp, i32, i32, vp]),

@@ -157,6 +157,41 @@ int aic_hip_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float 
     });
 }
 
+int aic_hip_gemm_lowrank(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+                         int64_t lda, const void* B, int64_t ldb, const void* X2, int64_t ldx2, const void* Y2,
+                         int64_t ldy2, int64_t r2, int64_t seg_n, int y2_kmajor, float beta, void* C, int64_t ldc,
+                         const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(r2 > 0, InvalidArgument, "gemm_lowrank: r2 must be positive");
+        aic::hip::GemmArgs a;
+        a.transA = transA;
+        a.transB = transB;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.alpha = alpha;
+        a.beta = beta;
+        a.A = A;
+        a.lda = lda;
+        a.B = B;
+        a.ldb = ldb;
+        a.C = C;
+        a.ldc = ldc;
+        a.R = R;
+        a.ldr = ldr;
+        a.ab = dt(ab_type);
+        a.c = dt(c_type);
+        a.X2 = X2;
+        a.ldx2 = ldx2;
+        a.Y2 = Y2;
+        a.ldy2 = ldy2;
+        a.r2 = r2;
+        a.seg_n = seg_n;
+        a.y2_kmajor = y2_kmajor;
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, float* rms, int64_t rows,
                         int64_t dim, float eps, aic_dtype d, aic_stream stream) {
     return guard([&] { aic::hip::rmsnorm_fwd(x, ldx, w, y, ldy, rms, rows, dim, eps, dt(d), st(stream)); });

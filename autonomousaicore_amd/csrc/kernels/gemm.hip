@@ -23,9 +23,11 @@
 // fp32 path (the fp32 reference configuration) and odd shapes: a plain SIMT tiled kernel.
 #include "gemm.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
+#include "../runtime/memory_pool.hpp"
 
 namespace aic::hip {
 
@@ -44,6 +46,12 @@ struct MfmaParams {
     int M, N, K;
     float alpha, beta;
     int vec;  // C (and R) rows allow 4-element vector access: ld % 4 == 0, 16-byte aligned base
+    // low-rank term acc += X2 Y2^T (r2 % 8 == 0; 0: none); split-K: block z covers K rows
+    // [z K, (z+1) K) of the operands and writes the fp32 partial C + z * cz
+    const bf16* X2;
+    const bf16* Y2;
+    int64_t ldx2, ldy2, cz;
+    int r2, seg_n, y2k;
 };
 
 // Four consecutive elements of a C / R row, as floats.
@@ -478,6 +486,51 @@ __device__ __forceinline__ void gemm_epilogue(const MfmaParams& p, const f32x16 
     }
 }
 
+// acc += X2 Y2^T for this wave's 32x32 blocks: the low-rank term of a LoRA projection
+// (forward: X2 = s x A^T, Y2 = B; backward: X2 = dxa, Y2 = A read k-major).  The operands are
+// a few KB per tile, so fragments come straight from global memory (L2): 16 bytes per lane
+// for rows contiguous in k, eight 2-byte loads (consecutive n across lanes) for a k-major Y2.
+template <int FM, int FN, int WM, int WN>
+__device__ __forceinline__ void rank_tail(const MfmaParams& p, f32x16 (&acc)[FM][FN], int m0, int n0, int wm,
+                                          int wn) {
+    const int lane = threadIdx.x & 63, hl = lane >> 5, r = lane & 31;
+    const bf16* X2 = p.X2 + (p.seg_n > 0 ? static_cast<int64_t>(n0 / p.seg_n) * p.r2 : 0);
+    const uint16_t* Y2 = reinterpret_cast<const uint16_t*>(p.Y2);
+    for (int k0 = 0; k0 < p.r2; k0 += 16) {
+        const int k = k0 + 8 * hl;
+        const bool kin = k < p.r2;
+        bf16x8 a[FM], b[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int m = m0 + wm * WM + i * 32 + r;
+            const uint4 v = (kin && m < p.M) ? *reinterpret_cast<const uint4*>(X2 + static_cast<int64_t>(m) * p.ldx2 + k)
+                                             : make_uint4(0, 0, 0, 0);
+            a[i] = __builtin_bit_cast(bf16x8, v);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WN + j * 32 + r;
+            const bool ok = kin && n < p.N;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (ok) {
+                if (p.y2k) {
+                    uint32_t w[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) w[q] = Y2[static_cast<int64_t>(k + q) * p.ldy2 + n];
+                    v = make_uint4(w[0] | (w[1] << 16), w[2] | (w[3] << 16), w[4] | (w[5] << 16), w[6] | (w[7] << 16));
+                } else {
+                    v = *reinterpret_cast<const uint4*>(Y2 + static_cast<int64_t>(n) * p.ldy2 + k);
+                }
+            }
+            b[j] = __builtin_bit_cast(bf16x8, v);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[i], acc[i][j], 0, 0, 0);
+    }
+}
+
 // Main loop schedule (per wave): fragments are double-buffered in registers; the reads of
 // k step ks+1 are interleaved with the MFMAs of step ks (sched_group_barrier hints).  The
 // barrier that publishes tile kt+1 sits before the MFMAs of the tile's last k step, so the
@@ -508,6 +561,15 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
+    // split-K: this block's K range (k-contiguous operands move along columns, the others
+    // along rows)
+    const bf16* Ag = p.A;
+    const bf16* Bg = p.B;
+    if (blockIdx.y > 0) {
+        const int64_t kz = static_cast<int64_t>(blockIdx.y) * p.K;
+        Ag += AKC ? kz : kz * p.lda;
+        Bg += BKC ? kz : kz * p.ldb;
+    }
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -519,8 +581,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
 
     auto copy = [&](int tile, int stage) {
         bf16* dst = smem + stage * STAGE;
-        dma_tile<BM, BK, AKC>(p.A, p.lda, m0, p.M, tile * BK, dst);
-        dma_tile<BN, BK, BKC>(p.B, p.ldb, n0, p.N, tile * BK, dst + BM * BK);
+        dma_tile<BM, BK, AKC>(Ag, p.lda, m0, p.M, tile * BK, dst);
+        dma_tile<BN, BK, BKC>(Bg, p.ldb, n0, p.N, tile * BK, dst + BM * BK);
     };
     auto read = [&](int stage, int kk, bf16x8* af, bf16x8* bfr) {
         const bf16* As = smem + stage * STAGE;
@@ -533,8 +595,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     constexpr int PA = BM * BK / 512 / 4;  // A-tile copy instructions per wave
     auto copy_one = [&](int tile, int stage, int q) {
         bf16* dst = smem + stage * STAGE;
-        if (q < PA) dma_one<BM, BK, AKC>(p.A, p.lda, m0, p.M, tile * BK, dst, q);
-        else dma_one<BN, BK, BKC>(p.B, p.ldb, n0, p.N, tile * BK, dst + BM * BK, q - PA);
+        if (q < PA) dma_one<BM, BK, AKC>(Ag, p.lda, m0, p.M, tile * BK, dst, q);
+        else dma_one<BN, BK, BKC>(Bg, p.ldb, n0, p.N, tile * BK, dst + BM * BK, q - PA);
     };
     auto read_one = [&](int stage, int kk, int f, bf16x8* af, bf16x8* bfr) {
         const bf16* As = smem + stage * STAGE;
@@ -599,7 +661,33 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
         }
     }
 
-    gemm_epilogue<BM, BN, S * STAGE * 2, CT>(p, acc, smem, m0, n0);
+    if (p.r2 > 0) rank_tail<FM, FN, WM, WN>(p, acc, m0, n0, wm, wn);
+    if (blockIdx.y > 0) {
+        MfmaParams q = p;
+        q.C = static_cast<float*>(p.C) + static_cast<int64_t>(blockIdx.y) * p.cz;
+        gemm_epilogue<BM, BN, S * STAGE * 2, CT>(q, acc, smem, m0, n0);
+    } else {
+        gemm_epilogue<BM, BN, S * STAGE * 2, CT>(p, acc, smem, m0, n0);
+    }
+}
+
+// C = alpha * sum_z P[z] + beta * C + R over the split-K partials P [splits][M][N] (fp32,
+// summed in z order: deterministic).
+template <typename CT>
+__global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ P, int splits, int64_t pz, int M, int N,
+                                                       float alpha, float beta, CT* C, int64_t ldc, const CT* R,
+                                                       int64_t ldr) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int m = static_cast<int>(i / N), n = static_cast<int>(i % N);
+        float acc = P[i];
+        for (int z = 1; z < splits; ++z) acc += P[z * pz + i];
+        const int64_t ci = static_cast<int64_t>(m) * ldc + n;
+        float v = alpha * acc;
+        if (beta != 0.0f) v += beta * ld(C, ci);
+        if (R) v += ld(R, static_cast<int64_t>(m) * ldr + n);
+        st(C, ci, v);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -672,13 +760,19 @@ void launch_mfma(const GemmArgs& a, hipStream_t s) {
     p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
     p.alpha = a.alpha; p.beta = a.beta;
     p.vec = 0;
+    p.X2 = p.Y2 = nullptr;
+    p.ldx2 = p.ldy2 = p.cz = 0;
+    p.r2 = p.seg_n = p.y2k = 0;
     const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, TA, TB, CT>), dim3(tiles), dim3(256), 0, s, p);
     AIC_LAUNCH_CHECK("gemm_bf16_mfma");
 }
 
+// splits > 1: the K range is cut into `splits` equal parts (K % (64 splits) == 0), block z
+// writes its fp32 partial to part + z M N, and splitk_reduce_k forms C.  Otherwise the
+// low-rank term of `a` (if any) runs in the kernel's tail.
 template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
-void launch_dma(const GemmArgs& a, hipStream_t s) {
+void launch_dma(const GemmArgs& a, hipStream_t s, int splits = 1, float* part = nullptr) {
     MfmaParams p;
     p.A = static_cast<const bf16*>(a.A);
     p.B = static_cast<const bf16*>(a.B);
@@ -687,7 +781,23 @@ void launch_dma(const GemmArgs& a, hipStream_t s) {
     p.lda = a.lda; p.ldb = a.ldb; p.ldc = a.ldc; p.ldr = a.ldr;
     p.M = static_cast<int>(a.M); p.N = static_cast<int>(a.N); p.K = static_cast<int>(a.K);
     p.alpha = a.alpha; p.beta = a.beta;
-    p.vec = a.ldc % 4 == 0 && aligned16(a.C) && (!a.R || (a.ldr % 4 == 0 && aligned16(a.R)));
+    p.X2 = static_cast<const bf16*>(a.X2);
+    p.Y2 = static_cast<const bf16*>(a.Y2);
+    p.ldx2 = a.ldx2; p.ldy2 = a.ldy2;
+    p.r2 = static_cast<int>(a.r2); p.seg_n = static_cast<int>(a.seg_n); p.y2k = a.y2_kmajor;
+    p.cz = 0;
+    if (splits > 1) {
+        p.C = part;
+        p.R = nullptr;
+        p.ldc = a.N;
+        p.ldr = 0;
+        p.alpha = 1.0f;
+        p.beta = 0.0f;
+        p.K = static_cast<int>(a.K / splits);
+        p.cz = a.M * a.N;
+        p.r2 = 0;
+    }
+    p.vec = p.ldc % 4 == 0 && aligned16(p.C) && (!p.R || (p.ldr % 4 == 0 && aligned16(p.R)));
     const int tiles = static_cast<int>(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN));
     constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * BK * sizeof(uint16_t);
     static_assert(lds <= 160 * 1024, "LDS per block");
@@ -697,16 +807,16 @@ void launch_dma(const GemmArgs& a, hipStream_t s) {
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         configured = true;
     }
-    hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, BK, S, TA, TB, CT>), dim3(tiles), dim3(256), lds, s, p);
+    hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, BK, S, TA, TB, CT>), dim3(tiles, splits), dim3(256), lds, s, p);
     AIC_LAUNCH_CHECK("gemm_bf16_dma");
 }
 
 template <int BM, int BN, int BK, int S, typename CT>
-void dispatch_dma(const GemmArgs& a, hipStream_t s) {
-    if (!a.transA && a.transB) launch_dma<BM, BN, BK, S, false, true, CT>(a, s);
-    else if (!a.transA && !a.transB) launch_dma<BM, BN, BK, S, false, false, CT>(a, s);
-    else if (a.transA && !a.transB) launch_dma<BM, BN, BK, S, true, false, CT>(a, s);
-    else launch_dma<BM, BN, BK, S, true, true, CT>(a, s);
+void dispatch_dma(const GemmArgs& a, hipStream_t s, int splits = 1, float* part = nullptr) {
+    if (!a.transA && a.transB) launch_dma<BM, BN, BK, S, false, true, CT>(a, s, splits, part);
+    else if (!a.transA && !a.transB) launch_dma<BM, BN, BK, S, false, false, CT>(a, s, splits, part);
+    else if (a.transA && !a.transB) launch_dma<BM, BN, BK, S, true, false, CT>(a, s, splits, part);
+    else launch_dma<BM, BN, BK, S, true, true, CT>(a, s, splits, part);
 }
 
 template <int BM, int BN, typename CT>
@@ -743,6 +853,36 @@ bool gemm_dma_eligible(const GemmArgs& a) {
     return true;
 }
 
+namespace {
+
+// C = alpha X2 Y2^T + C, per segment, as ordinary GEMMs (the shapes the kernel tail cannot take).
+void rank_term_separately(const GemmArgs& a, hipStream_t s) {
+    const size_t es = dtype_size(a.ab), ec = dtype_size(a.c);
+    const int64_t nseg = a.seg_n > 0 ? a.N / a.seg_n : 1, nn = a.seg_n > 0 ? a.seg_n : a.N;
+    for (int64_t g = 0; g < nseg; ++g) {
+        GemmArgs t;
+        t.transA = 0;
+        t.transB = a.y2_kmajor ? 0 : 1;
+        t.M = a.M;
+        t.N = nn;
+        t.K = a.r2;
+        t.alpha = a.alpha;
+        t.beta = 1.0f;
+        t.A = static_cast<const char*>(a.X2) + es * g * a.r2;
+        t.lda = a.ldx2;
+        t.B = a.y2_kmajor ? static_cast<const char*>(a.Y2) + es * g * nn
+                          : static_cast<const char*>(a.Y2) + es * g * nn * a.ldy2;
+        t.ldb = a.ldy2;
+        t.C = static_cast<char*>(a.C) + ec * g * nn;
+        t.ldc = a.ldc;
+        t.ab = a.ab;
+        t.c = a.c;
+        gemm(t, s);
+    }
+}
+
+}  // namespace
+
 void gemm(const GemmArgs& a, hipStream_t s) {
     AIC_CHECK(a.M >= 0 && a.N >= 0 && a.K >= 0, InvalidArgument, "negative GEMM size");
     AIC_CHECK(a.M < (1LL << 31) && a.N < (1LL << 31) && a.K < (1LL << 31), InvalidArgument, "GEMM size too large");
@@ -752,16 +892,69 @@ void gemm(const GemmArgs& a, hipStream_t s) {
     const int64_t amin = a.transA ? a.M : a.K, bmin = a.transB ? a.K : a.N;
     AIC_CHECK(a.lda >= (amin > 0 ? amin : 1) && a.ldb >= (bmin > 0 ? bmin : 1) && a.ldc >= (a.N > 0 ? a.N : 1),
               InvalidArgument, "leading dimension smaller than the row length");
+    if (a.r2 > 0) {
+        AIC_CHECK(a.X2 && a.Y2, InvalidArgument, "low-rank GEMM term without X2 / Y2");
+        AIC_CHECK(a.seg_n >= 0 && (a.seg_n == 0 || a.N % a.seg_n == 0), InvalidArgument,
+                  "low-rank segments must tile N");
+        const int64_t segs = a.seg_n > 0 ? a.N / a.seg_n : 1;
+        AIC_CHECK(a.ldx2 >= segs * a.r2 && a.ldy2 >= (a.y2_kmajor ? a.N : a.r2), InvalidArgument,
+                  "low-rank term: leading dimension smaller than the row length");
+    }
     if (a.M == 0 || a.N == 0) return;
     if (gemm_dma_eligible(a)) {
         const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+        const int64_t t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+        const bool big = t256 >= 192;
+        if (a.r2 > 0) {
+            const int64_t bn = big ? 256 : 128;
+            const bool tail = a.r2 % 8 == 0 && a.ldx2 % 8 == 0 && aligned16(a.X2) &&
+                              (a.y2_kmajor || (a.ldy2 % 8 == 0 && aligned16(a.Y2))) &&
+                              (a.seg_n == 0 || a.seg_n % bn == 0);
+            if (!tail) {
+                GemmArgs b = a;
+                b.r2 = 0;
+                gemm(b, s);
+                rank_term_separately(a, s);
+                return;
+            }
+        }
+        // few output tiles over a long K: split K so that the launch fills the chip (partials
+        // summed in a fixed order afterwards)
+        int splits = 1;
+        if (a.r2 == 0 && !big && t128 < 128 && a.K >= 1024) {
+            splits = static_cast<int>(std::min<int64_t>({a.K / 512, (256 + t128 - 1) / t128, 16}));
+            while (splits > 1 && a.K % (64LL * splits)) --splits;
+        }
+        if (splits > 1) {
+            float* part = static_cast<float*>(stream_scratch(sizeof(float) * splits * a.M * a.N, s, 7));
+            dispatch_dma<128, 128, 64, 4, float>(a, s, splits, part);
+            const int64_t total = a.M * a.N;
+            const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 4096));
+            if (a.c == DType::Float32)
+                hipLaunchKernelGGL(splitk_reduce_k<float>, dim3(grid), dim3(256), 0, s, part, splits, total,
+                                   static_cast<int>(a.M), static_cast<int>(a.N), a.alpha, a.beta,
+                                   static_cast<float*>(a.C), a.ldc, static_cast<const float*>(a.R), a.ldr);
+            else
+                hipLaunchKernelGGL(splitk_reduce_k<bf16>, dim3(grid), dim3(256), 0, s, part, splits, total,
+                                   static_cast<int>(a.M), static_cast<int>(a.N), a.alpha, a.beta,
+                                   static_cast<bf16*>(a.C), a.ldc, static_cast<const bf16*>(a.R), a.ldr);
+            AIC_LAUNCH_CHECK("splitk_reduce_k");
+            return;
+        }
         if (a.c == DType::Float32) {
-            if (t256 >= 192) dispatch_dma<256, 256, 64, 2, float>(a, s);
+            if (big) dispatch_dma<256, 256, 64, 2, float>(a, s);
             else dispatch_dma<128, 128, 64, 4, float>(a, s);
         } else {
-            if (t256 >= 192) dispatch_dma<256, 256, 64, 2, bf16>(a, s);
+            if (big) dispatch_dma<256, 256, 64, 2, bf16>(a, s);
             else dispatch_dma<128, 128, 64, 4, bf16>(a, s);
         }
+        return;
+    }
+    if (a.r2 > 0) {
+        GemmArgs b = a;
+        b.r2 = 0;
+        gemm(b, s);
+        rank_term_separately(a, s);
         return;
     }
     if (gemm_mfma_eligible(a)) {

@@ -29,6 +29,15 @@ struct GemmArgs {
     int64_t ldr = 0;
     DType ab = DType::BFloat16;
     DType c = DType::BFloat16;
+    // Optional low-rank term (the LoRA path), added to the product before scaling:
+    //   C = alpha * (op(A) op(B) + X2 Y2^T) + beta * C + R
+    // X2 [M, r2] row-major (ldx2; with seg_n > 0, output columns [s seg_n, (s+1) seg_n) take
+    // the X2 columns [s r2, (s+1) r2)); Y2 [N, r2] row-major (ldy2), or [r2, N] when
+    // y2_kmajor.  Same dtype as A and B.
+    const void* X2 = nullptr;
+    const void* Y2 = nullptr;
+    int64_t ldx2 = 0, ldy2 = 0, r2 = 0, seg_n = 0;
+    int y2_kmajor = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);

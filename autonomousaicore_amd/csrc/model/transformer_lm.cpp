@@ -29,11 +29,22 @@ constexpr int64_t kAlign = 64;  // arena offsets are multiples of 64 elements (2
 
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+// The low-rank term X2 Y2^T a LoRA projection adds to its base product (GemmArgs::X2).
+struct LowRank {
+    const void* x2;
+    int64_t ldx2;
+    const void* y2;
+    int64_t ldy2, r2, seg_n;
+    int y2_kmajor;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
-          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f) {
+          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
-    auto scope = prof.scope(ta ? kGemmWgrad : (tb ? kGemmFwd : kGemmDgrad), 2.0 * M * N * K, es * (M * K + N * K) + ec * M * N * (R ? 2 : 1), s);
+    const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
+    auto scope = prof.scope(ta ? kGemmWgrad : (tb ? kGemmFwd : kGemmDgrad), 2.0 * M * N * (K + kr),
+                            es * (M * K + N * K) + ec * M * N * (R ? 2 : 1), s);
     hip::GemmArgs a;
     a.transA = ta;
     a.transB = tb;
@@ -52,6 +63,15 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
     a.alpha = alpha;
     a.ab = ab;
     a.c = c;
+    if (lr) {
+        a.X2 = lr->x2;
+        a.ldx2 = lr->ldx2;
+        a.Y2 = lr->y2;
+        a.ldy2 = lr->ldy2;
+        a.r2 = lr->r2;
+        a.seg_n = lr->seg_n;
+        a.y2_kmajor = lr->y2_kmajor;
+    }
     hip::gemm(a, s);
 }
 
@@ -130,7 +150,8 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
         AIC_CHECK(G > 0 && G % 2 == 0 && (d * d) % G == 0 && (f * d) % G == 0, InvalidArgument,
                   "QLoRA: the group size must be even and divide d*d and d_ffn*d");
         // A of q, k, v (and of gate, up) must be adjacent to act as one stacked matrix
-        AIC_CHECK((r * d) % kAlign == 0, InvalidArgument, "QLoRA: lora_rank * d_model must be a multiple of 64");
+        AIC_CHECK((r * d) % kAlign == 0 && (r * f) % kAlign == 0, InvalidArgument,
+                  "QLoRA: lora_rank * d_model and lora_rank * d_ffn must be multiples of 64");
         int64_t o2 = 0;
         auto lo = [&](const std::string& name, std::vector<int64_t> shape) { return add_to(params_, o2, name, shape); };
         for (int64_t l = 0; l < L; ++l) {
@@ -443,17 +464,16 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_fwd(x, d, PB(ly.n1), h1l, d, atf(r1, l * T), T, d, eps, dt, s);
         }
-        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s);
+        // LoRA (LoRALinear::forward, src/nn/lora.cpp:75-93): xs = s (x A^T) is formed first (A of
+        // q, k, v stacked, [3r, d]); the base GEMM then adds xs B^T to its accumulators, each
+        // output column block (q, k, v) with its own r columns of xs and its own B
+        LowRank lq{};
         if (ql) {
-            // LoRA of q, k, v (LoRALinear::forward, src/nn/lora.cpp:75-93): xa = h1 A^T once for
-            // the stacked A [3r, d], then y_j += s * xa_j B_j^T into each column block
-            void* xa = xaq(l);
-            gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xa, 3 * r, dt, dt, s);
-            const int64_t bs[3] = {ly.bq, ly.bk, ly.bv};
-            for (int j = 0; j < 3; ++j)
-                gemm(prof_, 0, 1, T, d, r, static_cast<char*>(xa) + es * j * r, 3 * r, W(bs[j]), r,
-                     static_cast<char*>(qkvl) + es * j * d, 3 * d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+            gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xaq(l), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lq = LowRank{xaq(l), 3 * r, W(ly.bq), r, r, d, 0};
         }
+        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lq : nullptr);
         {
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
             hip::rope(qkvl, 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, false, dt, s);
@@ -463,11 +483,13 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             hip::attn_fwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
                           d, atf(lse, l * T * H), B, H, S, hd, true, scale, dt, s);
         }
-        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d);
+        LowRank lo_{};
         if (ql) {
-            gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s);
-            gemm(prof_, 0, 1, T, d, r, xao(l), r, W(ly.bo), r, x1l, d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+            gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lo_ = LowRank{xao(l), r, W(ly.bo), r, r, 0, 0};
         }
+        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
+             ql ? &lo_ : nullptr);
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_fwd(x1l, d, PB(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
@@ -477,23 +499,24 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             moe_[l]->forward(h2l, T, W(ly.wr), W(ly.wex), x1l, xn, aux_dev_ + l, s);
             continue;
         }
-        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s);
+        LowRank lg{};
         if (ql) {
-            void* xa = xagu(l);
-            gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xa, 2 * r, dt, dt, s);
-            gemm(prof_, 0, 1, T, f, r, xa, 2 * r, W(ly.bg), r, gul, 2 * f, dt, dt, s, nullptr, 0, 1.0f, lsc);
-            gemm(prof_, 0, 1, T, f, r, static_cast<char*>(xa) + es * r, 2 * r, W(ly.bu), r,
-                 static_cast<char*>(gul) + es * f, 2 * f, dt, dt, s, nullptr, 0, 1.0f, lsc);
+            gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xagu(l), 2 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lg = LowRank{xagu(l), 2 * r, W(ly.bg), r, r, f, 0};
         }
+        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lg : nullptr);
         {
             auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
             hip::swiglu_fwd(gul, static_cast<char*>(gul) + es * f, 2 * f, aml, f, T, f, dt, s);
         }
-        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d);
+        LowRank ld_{};
         if (ql) {
-            gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s);
-            gemm(prof_, 0, 1, T, d, r, xad(l), r, W(ly.bd), r, xn, d, dt, dt, s, nullptr, 0, 1.0f, lsc);
+            gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            ld_ = LowRank{xad(l), r, W(ly.bd), r, r, 0, 0};
         }
+        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
+             ql ? &ld_ : nullptr);
     }
     void* xL = at(xs, L * T * d);
     {
@@ -530,11 +553,11 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(moe ? 0 : T * 2 * f),
                  da = act(moe ? 0 : T * f), dxa = act(ql ? T * 3 * r : 0);
     // LoRA backward of one projection (LoRALinear, src/nn/lora.cpp:75-93, through autograd):
-    // with y += s * (x A^T) B^T and xa = x A^T kept from the forward,
-    //   dB = s dy^T xa, dxa = s dy B   (then dA = dxa^T x and dx += dxa A by the caller)
-    auto lora_b_bwd = [&](const void* dy, int64_t lddy, int64_t n_out, const void* xa, int64_t ldxa, int64_t boff,
+    // with y += xs B^T and xs = s (x A^T) kept from the forward,
+    //   dB = dy^T xs, dxa = s dy B   (then dA = dxa^T x, and dx += dxa A in the base dgrad GEMM)
+    auto lora_b_bwd = [&](const void* dy, int64_t lddy, int64_t n_out, const void* xs, int64_t ldxs, int64_t boff,
                           void* dxa_out, int64_t lddxa) {
-        gemm(prof_, 1, 0, n_out, r, T, dy, lddy, xa, ldxa, G(boff), r, dt, DType::Float32, s, nullptr, 0, 0.0f, lsc);
+        gemm(prof_, 1, 0, n_out, r, T, dy, lddy, xs, ldxs, G(boff), r, dt, DType::Float32, s);
         gemm(prof_, 0, 0, T, r, n_out, dy, lddy, W(boff), r, dxa_out, lddxa, dt, dt, s, nullptr, 0, 0.0f, lsc);
     };
     if (!ql) gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
@@ -559,29 +582,34 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             void* gul = at(gu, l * T * 2 * f);
             void* aml = at(am, l * T * f);
             // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
-            if (!ql) gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s);
+            LowRank ld_{};
             if (ql) {
                 lora_b_bwd(dx.get(), d, d, xad(l), r, ly.bd, dxa.get(), r);
                 gemm(prof_, 1, 0, r, f, T, dxa.get(), r, aml, f, G(ly.ad), f, dt, DType::Float32, s);
-                gemm(prof_, 0, 0, T, f, r, dxa.get(), r, W(ly.ad), f, da.get(), f, dt, dt, s, nullptr, 0, 1.0f);
+                ld_ = LowRank{dxa.get(), r, W(ly.ad), f, r, 0, 1};
+            } else {
+                gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
             }
+            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s, nullptr, 0, 0.0f,
+                 1.0f, ql ? &ld_ : nullptr);
             {
                 auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
                 hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
                                 static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
             }
-            if (!ql) gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s);
+            LowRank lg{};
             if (ql) {
                 void* xa = xagu(l);
                 lora_b_bwd(dgu.get(), 2 * f, f, xa, 2 * r, ly.bg, dxa.get(), 2 * r);
                 lora_b_bwd(static_cast<char*>(dgu.get()) + es * f, 2 * f, f, static_cast<char*>(xa) + es * r, 2 * r,
                            ly.bu, static_cast<char*>(dxa.get()) + es * r, 2 * r);
                 gemm(prof_, 1, 0, 2 * r, d, T, dxa.get(), 2 * r, h2l, d, G(ly.agu), d, dt, DType::Float32, s);
-                gemm(prof_, 0, 0, T, d, 2 * r, dxa.get(), 2 * r, W(ly.agu), d, dh.get(), d, dt, dt, s, nullptr, 0,
-                     1.0f);
+                lg = LowRank{dxa.get(), 2 * r, W(ly.agu), d, 2 * r, 0, 1};
+            } else {
+                gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
             }
+            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s,
+                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr);
         }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
@@ -589,13 +617,16 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                              false, T, d, dt, s);
         }
         // x1 = x + out_proj(attn(rope(q), rope(k), v))
-        if (!ql) gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s);
+        LowRank lo_{};
         if (ql) {
             lora_b_bwd(dx.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
             gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, d, r, dxa.get(), r, W(ly.ao), d, dh.get(), d, dt, dt, s, nullptr, 0, 1.0f);
+            lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
+        } else {
+            gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
         }
+        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lo_ : nullptr);
         {
             // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
             auto _p = prof_.scope(kAttnBwd, 2.0 * attn_flops, 8.0 * es * T * d, s);
@@ -607,8 +638,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
             hip::rope(dqkv.get(), 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, true, dt, s);
         }
-        if (!ql) gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
-        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s);
+        LowRank lq{};
         if (ql) {
             const int64_t bs[3] = {ly.bq, ly.bk, ly.bv};
             for (int j = 0; j < 3; ++j)
@@ -616,8 +646,12 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                            static_cast<char*>(xaq(l)) + es * j * r, 3 * r, bs[j],
                            static_cast<char*>(dxa.get()) + es * j * r, 3 * r);
             gemm(prof_, 1, 0, 3 * r, d, T, dxa.get(), 3 * r, h1l, d, G(ly.aqkv), d, dt, DType::Float32, s);
-            gemm(prof_, 0, 0, T, d, 3 * r, dxa.get(), 3 * r, W(ly.aqkv), d, dh.get(), d, dt, dt, s, nullptr, 0, 1.0f);
+            lq = LowRank{dxa.get(), 3 * r, W(ly.aqkv), d, 3 * r, 0, 1};
+        } else {
+            gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
         }
+        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
+             0, 0.0f, 1.0f, ql ? &lq : nullptr);
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, GB(ly.n1), false,

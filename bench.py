@@ -33,19 +33,45 @@ CONFIGS = {
                H=16, f=5632, B=4, S=2048, amp=True, resid_scale=False),
     "125m": dict(workload="125M-class decoder, bf16 AMP training step (BASELINE configs[1])", vocab=32000, d=768,
                  L=12, H=12, f=2048, B=8, S=1024, amp=True, resid_scale=True),
+    "tiny": dict(workload="tiny decoder, fp32 training step, tied embeddings (BASELINE configs[0])", vocab=512,
+                 d=128, L=2, H=4, f=352, B=8, S=64, amp=False, resid_scale=False, compute="float32", tied=True),
+    "moe": dict(workload="sparse MoE decoder, 8 experts top-2, bf16 AMP training step (BASELINE configs[3])",
+                vocab=32000, d=1024, L=12, H=16, f=2816, B=8, S=1024, amp=True, resid_scale=False, experts=8,
+                top_k=2),
+    "qlora": dict(workload="QLoRA step on the 1B shape: INT4 base (G 128, fp16 scales), rank-16 alpha-32 adapters "
+                           "on 7 projections, bf16 AMP (BASELINE configs[4])", vocab=32000, d=2048, L=16, H=16,
+                  f=5632, B=4, S=2048, amp=True, resid_scale=False, lora_rank=16, lora_alpha=32.0, group=128),
 }
 
 
 def matmul_params(c):
+    """Matmul parameters a token passes through (the MoE router and its top_k experts only)."""
     d, f, V, L = c["d"], c["f"], c["vocab"], c["L"]
+    if c.get("experts"):
+        return L * (4 * d * d + c["experts"] * d + c["top_k"] * 3 * d * f) + V * d
     return L * (4 * d * d + 3 * d * f) + V * d  # lm_head; the embedding gather has no FLOPs
+
+
+def total_params(c):
+    d, f, V, L, E = c["d"], c["f"], c["vocab"], c["L"], c.get("experts", 0)
+    per_layer = 4 * d * d + (E * d + E * 3 * d * f if E else 3 * d * f) + 2 * d
+    return L * per_layer + d + V * d * (1 if c.get("tied") else 2)
+
+
+def lora_params(c):
+    d, f, r = c["d"], c["f"], c.get("lora_rank", 0)
+    return c["L"] * (4 * 2 * r * d + 2 * (r * d + f * r) + r * f + d * r)
 
 
 def step_flops(c):
     """Algorithmic FLOPs per step: 6 T P_mm + 6 L T S d (causal attention: forward Q K^T and
-    P V at 2 S d per token per layer on the causal average, backward twice that)."""
+    P V at 2 S d per token per layer on the causal average, backward twice that).  QLoRA: the
+    frozen base has no weight gradient, 4 T P_mm, plus 6 T P_lora for the adapters."""
     T = c["B"] * c["S"]
-    return 6.0 * T * matmul_params(c) + 6.0 * c["L"] * T * c["S"] * c["d"]
+    attn = 6.0 * c["L"] * T * c["S"] * c["d"]
+    if c.get("lora_rank"):
+        return 4.0 * T * matmul_params(c) + 6.0 * T * lora_params(c) + attn
+    return 6.0 * T * matmul_params(c) + attn
 
 
 def profiled_traffic(kernel_class):
@@ -75,27 +101,43 @@ def cpu_baseline(c, seed=1234):
     threads = max(1, min(threads, 24))
     orc.set_threads(threads)
     S = c["S"]
-    cfg = orc.make_config(c["vocab"], c["d"], 1, c["H"], c["f"], S, norm_eps=1e-6)
+    E = c.get("experts", 0)
+    cfg = orc.make_config(c["vocab"], c["d"], 1, c["H"], c["f"], S, norm_eps=1e-6, n_experts=E,
+                          top_k=c.get("top_k", 2), tied=c.get("tied", False))
     n = orc.num_params(cfg)
     import autonomousaicore_amd as aic
     params = aic.normal(5678, n, 0.0, 0.02)
     d = c["d"]
-    # norms at 1: per-layer norm1/norm2 and the final norm
+    # norms at 1: norm1/norm2 of the layer and the final norm (oracle order: embedding, q k v o,
+    # FFN or router + experts, norm1, norm2, final norm, head)
     V, f = c["vocab"], c["f"]
-    off = V * d + 4 * d * d + 3 * d * f
-    params[off:off + 2 * d] = 1.0
-    params[off + 2 * d:off + 3 * d] = 1.0
+    off = V * d + 4 * d * d + (E * d + E * 3 * d * f if E else 3 * d * f)
+    params[off:off + 3 * d] = 1.0
     ids, tgt = aic.batch(seed, 1, S, c["vocab"], dist="zipf")
-    full_params = matmul_params(c) + c["vocab"] * d + c["L"] * 2 * d + d
+    r = c.get("lora_rank", 0)
+    if r:
+        nl = orc.qlora_num_params(cfg, r)
+        lora = aic.normal(9012, nl, 0.0, 0.02)
+        trainable = lora_params(c)
+
+        def one_step():
+            return orc.qlora_step(cfg, r, c["lora_alpha"], c["group"], params, lora.copy(), ids, tgt, 1, S)[0]
+    else:
+        trainable = total_params(c)
+
+        def one_step():
+            return orc.lm_step(cfg, params.copy(), ids, tgt, 1, S)[0]
+    n_opt = nl if r else n
+    full_params = trainable
     # one untimed warm-up, then the median of three sample steps (each from the same weights)
-    orc.lm_step(cfg, params.copy(), ids, tgt, 1, S)
+    one_step()
     t0 = time.perf_counter()
     est = []
     for _ in range(3):
-        res, *_ = orc.lm_step(cfg, params.copy(), ids, tgt, 1, S)
+        res = one_step()
         per_token = (res.t_embed + res.t_embed_bwd + res.t_head_fwd + res.t_loss + res.t_head_bwd)
         blocks = res.t_blocks_fwd + res.t_blocks_bwd
-        est.append(c["B"] * (per_token + c["L"] * blocks) + res.t_optim * (full_params / n))
+        est.append(c["B"] * (per_token + c["L"] * blocks) + res.t_optim * (full_params / n_opt))
     wall = time.perf_counter() - t0
     t_step = sorted(est)[1]
     tokens = c["B"] * S
@@ -144,7 +186,11 @@ def main():
         del src, dst
     model = aic.TransformerLM(
         aic.TransformerLMConfig(vocab_size=c["vocab"], hidden_dim=c["d"], num_layers=c["L"], num_heads=c["H"],
-                                intermediate_dim=c["f"], max_seq_len=S, rms_norm_eps=1e-6, compute="bfloat16"),
+                                intermediate_dim=c["f"], max_seq_len=S, rms_norm_eps=1e-6,
+                                compute=c.get("compute", "bfloat16"), tie_word_embeddings=c.get("tied", False),
+                                num_experts=c.get("experts", 0), top_k=c.get("top_k", 2), aux_loss_coef=0.01,
+                                lora_rank=c.get("lora_rank", 0), lora_alpha=c.get("lora_alpha", 32.0),
+                                quant_group=c.get("group", 128)),
         aic.TrainingConfig(adamw=aic.AdamWOptions(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1),
                            max_grad_norm=1.0, use_amp=c["amp"]))
     model.init_normal(5678, 0.02, residual_scaling=c["resid_scale"])
@@ -210,11 +256,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f32" if c.get("compute") == "float32" else "bf16",
         "data": "synthetic",
         "config": {"workload": c["workload"], "layers": c["L"], "d_model": c["d"], "heads": c["H"],
                    "d_ffn": c["f"], "vocab": c["vocab"], "global_batch": B, "seq_len": S,
-                   "tokens_per_step": B * S, "parallelism": "none (1 GPU)"},
+                   "tokens_per_step": B * S, "parallelism": "none (1 GPU)",
+                   **({"experts": c["experts"], "top_k": c["top_k"]} if c.get("experts") else {}),
+                   **({"lora_rank": c["lora_rank"], "lora_alpha": c["lora_alpha"], "quant_group": c["group"],
+                       "trainable_params": lora_params(c)} if c.get("lora_rank") else {})},
         "step_flops": flops,
         "mfma_peak_frac_step": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "loss": round(float(stats.loss), 5),

@@ -72,6 +72,19 @@ int aic_hip_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float 
                  const void* B, int64_t ldb, float beta, void* C, int64_t ldc, const void* R, int64_t ldr,
                  aic_dtype ab_type, aic_dtype c_type, aic_stream stream);
 
+/* The same product with a low-rank term added before scaling (a LoRA projection in one pass):
+ *   C = alpha * (op(A) op(B) + X2 Y2^T) + beta * C + R
+ * X2 [M, r2] row-major (ldx2); with seg_n > 0 the output columns [s*seg_n, (s+1)*seg_n) take the
+ * X2 columns [s*r2, (s+1)*r2) (q, k, v or gate, up stacked in one product); Y2 [N, r2] row-major
+ * (ldy2), or [r2, N] when y2_kmajor.  X2 / Y2 have dtype ab_type.  On the bf16 MFMA path the
+ * term is accumulated in the product's own registers.
+ * Replaces: the sum y = base(x) + lora_B(lora_A(x)) * scaling of LoRALinear::forward
+ * (src/nn/lora.cpp:75-93) and the input-gradient sum of its backward. */
+int aic_hip_gemm_lowrank(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+                         int64_t lda, const void* B, int64_t ldb, const void* X2, int64_t ldx2, const void* Y2,
+                         int64_t ldy2, int64_t r2, int64_t seg_n, int y2_kmajor, float beta, void* C, int64_t ldc,
+                         const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type, aic_stream stream);
+
 /* ---------------------------------------------------------------- RMSNorm ---------- */
 /* y = x / rms * w with rms = sqrt(mean(x^2) + eps) per row; rms[rows] (fp32) is saved.
  * x/y have dtype dt (F32 or BF16), leading dimensions ldx/ldy; w is fp32 [dim].

@@ -66,8 +66,10 @@ def test_gemm_epilogue_residual_alpha_beta():
 
 # Weight-gradient shapes of the 1B step (o_proj, gate/up) over the full K = 8192, partial
 # tiles with long K, each with residual / alpha / beta epilogues; runs must be bit-identical.
+# Few-tile shapes (the LoRA adapter products: dB, dA, x A^T, dy B) take the split-K path.
 LONG_K_CASES = [(1, 0, 2048, 2048, 8192), (1, 0, 11264, 2048, 8192), (0, 1, 600, 520, 8192),
-                (0, 0, 1000, 1000, 4096), (1, 1, 264, 1032, 8192)]
+                (0, 0, 1000, 1000, 4096), (1, 1, 264, 1032, 8192), (1, 0, 2048, 16, 8192), (1, 0, 48, 2048, 8192),
+                (0, 1, 8192, 48, 2048), (0, 0, 4096, 16, 5632)]
 
 
 @pytest.mark.parametrize("ta,tb,M,N,K", LONG_K_CASES)
@@ -87,6 +89,50 @@ def test_gemm_long_k_and_epilogues(ta, tb, M, N, K):
     C0 = rng.standard_normal((M, N)).astype(np.float32)
     cb = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32, R=Rd, alpha=0.25, beta=-1.5, C0=dev(C0))
     assert rel(host(cb), 0.25 * ref - 1.5 * C0 + R) < 1e-5
+
+
+def _gemm_lowrank(ta, tb, M, N, K, A, B, X2, Y2, r2, seg_n, y2k, ab, ct, R=None, alpha=1.0, beta=0.0, C0=None):
+    Cout = C0.clone() if C0 is not None else torch.empty((M, N), dtype=ct, device="cuda")
+    call("aic_hip_gemm_lowrank", ta, tb, M, N, K, alpha, ptr(A), A.shape[1], ptr(B), B.shape[1], ptr(X2),
+         X2.shape[1], ptr(Y2), Y2.shape[1], r2, seg_n, y2k, beta, ptr(Cout), N, ptr(R), N if R is not None else 0,
+         ab, F32 if ct == torch.float32 else BF16, stream())
+    return Cout
+
+
+# (ta, tb, M, N, K, r2, seg_n, y2_kmajor): LoRA forward (q/k/v or gate/up segments, single
+# projections), LoRA input gradients (k-major A), a 256x256-tile launch, and shapes the kernel
+# tail cannot take (segments not a multiple of the tile, rank not a multiple of 8)
+LOWRANK_CASES = [(0, 1, 512, 768, 256, 16, 256, 0), (0, 1, 384, 256, 128, 16, 0, 0), (0, 0, 512, 256, 384, 48, 0, 1),
+                 (0, 0, 300, 136, 192, 32, 0, 1), (0, 1, 4096, 6144, 256, 16, 2048, 0), (0, 1, 256, 384, 128, 16, 192, 0),
+                 (0, 1, 256, 256, 128, 4, 0, 0), (0, 0, 256, 256, 128, 12, 0, 1)]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K,r2,seg,y2k", LOWRANK_CASES)
+def test_gemm_lowrank_term(ta, tb, M, N, K, r2, seg, y2k):
+    rng = np.random.default_rng(M + N + K + r2 + seg)
+    nseg = N // seg if seg else 1
+    A = bf16_round(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = bf16_round(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    X2 = bf16_round(rng.standard_normal((M, nseg * r2)).astype(np.float32))
+    Y2 = bf16_round(rng.standard_normal((r2, N) if y2k else (N, r2)).astype(np.float32))
+    R = bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    ref = _ref_gemm(ta, tb, A, B)
+    y = Y2.T.astype(np.float64) if y2k else Y2.astype(np.float64)  # [N, r2]
+    nn = seg if seg else N
+    for g in range(nseg):
+        ref[:, g * nn:(g + 1) * nn] += X2[:, g * r2:(g + 1) * r2].astype(np.float64) @ y[g * nn:(g + 1) * nn].T
+    Ad, Bd, X2d, Y2d = (dev(t, torch.bfloat16) for t in (A, B, X2, Y2))
+    c32 = _gemm_lowrank(ta, tb, M, N, K, Ad, Bd, X2d, Y2d, r2, seg, y2k, BF16, torch.float32, R=dev(R), alpha=0.5)
+    assert rel(host(c32), 0.5 * ref + R) < 1e-5
+    c16 = _gemm_lowrank(ta, tb, M, N, K, Ad, Bd, X2d, Y2d, r2, seg, y2k, BF16, torch.bfloat16,
+                        R=dev(R, torch.bfloat16))
+    assert rel(host(c16), ref + R) < 4e-3
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    cb = _gemm_lowrank(ta, tb, M, N, K, Ad, Bd, X2d, Y2d, r2, seg, y2k, BF16, torch.float32, beta=-1.0, C0=dev(C0))
+    assert rel(host(cb), ref - C0) < 1e-5
+    # fp32 operands take the SIMT kernels for both terms
+    f32 = _gemm_lowrank(ta, tb, M, N, K, dev(A), dev(B), dev(X2), dev(Y2), r2, seg, y2k, F32, torch.float32)
+    assert rel(host(f32), ref) < 1e-5
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0)])
