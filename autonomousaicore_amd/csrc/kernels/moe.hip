@@ -76,36 +76,59 @@ __global__ __launch_bounds__(256) void moe_route_k(const float* __restrict__ log
 }
 
 // One block: per-expert counts, mean probabilities (double, fixed order) and the aux loss.
-__global__ __launch_bounds__(256) void moe_stats_k(const int64_t* __restrict__ idx, const float* __restrict__ probs,
-                                                   int T, int E, int k, float aux_coef, int64_t* __restrict__ counts,
-                                                   float* __restrict__ mean_probs, float* __restrict__ aux) {
-    __shared__ double sp[256];
-    __shared__ long long sc[256];
+__global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ idx, const float* __restrict__ probs,
+                                                    int T, int E, int k, float aux_coef, int64_t* __restrict__ counts,
+                                                    float* __restrict__ mean_probs, float* __restrict__ aux) {
+    // thread t sums tokens t, t + 1024, ... for 8 experts at a time in registers; the 16 waves
+    // reduce with shuffles, then their partials are added in wave order (fixed: deterministic)
+    __shared__ double sp[16][kMaxE];
+    __shared__ long long sc[16][kMaxE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int e0 = 0; e0 < E; e0 += 8) {
+        double a[8];
+        long long c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a[u] = 0.0;
+            c[u] = 0;
+        }
+        for (int t = threadIdx.x; t < T; t += 1024) {
+            const float* pr = probs + static_cast<int64_t>(t) * E + e0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (e0 + u < E) a[u] += static_cast<double>(pr[u]);
+            for (int j = 0; j < k; ++j) {
+                const int64_t id = idx[static_cast<int64_t>(t) * k + j] - e0;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) c[u] += id == u;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            for (int w = 32; w > 0; w >>= 1) {
+                a[u] += __shfl_xor(a[u], w);
+                c[u] += __shfl_xor(c[u], w);
+            }
+            if (lane == 0 && e0 + u < E) {
+                sp[wave][e0 + u] = a[u];
+                sc[wave][e0 + u] = c[u];
+            }
+        }
+    }
+    __syncthreads();
     __shared__ float mp_s[kMaxE];
     __shared__ long long cnt_s[kMaxE];
-    for (int e = 0; e < E; ++e) {
+    if (threadIdx.x < E) {
         double a = 0.0;
         long long c = 0;
-        for (int t = threadIdx.x; t < T; t += blockDim.x) {
-            a += static_cast<double>(probs[static_cast<int64_t>(t) * E + e]);
-            for (int j = 0; j < k; ++j) c += idx[static_cast<int64_t>(t) * k + j] == e;
+        for (int w = 0; w < 16; ++w) {
+            a += sp[w][threadIdx.x];
+            c += sc[w][threadIdx.x];
         }
-        sp[threadIdx.x] = a;
-        sc[threadIdx.x] = c;
-        __syncthreads();
-        for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-            if (threadIdx.x < w) {
-                sp[threadIdx.x] += sp[threadIdx.x + w];
-                sc[threadIdx.x] += sc[threadIdx.x + w];
-            }
-            __syncthreads();
-        }
-        if (threadIdx.x == 0) {
-            mp_s[e] = static_cast<float>(sp[0] / static_cast<double>(T));
-            cnt_s[e] = sc[0];
-        }
-        __syncthreads();
+        mp_s[threadIdx.x] = static_cast<float>(a / static_cast<double>(T));
+        cnt_s[threadIdx.x] = c;
     }
+    __syncthreads();
     if (threadIdx.x == 0) {
         double a = 0.0;
         const float scale = (static_cast<float>(E) * aux_coef) / (static_cast<float>(T) * static_cast<float>(k));
@@ -124,11 +147,12 @@ __device__ __forceinline__ long long align_rows(long long n) { return (n + kRowA
 // One block per expert: stable positions of its (token, slot) entries in token order, in a
 // row block that starts at offsets[e] (a multiple of 64; the block is padded to 64 rows).
 // dst_row[t * k + j] = row of that entry; src_ent[row] = t * k + j, or -1 for a padding row.
-__global__ __launch_bounds__(256) void moe_permute_k(const int64_t* __restrict__ idx, const int64_t* __restrict__ counts,
-                                                     int T, int k, int E, int64_t* __restrict__ offsets,
-                                                     int* __restrict__ dst_row, int* __restrict__ src_ent) {
+__global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict__ idx, const int64_t* __restrict__ counts,
+                                                      int T, int k, int E, int64_t* __restrict__ offsets,
+                                                      int* __restrict__ dst_row, int* __restrict__ src_ent) {
     const int e = blockIdx.x;
-    __shared__ int scan[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ int wsum[16];
     __shared__ int base_s, start_s;
     if (threadIdx.x == 0) {
         long long off = 0;
@@ -146,29 +170,31 @@ __global__ __launch_bounds__(256) void moe_permute_k(const int64_t* __restrict__
     }
     __syncthreads();
     const int n = T * k;
-    for (int c0 = 0; c0 < n; c0 += blockDim.x) {
-        const int i = c0 + threadIdx.x;
-        const int hit = (i < n && idx[i] == e) ? 1 : 0;
-        scan[threadIdx.x] = hit;
+    // 1024 entries per round: a ballot gives each hit its rank within the wave, the 16 wave
+    // totals its wave's offset, so the order stays the entries' (token-major) order
+    for (int c0 = 0; c0 < n; c0 += 1024) {
+        const int i = c0 + static_cast<int>(threadIdx.x);
+        const bool hit = i < n && idx[i] == e;
+        const unsigned long long m = __ballot(hit);
+        if (lane == 0) wsum[wave] = __popcll(m);
         __syncthreads();
-        for (int w = 1; w < static_cast<int>(blockDim.x); w <<= 1) {  // inclusive Hillis-Steele scan
-            const int v = threadIdx.x >= w ? scan[threadIdx.x - w] : 0;
-            __syncthreads();
-            scan[threadIdx.x] += v;
-            __syncthreads();
-        }
+        int off = base_s;
+        for (int w = 0; w < wave; ++w) off += wsum[w];
         if (hit) {
-            const int row = base_s + scan[threadIdx.x] - 1;
+            const int row = off + __popcll(m & ((1ull << lane) - 1ull));
             dst_row[i] = row;
             src_ent[row] = i;
         }
-        const int total = scan[blockDim.x - 1];
         __syncthreads();
-        if (threadIdx.x == 0) base_s += total;
+        if (threadIdx.x == 0) {
+            int t = 0;
+            for (int w = 0; w < 16; ++w) t += wsum[w];
+            base_s += t;
+        }
         __syncthreads();
     }
     const int end = start_s + static_cast<int>(align_rows(base_s - start_s));
-    for (int r = base_s + threadIdx.x; r < end; r += blockDim.x) src_ent[r] = -1;
+    for (int r = base_s + static_cast<int>(threadIdx.x); r < end; r += 1024) src_ent[r] = -1;
 }
 
 // xp[r, :] = x[token of entry src_ent[r], :], zero for padding rows
@@ -329,7 +355,7 @@ void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_c
     hipLaunchKernelGGL(moe_route_k, dim3(grid_for(T, 256)), dim3(256), 0, s, logits, static_cast<int>(T),
                        static_cast<int>(E), static_cast<int>(k), idx, gsel, probs, rweights);
     AIC_LAUNCH_CHECK("moe_route");
-    hipLaunchKernelGGL(moe_stats_k, dim3(1), dim3(256), 0, s, idx, probs, static_cast<int>(T), static_cast<int>(E),
+    hipLaunchKernelGGL(moe_stats_k, dim3(1), dim3(1024), 0, s, idx, probs, static_cast<int>(T), static_cast<int>(E),
                        static_cast<int>(k), aux_coef, counts, mean_probs, aux);
     AIC_LAUNCH_CHECK("moe_stats");
 }
@@ -340,7 +366,7 @@ void moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k
                  int* dst_row, int* src_ent, hipStream_t s) {
     check_moe(T, E, k);
     AIC_CHECK(idx && counts && offsets && dst_row && src_ent, InvalidArgument, "moe_permute: null argument");
-    hipLaunchKernelGGL(moe_permute_k, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, idx, counts,
+    hipLaunchKernelGGL(moe_permute_k, dim3(static_cast<unsigned>(E)), dim3(1024), 0, s, idx, counts,
                        static_cast<int>(T), static_cast<int>(k), static_cast<int>(E), offsets, dst_row, src_ent);
     AIC_LAUNCH_CHECK("moe_permute");
 }
