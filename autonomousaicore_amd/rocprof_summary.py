@@ -31,15 +31,19 @@ _RULES = [
     (r"attn_bwd|attn_dot", "attn_bwd"),
     (r"rmsnorm_fwd", "rmsnorm_fwd"),
     (r"rmsnorm_bwd|reduce_parts", "rmsnorm_bwd"),
-    (r"rope_k", "rope"),
+    (r"rope_k|rope_v", "rope"),
     (r"swiglu_fwd", "swiglu_fwd"),
     (r"swiglu_bwd", "swiglu_bwd"),
     (r"ce_fwd|ce_mean", "ce_fwd"),
     (r"ce_bwd", "ce_bwd"),
     (r"embed_fwd", "embed_fwd"),
-    (r"embed_sort|embed_seg", "embed_bwd"),
+    (r"embed_sort|embed_seg|embed_run", "embed_bwd"),
     (r"sqnorm|finalize", "grad_norm"),
     (r"adamw", "adamw"),
+    # kernels outside bench.py's event classes (the MoE and QLoRA configurations)
+    (r"moe_", "moe_routing"),
+    (r"int4_", "int4"),
+    (r"splitk_reduce", "gemm_splitk_reduce"),
 ]
 
 
@@ -50,7 +54,7 @@ _ANCHOR = {
     "rmsnorm_bwd": r"rmsnorm_bwd",
     "grad_norm": r"sqnorm_k",
     "ce_fwd": r"ce_fwd",
-    "embed_bwd": r"embed_seg",
+    "embed_bwd": r"embed_sort",
 }
 
 

@@ -74,20 +74,18 @@ def step_flops(c):
     return 6.0 * T * matmul_params(c) + attn
 
 
-def profiled_traffic(kernel_class):
-    """HBM bytes per launch of a kernel class, from the committed rocprofv3 PMC summaries
-    (lines `traffic <class> <bytes>` written by autonomousaicore_amd.rocprof_summary), or None."""
-    pdir = os.path.join(HERE, "profiles")
-    if not os.path.isdir(pdir):
+def profiled_traffic(kernel_class, config):
+    """HBM bytes per launch of a kernel class in this workload, from its committed rocprofv3 PMC
+    summary (lines `traffic <class> <bytes>` written by autonomousaicore_amd.rocprof_summary in
+    profiles/lm_step_<config>_kernel_classes.txt), or None."""
+    path = os.path.join(HERE, "profiles", f"lm_step_{config}_kernel_classes.txt")
+    if not os.path.isfile(path):
         return None
-    for fn in sorted(os.listdir(pdir)):
-        if not fn.endswith(".txt"):
-            continue
-        with open(os.path.join(pdir, fn)) as f:
-            for line in f:
-                parts = line.split()
-                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel_class:
-                    return int(parts[2])
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel_class:
+                return int(parts[2])
     return None
 
 
@@ -236,7 +234,7 @@ def main():
     d = kc[dom["name"]]
     roofline = {"kernel": dom["name"], "bound": d["bound"], "achieved": d["achieved"],
                 "peak": PEAK_BF16_TFLOPS if d["bound"] == "mfma" else PEAK_HBM_GBS, "unit": d["unit"],
-                "frac": d["frac"], "avg_launch_ms": d["avg_ms"], "traffic": profiled_traffic(dom["name"])}
+                "frac": d["frac"], "avg_launch_ms": d["avg_ms"], "traffic": profiled_traffic(dom["name"], args.config)}
 
     cpu = None
     if not args.no_cpu_baseline:
