@@ -737,3 +737,75 @@ int aic_hip_sum_to_shape(const float* grad, int ndim, const int64_t* shape, int 
 }
 
 }  // extern "C"
+
+int aic_checkpoint_write(const char* path, int64_t step, int64_t epoch, float best_val_loss, const char* description,
+                         int64_t n, const char* const* names, const int32_t* ranks, const int64_t* dims,
+                         const int32_t* dtypes, const void* const* data, const uint64_t* nbytes) {
+    return guard([&] {
+        AIC_CHECK(path && n >= 0 && (n == 0 || (names && ranks && dtypes && data && nbytes)), InvalidArgument,
+                  "aic_checkpoint_write: null argument");
+        aic::CheckpointMeta meta{step, epoch, best_val_loss, description ? description : ""};
+        std::vector<aic::CheckpointTensorRef> refs;
+        const int64_t* d = dims;
+        for (int64_t i = 0; i < n; ++i) {
+            AIC_CHECK(names[i] && ranks[i] >= 0 && (ranks[i] == 0 || d), InvalidArgument,
+                      "aic_checkpoint_write: bad tensor ", i);
+            std::vector<int64_t> shape(d, d + ranks[i]);
+            d += ranks[i];
+            refs.push_back({names[i], shape, dtypes[i], data[i], nbytes[i]});
+        }
+        aic::write_checkpoint(path, meta, refs);
+    });
+}
+
+int aic_checkpoint_verify(const char* path, int64_t* num_tensors, int64_t* step, int64_t* epoch, float* best_val_loss) {
+    return guard([&] {
+        AIC_CHECK(path, InvalidArgument, "aic_checkpoint_verify: null path");
+        aic::CheckpointMeta meta;
+        std::vector<aic::CheckpointTensor> ts;
+        aic::read_checkpoint(path, meta, ts);
+        if (num_tensors) *num_tensors = static_cast<int64_t>(ts.size());
+        if (step) *step = meta.step;
+        if (epoch) *epoch = meta.epoch;
+        if (best_val_loss) *best_val_loss = meta.best_val_loss;
+    });
+}
+
+int aic_checkpoint_module_order(int64_t n, const char* const* names, int64_t* order) {
+    return guard([&] {
+        AIC_CHECK(n >= 0 && (n == 0 || (names && order)), InvalidArgument, "aic_checkpoint_module_order: null argument");
+        std::vector<std::string> v;
+        for (int64_t i = 0; i < n; ++i) {
+            AIC_CHECK(names[i], InvalidArgument, "aic_checkpoint_module_order: null name ", i);
+            v.emplace_back(names[i]);
+        }
+        const std::vector<size_t> idx = aic::module_order(v);
+        for (int64_t i = 0; i < n; ++i) order[i] = static_cast<int64_t>(idx[static_cast<size_t>(i)]);
+    });
+}
+
+int aic_lm_save_checkpoint(aic_lm* lm, const char* path, int64_t step, int64_t epoch, float best_val_loss,
+                           const char* description, int with_optimizer) {
+    return guard([&] {
+        AIC_CHECK(lm && path, InvalidArgument, "null argument");
+        aic::CheckpointMeta meta{step, epoch, best_val_loss, description ? description : ""};
+        lm->model->save_checkpoint(path, meta, with_optimizer != 0);
+    });
+}
+
+int aic_lm_load_checkpoint(aic_lm* lm, const char* path, int64_t* step, int64_t* epoch, float* best_val_loss,
+                           char* description, int desc_cap, int* has_optimizer) {
+    return guard([&] {
+        AIC_CHECK(lm && path, InvalidArgument, "null argument");
+        bool has = false;
+        const aic::CheckpointMeta meta = lm->model->load_checkpoint(path, &has);
+        if (step) *step = meta.step;
+        if (epoch) *epoch = meta.epoch;
+        if (best_val_loss) *best_val_loss = meta.best_val_loss;
+        if (description && desc_cap > 0) {
+            std::strncpy(description, meta.description.c_str(), static_cast<size_t>(desc_cap) - 1);
+            description[desc_cap - 1] = '\0';
+        }
+        if (has_optimizer) *has_optimizer = has ? 1 : 0;
+    });
+}

@@ -2,6 +2,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <unordered_map>
 
 #include "../kernels/gemm.hpp"
 #include "../kernels/kernels.hpp"
@@ -359,6 +360,161 @@ void TransformerLM::get_adam_state(float* m, float* v, int64_t* step) const {
         AIC_HIP_CHECK(hipStreamSynchronize(stream_));
         *step = h.ctl.step;
     }
+}
+
+namespace {
+std::vector<float> gather_packed(const float* dev, const std::vector<ParamInfo>& ps, int64_t arena, hipStream_t s) {
+    int64_t n = 0;
+    for (const auto& p : ps) n += p.numel;
+    std::vector<float> out(static_cast<size_t>(n));
+    gather_host(dev, ps, arena, out.data(), s);
+    return out;
+}
+}  // namespace
+
+void TransformerLM::save_checkpoint(const std::string& path, const CheckpointMeta& meta, bool with_optimizer) {
+    struct Src {
+        const ParamInfo* p;
+        const float* host;
+    };
+    std::vector<float> tp = gather_packed(params_dev_, params_, arena_, stream_);
+    std::vector<float> bp;
+    std::vector<Src> model;
+    int64_t o = 0;
+    for (const auto& p : params_) {
+        model.push_back({&p, tp.data() + o});
+        o += p.numel;
+    }
+    if (lora()) {
+        bp = gather_packed(base_dev_, base_, base_arena_, stream_);
+        o = 0;
+        for (const auto& p : base_) {
+            model.push_back({&p, bp.data() + o});
+            o += p.numel;
+        }
+    }
+    std::vector<std::string> names;
+    for (const auto& m : model) names.push_back(m.p->name);
+    std::vector<CheckpointTensorRef> refs;
+    for (size_t i : module_order(names)) {
+        const ParamInfo& p = *model[i].p;
+        refs.push_back({p.name, p.shape, 0, model[i].host, sizeof(float) * static_cast<uint64_t>(p.numel)});
+    }
+    std::vector<float> m, v;
+    int64_t step = 0, good = 0;
+    float scale = 1.0f;
+    if (with_optimizer) {
+        m = gather_packed(m_dev_, params_, arena_, stream_);
+        v = gather_packed(v_dev_, params_, arena_, stream_);
+        DevScalars h{};
+        AIC_HIP_CHECK(hipMemcpyAsync(&h, dev_, sizeof(h), hipMemcpyDeviceToHost, stream_));
+        AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+        step = h.ctl.step;
+        good = h.ctl.good_steps;
+        scale = h.ctl.scale;
+        std::vector<std::string> tn;
+        for (const auto& p : params_) tn.push_back(p.name);
+        const std::vector<size_t> order = module_order(tn);
+        std::vector<int64_t> offs(params_.size());
+        o = 0;
+        for (size_t i = 0; i < params_.size(); ++i) {
+            offs[i] = o;
+            o += params_[i].numel;
+        }
+        for (int which = 0; which < 2; ++which)
+            for (size_t i : order) {
+                const ParamInfo& p = params_[i];
+                refs.push_back({std::string(which ? "optimizer.exp_avg_sq." : "optimizer.exp_avg.") + p.name, p.shape,
+                                0, (which ? v.data() : m.data()) + offs[i],
+                                sizeof(float) * static_cast<uint64_t>(p.numel)});
+            }
+        refs.push_back({"optimizer.step", {1}, 4, &step, sizeof(int64_t)});
+        refs.push_back({"amp.loss_scale", {1}, 0, &scale, sizeof(float)});
+        refs.push_back({"amp.good_steps", {1}, 4, &good, sizeof(int64_t)});
+    }
+    write_checkpoint(path, meta, refs);
+}
+
+CheckpointMeta TransformerLM::load_checkpoint(const std::string& path, bool* has_optimizer) {
+    CheckpointMeta meta;
+    std::vector<CheckpointTensor> ts;
+    read_checkpoint(path, meta, ts);
+    struct Dst {
+        const ParamInfo* p;
+        int64_t packed;  // offset in the packed host copy
+        int arena;       // 0 trainable, 1 base
+    };
+    std::unordered_map<std::string, Dst> where;
+    int64_t o = 0;
+    for (const auto& p : params_) {
+        where[p.name] = {&p, o, 0};
+        o += p.numel;
+    }
+    if (lora()) {
+        o = 0;
+        for (const auto& p : base_) {
+            where[p.name] = {&p, o, 1};
+            o += p.numel;
+        }
+    }
+    std::vector<float> tp = gather_packed(params_dev_, params_, arena_, stream_);
+    std::vector<float> bp = lora() ? gather_packed(base_dev_, base_, base_arena_, stream_) : std::vector<float>();
+    std::vector<float> m, v;
+    bool got_t = false, got_b = false, got_m = false, got_v = false, got_ctl = false;
+    int64_t step = -1, good = -1;
+    float scale = -1.0f;
+    auto check_f32 = [&](const CheckpointTensor& t, const ParamInfo& p) {
+        AIC_CHECK(t.dims == p.shape, ShapeMismatch, "Shape mismatch loading tensor '", t.name, "'");
+        AIC_CHECK(t.dtype == 0 && t.data.size() == sizeof(float) * static_cast<size_t>(p.numel), DTypeMismatch,
+                  "DType mismatch loading tensor '", t.name, "'");
+    };
+    for (const auto& t : ts) {
+        const std::string kM = "optimizer.exp_avg.", kV = "optimizer.exp_avg_sq.";
+        if (auto it = where.find(t.name); it != where.end()) {
+            check_f32(t, *it->second.p);
+            float* dst = (it->second.arena ? bp.data() : tp.data()) + it->second.packed;
+            std::memcpy(dst, t.data.data(), t.data.size());
+            (it->second.arena ? got_b : got_t) = true;
+        } else if (t.name.rfind(kV, 0) == 0 || t.name.rfind(kM, 0) == 0) {
+            const bool is_v = t.name.rfind(kV, 0) == 0;
+            auto jt = where.find(t.name.substr(is_v ? kV.size() : kM.size()));
+            if (jt == where.end() || jt->second.arena != 0) continue;
+            check_f32(t, *jt->second.p);
+            std::vector<float>& dst = is_v ? v : m;
+            if (dst.empty()) dst = gather_packed(is_v ? v_dev_ : m_dev_, params_, arena_, stream_);
+            std::memcpy(dst.data() + jt->second.packed, t.data.data(), t.data.size());
+            (is_v ? got_v : got_m) = true;
+        } else if (t.name == "optimizer.step" && t.dtype == 4 && t.data.size() == 8) {
+            std::memcpy(&step, t.data.data(), 8);
+            got_ctl = true;
+        } else if (t.name == "amp.good_steps" && t.dtype == 4 && t.data.size() == 8) {
+            std::memcpy(&good, t.data.data(), 8);
+            got_ctl = true;
+        } else if (t.name == "amp.loss_scale" && t.dtype == 0 && t.data.size() == 4) {
+            std::memcpy(&scale, t.data.data(), 4);
+            got_ctl = true;
+        }
+    }
+    if (got_t) scatter_to_device(tp.data(), params_, arena_, params_dev_, stream_);
+    if (got_b) {
+        scatter_to_device(bp.data(), base_, base_arena_, base_dev_, stream_);
+        quantize_base();
+    }
+    if (got_m) scatter_to_device(m.data(), params_, arena_, m_dev_, stream_);
+    if (got_v) scatter_to_device(v.data(), params_, arena_, v_dev_, stream_);
+    if (got_ctl) {
+        DevScalars h{};
+        AIC_HIP_CHECK(hipMemcpyAsync(&h, dev_, sizeof(h), hipMemcpyDeviceToHost, stream_));
+        AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+        if (step >= 0) h.ctl.step = static_cast<int>(step);
+        if (good >= 0) h.ctl.good_steps = static_cast<int>(good);
+        if (scale > 0.0f) h.ctl.scale = scale;
+        AIC_HIP_CHECK(hipMemcpyAsync(dev_, &h, sizeof(h), hipMemcpyHostToDevice, stream_));
+    }
+    refresh_low_precision();
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    if (has_optimizer) *has_optimizer = got_m && got_v && step >= 0;
+    return meta;
 }
 
 void TransformerLM::init_normal(uint64_t seed, float std, bool residual_scaling) {

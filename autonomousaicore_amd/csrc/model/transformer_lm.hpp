@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "../../../include/aic_hip.h"
+#include "../runtime/checkpoint.hpp"
 #include "../runtime/dtype.hpp"
 #include "../runtime/profiler.hpp"
 #include "moe_ffn.hpp"
@@ -112,6 +113,18 @@ public:
     void get_grads(float* host) const;
     void get_adam_state(float* m, float* v, int64_t* step) const;
     void init_normal(uint64_t seed, float std, bool residual_scaling);
+
+    // The reference's .aic checkpoint (save_checkpoint / load_checkpoint,
+    // src/train/checkpoint.cpp:30-186): every parameter (with QLoRA the frozen base and the
+    // adapters) as fp32 under its reference name, in Module::named_parameters() order.  With
+    // with_optimizer the file also carries the AdamW moments ("optimizer.exp_avg.<name>",
+    // "optimizer.exp_avg_sq.<name>"), the step count ("optimizer.step", i64) and the loss
+    // scaler ("amp.loss_scale" f32, "amp.good_steps" i64) after the parameters -- entries the
+    // reference's loader skips as unknown names.  load_checkpoint restores what the file holds
+    // (unknown names are skipped, a shape or dtype mismatch throws) and reports in
+    // *has_optimizer whether optimizer state was found.
+    void save_checkpoint(const std::string& path, const CheckpointMeta& meta, bool with_optimizer);
+    CheckpointMeta load_checkpoint(const std::string& path, bool* has_optimizer);
 
     // ids/targets: device pointers to [B, S] int64.
     void train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);

@@ -81,6 +81,16 @@ class TrainingConfig:
 
 
 @dataclass
+class CheckpointMetadata:
+    """train::CheckpointMetadata (include/train/checkpoint.hpp:15-22)."""
+    step: int = 0
+    epoch: int = 0
+    best_val_loss: float = 0.0
+    description: str = ""
+    has_optimizer: bool = False
+
+
+@dataclass
 class StepMetrics:
     loss: float
     grad_norm: float
@@ -205,6 +215,25 @@ class TransformerLM:
         loss = C.c_float()
         _lib.call("aic_lm_eval_loss", self._h, ip, tp, B, S, 1 if on_dev else 0, C.byref(loss))
         return float(loss.value)
+
+    def save_checkpoint(self, path: str, meta: "CheckpointMetadata | None" = None,
+                        with_optimizer: bool = False) -> None:
+        """save_checkpoint (src/train/checkpoint.cpp:30-95): the .aic file of every parameter;
+        with_optimizer adds the AdamW moments, step and loss-scaler state."""
+        meta = meta or CheckpointMetadata()
+        _lib.call("aic_lm_save_checkpoint", self._h, path.encode(), meta.step, meta.epoch, meta.best_val_loss,
+                  meta.description.encode(), 1 if with_optimizer else 0)
+
+    def load_checkpoint(self, path: str) -> "CheckpointMetadata":
+        """load_checkpoint (src/train/checkpoint.cpp:97-186); `has_optimizer` on the result says
+        whether AdamW state was restored."""
+        step, epoch, loss = C.c_int64(), C.c_int64(), C.c_float()
+        desc = C.create_string_buffer(4096)
+        has = C.c_int()
+        _lib.call("aic_lm_load_checkpoint", self._h, path.encode(), C.byref(step), C.byref(epoch), C.byref(loss),
+                  desc, 4096, C.byref(has))
+        return CheckpointMetadata(int(step.value), int(epoch.value), float(loss.value), desc.value.decode(),
+                                  bool(has.value))
 
     def synchronize(self) -> None:
         _lib.call("aic_lm_synchronize", self._h)

@@ -471,6 +471,35 @@ int aic_lm_profile(aic_lm* lm, int enable);
 /* Synchronises, then writes up to cap classes with at least one launch; *n = count. */
 int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n);
 
+/* ---------------------------------------------------------------- checkpoints ------- */
+/* The reference's .aic format (save_checkpoint / load_checkpoint, src/train/checkpoint.cpp:30-186;
+ * docs/architecture.md:96-117): header (magic 'AIC0', version 1, step, epoch, best_val_loss,
+ * description), then per tensor name, rank, i64 dims, i32 dtype (reference DType numbering),
+ * u64 nbytes, data and its Adler-32.  Host memory only; no GPU is needed.
+ * aic_checkpoint_write: tensor i has ranks[i] dims, taken in turn from `dims`.
+ * aic_checkpoint_verify: reads the whole file, checking magic, version and every checksum
+ * (FormatError otherwise); any output may be NULL.
+ * aic_checkpoint_module_order: the order in which Module::named_parameters()
+ * (include/nn/module.hpp:63-76) visits the given parameter names, as indices into names. */
+int aic_checkpoint_write(const char* path, int64_t step, int64_t epoch, float best_val_loss, const char* description,
+                         int64_t n, const char* const* names, const int32_t* ranks, const int64_t* dims,
+                         const int32_t* dtypes, const void* const* data, const uint64_t* nbytes);
+int aic_checkpoint_verify(const char* path, int64_t* num_tensors, int64_t* step, int64_t* epoch, float* best_val_loss);
+int aic_checkpoint_module_order(int64_t n, const char* const* names, int64_t* order);
+/* Save / load a model.  The parameters (QLoRA: the frozen base and the adapters) are written
+ * as fp32 in named_parameters() order, so a file without optimizer state is what the
+ * reference's save_checkpoint writes for the same weights.  with_optimizer appends the AdamW
+ * moments ("optimizer.exp_avg.<name>", "optimizer.exp_avg_sq.<name>"), "optimizer.step" (i64)
+ * and the loss scaler ("amp.loss_scale" f32, "amp.good_steps" i64), which the reference's
+ * loader skips as unknown names; the reference saves no optimizer state (the argument is
+ * unused at checkpoint.cpp:34).  Loading skips unknown names and fails on a shape or dtype
+ * mismatch, as the reference does; *has_optimizer reports whether AdamW state was restored.
+ * description: up to desc_cap bytes including the terminating NUL. */
+int aic_lm_save_checkpoint(aic_lm* lm, const char* path, int64_t step, int64_t epoch, float best_val_loss,
+                           const char* description, int with_optimizer);
+int aic_lm_load_checkpoint(aic_lm* lm, const char* path, int64_t* step, int64_t* epoch, float* best_val_loss,
+                           char* description, int desc_cap, int* has_optimizer);
+
 /* ---------------------------------------------------------------- synthetic data ---- */
 /* Host-side counter-based generators (splitmix64), shared by the tests and the bench.
  * Uniform ids in [0, vocab); Zipf(s) ids (P(k) ~ k^-s over ranks k = 1..vocab, id = k-1,
