@@ -136,6 +136,20 @@ SIGNATURES = {
     "aic_lm_last_stats": (i32, [vp, C.POINTER(StepStats)]),
     "aic_lm_profile": (i32, [vp, i32]),
     "aic_lm_profile_stats": (i32, [vp, C.POINTER(KernelStat), i32, C.POINTER(i32)]),
+    "aic_dataset_open": (i32, [C.c_char_p, i64, i64, C.POINTER(vp)]),
+    "aic_dataset_from_tokens": (i32, [vp, i64, i64, i64, C.POINTER(vp)]),
+    "aic_dataset_destroy": (i32, [vp]),
+    "aic_dataset_size": (i64, [vp]),
+    "aic_dataset_total_tokens": (i64, [vp]),
+    "aic_dataset_get_item": (i32, [vp, i64, vp, vp]),
+    "aic_dataset_write_binary_file": (i32, [C.c_char_p, vp, i64]),
+    "aic_loader_create": (i32, [vp, i64, i32, i32, C.c_uint64, i32, C.POINTER(vp)]),
+    "aic_loader_destroy": (i32, [vp]),
+    "aic_loader_num_batches": (i64, [vp]),
+    "aic_loader_has_next": (i32, [vp]),
+    "aic_loader_reset": (i32, [vp]),
+    "aic_loader_next_host": (i32, [vp, vp, vp, i64p]),
+    "aic_loader_next_device": (i32, [vp, vp, vp, i64p, vp]),
     "aic_synth_uniform_ids": (i32, [C.c_uint64, i64, i64, vp]),
     "aic_synth_zipf_ids": (i32, [C.c_uint64, i64, i64, C.c_double, vp]),
     "aic_synth_normal": (i32, [C.c_uint64, i64, f32, f32, vp]),

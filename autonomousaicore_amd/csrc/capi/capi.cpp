@@ -10,6 +10,7 @@
 
 #include "../../../include/aic_hip.h"
 #include "../data/synthetic.hpp"
+#include "../data/token_data.hpp"
 #include "../kernels/gemm.hpp"
 #include "../kernels/kernels.hpp"
 #include "../model/moe_ffn.hpp"
@@ -807,5 +808,89 @@ int aic_lm_load_checkpoint(aic_lm* lm, const char* path, int64_t* step, int64_t*
             description[desc_cap - 1] = '\0';
         }
         if (has_optimizer) *has_optimizer = has ? 1 : 0;
+    });
+}
+
+struct aic_token_dataset {
+    std::shared_ptr<aic::data::TokenDataset> ds;
+};
+struct aic_token_loader {
+    std::unique_ptr<aic::data::TokenLoader> loader;
+};
+
+int aic_dataset_open(const char* path, int64_t seq_len, int64_t stride, aic_token_dataset** out) {
+    return guard([&] {
+        AIC_CHECK(path && out, InvalidArgument, "null argument");
+        *out = new aic_token_dataset{std::make_shared<aic::data::TokenDataset>(path, seq_len, stride)};
+    });
+}
+
+int aic_dataset_from_tokens(const int64_t* tokens, int64_t n, int64_t seq_len, int64_t stride,
+                            aic_token_dataset** out) {
+    return guard([&] {
+        AIC_CHECK(out && n >= 0 && (tokens || n == 0), InvalidArgument, "null argument");
+        std::vector<int64_t> v(tokens, tokens + n);
+        *out = new aic_token_dataset{std::make_shared<aic::data::TokenDataset>(std::move(v), seq_len, stride)};
+    });
+}
+
+int aic_dataset_destroy(aic_token_dataset* ds) {
+    return guard([&] { delete ds; });
+}
+
+int64_t aic_dataset_size(const aic_token_dataset* ds) { return ds ? ds->ds->size() : -1; }
+int64_t aic_dataset_total_tokens(const aic_token_dataset* ds) { return ds ? ds->ds->total_tokens() : -1; }
+
+int aic_dataset_get_item(const aic_token_dataset* ds, int64_t idx, int64_t* input, int64_t* target) {
+    return guard([&] {
+        AIC_CHECK(ds, InvalidArgument, "null dataset");
+        ds->ds->get_item(idx, input, target);
+    });
+}
+
+int aic_dataset_write_binary_file(const char* path, const int64_t* tokens, int64_t n) {
+    return guard([&] {
+        AIC_CHECK(path && n >= 0 && (tokens || n == 0), InvalidArgument, "null argument");
+        aic::data::TokenDataset::write_binary_file(path, tokens, n);
+    });
+}
+
+int aic_loader_create(aic_token_dataset* ds, int64_t batch_size, int shuffle, int drop_last, uint64_t seed,
+                      int resident, aic_token_loader** out) {
+    return guard([&] {
+        AIC_CHECK(ds && out, InvalidArgument, "null argument");
+        *out = new aic_token_loader{std::make_unique<aic::data::TokenLoader>(ds->ds, batch_size, shuffle != 0,
+                                                                             drop_last != 0, seed, resident != 0)};
+    });
+}
+
+int aic_loader_destroy(aic_token_loader* loader) {
+    return guard([&] { delete loader; });
+}
+
+int64_t aic_loader_num_batches(const aic_token_loader* loader) { return loader ? loader->loader->num_batches() : -1; }
+int aic_loader_has_next(const aic_token_loader* loader) { return loader && loader->loader->has_next() ? 1 : 0; }
+
+int aic_loader_reset(aic_token_loader* loader) {
+    return guard([&] {
+        AIC_CHECK(loader, InvalidArgument, "null loader");
+        loader->loader->reset();
+    });
+}
+
+int aic_loader_next_host(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch) {
+    return guard([&] {
+        AIC_CHECK(loader && inputs && targets, InvalidArgument, "null argument");
+        const int64_t b = loader->loader->next_host(inputs, targets);
+        if (actual_batch) *actual_batch = b;
+    });
+}
+
+int aic_loader_next_device(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch,
+                           aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(loader && inputs && targets, InvalidArgument, "null argument");
+        const int64_t b = loader->loader->next_device(inputs, targets, st(stream));
+        if (actual_batch) *actual_batch = b;
     });
 }

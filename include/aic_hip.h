@@ -500,6 +500,42 @@ int aic_lm_save_checkpoint(aic_lm* lm, const char* path, int64_t step, int64_t e
 int aic_lm_load_checkpoint(aic_lm* lm, const char* path, int64_t* step, int64_t* epoch, float* best_val_loss,
                            char* description, int desc_cap, int* has_optimizer);
 
+/* ---------------------------------------------------------------- token data -------- */
+/* BinaryTokenDataset (include/data/dataset.hpp, src/data/dataset.cpp:155-219): a file of raw
+ * int64 tokens (memory-mapped) or an in-memory copy; sample i is tokens[i*stride, +seq_len]
+ * with targets shifted by one token; size = (total - 1 - seq_len) / stride + 1 (0 when
+ * total < seq_len + 1); stride <= 0 means seq_len.  get_item writes seq_len tokens to each
+ * (host) output, either may be NULL. */
+typedef struct aic_token_dataset aic_token_dataset;
+int aic_dataset_open(const char* path, int64_t seq_len, int64_t stride, aic_token_dataset** out);
+int aic_dataset_from_tokens(const int64_t* tokens, int64_t n, int64_t seq_len, int64_t stride,
+                            aic_token_dataset** out);
+int aic_dataset_destroy(aic_token_dataset* ds);
+int64_t aic_dataset_size(const aic_token_dataset* ds);
+int64_t aic_dataset_total_tokens(const aic_token_dataset* ds);
+int aic_dataset_get_item(const aic_token_dataset* ds, int64_t idx, int64_t* input, int64_t* target);
+/* BinaryTokenDataset::write_binary_file (src/data/dataset.cpp:207-217). */
+int aic_dataset_write_binary_file(const char* path, const int64_t* tokens, int64_t n);
+/* DataLoader (include/data/dataloader.hpp, src/data/dataloader.cpp:12-78): batches of
+ * batch_size samples (the last one smaller unless drop_last), the sample order shuffled with
+ * std::shuffle over a std::mt19937_64(seed) at creation and at every reset (the reference's
+ * order exactly, with the same standard library).  The loader keeps the dataset alive.
+ * next_host: [b, seq_len] int64 inputs / targets in host memory; *actual_batch = b.
+ * next_device: the same batch into device buffers, ordered on `stream`; with resident = 1 the
+ * token array is copied to the device once (first call) and each batch is one gather kernel
+ * over its window starts, otherwise the batch is assembled in pinned host memory and copied
+ * asynchronously (two staging buffers, each reused after its copy completed). */
+typedef struct aic_token_loader aic_token_loader;
+int aic_loader_create(aic_token_dataset* ds, int64_t batch_size, int shuffle, int drop_last, uint64_t seed,
+                      int resident, aic_token_loader** out);
+int aic_loader_destroy(aic_token_loader* loader);
+int64_t aic_loader_num_batches(const aic_token_loader* loader);
+int aic_loader_has_next(const aic_token_loader* loader);
+int aic_loader_reset(aic_token_loader* loader);
+int aic_loader_next_host(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch);
+int aic_loader_next_device(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch,
+                           aic_stream stream);
+
 /* ---------------------------------------------------------------- synthetic data ---- */
 /* Host-side counter-based generators (splitmix64), shared by the tests and the bench.
  * Uniform ids in [0, vocab); Zipf(s) ids (P(k) ~ k^-s over ranks k = 1..vocab, id = k-1,
