@@ -119,6 +119,8 @@ SIGNATURES = {
     "aic_lm_base_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
     "aic_lm_set_base_params": (i32, [vp, vp]),
     "aic_lm_set_params": (i32, [vp, vp]),
+    "aic_lm_forward_step": (i32, [vp, vp, i64, i64, i64, i32, vp]),
+    "aic_lm_generate": (i32, [vp, vp, i64, i64, f32, i32, f32, i64, C.c_uint64, vp, i64p]),
     "aic_lm_save_checkpoint": (i32, [vp, C.c_char_p, i64, i64, f32, C.c_char_p, i32]),
     "aic_lm_load_checkpoint": (i32, [vp, C.c_char_p, i64p, i64p, f32p, C.c_char_p, i32, C.POINTER(i32)]),
     "aic_checkpoint_write": (i32, [C.c_char_p, i64, i64, f32, C.c_char_p, i64, C.POINTER(C.c_char_p),

@@ -3,6 +3,7 @@
 // the error code; nothing throws across the ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <new>
@@ -892,5 +893,37 @@ int aic_loader_next_device(aic_token_loader* loader, int64_t* inputs, int64_t* t
         AIC_CHECK(loader && inputs && targets, InvalidArgument, "null argument");
         const int64_t b = loader->loader->next_device(inputs, targets, st(stream));
         if (actual_batch) *actual_batch = b;
+    });
+}
+
+int aic_lm_forward_step(aic_lm* lm, const int64_t* ids, int64_t B, int64_t S, int64_t start_pos, int on_device,
+                        float* logits) {
+    return guard([&] {
+        AIC_CHECK(lm && ids && logits && B > 0 && S > 0, InvalidArgument, "forward_step: bad arguments");
+        auto* m = lm->model;
+        hipStream_t s = m->stream();
+        const int64_t V = m->config().vocab_size, T = B * S;
+        if (on_device) {
+            m->forward_step(ids, B, S, start_pos, logits);
+            return;
+        }
+        aic::DeviceBuffer dids(sizeof(int64_t) * static_cast<size_t>(T), s), dl(sizeof(float) * T * V, s);
+        AIC_HIP_CHECK(hipMemcpyAsync(dids.get(), ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
+        m->forward_step(dids.as<int64_t>(), B, S, start_pos, dl.as<float>());
+        AIC_HIP_CHECK(hipMemcpyAsync(logits, dl.get(), sizeof(float) * T * V, hipMemcpyDeviceToHost, s));
+        AIC_HIP_CHECK(hipStreamSynchronize(s));
+    });
+}
+
+int aic_lm_generate(aic_lm* lm, const int64_t* prompt, int64_t n_prompt, int64_t max_new_tokens, float temperature,
+                    int top_k, float top_p, int64_t eos_token_id, uint64_t seed, int64_t* out_tokens, int64_t* n_out) {
+    return guard([&] {
+        AIC_CHECK(lm && out_tokens && n_out && n_prompt >= 0 && (prompt || n_prompt == 0), InvalidArgument,
+                  "generate: bad arguments");
+        std::vector<int64_t> p(prompt, prompt + n_prompt);
+        const std::vector<int64_t> out =
+            lm->model->generate(p, max_new_tokens, temperature, top_k, top_p, eos_token_id, seed);
+        std::copy(out.begin(), out.end(), out_tokens);
+        *n_out = static_cast<int64_t>(out.size());
     });
 }

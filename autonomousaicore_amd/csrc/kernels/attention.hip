@@ -702,6 +702,74 @@ __global__ __launch_bounds__(64) void attn_bwd_q_simt(const T* __restrict__ q, c
         for (int d = 0; d < HD; ++d) st(dq, (tok0 + qi) * ldd + hoff + d, acc[d] * scale);
 }
 
+// ---------------------------------------------------------------------------------------
+// Attention over a KV cache (decode): block (i, h, b) is query i of the S_new new tokens at
+// position start_pos + i; it attends to cache rows 0 .. start_pos + i.  Scores go to LDS
+// (one wave per key, lanes across head_dim, shuffle sums), then max, exp and sum in fixed
+// trees, then each thread accumulates one head_dim column over a strided key subset and the
+// subsets are added in a fixed order.  fp32 math; the row sums are deterministic.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void attn_cached_k(const T* __restrict__ q, int64_t ldq, const T* __restrict__ kc,
+                                                     const T* __restrict__ vc, int64_t ldkv, int64_t bstride,
+                                                     T* __restrict__ o, int64_t ldo, int S_new, int start_pos, int hd,
+                                                     float scale) {
+    extern __shared__ float sm_dec[];
+    const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int L = start_pos + i + 1;
+    float* sc = sm_dec;           // [L] scores, then probabilities
+    float* red = sm_dec + L;      // [256]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const T* qr = q + (static_cast<int64_t>(b) * S_new + i) * ldq + static_cast<int64_t>(h) * hd;
+    const T* kb = kc + static_cast<int64_t>(b) * bstride + static_cast<int64_t>(h) * hd;
+    const T* vb = vc + static_cast<int64_t>(b) * bstride + static_cast<int64_t>(h) * hd;
+    const float q0 = lane < hd ? ld(qr, lane) : 0.0f, q1 = lane + 64 < hd ? ld(qr, lane + 64) : 0.0f;
+    for (int j = wave; j < L; j += 4) {
+        const T* kr = kb + static_cast<int64_t>(j) * ldkv;
+        float p = (lane < hd ? q0 * ld(kr, lane) : 0.0f) + (lane + 64 < hd ? q1 * ld(kr, lane + 64) : 0.0f);
+#pragma unroll
+        for (int w = 32; w > 0; w >>= 1) p += __shfl_xor(p, w);
+        if (lane == 0) sc[j] = p * scale;
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int j = tid; j < L; j += 256) m = fmaxf(m, sc[j]);
+    red[tid] = m;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+        __syncthreads();
+    }
+    m = red[0];
+    __syncthreads();
+    float sum = 0.0f;
+    for (int j = tid; j < L; j += 256) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        sum += e;
+    }
+    red[tid] = sum;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] += red[tid + w];
+        __syncthreads();
+    }
+    const float inv = 1.0f / red[0];
+    __syncthreads();
+    // thread t: column t % hd over keys j = t / hd, t / hd + G, ... (G = 256 / hd groups)
+    const int G = 256 / hd, d = tid % hd, g = tid / hd;
+    float acc = 0.0f;
+    if (g < G)
+        for (int j = g; j < L; j += G) acc += sc[j] * ld(vb + static_cast<int64_t>(j) * ldkv, d);
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float t = 0.0f;
+        for (int u = 0; u < G; ++u) t += red[u * hd + tid];
+        st(o + (static_cast<int64_t>(b) * S_new + i) * ldo + static_cast<int64_t>(h) * hd, tid, t * inv);
+    }
+}
+
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool mfma_ok(const void* q, const void* k, const void* v, int64_t ldq, const void* o, int64_t ldo, int64_t hd) {
@@ -829,6 +897,41 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
     }
     if (dt == DType::Float32) bwd_simt<float>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
     else bwd_simt<bf16>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
+}
+
+void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,
+                 int64_t ldo, int64_t B, int64_t H, int64_t S_new, int64_t start_pos, int64_t hd, float scale, DType dt,
+                 hipStream_t s) {
+    AIC_CHECK(B >= 0 && H > 0 && S_new >= 0 && start_pos >= 0 && hd > 0 && hd <= 128 && 256 % hd == 0 &&
+                  ldq >= H * hd && ldkv >= H * hd && ldo >= H * hd,
+              InvalidArgument, "attn_cached: bad shape");
+    AIC_CHECK(start_pos + S_new <= cache_rows && start_pos + S_new <= 16384, InvalidArgument,
+              "attn_cached: the cache holds ", cache_rows, " positions (at most 16384), needed ", start_pos + S_new);
+    if (B == 0 || S_new == 0) return;
+    const dim3 grid(static_cast<unsigned>(S_new), static_cast<unsigned>(H), static_cast<unsigned>(B));
+    const size_t lds = sizeof(float) * static_cast<size_t>(start_pos + S_new + 256);
+    const int64_t bstride = cache_rows * ldkv;
+    static bool configured = false;  // allow the scores of up to 16384 positions in LDS
+    if (!configured) {
+        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_cached_k<bf16>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_cached_k<float>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        configured = true;
+    }
+    if (dt == DType::BFloat16)
+        hipLaunchKernelGGL(attn_cached_k<bf16>, grid, dim3(256), lds, s, static_cast<const bf16*>(q), ldq,
+                           static_cast<const bf16*>(kc), static_cast<const bf16*>(vc), ldkv, bstride,
+                           static_cast<bf16*>(o), ldo, static_cast<int>(S_new), static_cast<int>(start_pos),
+                           static_cast<int>(hd), scale);
+    else if (dt == DType::Float32)
+        hipLaunchKernelGGL(attn_cached_k<float>, grid, dim3(256), lds, s, static_cast<const float*>(q), ldq,
+                           static_cast<const float*>(kc), static_cast<const float*>(vc), ldkv, bstride,
+                           static_cast<float*>(o), ldo, static_cast<int>(S_new), static_cast<int>(start_pos),
+                           static_cast<int>(hd), scale);
+    else
+        AIC_THROW(DTypeMismatch, "attn_cached: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("attn_cached");
 }
 
 }  // namespace aic::hip

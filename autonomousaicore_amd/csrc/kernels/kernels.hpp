@@ -92,6 +92,11 @@ void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void*
 void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
               int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
               int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);
+// Queries of S_new new tokens (rows of q, [B*S_new] x ldq) at positions start_pos.. against a
+// KV cache kc / vc ([B][cache_rows][ldkv], positions 0 .. start_pos+S_new-1 filled), causal.
+void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,
+                 int64_t ldo, int64_t B, int64_t H, int64_t S_new, int64_t start_pos, int64_t hd, float scale, DType dt,
+                 hipStream_t s);
 
 // Optimizer tail (optim.hip)
 struct OptimCtl;  // = aic_optim_ctl (include/aic_hip.h)

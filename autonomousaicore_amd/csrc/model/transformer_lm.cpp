@@ -1,7 +1,10 @@
 #include "transformer_lm.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <numeric>
+#include <random>
 #include <unordered_map>
 
 #include "../kernels/gemm.hpp"
@@ -74,6 +77,72 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.y2_kmajor = lr->y2_kmajor;
     }
     hip::gemm(a, s);
+}
+
+}  // namespace
+
+namespace {
+
+// The next token from fp32 logits, as TransformerLM::generate samples it
+// (src/models/transformer_lm.cpp:113-206): argmax when temperature <= 0.001 or top_k == 1;
+// otherwise softmax(logits / temperature) (sum in double), top-k filtering (std::partial_sort
+// by probability) and renormalisation, top-p filtering (std::sort by probability, cumulative
+// sum in double, cut at the first index reaching top_p) and renormalisation, then one draw of
+// std::discrete_distribution from rng.
+int64_t sample_token(const std::vector<float>& l, float temperature, int top_k, float top_p, std::mt19937_64& rng) {
+    const int64_t V = static_cast<int64_t>(l.size());
+    if (temperature <= 0.001f || top_k == 1) return std::max_element(l.begin(), l.end()) - l.begin();
+    std::vector<float> z(l.size());
+    float mx = l[0] / temperature;
+    for (int64_t v = 0; v < V; ++v) {
+        z[v] = l[v] / temperature;
+        if (z[v] > mx) mx = z[v];
+    }
+    std::vector<float> p(l.size());
+    double sum = 0.0;
+    for (int64_t v = 0; v < V; ++v) {
+        p[v] = std::exp(z[v] - mx);
+        sum += p[v];
+    }
+    for (auto& e : p) e /= static_cast<float>(sum);
+    if (top_k > 0 && top_k < V) {
+        std::vector<int64_t> idx(l.size());
+        std::iota(idx.begin(), idx.end(), int64_t{0});
+        std::partial_sort(idx.begin(), idx.begin() + top_k, idx.end(), [&p](int64_t a, int64_t b) { return p[a] > p[b]; });
+        std::vector<float> kept(l.size(), 0.0f);
+        double ks = 0.0;
+        for (int i = 0; i < top_k; ++i) {
+            kept[idx[i]] = p[idx[i]];
+            ks += p[idx[i]];
+        }
+        for (int i = 0; i < top_k; ++i) kept[idx[i]] /= static_cast<float>(ks);
+        p = std::move(kept);
+    }
+    if (top_p < 1.0f && top_p > 0.0f) {
+        std::vector<std::pair<float, int64_t>> pi;
+        for (int64_t v = 0; v < V; ++v)
+            if (p[v] > 0.0f) pi.push_back({p[v], v});
+        std::sort(pi.begin(), pi.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
+        double c = 0.0;
+        size_t cut = pi.size();
+        for (size_t i = 0; i < pi.size(); ++i) {
+            c += pi[i].first;
+            if (c >= top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        std::vector<float> kept(l.size(), 0.0f);
+        double ns = 0.0;
+        for (size_t i = 0; i < cut; ++i) {
+            kept[pi[i].second] = pi[i].first;
+            ns += pi[i].first;
+        }
+        for (size_t i = 0; i < cut; ++i) kept[pi[i].second] /= static_cast<float>(ns);
+        p = std::move(kept);
+    }
+    std::discrete_distribution<int64_t> dist(p.begin(), p.end());
+    return dist(rng);
 }
 
 }  // namespace
@@ -250,6 +319,10 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
 TransformerLM::~TransformerLM() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     moe_.clear();  // their buffers are freed on stream_, so before it is destroyed
+    if (kv_cache_ && stream_) {
+        (void)hipFreeAsync(kv_cache_, stream_);
+        (void)hipStreamSynchronize(stream_);
+    }
     for (void* p : {static_cast<void*>(params_dev_), static_cast<void*>(grads_dev_), static_cast<void*>(m_dev_),
                     static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
                     static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
@@ -837,6 +910,138 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         hip::adamw_multi(pp, gp, mp, vp, low_dev_ ? lp : nullptr, sizes, 1, a.lr, a.beta1, a.beta2, a.eps,
                          a.weight_decay, 0, &dev_->ctl, s);
     }
+}
+
+void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64_t start_pos, float* logits) {
+    const int64_t V = cfg_.vocab_size, d = cfg_.hidden_dim, L = cfg_.num_layers, H = cfg_.num_heads,
+                  f = cfg_.intermediate_dim, hd = d / H, T = B * S, MS = cfg_.max_seq_len;
+    AIC_CHECK(ids && logits && B > 0 && S > 0 && start_pos >= 0, InvalidArgument, "forward_step: bad arguments");
+    AIC_CHECK(start_pos + S <= MS, OutOfRange, "forward_step: positions up to ", start_pos + S,
+              " exceed max_seq_len ", MS);
+    AIC_CHECK(start_pos == 0 || B == kv_B_, InvalidState,
+              "forward_step: a continuation (start_pos > 0) must keep the batch size of its sequence");
+    const DType dt = cfg_.compute;
+    const size_t es = dtype_size(dt);
+    const float eps = cfg_.rms_norm_eps, scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    hipStream_t s = stream_;
+    if (start_pos == 0 && B != kv_B_) {
+        if (kv_cache_) AIC_HIP_CHECK(hipFreeAsync(kv_cache_, s));
+        kv_cache_ = nullptr;
+        AIC_HIP_CHECK(hipMallocAsync(&kv_cache_, es * static_cast<size_t>(L * 2 * B * MS * d), s));
+        kv_B_ = B;
+    }
+    auto act = [&](int64_t elems) { return DeviceBuffer(es * static_cast<size_t>(elems), s); };
+    auto f32 = [&](int64_t elems) { return DeviceBuffer(sizeof(float) * static_cast<size_t>(elems), s); };
+    auto at = [&](const DeviceBuffer& b, int64_t elem) {
+        return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
+    };
+    const bool moe = cfg_.num_experts > 0, ql = lora();
+    const int64_t r = cfg_.lora_rank;
+    const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
+    DeviceBuffer xa = act(T * d), xb = act(T * d), h = act(T * d), qkv = act(T * 3 * d), ob = act(T * d),
+                 x1 = act(T * d), gu = act(moe ? 0 : T * 2 * f), am = act(moe ? 0 : T * f), rr = f32(T),
+                 lse = f32(start_pos == 0 ? T * H : 0), xs = act(ql ? T * 7 * r : 0),
+                 wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
+    auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
+        if (!ql) return WB(off);
+        int64_t o = 0;
+        for (int j = j0; j <= j1; ++j) {
+            int64_t po, n;
+            proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, po, n);
+            dequant(ly, j, n, static_cast<char*>(wbuf.get()) + es * o, s);
+            o += n;
+        }
+        return wbuf.get();
+    };
+    hip::embed_fwd(ids, T, WB(emb_), V, d, xa.get(), dt, s);
+    void* x = xa.get();
+    void* xn = xb.get();
+    for (int64_t l = 0; l < L; ++l) {
+        const Layer& ly = layers_[l];
+        hip::rmsnorm_fwd(x, d, PB(ly.n1), h.get(), d, rr.as<float>(), T, d, eps, dt, s);
+        LowRank lq{};
+        if (ql) {
+            gemm(prof_, 0, 1, T, 3 * r, d, h.get(), d, W(ly.aqkv), d, xs.get(), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lq = LowRank{xs.get(), 3 * r, W(ly.bq), r, r, d, 0};
+        }
+        gemm(prof_, 0, 1, T, 3 * d, d, h.get(), d, wbase(ly, ly.wqkv, 0, 2), d, qkv.get(), 3 * d, dt, dt, s, nullptr,
+             0, 0.0f, 1.0f, ql ? &lq : nullptr);
+        hip::rope(qkv.get(), 3 * d, B, S, 2 * H, hd, start_pos, cos_dev_, sin_dev_, false, dt, s);
+        // the new keys and values join the cache at rows start_pos .. start_pos + S - 1
+        char* kc = static_cast<char*>(kv_cache_) + es * static_cast<size_t>(l * 2 * B * MS * d);
+        char* vc = kc + es * static_cast<size_t>(B * MS * d);
+        for (int64_t b = 0; b < B; ++b)
+            for (int kv = 0; kv < 2; ++kv)
+                AIC_HIP_CHECK(hipMemcpy2DAsync((kv ? vc : kc) + es * static_cast<size_t>((b * MS + start_pos) * d),
+                                               es * d, static_cast<char*>(qkv.get()) + es * ((b * S) * 3 * d + (1 + kv) * d),
+                                               es * 3 * d, es * d, S, hipMemcpyDeviceToDevice, s));
+        if (start_pos == 0)  // a fresh sequence: the flash kernel on the new rows is the same causal attention
+            hip::attn_fwd(qkv.get(), static_cast<char*>(qkv.get()) + es * d, static_cast<char*>(qkv.get()) + es * 2 * d,
+                          3 * d, ob.get(), d, lse.as<float>(), B, H, S, hd, true, scale, dt, s);
+        else
+            hip::attn_cached(qkv.get(), 3 * d, kc, vc, d, MS, ob.get(), d, B, H, S, start_pos, hd, scale, dt, s);
+        LowRank lo_{};
+        if (ql) {
+            gemm(prof_, 0, 1, T, r, d, ob.get(), d, W(ly.ao), d, xs.get(), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lo_ = LowRank{xs.get(), r, W(ly.bo), r, r, 0, 0};
+        }
+        gemm(prof_, 0, 1, T, d, d, ob.get(), d, wbase(ly, ly.wo, 3, 3), d, x1.get(), d, dt, dt, s, x, d, 0.0f, 1.0f,
+             ql ? &lo_ : nullptr);
+        hip::rmsnorm_fwd(x1.get(), d, PB(ly.n2), h.get(), d, rr.as<float>(), T, d, eps, dt, s);
+        if (moe) {
+            moe_[l]->forward(h.get(), T, W(ly.wr), W(ly.wex), x1.get(), xn, aux_dev_ + l, s);
+        } else {
+            LowRank lg{};
+            if (ql) {
+                gemm(prof_, 0, 1, T, 2 * r, d, h.get(), d, W(ly.agu), d, xs.get(), 2 * r, dt, dt, s, nullptr, 0, 0.0f,
+                     lsc);
+                lg = LowRank{xs.get(), 2 * r, W(ly.bg), r, r, f, 0};
+            }
+            gemm(prof_, 0, 1, T, 2 * f, d, h.get(), d, wbase(ly, ly.wgu, 4, 5), d, gu.get(), 2 * f, dt, dt, s,
+                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr);
+            hip::swiglu_fwd(gu.get(), at(gu, f), 2 * f, am.get(), f, T, f, dt, s);
+            LowRank ld_{};
+            if (ql) {
+                gemm(prof_, 0, 1, T, r, f, am.get(), f, W(ly.ad), f, xs.get(), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+                ld_ = LowRank{xs.get(), r, W(ly.bd), r, r, 0, 0};
+            }
+            gemm(prof_, 0, 1, T, d, f, am.get(), f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1.get(), d, 0.0f,
+                 1.0f, ql ? &ld_ : nullptr);
+        }
+        std::swap(x, xn);
+    }
+    hip::rmsnorm_fwd(x, d, PB(normf_), h.get(), d, rr.as<float>(), T, d, eps, dt, s);
+    gemm(prof_, 0, 1, T, V, d, h.get(), d, WB(head_), d, logits, V, dt, DType::Float32, s);
+}
+
+std::vector<int64_t> TransformerLM::generate(const std::vector<int64_t>& prompt, int64_t max_new_tokens,
+                                             float temperature, int top_k, float top_p, int64_t eos_token_id,
+                                             uint64_t seed) {
+    AIC_CHECK(max_new_tokens >= 0, InvalidArgument, "max_new_tokens must be non-negative");
+    const int64_t V = cfg_.vocab_size;
+    std::vector<int64_t> out = prompt.empty() ? std::vector<int64_t>{0} : prompt;
+    const int64_t n0 = static_cast<int64_t>(out.size());
+    AIC_CHECK(n0 + max_new_tokens <= cfg_.max_seq_len + 1, OutOfRange, "generate: ", n0, " + ", max_new_tokens,
+              " tokens exceed max_seq_len ", cfg_.max_seq_len);
+    for (int64_t t : out) AIC_CHECK(t >= 0 && t < V, OutOfRange, "generate: token ", t, " outside the vocabulary");
+    std::mt19937_64 rng(seed);
+    DeviceBuffer ids(sizeof(int64_t) * static_cast<size_t>(n0), stream_), logits(sizeof(float) * n0 * V, stream_);
+    AIC_HIP_CHECK(hipMemcpyAsync(ids.get(), out.data(), sizeof(int64_t) * n0, hipMemcpyHostToDevice, stream_));
+    forward_step(ids.as<int64_t>(), 1, n0, 0, logits.as<float>());  // the prompt in one prefill
+    std::vector<float> l(static_cast<size_t>(V));
+    AIC_HIP_CHECK(hipMemcpyAsync(l.data(), logits.as<float>() + (n0 - 1) * V, sizeof(float) * V, hipMemcpyDeviceToHost,
+                                 stream_));
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    for (int64_t step = 0; step < max_new_tokens; ++step) {
+        const int64_t next = sample_token(l, temperature, top_k, top_p, rng);
+        out.push_back(next);
+        if ((eos_token_id >= 0 && next == eos_token_id) || step + 1 == max_new_tokens) break;
+        AIC_HIP_CHECK(hipMemcpyAsync(ids.get(), &next, sizeof(int64_t), hipMemcpyHostToDevice, stream_));
+        forward_step(ids.as<int64_t>(), 1, 1, n0 + step, logits.as<float>());
+        AIC_HIP_CHECK(hipMemcpyAsync(l.data(), logits.get(), sizeof(float) * V, hipMemcpyDeviceToHost, stream_));
+        AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    }
+    return out;
 }
 
 void TransformerLM::train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S) {

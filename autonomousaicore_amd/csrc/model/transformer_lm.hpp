@@ -126,6 +126,18 @@ public:
     void save_checkpoint(const std::string& path, const CheckpointMeta& meta, bool with_optimizer);
     CheckpointMeta load_checkpoint(const std::string& path, bool* has_optimizer);
 
+    // KV-cached inference (TransformerLM::forward_step and generate,
+    // src/models/transformer_lm.cpp:64-233): ids are the device [B, S] int64 tokens at
+    // positions start_pos .. start_pos + S - 1, whose keys and values join the cache (one cache
+    // per layer, [B][max_seq_len][d] rows for K and for V, allocated on first use); logits
+    // receives their fp32 logits [B * S, V] (device).  A call with start_pos == 0 starts a new
+    // sequence (the whole prompt in one prefill).  generate() is the reference's loop for one
+    // sequence: prefill, then one token per step, sampled on the host from the fp32 logits with
+    // the reference's greedy / temperature / top-k / top-p rules and std::mt19937_64(seed).
+    void forward_step(const int64_t* ids, int64_t B, int64_t S, int64_t start_pos, float* logits);
+    std::vector<int64_t> generate(const std::vector<int64_t>& prompt, int64_t max_new_tokens, float temperature,
+                                  int top_k, float top_p, int64_t eos_token_id, uint64_t seed);
+
     // ids/targets: device pointers to [B, S] int64.
     void train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
     float eval_loss(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
@@ -184,6 +196,8 @@ private:
     uint8_t* q4_ = nullptr;      // QLoRA: INT4 projections
     void* q4s_ = nullptr;        //        and their fp16 scales
     std::vector<std::unique_ptr<MoEFFN>> moe_;
+    void* kv_cache_ = nullptr;  // [L][K, V][B][max_seq_len][d] in the compute dtype
+    int64_t kv_B_ = 0;
     Profiler prof_;
 };
 

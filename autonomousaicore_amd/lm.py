@@ -216,6 +216,27 @@ class TransformerLM:
         _lib.call("aic_lm_eval_loss", self._h, ip, tp, B, S, 1 if on_dev else 0, C.byref(loss))
         return float(loss.value)
 
+    def forward_step(self, ids, start_pos: int = 0) -> np.ndarray:
+        """TransformerLM::forward_step: ids [B, S] (host) at positions start_pos..; returns the fp32
+        logits [B, S, V] and appends the tokens' keys / values to the cache."""
+        ids = np.ascontiguousarray(ids, np.int64)
+        if ids.ndim == 1:
+            ids = ids[None]
+        B, S = ids.shape
+        out = np.empty((B, S, self.cfg.vocab_size), np.float32)
+        _lib.call("aic_lm_forward_step", self._h, ids.ctypes.data, B, S, start_pos, 0, out.ctypes.data)
+        return out
+
+    def generate(self, prompt, max_new_tokens: int, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
+                 eos_token_id: int = -1, seed: int = 42) -> list[int]:
+        """TransformerLM::generate (src/models/transformer_lm.cpp:89-233)."""
+        p = np.ascontiguousarray(prompt, np.int64)
+        out = np.empty(max(1, p.size) + max_new_tokens, np.int64)
+        n = C.c_int64()
+        _lib.call("aic_lm_generate", self._h, p.ctypes.data if p.size else None, p.size, max_new_tokens,
+                  temperature, top_k, top_p, eos_token_id, C.c_uint64(seed), out.ctypes.data, C.byref(n))
+        return [int(v) for v in out[:n.value]]
+
     def save_checkpoint(self, path: str, meta: "CheckpointMetadata | None" = None,
                         with_optimizer: bool = False) -> None:
         """save_checkpoint (src/train/checkpoint.cpp:30-95): the .aic file of every parameter;

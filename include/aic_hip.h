@@ -448,6 +448,22 @@ int aic_lm_train_step(aic_lm* lm, const int64_t* ids, const int64_t* targets, in
 /* Loss only (no gradient, no update); synchronous. */
 int aic_lm_eval_loss(aic_lm* lm, const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, int on_device,
                      float* loss);
+/* KV-cached inference.  forward_step: tokens ids [B, S] (device when on_device, else host) at
+ * positions start_pos .. start_pos + S - 1 go through the model, their keys and values join
+ * the per-layer cache, and their fp32 logits [B * S, V] are written to logits (device memory
+ * when on_device, else host; synchronous when host).  start_pos == 0 starts new sequences; a
+ * continuation keeps B.  generate: the reference's sampling loop for one sequence (greedy
+ * when temperature <= 0.001 or top_k == 1, else temperature / top-k / top-p and
+ * std::mt19937_64(seed)); out_tokens (host, capacity n_prompt + max_new_tokens, at least 1)
+ * receives the prompt (or {0} when it is empty) followed by the new tokens, *n_out their count;
+ * generation stops after eos_token_id when it is >= 0.
+ * Replaces: TransformerLM::forward_step and TransformerLM::generate
+ * (src/models/transformer_lm.cpp:64-233) with CausalSelfAttention::forward_with_cache
+ * (include/nn/attention.hpp:49-120). */
+int aic_lm_forward_step(aic_lm* lm, const int64_t* ids, int64_t B, int64_t S, int64_t start_pos, int on_device,
+                        float* logits);
+int aic_lm_generate(aic_lm* lm, const int64_t* prompt, int64_t n_prompt, int64_t max_new_tokens, float temperature,
+                    int top_k, float top_p, int64_t eos_token_id, uint64_t seed, int64_t* out_tokens, int64_t* n_out);
 /* The model's HIP stream and a full synchronisation of it. */
 int aic_lm_stream(const aic_lm* lm, aic_stream* stream);
 int aic_lm_synchronize(aic_lm* lm);

@@ -989,6 +989,22 @@ static int lm_step_core(const orc_lm_config* c, float* params, float* grads, con
     return 0;
 }
 
+/* TransformerLM::forward (src/models/transformer_lm.cpp:50-62): logits [B*S, V]. */
+int orc_lm_logits(const orc_lm_config* c, const float* params, const int64_t* ids, int64_t B, int64_t S,
+                  float* logits) {
+    if (S > c->max_seq_len) return -1;
+    lm_ptrs P = map_params(c, (float*)params);
+    int64_t hd = c->d_model / c->n_heads;
+    float* cos_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    float* sin_t = (float*)xcalloc((size_t)(S * hd / 2), sizeof(float));
+    orc_rope_tables(cos_t, sin_t, S, hd, c->rope_base);
+    float aux = 0.0f;
+    float* l = lm_forward(c, &P, ids, B, S, NULL, NULL, NULL, NULL, cos_t, sin_t, NULL, &aux, NULL);
+    memcpy(logits, l, sizeof(float) * (size_t)(B * S * c->vocab));
+    free(l); free(cos_t); free(sin_t); free(P.layers);
+    return 0;
+}
+
 int orc_lm_step(const orc_lm_config* c, float* params, float* grads, float* m, float* v, int64_t* step_count,
                 const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* o,
                 orc_scaler* scaler, orc_step_result* res) {

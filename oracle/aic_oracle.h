@@ -176,6 +176,9 @@ float orc_lm_loss(const orc_lm_config* cfg, const float* params, const int64_t* 
 /* One step: forward, cross_entropy(mean, ignore -100), backward, [scaler], clip, AdamW.
  * grads receives the gradients seen by the optimizer (unscaled, post-clip).
  * m/v/step_count: AdamW state; scaler may be NULL when opts->use_scaler == 0. */
+/* Forward only: logits [B*S, V] of TransformerLM::forward. */
+int orc_lm_logits(const orc_lm_config* cfg, const float* params, const int64_t* ids, int64_t B, int64_t S,
+                  float* logits);
 int orc_lm_step(const orc_lm_config* cfg, float* params, float* grads, float* m, float* v, int64_t* step_count,
                 const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, const orc_train_opts* opts,
                 orc_scaler* scaler, orc_step_result* res);

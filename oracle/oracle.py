@@ -298,6 +298,15 @@ def lm_loss(cfg, params, ids, targets, B, S):
                                    _i(np.ascontiguousarray(targets, np.int64)), C.c_int64(B), C.c_int64(S)))
 
 
+def lm_logits(cfg, params, ids, B, S):
+    out = np.empty((B * S, cfg.vocab), np.float32)
+    rc = lib().orc_lm_logits(C.byref(cfg), _f(np.ascontiguousarray(params, np.float32)),
+                             _i(np.ascontiguousarray(ids, np.int64)), C.c_int64(B), C.c_int64(S), _f(out))
+    if rc != 0:
+        raise RuntimeError(f"orc_lm_logits failed with {rc}")
+    return out.reshape(B, S, cfg.vocab)
+
+
 def lm_step(cfg, params, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1,
             max_grad_norm=1.0, m=None, v=None, step=0, scaler: LossScaler | None = None, do_update=True):
     """One training step in place on `params` (float32 flat).  Returns (result, grads, m, v, step)."""

@@ -809,3 +809,19 @@ def test_qlora_lm_step_vs_torch(orc, r, alpha, G):
         assert rel(grads[off:off + n], grads_t[off:off + n]) < 1e-4, name
         off += n
     assert rel(p, new_t) < 1e-4
+
+
+def test_lm_logits_match_the_step_loss(orc):
+    # the forward-only logits give the step's cross-entropy
+    vocab, d, L, H, f, B, S = 64, 32, 2, 2, 48, 2, 16
+    rng = np.random.default_rng(90)
+    lay = torch_ref.layout(vocab, d, L, f, False)
+    params = np.concatenate([(np.ones(s) if len(s) == 1 else rng.standard_normal(s) * 0.2).ravel()
+                             for _, s in lay]).astype(np.float32)
+    ids = rng.integers(0, vocab, B * S).astype(np.int64)
+    tgt = np.roll(ids, -1)
+    cfg = orc.make_config(vocab, d, L, H, f, S)
+    lg = orc.lm_logits(cfg, params, ids, B, S).reshape(B * S, vocab).astype(np.float64)
+    lse = np.log(np.exp(lg - lg.max(1, keepdims=True)).sum(1)) + lg.max(1)
+    ce = float(np.mean(lse - lg[np.arange(B * S), tgt]))
+    assert abs(ce - orc.lm_loss(cfg, params, ids, tgt, B, S)) < 1e-5 * ce
