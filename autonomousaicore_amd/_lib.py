@@ -28,6 +28,19 @@ class OptimCtl(C.Structure):
                 ("step", i32)]
 
 
+class StepRecord(C.Structure):
+    _fields_ = [("step", i64), ("loss", f32), ("aux_loss", f32), ("grad_norm", f32), ("loss_scale", f32),
+                ("found_inf", i32), ("pad", i32)]
+
+
+class TelemetrySnapshot(C.Structure):
+    _fields_ = [("step", i64), ("loss", f32), ("loss_ema_short", f32), ("loss_ema_long", f32),
+                ("loss_variance", f32), ("grad_norm", f32), ("grad_norm_ema", f32), ("lr", f32),
+                ("tokens_per_sec", f32), ("estimated_tflops", f32), ("host_total_bytes", C.c_uint64),
+                ("host_free_bytes", C.c_uint64), ("gpu_total_bytes", C.c_uint64), ("gpu_free_bytes", C.c_uint64),
+                ("anomaly", i32), ("pad", i32)]
+
+
 class LMConfig(C.Structure):
     _fields_ = [("vocab", i64), ("d_model", i64), ("n_layers", i64), ("n_heads", i64), ("d_ffn", i64),
                 ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32),
@@ -119,6 +132,20 @@ SIGNATURES = {
     "aic_lm_base_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
     "aic_lm_set_base_params": (i32, [vp, vp]),
     "aic_lm_set_params": (i32, [vp, vp]),
+    "aic_lm_step_history": (i32, [vp, C.POINTER(StepRecord), i32, C.POINTER(i32), i64p]),
+    "aic_lm_snapshot": (i32, [vp]),
+    "aic_lm_restore": (i32, [vp]),
+    "aic_telemetry_create": (i32, [i64, f32, f32, C.POINTER(vp)]),
+    "aic_telemetry_destroy": (i32, [vp]),
+    "aic_telemetry_record": (i32, [vp, i64, f32, f32, f32, f32, C.c_double, i64, i64, i32,
+                                   C.POINTER(TelemetrySnapshot)]),
+    "aic_telemetry_count": (i64, [vp]),
+    "aic_telemetry_is_nan_or_inf": (i32, [vp]),
+    "aic_telemetry_is_diverging": (i32, [vp, f32, i32]),
+    "aic_telemetry_is_gradient_exploding": (i32, [vp, f32]),
+    "aic_telemetry_is_gradient_vanishing": (i32, [vp, f32]),
+    "aic_telemetry_reset": (i32, [vp]),
+    "aic_telemetry_latest_json": (i32, [vp, C.c_char_p, i32]),
     "aic_lm_forward_step": (i32, [vp, vp, i64, i64, i64, i32, vp]),
     "aic_lm_generate": (i32, [vp, vp, i64, i64, f32, i32, f32, i64, C.c_uint64, vp, i64p]),
     "aic_lm_save_checkpoint": (i32, [vp, C.c_char_p, i64, i64, f32, C.c_char_p, i32]),

@@ -19,6 +19,7 @@
 #include "../model/transformer_lm.hpp"
 #include "../runtime/error.hpp"
 #include "../runtime/memory_pool.hpp"
+#include "../runtime/telemetry.hpp"
 
 namespace aic {
 
@@ -925,5 +926,98 @@ int aic_lm_generate(aic_lm* lm, const int64_t* prompt, int64_t n_prompt, int64_t
             lm->model->generate(p, max_new_tokens, temperature, top_k, top_p, eos_token_id, seed);
         std::copy(out.begin(), out.end(), out_tokens);
         *n_out = static_cast<int64_t>(out.size());
+    });
+}
+
+int aic_lm_step_history(aic_lm* lm, aic_step_record* out, int cap, int* n, int64_t* dropped) {
+    return guard([&] {
+        AIC_CHECK(lm && n && (out || cap == 0), InvalidArgument, "null argument");
+        *n = lm->model->step_history(out, cap, dropped);
+    });
+}
+
+int aic_lm_snapshot(aic_lm* lm) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        lm->model->snapshot();
+    });
+}
+
+int aic_lm_restore(aic_lm* lm) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        lm->model->restore();
+    });
+}
+
+struct aic_telemetry {
+    aic::TelemetryTracker t;
+};
+
+int aic_telemetry_create(int64_t window, float alpha_short, float alpha_long, aic_telemetry** out) {
+    return guard([&] {
+        AIC_CHECK(out && window > 0, InvalidArgument, "telemetry: bad arguments");
+        *out = new aic_telemetry{aic::TelemetryTracker(static_cast<size_t>(window), alpha_short, alpha_long)};
+    });
+}
+
+int aic_telemetry_destroy(aic_telemetry* t) {
+    return guard([&] { delete t; });
+}
+
+int aic_telemetry_record(aic_telemetry* t, int64_t step, float loss, float grad_norm, float lr, float tokens_per_sec,
+                         double step_seconds, int64_t total_tokens, int64_t model_params, int device_index,
+                         aic_telemetry_snapshot* out) {
+    return guard([&] {
+        AIC_CHECK(t, InvalidArgument, "null tracker");
+        const aic::TelemetrySnapshot s = t->t.record_step(step, loss, grad_norm, lr, tokens_per_sec, step_seconds,
+                                                          total_tokens, model_params, device_index);
+        if (out) {
+            out->step = s.step;
+            out->loss = s.loss;
+            out->loss_ema_short = s.loss_ema_short;
+            out->loss_ema_long = s.loss_ema_long;
+            out->loss_variance = s.loss_variance;
+            out->grad_norm = s.grad_norm;
+            out->grad_norm_ema = s.grad_norm_ema;
+            out->lr = s.lr;
+            out->tokens_per_sec = s.tokens_per_sec;
+            out->estimated_tflops = s.estimated_tflops;
+            out->host_total_bytes = s.memory.host_total;
+            out->host_free_bytes = s.memory.host_free;
+            out->gpu_total_bytes = s.memory.gpu_total;
+            out->gpu_free_bytes = s.memory.gpu_free;
+            out->anomaly = static_cast<int32_t>(s.anomaly);
+            out->pad = 0;
+        }
+    });
+}
+
+int64_t aic_telemetry_count(const aic_telemetry* t) { return t ? static_cast<int64_t>(t->t.count()) : -1; }
+int aic_telemetry_is_nan_or_inf(const aic_telemetry* t) { return t && t->t.is_nan_or_inf() ? 1 : 0; }
+int aic_telemetry_is_diverging(const aic_telemetry* t, float threshold_ratio, int min_consecutive) {
+    return t && t->t.is_diverging(threshold_ratio > 0.0f ? threshold_ratio : 1.4f,
+                                  min_consecutive > 0 ? min_consecutive : 3)
+               ? 1
+               : 0;
+}
+int aic_telemetry_is_gradient_exploding(const aic_telemetry* t, float spike_factor) {
+    return t && t->t.is_gradient_exploding(spike_factor > 0.0f ? spike_factor : 4.0f) ? 1 : 0;
+}
+int aic_telemetry_is_gradient_vanishing(const aic_telemetry* t, float min_norm) {
+    return t && t->t.is_gradient_vanishing(min_norm > 0.0f ? min_norm : 1e-7f) ? 1 : 0;
+}
+int aic_telemetry_reset(aic_telemetry* t) {
+    return guard([&] {
+        AIC_CHECK(t, InvalidArgument, "null tracker");
+        t->t.reset();
+    });
+}
+int aic_telemetry_latest_json(const aic_telemetry* t, char* buf, int cap) {
+    return guard([&] {
+        AIC_CHECK(t && buf && cap > 0, InvalidArgument, "null argument");
+        const std::string j = t->t.latest().to_json();
+        std::strncpy(buf, j.c_str(), static_cast<size_t>(cap) - 1);
+        buf[cap - 1] = '\0';
     });
 }

@@ -111,6 +111,10 @@ void adamw_multi(float* const* p, const float* const* g, float* const* m, float*
 void adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
                 float wd, float bc1, float bc2, hipStream_t s);
 void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s);
+// Appends {step, loss, aux, grad_norm, loss scale, found_inf} (an aic_step_record) to a device
+// ring of cap records; *count (device) counts all records ever appended.
+void step_record(const float* loss, const float* aux, const void* ctl, const float* scale_used, void* ring,
+                 int64_t* count, int cap, hipStream_t s);
 void fill_normal(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t s);
 void fill_const(float* dst, int64_t n, float v, hipStream_t s);
 

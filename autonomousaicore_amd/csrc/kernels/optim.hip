@@ -320,4 +320,30 @@ void fill_const(float* dst, int64_t n, float v, hipStream_t s) {
     AIC_LAUNCH_CHECK("fill_const");
 }
 
+namespace {
+// one thread: appends the step's statistics to the ring (slot = count % cap) and advances count
+__global__ void step_record_k(const float* loss, const float* aux, const aic_optim_ctl* ctl, const float* scale_used,
+                              aic_step_record* ring, int64_t* count, int cap) {
+    const int64_t i = *count;
+    aic_step_record r;
+    r.step = ctl->step;
+    r.loss = *loss;
+    r.aux_loss = aux ? *aux : 0.0f;
+    r.grad_norm = ctl->grad_norm;
+    r.loss_scale = *scale_used;
+    r.found_inf = ctl->skip;
+    r.pad = 0;
+    ring[i % cap] = r;
+    *count = i + 1;
+}
+}  // namespace
+
+void step_record(const float* loss, const float* aux, const void* ctl, const float* scale_used, void* ring,
+                 int64_t* count, int cap, hipStream_t s) {
+    AIC_CHECK(loss && ctl && scale_used && ring && count && cap > 0, InvalidArgument, "step_record: bad arguments");
+    hipLaunchKernelGGL(step_record_k, dim3(1), dim3(1), 0, s, loss, aux, static_cast<const aic_optim_ctl*>(ctl),
+                       scale_used, static_cast<aic_step_record*>(ring), count, cap);
+    AIC_LAUNCH_CHECK("step_record");
+}
+
 }  // namespace aic::hip

@@ -264,6 +264,9 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     AIC_HIP_CHECK(hipMemsetAsync(grads_dev_, 0, bytes, stream_));
     AIC_HIP_CHECK(hipMemsetAsync(m_dev_, 0, bytes, stream_));
     AIC_HIP_CHECK(hipMemsetAsync(v_dev_, 0, bytes, stream_));
+    AIC_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&hist_), sizeof(aic_step_record) * kHistory));
+    AIC_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&hist_count_), sizeof(int64_t)));
+    AIC_HIP_CHECK(hipMemsetAsync(hist_count_, 0, sizeof(int64_t), stream_));
     if (cfg.compute == DType::BFloat16) {
         AIC_HIP_CHECK(hipMalloc(&low_dev_, sizeof(uint16_t) * static_cast<size_t>(arena_)));
         AIC_HIP_CHECK(hipMemsetAsync(low_dev_, 0, sizeof(uint16_t) * static_cast<size_t>(arena_), stream_));
@@ -326,6 +329,8 @@ TransformerLM::~TransformerLM() {
     for (void* p : {static_cast<void*>(params_dev_), static_cast<void*>(grads_dev_), static_cast<void*>(m_dev_),
                     static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
                     static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
+        if (p) (void)hipFree(p);
+    for (void* p : {static_cast<void*>(hist_), static_cast<void*>(hist_count_), static_cast<void*>(backup_)})
         if (p) (void)hipFree(p);
     if (lora())
         for (void* p : {static_cast<void*>(base_dev_), base_low_, static_cast<void*>(q4_), q4s_})
@@ -910,6 +915,48 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         hip::adamw_multi(pp, gp, mp, vp, low_dev_ ? lp : nullptr, sizes, 1, a.lr, a.beta1, a.beta2, a.eps,
                          a.weight_decay, 0, &dev_->ctl, s);
     }
+    hip::step_record(&dev_->loss, moe ? &dev_->aux : nullptr, &dev_->ctl, &dev_->scale_used, hist_, hist_count_,
+                     kHistory, s);
+}
+
+int TransformerLM::step_history(aic_step_record* out, int cap, int64_t* dropped) {
+    if (dropped) *dropped = 0;
+    if (cap <= 0) return 0;
+    int64_t total = 0;
+    std::vector<aic_step_record> ring(kHistory);
+    AIC_HIP_CHECK(hipMemcpyAsync(&total, hist_count_, sizeof(int64_t), hipMemcpyDeviceToHost, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(ring.data(), hist_, sizeof(aic_step_record) * kHistory, hipMemcpyDeviceToHost,
+                                 stream_));
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    int64_t first = std::max(hist_read_, total - kHistory);
+    if (dropped) *dropped = first - hist_read_;
+    const int64_t n = std::min<int64_t>(total - first, cap);
+    for (int64_t i = 0; i < n; ++i) out[i] = ring[static_cast<size_t>((first + i) % kHistory)];
+    hist_read_ = first + n;
+    return static_cast<int>(n);
+}
+
+void TransformerLM::snapshot() {
+    const size_t a = sizeof(float) * static_cast<size_t>(arena_);
+    if (!backup_) AIC_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&backup_), 3 * a + sizeof(DevScalars)));
+    char* b = reinterpret_cast<char*>(backup_);
+    AIC_HIP_CHECK(hipMemcpyAsync(b, params_dev_, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(b + a, m_dev_, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(b + 2 * a, v_dev_, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(b + 3 * a, dev_, sizeof(DevScalars), hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void TransformerLM::restore() {
+    AIC_CHECK(backup_, InvalidState, "restore: no snapshot taken");
+    const size_t a = sizeof(float) * static_cast<size_t>(arena_);
+    const char* b = reinterpret_cast<const char*>(backup_);
+    AIC_HIP_CHECK(hipMemcpyAsync(params_dev_, b, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(m_dev_, b + a, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(v_dev_, b + 2 * a, a, hipMemcpyDeviceToDevice, stream_));
+    AIC_HIP_CHECK(hipMemcpyAsync(dev_, b + 3 * a, sizeof(DevScalars), hipMemcpyDeviceToDevice, stream_));
+    refresh_low_precision();
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64_t start_pos, float* logits) {

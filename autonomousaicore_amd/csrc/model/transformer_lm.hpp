@@ -138,6 +138,14 @@ public:
     std::vector<int64_t> generate(const std::vector<int64_t>& prompt, int64_t max_new_tokens, float temperature,
                                   int top_k, float top_p, int64_t eos_token_id, uint64_t seed);
 
+    // Telemetry hooks: the records of the steps since the previous call (one synchronisation),
+    // oldest first, at most cap; *dropped counts older records the ring overwrote.  snapshot()
+    // keeps a device copy of the trainable parameters, AdamW moments and optimiser state;
+    // restore() puts it back.
+    int step_history(aic_step_record* out, int cap, int64_t* dropped);
+    void snapshot();
+    void restore();
+
     // ids/targets: device pointers to [B, S] int64.
     void train_step(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
     float eval_loss(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S);
@@ -197,6 +205,11 @@ private:
     void* q4s_ = nullptr;        //        and their fp16 scales
     std::vector<std::unique_ptr<MoEFFN>> moe_;
     void* kv_cache_ = nullptr;  // [L][K, V][B][max_seq_len][d] in the compute dtype
+    static constexpr int kHistory = 1024;
+    aic_step_record* hist_ = nullptr;  // device ring of the last kHistory steps
+    int64_t* hist_count_ = nullptr;    // device: records ever written
+    int64_t hist_read_ = 0;            // host: records already returned
+    float* backup_ = nullptr;          // snapshot: params, m, v (3 arenas) then the device scalars
     int64_t kv_B_ = 0;
     Profiler prof_;
 };

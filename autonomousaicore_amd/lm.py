@@ -216,6 +216,24 @@ class TransformerLM:
         _lib.call("aic_lm_eval_loss", self._h, ip, tp, B, S, 1 if on_dev else 0, C.byref(loss))
         return float(loss.value)
 
+    def step_history(self, cap: int = 1024):
+        """Records of the steps run since the previous call (one synchronisation): a list of
+        StepMetrics, and the number of older records the device ring overwrote."""
+        arr = (_lib.StepRecord * cap)()
+        n, dropped = C.c_int(), C.c_int64()
+        _lib.call("aic_lm_step_history", self._h, arr, cap, C.byref(n), C.byref(dropped))
+        out = [StepMetrics(r.loss, r.grad_norm, bool(r.found_inf), r.loss_scale, int(r.step), r.aux_loss)
+               for r in arr[:n.value]]
+        return out, int(dropped.value)
+
+    def snapshot(self) -> None:
+        """Keep a device copy of the parameters, AdamW moments and optimiser state."""
+        _lib.call("aic_lm_snapshot", self._h)
+
+    def restore(self) -> None:
+        """Roll back to the last snapshot."""
+        _lib.call("aic_lm_restore", self._h)
+
     def forward_step(self, ids, start_pos: int = 0) -> np.ndarray:
         """TransformerLM::forward_step: ids [B, S] (host) at positions start_pos..; returns the fp32
         logits [B, S, V] and appends the tokens' keys / values to the cache."""

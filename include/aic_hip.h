@@ -412,6 +412,18 @@ typedef struct {
     float aux_loss;        /* MoE: total_aux_loss, included in loss (0 for a dense model) */
 } aic_step_stats;
 
+/* One training step's statistics as the device records them after the step (the step
+ * history ring holds the last 1024 steps). */
+typedef struct {
+    int64_t step;          /* AdamW step count after the step */
+    float loss;
+    float aux_loss;
+    float grad_norm;
+    float loss_scale;      /* scale used by the step */
+    int32_t found_inf;
+    int32_t pad;
+} aic_step_record;
+
 /* Creates the model on the current device; parameters are zero until set or initialised. */
 int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm** out);
 int aic_lm_destroy(aic_lm* lm);
@@ -464,6 +476,17 @@ int aic_lm_forward_step(aic_lm* lm, const int64_t* ids, int64_t B, int64_t S, in
                         float* logits);
 int aic_lm_generate(aic_lm* lm, const int64_t* prompt, int64_t n_prompt, int64_t max_new_tokens, float temperature,
                     int top_k, float top_p, int64_t eos_token_id, uint64_t seed, int64_t* out_tokens, int64_t* n_out);
+/* Telemetry hooks.  aic_lm_step_history copies (synchronising once) the records of the steps
+ * run since the previous call, oldest first, up to cap (*n = count; *dropped = older records
+ * the ring overwrote, nullable) -- so a training loop can feed a telemetry tracker without a
+ * host synchronisation per step.  aic_lm_snapshot keeps a device-memory copy of the
+ * trainable parameters, the AdamW moments and the optimiser / loss-scaler state;
+ * aic_lm_restore puts it back (a rollback in HBM, without a checkpoint file).
+ * No counterpart in the reference's step (its controller reloads checkpoint files,
+ * src/autonomous/controller.cpp:68-236). */
+int aic_lm_step_history(aic_lm* lm, aic_step_record* out, int cap, int* n, int64_t* dropped);
+int aic_lm_snapshot(aic_lm* lm);
+int aic_lm_restore(aic_lm* lm);
 /* The model's HIP stream and a full synchronisation of it. */
 int aic_lm_stream(const aic_lm* lm, aic_stream* stream);
 int aic_lm_synchronize(aic_lm* lm);
@@ -551,6 +574,39 @@ int aic_loader_reset(aic_token_loader* loader);
 int aic_loader_next_host(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch);
 int aic_loader_next_device(aic_token_loader* loader, int64_t* inputs, int64_t* targets, int64_t* actual_batch,
                            aic_stream stream);
+
+/* ---------------------------------------------------------------- telemetry --------- */
+/* TelemetryTracker (include/autonomous/telemetry.hpp, src/autonomous/telemetry.cpp:126-275):
+ * EMAs of the loss (alpha_short, alpha_long) and gradient norm, the population variance of the
+ * finite losses in the window, TFLOP/s = 6 P tokens/s, host (and, for device_index >= 0, GPU)
+ * memory, and the anomaly of the step: non-finite loss (1) or gradient (2); else divergence
+ * (3: loss above 1.4x the long EMA for 3 consecutive steps, from the third record), gradient
+ * explosion (4: above 4x the gradient EMA, from the fifth record), vanishing gradient (5: below
+ * 1e-7), GPU memory critical (6: under 8% free).  The is_* queries take the reference's
+ * default thresholds when their arguments are <= 0. */
+typedef struct aic_telemetry aic_telemetry;
+typedef struct {
+    int64_t step;
+    float loss, loss_ema_short, loss_ema_long, loss_variance, grad_norm, grad_norm_ema, lr, tokens_per_sec,
+        estimated_tflops;
+    uint64_t host_total_bytes, host_free_bytes, gpu_total_bytes, gpu_free_bytes;
+    int32_t anomaly;
+    int32_t pad;
+} aic_telemetry_snapshot;
+int aic_telemetry_create(int64_t window, float alpha_short, float alpha_long, aic_telemetry** out);
+int aic_telemetry_destroy(aic_telemetry* t);
+int aic_telemetry_record(aic_telemetry* t, int64_t step, float loss, float grad_norm, float lr, float tokens_per_sec,
+                         double step_seconds, int64_t total_tokens, int64_t model_params, int device_index,
+                         aic_telemetry_snapshot* out);
+int64_t aic_telemetry_count(const aic_telemetry* t);
+int aic_telemetry_is_nan_or_inf(const aic_telemetry* t);
+int aic_telemetry_is_diverging(const aic_telemetry* t, float threshold_ratio, int min_consecutive);
+int aic_telemetry_is_gradient_exploding(const aic_telemetry* t, float spike_factor);
+int aic_telemetry_is_gradient_vanishing(const aic_telemetry* t, float min_norm);
+int aic_telemetry_reset(aic_telemetry* t);
+/* The snapshot as one JSON object (the reference's TelemetrySnapshot::to_json fields plus the
+ * memory counters and the anomaly name); buf of cap bytes, NUL-terminated. */
+int aic_telemetry_latest_json(const aic_telemetry* t, char* buf, int cap);
 
 /* ---------------------------------------------------------------- synthetic data ---- */
 /* Host-side counter-based generators (splitmix64), shared by the tests and the bench.
