@@ -164,6 +164,8 @@ SIGNATURES = {
     "aic_lm_synchronize": (i32, [vp]),
     "aic_lm_last_stats": (i32, [vp, C.POINTER(StepStats)]),
     "aic_lm_profile": (i32, [vp, i32]),
+    "aic_lm_profile_classes": (i32, [vp, C.c_uint32]),
+    "aic_lm_profile_class_index": (i32, [C.c_char_p]),
     "aic_lm_profile_stats": (i32, [vp, C.POINTER(KernelStat), i32, C.POINTER(i32)]),
     "aic_dataset_open": (i32, [C.c_char_p, i64, i64, C.POINTER(vp)]),
     "aic_dataset_from_tokens": (i32, [vp, i64, i64, i64, C.POINTER(vp)]),

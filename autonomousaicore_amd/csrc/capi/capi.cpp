@@ -489,6 +489,15 @@ int aic_lm_profile(aic_lm* lm, int enable) {
     });
 }
 
+int aic_lm_profile_classes(aic_lm* lm, uint32_t class_mask) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        lm->model->set_profiling(class_mask != 0, class_mask);
+    });
+}
+
+int aic_lm_profile_class_index(const char* name) { return aic::Profiler::class_index(name); }
+
 int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n) {
     return guard([&] {
         AIC_CHECK(lm && n, InvalidArgument, "null argument");

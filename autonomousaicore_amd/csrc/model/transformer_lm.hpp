@@ -153,7 +153,10 @@ public:
     void synchronize();
 
     // Per-kernel-class HIP-event timing of the following steps (resets when enabled).
-    void set_profiling(bool on) { prof_.enable(on); }
+    void set_profiling(bool on, uint32_t class_mask = 0xffffffffu) {
+        prof_.set_mask(class_mask);
+        prof_.enable(on);
+    }
     std::vector<KernelClassStats> profile_stats() { return prof_.collect(); }
 
 private:

@@ -1,5 +1,7 @@
 #include "profiler.hpp"
 
+#include <cstring>
+
 #include "error.hpp"
 
 namespace aic {
@@ -12,6 +14,12 @@ const char* kNames[kNumKernelClasses] = {"gemm_fwd",   "gemm_dgrad", "gemm_wgrad
 const bool kMfma[kNumKernelClasses] = {true,  true,  true,  true,  true,  false, false, false,
                                        false, false, false, false, false, false, false, false};
 }  // namespace
+
+int Profiler::class_index(const char* name) {
+    for (int c = 0; c < kNumKernelClasses; ++c)
+        if (name && std::strcmp(name, kNames[c]) == 0) return c;
+    return -1;
+}
 
 Profiler::~Profiler() {
     for (hipEvent_t e : pool_) (void)hipEventDestroy(e);
@@ -40,7 +48,7 @@ hipEvent_t Profiler::take() {
 }
 
 Profiler::Scope::Scope(Profiler* p, int cls, double flops, double bytes, hipStream_t s)
-    : p_(p->on_ ? p : nullptr), s_(s), idx_(0) {
+    : p_(p->on_ && ((p->mask_ >> cls) & 1u) ? p : nullptr), s_(s), idx_(0) {
     if (!p_) return;
     Rec r{cls, flops, bytes, p_->take(), p_->take()};
     AIC_HIP_CHECK(hipEventRecord(r.a, s));

@@ -43,7 +43,12 @@ class Profiler {
 public:
     ~Profiler();
     void enable(bool on);
+    // Classes timed while enabled: bit c for class c (all by default).  Recording an event pair
+    // costs a few microseconds of queue time per launch, so a measurement that must not perturb
+    // the step times only the class it reports.
+    void set_mask(uint32_t mask) { mask_ = mask; }
     bool enabled() const { return on_; }
+    static int class_index(const char* name);
 
     class Scope {
     public:
@@ -70,6 +75,7 @@ private:
     };
     hipEvent_t take();
     bool on_ = false;
+    uint32_t mask_ = 0xffffffffu;
     std::vector<Rec> recs_;
     std::vector<hipEvent_t> pool_;
     size_t pool_used_ = 0;

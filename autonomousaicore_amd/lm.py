@@ -282,9 +282,19 @@ class TransformerLM:
         _lib.call("aic_lm_last_stats", self._h, C.byref(st))
         return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step), float(st.aux_loss))
 
-    def set_profiling(self, on: bool) -> None:
-        """Time every kernel launch of the following steps with HIP events (resets)."""
-        _lib.call("aic_lm_profile", self._h, 1 if on else 0)
+    def set_profiling(self, on: bool, classes=None) -> None:
+        """Time the kernel launches of the following steps with HIP events (resets); `classes`
+        (names) restricts the timing to those kernel classes."""
+        if classes is None:
+            _lib.call("aic_lm_profile", self._h, 1 if on else 0)
+            return
+        mask = 0
+        for name in classes:
+            c = _lib.load().aic_lm_profile_class_index(name.encode())
+            if c < 0:
+                raise ValueError(f"unknown kernel class {name}")
+            mask |= 1 << c
+        _lib.call("aic_lm_profile_classes", self._h, C.c_uint32(mask if on else 0))
 
     def profile_stats(self) -> list[dict]:
         """Per kernel class: launches, total_ms, algorithmic flops/bytes, mfma_bound."""

@@ -507,6 +507,11 @@ typedef struct {
     int mfma_bound;        /* 1: judge against the bf16 MFMA peak, 0: against HBM bandwidth */
 } aic_kernel_stat;
 int aic_lm_profile(aic_lm* lm, int enable);
+/* Profiling restricted to some classes (bit c = class c, as numbered by
+ * aic_lm_profile_class_index; 0 disables): each timed launch adds an event pair to the queue,
+ * so a step measurement times only the class it reports. */
+int aic_lm_profile_classes(aic_lm* lm, uint32_t class_mask);
+int aic_lm_profile_class_index(const char* name);
 /* Synchronises, then writes up to cap classes with at least one launch; *n = count. */
 int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n);
 
