@@ -322,6 +322,7 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
 TransformerLM::~TransformerLM() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     moe_.clear();  // their buffers are freed on stream_, so before it is destroyed
+    for (auto& b : ws_) b.reset();
     if (kv_cache_ && stream_) {
         (void)hipFreeAsync(kv_cache_, stream_);
         (void)hipStreamSynchronize(stream_);
@@ -622,6 +623,13 @@ void TransformerLM::init_normal(uint64_t seed, float std, bool residual_scaling)
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
+DeviceBuffer& TransformerLM::workspace(int slot, size_t bytes) {
+    AIC_CHECK(slot >= 0 && static_cast<size_t>(slot) < ws_.size(), InvalidState, "workspace slot ", slot);
+    DeviceBuffer& b = ws_[static_cast<size_t>(slot)];
+    if (b.bytes() < bytes) b = DeviceBuffer(bytes, stream_);  // the old one is freed in stream order
+    return b;
+}
+
 void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, bool backward,
                                      float* loss_out) {
     AIC_CHECK(B > 0 && S > 0, InvalidArgument, "batch and sequence must be positive");
@@ -636,23 +644,26 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     // causal attention: S(S+1)/2 (query, key) pairs per head, 2 products of 2*hd FLOPs each
     const double attn_flops = 2.0 * static_cast<double>(B * H) * static_cast<double>(S) * (S + 1) * hd;
 
-    auto act = [&](int64_t elems) { return DeviceBuffer(es * static_cast<size_t>(elems), s); };
-    auto f32 = [&](int64_t elems) { return DeviceBuffer(sizeof(float) * static_cast<size_t>(elems), s); };
+    int slot = 0;  // workspace slots in a fixed order
+    auto act = [&](int64_t elems) -> DeviceBuffer& { return workspace(slot++, es * static_cast<size_t>(elems)); };
+    auto f32 = [&](int64_t elems) -> DeviceBuffer& {
+        return workspace(slot++, sizeof(float) * static_cast<size_t>(elems));
+    };
 
     // ---- activations kept for the backward ----
-    DeviceBuffer xs = act((L + 1) * T * d);  // residual stream x_0 .. x_L
+    DeviceBuffer& xs = act((L + 1) * T * d);  // residual stream x_0 .. x_L
     const bool moe = cfg_.num_experts > 0;
-    DeviceBuffer h1 = act(L * T * d), qkv = act(L * T * 3 * d), ob = act(L * T * d), x1 = act(L * T * d),
-                 h2 = act(L * T * d), gu = act(moe ? 0 : L * T * 2 * f), am = act(moe ? 0 : L * T * f);
-    DeviceBuffer r1 = f32(L * T), r2 = f32(L * T), lse = f32(L * T * H);
-    DeviceBuffer hf = act(T * d), rf = f32(T), logits = act(T * V), lse_ce = f32(T);
+    DeviceBuffer &h1 = act(L * T * d), &qkv = act(L * T * 3 * d), &ob = act(L * T * d), &x1 = act(L * T * d),
+                 &h2 = act(L * T * d), &gu = act(moe ? 0 : L * T * 2 * f), &am = act(moe ? 0 : L * T * f);
+    DeviceBuffer &r1 = f32(L * T), &r2 = f32(L * T), &lse = f32(L * T * H);
+    DeviceBuffer &hf = act(T * d), &rf = f32(T), &logits = act(T * V), &lse_ce = f32(T);
     // QLoRA: each layer's adapter inputs x A^T (q/k/v stacked [T,3r], o [T,r], gate/up [T,2r],
     // down [T,r]) kept for the backward, and one dequantized projection (or stack) at a time
     const bool ql = lora();
     const int64_t r = cfg_.lora_rank;
     const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
-    DeviceBuffer xa_all = act(ql ? L * T * 7 * r : 0);
-    DeviceBuffer wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
+    DeviceBuffer& xa_all = act(ql ? L * T * 7 * r : 0);
+    DeviceBuffer& wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
         return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
     };
@@ -784,8 +795,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                     s);
     }
     void* dl = logits.get();
-    DeviceBuffer dx = act(T * d), dh = act(T * d), dqkv = act(T * 3 * d), dgu = act(moe ? 0 : T * 2 * f),
-                 da = act(moe ? 0 : T * f), dxa = act(ql ? T * 3 * r : 0);
+    DeviceBuffer &dx = act(T * d), &dh = act(T * d), &dqkv = act(T * 3 * d), &dgu = act(moe ? 0 : T * 2 * f),
+                 &da = act(moe ? 0 : T * f), &dxa = act(ql ? T * 3 * r : 0);
     // LoRA backward of one projection (LoRALinear, src/nn/lora.cpp:75-93, through autograd):
     // with y += xs B^T and xs = s (x A^T) kept from the forward,
     //   dB = dy^T xs, dxa = s dy B   (then dA = dxa^T x, and dx += dxa A in the base dgrad GEMM)
@@ -977,18 +988,21 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
         AIC_HIP_CHECK(hipMallocAsync(&kv_cache_, es * static_cast<size_t>(L * 2 * B * MS * d), s));
         kv_B_ = B;
     }
-    auto act = [&](int64_t elems) { return DeviceBuffer(es * static_cast<size_t>(elems), s); };
-    auto f32 = [&](int64_t elems) { return DeviceBuffer(sizeof(float) * static_cast<size_t>(elems), s); };
+    int slot = 40;  // the decode path's own workspace slots (its sizes differ from the step's)
+    auto act = [&](int64_t elems) -> DeviceBuffer& { return workspace(slot++, es * static_cast<size_t>(elems)); };
+    auto f32 = [&](int64_t elems) -> DeviceBuffer& {
+        return workspace(slot++, sizeof(float) * static_cast<size_t>(elems));
+    };
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
         return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
     };
     const bool moe = cfg_.num_experts > 0, ql = lora();
     const int64_t r = cfg_.lora_rank;
     const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
-    DeviceBuffer xa = act(T * d), xb = act(T * d), h = act(T * d), qkv = act(T * 3 * d), ob = act(T * d),
-                 x1 = act(T * d), gu = act(moe ? 0 : T * 2 * f), am = act(moe ? 0 : T * f), rr = f32(T),
-                 lse = f32(start_pos == 0 ? T * H : 0), xs = act(ql ? T * 7 * r : 0),
-                 wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
+    DeviceBuffer &xa = act(T * d), &xb = act(T * d), &h = act(T * d), &qkv = act(T * 3 * d), &ob = act(T * d),
+                 &x1 = act(T * d), &gu = act(moe ? 0 : T * 2 * f), &am = act(moe ? 0 : T * f), &rr = f32(T),
+                 &lse = f32(start_pos == 0 ? T * H : 0), &xs = act(ql ? T * 7 * r : 0),
+                 &wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
     auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
         if (!ql) return WB(off);
         int64_t o = 0;

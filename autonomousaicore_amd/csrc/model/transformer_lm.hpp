@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <cstdint>
 #include <memory>
 #include <string>
@@ -207,6 +208,12 @@ private:
     uint8_t* q4_ = nullptr;      // QLoRA: INT4 projections
     void* q4s_ = nullptr;        //        and their fp16 scales
     std::vector<std::unique_ptr<MoEFFN>> moe_;
+    // Step workspace: each buffer of the step (activations kept for the backward, gradients
+    // in flight) stays allocated between steps and only grows.  A stream-ordered allocation
+    // cannot reuse memory whose free is still queued behind the running step, so fresh
+    // per-step allocations would make the host wait for the previous step before enqueueing.
+    std::array<DeviceBuffer, 64> ws_;  // fixed size: references to slots stay valid
+    DeviceBuffer& workspace(int slot, size_t bytes);
     void* kv_cache_ = nullptr;  // [L][K, V][B][max_seq_len][d] in the compute dtype
     static constexpr int kHistory = 1024;
     aic_step_record* hist_ = nullptr;  // device ring of the last kHistory steps
