@@ -66,10 +66,11 @@ def test_gemm_epilogue_residual_alpha_beta():
 
 # Weight-gradient shapes of the 1B step (o_proj, gate/up) over the full K = 8192, partial
 # tiles with long K, each with residual / alpha / beta epilogues; runs must be bit-identical.
-# Few-tile shapes (the LoRA adapter products: dB, dA, x A^T, dy B) take the split-K path.
+# Few-tile shapes (the LoRA adapter products: dB, dA, x A^T, dy B; 32-127 tiles of 256x256 over a
+# long K) take the split-K paths; 136 tiles of 256x256 take the big-tile path.
 LONG_K_CASES = [(1, 0, 2048, 2048, 8192), (1, 0, 11264, 2048, 8192), (0, 1, 600, 520, 8192),
                 (0, 0, 1000, 1000, 4096), (1, 1, 264, 1032, 8192), (1, 0, 2048, 16, 8192), (1, 0, 48, 2048, 8192),
-                (0, 1, 8192, 48, 2048), (0, 0, 4096, 16, 5632)]
+                (0, 1, 8192, 48, 2048), (0, 0, 4096, 16, 5632), (0, 1, 2048, 4352, 512), (1, 0, 1024, 2048, 4096)]
 
 
 @pytest.mark.parametrize("ta,tb,M,N,K", LONG_K_CASES)
