@@ -41,6 +41,11 @@ class TelemetrySnapshot(C.Structure):
                 ("anomaly", i32), ("pad", i32)]
 
 
+class GemmDesc(C.Structure):
+    _fields_ = [("transA", i32), ("transB", i32), ("M", i64), ("N", i64), ("K", i64), ("A", vp), ("lda", i64),
+                ("B", vp), ("ldb", i64), ("C", vp), ("ldc", i64)]
+
+
 class LMConfig(C.Structure):
     _fields_ = [("vocab", i64), ("d_model", i64), ("n_layers", i64), ("n_heads", i64), ("d_ffn", i64),
                 ("max_seq_len", i64), ("norm_eps", f32), ("rope_base", f32), ("tied", i32), ("compute", i32),
@@ -73,6 +78,7 @@ SIGNATURES = {
     "aic_hip_mem_free_async": (i32, [vp, vp]),
     "aic_hip_mem_stats": (i32, [i64p, i64p]),
     "aic_hip_gemm": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp, i64, i32, i32, vp]),
+    "aic_hip_gemm_grouped": (i32, [i32, C.POINTER(GemmDesc), f32, f32, i32, i32, vp]),
     "aic_hip_gemm_lowrank": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32,
                                    f32, vp, i64, vp, i64, i32, i32, vp]),
     "aic_hip_rmsnorm_fwd": (i32, [vp, i64, vp, vp, i64, vp, i64, i64, f32, i32, vp]),

@@ -1030,3 +1030,33 @@ int aic_telemetry_latest_json(const aic_telemetry* t, char* buf, int cap) {
         buf[cap - 1] = '\0';
     });
 }
+
+int aic_hip_gemm_grouped(int n, const aic_gemm_desc* descs, float alpha, float beta, aic_dtype ab_type,
+                         aic_dtype c_type, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(n >= 0 && (descs || n == 0), InvalidArgument, "gemm_grouped: bad arguments");
+        std::vector<aic::hip::GemmArgs> v(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) {
+            const aic_gemm_desc& d = descs[i];
+            aic::hip::GemmArgs& a = v[static_cast<size_t>(i)];
+            a.transA = d.transA;
+            a.transB = d.transB;
+            a.M = d.M;
+            a.N = d.N;
+            a.K = d.K;
+            a.A = d.A;
+            a.lda = d.lda;
+            a.B = d.B;
+            a.ldb = d.ldb;
+            a.C = d.C;
+            a.ldc = d.ldc;
+            a.alpha = alpha;
+            a.beta = beta;
+            a.ab = dt(ab_type);
+            a.c = dt(c_type);
+            AIC_CHECK(a.A && a.B && a.C && a.M >= 0 && a.N >= 0 && a.K >= 0, InvalidArgument,
+                      "gemm_grouped: bad product ", i);
+        }
+        aic::hip::gemm_grouped(v.data(), n, st(stream));
+    });
+}

@@ -54,6 +54,25 @@ struct MfmaParams {
     int r2, seg_n, y2k;
 };
 
+// A grouped launch: up to kMaxGroups independent products of one kernel configuration, each
+// with its own operands and sizes, in one grid.  Group g owns the blocks [tile0, tile0 +
+// nblocks), nblocks its tile count rounded up to a multiple of 8 so that every group's block ids
+// keep the XCD mapping (block b runs on XCD b % 8).
+constexpr int kMaxGroups = 8;
+struct GroupDesc {
+    const bf16* A;
+    const bf16* B;
+    void* C;
+    int64_t lda, ldb, ldc;
+    int M, N, K;
+    int tile0, nblocks;
+};
+struct DmaParams {
+    MfmaParams p;
+    int ngroups;  // 0: the single product of p
+    GroupDesc g[kMaxGroups];
+};
+
 // Four consecutive elements of a C / R row, as floats.
 __device__ __forceinline__ void ld4(const float* p, float v[4]) {
     const float4 t = *reinterpret_cast<const float4*>(p);
@@ -73,10 +92,26 @@ __device__ __forceinline__ void st4(bf16* p, const float v[4]) {
 
 // Map the hardware block id to a tile so that consecutive tiles (same A row panel,
 // neighbouring B panels) land on the same XCD.
-__device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ int xcd_id(int bid, int nb) {
     const int q = nb / 8, r = nb % 8;
     const int xcd = bid % 8, local = bid / 8;
-    const int id = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+    return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+// Tile (tm, tn) of linear id (id < tiles_m * tiles_n): groups of 8 consecutive row tiles.
+__device__ __forceinline__ void id_to_tile(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int G = 8;
+    const int per_group = G * tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * G;
+    const int gsize = min(tiles_m - first_m, G);
+    const int inner = id % per_group;
+    tm = first_m + inner % gsize;
+    tn = inner / gsize;
+}
+
+__device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int id = xcd_id(bid, nb);
     constexpr int G = 8;
     const int per_group = G * tiles_n;
     const int group = id / per_group;
@@ -537,7 +572,7 @@ __device__ __forceinline__ void rank_tail(const MfmaParams& p, f32x16 (&acc)[FM]
 // MFMA pipe keeps working across it; right after it the freed stage receives tile kt+S and
 // the first fragments of tile kt+1 are read while the last step's MFMAs issue.
 template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
+__device__ __forceinline__ void dma_body(const MfmaParams& p, int m0, int n0) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int KS = BK / 16;
@@ -555,10 +590,6 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     static_assert((S - 2) * LPT < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) bf16 smem[];
 
-    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
-    int tm, tn;
-    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     // split-K: this block's K range (k-contiguous operands move along columns, the others
@@ -669,6 +700,39 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
     } else {
         gemm_epilogue<BM, BN, S * STAGE * 2, CT>(p, acc, smem, m0, n0);
     }
+}
+
+template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma(const MfmaParams p) {
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    dma_body<BM, BN, BK, S, TA, TB, CT>(p, tm * BM, tn * BN);
+}
+
+// Grouped launch: the block's group, then its tile within the group.
+template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma_grouped(const DmaParams dp) {
+    MfmaParams p = dp.p;
+    const int bid = static_cast<int>(blockIdx.x);
+    int g = 0;
+    while (g + 1 < dp.ngroups && bid >= dp.g[g + 1].tile0) ++g;
+    const GroupDesc& d = dp.g[g];
+    p.A = d.A;
+    p.B = d.B;
+    p.C = d.C;
+    p.lda = d.lda;
+    p.ldb = d.ldb;
+    p.ldc = d.ldc;
+    p.M = d.M;
+    p.N = d.N;
+    p.K = d.K;
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    const int id = xcd_id(bid - d.tile0, d.nblocks);
+    if (id >= tiles_m * tiles_n) return;  // a group's padding block (the whole block leaves)
+    int tm, tn;
+    id_to_tile(id, tiles_m, tiles_n, tm, tn);
+    dma_body<BM, BN, BK, S, TA, TB, CT>(p, tm * BM, tn * BN);
 }
 
 // C = alpha * sum_z P[z] + beta * C + R over the split-K partials P [splits][M][N] (fp32,
@@ -809,6 +873,58 @@ void launch_dma(const GemmArgs& a, hipStream_t s, int splits = 1, float* part = 
     }
     hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, BK, S, TA, TB, CT>), dim3(tiles, splits), dim3(256), lds, s, p);
     AIC_LAUNCH_CHECK("gemm_bf16_dma");
+}
+
+// One launch for several products of the same shape class (see DmaParams).
+template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
+void launch_dma_grouped(const GemmArgs* a, int n, hipStream_t s) {
+    DmaParams dp;
+    MfmaParams& p = dp.p;
+    p.A = static_cast<const bf16*>(a[0].A);
+    p.B = static_cast<const bf16*>(a[0].B);
+    p.C = a[0].C;
+    p.R = nullptr;
+    p.lda = a[0].lda; p.ldb = a[0].ldb; p.ldc = a[0].ldc; p.ldr = 0;
+    p.M = static_cast<int>(a[0].M); p.N = static_cast<int>(a[0].N); p.K = static_cast<int>(a[0].K);
+    p.alpha = a[0].alpha; p.beta = a[0].beta;
+    p.X2 = p.Y2 = nullptr;
+    p.ldx2 = p.ldy2 = p.cz = 0;
+    p.r2 = p.seg_n = p.y2k = 0;
+    p.vec = 1;
+    dp.ngroups = n;
+    int blocks = 0;
+    for (int i = 0; i < n; ++i) {
+        const int tiles = static_cast<int>(((a[i].M + BM - 1) / BM) * ((a[i].N + BN - 1) / BN));
+        GroupDesc& d = dp.g[i];
+        d.A = static_cast<const bf16*>(a[i].A);
+        d.B = static_cast<const bf16*>(a[i].B);
+        d.C = a[i].C;
+        d.lda = a[i].lda; d.ldb = a[i].ldb; d.ldc = a[i].ldc;
+        d.M = static_cast<int>(a[i].M); d.N = static_cast<int>(a[i].N); d.K = static_cast<int>(a[i].K);
+        d.tile0 = blocks;
+        d.nblocks = (tiles + 7) / 8 * 8;
+        blocks += d.nblocks;
+        p.vec = p.vec && a[i].ldc % 4 == 0 && aligned16(a[i].C);
+    }
+    for (int i = n; i < kMaxGroups; ++i) dp.g[i] = dp.g[0];
+    constexpr size_t lds = static_cast<size_t>(S) * (BM + BN) * BK * sizeof(uint16_t);
+    static bool configured = false;
+    if (!configured) {
+        AIC_HIP_CHECK(hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemm_bf16_dma_grouped<BM, BN, BK, S, TA, TB, CT>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        configured = true;
+    }
+    hipLaunchKernelGGL((gemm_bf16_dma_grouped<BM, BN, BK, S, TA, TB, CT>), dim3(blocks), dim3(256), lds, s, dp);
+    AIC_LAUNCH_CHECK("gemm_bf16_dma_grouped");
+}
+
+template <int BM, int BN, int BK, int S, typename CT>
+void dispatch_grouped(const GemmArgs* a, int n, hipStream_t s) {
+    if (!a[0].transA && a[0].transB) launch_dma_grouped<BM, BN, BK, S, false, true, CT>(a, n, s);
+    else if (!a[0].transA && !a[0].transB) launch_dma_grouped<BM, BN, BK, S, false, false, CT>(a, n, s);
+    else if (a[0].transA && !a[0].transB) launch_dma_grouped<BM, BN, BK, S, true, false, CT>(a, n, s);
+    else launch_dma_grouped<BM, BN, BK, S, true, true, CT>(a, n, s);
 }
 
 template <int BM, int BN, int BK, int S, typename CT>
@@ -994,6 +1110,31 @@ void gemm(const GemmArgs& a, hipStream_t s) {
     } else {
         if (a.c == DType::Float32) launch_simt<bf16, float>(a, s);
         else launch_simt<bf16, bf16>(a, s);
+    }
+}
+
+void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
+    AIC_CHECK(a && n >= 0, InvalidArgument, "gemm_grouped: bad arguments");
+    bool one_launch = n >= 2 && n <= kMaxGroups;
+    int64_t t256 = 0;
+    for (int i = 0; i < n && one_launch; ++i) {
+        const GemmArgs& x = a[i];
+        one_launch = gemm_dma_eligible(x) && x.transA == a[0].transA && x.transB == a[0].transB &&
+                     x.ab == a[0].ab && x.c == a[0].c && !x.R && x.r2 == 0 && x.alpha == a[0].alpha &&
+                     x.beta == a[0].beta && x.M > 0 && x.N > 0 && x.ldc >= x.N &&
+                     x.lda >= (x.transA ? x.M : x.K) && x.ldb >= (x.transB ? x.K : x.N);
+        t256 += ((x.M + 255) / 256) * ((x.N + 255) / 256);
+    }
+    if (!one_launch) {
+        for (int i = 0; i < n; ++i) gemm(a[i], s);
+        return;
+    }
+    if (a[0].c == DType::Float32) {
+        if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, float>(a, n, s);
+        else dispatch_grouped<128, 128, 64, 4, float>(a, n, s);
+    } else {
+        if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, bf16>(a, n, s);
+        else dispatch_grouped<128, 128, 64, 4, bf16>(a, n, s);
     }
 }
 

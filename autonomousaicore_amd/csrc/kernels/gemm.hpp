@@ -43,5 +43,9 @@ struct GemmArgs {
 bool gemm_mfma_eligible(const GemmArgs& a);
 bool gemm_dma_eligible(const GemmArgs& a);
 void gemm(const GemmArgs& a, hipStream_t stream);
+// Independent products in one launch when they share the kernel configuration (transposes,
+// dtypes, alpha, beta; no residual or low-rank term; up to 8), so that their tiles fill the
+// chip together instead of each product's last partial round; otherwise one gemm() each.
+void gemm_grouped(const GemmArgs* a, int n, hipStream_t stream);
 
 }  // namespace aic::hip

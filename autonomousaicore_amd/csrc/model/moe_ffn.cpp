@@ -1,5 +1,8 @@
 #include "moe_ffn.hpp"
 
+#include <algorithm>
+#include <vector>
+
 #include "../kernels/gemm.hpp"
 #include "../kernels/kernels.hpp"
 #include "../runtime/error.hpp"
@@ -26,6 +29,31 @@ void gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_
     a.ab = ab;
     a.c = c;
     hip::gemm(a, s);
+}
+
+hip::GemmArgs args(int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B,
+                   int64_t ldb, void* C, int64_t ldc, DType ab, DType c) {
+    hip::GemmArgs a;
+    a.transA = ta;
+    a.transB = tb;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.A = A;
+    a.lda = lda;
+    a.B = B;
+    a.ldb = ldb;
+    a.C = C;
+    a.ldc = ldc;
+    a.ab = ab;
+    a.c = c;
+    return a;
+}
+
+// The experts' products of one kind in launches of up to 8 (hip::gemm_grouped).
+void run_grouped(const std::vector<hip::GemmArgs>& v, hipStream_t s) {
+    for (size_t i = 0; i < v.size(); i += 8)
+        hip::gemm_grouped(v.data() + i, static_cast<int>(std::min<size_t>(8, v.size() - i)), s);
 }
 
 }  // namespace
@@ -75,18 +103,24 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
     hip::moe_gather(h, d_, src_ent_.as<int>(), k_, used, d_, xp_.get(), dt_, s);
     auto at = [&](const DeviceBuffer& b, int64_t elem) { return static_cast<char*>(b.get()) + es * elem; };
     const char* exb = static_cast<const char*>(experts);
+    // each expert's rows (a block of m rows starting at offsets_h_[e]) through its gate/up
+    // projection, all experts in shared launches; then SwiGLU; then the down projections
+    std::vector<hip::GemmArgs> v;
     for (int64_t e = 0; e < E_; ++e) {
         const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
         if (counts_h_[e] == 0) continue;
-        gemm(0, 1, m, f2, d_, at(xp_, o * d_), d_, exb + es * e * ex, d_, at(gu_, o * f2), f2, dt_, dt_, s);
+        v.push_back(args(0, 1, m, f2, d_, at(xp_, o * d_), d_, exb + es * e * ex, d_, at(gu_, o * f2), f2, dt_, dt_));
     }
+    run_grouped(v, s);
     hip::swiglu_fwd(gu_.get(), at(gu_, f_), f2, a_.get(), f_, used, f_, dt_, s);
+    v.clear();
     for (int64_t e = 0; e < E_; ++e) {
         const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
         if (counts_h_[e] == 0) continue;
-        gemm(0, 1, m, d_, f_, at(a_, o * f_), f_, exb + es * (e * ex + 2 * f_ * d_), f_, at(ye_, o * d_), d_, dt_, dt_,
-             s);
+        v.push_back(args(0, 1, m, d_, f_, at(a_, o * f_), f_, exb + es * (e * ex + 2 * f_ * d_), f_, at(ye_, o * d_),
+                         d_, dt_, dt_));
     }
+    run_grouped(v, s);
     hip::moe_combine(ye_.get(), idx_.as<int64_t>(), dst_row_.as<int>(), gsel_.as<float>(), T, k_, d_, R, d_, y, d_, dt_,
                      s);
 }
@@ -102,6 +136,8 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
     hip::moe_combine_bwd(dy, d_, ye_.get(), src_ent_.as<int>(), gsel_.as<float>(), used, k_, d_, dye.get(),
                          dgsel.as<float>(), dt_, s);
     const char* exb = static_cast<const char*>(ex_);
+    // down projections: da = dye . Wd and dWd = dye^T . a per expert, each kind in shared launches
+    std::vector<hip::GemmArgs> vd, vw;
     for (int64_t e = 0; e < E_; ++e) {
         const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
         float* dgu_w = dexperts + e * ex;
@@ -110,19 +146,25 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
             AIC_HIP_CHECK(hipMemsetAsync(dgu_w, 0, sizeof(float) * ex, s));
             continue;
         }
-        // down projection: da = dye . Wd, dWd = dye^T . a
-        gemm(0, 0, m, f_, d_, at(dye, o * d_), d_, exb + es * (e * ex + 2 * f_ * d_), f_, at(da, o * f_), f_, dt_, dt_,
-             s);
-        gemm(1, 0, d_, f_, m, at(dye, o * d_), d_, at(a_, o * f_), f_, dd_w, f_, dt_, DType::Float32, s);
+        vd.push_back(args(0, 0, m, f_, d_, at(dye, o * d_), d_, exb + es * (e * ex + 2 * f_ * d_), f_, at(da, o * f_),
+                          f_, dt_, dt_));
+        vw.push_back(args(1, 0, d_, f_, m, at(dye, o * d_), d_, at(a_, o * f_), f_, dd_w, f_, dt_, DType::Float32));
     }
+    run_grouped(vd, s);
+    run_grouped(vw, s);
     hip::swiglu_bwd(gu_.get(), at(gu_, f_), f2, da.get(), f_, dgu.get(), at(dgu, f_), f2, used, f_, dt_, s);
+    // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
+    vd.clear();
+    vw.clear();
     for (int64_t e = 0; e < E_; ++e) {
         const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
         if (counts_h_[e] == 0) continue;
-        // gate/up projections: dxp = dgu . Wgu, dWgu = dgu^T . xp
-        gemm(0, 0, m, d_, f2, at(dgu, o * f2), f2, exb + es * e * ex, d_, at(dxp, o * d_), d_, dt_, dt_, s);
-        gemm(1, 0, f2, d_, m, at(dgu, o * f2), f2, at(xp_, o * d_), d_, dexperts + e * ex, d_, dt_, DType::Float32, s);
+        vd.push_back(args(0, 0, m, d_, f2, at(dgu, o * f2), f2, exb + es * e * ex, d_, at(dxp, o * d_), d_, dt_, dt_));
+        vw.push_back(args(1, 0, f2, d_, m, at(dgu, o * f2), f2, at(xp_, o * d_), d_, dexperts + e * ex, d_, dt_,
+                          DType::Float32));
     }
+    run_grouped(vd, s);
+    run_grouped(vw, s);
     hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
     // router: dlogits from the gates and the aux loss, then both router products
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,

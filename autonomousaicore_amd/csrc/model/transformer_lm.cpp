@@ -1,6 +1,8 @@
 #include "transformer_lm.hpp"
 
 #include <algorithm>
+#include <array>
+#include <initializer_list>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -77,6 +79,36 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.y2_kmajor = lr->y2_kmajor;
     }
     hip::gemm(a, s);
+}
+
+// Weight gradients dW_i = A_i^T B_i (fp32 out) of independent products in one launch.
+void wgrad_grouped(Profiler& prof, std::initializer_list<std::array<const void*, 3>> ops,
+                   std::initializer_list<std::array<int64_t, 3>> mnk, DType ab, hipStream_t s) {
+    std::vector<hip::GemmArgs> v;
+    double flops = 0.0, bytes = 0.0;
+    auto op = ops.begin();
+    for (const auto& d : mnk) {
+        hip::GemmArgs a;
+        a.transA = 1;
+        a.transB = 0;
+        a.M = d[0];
+        a.N = d[1];
+        a.K = d[2];
+        a.A = (*op)[0];
+        a.lda = d[0];
+        a.B = (*op)[1];
+        a.ldb = d[1];
+        a.C = const_cast<void*>((*op)[2]);
+        a.ldc = d[1];
+        a.ab = ab;
+        a.c = DType::Float32;
+        v.push_back(a);
+        flops += 2.0 * d[0] * d[1] * d[2];
+        bytes += static_cast<double>(dtype_size(ab)) * (d[0] * d[2] + d[1] * d[2]) + 4.0 * d[0] * d[1];
+        ++op;
+    }
+    auto scope = prof.scope(kGemmWgrad, flops, bytes, s);
+    hip::gemm_grouped(v.data(), static_cast<int>(v.size()), s);
 }
 
 }  // namespace
@@ -867,9 +899,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             lora_b_bwd(dx.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
             gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
             lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
-        } else {
-            gemm(prof_, 1, 0, d, d, T, dx.get(), d, ol, d, G(ly.wo), d, dt, DType::Float32, s);
-        }
+        }  // else: the out_proj weight gradient joins the q/k/v one below (dx is unchanged until then)
         gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lo_ : nullptr);
         {
@@ -893,7 +923,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 1, 0, 3 * r, d, T, dxa.get(), 3 * r, h1l, d, G(ly.aqkv), d, dt, DType::Float32, s);
             lq = LowRank{dxa.get(), 3 * r, W(ly.aqkv), d, 3 * r, 0, 1};
         } else {
-            gemm(prof_, 1, 0, 3 * d, d, T, dqkv.get(), 3 * d, h1l, d, G(ly.wqkv), d, dt, DType::Float32, s);
+            // dWqkv = dqkv^T h1 and dWo = dx^T o in one launch (192 + 64 tiles of 256x256 at the 1B
+            // shape: one round of the chip instead of two partial ones)
+            wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dx.get(), ol, G(ly.wo)}},
+                          {{3 * d, d, T}, {d, d, T}}, dt, s);
         }
         gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
              0, 0.0f, 1.0f, ql ? &lq : nullptr);

@@ -85,6 +85,25 @@ int aic_hip_gemm_lowrank(int transA, int transB, int64_t M, int64_t N, int64_t K
                          int64_t ldy2, int64_t r2, int64_t seg_n, int y2_kmajor, float beta, void* C, int64_t ldc,
                          const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type, aic_stream stream);
 
+/* Several independent products in one launch (for example every expert's projection of an MoE
+ * layer, or two weight gradients whose tiles together fill the chip once).  They must share
+ * transA, transB, the dtypes, alpha and beta, and take the MFMA path (bf16, 16-byte aligned
+ * operands, K % 64 == 0, at most 8 products); otherwise each runs as aic_hip_gemm.
+ * Replaces: the per-expert matmul loop of MoELayer::forward / backward
+ * (src/nn/moe.cpp:205-245), one launch per expert there. */
+typedef struct {
+    int transA, transB;
+    int64_t M, N, K;
+    const void* A;
+    int64_t lda;
+    const void* B;
+    int64_t ldb;
+    void* C;
+    int64_t ldc;
+} aic_gemm_desc;
+int aic_hip_gemm_grouped(int n, const aic_gemm_desc* descs, float alpha, float beta, aic_dtype ab_type,
+                         aic_dtype c_type, aic_stream stream);
+
 /* ---------------------------------------------------------------- RMSNorm ---------- */
 /* y = x / rms * w with rms = sqrt(mean(x^2) + eps) per row; rms[rows] (fp32) is saved.
  * x/y have dtype dt (F32 or BF16), leading dimensions ldx/ldy; w is fp32 [dim].

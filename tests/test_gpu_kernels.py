@@ -461,3 +461,35 @@ def test_optim_finalize_scaler_and_clip_semantics(orc):
     # below the threshold only the unscale remains
     c = _finalize(_ctl(scale=scale, max_grad_norm=100.0), 91.0 * scale * scale, 0)
     assert c.grad_mult == 1.0 / scale
+
+
+# (ta, tb, [(M, N, K), ...]): MoE experts of different row counts, the q/k/v + out_proj weight
+# gradients together, a 128x128-tile group, and a mixed set that falls back to single launches
+GROUPED_CASES = [(0, 1, [(192, 704, 256), (64, 704, 256), (448, 704, 256), (128, 704, 256)]),
+                 (1, 0, [(768, 256, 1024), (256, 256, 1024)]),
+                 (0, 0, [(64, 256, 128), (128, 128, 256), (256, 192, 64)]),
+                 (1, 0, [(1536, 512, 2048), (512, 512, 2048)]),
+                 (1, 0, [(4096, 2048, 512), (2048, 2048, 512)])]
+
+
+@pytest.mark.parametrize("ta,tb,shapes", GROUPED_CASES)
+def test_gemm_grouped(ta, tb, shapes):
+    rng = np.random.default_rng(len(shapes) + ta)
+    descs, refs, outs, keep = [], [], [], []
+    for M, N, K in shapes:
+        A = bf16_round(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+        B = bf16_round(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+        Ad, Bd = dev(A, torch.bfloat16), dev(B, torch.bfloat16)
+        Cd = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+        keep += [Ad, Bd]
+        outs.append(Cd)
+        refs.append(_ref_gemm(ta, tb, A, B))
+        descs.append(_lib.GemmDesc(ta, tb, M, N, K, ptr(Ad), A.shape[1], ptr(Bd), B.shape[1], ptr(Cd), N))
+    arr = (_lib.GemmDesc * len(descs))(*descs)
+    call("aic_hip_gemm_grouped", len(descs), arr, 0.5, 0.0, BF16, F32, stream())
+    first = [host(c).copy() for c in outs]
+    for c, r in zip(first, refs):
+        assert rel(c, 0.5 * r) < 1e-5
+    call("aic_hip_gemm_grouped", len(descs), arr, 0.5, 0.0, BF16, F32, stream())
+    for c, f in zip(outs, first):
+        np.testing.assert_array_equal(host(c), f)
