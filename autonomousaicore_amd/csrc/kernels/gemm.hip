@@ -664,7 +664,10 @@ __device__ __forceinline__ void dma_body(const MfmaParams& p, int m0, int n0) {
     __builtin_amdgcn_s_barrier();
     bf16x8 fa[2][FM], fb[2][FN];
     read(0, 0, fa[0], fb[0]);
-    for (int kt = 0; kt < nk; ++kt) {
+    // One K tile.  MC: tile kt+S exists (its copy goes into the freed stage); MT: tile kt+1
+    // exists.  Both are compile-time, so the interleaved last k step has no branches.
+    auto tile_step = [&](int kt, auto mc, auto mt) {
+        constexpr bool MC = decltype(mc)::value, MT = decltype(mt)::value;
         const int cur = kt % S;
 #pragma unroll
         for (int ks = 0; ks + 1 < KS; ++ks) {
@@ -673,24 +676,34 @@ __device__ __forceinline__ void dma_body(const MfmaParams& p, int m0, int n0) {
             interleave();
         }
         wait_lds();  // this wave's reads of stage `cur` are complete
-        if (kt + 1 < nk) wait_tiles<LPT>(min(S - 2, nk - 1 - (kt + 1)));  // tile kt+1 has landed
+        // tile kt+1 has landed: at most min(S - 2, tiles after kt+1) later tiles in flight
+        if constexpr (MC) wait_tiles<LPT>(S - 2);
+        else if constexpr (MT) wait_tiles<LPT>(min(S - 2, nk - 1 - (kt + 1)));
         __builtin_amdgcn_s_barrier();
         // Last k step: its MFMAs, the copy of tile kt+S into the freed stage and the first
         // fragment reads of tile kt+1 go out interleaved one by one, so the copy issue never
         // holds back the MFMA pipe.
         const int nxt = (kt + 1) % S;
-        const bool more_copies = kt + S < nk, more_tiles = kt + 1 < nk;
 #pragma unroll
         for (int q = 0; q < NMF; ++q) {
             acc[q / FN][q % FN] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][q % FN], fa[1][q / FN], acc[q / FN][q % FN], 0, 0, 0);
-            if (more_copies) {
+            if constexpr (MC) {
 #pragma unroll
                 for (int c = q * LPT / NMF; c < (q + 1) * LPT / NMF; ++c) copy_one(kt + S, cur, c);
             }
-            if (q < FM + FN && more_tiles) read_one(nxt, 0, q, fa[0], fb[0]);
+            if constexpr (MT) {
+                if (q < FM + FN) read_one(nxt, 0, q, fa[0], fb[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the copies spread over the MFMAs
         }
-    }
+    };
+    using T1 = std::true_type;
+    using F0 = std::false_type;
+    int kt = 0;
+    for (; kt + S < nk; ++kt) tile_step(kt, T1{}, T1{});
+    for (; kt + 1 < nk; ++kt) tile_step(kt, F0{}, T1{});
+    if (kt < nk) tile_step(kt, F0{}, F0{});
 
     if (p.r2 > 0) rank_tail<FM, FN, WM, WN>(p, acc, m0, n0, wm, wn);
     if (blockIdx.y > 0) {

@@ -166,6 +166,8 @@ def main():
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    if args.warmup < 1 or args.steps < 1:
+        ap.error("--warmup and --steps must be at least 1 (the last warm-up step names the dominant class)")
 
     import torch
 
@@ -221,9 +223,12 @@ def main():
                                      unit="GB/s", frac=round(ach / PEAK_HBM_GBS, 4))
         return kc
 
-    # warm-up, every class timed with HIP events: names the dominant class (the most GPU time)
+    # warm-up; its last step has every class timed with HIP events and names the dominant class
+    # (the most GPU time).  The first step also allocates the step's workspace, which would be
+    # charged to whichever class's events bracket the allocation, so it is not the one timed.
+    run(max(args.warmup - 1, 0))
     model.set_profiling(True)
-    run(args.warmup)
+    run(1)
     warm = model.profile_stats()
     model.set_profiling(False)
     dom_name = max(warm, key=lambda k: k["total_ms"])["name"]
