@@ -48,4 +48,23 @@ void gemm(const GemmArgs& a, hipStream_t stream);
 // chip together instead of each product's last partial round; otherwise one gemm() each.
 void gemm_grouped(const GemmArgs* a, int n, hipStream_t stream);
 
+// The products of E experts over row-ragged operands, one launch, with the row ranges read on
+// the device (no host round trip to size them).  Expert e owns the rows [offsets[e],
+// offsets[e+1]) of the row-ragged operands (offsets: E + 1 device int64 values, each a
+// multiple of 64, non-decreasing).  `g` describes expert 0's product at row offset 0:
+//   ragged M (ragged_k = 0; g.transA = 0): rows of A and C are ragged, g.M is a bound on
+//     offsets[E]; expert e uses B + e * b_stride;
+//   ragged K (ragged_k = 1; g.transA = 1, g.transB = 0): the K rows of A and B are ragged;
+//     expert e writes C + e * c_stride (all zeros when it owns no rows).
+// bf16 operands, no residual, no low-rank term; g.K (ragged M) a multiple of 64.
+struct RaggedArgs {
+    GemmArgs g;
+    const int64_t* offsets = nullptr;
+    int E = 0;
+    int ragged_k = 0;
+    int64_t b_stride = 0, c_stride = 0;
+};
+bool gemm_ragged_eligible(const RaggedArgs& r);
+void gemm_ragged(const RaggedArgs& r, hipStream_t stream);
+
 }  // namespace aic::hip

@@ -1,0 +1,4 @@
+// GEMM kernels for the operand layout op(A) = A^T, op(B) = B^T (true, true), bf16 output.
+#include "gemm_kernels.inc"
+
+AIC_GEMM_LAUNCHES_CT(true, true, aic::hip::bf16)

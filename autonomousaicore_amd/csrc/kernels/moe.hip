@@ -148,8 +148,9 @@ __device__ __forceinline__ long long align_rows(long long n) { return (n + kRowA
 // row block that starts at offsets[e] (a multiple of 64; the block is padded to 64 rows).
 // dst_row[t * k + j] = row of that entry; src_ent[row] = t * k + j, or -1 for a padding row.
 __global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict__ idx, const int64_t* __restrict__ counts,
-                                                      int T, int k, int E, int64_t* __restrict__ offsets,
-                                                      int* __restrict__ dst_row, int* __restrict__ src_ent) {
+                                                      int T, int k, int E, int max_rows,
+                                                      int64_t* __restrict__ offsets, int* __restrict__ dst_row,
+                                                      int* __restrict__ src_ent) {
     const int e = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __shared__ int wsum[16];
@@ -193,7 +194,9 @@ __global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict_
         }
         __syncthreads();
     }
-    const int end = start_s + static_cast<int>(align_rows(base_s - start_s));
+    // padding rows of this expert's block; the last expert also marks the rows after all
+    // blocks (up to max_rows) as padding, so that every row of src_ent is defined
+    const int end = e == E - 1 ? max_rows : start_s + static_cast<int>(align_rows(base_s - start_s));
     for (int r = base_s + static_cast<int>(threadIdx.x); r < end; r += 1024) src_ent[r] = -1;
 }
 
@@ -366,8 +369,10 @@ void moe_permute(const int64_t* idx, const int64_t* counts, int64_t T, int64_t k
                  int* dst_row, int* src_ent, hipStream_t s) {
     check_moe(T, E, k);
     AIC_CHECK(idx && counts && offsets && dst_row && src_ent, InvalidArgument, "moe_permute: null argument");
+    AIC_CHECK(moe_max_rows(T, E, k) < (int64_t{1} << 31), InvalidArgument, "moe_permute: too many rows");
     hipLaunchKernelGGL(moe_permute_k, dim3(static_cast<unsigned>(E)), dim3(1024), 0, s, idx, counts,
-                       static_cast<int>(T), static_cast<int>(k), static_cast<int>(E), offsets, dst_row, src_ent);
+                       static_cast<int>(T), static_cast<int>(k), static_cast<int>(E),
+                       static_cast<int>(moe_max_rows(T, E, k)), offsets, dst_row, src_ent);
     AIC_LAUNCH_CHECK("moe_permute");
 }
 

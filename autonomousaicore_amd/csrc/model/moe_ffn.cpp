@@ -65,15 +65,74 @@ MoEFFN::MoEFFN(int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, DType
     AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "MoEFFN: dtype must be f32 or bf16");
 }
 
-void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* experts, const void* R, void* y,
+void MoEFFN::host_offsets(hipStream_t s) {
+    if (host_valid_) return;
+    counts_h_.assign(E_, 0);
+    offsets_h_.assign(E_ + 1, 0);
+    AIC_HIP_CHECK(hipMemcpyAsync(counts_h_.data(), counts_.get(), sizeof(int64_t) * E_, hipMemcpyDeviceToHost, s));
+    AIC_HIP_CHECK(hipMemcpyAsync(offsets_h_.data(), offsets_.get(), sizeof(int64_t) * (E_ + 1),
+                                 hipMemcpyDeviceToHost, s));
+    AIC_HIP_CHECK(hipStreamSynchronize(s));
+    host_valid_ = true;
+}
+
+const std::vector<int64_t>& MoEFFN::counts_host() {
+    host_offsets(nullptr);
+    return counts_h_;
+}
+
+// One kind of expert product: g is expert 0's product at row offset 0 (M or K: the rows).
+// Ragged launch with the device offsets when the layout allows it, else one product per
+// expert from the host offsets.
+void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s) {
+    hip::RaggedArgs r;
+    r.g = g;
+    r.offsets = offsets_.as<int64_t>();
+    r.E = static_cast<int>(E_);
+    r.ragged_k = ragged_k;
+    r.b_stride = b_stride;
+    r.c_stride = c_stride;
+    if (hip::gemm_ragged_eligible(r)) {
+        hip::gemm_ragged(r, s);
+        return;
+    }
+    host_offsets(s);
+    const size_t es = dtype_size(dt_), ec = dtype_size(g.c);
+    std::vector<hip::GemmArgs> v;
+    for (int64_t e = 0; e < E_; ++e) {
+        const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
+        hip::GemmArgs a = g;
+        if (ragged_k) {
+            if (m == 0) {  // no rows: a zero gradient
+                AIC_HIP_CHECK(hipMemsetAsync(static_cast<char*>(g.C) + ec * e * c_stride, 0,
+                                             ec * static_cast<size_t>(g.M * g.ldc), s));
+                continue;
+            }
+            a.K = m;
+            a.A = static_cast<const char*>(g.A) + es * o * g.lda;
+            a.B = static_cast<const char*>(g.B) + es * o * g.ldb;
+            a.C = static_cast<char*>(g.C) + ec * e * c_stride;
+        } else {
+            if (m == 0) continue;
+            a.M = m;
+            a.A = static_cast<const char*>(g.A) + es * o * g.lda;
+            a.B = static_cast<const char*>(g.B) + es * e * b_stride;
+            a.C = static_cast<char*>(g.C) + ec * o * g.ldc;
+        }
+        v.push_back(a);
+    }
+    run_grouped(v, s);
+}
+
+void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* experts_w, const void* R, void* y,
                      float* aux, hipStream_t s) {
-    AIC_CHECK(h && wr && experts && y && aux && T > 0, InvalidArgument, "MoEFFN::forward: bad arguments");
+    AIC_CHECK(h && wr && experts_w && y && aux && T > 0, InvalidArgument, "MoEFFN::forward: bad arguments");
     const size_t es = dtype_size(dt_);
     const int64_t rows = hip::moe_max_rows(T, E_, k_), f2 = 2 * f_, ex = 3 * f_ * d_;
     T_ = T;
     h_ = h;
     wr_ = wr;
-    ex_ = experts;
+    ex_ = experts_w;
     logits_ = DeviceBuffer(sizeof(float) * T * E_, s);
     idx_ = DeviceBuffer(sizeof(int64_t) * T * k_, s);
     gsel_ = DeviceBuffer(sizeof(float) * T * k_, s);
@@ -82,45 +141,32 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
     offsets_ = DeviceBuffer(sizeof(int64_t) * (E_ + 1), s);
     dst_row_ = DeviceBuffer(sizeof(int) * T * k_, s);
     src_ent_ = DeviceBuffer(sizeof(int) * rows, s);
+    host_valid_ = false;
     // router logits in fp32, routing, dispatch order
     gemm(0, 1, T, E_, d_, h, d_, wr, d_, logits_.get(), E_, dt_, DType::Float32, s);
     hip::moe_route(logits_.as<float>(), T, E_, k_, coef_, idx_.as<int64_t>(), gsel_.as<float>(), probs_.as<float>(),
                    nullptr, counts_.as<int64_t>(), nullptr, aux, s);
     hip::moe_permute(idx_.as<int64_t>(), counts_.as<int64_t>(), T, k_, E_, offsets_.as<int64_t>(), dst_row_.as<int>(),
                      src_ent_.as<int>(), s);
-    // expert row counts on the host: they size the per-expert GEMMs
-    counts_h_.assign(E_, 0);
-    offsets_h_.assign(E_ + 1, 0);
-    AIC_HIP_CHECK(hipMemcpyAsync(counts_h_.data(), counts_.get(), sizeof(int64_t) * E_, hipMemcpyDeviceToHost, s));
-    AIC_HIP_CHECK(hipMemcpyAsync(offsets_h_.data(), offsets_.get(), sizeof(int64_t) * (E_ + 1),
-                                 hipMemcpyDeviceToHost, s));
-    AIC_HIP_CHECK(hipStreamSynchronize(s));
-    const int64_t used = offsets_h_[E_];
-    xp_ = DeviceBuffer(es * used * d_, s);
-    gu_ = DeviceBuffer(es * used * f2, s);
-    a_ = DeviceBuffer(es * used * f_, s);
-    ye_ = DeviceBuffer(es * used * d_, s);
-    hip::moe_gather(h, d_, src_ent_.as<int>(), k_, used, d_, xp_.get(), dt_, s);
-    auto at = [&](const DeviceBuffer& b, int64_t elem) { return static_cast<char*>(b.get()) + es * elem; };
-    const char* exb = static_cast<const char*>(experts);
-    // each expert's rows (a block of m rows starting at offsets_h_[e]) through its gate/up
-    // projection, all experts in shared launches; then SwiGLU; then the down projections
-    std::vector<hip::GemmArgs> v;
-    for (int64_t e = 0; e < E_; ++e) {
-        const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
-        if (counts_h_[e] == 0) continue;
-        v.push_back(args(0, 1, m, f2, d_, at(xp_, o * d_), d_, exb + es * e * ex, d_, at(gu_, o * f2), f2, dt_, dt_));
+    // The expert products read the row offsets on the device (bf16), so the row passes and
+    // buffers cover the bound `rows` (the rows after the experts' blocks are padding rows);
+    // the fp32 path sizes everything from the host copy of the offsets.
+    if (dt_ == DType::BFloat16) {
+        used_ = rows;
+    } else {
+        host_offsets(s);
+        used_ = offsets_h_[E_];
     }
-    run_grouped(v, s);
-    hip::swiglu_fwd(gu_.get(), at(gu_, f_), f2, a_.get(), f_, used, f_, dt_, s);
-    v.clear();
-    for (int64_t e = 0; e < E_; ++e) {
-        const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
-        if (counts_h_[e] == 0) continue;
-        v.push_back(args(0, 1, m, d_, f_, at(a_, o * f_), f_, exb + es * (e * ex + 2 * f_ * d_), f_, at(ye_, o * d_),
-                         d_, dt_, dt_));
-    }
-    run_grouped(v, s);
+    xp_ = DeviceBuffer(es * used_ * d_, s);
+    gu_ = DeviceBuffer(es * used_ * f2, s);
+    a_ = DeviceBuffer(es * used_ * f_, s);
+    ye_ = DeviceBuffer(es * used_ * d_, s);
+    hip::moe_gather(h, d_, src_ent_.as<int>(), k_, used_, d_, xp_.get(), dt_, s);
+    const char* exb = static_cast<const char*>(experts_w);
+    // gate/up of each expert's rows, SwiGLU, then the down projections
+    experts(args(0, 1, used_, f2, d_, xp_.get(), d_, exb, d_, gu_.get(), f2, dt_, dt_), 0, ex, 0, s);
+    hip::swiglu_fwd(gu_.get(), static_cast<char*>(gu_.get()) + es * f_, f2, a_.get(), f_, used_, f_, dt_, s);
+    experts(args(0, 1, used_, d_, f_, a_.get(), f_, exb + es * 2 * f_ * d_, f_, ye_.get(), d_, dt_, dt_), 0, ex, 0, s);
     hip::moe_combine(ye_.get(), idx_.as<int64_t>(), dst_row_.as<int>(), gsel_.as<float>(), T, k_, d_, R, d_, y, d_, dt_,
                      s);
 }
@@ -129,42 +175,21 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
                       const float* daux_scale) {
     AIC_CHECK(T_ > 0 && dy && dh && dwr && dexperts, InvalidArgument, "MoEFFN::backward: forward first, no nulls");
     const size_t es = dtype_size(dt_);
-    const int64_t T = T_, f2 = 2 * f_, ex = 3 * f_ * d_, used = offsets_h_[E_];
-    auto at = [&](const DeviceBuffer& b, int64_t elem) { return static_cast<char*>(b.get()) + es * elem; };
+    const int64_t T = T_, f2 = 2 * f_, ex = 3 * f_ * d_, used = used_;
     DeviceBuffer dye(es * used * d_, s), dgsel(sizeof(float) * T * k_, s), da(es * used * f_, s),
         dgu(es * used * f2, s), dxp(es * used * d_, s), dlog(sizeof(float) * T * E_, s);
     hip::moe_combine_bwd(dy, d_, ye_.get(), src_ent_.as<int>(), gsel_.as<float>(), used, k_, d_, dye.get(),
                          dgsel.as<float>(), dt_, s);
     const char* exb = static_cast<const char*>(ex_);
-    // down projections: da = dye . Wd and dWd = dye^T . a per expert, each kind in shared launches
-    std::vector<hip::GemmArgs> vd, vw;
-    for (int64_t e = 0; e < E_; ++e) {
-        const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
-        float* dgu_w = dexperts + e * ex;
-        float* dd_w = dgu_w + 2 * f_ * d_;
-        if (counts_h_[e] == 0) {
-            AIC_HIP_CHECK(hipMemsetAsync(dgu_w, 0, sizeof(float) * ex, s));
-            continue;
-        }
-        vd.push_back(args(0, 0, m, f_, d_, at(dye, o * d_), d_, exb + es * (e * ex + 2 * f_ * d_), f_, at(da, o * f_),
-                          f_, dt_, dt_));
-        vw.push_back(args(1, 0, d_, f_, m, at(dye, o * d_), d_, at(a_, o * f_), f_, dd_w, f_, dt_, DType::Float32));
-    }
-    run_grouped(vd, s);
-    run_grouped(vw, s);
-    hip::swiglu_bwd(gu_.get(), at(gu_, f_), f2, da.get(), f_, dgu.get(), at(dgu, f_), f2, used, f_, dt_, s);
+    // down projections: da = dye . Wd and dWd = dye^T . a (fp32, zero for an expert with no rows)
+    experts(args(0, 0, used, f_, d_, dye.get(), d_, exb + es * 2 * f_ * d_, f_, da.get(), f_, dt_, dt_), 0, ex, 0, s);
+    experts(args(1, 0, d_, f_, 0, dye.get(), d_, a_.get(), f_, dexperts + 2 * f_ * d_, f_, dt_, DType::Float32), 1, 0,
+            ex, s);
+    hip::swiglu_bwd(gu_.get(), static_cast<char*>(gu_.get()) + es * f_, f2, da.get(), f_, dgu.get(),
+                    static_cast<char*>(dgu.get()) + es * f_, f2, used, f_, dt_, s);
     // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
-    vd.clear();
-    vw.clear();
-    for (int64_t e = 0; e < E_; ++e) {
-        const int64_t m = offsets_h_[e + 1] - offsets_h_[e], o = offsets_h_[e];
-        if (counts_h_[e] == 0) continue;
-        vd.push_back(args(0, 0, m, d_, f2, at(dgu, o * f2), f2, exb + es * e * ex, d_, at(dxp, o * d_), d_, dt_, dt_));
-        vw.push_back(args(1, 0, f2, d_, m, at(dgu, o * f2), f2, at(xp_, o * d_), d_, dexperts + e * ex, d_, dt_,
-                          DType::Float32));
-    }
-    run_grouped(vd, s);
-    run_grouped(vw, s);
+    experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s);
+    experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s);
     hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
     // router: dlogits from the gates and the aux loss, then both router products
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,

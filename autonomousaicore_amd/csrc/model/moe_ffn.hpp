@@ -9,6 +9,7 @@
 #include <cstdint>
 #include <vector>
 
+#include "../kernels/gemm.hpp"
 #include "../runtime/dtype.hpp"
 #include "../runtime/memory_pool.hpp"
 
@@ -32,7 +33,8 @@ public:
     // Routing of the last forward: idx [T, k] and counts [E] (device pointers).
     const int64_t* idx() const { return idx_.as<int64_t>(); }
     const int64_t* counts() const { return counts_.as<int64_t>(); }
-    const std::vector<int64_t>& counts_host() const { return counts_h_; }
+    // counts on the host (copied from the device, with a stream synchronisation, on first use)
+    const std::vector<int64_t>& counts_host();
 
 private:
     int64_t d_, f_, E_, k_;
@@ -42,6 +44,10 @@ private:
     const void* h_ = nullptr;
     const void* wr_ = nullptr;
     const void* ex_ = nullptr;
+    void host_offsets(hipStream_t s);
+    void experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s);
+    int64_t used_ = 0;  // rows of the permuted buffers
+    bool host_valid_ = false;
     std::vector<int64_t> counts_h_, offsets_h_;
     DeviceBuffer logits_, idx_, gsel_, probs_, counts_, offsets_, dst_row_, src_ent_, xp_, gu_, a_, ye_;
 };

@@ -178,3 +178,32 @@ def test_moe_ffn_bf16_close_to_fp32_oracle(orc):
     ref = orc.moe_ffn_bwd(h, wr, wg, wu, wd, k, 0.01, dy, 1.0)
     for name, got, r in zip(["dh", "dwr", "dwg", "dwu", "dwd"], [dh, dwr, dwg, dwu, dwd], ref):
         assert rel(got, r) < 6e-2, name
+
+
+@pytest.mark.parametrize("T", [384, 4096])
+def test_moe_ffn_bf16_idle_expert_and_determinism(orc, T):
+    """bf16: the expert products read the row offsets on the device (128- and 256-row tiles at
+    these sizes); an expert with no rows gets exactly zero weight gradients, the rest follow the
+    fp32 oracle, and two runs are bit-identical."""
+    rng = np.random.default_rng(29 + T)
+    d, f, E, k = 256, 704, 8, 2
+    h, wr, wg, wu, wd, dy = _weights(rng, T, d, f, E, scale=0.05)
+    wr[5] = -50.0 * np.abs(wr[5]) - 5.0
+    h = np.abs(h)
+    h, wr, wg, wu, wd, dy = (bf16_round(a) for a in (h, wr, wg, wu, wd, dy))
+    out1 = _ffn_run(h, wr, wg, wu, wd, k, 0.01, dy, 1.0, BF16)
+    out2 = _ffn_run(h, wr, wg, wu, wd, k, 0.01, dy, 1.0, BF16)
+    y, aux, idx, counts, dh, dwr, (dwg, dwu, dwd) = out1
+    assert counts[5] == 0 and counts.sum() == T * k
+    assert np.all(dwg[5] == 0) and np.all(dwu[5] == 0) and np.all(dwd[5] == 0)
+    for a, b in zip(out1[:6], out2[:6]):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(out1[6], out2[6]):
+        np.testing.assert_array_equal(a, b)
+    y_ref, aux_ref, idx_ref, _ = orc.moe_ffn_fwd(h, wr, wg, wu, wd, k, 0.01)
+    same = np.all(np.sort(idx, 1) == np.sort(idx_ref, 1), axis=1)
+    assert np.mean(same) > 0.97
+    assert rel(y[same], y_ref[same]) < 3e-2
+    ref = orc.moe_ffn_bwd(h, wr, wg, wu, wd, k, 0.01, dy, 1.0)
+    for name, got, r in zip(["dh", "dwr", "dwg", "dwu", "dwd"], [dh, dwr, dwg, dwu, dwd], ref):
+        assert rel(got, r) < 6e-2, name
