@@ -23,10 +23,10 @@ from collections import defaultdict
 
 # (regex on the demangled or mangled symbol, class); first match wins.
 _RULES = [
-    # gemm_bf16_dma[_grouped]<BM, BN, BK, STAGES, transA, transB, C>, demangled or mangled
-    (r"gemm_bf16_dma(_grouped)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
-    (r"gemm_bf16_dma(_grouped)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
-    (r"gemm_bf16_dma(_grouped)?(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
+    # gemm_bf16_dma[_grouped|_ragged]<BM, BN, BK, STAGES, transA, transB, C>, demangled or mangled
+    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
+    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
     (r"attn_fwd", "attn_fwd"),
     (r"attn_bwd|attn_dot", "attn_bwd"),
     (r"rmsnorm_fwd", "rmsnorm_fwd"),

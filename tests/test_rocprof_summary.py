@@ -12,6 +12,8 @@ SYMS = {
     "void aic::hip::(anonymous namespace)::gemm_bf16_dma_grouped<256, 256, 64, 2, true, false, float>(x)": "gemm_wgrad",
     "void aic::hip::(anonymous namespace)::gemm_bf16_dma_grouped<256, 256, 64, 2, false, true, float>(x)": "gemm_fwd",
     "_ZN3aic3hip12_GLOBAL__N_121gemm_bf16_dma_groupedILi256ELi256ELi64ELi2ELb0ELb0EDF16bEEvNS1_9DmaParamsE": "gemm_dgrad",
+    "void aic::hip::(anonymous namespace)::gemm_bf16_dma_ragged<256, 256, 64, 2, true, false, float>(x)": "gemm_wgrad",
+    "_ZN3aic3hip12_GLOBAL__N_120gemm_bf16_dma_raggedILi256ELi256ELi64ELi2ELb0ELb1EDF16bEEvNS1_12RaggedParamsE": "gemm_fwd",
     "void aic::hip::(anonymous namespace)::attn_bwd_dkdv_mfma<128>(x)": "attn_bwd",
     "_ZN3aic3hip12_GLOBAL__N_110attn_dot_kIDF16bEEvPKT_S5_lPfliii": "attn_bwd",
     "aic::hip::(anonymous namespace)::sqnorm_k(float const*, long, double*, int*)": "grad_norm",
