@@ -16,6 +16,7 @@
 //   aux = sum_e mean_t(probs[t, e]) * counts[e] * E * coef / (T * k) when coef > 0 and E > 1
 //   (moe.cpp:84-101), the counts entering as constants.
 #include <cstring>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -200,19 +201,51 @@ __global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict_
     for (int r = base_s + static_cast<int>(threadIdx.x); r < end; r += 1024) src_ent[r] = -1;
 }
 
+// VN consecutive elements as floats, and back: VN = 8 is one 16-byte access for bf16 (two for
+// fp32), VN = 1 the scalar form; the values and their rounding are the same either way.
+template <int VN, typename T>
+__device__ __forceinline__ void ldv(const T* p, float* v) {
+    if constexpr (VN == 8 && std::is_same_v<T, bf16>) {
+        const uint4 u = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[2 * q] = __uint_as_float(w[q] << 16);
+            v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+        }
+    } else if constexpr (VN == 8) {
+        const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        v[0] = ld(p, 0);
+    }
+}
+template <int VN, typename T>
+__device__ __forceinline__ void stv(T* p, const float* v) {
+    if constexpr (VN == 8 && std::is_same_v<T, bf16>) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                  pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+    } else if constexpr (VN == 8) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        st(p, 0, v[0]);
+    }
+}
+
 // xp[r, :] = x[token of entry src_ent[r], :], zero for padding rows
-template <typename T>
+template <typename T, int VN>
 __global__ __launch_bounds__(256) void moe_gather_k(const T* __restrict__ x, int64_t ldx, const int* __restrict__ src,
                                                     int k, int d, T* __restrict__ xp) {
     const int r = blockIdx.x;
     const int ent = src[r];
     T* o = xp + static_cast<int64_t>(r) * d;
-    if (ent < 0) {
-        for (int c = threadIdx.x; c < d; c += blockDim.x) st(o, c, 0.0f);
-        return;
-    }
-    const T* s = x + static_cast<int64_t>(ent / k) * ldx;
-    for (int c = threadIdx.x; c < d; c += blockDim.x) o[c] = s[c];
+    const T* sr = x + static_cast<int64_t>(ent < 0 ? 0 : ent / k) * ldx;
+    // raw copies (VN elements of 16 bytes' worth, or one element)
+    using V = std::conditional_t<VN == 1, T, uint4>;
+    constexpr int PER = VN == 1 ? 1 : static_cast<int>(16 / sizeof(T));
+    for (int c = threadIdx.x * PER; c < d; c += blockDim.x * PER)
+        *reinterpret_cast<V*>(o + c) = ent < 0 ? V{} : *reinterpret_cast<const V*>(sr + c);
 }
 
 // The token's slots in increasing expert order (the order the reference accumulates experts).
@@ -227,23 +260,37 @@ __device__ __forceinline__ void slot_order(const int64_t* idx_t, int k, int* ord
 }
 
 // out[t, :] = R[t, :] + sum over slots (increasing expert) of gsel[t, j] * ye[dst_row[t, j], :]
-template <typename T>
+template <typename T, int VN>
 __global__ __launch_bounds__(256) void moe_combine_k(const T* __restrict__ ye, const int64_t* __restrict__ idx,
                                                      const int* __restrict__ dst_row, const float* __restrict__ gsel,
                                                      int k, int d, const T* __restrict__ R, int64_t ldr,
                                                      T* __restrict__ out, int64_t ldo) {
     const int t = blockIdx.x;
-    int ord[kMaxK];
+    int ord[kMaxK], row[kMaxK];
+    float gs[kMaxK];
     slot_order(idx + static_cast<int64_t>(t) * k, k, ord);
-    for (int c = threadIdx.x; c < d; c += blockDim.x) {
-        float y = 0.0f;
+    for (int q = 0; q < k; ++q) {
+        row[q] = dst_row[static_cast<int64_t>(t) * k + ord[q]];
+        gs[q] = gsel[static_cast<int64_t>(t) * k + ord[q]];
+    }
+    for (int c = threadIdx.x * VN; c < d; c += blockDim.x * VN) {
+        float y[VN], v[VN];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) y[i] = 0.0f;
         for (int q = 0; q < k; ++q) {
-            const int j = ord[q];
-            const int r = dst_row[static_cast<int64_t>(t) * k + j];
-            y += ld(ye, static_cast<int64_t>(r) * d + c) * gsel[static_cast<int64_t>(t) * k + j];
+            ldv<VN>(ye + static_cast<int64_t>(row[q]) * d + c, v);
+#pragma unroll
+            for (int i = 0; i < VN; ++i) y[i] += v[i] * gs[q];
         }
-        const float base = R ? ld(R, static_cast<int64_t>(t) * ldr + c) : 0.0f;
-        st(out, static_cast<int64_t>(t) * ldo + c, base + y);
+        if (R) {
+            ldv<VN>(R + static_cast<int64_t>(t) * ldr + c, v);
+#pragma unroll
+            for (int i = 0; i < VN; ++i) y[i] = v[i] + y[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < VN; ++i) y[i] = 0.0f + y[i];
+        }
+        stv<VN>(out + static_cast<int64_t>(t) * ldo + c, y);
     }
 }
 
@@ -279,21 +326,30 @@ __global__ __launch_bounds__(256) void moe_combine_bwd_k(const T* __restrict__ d
 }
 
 // dx[t, :] (+)= sum over slots (increasing expert) of dxp[dst_row[t, j], :]
-template <typename T>
+template <typename T, int VN>
 __global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, const int64_t* __restrict__ idx,
                                                      const int* __restrict__ dst_row, int k, int d, T* __restrict__ dx,
                                                      int64_t ldx, int accumulate) {
     const int t = blockIdx.x;
-    int ord[kMaxK];
+    int ord[kMaxK], row[kMaxK];
     slot_order(idx + static_cast<int64_t>(t) * k, k, ord);
-    for (int c = threadIdx.x; c < d; c += blockDim.x) {
-        float s = 0.0f;
+    for (int q = 0; q < k; ++q) row[q] = dst_row[static_cast<int64_t>(t) * k + ord[q]];
+    for (int c = threadIdx.x * VN; c < d; c += blockDim.x * VN) {
+        float sm[VN], v[VN];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) sm[i] = 0.0f;
         for (int q = 0; q < k; ++q) {
-            const int r = dst_row[static_cast<int64_t>(t) * k + ord[q]];
-            s += ld(dxp, static_cast<int64_t>(r) * d + c);
+            ldv<VN>(dxp + static_cast<int64_t>(row[q]) * d + c, v);
+#pragma unroll
+            for (int i = 0; i < VN; ++i) sm[i] += v[i];
         }
-        const int64_t o = static_cast<int64_t>(t) * ldx + c;
-        st(dx, o, accumulate ? ld(dx, o) + s : s);
+        T* o = dx + static_cast<int64_t>(t) * ldx + c;
+        if (accumulate) {
+            ldv<VN>(o, v);
+#pragma unroll
+            for (int i = 0; i < VN; ++i) sm[i] = v[i] + sm[i];
+        }
+        stv<VN>(o, sm);
     }
 }
 
@@ -343,6 +399,8 @@ __global__ __launch_bounds__(256) void moe_router_bwd_k(const float* __restrict_
     for (int e = 0; e < E; ++e) dlogits[static_cast<int64_t>(t) * E + e] = dl[e];
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 void check_moe(int64_t T, int64_t E, int64_t k) {
     AIC_CHECK(T >= 1 && T < (1LL << 28), InvalidArgument, "moe: token count out of range");
     AIC_CHECK(E >= 1 && E <= kMaxE, InvalidArgument, "moe: experts must be in [1, ", kMaxE, "]");
@@ -380,16 +438,22 @@ void moe_gather(const void* x, int64_t ldx, const int* src_ent, int64_t k, int64
                 hipStream_t s) {
     AIC_CHECK(rows >= 0 && d > 0 && ldx >= d && k >= 1, InvalidArgument, "moe_gather: bad shape");
     if (rows == 0) return;
-    if (dt == DType::BFloat16)
-        hipLaunchKernelGGL(moe_gather_k<bf16>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
-                           static_cast<const bf16*>(x), ldx, src_ent, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<bf16*>(xp));
-    else if (dt == DType::Float32)
-        hipLaunchKernelGGL(moe_gather_k<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
-                           static_cast<const float*>(x), ldx, src_ent, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<float*>(xp));
-    else
+    // 16-byte accesses when every row start is 16-byte aligned
+    const bool v = d % 8 == 0 && ldx % 8 == 0 && aligned16(x) && aligned16(xp);
+    const dim3 g(static_cast<unsigned>(rows)), b(v ? 128 : 256);
+    if (dt == DType::BFloat16) {
+        if (v) hipLaunchKernelGGL((moe_gather_k<bf16, 8>), g, b, 0, s, static_cast<const bf16*>(x), ldx, src_ent,
+                                  static_cast<int>(k), static_cast<int>(d), static_cast<bf16*>(xp));
+        else hipLaunchKernelGGL((moe_gather_k<bf16, 1>), g, b, 0, s, static_cast<const bf16*>(x), ldx, src_ent,
+                                static_cast<int>(k), static_cast<int>(d), static_cast<bf16*>(xp));
+    } else if (dt == DType::Float32) {
+        if (v) hipLaunchKernelGGL((moe_gather_k<float, 8>), g, b, 0, s, static_cast<const float*>(x), ldx, src_ent,
+                                  static_cast<int>(k), static_cast<int>(d), static_cast<float*>(xp));
+        else hipLaunchKernelGGL((moe_gather_k<float, 1>), g, b, 0, s, static_cast<const float*>(x), ldx, src_ent,
+                                static_cast<int>(k), static_cast<int>(d), static_cast<float*>(xp));
+    } else {
         AIC_THROW(DTypeMismatch, "moe_gather: dtype must be f32 or bf16");
+    }
     AIC_LAUNCH_CHECK("moe_gather");
 }
 
@@ -397,16 +461,23 @@ void moe_combine(const void* ye, const int64_t* idx, const int* dst_row, const f
                  int64_t d, const void* R, int64_t ldr, void* out, int64_t ldo, DType dt, hipStream_t s) {
     AIC_CHECK(T >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldo >= d, InvalidArgument, "moe_combine: bad shape");
     if (T == 0) return;
-    if (dt == DType::BFloat16)
-        hipLaunchKernelGGL(moe_combine_k<bf16>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           static_cast<const bf16*>(ye), idx, dst_row, gsel, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<const bf16*>(R), ldr, static_cast<bf16*>(out), ldo);
-    else if (dt == DType::Float32)
-        hipLaunchKernelGGL(moe_combine_k<float>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           static_cast<const float*>(ye), idx, dst_row, gsel, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<const float*>(R), ldr, static_cast<float*>(out), ldo);
-    else
+    const bool v = d % 8 == 0 && ldo % 8 == 0 && aligned16(ye) && aligned16(out) &&
+                   (!R || (ldr % 8 == 0 && aligned16(R)));
+    const dim3 g(static_cast<unsigned>(T)), b(v ? 128 : 256);
+#define AIC_COMBINE(TT, VN)                                                                                        \
+    hipLaunchKernelGGL((moe_combine_k<TT, VN>), g, b, 0, s, static_cast<const TT*>(ye), idx, dst_row, gsel,       \
+                       static_cast<int>(k), static_cast<int>(d), static_cast<const TT*>(R), ldr,                  \
+                       static_cast<TT*>(out), ldo)
+    if (dt == DType::BFloat16) {
+        if (v) AIC_COMBINE(bf16, 8);
+        else AIC_COMBINE(bf16, 1);
+    } else if (dt == DType::Float32) {
+        if (v) AIC_COMBINE(float, 8);
+        else AIC_COMBINE(float, 1);
+    } else {
         AIC_THROW(DTypeMismatch, "moe_combine: dtype must be f32 or bf16");
+    }
+#undef AIC_COMBINE
     AIC_LAUNCH_CHECK("moe_combine");
 }
 
@@ -432,16 +503,21 @@ void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_
                  int64_t ldx, bool accumulate, DType dt, hipStream_t s) {
     AIC_CHECK(T >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldx >= d, InvalidArgument, "moe_scatter: bad shape");
     if (T == 0) return;
-    if (dt == DType::BFloat16)
-        hipLaunchKernelGGL(moe_scatter_k<bf16>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           static_cast<const bf16*>(dxp), idx, dst_row, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<bf16*>(dx), ldx, accumulate ? 1 : 0);
-    else if (dt == DType::Float32)
-        hipLaunchKernelGGL(moe_scatter_k<float>, dim3(static_cast<unsigned>(T)), dim3(256), 0, s,
-                           static_cast<const float*>(dxp), idx, dst_row, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<float*>(dx), ldx, accumulate ? 1 : 0);
-    else
+    const bool v = d % 8 == 0 && ldx % 8 == 0 && aligned16(dxp) && aligned16(dx);
+    const dim3 g(static_cast<unsigned>(T)), b(v ? 128 : 256);
+#define AIC_SCATTER(TT, VN)                                                                                        \
+    hipLaunchKernelGGL((moe_scatter_k<TT, VN>), g, b, 0, s, static_cast<const TT*>(dxp), idx, dst_row,             \
+                       static_cast<int>(k), static_cast<int>(d), static_cast<TT*>(dx), ldx, accumulate ? 1 : 0)
+    if (dt == DType::BFloat16) {
+        if (v) AIC_SCATTER(bf16, 8);
+        else AIC_SCATTER(bf16, 1);
+    } else if (dt == DType::Float32) {
+        if (v) AIC_SCATTER(float, 8);
+        else AIC_SCATTER(float, 1);
+    } else {
         AIC_THROW(DTypeMismatch, "moe_scatter: dtype must be f32 or bf16");
+    }
+#undef AIC_SCATTER
     AIC_LAUNCH_CHECK("moe_scatter");
 }
 
