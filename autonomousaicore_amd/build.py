@@ -40,9 +40,15 @@ def _obj(src: str) -> str:
     return os.path.join(BUILD, rel + ".o")
 
 
+# Per-file code generation options.  attention.hip: MFMAs in the VGPR form, so that the
+# backward's long-lived dK/dV accumulators are not copied between VGPRs and AGPRs around every
+# MFMA of the inner loop (the AGPR form's register assignment does that for these kernels).
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> tuple[str, int, str]:
     obj = _obj(src)
-    cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     msg = "\n".join(l for l in (p.stdout + p.stderr).splitlines() if "packed-fp32-ops" not in l)
     return src, p.returncode, msg
