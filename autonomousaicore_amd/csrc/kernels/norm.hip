@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_k(const T* __restrict__ dy, i
 // twice as many waves are in flight as in the loop form); the lane's
 // dw contributions accumulate in registers over its rows, then the four waves' sums are
 // added in wave order, as the loop form does through LDS.
-constexpr int kBwdRegRowsPerWave = 2;
+constexpr int kBwdRegRowsPerWave = 4;
 
 template <typename T, int VN, int CH>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_r(const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x,

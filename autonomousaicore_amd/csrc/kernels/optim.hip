@@ -30,7 +30,21 @@ __global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int
     int nf = 0;
     const int64_t n4 = ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) ? n / 4 : 0;
     const float4* g4 = reinterpret_cast<const float4*>(g);
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    // four loads in flight per thread; the values are added in the same order as one at a time
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g4) + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            nf |= !finite_(v[u].x) | !finite_(v[u].y) | !finite_(v[u].z) | !finite_(v[u].w);
+            acc += static_cast<double>(v[u].x * v[u].x + v[u].y * v[u].y) +
+                   static_cast<double>(v[u].z * v[u].z + v[u].w * v[u].w);
+        }
+    }
+    for (; i < n4; i += stride) {
         const float4 v = g4[i];
         nf |= !finite_(v.x) | !finite_(v.y) | !finite_(v.z) | !finite_(v.w);
         acc += static_cast<double>(v.x * v.x + v.y * v.y) + static_cast<double>(v.z * v.z + v.w * v.w);
