@@ -293,6 +293,39 @@ __global__ __launch_bounds__(256) void attn_dot_k(const T* __restrict__ o, const
     }
 }
 
+// The same for bf16 rows of HD % 8 == 0 elements with 16-byte loads: HD / 8 lanes per
+// (token, head) row, 64 / (HD / 8) rows per wave; each lane's eight products, then a
+// butterfly over the row's lanes.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_dot_v8_k(const bf16* __restrict__ o, const bf16* __restrict__ dout,
+                                                     int64_t ldo, float* __restrict__ D, int64_t Ttok, int H, int S) {
+    constexpr int LPR = HD / 8, RPW = 64 / LPR;
+    const int64_t gw = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63, sub = lane % LPR;
+    const int64_t row = gw * RPW + lane / LPR;
+    const bool ok = row < Ttok * H;
+    float acc = 0.0f;
+    if (ok) {
+        const int64_t t = row / H;
+        const int h = static_cast<int>(row % H);
+        const int64_t i = t * ldo + static_cast<int64_t>(h) * HD + sub * 8;
+        const uint4 a = *reinterpret_cast<const uint4*>(o + i), b = *reinterpret_cast<const uint4*>(dout + i);
+        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc += __uint_as_float(wa[q] << 16) * __uint_as_float(wb[q] << 16);
+            acc += __uint_as_float(wa[q] & 0xffff0000u) * __uint_as_float(wb[q] & 0xffff0000u);
+        }
+    }
+#pragma unroll
+    for (int w = LPR / 2; w > 0; w >>= 1) acc += __shfl_xor(acc, w);
+    if (ok && sub == 0) {
+        const int64_t t = row / H, b = t / S, s = t % S;
+        const int h = static_cast<int>(row % H);
+        D[(b * H + h) * S + s] = acc;
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Backward: dK, dV.  Stage = Q tile, dO tile (64 x HD each), lse and D of the 64 queries.
 // ---------------------------------------------------------------------------------------
@@ -859,7 +892,22 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
     float* D = static_cast<float*>(stream_scratch(sizeof(float) * B * H * S, s));
     const int64_t waves = B * S * H;
     const unsigned dgrid = static_cast<unsigned>((waves * 64 + 255) / 256);
-    if (dt == DType::BFloat16)
+    const bool al16 = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15u) == 0;
+    if (dt == DType::BFloat16 && ld_o % 8 == 0 && al16 && (hd == 32 || hd == 64 || hd == 128)) {
+        const int64_t rpw = 64 / (hd / 8);  // rows per wave
+        const unsigned g8 = static_cast<unsigned>(((waves + rpw - 1) / rpw * 64 + 255) / 256);
+        const bf16* ob = static_cast<const bf16*>(o);
+        const bf16* db = static_cast<const bf16*>(dout);
+        if (hd == 128)
+            hipLaunchKernelGGL(attn_dot_v8_k<128>, dim3(g8), dim3(256), 0, s, ob, db, ld_o, D, B * S,
+                               static_cast<int>(H), static_cast<int>(S));
+        else if (hd == 64)
+            hipLaunchKernelGGL(attn_dot_v8_k<64>, dim3(g8), dim3(256), 0, s, ob, db, ld_o, D, B * S,
+                               static_cast<int>(H), static_cast<int>(S));
+        else
+            hipLaunchKernelGGL(attn_dot_v8_k<32>, dim3(g8), dim3(256), 0, s, ob, db, ld_o, D, B * S,
+                               static_cast<int>(H), static_cast<int>(S));
+    } else if (dt == DType::BFloat16)
         hipLaunchKernelGGL(attn_dot_k<bf16>, dim3(dgrid), dim3(256), 0, s, static_cast<const bf16*>(o),
                            static_cast<const bf16*>(dout), ld_o, D, B * S, static_cast<int>(H), static_cast<int>(S),
                            static_cast<int>(hd));
