@@ -343,15 +343,20 @@ bool gemm_ragged_eligible(const RaggedArgs& r) {
 void gemm_ragged(const RaggedArgs& r, hipStream_t s) {
     AIC_CHECK(gemm_ragged_eligible(r), InvalidArgument, "gemm_ragged: unsupported shape, layout or dtype");
     const GemmArgs& a = r.g;
-    // tile size from the product's size at full occupancy: the row bound (ragged M) or E
-    // experts' output tiles (ragged K)
-    const int64_t t256 = r.ragged_k ? r.E * ((a.M + 255) / 256) * ((a.N + 255) / 256)
-                                    : ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    // Tile shape: the grid's tiles (a bound for ragged M) in rounds of 256 CUs; the 256x256
+    // tile unless its last round leaves so many CUs idle that 128x128 tiles (taken as 0.8 of
+    // its rate) fill the rounds better.
+    auto tiles = [&](int64_t t) {
+        const int64_t tn = (a.N + t - 1) / t;
+        return r.ragged_k ? r.E * ((a.M + t - 1) / t) * tn : ((a.M + t - 1) / t + r.E) * tn;
+    };
+    auto fill = [](int64_t n) { return static_cast<double>(n) / (256.0 * static_cast<double>((n + 255) / 256)); };
+    const bool big = tiles(256) >= 128 && fill(tiles(256)) >= 0.8 * fill(tiles(128));
     if (a.c == DType::Float32) {
-        if (t256 >= 128) dispatch_ragged<256, 256, 64, 2, float>(r, s);
+        if (big) dispatch_ragged<256, 256, 64, 2, float>(r, s);
         else dispatch_ragged<128, 128, 64, 4, float>(r, s);
     } else {
-        if (t256 >= 128) dispatch_ragged<256, 256, 64, 2, bf16>(r, s);
+        if (big) dispatch_ragged<256, 256, 64, 2, bf16>(r, s);
         else dispatch_ragged<128, 128, 64, 4, bf16>(r, s);
     }
 }

@@ -77,6 +77,10 @@ void MoEFFN::host_offsets(hipStream_t s) {
 }
 
 const std::vector<int64_t>& MoEFFN::counts_host() {
+    if (T_ == 0) {  // no forward yet: no routing
+        counts_h_.clear();
+        return counts_h_;
+    }
     host_offsets(nullptr);
     return counts_h_;
 }
