@@ -20,6 +20,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "../runtime/memory_pool.hpp"
 
 namespace aic::hip {
 
@@ -76,15 +77,16 @@ __global__ __launch_bounds__(256) void moe_route_k(const float* __restrict__ log
     }
 }
 
-// One block: per-expert counts, mean probabilities (double, fixed order) and the aux loss.
+// Per-expert probability sums and counts of the tokens [blockIdx.x * 1024, + 1024): thread t
+// takes one token for 8 experts at a time, the 16 waves reduce with shuffles and their
+// partials are added in wave order; part_p / part_c [block][E] (fixed order: deterministic).
 __global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ idx, const float* __restrict__ probs,
-                                                    int T, int E, int k, float aux_coef, int64_t* __restrict__ counts,
-                                                    float* __restrict__ mean_probs, float* __restrict__ aux) {
-    // thread t sums tokens t, t + 1024, ... for 8 experts at a time in registers; the 16 waves
-    // reduce with shuffles, then their partials are added in wave order (fixed: deterministic)
+                                                    int T, int E, int k, double* __restrict__ part_p,
+                                                    long long* __restrict__ part_c) {
     __shared__ double sp[16][kMaxE];
     __shared__ long long sc[16][kMaxE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = static_cast<int>(blockIdx.x) * 1024 + static_cast<int>(threadIdx.x);
     for (int e0 = 0; e0 < E; e0 += 8) {
         double a[8];
         long long c[8];
@@ -93,11 +95,11 @@ __global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ 
             a[u] = 0.0;
             c[u] = 0;
         }
-        for (int t = threadIdx.x; t < T; t += 1024) {
+        if (t < T) {
             const float* pr = probs + static_cast<int64_t>(t) * E + e0;
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                if (e0 + u < E) a[u] += static_cast<double>(pr[u]);
+                if (e0 + u < E) a[u] = static_cast<double>(pr[u]);
             for (int j = 0; j < k; ++j) {
                 const int64_t id = idx[static_cast<int64_t>(t) * k + j] - e0;
 #pragma unroll
@@ -117,14 +119,31 @@ __global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ 
         }
     }
     __syncthreads();
-    __shared__ float mp_s[kMaxE];
-    __shared__ long long cnt_s[kMaxE];
     if (threadIdx.x < E) {
         double a = 0.0;
         long long c = 0;
         for (int w = 0; w < 16; ++w) {
             a += sp[w][threadIdx.x];
             c += sc[w][threadIdx.x];
+        }
+        part_p[static_cast<int64_t>(blockIdx.x) * E + threadIdx.x] = a;
+        part_c[static_cast<int64_t>(blockIdx.x) * E + threadIdx.x] = c;
+    }
+}
+
+// The block partials added in block order: counts, mean probabilities and the aux loss.
+__global__ __launch_bounds__(64) void moe_stats_final_k(const double* __restrict__ part_p,
+                                                        const long long* __restrict__ part_c, int nparts, int T,
+                                                        int E, int k, float aux_coef, int64_t* __restrict__ counts,
+                                                        float* __restrict__ mean_probs, float* __restrict__ aux) {
+    __shared__ float mp_s[kMaxE];
+    __shared__ long long cnt_s[kMaxE];
+    if (threadIdx.x < E) {
+        double a = 0.0;
+        long long c = 0;
+        for (int b = 0; b < nparts; ++b) {
+            a += part_p[static_cast<int64_t>(b) * E + threadIdx.x];
+            c += part_c[static_cast<int64_t>(b) * E + threadIdx.x];
         }
         mp_s[threadIdx.x] = static_cast<float>(a / static_cast<double>(T));
         cnt_s[threadIdx.x] = c;
@@ -416,9 +435,16 @@ void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_c
     hipLaunchKernelGGL(moe_route_k, dim3(grid_for(T, 256)), dim3(256), 0, s, logits, static_cast<int>(T),
                        static_cast<int>(E), static_cast<int>(k), idx, gsel, probs, rweights);
     AIC_LAUNCH_CHECK("moe_route");
-    hipLaunchKernelGGL(moe_stats_k, dim3(1), dim3(1024), 0, s, idx, probs, static_cast<int>(T), static_cast<int>(E),
-                       static_cast<int>(k), aux_coef, counts, mean_probs, aux);
+    // statistics: 1024 tokens per block, then the partials in block order
+    const int nparts = static_cast<int>((T + 1023) / 1024);
+    double* part_p = static_cast<double*>(stream_scratch((sizeof(double) + sizeof(long long)) * nparts * E, s));
+    long long* part_c = reinterpret_cast<long long*>(part_p + static_cast<int64_t>(nparts) * E);
+    hipLaunchKernelGGL(moe_stats_k, dim3(static_cast<unsigned>(nparts)), dim3(1024), 0, s, idx, probs,
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), part_p, part_c);
     AIC_LAUNCH_CHECK("moe_stats");
+    hipLaunchKernelGGL(moe_stats_final_k, dim3(1), dim3(64), 0, s, part_p, part_c, nparts, static_cast<int>(T),
+                       static_cast<int>(E), static_cast<int>(k), aux_coef, counts, mean_probs, aux);
+    AIC_LAUNCH_CHECK("moe_stats_final");
 }
 
 int64_t moe_max_rows(int64_t T, int64_t E, int64_t k) { return T * k + E * (kRowAlign - 1); }
