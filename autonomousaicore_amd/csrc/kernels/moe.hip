@@ -315,7 +315,7 @@ __global__ __launch_bounds__(256) void moe_combine_k(const T* __restrict__ ye, c
 
 // Per expert row r (entry t * k + j): dye[r] = gsel[t, j] * dout[t] and
 // dgsel[t, j] = sum_c dout[t, c] * ye[r, c] (double, fixed order); padding rows get dye = 0.
-template <typename T>
+template <typename T, int VN>
 __global__ __launch_bounds__(256) void moe_combine_bwd_k(const T* __restrict__ dout, int64_t ldo, const T* __restrict__ ye,
                                                          const int* __restrict__ src_ent, const float* __restrict__ gsel,
                                                          int k, int d, T* __restrict__ dye, float* __restrict__ dgsel) {
@@ -323,17 +323,26 @@ __global__ __launch_bounds__(256) void moe_combine_bwd_k(const T* __restrict__ d
     const int ent = src_ent[r];
     T* dr = dye + static_cast<int64_t>(r) * d;
     if (ent < 0) {
-        for (int c = threadIdx.x; c < d; c += blockDim.x) st(dr, c, 0.0f);
+        float z[VN];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) z[i] = 0.0f;
+        for (int c = threadIdx.x * VN; c < d; c += blockDim.x * VN) stv<VN>(dr + c, z);
         return;
     }
     const int t = ent / k;
     const float g = gsel[ent];
     __shared__ double red[256];
     double acc = 0.0;
-    for (int c = threadIdx.x; c < d; c += blockDim.x) {
-        const float go = ld(dout, static_cast<int64_t>(t) * ldo + c);
-        acc += static_cast<double>(go * ld(ye, static_cast<int64_t>(r) * d + c));
-        st(dr, c, go * g);
+    for (int c = threadIdx.x * VN; c < d; c += blockDim.x * VN) {
+        float go[VN], yv[VN], o[VN];
+        ldv<VN>(dout + static_cast<int64_t>(t) * ldo + c, go);
+        ldv<VN>(ye + static_cast<int64_t>(r) * d + c, yv);
+#pragma unroll
+        for (int i = 0; i < VN; ++i) {
+            acc += static_cast<double>(go[i] * yv[i]);
+            o[i] = go[i] * g;
+        }
+        stv<VN>(dr + c, o);
     }
     red[threadIdx.x] = acc;
     __syncthreads();
@@ -511,17 +520,22 @@ void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* s
                      int64_t k, int64_t d, void* dye, float* dgsel, DType dt, hipStream_t s) {
     AIC_CHECK(rows >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldo >= d, InvalidArgument, "moe_combine_bwd: bad shape");
     if (rows == 0) return;
-    const dim3 g(static_cast<unsigned>(rows));
-    if (dt == DType::BFloat16)
-        hipLaunchKernelGGL(moe_combine_bwd_k<bf16>, g, dim3(256), 0, s, static_cast<const bf16*>(dout), ldo,
-                           static_cast<const bf16*>(ye), src_ent, gsel, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<bf16*>(dye), dgsel);
-    else if (dt == DType::Float32)
-        hipLaunchKernelGGL(moe_combine_bwd_k<float>, g, dim3(256), 0, s, static_cast<const float*>(dout), ldo,
-                           static_cast<const float*>(ye), src_ent, gsel, static_cast<int>(k), static_cast<int>(d),
-                           static_cast<float*>(dye), dgsel);
-    else
+    const bool v = d % 8 == 0 && ldo % 8 == 0 && aligned16(dout) && aligned16(ye) && aligned16(dye);
+    const dim3 g(static_cast<unsigned>(rows)), b(v ? 128 : 256);
+#define AIC_COMBINE_BWD(TT, VN)                                                                                    \
+    hipLaunchKernelGGL((moe_combine_bwd_k<TT, VN>), g, b, 0, s, static_cast<const TT*>(dout), ldo,                \
+                       static_cast<const TT*>(ye), src_ent, gsel, static_cast<int>(k), static_cast<int>(d),       \
+                       static_cast<TT*>(dye), dgsel)
+    if (dt == DType::BFloat16) {
+        if (v) AIC_COMBINE_BWD(bf16, 8);
+        else AIC_COMBINE_BWD(bf16, 1);
+    } else if (dt == DType::Float32) {
+        if (v) AIC_COMBINE_BWD(float, 8);
+        else AIC_COMBINE_BWD(float, 1);
+    } else {
         AIC_THROW(DTypeMismatch, "moe_combine_bwd: dtype must be f32 or bf16");
+    }
+#undef AIC_COMBINE_BWD
     AIC_LAUNCH_CHECK("moe_combine_bwd");
 }
 
