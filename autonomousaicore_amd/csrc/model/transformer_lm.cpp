@@ -695,7 +695,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     const int64_t r = cfg_.lora_rank;
     const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
     DeviceBuffer& xa_all = act(ql ? L * T * 7 * r : 0);
-    DeviceBuffer& wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
+    // and each layer's dequantized base projections: formed in the forward, reused by the
+    // backward (one dequantization per projection per step, at 2 B per base weight in HBM)
+    const int64_t wl = 4 * d * d + 3 * f * d;
+    DeviceBuffer& wbuf = act(ql ? L * wl : 0);
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
         return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
     };
@@ -707,17 +710,25 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     // a projection's base weight: the arena, or with QLoRA the INT4 copy dequantized into wbuf
     // (QuantizedLinear::forward, src/nn/quantization.cpp:602-615); projections j0..j1 (q, k, v,
     // o, gate, up, down) stacked
-    auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
+    // projections j0.. of layer l in wbuf: q/k/v (j0 = 0), o (3), gate/up (4), down (6)
+    auto wslot = [&](int64_t l, int j0) -> void* {
+        const int64_t o = j0 == 0 ? 0 : j0 == 3 ? 3 * d * d : j0 == 4 ? 4 * d * d : 4 * d * d + 2 * f * d;
+        return at(wbuf, l * wl + o);
+    };
+    auto wbase = [&](const Layer& ly, int64_t l, int64_t off, int j0, int j1) -> const void* {
         if (!ql) return WB(off);
+        char* dst = static_cast<char*>(wslot(l, j0));
         int64_t o = 0;
         for (int j = j0; j <= j1; ++j) {
             int64_t po, n;
             proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, po, n);
-            dequant(ly, j, n, static_cast<char*>(wbuf.get()) + es * o, s);
+            dequant(ly, j, n, dst + es * o, s);
             o += n;
         }
-        return wbuf.get();
+        return dst;
     };
+    // the backward's view of the same weights (dequantized by the forward)
+    auto wkept = [&](int64_t l, int64_t off, int j0) -> const void* { return ql ? wslot(l, j0) : WB(off); };
     // the frozen model's gradients are not formed with QLoRA
     auto GB = [&](int64_t off) -> float* { return ql ? nullptr : G(off); };
 
@@ -749,7 +760,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xaq(l), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lq = LowRank{xaq(l), 3 * r, W(ly.bq), r, r, d, 0};
         }
-        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
+        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, l, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lq : nullptr);
         {
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
@@ -765,7 +776,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lo_ = LowRank{xao(l), r, W(ly.bo), r, r, 0, 0};
         }
-        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
+        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, l, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
              ql ? &lo_ : nullptr);
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
@@ -781,7 +792,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xagu(l), 2 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lg = LowRank{xagu(l), 2 * r, W(ly.bg), r, r, f, 0};
         }
-        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
+        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, l, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lg : nullptr);
         {
             auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
@@ -792,7 +803,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             ld_ = LowRank{xad(l), r, W(ly.bd), r, r, 0, 0};
         }
-        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
+        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, l, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
              ql ? &ld_ : nullptr);
     }
     void* xL = at(xs, L * T * d);
@@ -867,7 +878,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             } else {
                 gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
             }
-            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s, nullptr, 0, 0.0f,
+            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wkept(l, ly.wd, 6), f, da.get(), f, dt, dt, s, nullptr, 0, 0.0f,
                  1.0f, ql ? &ld_ : nullptr);
             {
                 auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
@@ -885,7 +896,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             } else {
                 gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
             }
-            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s,
+            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wkept(l, ly.wgu, 4), d, dh.get(), d, dt, dt, s,
                  nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr);
         }
         {
@@ -900,7 +911,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
             lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
         }  // else: the out_proj weight gradient joins the q/k/v one below (dx is unchanged until then)
-        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
+        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wkept(l, ly.wo, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lo_ : nullptr);
         {
             // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
@@ -928,7 +939,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dx.get(), ol, G(ly.wo)}},
                           {{3 * d, d, T}, {d, d, T}}, dt, s);
         }
-        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
+        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wkept(l, ly.wqkv, 0), d, dh.get(), d, dt, dt, s, nullptr,
              0, 0.0f, 1.0f, ql ? &lq : nullptr);
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
