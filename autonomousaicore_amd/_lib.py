@@ -92,6 +92,8 @@ SIGNATURES = {
     "aic_hip_swiglu_bwd": (i32, [vp, vp, i64, vp, i64, vp, vp, i64, i64, i64, i32, vp]),
     "aic_hip_ce_fwd": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, vp, i32, vp]),
     "aic_hip_ce_bwd": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, vp, vp, i64, i32, vp]),
+    "aic_hip_ce_bwd_rows": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, i32, f32, vp, i64, i32, vp]),
+    "aic_hip_memcpy_sync": (i32, [vp, vp, C.c_size_t, vp]),
     "aic_hip_embed_fwd": (i32, [vp, i64, vp, i64, i64, vp, i32, vp]),
     "aic_hip_embed_bwd": (i32, [vp, i64, vp, i64, i64, vp, i32, i32, vp]),
     "aic_hip_grad_sqnorm_multi": (i32, [C.POINTER(vp), i64p, i32, vp, vp, vp]),
@@ -137,6 +139,7 @@ SIGNATURES = {
     "aic_lm_num_base_tensors": (i32, [vp]),
     "aic_lm_base_tensor_info": (i32, [vp, i32, C.c_char_p, i32, C.POINTER(i32), i64p, i64p]),
     "aic_lm_set_base_params": (i32, [vp, vp]),
+    "aic_lm_get_base_params": (i32, [vp, vp]),
     "aic_lm_set_params": (i32, [vp, vp]),
     "aic_lm_step_history": (i32, [vp, C.POINTER(StepRecord), i32, C.POINTER(i32), i64p]),
     "aic_lm_snapshot": (i32, [vp]),
@@ -153,6 +156,7 @@ SIGNATURES = {
     "aic_telemetry_reset": (i32, [vp]),
     "aic_telemetry_latest_json": (i32, [vp, C.c_char_p, i32]),
     "aic_lm_forward_step": (i32, [vp, vp, i64, i64, i64, i32, vp]),
+    "aic_sample_tokens": (i32, [vp, i64, f32, i32, f32, C.c_uint64, i64, vp]),
     "aic_lm_generate": (i32, [vp, vp, i64, i64, f32, i32, f32, i64, C.c_uint64, vp, i64p]),
     "aic_lm_save_checkpoint": (i32, [vp, C.c_char_p, i64, i64, f32, C.c_char_p, i32]),
     "aic_lm_load_checkpoint": (i32, [vp, C.c_char_p, i64p, i64p, f32p, C.c_char_p, i32, C.POINTER(i32)]),

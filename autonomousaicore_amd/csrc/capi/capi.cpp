@@ -265,6 +265,24 @@ int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const
     });
 }
 
+int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N,
+                        int64_t C, int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits,
+                        int64_t ld_d, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::ce_bwd_rows(logits, ld, targets, lse, N, C, ignore_index, grad, per_row, divisor, dlogits, ld_d,
+                              dt(d), st(stream));
+    });
+}
+
+int aic_hip_memcpy_sync(void* dst, const void* src, size_t bytes, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(bytes == 0 || (dst && src), InvalidArgument, "memcpy_sync: null pointer");
+        if (bytes == 0) return;
+        AIC_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, st(stream)));
+        AIC_HIP_CHECK(hipStreamSynchronize(st(stream)));
+    });
+}
+
 int aic_hip_embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, aic_dtype d,
                       aic_stream stream) {
     return guard([&] { aic::hip::embed_fwd(ids, N, W, V, D, out, dt(d), st(stream)); });
@@ -408,6 +426,13 @@ int aic_lm_set_base_params(aic_lm* lm, const float* host) {
     return guard([&] {
         AIC_CHECK(lm && host, InvalidArgument, "null argument");
         lm->model->set_base_params(host);
+    });
+}
+
+int aic_lm_get_base_params(const aic_lm* lm, float* host) {
+    return guard([&] {
+        AIC_CHECK(lm && host, InvalidArgument, "null argument");
+        lm->model->get_base_params(host);
     });
 }
 
@@ -922,6 +947,16 @@ int aic_lm_forward_step(aic_lm* lm, const int64_t* ids, int64_t B, int64_t S, in
         m->forward_step(dids.as<int64_t>(), B, S, start_pos, dl.as<float>());
         AIC_HIP_CHECK(hipMemcpyAsync(logits, dl.get(), sizeof(float) * T * V, hipMemcpyDeviceToHost, s));
         AIC_HIP_CHECK(hipStreamSynchronize(s));
+    });
+}
+
+int aic_sample_tokens(const float* logits, int64_t V, float temperature, int top_k, float top_p, uint64_t seed,
+                      int64_t n_draws, int64_t* out) {
+    return guard([&] {
+        AIC_CHECK(logits && out && V > 0 && n_draws >= 0, InvalidArgument, "sample_tokens: bad arguments");
+        const std::vector<float> l(logits, logits + V);
+        std::mt19937_64 rng(seed);
+        for (int64_t i = 0; i < n_draws; ++i) out[i] = aic::models::sample_token(l, temperature, top_k, top_p, rng);
     });
 }
 

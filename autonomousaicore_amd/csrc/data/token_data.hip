@@ -8,7 +8,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
-#include <numeric>
+#include <memory>
 
 #include "../kernels/common.hpp"
 #include "../runtime/error.hpp"
@@ -17,72 +17,80 @@
 namespace aic::data {
 
 // ---------------------------------------------------------------------------- dataset
-TokenDataset::TokenDataset(const std::string& path, int64_t seq_len, int64_t stride)
-    : seq_len_(seq_len), stride_(stride) {
-    AIC_CHECK(seq_len_ > 0, InvalidArgument, "seq_len must be positive, got ", seq_len_);
-    const int fd = ::open(path.c_str(), O_RDONLY);
-    AIC_CHECK(fd >= 0, IOError, "Failed to open token file: ", path);
-    struct stat st {};
-    if (::fstat(fd, &st) != 0) {
+namespace {
+
+// The whole file as a private read-only mapping; the returned pointer unmaps it when the last
+// owner lets go.
+std::shared_ptr<const int64_t> map_tokens(const std::string& path, int64_t& count) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    AIC_CHECK(fd >= 0, IOError, "cannot open the token file ", path);
+    struct stat info {};
+    const bool have_size = ::fstat(fd, &info) == 0;
+    const size_t bytes = have_size ? static_cast<size_t>(info.st_size) : 0;
+    if (!have_size || bytes % sizeof(int64_t) != 0) {
         ::close(fd);
-        AIC_THROW(IOError, "Failed to stat token file: ", path);
+        AIC_CHECK(have_size, IOError, "cannot read the size of the token file ", path);
+        AIC_THROW(InvalidArgument, "token file ", path, " holds ", bytes, " bytes, not a whole number of int64 tokens");
     }
-    map_bytes_ = static_cast<size_t>(st.st_size);
-    if (map_bytes_ % sizeof(int64_t) != 0) {
+    count = static_cast<int64_t>(bytes / sizeof(int64_t));
+    if (bytes == 0) {
         ::close(fd);
-        AIC_THROW(InvalidArgument, "File size in bytes (", map_bytes_, ") is not a multiple of sizeof(int64_t)");
+        return std::shared_ptr<const int64_t>(new int64_t[1](), std::default_delete<int64_t[]>());
     }
-    if (map_bytes_ > 0) {
-        map_ = ::mmap(nullptr, map_bytes_, PROT_READ, MAP_PRIVATE, fd, 0);
-        if (map_ == MAP_FAILED) {
-            map_ = nullptr;
-            ::close(fd);
-            AIC_THROW(IOError, "Failed to map token file: ", path);
-        }
-    }
-    ::close(fd);
-    tok_ = static_cast<const int64_t*>(map_);
-    total_ = static_cast<int64_t>(map_bytes_ / sizeof(int64_t));
-    compute_samples();
+    void* base = ::mmap(nullptr, bytes, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);  // the mapping keeps the file open
+    AIC_CHECK(base != MAP_FAILED, IOError, "cannot map the token file ", path);
+    return std::shared_ptr<const int64_t>(static_cast<const int64_t*>(base),
+                                          [bytes](const int64_t* p) { ::munmap(const_cast<int64_t*>(p), bytes); });
 }
 
-TokenDataset::TokenDataset(std::vector<int64_t> tokens, int64_t seq_len, int64_t stride)
-    : mem_(std::move(tokens)), seq_len_(seq_len), stride_(stride) {
-    AIC_CHECK(seq_len_ > 0, InvalidArgument, "seq_len must be positive, got ", seq_len_);
-    tok_ = mem_.data();
-    total_ = static_cast<int64_t>(mem_.size());
-    compute_samples();
+}  // namespace
+
+TokenDataset::TokenDataset(const std::string& path, int64_t seq_len, int64_t stride) {
+    AIC_CHECK(seq_len > 0, InvalidArgument, "window length must be positive (got ", seq_len, ")");
+    data_ = map_tokens(path, count_);
+    set_geometry(seq_len, stride);
 }
 
-TokenDataset::~TokenDataset() {
-    if (map_) ::munmap(map_, map_bytes_);
+TokenDataset::TokenDataset(std::vector<int64_t> tokens, int64_t seq_len, int64_t stride) {
+    AIC_CHECK(seq_len > 0, InvalidArgument, "window length must be positive (got ", seq_len, ")");
+    auto owner = std::make_shared<std::vector<int64_t>>(std::move(tokens));
+    count_ = static_cast<int64_t>(owner->size());
+    data_ = std::shared_ptr<const int64_t>(owner, owner->data());  // aliases the vector's storage
+    set_geometry(seq_len, stride);
 }
 
-void TokenDataset::compute_samples() {
-    if (stride_ <= 0) stride_ = seq_len_;
-    // a sample needs seq_len + 1 tokens (inputs and the next-token targets)
-    num_samples_ = total_ >= seq_len_ + 1 ? (total_ - 1 - seq_len_) / stride_ + 1 : 0;
+void TokenDataset::set_geometry(int64_t seq_len, int64_t stride) {
+    seq_len_ = seq_len;
+    stride_ = stride > 0 ? stride : seq_len;  // non-positive stride: non-overlapping windows
+    // the last window must end at or before the last token: k * stride + seq_len + 1 <= count
+    windows_ = count_ > seq_len_ ? (count_ - seq_len_ - 1) / stride_ + 1 : 0;
+}
+
+int64_t TokenDataset::window_start(int64_t idx) const {
+    AIC_CHECK(idx >= 0 && idx < windows_, OutOfRange, "window ", idx, " requested from a dataset of ", windows_);
+    return idx * stride_;
 }
 
 void TokenDataset::get_item(int64_t idx, int64_t* input, int64_t* target) const {
-    AIC_CHECK(idx >= 0 && idx < num_samples_, OutOfRange, "Dataset index ", idx, " out of range [0, ", num_samples_,
-              ")");
-    const int64_t start = idx * stride_;
-    if (input) std::memcpy(input, tok_ + start, sizeof(int64_t) * static_cast<size_t>(seq_len_));
-    if (target) std::memcpy(target, tok_ + start + 1, sizeof(int64_t) * static_cast<size_t>(seq_len_));
+    const int64_t* w = data_.get() + window_start(idx);
+    const size_t bytes = sizeof(int64_t) * static_cast<size_t>(seq_len_);
+    if (input) std::memcpy(input, w, bytes);
+    if (target) std::memcpy(target, w + 1, bytes);
 }
 
 int64_t TokenDataset::token_at(int64_t i) const {
-    AIC_CHECK(i >= 0 && i < total_, OutOfRange, "Token index ", i, " out of bounds for total tokens ", total_);
-    return tok_[i];
+    AIC_CHECK(i >= 0 && i < count_, OutOfRange, "token ", i, " requested from ", count_, " tokens");
+    return data_.get()[i];
 }
 
 void TokenDataset::write_binary_file(const std::string& path, const int64_t* tokens, int64_t n) {
-    std::FILE* f = std::fopen(path.c_str(), "wb");
-    AIC_CHECK(f, IOError, "Failed to open output binary token file: ", path);
-    const size_t w = n > 0 ? std::fwrite(tokens, sizeof(int64_t), static_cast<size_t>(n), f) : 0;
-    const int c = std::fclose(f);
-    AIC_CHECK(w == static_cast<size_t>(n > 0 ? n : 0) && c == 0, IOError, "write failed: ", path);
+    AIC_CHECK(n >= 0 && (n == 0 || tokens), InvalidArgument, "write_binary_file: bad token array");
+    std::unique_ptr<std::FILE, int (*)(std::FILE*)> f(std::fopen(path.c_str(), "wb"), &std::fclose);
+    AIC_CHECK(f != nullptr, IOError, "cannot create the token file ", path);
+    const size_t written = n > 0 ? std::fwrite(tokens, sizeof(int64_t), static_cast<size_t>(n), f.get()) : 0;
+    AIC_CHECK(written == static_cast<size_t>(n) && std::fclose(f.release()) == 0, IOError,
+              "short write to the token file ", path);
 }
 
 // ---------------------------------------------------------------------------- gather kernel
@@ -106,41 +114,41 @@ __global__ __launch_bounds__(256) void gather_windows_k(const int64_t* __restric
 // ---------------------------------------------------------------------------- loader
 TokenLoader::TokenLoader(std::shared_ptr<TokenDataset> ds, int64_t batch_size, bool shuffle, bool drop_last,
                          uint64_t seed, bool resident)
-    : ds_(std::move(ds)), batch_(batch_size), shuffle_(shuffle), drop_last_(drop_last), resident_(resident),
-      rng_(seed) {
-    AIC_CHECK(ds_ != nullptr, InvalidArgument, "DataLoader requires a valid dataset");
-    AIC_CHECK(batch_ > 0, InvalidArgument, "batch_size must be positive, got ", batch_);
+    : ds_(std::move(ds)), batch_(batch_size), shuffle_(shuffle), resident_(resident), engine_(seed) {
+    AIC_CHECK(ds_, InvalidArgument, "a loader needs a dataset");
+    AIC_CHECK(batch_ > 0, InvalidArgument, "batch size must be positive (got ", batch_, ")");
     const int64_t n = ds_->size();
-    idx_.resize(static_cast<size_t>(n));
-    std::iota(idx_.begin(), idx_.end(), int64_t{0});
-    num_batches_ = drop_last_ ? n / batch_ : (n + batch_ - 1) / batch_;
+    order_.resize(static_cast<size_t>(n));
+    for (int64_t i = 0; i < n; ++i) order_[static_cast<size_t>(i)] = i;
+    batches_ = n / batch_ + ((!drop_last && n % batch_ != 0) ? 1 : 0);
     reset();
 }
 
 TokenLoader::~TokenLoader() {
-    for (int i = 0; i < 2; ++i) {
-        if (done_[i]) {
-            (void)hipEventSynchronize(done_[i]);
-            (void)hipEventDestroy(done_[i]);
+    for (Staging& st : stage_) {
+        if (st.copied) {
+            (void)hipEventSynchronize(st.copied);
+            (void)hipEventDestroy(st.copied);
         }
-        if (pinned_[i]) (void)hipHostFree(pinned_[i]);
+        if (st.host) (void)hipHostFree(st.host);
     }
     if (dev_tokens_) (void)hipFree(dev_tokens_);
 }
 
 void TokenLoader::reset() {
-    cur_ = 0;
-    if (shuffle_ && !idx_.empty()) std::shuffle(idx_.begin(), idx_.end(), rng_);
+    next_ = 0;
+    // the next permutation of the same engine: epoch e is the e-th draw
+    if (shuffle_) std::shuffle(order_.begin(), order_.end(), engine_);
 }
 
 int64_t TokenLoader::take(std::vector<int64_t>& samples) {
-    AIC_CHECK(has_next(), OutOfRange, "DataLoader reached end of epoch (current_batch = ", cur_, ", num_batches = ",
-              num_batches_, ")");
-    const int64_t start = cur_ * batch_;
-    const int64_t b = std::min(batch_, ds_->size() - start);
-    samples.assign(idx_.begin() + start, idx_.begin() + start + b);
-    ++cur_;
-    return b;
+    AIC_CHECK(has_next(), OutOfRange, "the epoch's ", batches_, " batches are used up; reset() starts the next epoch");
+    const size_t first = static_cast<size_t>(next_ * batch_);
+    const size_t last = std::min(first + static_cast<size_t>(batch_), order_.size());
+    samples.assign(order_.begin() + static_cast<std::ptrdiff_t>(first),
+                   order_.begin() + static_cast<std::ptrdiff_t>(last));
+    ++next_;
+    return static_cast<int64_t>(last - first);
 }
 
 int64_t TokenLoader::next_host(int64_t* inputs, int64_t* targets) {
@@ -151,26 +159,28 @@ int64_t TokenLoader::next_host(int64_t* inputs, int64_t* targets) {
     return b;
 }
 
+void TokenLoader::ensure_staging(size_t elems) {
+    if (stage_elems_ >= elems) return;
+    for (Staging& st : stage_) {
+        if (st.copied) AIC_HIP_CHECK(hipEventSynchronize(st.copied));
+        if (st.host) AIC_HIP_CHECK(hipHostFree(st.host));
+        st.host = nullptr;
+        AIC_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&st.host), elems * sizeof(int64_t), hipHostMallocDefault));
+        if (!st.copied) AIC_HIP_CHECK(hipEventCreateWithFlags(&st.copied, hipEventDisableTiming));
+        st.in_flight = false;
+    }
+    stage_elems_ = elems;
+}
+
 int64_t TokenLoader::next_device(int64_t* inputs, int64_t* targets, hipStream_t s) {
     AIC_CHECK(inputs && targets, InvalidArgument, "next_device: null output");
     int dev = 0;
     AIC_HIP_CHECK(hipGetDevice(&dev));
-    AIC_CHECK(dev_ < 0 || dev_ == dev, DeviceMismatch, "DataLoader: batches go to the device of the first call");
+    AIC_CHECK(dev_ < 0 || dev_ == dev, DeviceMismatch, "a loader feeds the device of its first next_device call");
     dev_ = dev;
     const int64_t S = ds_->seq_len();
-    // staging: the sample starts (resident) or both windows (streaming), double-buffered
-    const size_t need = resident_ ? static_cast<size_t>(batch_) : static_cast<size_t>(2 * batch_ * S);
-    if (pinned_elems_ < need) {
-        for (int i = 0; i < 2; ++i) {
-            if (done_[i]) AIC_HIP_CHECK(hipEventSynchronize(done_[i]));
-            if (pinned_[i]) AIC_HIP_CHECK(hipHostFree(pinned_[i]));
-            AIC_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&pinned_[i]), need * sizeof(int64_t),
-                                        hipHostMallocDefault));
-            if (!done_[i]) AIC_HIP_CHECK(hipEventCreateWithFlags(&done_[i], hipEventDisableTiming));
-            used_[i] = false;
-        }
-        pinned_elems_ = need;
-    }
+    // staging: the window starts (resident) or both windows (streaming), double-buffered
+    ensure_staging(resident_ ? static_cast<size_t>(batch_) : static_cast<size_t>(2 * batch_ * S));
     if (resident_ && !dev_tokens_ && ds_->total_tokens() > 0) {
         const size_t bytes = sizeof(int64_t) * static_cast<size_t>(ds_->total_tokens());
         AIC_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&dev_tokens_), bytes));
@@ -178,26 +188,26 @@ int64_t TokenLoader::next_device(int64_t* inputs, int64_t* targets, hipStream_t 
     }
     std::vector<int64_t> samples;
     const int64_t b = take(samples);
-    const int k = slot_;
-    slot_ ^= 1;
-    if (used_[k]) AIC_HIP_CHECK(hipEventSynchronize(done_[k]));  // its previous copy has finished
-    int64_t* host = pinned_[k];
+    Staging& st = stage_[turn_];
+    turn_ ^= 1;
+    if (st.in_flight) AIC_HIP_CHECK(hipEventSynchronize(st.copied));  // its previous copy has finished
     if (resident_) {
-        for (int64_t i = 0; i < b; ++i) host[i] = samples[static_cast<size_t>(i)] * ds_->stride();
+        for (int64_t i = 0; i < b; ++i) st.host[i] = ds_->window_start(samples[static_cast<size_t>(i)]);
         int64_t* starts = static_cast<int64_t*>(stream_scratch(sizeof(int64_t) * static_cast<size_t>(batch_), s, 6));
-        AIC_HIP_CHECK(hipMemcpyAsync(starts, host, sizeof(int64_t) * static_cast<size_t>(b), hipMemcpyHostToDevice, s));
+        AIC_HIP_CHECK(hipMemcpyAsync(starts, st.host, sizeof(int64_t) * static_cast<size_t>(b), hipMemcpyHostToDevice,
+                                     s));
         hipLaunchKernelGGL(gather_windows_k, dim3(static_cast<unsigned>(b)), dim3(256), 0, s, dev_tokens_, starts, S,
                            inputs, targets);
         AIC_LAUNCH_CHECK("gather_windows");
     } else {
         for (int64_t i = 0; i < b; ++i)
-            ds_->get_item(samples[static_cast<size_t>(i)], host + i * S, host + (b + i) * S);
+            ds_->get_item(samples[static_cast<size_t>(i)], st.host + i * S, st.host + (b + i) * S);
         const size_t bytes = sizeof(int64_t) * static_cast<size_t>(b * S);
-        AIC_HIP_CHECK(hipMemcpyAsync(inputs, host, bytes, hipMemcpyHostToDevice, s));
-        AIC_HIP_CHECK(hipMemcpyAsync(targets, host + b * S, bytes, hipMemcpyHostToDevice, s));
+        AIC_HIP_CHECK(hipMemcpyAsync(inputs, st.host, bytes, hipMemcpyHostToDevice, s));
+        AIC_HIP_CHECK(hipMemcpyAsync(targets, st.host + b * S, bytes, hipMemcpyHostToDevice, s));
     }
-    AIC_HIP_CHECK(hipEventRecord(done_[k], s));
-    used_[k] = true;
+    AIC_HIP_CHECK(hipEventRecord(st.copied, s));
+    st.in_flight = true;
     return b;
 }
 

@@ -26,33 +26,37 @@
 
 namespace aic::data {
 
+// A sequence of int64 tokens cut into training windows: window i starts at token i * stride
+// and holds seq_len inputs followed by their next tokens as targets, so it spans seq_len + 1
+// tokens.  The tokens live in memory or in a read-only mapping of a raw little-endian int64
+// file; the storage is shared (the loader's resident copy reads it once).
 class TokenDataset {
 public:
-    TokenDataset(const std::string& path, int64_t seq_len, int64_t stride);  // int64 tokens, mapped
+    TokenDataset(const std::string& path, int64_t seq_len, int64_t stride);  // mapped file
     TokenDataset(std::vector<int64_t> tokens, int64_t seq_len, int64_t stride);
-    ~TokenDataset();
-    TokenDataset(const TokenDataset&) = delete;
-    TokenDataset& operator=(const TokenDataset&) = delete;
 
-    int64_t size() const { return num_samples_; }
+    int64_t size() const { return windows_; }
     int64_t seq_len() const { return seq_len_; }
     int64_t stride() const { return stride_; }
-    int64_t total_tokens() const { return total_; }
-    const int64_t* tokens() const { return tok_; }
-    // input / target windows of sample idx (host, seq_len each)
+    int64_t total_tokens() const { return count_; }
+    const int64_t* tokens() const { return data_.get(); }
+    // first token of window idx (checked)
+    int64_t window_start(int64_t idx) const;
+    // input / target windows of sample idx (host, seq_len each; either may be null)
     void get_item(int64_t idx, int64_t* input, int64_t* target) const;
     int64_t token_at(int64_t i) const;
     static void write_binary_file(const std::string& path, const int64_t* tokens, int64_t n);
 
 private:
-    void compute_samples();
-    void* map_ = nullptr;
-    size_t map_bytes_ = 0;
-    std::vector<int64_t> mem_;
-    const int64_t* tok_ = nullptr;
-    int64_t total_ = 0, seq_len_ = 0, stride_ = 0, num_samples_ = 0;
+    void set_geometry(int64_t seq_len, int64_t stride);
+    std::shared_ptr<const int64_t> data_;  // releases the mapping or the vector
+    int64_t count_ = 0, seq_len_ = 0, stride_ = 0, windows_ = 0;
 };
 
+// Batches of windows in epoch order: the identity, or a permutation drawn by std::shuffle from
+// one std::mt19937_64(seed) that keeps running across epochs (a new draw at construction and at
+// every reset()).  Batch k holds positions [k * batch_size, (k + 1) * batch_size) of the order;
+// a short last batch is kept unless drop_last.
 class TokenLoader {
 public:
     TokenLoader(std::shared_ptr<TokenDataset> ds, int64_t batch_size, bool shuffle, bool drop_last, uint64_t seed,
@@ -61,9 +65,9 @@ public:
     TokenLoader(const TokenLoader&) = delete;
     TokenLoader& operator=(const TokenLoader&) = delete;
 
-    int64_t num_batches() const { return num_batches_; }
+    int64_t num_batches() const { return batches_; }
     int64_t batch_size() const { return batch_; }
-    bool has_next() const { return cur_ < num_batches_; }
+    bool has_next() const { return next_ < batches_; }
     void reset();
     // Sample indices of the next batch (advances); returns the batch's size.
     int64_t take(std::vector<int64_t>& samples);
@@ -73,19 +77,21 @@ public:
     int64_t next_device(int64_t* inputs, int64_t* targets, hipStream_t s);
 
 private:
+    void ensure_staging(size_t elems);
     std::shared_ptr<TokenDataset> ds_;
-    int64_t batch_;
-    bool shuffle_, drop_last_, resident_;
-    int64_t num_batches_ = 0, cur_ = 0;
-    std::vector<int64_t> idx_;
-    std::mt19937_64 rng_;
+    int64_t batch_, batches_ = 0, next_ = 0;
+    bool shuffle_, resident_;
+    std::vector<int64_t> order_;
+    std::mt19937_64 engine_;
     int dev_ = -1;
     int64_t* dev_tokens_ = nullptr;  // resident copy
-    int64_t* pinned_[2] = {nullptr, nullptr};
-    hipEvent_t done_[2] = {nullptr, nullptr};
-    bool used_[2] = {false, false};
-    int slot_ = 0;
-    size_t pinned_elems_ = 0;
+    struct Staging {
+        int64_t* host = nullptr;  // pinned
+        hipEvent_t copied = nullptr;
+        bool in_flight = false;
+    } stage_[2];
+    int turn_ = 0;
+    size_t stage_elems_ = 0;
 };
 
 }  // namespace aic::data

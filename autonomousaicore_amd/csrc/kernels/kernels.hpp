@@ -34,6 +34,9 @@ void ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, i
 void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
             int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d, DType dt,
             hipStream_t s);
+void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                 int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
+                 DType dt, hipStream_t s);
 
 // Embedding (embedding.hip)
 void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, DType dt, hipStream_t s);

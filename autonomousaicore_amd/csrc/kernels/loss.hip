@@ -80,11 +80,27 @@ __global__ __launch_bounds__(1024) void ce_mean_k(const float* __restrict__ loss
     }
 }
 
+// Row weight of the gradient, as CrossEntropyBackward scales it (src/loss/cross_entropy.cpp:86-105):
+// per_row ("none"): grad[row] (1 without grad); otherwise grad[0] (1 without grad) divided by the
+// valid-row count -- *valid from the device when given, else the host's divisor ("mean": the
+// count, "sum": 1) -- and 0 when that count is 0.
+struct RowWeight {
+    const float* grad;
+    const int64_t* valid;
+    float divisor;
+    int per_row;
+    __device__ __forceinline__ float operator()(int64_t row) const {
+        if (per_row) return grad ? grad[row] : 1.0f;
+        const float g = grad ? *grad : 1.0f;
+        const float dv = valid ? static_cast<float>(*valid) : divisor;
+        return dv > 0.0f ? g / dv : 0.0f;
+    }
+};
+
 template <typename T, bool PRECISE>
 __global__ __launch_bounds__(256) void ce_bwd_k(const T* logits, int64_t ldl, const int64_t* __restrict__ targets,
                                                 const float* __restrict__ lse, int C, int64_t ignore_index,
-                                                const float* __restrict__ grad, const int64_t* __restrict__ valid,
-                                                T* dl, int64_t ldd) {
+                                                RowWeight rw, T* dl, int64_t ldd) {
     const int64_t row = blockIdx.x;
     const int64_t t = targets[row];
     const T* z = logits + row * ldl;
@@ -93,8 +109,7 @@ __global__ __launch_bounds__(256) void ce_bwd_k(const T* logits, int64_t ldl, co
         for (int j = threadIdx.x; j < C; j += 256) st(d, j, 0.0f);
         return;
     }
-    const int64_t v = *valid;
-    const float scale = v > 0 ? (*grad) / static_cast<float>(v) : 0.0f;
+    const float scale = rw(row);
     const float l = lse[row];
     for (int j = threadIdx.x; j < C; j += 256) {
         const float p = ex<PRECISE>(ld(z, j) - l);
@@ -145,15 +160,13 @@ __global__ __launch_bounds__(256) void ce_fwd_bf16v(const bf16* __restrict__ log
 
 __global__ __launch_bounds__(256) void ce_bwd_bf16v(const bf16* logits, int64_t ldl,
                                                     const int64_t* __restrict__ targets, const float* __restrict__ lse,
-                                                    int C, int64_t ignore_index, const float* __restrict__ grad,
-                                                    const int64_t* __restrict__ valid, bf16* dl, int64_t ldd) {
+                                                    int C, int64_t ignore_index, RowWeight rw, bf16* dl, int64_t ldd) {
     const int64_t row = blockIdx.x;
     const int64_t t = targets[row];
     const bf16* z = logits + row * ldl;
     bf16* d = dl + row * ldd;
-    const int64_t v = *valid;
     const bool ign = (t == ignore_index);
-    const float scale = (v > 0 && !ign) ? (*grad) / static_cast<float>(v) : 0.0f;
+    const float scale = ign ? 0.0f : rw(row);
     const float l = ign ? 0.0f : lse[row];
     for (int j = threadIdx.x * 8; j < C; j += 256 * 8) {
         const uint4 raw = *reinterpret_cast<const uint4*>(z + j);
@@ -208,27 +221,44 @@ void ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, i
     }
 }
 
-void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
-            int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d, DType dt,
-            hipStream_t s) {
+namespace {
+
+void ce_bwd_launch(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                   int64_t ignore_index, RowWeight w, void* dlogits, int64_t ld_d, DType dt, hipStream_t s) {
     AIC_CHECK(N >= 0 && C > 0 && ld >= C && ld_d >= C && C < (1LL << 31), InvalidArgument, "ce_bwd: bad shape");
-    AIC_CHECK(grad && valid && lse, InvalidArgument, "ce_bwd: grad, valid and lse are required");
+    AIC_CHECK(lse && targets, InvalidArgument, "ce_bwd: targets and lse are required");
     if (N == 0) return;
     const dim3 grid(static_cast<unsigned>(N));
     if (dt == DType::BFloat16 && C % 8 == 0 && ld % 8 == 0 && ld_d % 8 == 0 && a16(logits) && a16(dlogits))
         hipLaunchKernelGGL(ce_bwd_bf16v, grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld, targets, lse,
-                           static_cast<int>(C), ignore_index, grad, valid, static_cast<bf16*>(dlogits), ld_d);
+                           static_cast<int>(C), ignore_index, w, static_cast<bf16*>(dlogits), ld_d);
     else if (dt == DType::BFloat16)
         hipLaunchKernelGGL((ce_bwd_k<bf16, false>), grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld,
-                           targets, lse, static_cast<int>(C), ignore_index, grad, valid, static_cast<bf16*>(dlogits),
-                           ld_d);
+                           targets, lse, static_cast<int>(C), ignore_index, w, static_cast<bf16*>(dlogits), ld_d);
     else if (dt == DType::Float32)
         hipLaunchKernelGGL((ce_bwd_k<float, true>), grid, dim3(256), 0, s, static_cast<const float*>(logits), ld,
-                           targets, lse, static_cast<int>(C), ignore_index, grad, valid, static_cast<float*>(dlogits),
-                           ld_d);
+                           targets, lse, static_cast<int>(C), ignore_index, w, static_cast<float*>(dlogits), ld_d);
     else
         AIC_THROW(DTypeMismatch, "ce_bwd: dtype must be f32 or bf16");
     AIC_LAUNCH_CHECK("ce_bwd");
+}
+
+}  // namespace
+
+void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+            int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d, DType dt,
+            hipStream_t s) {
+    AIC_CHECK(grad && valid, InvalidArgument, "ce_bwd: grad and valid are required");
+    ce_bwd_launch(logits, ld, targets, lse, N, C, ignore_index, RowWeight{grad, valid, 0.0f, 0}, dlogits, ld_d, dt,
+                  s);
+}
+
+void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                 int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
+                 DType dt, hipStream_t s) {
+    AIC_CHECK(per_row || divisor >= 0.0f, InvalidArgument, "ce_bwd_rows: negative divisor");
+    ce_bwd_launch(logits, ld, targets, lse, N, C, ignore_index, RowWeight{grad, nullptr, divisor, per_row ? 1 : 0},
+                  dlogits, ld_d, dt, s);
 }
 
 }  // namespace aic::hip

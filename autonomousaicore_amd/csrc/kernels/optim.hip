@@ -248,28 +248,47 @@ __global__ void fill_const_k(float* dst, int64_t n, float v) {
 
 }  // namespace
 
-void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm, int* nonfinite,
-                       hipStream_t s) {
-    AIC_CHECK(count >= 0 && sqnorm && nonfinite, InvalidArgument, "grad_sqnorm_multi: bad arguments");
-    int total_blocks = 0;
-    int blocks[4096];
-    AIC_CHECK(count <= 4096, InvalidArgument, "grad_sqnorm_multi: at most 4096 tensors");
+namespace {
+
+constexpr int kMaxNormTensors = 4096;
+
+// Blocks of sqnorm_k per tensor (one fp64 partial and one flag each); returns the total.
+int64_t sqnorm_blocks(const int64_t* sizes, int count, int* blocks) {
+    int64_t total = 0;
     for (int t = 0; t < count; ++t) {
+        AIC_CHECK(sizes[t] >= 0, InvalidArgument, "grad_sqnorm_multi: negative size of tensor ", t);
         const int64_t nb = (sizes[t] + 256 * 16 - 1) / (256 * 16);
         blocks[t] = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(nb, kNormBlocks)));
-        total_blocks += blocks[t];
+        total += blocks[t];
     }
-    double* pd = static_cast<double*>(
-        stream_scratch(sizeof(double) * std::max(total_blocks, 1) + sizeof(int) * std::max(total_blocks, 1), s));
-    int* pn = reinterpret_cast<int*>(pd + std::max(total_blocks, 1));
+    return total;
+}
+
+// pd: max(total, 1) fp64 partials; pn: as many int flags.
+void sqnorm_launch(const float* const* grads, const int64_t* sizes, int count, const int* blocks, int total,
+                   double* pd, int* pn, double* sqnorm, int* nonfinite, hipStream_t s) {
     int off = 0;
     for (int t = 0; t < count; ++t) {
         hipLaunchKernelGGL(sqnorm_k, dim3(blocks[t]), dim3(256), 0, s, grads[t], sizes[t], pd + off, pn + off);
         AIC_LAUNCH_CHECK("grad_sqnorm");
         off += blocks[t];
     }
-    hipLaunchKernelGGL(sqnorm_final_k, dim3(1), dim3(1024), 0, s, pd, pn, total_blocks, sqnorm, nonfinite);
+    hipLaunchKernelGGL(sqnorm_final_k, dim3(1), dim3(1024), 0, s, pd, pn, total, sqnorm, nonfinite);
     AIC_LAUNCH_CHECK("grad_sqnorm_final");
+}
+
+}  // namespace
+
+void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm, int* nonfinite,
+                       hipStream_t s) {
+    AIC_CHECK(count >= 0 && sqnorm && nonfinite, InvalidArgument, "grad_sqnorm_multi: bad arguments");
+    AIC_CHECK(count <= kMaxNormTensors, InvalidArgument, "grad_sqnorm_multi: at most ", kMaxNormTensors, " tensors");
+    int blocks[kMaxNormTensors];
+    const int total = static_cast<int>(sqnorm_blocks(sizes, count, blocks));
+    double* pd = static_cast<double*>(
+        stream_scratch(sizeof(double) * std::max(total, 1) + sizeof(int) * std::max(total, 1), s));
+    int* pn = reinterpret_cast<int*>(pd + std::max(total, 1));
+    sqnorm_launch(grads, sizes, count, blocks, total, pd, pn, sqnorm, nonfinite, s);
 }
 
 void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s) {

@@ -113,8 +113,6 @@ void wgrad_grouped(Profiler& prof, std::initializer_list<std::array<const void*,
 
 }  // namespace
 
-namespace {
-
 // The next token from fp32 logits, as TransformerLM::generate samples it
 // (src/models/transformer_lm.cpp:113-206): argmax when temperature <= 0.001 or top_k == 1;
 // otherwise softmax(logits / temperature) (sum in double), top-k filtering (std::partial_sort
@@ -176,8 +174,6 @@ int64_t sample_token(const std::vector<float>& l, float temperature, int top_k, 
     std::discrete_distribution<int64_t> dist(p.begin(), p.end());
     return dist(rng);
 }
-
-}  // namespace
 
 TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions& opt) : cfg_(cfg), opt_(opt) {
     const int64_t V = cfg.vocab_size, d = cfg.hidden_dim, L = cfg.num_layers, H = cfg.num_heads,
@@ -460,6 +456,10 @@ void gather_host(const float* dev, const std::vector<ParamInfo>& ps, int64_t are
 }  // namespace
 
 void TransformerLM::get_params(float* host) const { gather_host(params_dev_, params_, arena_, host, stream_); }
+void TransformerLM::get_base_params(float* host) const {
+    AIC_CHECK(lora(), InvalidState, "get_base_params: the model has no frozen base (lora_rank == 0); use get_params");
+    gather_host(base_dev_, base_, base_arena_, host, stream_);
+}
 void TransformerLM::get_grads(float* host) const { gather_host(grads_dev_, params_, arena_, host, stream_); }
 
 void TransformerLM::get_adam_state(float* m, float* v, int64_t* step) const {

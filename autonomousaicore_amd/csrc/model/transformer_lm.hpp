@@ -20,6 +20,7 @@
 #include <array>
 #include <cstdint>
 #include <memory>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -90,6 +91,11 @@ struct StepStats {
     int64_t step = 0;
 };
 
+// One token drawn from fp32 logits by TransformerLM::generate's rules (greedy, temperature,
+// top-k, top-p, std::discrete_distribution over rng).
+int64_t sample_token(const std::vector<float>& logits, float temperature, int top_k, float top_p,
+                     std::mt19937_64& rng);
+
 class TransformerLM {
 public:
     TransformerLM(const TransformerLMConfig& cfg, const TrainOptions& opt);
@@ -111,6 +117,7 @@ public:
     // projections of each layer are then quantized to INT4 (QuantizedLinear::from_linear).
     void set_base_params(const float* host);
     void get_params(float* host) const;
+    void get_base_params(float* host) const;
     void get_grads(float* host) const;
     void get_adam_state(float* m, float* v, int64_t* step) const;
     void init_normal(uint64_t seed, float std, bool residual_scaling);

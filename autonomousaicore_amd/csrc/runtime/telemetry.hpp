@@ -1,15 +1,22 @@
-// Step telemetry and anomaly detection (TelemetryTracker, include/autonomous/telemetry.hpp,
-// src/autonomous/telemetry.cpp:126-275): per-step loss / gradient-norm EMAs, the rolling
-// loss variance over a window, TFLOP/s from 6 P tokens/s, host and GPU memory, and the
-// reference's anomaly rules (non-finite loss or gradient, loss divergence above 1.4x the long
-// EMA for 3 steps, gradient spikes above 4x the gradient EMA, vanishing gradients, GPU memory
-// under 8% free).  The step statistics it consumes come from the device-side step history of
-// TransformerLM, read in batches, so the training loop needs no host synchronisation per step.
+// Step telemetry and anomaly detection behind the interface of the reference's
+// TelemetryTracker (include/autonomous/telemetry.hpp; behaviour of
+// src/autonomous/telemetry.cpp:126-275).  Rules, per recorded step:
+//   * loss EMAs (short and long alpha) and a gradient-norm EMA (short alpha), each seeded by the
+//     first finite value it sees, non-finite values skipped;
+//   * the population variance of the finite losses among the last `window` steps;
+//   * TFLOP/s = 6 * parameters * tokens/s (tokens/s from total tokens / seconds when not given);
+//   * host memory from /proc/meminfo, GPU memory from hipMemGetInfo;
+//   * the anomaly, first match: non-finite loss, non-finite gradient norm, divergence (the last 3
+//     losses each above 1.4x the long EMA of their step), gradient explosion (at least 5 steps,
+//     norm above 4x its EMA, or above 100 while the EMA is ~0), vanishing gradient (at least 5
+//     steps, norm below 1e-7), GPU memory under 8% free.
+// The statistics it consumes come from the device-side step history of TransformerLM, read in
+// batches, so the training loop needs no host synchronisation per step.
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
-#include <deque>
+#include <vector>
 #include <string>
 
 namespace aic {
@@ -50,16 +57,28 @@ public:
     bool is_gradient_exploding(float spike_factor = 4.0f) const;
     bool is_gradient_vanishing(float min_norm = 1e-7f) const;
     bool is_memory_critical(float min_free_ratio = 0.08f) const;
-    size_t count() const { return history_.size(); }
+    size_t count() const { return size_; }
     const TelemetrySnapshot& latest() const { return latest_; }
     void reset();
 
 private:
-    size_t window_;
-    float a_short_, a_long_;
-    float ema_s_ = 0.0f, ema_l_ = 0.0f, gn_ema_ = 0.0f;
-    int consecutive_ = 0;
-    std::deque<TelemetrySnapshot> history_;
+    struct Ema {
+        float alpha;
+        float value = 0.0f;
+        bool seeded = false;
+        void add(float x);
+    };
+    struct Record {
+        float loss, grad_norm, loss_ema_long;
+    };
+    const Record& from_newest(size_t i) const;  // i = 0: the latest step
+    float window_loss_variance() const;
+    static float tflops(int64_t model_params, float tokens_per_sec, double step_seconds, int64_t total_tokens);
+    AnomalyType classify() const;
+
+    std::vector<Record> ring_;  // the last `window` steps
+    size_t head_ = 0, size_ = 0;
+    Ema loss_short_, loss_long_, grad_;
     TelemetrySnapshot latest_;
 };
 

@@ -163,6 +163,12 @@ class TransformerLM:
         assert flat.size == self.num_base_params
         _lib.call("aic_lm_set_base_params", self._h, flat.ctypes.data)
 
+    def get_base_params(self) -> np.ndarray:
+        """QLoRA: the frozen base model in base_layout order (fp32)."""
+        out = np.empty(self.num_base_params, np.float32)
+        _lib.call("aic_lm_get_base_params", self._h, out.ctypes.data)
+        return out
+
     def set_params(self, flat: np.ndarray) -> None:
         flat = np.ascontiguousarray(flat, np.float32)
         assert flat.size == self.num_params

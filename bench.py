@@ -91,14 +91,34 @@ def profiled_traffic(kernel_class, config):
     return None
 
 
+def host_cpu():
+    """nproc (CPUs this process may run on), online CPUs, and the CPU model name (lscpu's)."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": nproc, "online_cpus": os.cpu_count(), "model": model}
+
+
 def cpu_baseline(c, seed=1234):
     """Time the oracle on one layer at the config's widths, B=1 x S, and extrapolate to the
     full step (L layers, B sequences, all parameters in AdamW)."""
     from oracle import oracle as orc
 
     orc.build()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    threads = max(1, min(threads, 24))
+    host = host_cpu()
+    # the reference's GEMM row split: min(hardware threads, 24) (src/ops/cpu_gemm.cpp:143-146);
+    # hardware threads = the CPUs this process may run on
+    threads = max(1, min(host["nproc"], 24))
     orc.set_threads(threads)
     S = c["S"]
     E = c.get("experts", 0)
@@ -146,6 +166,10 @@ def cpu_baseline(c, seed=1234):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
+        "nproc": host["nproc"],
+        "online_cpus": host["online_cpus"],
+        "cpu_model": host["model"],
+        "thread_rule": "min(nproc, 24) GEMM threads as src/ops/cpu_gemm.cpp:143-146; elementwise ops single-threaded",
         "sample": (f"oracle fp32 step (restatement of the reference AVX2 CPU path) on 1 layer at the "
                    f"config widths, B=1 x S={S}, median of 3 after 1 warm-up ({wall:.1f} s timed); extrapolated to {c['L']} layers, "
                    f"B={c['B']} and AdamW over {full_params / 1e6:.0f}M parameters: {t_step:.1f} s/step"),

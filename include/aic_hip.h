@@ -58,6 +58,11 @@ int aic_hip_mem_free_async(void* ptr, aic_stream stream);
 /* Bytes currently allocated through the pool and the high-water mark
  * (replaces MemoryStats, include/memory/allocator.hpp:14-50). */
 int aic_hip_mem_stats(int64_t* allocated_bytes, int64_t* peak_bytes);
+/* Copy of `bytes` between any two of host and device memory, ordered on the stream, returning
+ * when it is done (hipMemcpyDefault: the direction comes from the pointers).
+ * Replaces: the reference's raw cudaMemcpy calls (e.g. src/tensor/tensor.cpp:266,320,
+ * src/cuda/cuda_loss.cu:228-234). */
+int aic_hip_memcpy_sync(void* dst, const void* src, size_t bytes, aic_stream stream);
 
 /* ---------------------------------------------------------------- GEMM ------------- */
 /* C[M,N] = alpha * op(A) . op(B) + beta * C + R  (fp32 accumulation).
@@ -172,6 +177,17 @@ int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const
                    int64_t ignore_index, const float* grad, const int64_t* valid, void* dlogits, int64_t ld_d,
                    aic_dtype dt, aic_stream stream);
 
+/* The gradient with the reference launcher's reductions (CrossEntropyBackward,
+ * src/loss/cross_entropy.cpp:86-105): dlogits[i,:] = (softmax(z_i) - onehot(t_i)) * w_i,
+ * ignored rows 0, where w_i = grad[i] for reduction "none" (per_row = 1; grad NULL: 1), and
+ * otherwise w_i = grad[0] / divisor (grad NULL: 1 / divisor; divisor 0: w_i = 0) with divisor =
+ * the host's valid-row count for "mean" and 1 for "sum".  grad is a device pointer.
+ * Replaces: cuda_cross_entropy_backward (src/cuda/cuda_loss.cuh:35-52) with its reduction
+ * string and host valid_count. */
+int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N,
+                        int64_t C, int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits,
+                        int64_t ld_d, aic_dtype dt, aic_stream stream);
+
 /* ---------------------------------------------------------------- embedding -------- */
 /* out[i,:] = W[ids[i],:] (zero row for ids outside [0, V)); W/out dtype dt.
  * Replaces: cuda_embedding_forward (src/cuda/cuda_embedding.cuh:10-18). */
@@ -214,7 +230,7 @@ typedef struct {
     int step;              /* AdamW step count; finalize increments it when the step is applied */
 } aic_optim_ctl;
 
-/* One thread: from *sqnorm/*nonfinite decide skip / backoff / growth exactly as
+/* One thread: from *sqnorm and *nonfinite decide skip / backoff / growth exactly as
  * DynamicLossScaler::unscale_and_update, then norm = sqrt(sqnorm)/scale and the clip
  * coefficient max/(norm + 1e-6) when < 1 (clip_grad_norm_), leaving grad_mult =
  * coef/scale for AdamW, and increments step unless the step is skipped.  The scale used
@@ -453,13 +469,15 @@ int aic_lm_num_tensors(const aic_lm* lm);
 int aic_lm_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims, int64_t* offset);
 /* QLoRA: the frozen base model's tensors (the dense model's names, shapes and packed order; with
  * lora_rank == 0 the same list as aic_lm_tensor_info), and setting them, after which the seven
- * projections of every layer are quantized again.  InvalidState without QLoRA.
+ * projections of every layer are quantized again; and reading them back (fp32, packed).
+ * InvalidState without QLoRA.
  * Replaces: loading the base weights before LoRAAdapter::apply (src/nn/lora.cpp:116-175). */
 int64_t aic_lm_num_base_params(const aic_lm* lm);
 int aic_lm_num_base_tensors(const aic_lm* lm);
 int aic_lm_base_tensor_info(const aic_lm* lm, int i, char* name, int name_cap, int* rank, int64_t* dims,
                             int64_t* offset);
 int aic_lm_set_base_params(aic_lm* lm, const float* host);
+int aic_lm_get_base_params(const aic_lm* lm, float* host);
 /* Host <-> device copies of the flat fp32 arenas (synchronous); with QLoRA the trainable
  * arena holds the LoRA adapters only. */
 int aic_lm_set_params(aic_lm* lm, const float* host);
@@ -495,6 +513,11 @@ int aic_lm_forward_step(aic_lm* lm, const int64_t* ids, int64_t B, int64_t S, in
                         float* logits);
 int aic_lm_generate(aic_lm* lm, const int64_t* prompt, int64_t n_prompt, int64_t max_new_tokens, float temperature,
                     int top_k, float top_p, int64_t eos_token_id, uint64_t seed, int64_t* out_tokens, int64_t* n_out);
+/* generate's sampling step on its own (host only, no GPU): n_draws tokens drawn one after
+ * another from the same fp32 logits [V] with one std::mt19937_64(seed), by the rules above.
+ * Replaces: the sampling block of TransformerLM::generate (src/models/transformer_lm.cpp:113-213). */
+int aic_sample_tokens(const float* logits, int64_t V, float temperature, int top_k, float top_p, uint64_t seed,
+                      int64_t n_draws, int64_t* out);
 /* Telemetry hooks.  aic_lm_step_history copies (synchronising once) the records of the steps
  * run since the previous call, oldest first, up to cap (*n = count; *dropped = older records
  * the ring overwrote, nullable) -- so a training loop can feed a telemetry tracker without a

@@ -486,6 +486,31 @@ void orc_ce_bwd(const float* logits, const int64_t* targets, const float* lse, i
     }
 }
 
+/* CrossEntropyBackward's row scale for the three reductions (src/loss/cross_entropy.cpp:86-105):
+ * "mean" g / valid_count (0 when no row is valid), "sum" g, "none" g[i] (1 without g). */
+void orc_ce_bwd_reduction(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                          int64_t ignore_index, int reduction, int64_t valid_count, const float* g, float* dlogits) {
+    const float g_scalar = g ? g[0] : 1.0f;
+    for (int64_t i = 0; i < N; ++i) {
+        float* gz = dlogits + i * C;
+        int64_t t = targets[i];
+        if (t == ignore_index) {
+            memset(gz, 0, sizeof(float) * (size_t)C);
+            continue;
+        }
+        float scale;
+        if (reduction == ORC_CE_MEAN) scale = valid_count > 0 ? g_scalar / (float)valid_count : 0.0f;
+        else if (reduction == ORC_CE_SUM) scale = g_scalar;
+        else scale = g ? g[i] : 1.0f;
+        const float* z = logits + i * C;
+        for (int64_t j = 0; j < C; ++j) {
+            float prob = expf(z[j] - lse[i]);
+            float ind = (j == t) ? 1.0f : 0.0f;
+            gz[j] = (prob - ind) * scale;
+        }
+    }
+}
+
 /* ======================================================================================
  * Embedding
  * ====================================================================================== */

@@ -107,6 +107,11 @@ float orc_ce_fwd(const float* logits, const int64_t* targets, int64_t N, int64_t
 /* grad = (exp(z - lse) - onehot) * g / valid (src/loss/cross_entropy.cpp:77-127). */
 void orc_ce_bwd(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
                 int64_t ignore_index, int64_t valid_count, float g, float* dlogits);
+/* The same for the reductions "mean" (g[0] / valid_count), "sum" (g[0]) and "none" (g[i]);
+ * g may be NULL (1) (src/loss/cross_entropy.cpp:86-105). */
+enum { ORC_CE_MEAN = 0, ORC_CE_SUM = 1, ORC_CE_NONE = 2 };
+void orc_ce_bwd_reduction(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
+                          int64_t ignore_index, int reduction, int64_t valid_count, const float* g, float* dlogits);
 
 /* ---- Embedding (src/nn/embedding.cpp:96-156, :26-82) ---- */
 void orc_embedding_fwd(const int64_t* ids, const float* W, float* out, int64_t N, int64_t D, int64_t V);

@@ -222,6 +222,22 @@ def ce_bwd(logits, targets, lse, valid, g=1.0, ignore_index=-100):
     return d
 
 
+CE_REDUCTIONS = {"mean": 0, "sum": 1, "none": 2}
+
+
+def ce_bwd_reduction(logits, targets, lse, valid, reduction, g=None, ignore_index=-100):
+    """orc_ce_bwd_reduction: g None (1), a scalar ("mean"/"sum") or per-row values ("none")."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, Cn = logits.shape
+    d = np.empty_like(logits)
+    gp = None if g is None else np.ascontiguousarray(np.atleast_1d(g), np.float32)
+    lib().orc_ce_bwd_reduction(_f(logits), _i(targets), _f(np.ascontiguousarray(lse, np.float32)), C.c_int64(N),
+                               C.c_int64(Cn), C.c_int64(ignore_index), C.c_int(CE_REDUCTIONS[reduction]),
+                               C.c_int64(valid), _f(gp) if gp is not None else None, _f(d))
+    return d
+
+
 def embedding_fwd(ids, W):
     ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
     W = np.ascontiguousarray(W, np.float32)

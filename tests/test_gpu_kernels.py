@@ -266,6 +266,42 @@ def test_cross_entropy(orc, dt, N, Cn):
     assert rel(host(zd), d_ref) < (1e-5 if dt == F32 else 4e-3)
 
 
+@pytest.mark.parametrize("dt", [F32, BF16])
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_cross_entropy_reductions(orc, dt, reduction):
+    """aic_hip_ce_bwd_rows: the launcher-level backward with the reference's reduction string and
+    host valid_count (cuda_loss.cuh:35-52), against orc_ce_bwd_reduction; with and without an
+    incoming gradient; an all-ignored batch ("mean" with valid_count 0) gives zeros."""
+    N, Cn = 300, 1000
+    rng = np.random.default_rng(N + Cn + len(reduction))
+    z = (2 * rng.standard_normal((N, Cn))).astype(np.float32)
+    t = rng.integers(0, Cn, N).astype(np.int64)
+    t[::5] = -100
+    if dt == BF16:
+        z = bf16_round(z)
+    tdt = torch.float32 if dt == F32 else torch.bfloat16
+    _, _, lse_ref, valid_ref = orc.ce_fwd(z, t)
+    zd, td, lsed = dev(z, tdt), dev(t), dev(lse_ref)
+    g = rng.standard_normal(N).astype(np.float32) if reduction == "none" else np.float32([0.75])
+    tol = 1e-5 if dt == F32 else 4e-3
+    per_row = 1 if reduction == "none" else 0
+    divisor = float(valid_ref) if reduction == "mean" else 1.0
+    for gg in (g, None):
+        d = torch.empty_like(zd)
+        gd = dev(gg) if gg is not None else None
+        call("aic_hip_ce_bwd_rows", ptr(zd), Cn, ptr(td), ptr(lsed), N, Cn, -100, ptr(gd), per_row, divisor, ptr(d),
+             Cn, dt, stream())
+        ref = orc.ce_bwd_reduction(z, t, lse_ref, valid_ref, reduction, gg)
+        assert rel(host(d), ref) < tol
+        assert np.all(host(d)[t == -100] == 0)
+    if reduction == "mean":
+        ti = np.full(N, -100, np.int64)
+        d = torch.full_like(zd, 7.0)
+        call("aic_hip_ce_bwd_rows", ptr(zd), Cn, ptr(dev(ti)), ptr(lsed), N, Cn, -100, None, 0, 0.0, ptr(d), Cn, dt,
+             stream())
+        assert not host(d).any()
+
+
 # ----------------------------------------------------------------------------- embedding
 @pytest.mark.parametrize("dt", [F32, BF16])
 @pytest.mark.parametrize("V,D,N", [(1000, 136, 4096), (1500, 1024, 8192), (32000, 2048, 2048)])
@@ -304,53 +340,59 @@ def test_embedding_gather_bit_exact_and_scatter(orc, dt, V, D, N):
 
 
 # ----------------------------------------------------------------------------- attention
-@pytest.mark.parametrize("B,S,H,hd", [(2, 64, 4, 32), (1, 100, 2, 64), (1, 128, 2, 16), (1, 96, 2, 128)])
-def test_attention_fp32_matches_oracle(orc, B, S, H, hd):
+@pytest.mark.parametrize("B,S,H,hd,causal", [(2, 64, 4, 32, 1), (1, 100, 2, 64, 1), (1, 128, 2, 16, 1),
+                                               (1, 96, 2, 128, 1), (2, 100, 2, 64, 0), (1, 77, 3, 128, 0)])
+def test_attention_fp32_matches_oracle(orc, B, S, H, hd, causal):
+    """causal = 0 is the reference launcher's is_causal = false (cuda_flash_attention.cuh:12-46)."""
     rng = np.random.default_rng(S * hd)
     d = H * hd
     qkv = rng.standard_normal((B * S, 3 * d)).astype(np.float32)
     q, k, v = (np.ascontiguousarray(qkv[:, i * d:(i + 1) * d]) for i in range(3))
     do = rng.standard_normal((B * S, d)).astype(np.float32)
-    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd)
+    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd, causal=bool(causal))
     dq_ref, dk_ref, dv_ref = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
     x = dev(qkv)
     o = torch.empty((B * S, d), dtype=torch.float32, device="cuda")
     lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
     sc = 1.0 / np.sqrt(hd)
-    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 4 * d, ptr(x) + 8 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, 1, sc,
-         F32, stream())
+    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 4 * d, ptr(x) + 8 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, causal,
+         sc, F32, stream())
     assert rel(host(o), o_ref) < 1e-5
     dqkv = torch.empty_like(x)
     dod = dev(do)
     call("aic_hip_attn_bwd", ptr(x), ptr(x) + 4 * d, ptr(x) + 8 * d, 3 * d, ptr(o), ptr(dod), d, ptr(lse),
-         ptr(dqkv), ptr(dqkv) + 4 * d, ptr(dqkv) + 8 * d, 3 * d, B, H, S, hd, 1, sc, F32, stream())
+         ptr(dqkv), ptr(dqkv) + 4 * d, ptr(dqkv) + 8 * d, 3 * d, B, H, S, hd, causal, sc, F32, stream())
     g = host(dqkv)
     assert rel(g[:, :d], dq_ref) < 1e-4
     assert rel(g[:, d:2 * d], dk_ref) < 1e-4
     assert rel(g[:, 2 * d:], dv_ref) < 1e-4
 
 
-@pytest.mark.parametrize("B,S,H,hd", [(1, 256, 2, 128), (2, 192, 3, 64), (1, 1024, 2, 128), (1, 72, 1, 64)])
-def test_attention_bf16_mfma(orc, B, S, H, hd):
+# (1, 2048, 2, 128): the 1B configuration's sequence and head width; causal = 0 with S not a
+# multiple of the 128-row tiles
+@pytest.mark.parametrize("B,S,H,hd,causal", [(1, 256, 2, 128, 1), (2, 192, 3, 64, 1), (1, 1024, 2, 128, 1),
+                                               (1, 72, 1, 64, 1), (1, 2048, 2, 128, 1), (2, 200, 2, 128, 0),
+                                               (1, 333, 2, 64, 0)])
+def test_attention_bf16_mfma(orc, B, S, H, hd, causal):
     rng = np.random.default_rng(S + hd + H)
     d = H * hd
     qkv = bf16_round(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
     do = bf16_round(rng.standard_normal((B * S, d)).astype(np.float32))
     q, k, v = (np.ascontiguousarray(qkv[:, i * d:(i + 1) * d]) for i in range(3))
-    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd)
+    o_ref, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd, causal=bool(causal))
     dq_ref, dk_ref, dv_ref = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
     x = dev(qkv, torch.bfloat16)
     o = torch.empty((B * S, d), dtype=torch.bfloat16, device="cuda")
     lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
     sc = 1.0 / np.sqrt(hd)
-    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, 1, sc,
-         BF16, stream())
+    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, causal,
+         sc, BF16, stream())
     # bf16 P and a bf16 output: errors at the bf16 rounding level
     assert rel(host(o), o_ref) < 1e-2
     dqkv = torch.empty_like(x)
     dod = dev(do, torch.bfloat16)
     call("aic_hip_attn_bwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
-         ptr(lse), ptr(dqkv), ptr(dqkv) + 2 * d, ptr(dqkv) + 4 * d, 3 * d, B, H, S, hd, 1, sc, BF16, stream())
+         ptr(lse), ptr(dqkv), ptr(dqkv) + 2 * d, ptr(dqkv) + 4 * d, 3 * d, B, H, S, hd, causal, sc, BF16, stream())
     g = host(dqkv)
     assert rel(g[:, :d], dq_ref) < 2e-2
     assert rel(g[:, d:2 * d], dk_ref) < 2e-2
@@ -358,7 +400,7 @@ def test_attention_bf16_mfma(orc, B, S, H, hd):
     # deterministic backward
     dqkv2 = torch.empty_like(x)
     call("aic_hip_attn_bwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
-         ptr(lse), ptr(dqkv2), ptr(dqkv2) + 2 * d, ptr(dqkv2) + 4 * d, 3 * d, B, H, S, hd, 1, sc, BF16, stream())
+         ptr(lse), ptr(dqkv2), ptr(dqkv2) + 2 * d, ptr(dqkv2) + 4 * d, 3 * d, B, H, S, hd, causal, sc, BF16, stream())
     np.testing.assert_array_equal(host(dqkv2), g)
 
 

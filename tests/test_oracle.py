@@ -211,6 +211,32 @@ def test_ce_vs_torch(orc):
     assert rel(orc.ce_bwd(z, t, lse, valid, g=2.0), zt.grad.numpy()) < 1e-6
 
 
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_ce_reductions_vs_torch(orc, reduction):
+    """The reductions of CrossEntropyBackward (src/loss/cross_entropy.cpp:86-105) against torch
+    float64 autograd of F.cross_entropy with the same reduction and incoming gradient."""
+    rng = np.random.default_rng(12)
+    z = (2 * rng.standard_normal((33, 50))).astype(np.float32)
+    t = rng.integers(0, 50, 33)
+    t[[0, 9, 10]] = -100
+    zt = torch.tensor(z, dtype=torch.float64, requires_grad=True)
+    lt = F.cross_entropy(zt, torch.tensor(t), ignore_index=-100, reduction=reduction)
+    g = rng.standard_normal(33).astype(np.float32) if reduction == "none" else np.float32(-1.5)
+    lt.backward(torch.tensor(g, dtype=torch.float64))
+    _, _, lse, valid = orc.ce_fwd(z, t)
+    d = orc.ce_bwd_reduction(z, t, lse, valid, reduction, g)
+    assert rel(d, zt.grad.numpy()) < 1e-6
+    assert np.all(d[[0, 9, 10]] == 0)
+    # mean with g equals the existing mean backward; sum = mean * valid; no g means g = 1
+    if reduction == "mean":
+        np.testing.assert_array_equal(d, orc.ce_bwd(z, t, lse, valid, g=-1.5))
+    if reduction == "sum":
+        assert rel(d, orc.ce_bwd(z, t, lse, valid, g=-1.5) * valid) < 1e-6
+    if reduction == "none":
+        ones = orc.ce_bwd_reduction(z, t, lse, valid, "none")
+        assert rel(ones, orc.ce_bwd(z, t, lse, valid, g=float(valid))) < 1e-6
+
+
 # --------------------------------------------------------------------------- embedding
 def test_embedding_known_answer(orc):
     # tests/unit/test_model.cpp:15-48
