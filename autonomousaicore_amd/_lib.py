@@ -97,6 +97,7 @@ SIGNATURES = {
     "aic_hip_embed_fwd": (i32, [vp, i64, vp, i64, i64, vp, i32, vp]),
     "aic_hip_embed_bwd": (i32, [vp, i64, vp, i64, i64, vp, i32, i32, vp]),
     "aic_hip_grad_sqnorm_multi": (i32, [C.POINTER(vp), i64p, i32, vp, vp, vp]),
+    "aic_hip_grad_sqnorm_multi_noalloc": (i32, [C.POINTER(vp), i64p, i32, vp, vp, vp]),
     "aic_hip_scale_multi": (i32, [C.POINTER(vp), i64p, i32, vp, vp]),
     "aic_hip_optim_finalize": (i32, [vp, vp, vp, vp]),
     "aic_hip_adamw_multi": (i32, [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i64p,

@@ -298,6 +298,11 @@ int aic_hip_grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, i
     return guard([&] { aic::hip::grad_sqnorm_multi(grads, sizes, count, sqnorm, nonfinite, st(stream)); });
 }
 
+int aic_hip_grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                                      int* nonfinite, aic_stream stream) {
+    return guard([&] { aic::hip::grad_sqnorm_multi_noalloc(grads, sizes, count, sqnorm, nonfinite, st(stream)); });
+}
+
 int aic_hip_scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, aic_stream stream) {
     return guard([&] { aic::hip::scale_multi(grads, sizes, count, scale, st(stream)); });
 }

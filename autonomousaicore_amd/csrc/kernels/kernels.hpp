@@ -105,6 +105,8 @@ void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int
 struct OptimCtl;  // = aic_optim_ctl (include/aic_hip.h)
 void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm, int* nonfinite,
                        hipStream_t s);
+void grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                               int* nonfinite, hipStream_t s);
 void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s);
 void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipStream_t s);
 void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,

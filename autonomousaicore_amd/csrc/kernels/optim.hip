@@ -9,6 +9,7 @@
 // one launch per parameter).  No host synchronisation is needed between backward and the
 // update.
 #include <cmath>
+#include <mutex>
 
 #include "../../../include/aic_hip.h"
 #include "common.hpp"
@@ -289,6 +290,55 @@ void grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int coun
         stream_scratch(sizeof(double) * std::max(total, 1) + sizeof(int) * std::max(total, 1), s));
     int* pn = reinterpret_cast<int*>(pd + std::max(total, 1));
     sqnorm_launch(grads, sizes, count, blocks, total, pd, pn, sqnorm, nonfinite, s);
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free grad_sqnorm_multi.  The per-block partials live in `scratch`, a file-scope
+// device array (each device holds its own copy until the process ends): fp64 partials in
+// the first kNoAllocMaxBlocks slots, then the int non-finite flags.  Host code never passes
+// the array's name to a kernel (on the host it is only a stand-in for the symbol); the
+// device address comes from hipGetSymbolAddress, once per device, on the first call with
+// that device current.  Every block overwrites its own partial, so nothing has to be
+// cleared between calls; calls that overlap on one device race on the array.
+// ---------------------------------------------------------------------------------------
+constexpr int64_t kNoAllocMaxBlocks = int64_t{1} << 17;  // 1.5 MiB in total
+static __device__ __align__(256) double scratch[kNoAllocMaxBlocks + kNoAllocMaxBlocks / 2];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+double* device_scratch() {
+    int dev = 0;
+    AIC_HIP_CHECK(hipGetDevice(&dev));
+    AIC_CHECK(dev >= 0 && dev < kMaxDevices, InvalidArgument, "grad_sqnorm_multi_noalloc: device ", dev,
+              " beyond the ", kMaxDevices, " supported");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        AIC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        AIC_CHECK(p != nullptr, HipError, "grad_sqnorm_multi_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    return static_cast<double*>(g_scratch_ptr[dev]);
+}
+
+}  // namespace
+
+void grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                               int* nonfinite, hipStream_t s) {
+    AIC_CHECK(count >= 0 && sqnorm && nonfinite, InvalidArgument, "grad_sqnorm_multi_noalloc: bad arguments");
+    AIC_CHECK(count <= kMaxNormTensors, InvalidArgument, "grad_sqnorm_multi_noalloc: at most ", kMaxNormTensors,
+              " tensors");
+    int blocks[kMaxNormTensors];
+    const int64_t total = sqnorm_blocks(sizes, count, blocks);
+    AIC_CHECK(total <= kNoAllocMaxBlocks, OutOfRange, "grad_sqnorm_multi_noalloc: the tensors need ", total,
+              " partial blocks (min(ceil(n / 4096), 1024) each), above the fixed scratch of ", kNoAllocMaxBlocks);
+    double* pd = device_scratch();
+    int* pn = reinterpret_cast<int*>(pd + kNoAllocMaxBlocks);
+    sqnorm_launch(grads, sizes, count, blocks, static_cast<int>(total), pd, pn, sqnorm, nonfinite, s);
 }
 
 void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s) {

@@ -208,6 +208,17 @@ int aic_hip_embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V
  * (src/optim/clip_grad.cpp:33-37) and launch_has_nan_or_inf_gpu (src/train/amp.cpp:12-15). */
 int aic_hip_grad_sqnorm_multi(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
                               int* nonfinite, aic_stream stream);
+/* aic_hip_grad_sqnorm_multi without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving or training loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments and results, bit for bit;
+ * the fp64 partials live in a fixed per-device array of the library (1.5 MiB, held until
+ * the process ends) instead of allocated scratch.  Limit: the tensors' partial blocks,
+ * min(ceil(n / 4096), 1024) per tensor, may total at most 131072 (e.g. 128 tensors of
+ * 4 M elements or more); beyond that it returns OutOfRange and launches nothing.  Every call
+ * on one device shares the array, so calls that overlap in time on one device (other
+ * streams, other threads) race; calls ordered on one stream do not. */
+int aic_hip_grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, int count, double* sqnorm,
+                                      int* nonfinite, aic_stream stream);
 /* grads[i] *= (*scale) for every buffer (device scalar).
  * Replaces: launch_unscale_gpu (src/train/amp.cpp:12-15) and mul_ of clip_grad_norm_
  * (src/optim/clip_grad.cpp:45-50). */
