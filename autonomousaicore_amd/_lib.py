@@ -77,6 +77,7 @@ SIGNATURES = {
     "aic_hip_mem_alloc_async": (i32, [C.POINTER(vp), C.c_size_t, vp]),
     "aic_hip_mem_free_async": (i32, [vp, vp]),
     "aic_hip_mem_stats": (i32, [i64p, i64p]),
+    "aic_hip_mem_release_stream": (i32, [vp]),
     "aic_hip_gemm": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp, i64, i32, i32, vp]),
     "aic_hip_gemm_grouped": (i32, [i32, C.POINTER(GemmDesc), f32, f32, i32, i32, vp]),
     "aic_hip_gemm_lowrank": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32,

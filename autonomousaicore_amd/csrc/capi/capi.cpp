@@ -126,6 +126,8 @@ int aic_hip_mem_alloc_async(void** ptr, size_t bytes, aic_stream stream) {
 
 int aic_hip_mem_free_async(void* ptr, aic_stream stream) { return guard([&] { aic::pool_free(ptr, st(stream)); }); }
 
+int aic_hip_mem_release_stream(aic_stream stream) { return guard([&] { aic::stream_scratch_release(st(stream)); }); }
+
 int aic_hip_mem_stats(int64_t* allocated_bytes, int64_t* peak_bytes) {
     return guard([&] {
         const aic::MemoryStats s = aic::pool_stats();

@@ -25,9 +25,14 @@ constexpr int kWave = 64;
 // non-NaN input; a NaN stays a NaN.
 __device__ __forceinline__ bf16 f2bf(float f) { return static_cast<bf16>(f); }
 __device__ __forceinline__ uint16_t f2bf_bits(float f) { return __builtin_bit_cast(uint16_t, f2bf(f)); }
-// Two floats -> packed bf16 pair (low half = a).
+// Two floats -> packed bf16 pair (low half = a), the same conversion as f2bf: one
+// v_cvt_pk_bf16_f32 with both sources (converting the halves one at a time costs a shift and an
+// or on top).
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return static_cast<uint32_t>(f2bf_bits(a)) | (static_cast<uint32_t>(f2bf_bits(b)) << 16);
+    const f32x2_v v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 __device__ __forceinline__ float bf2f(bf16 h) {
     return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);

@@ -151,6 +151,17 @@ bool gemm_mfma_eligible(const GemmArgs& a) {
     return true;
 }
 
+bool gemm_q4_eligible(const GemmArgs& a) {
+    if (!a.Bq || !a.Bscale || a.ab != DType::BFloat16 || a.transA) return false;
+    if (a.K <= 0 || a.K % 64 || a.M < 8 || a.N < 8 || a.lda % 8 || !aligned16(a.A) || !aligned16(a.Bq)) return false;
+    if (a.scale_t != DType::Float16 || reinterpret_cast<uintptr_t>(a.Bscale) % 4) return false;
+    if (a.group <= 0 || a.group % 64 || a.group >= (int64_t{1} << 31) || a.ldb % 64) return false;
+    if (!a.transB && (a.N % 64 || a.ldb < a.N)) return false;
+    if (a.transB && a.ldb < a.K) return false;
+    const int64_t rows = a.transB ? a.N : a.K;
+    return rows * a.ldb / 64 < (int64_t{1} << 32);
+}
+
 bool gemm_dma_eligible(const GemmArgs& a) {
     if (!gemm_mfma_eligible(a)) return false;
     if (a.K % 64 || a.M < 8 || a.N < 8) return false;
@@ -202,10 +213,44 @@ void rank_term_separately(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+// The product with an INT4 B operand; tile size as for the bf16 operands (two stages on both),
+// never split along K.
+void gemm_q4(const GemmArgs& a, hipStream_t s) {
+    AIC_CHECK(gemm_q4_eligible(a), InvalidArgument,
+              "INT4 GEMM: unsupported shape or layout (bf16 A, K % 64, group % 64, ldb % 64, N % 64 for dy W)");
+    const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    const bool big = t256 >= 128;
+    if (a.r2 > 0) {
+        const int64_t bn = big ? 256 : 128;
+        const bool tail = a.r2 % 8 == 0 && a.ldx2 % 8 == 0 && aligned16(a.X2) &&
+                          (a.y2_kmajor || (a.ldy2 % 8 == 0 && aligned16(a.Y2))) && (a.seg_n == 0 || a.seg_n % bn == 0);
+        if (!tail) {
+            GemmArgs b = a;
+            b.r2 = 0;
+            gemm_q4(b, s);
+            rank_term_separately(a, s);
+            return;
+        }
+    }
+    if (a.c == DType::Float32) {
+        if (big) a.transB ? gemm_impl::launch_dma_q4<256, 256, 64, 2, true, float>(a, s)
+                          : gemm_impl::launch_dma_q4<256, 256, 64, 2, false, float>(a, s);
+        else a.transB ? gemm_impl::launch_dma_q4<128, 128, 64, 2, true, float>(a, s)
+                      : gemm_impl::launch_dma_q4<128, 128, 64, 2, false, float>(a, s);
+    } else {
+        if (big) a.transB ? gemm_impl::launch_dma_q4<256, 256, 64, 2, true, bf16>(a, s)
+                          : gemm_impl::launch_dma_q4<256, 256, 64, 2, false, bf16>(a, s);
+        else a.transB ? gemm_impl::launch_dma_q4<128, 128, 64, 2, true, bf16>(a, s)
+                      : gemm_impl::launch_dma_q4<128, 128, 64, 2, false, bf16>(a, s);
+    }
+}
+}  // namespace
+
 void gemm(const GemmArgs& a, hipStream_t s) {
     AIC_CHECK(a.M >= 0 && a.N >= 0 && a.K >= 0, InvalidArgument, "negative GEMM size");
     AIC_CHECK(a.M < (1LL << 31) && a.N < (1LL << 31) && a.K < (1LL << 31), InvalidArgument, "GEMM size too large");
-    AIC_CHECK(a.A && a.B && a.C, InvalidArgument, "null GEMM operand");
+    AIC_CHECK(a.A && (a.B || a.Bq) && a.C, InvalidArgument, "null GEMM operand");
     AIC_CHECK(a.ab == DType::Float32 || a.ab == DType::BFloat16, DTypeMismatch, "GEMM inputs must be f32 or bf16");
     AIC_CHECK(a.c == DType::Float32 || a.c == DType::BFloat16, DTypeMismatch, "GEMM output must be f32 or bf16");
     const int64_t amin = a.transA ? a.M : a.K, bmin = a.transB ? a.K : a.N;
@@ -220,6 +265,10 @@ void gemm(const GemmArgs& a, hipStream_t s) {
                   "low-rank term: leading dimension smaller than the row length");
     }
     if (a.M == 0 || a.N == 0) return;
+    if (a.Bq) {
+        gemm_q4(a, s);
+        return;
+    }
     if (gemm_dma_eligible(a)) {
         // 256x256 tiles from half a round of tiles up (measured on the 1B shapes: 176 tiles of
         // 256x256 beat 704 of 128x128 by 24%); between 32 and 128 of them over a long K, 256x256

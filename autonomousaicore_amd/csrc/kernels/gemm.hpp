@@ -38,9 +38,24 @@ struct GemmArgs {
     const void* Y2 = nullptr;
     int64_t ldx2 = 0, ldy2 = 0, r2 = 0, seg_n = 0;
     int y2_kmajor = 0;
+    // Optional INT4 B operand (the QLoRA base weight; B is then ignored).  The weight is
+    // contiguous with row length ldb: W [N][ldb] when transB (the Linear forward x W^T), W [K][ldb]
+    // otherwise (the input gradient dy W).  Bq holds its symmetric INT4 values two per byte
+    // (element 2i in the low nibble of byte i), Bscale one scale (scale_t: f16 or f32) per `group`
+    // consecutive elements of its flat row-major index; op(B) = q * scale, rounded to bf16 as
+    // the standalone dequantization does, inside the kernel (gemm_q4_eligible lists the shapes).
+    const uint8_t* Bq = nullptr;
+    const void* Bscale = nullptr;
+    DType scale_t = DType::Float16;
+    int64_t group = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);
+// The INT4 B operand in the kernel: bf16 A (not transposed, lda % 8, 16-byte aligned), K a
+// positive multiple of 64, M and N >= 8, fp16 scales (4-byte aligned base), group % 64 == 0,
+// ldb % 64 == 0, Bq 16-byte aligned, N a multiple of 64 for the input-gradient layout, fewer
+// than 2^38 weight elements.
+bool gemm_q4_eligible(const GemmArgs& a);
 bool gemm_dma_eligible(const GemmArgs& a);
 void gemm(const GemmArgs& a, hipStream_t stream);
 // Independent products in one launch when they share the kernel configuration (transposes,

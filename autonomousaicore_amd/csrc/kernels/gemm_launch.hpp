@@ -22,6 +22,9 @@ void launch_dma(const GemmArgs& a, hipStream_t s, int splits = 1, float* part = 
 // Up to kMaxGroups products of one configuration in one grid.
 template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
 void launch_dma_grouped(const GemmArgs* a, int n, hipStream_t s);
+// The product with an INT4 B operand (GemmArgs::Bq), TB = a.transB.
+template <int BM, int BN, int BK, int S, bool TB, typename CT>
+void launch_dma_q4(const GemmArgs& a, hipStream_t s);
 // Expert-ragged products (gemm_ragged).
 template <int BM, int BN, int BK, int S, bool TA, bool TB, typename CT>
 void launch_dma_ragged(const RaggedArgs& r, hipStream_t s);

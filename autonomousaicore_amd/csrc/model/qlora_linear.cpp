@@ -32,6 +32,37 @@ void gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const vo
     hip::gemm(a, s);
 }
 
+// The product C = alpha X op(deq(Wq)) + beta C + R with the INT4 weight dequantized inside the
+// GEMM kernel (GemmArgs::Bq), when the kernel takes the shape.
+bool fused_q4(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx, const uint8_t* Wq,
+              const void* scales, DType scale_t, int64_t group, float beta, void* C, int64_t ldc, const void* R,
+              int64_t ldr, DType ab, DType c, hipStream_t s) {
+    hip::GemmArgs a;
+    a.transA = 0;
+    a.transB = transW ? 1 : 0;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = alpha;
+    a.A = X;
+    a.lda = ldx;
+    a.ldb = transW ? K : N;
+    a.beta = beta;
+    a.C = C;
+    a.ldc = ldc;
+    a.R = R;
+    a.ldr = ldr;
+    a.ab = ab;
+    a.c = c;
+    a.Bq = Wq;
+    a.Bscale = scales;
+    a.scale_t = scale_t;
+    a.group = hip::int4_group(N * K, group);
+    if (!hip::gemm_q4_eligible(a)) return false;
+    hip::gemm(a, s);
+    return true;
+}
+
 void check_dt(DType ab, DType c, DType scale_t) {
     AIC_CHECK(ab == DType::Float32 || ab == DType::BFloat16, DTypeMismatch, "int4 GEMM: operands must be f32 or bf16");
     AIC_CHECK(c == DType::Float32 || c == DType::BFloat16, DTypeMismatch, "int4 GEMM: output must be f32 or bf16");
@@ -47,6 +78,8 @@ void int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha,
     AIC_CHECK(M >= 0 && N >= 0 && K >= 0, InvalidArgument, "int4_dequant_gemm: negative size");
     if (M == 0 || N == 0) return;
     AIC_CHECK(X && Wq && scales && C, InvalidArgument, "int4_dequant_gemm: null pointer");
+    if (fused_q4(transW, M, N, K, alpha, X, ldx, Wq, scales, scale_t, group, beta, C, ldc, R, ldr, ab, c, s)) return;
+    // other shapes and fp32 operands: the weight dequantized into a pool buffer first
     DeviceBuffer w(dtype_size(ab) * static_cast<size_t>(N * K > 0 ? N * K : 1), s);
     hip::int4_dequant(Wq, scales, scale_t, N * K, group, w.get(), ab, s);
     gemm(0, transW ? 1 : 0, M, N, K, alpha, X, ldx, w.get(), transW ? K : N, beta, C, ldc, ab, c, s, R, ldr);
@@ -68,9 +101,8 @@ void QLoRALinear::forward(const void* x, int64_t T, const uint8_t* Wq, const voi
     x_ = x;
     A_ = A;
     B_ = B;
-    // the dequantized base weight is kept for the input gradient of backward
-    w_ = DeviceBuffer(es * static_cast<size_t>(out_ * in_), s);
-    hip::int4_dequant(Wq, scales, scale_t_, out_ * in_, group_, w_.get(), dt_, s);
+    Wq_ = Wq;
+    scales_ = scales;
     float beta = 0.0f;
     if (rank_ > 0) {
         xa_ = DeviceBuffer(es * static_cast<size_t>(T * rank_), s);
@@ -78,11 +110,12 @@ void QLoRALinear::forward(const void* x, int64_t T, const uint8_t* Wq, const voi
         gemm(0, 1, T, out_, rank_, scaling(), xa_.get(), rank_, B, rank_, 0.0f, y, out_, dt_, dt_, s);  // * B^T * s
         beta = 1.0f;
     }
-    gemm(0, 1, T, out_, in_, 1.0f, x, in_, w_.get(), in_, beta, y, out_, dt_, dt_, s, R, out_);  // + x W^T (+ R)
+    int4_dequant_gemm(1, T, out_, in_, 1.0f, x, in_, Wq, scales, scale_t_, group_, beta, y, out_, R, out_, dt_, dt_,
+                      s);  // + x deq(Wq)^T (+ R)
 }
 
 void QLoRALinear::backward(const void* dy, void* dx, float* dA, float* dB, bool accumulate, hipStream_t s) {
-    AIC_CHECK(dy && T_ > 0 && w_.get(), InvalidArgument, "QLoRALinear::backward: no forward to differentiate");
+    AIC_CHECK(dy && T_ > 0 && Wq_, InvalidArgument, "QLoRALinear::backward: no forward to differentiate");
     AIC_CHECK(rank_ == 0 || (dA && dB), InvalidArgument, "QLoRALinear::backward: null adapter gradient");
     const float acc = accumulate ? 1.0f : 0.0f;
     float beta = 0.0f;
@@ -95,7 +128,9 @@ void QLoRALinear::backward(const void* dy, void* dx, float* dA, float* dB, bool 
         if (dx) gemm(0, 0, T_, in_, rank_, 1.0f, dxa.get(), rank_, A_, in_, 0.0f, dx, in_, dt_, dt_, s);     // dxa A
         beta = 1.0f;
     }
-    if (dx) gemm(0, 0, T_, in_, out_, 1.0f, dy, out_, w_.get(), in_, beta, dx, in_, dt_, dt_, s);  // + dy W
+    if (dx)
+        int4_dequant_gemm(0, T_, in_, out_, 1.0f, dy, out_, Wq_, scales_, scale_t_, group_, beta, dx, in_, nullptr, 0,
+                          dt_, dt_, s);  // + dy deq(Wq)
 }
 
 }  // namespace aic::models

@@ -14,9 +14,12 @@
 
 namespace aic::models {
 
-// C[M,N] = alpha * X . op(deq(Wq)) + beta * C + R with the weight dequantized on the device into
-// a pool buffer of the GEMM operand type `ab`.  transW = 1: Wq holds W [N, K] (forward, x W^T);
-// transW = 0: Wq holds W [K, N] (input gradient, dy W).  Groups run along W's flat row-major index.
+// C[M,N] = alpha * X . op(deq(Wq)) + beta * C + R.  transW = 1: Wq holds W [N, K] (forward,
+// x W^T); transW = 0: Wq holds W [K, N] (input gradient, dy W).  Groups run along W's flat
+// row-major index.  bf16 operands in the shapes the GEMM kernel takes (K % 64, group % 64, the
+// weight's row length % 64, N % 64 for dy W): dequantized inside the GEMM's operand load.
+// Otherwise (fp32 operands, other shapes) the weight is dequantized into a pool buffer of the
+// operand type first.  Either way op(B) holds bf16(q * scale) (fp32 operands: q * scale).
 void int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx,
                        const uint8_t* Wq, const void* scales, DType scale_t, int64_t group, float beta, void* C,
                        int64_t ldc, const void* R, int64_t ldr, DType ab, DType c, hipStream_t s);
@@ -44,7 +47,9 @@ private:
     const void* x_ = nullptr;
     const void* A_ = nullptr;
     const void* B_ = nullptr;
-    DeviceBuffer w_, xa_;
+    const uint8_t* Wq_ = nullptr;  // the frozen base, read again (dequantized) by backward
+    const void* scales_ = nullptr;
+    DeviceBuffer xa_;
 };
 
 }  // namespace aic::models

@@ -44,13 +44,23 @@ struct LowRank {
     int y2_kmajor;
 };
 
+// A QLoRA base projection (stack) as the GEMM's B operand: packed INT4 values and fp16 group
+// scales, dequantized inside the GEMM (packed == nullptr: none; B is the dense operand).
+struct Q4B {
+    const uint8_t* packed = nullptr;
+    const void* scales = nullptr;
+    int64_t group = 0;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
-          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr) {
+          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {}) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
+    // INT4 operand: half a byte per weight plus one fp16 scale per group
+    const double bbytes = q4.packed ? 0.5 * N * K + 2.0 * N * K / static_cast<double>(q4.group) : es * N * K;
     auto scope = prof.scope(ta ? kGemmWgrad : (tb ? kGemmFwd : kGemmDgrad), 2.0 * M * N * (K + kr),
-                            es * (M * K + N * K) + ec * M * N * (R ? 2 : 1), s);
+                            es * M * K + bbytes + ec * M * N * (R ? 2 : 1), s);
     hip::GemmArgs a;
     a.transA = ta;
     a.transB = tb;
@@ -77,6 +87,13 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.r2 = lr->r2;
         a.seg_n = lr->seg_n;
         a.y2_kmajor = lr->y2_kmajor;
+    }
+    if (q4.packed) {
+        a.B = nullptr;
+        a.Bq = q4.packed;
+        a.Bscale = q4.scales;
+        a.scale_t = DType::Float16;
+        a.group = q4.group;
     }
     hip::gemm(a, s);
 }
@@ -269,15 +286,25 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
             ly.bu = lo(pre + "ffn.up_proj.lora_B", {f, r});
             ly.ad = lo(pre + "ffn.down_proj.lora_A", {r, f});
             ly.bd = lo(pre + "ffn.down_proj.lora_B", {d, r});
+            // each stack (q/k/v, o, gate/up, down) contiguous, so that it is one [rows][in] weight
+            // whose groups continue across its members; stacks start 256-byte aligned
             const int64_t sizes[7] = {d * d, d * d, d * d, d * d, f * d, f * d, d * f};
+            const bool stack_end[7] = {false, false, true, true, false, true, true};
             for (int j = 0; j < 7; ++j) {
                 ly.pk[j] = q4_bytes;
-                q4_bytes += (sizes[j] / 2 + 255) / 256 * 256;
+                q4_bytes += sizes[j] / 2;
                 ly.sc[j] = q4_scales;
-                q4_scales += (sizes[j] / G + 127) / 128 * 128;
+                q4_scales += sizes[j] / G;
+                if (stack_end[j]) {
+                    q4_bytes = (q4_bytes + 255) / 256 * 256;
+                    q4_scales = (q4_scales + 127) / 128 * 128;
+                }
             }
         }
         arena_ = o2;
+        // bf16 base projections dequantized inside the GEMM kernels (which need these multiples);
+        // otherwise each projection stack is dequantized into a scratch buffer before its GEMM
+        q4_fused_ = cfg.compute == DType::BFloat16 && G % 64 == 0 && d % 64 == 0 && f % 64 == 0;
     }
     AIC_CHECK((d * d) % kAlign == 0 && (f * d) % kAlign == 0, InvalidArgument,
               "d_model*d_model and d_ffn*d_model must be multiples of 64 (fused q/k/v and gate/up projections)");
@@ -364,7 +391,14 @@ TransformerLM::~TransformerLM() {
     if (lora())
         for (void* p : {static_cast<void*>(base_dev_), base_low_, static_cast<void*>(q4_), q4s_})
             if (p) (void)hipFree(p);
-    if (stream_) (void)hipStreamDestroy(stream_);
+    if (stream_) {
+        try {
+            stream_scratch_release(stream_);
+        } catch (...) {  // a destructor does not throw
+        }
+        (void)hipStreamSynchronize(stream_);
+        (void)hipStreamDestroy(stream_);
+    }
 }
 
 int64_t TransformerLM::num_params() const {
@@ -409,9 +443,18 @@ void TransformerLM::quantize_base() {
         }
 }
 
-void TransformerLM::dequant(const Layer& ly, int j, int64_t n, void* dst, hipStream_t s) const {
-    hip::int4_dequant(q4_ + ly.pk[j], static_cast<const uint16_t*>(q4s_) + ly.sc[j], DType::Float16, n,
+const void* TransformerLM::dequant_stack(const Layer& ly, int j0, int j1, void* dst, hipStream_t s) const {
+    // a stack's projections are contiguous (bytes and scales), one weight of the summed size
+    const int64_t d = cfg_.hidden_dim, f = cfg_.intermediate_dim;
+    int64_t n = 0;
+    for (int j = j0; j <= j1; ++j) {
+        int64_t off, nj;
+        proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, off, nj);
+        n += nj;
+    }
+    hip::int4_dequant(q4_ + ly.pk[j0], static_cast<const uint16_t*>(q4s_) + ly.sc[j0], DType::Float16, n,
                       cfg_.quant_group, dst, cfg_.compute, s);
+    return dst;
 }
 
 namespace {
@@ -690,15 +733,16 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     DeviceBuffer &r1 = f32(L * T), &r2 = f32(L * T), &lse = f32(L * T * H);
     DeviceBuffer &hf = act(T * d), &rf = f32(T), &logits = act(T * V), &lse_ce = f32(T);
     // QLoRA: each layer's adapter inputs x A^T (q/k/v stacked [T,3r], o [T,r], gate/up [T,2r],
-    // down [T,r]) kept for the backward, and one dequantized projection (or stack) at a time
+    // down [T,r]) kept for the backward.  The frozen INT4 base stays INT4 in HBM: with bf16
+    // operands the GEMMs dequantize it in their operand load (q4f); otherwise one projection
+    // stack at a time is dequantized into a scratch buffer right before each GEMM that reads it,
+    // in the forward and again in the backward.
     const bool ql = lora();
+    const bool q4f = ql && q4_fused_ && T >= 8;
     const int64_t r = cfg_.lora_rank;
     const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
     DeviceBuffer& xa_all = act(ql ? L * T * 7 * r : 0);
-    // and each layer's dequantized base projections: formed in the forward, reused by the
-    // backward (one dequantization per projection per step, at 2 B per base weight in HBM)
-    const int64_t wl = 4 * d * d + 3 * f * d;
-    DeviceBuffer& wbuf = act(ql ? L * wl : 0);
+    DeviceBuffer& wbuf = act(ql && !q4f ? std::max(3 * d * d, 2 * f * d) : 0);
     auto at = [&](const DeviceBuffer& b, int64_t elem) {
         return static_cast<void*>(static_cast<char*>(b.get()) + es * static_cast<size_t>(elem));
     };
@@ -707,28 +751,17 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     auto xao = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 3 * r); };
     auto xagu = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 4 * r); };
     auto xad = [&](int64_t l) { return at(xa_all, l * T * 7 * r + T * 6 * r); };
-    // a projection's base weight: the arena, or with QLoRA the INT4 copy dequantized into wbuf
-    // (QuantizedLinear::forward, src/nn/quantization.cpp:602-615); projections j0..j1 (q, k, v,
-    // o, gate, up, down) stacked
-    // projections j0.. of layer l in wbuf: q/k/v (j0 = 0), o (3), gate/up (4), down (6)
-    auto wslot = [&](int64_t l, int j0) -> void* {
-        const int64_t o = j0 == 0 ? 0 : j0 == 3 ? 3 * d * d : j0 == 4 ? 4 * d * d : 4 * d * d + 2 * f * d;
-        return at(wbuf, l * wl + o);
-    };
-    auto wbase = [&](const Layer& ly, int64_t l, int64_t off, int j0, int j1) -> const void* {
+    // a projection stack's base weight (projections j0..j1 of q, k, v, o, gate, up, down): the
+    // arena, or with QLoRA (QuantizedLinear::forward, src/nn/quantization.cpp:669-679) the INT4
+    // stack as an in-GEMM operand (wq) or dequantized into wbuf (wbase)
+    auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
         if (!ql) return WB(off);
-        char* dst = static_cast<char*>(wslot(l, j0));
-        int64_t o = 0;
-        for (int j = j0; j <= j1; ++j) {
-            int64_t po, n;
-            proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, po, n);
-            dequant(ly, j, n, dst + es * o, s);
-            o += n;
-        }
-        return dst;
+        if (q4f) return nullptr;
+        return dequant_stack(ly, j0, j1, wbuf.get(), s);
     };
-    // the backward's view of the same weights (dequantized by the forward)
-    auto wkept = [&](int64_t l, int64_t off, int j0) -> const void* { return ql ? wslot(l, j0) : WB(off); };
+    auto wq = [&](const Layer& ly, int j0) -> Q4B {
+        return q4f ? Q4B{q4_ + ly.pk[j0], static_cast<const uint16_t*>(q4s_) + ly.sc[j0], cfg_.quant_group} : Q4B{};
+    };
     // the frozen model's gradients are not formed with QLoRA
     auto GB = [&](int64_t off) -> float* { return ql ? nullptr : G(off); };
 
@@ -760,8 +793,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xaq(l), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lq = LowRank{xaq(l), 3 * r, W(ly.bq), r, r, d, 0};
         }
-        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, l, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
-             1.0f, ql ? &lq : nullptr);
+        gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lq : nullptr, wq(ly, 0));
         {
             auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
             hip::rope(qkvl, 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, false, dt, s);
@@ -776,8 +809,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lo_ = LowRank{xao(l), r, W(ly.bo), r, r, 0, 0};
         }
-        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, l, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
-             ql ? &lo_ : nullptr);
+        gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
+             ql ? &lo_ : nullptr, wq(ly, 3));
         {
             auto _p = prof_.scope(kNormFwd, 0.0, 2.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_fwd(x1l, d, PB(ly.n2), h2l, d, atf(r2, l * T), T, d, eps, dt, s);
@@ -792,8 +825,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xagu(l), 2 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lg = LowRank{xagu(l), 2 * r, W(ly.bg), r, r, f, 0};
         }
-        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, l, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
-             1.0f, ql ? &lg : nullptr);
+        gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lg : nullptr, wq(ly, 4));
         {
             auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
             hip::swiglu_fwd(gul, static_cast<char*>(gul) + es * f, 2 * f, aml, f, T, f, dt, s);
@@ -803,8 +836,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             ld_ = LowRank{xad(l), r, W(ly.bd), r, r, 0, 0};
         }
-        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, l, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
-             ql ? &ld_ : nullptr);
+        gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
+             ql ? &ld_ : nullptr, wq(ly, 6));
     }
     void* xL = at(xs, L * T * d);
     {
@@ -878,8 +911,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             } else {
                 gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
             }
-            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wkept(l, ly.wd, 6), f, da.get(), f, dt, dt, s, nullptr, 0, 0.0f,
-                 1.0f, ql ? &ld_ : nullptr);
+            gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s, nullptr, 0,
+                 0.0f, 1.0f, ql ? &ld_ : nullptr, wq(ly, 6));
             {
                 auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
                 hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
@@ -896,8 +929,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             } else {
                 gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
             }
-            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wkept(l, ly.wgu, 4), d, dh.get(), d, dt, dt, s,
-                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr);
+            gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s,
+                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr, wq(ly, 4));
         }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
@@ -911,8 +944,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
             lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
         }  // else: the out_proj weight gradient joins the q/k/v one below (dx is unchanged until then)
-        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wkept(l, ly.wo, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
-             1.0f, ql ? &lo_ : nullptr);
+        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
+             1.0f, ql ? &lo_ : nullptr, wq(ly, 3));
         {
             // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
             auto _p = prof_.scope(kAttnBwd, 2.0 * attn_flops, 8.0 * es * T * d, s);
@@ -939,8 +972,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dx.get(), ol, G(ly.wo)}},
                           {{3 * d, d, T}, {d, d, T}}, dt, s);
         }
-        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wkept(l, ly.wqkv, 0), d, dh.get(), d, dt, dt, s, nullptr,
-             0, 0.0f, 1.0f, ql ? &lq : nullptr);
+        gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
+             0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
             hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, GB(ly.n1), false,
@@ -1045,18 +1078,18 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
     const float lsc = ql ? cfg_.lora_alpha / static_cast<float>(r) : 0.0f;
     DeviceBuffer &xa = act(T * d), &xb = act(T * d), &h = act(T * d), &qkv = act(T * 3 * d), &ob = act(T * d),
                  &x1 = act(T * d), &gu = act(moe ? 0 : T * 2 * f), &am = act(moe ? 0 : T * f), &rr = f32(T),
-                 &lse = f32(start_pos == 0 ? T * H : 0), &xs = act(ql ? T * 7 * r : 0),
-                 &wbuf = act(ql ? std::max(3 * d * d, 2 * f * d) : 0);
+                 &lse = f32(start_pos == 0 ? T * H : 0), &xs = act(ql ? T * 7 * r : 0);
+    // QLoRA base projections as in the training step: in-GEMM INT4 operands, or dequantized
+    // stack by stack into a scratch buffer (fp32 operands, or fewer than 8 rows)
+    const bool q4f = ql && q4_fused_ && T >= 8;
+    DeviceBuffer& wbuf = act(ql && !q4f ? std::max(3 * d * d, 2 * f * d) : 0);
     auto wbase = [&](const Layer& ly, int64_t off, int j0, int j1) -> const void* {
         if (!ql) return WB(off);
-        int64_t o = 0;
-        for (int j = j0; j <= j1; ++j) {
-            int64_t po, n;
-            proj_of(ly.wqkv, ly.wo, ly.wgu, ly.wd, d, f, j, po, n);
-            dequant(ly, j, n, static_cast<char*>(wbuf.get()) + es * o, s);
-            o += n;
-        }
-        return wbuf.get();
+        if (q4f) return nullptr;
+        return dequant_stack(ly, j0, j1, wbuf.get(), s);
+    };
+    auto wq = [&](const Layer& ly, int j0) -> Q4B {
+        return q4f ? Q4B{q4_ + ly.pk[j0], static_cast<const uint16_t*>(q4s_) + ly.sc[j0], cfg_.quant_group} : Q4B{};
     };
     hip::embed_fwd(ids, T, WB(emb_), V, d, xa.get(), dt, s);
     void* x = xa.get();
@@ -1070,7 +1103,7 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
             lq = LowRank{xs.get(), 3 * r, W(ly.bq), r, r, d, 0};
         }
         gemm(prof_, 0, 1, T, 3 * d, d, h.get(), d, wbase(ly, ly.wqkv, 0, 2), d, qkv.get(), 3 * d, dt, dt, s, nullptr,
-             0, 0.0f, 1.0f, ql ? &lq : nullptr);
+             0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
         hip::rope(qkv.get(), 3 * d, B, S, 2 * H, hd, start_pos, cos_dev_, sin_dev_, false, dt, s);
         // the new keys and values join the cache at rows start_pos .. start_pos + S - 1
         char* kc = static_cast<char*>(kv_cache_) + es * static_cast<size_t>(l * 2 * B * MS * d);
@@ -1091,7 +1124,7 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
             lo_ = LowRank{xs.get(), r, W(ly.bo), r, r, 0, 0};
         }
         gemm(prof_, 0, 1, T, d, d, ob.get(), d, wbase(ly, ly.wo, 3, 3), d, x1.get(), d, dt, dt, s, x, d, 0.0f, 1.0f,
-             ql ? &lo_ : nullptr);
+             ql ? &lo_ : nullptr, wq(ly, 3));
         hip::rmsnorm_fwd(x1.get(), d, PB(ly.n2), h.get(), d, rr.as<float>(), T, d, eps, dt, s);
         if (moe) {
             moe_[l]->forward(h.get(), T, W(ly.wr), W(ly.wex), x1.get(), xn, aux_dev_ + l, s);
@@ -1103,7 +1136,7 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
                 lg = LowRank{xs.get(), 2 * r, W(ly.bg), r, r, f, 0};
             }
             gemm(prof_, 0, 1, T, 2 * f, d, h.get(), d, wbase(ly, ly.wgu, 4, 5), d, gu.get(), 2 * f, dt, dt, s,
-                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr);
+                 nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr, wq(ly, 4));
             hip::swiglu_fwd(gu.get(), at(gu, f), 2 * f, am.get(), f, T, f, dt, s);
             LowRank ld_{};
             if (ql) {
@@ -1111,7 +1144,7 @@ void TransformerLM::forward_step(const int64_t* ids, int64_t B, int64_t S, int64
                 ld_ = LowRank{xs.get(), r, W(ly.bd), r, r, 0, 0};
             }
             gemm(prof_, 0, 1, T, d, f, am.get(), f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1.get(), d, 0.0f,
-                 1.0f, ql ? &ld_ : nullptr);
+                 1.0f, ql ? &ld_ : nullptr, wq(ly, 6));
         }
         std::swap(x, xn);
     }

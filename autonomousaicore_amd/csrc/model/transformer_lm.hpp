@@ -184,8 +184,9 @@ private:
     const void* W(int64_t off) const;   // compute-precision trainable weight at arena offset
     const void* WB(int64_t off) const;  // compute-precision base weight at base arena offset
     float* PB(int64_t off) const { return base_dev_ + off; }
-    // dequantizes projection j (q, k, v, o, gate, up, down) of layer l into dst (compute dtype)
-    void dequant(const Layer& ly, int j, int64_t n, void* dst, hipStream_t s) const;
+    // dequantizes the contiguous projections j0..j1 (q, k, v, o, gate, up, down) of a layer into
+    // dst (compute dtype) and returns dst
+    const void* dequant_stack(const Layer& ly, int j0, int j1, void* dst, hipStream_t s) const;
     float* P(int64_t off) const { return params_dev_ + off; }
     float* G(int64_t off) const { return grads_dev_ + off; }
     void forward_backward(const int64_t* ids, const int64_t* targets, int64_t B, int64_t S, bool backward,
@@ -212,6 +213,7 @@ private:
     float* aux_dev_ = nullptr;  // per-layer MoE aux losses [L]
     float* base_dev_ = nullptr;  // frozen base weights (fp32); the trainable arena without QLoRA
     void* base_low_ = nullptr;   // their bf16 shadow (AMP)
+    bool q4_fused_ = false;      // QLoRA: base projections dequantized inside the GEMMs
     uint8_t* q4_ = nullptr;      // QLoRA: INT4 projections
     void* q4s_ = nullptr;        //        and their fp16 scales
     std::vector<std::unique_ptr<MoEFFN>> moe_;

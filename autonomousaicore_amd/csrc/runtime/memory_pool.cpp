@@ -70,13 +70,35 @@ MemoryStats pool_stats() {
     return g_stats;
 }
 
+namespace {
+struct ScratchEntry {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex scratch_mu;
+std::map<std::tuple<int, hipStream_t, int>, ScratchEntry>& scratch_cache() {
+    static std::map<std::tuple<int, hipStream_t, int>, ScratchEntry> cache;
+    return cache;
+}
+}  // namespace
+
+void stream_scratch_release(hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    auto& cache = scratch_cache();
+    for (auto it = cache.begin(); it != cache.end();) {
+        if (std::get<1>(it->first) == stream) {
+            if (it->second.ptr) pool_free(it->second.ptr, stream);
+            it = cache.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
 void* stream_scratch(size_t bytes, hipStream_t stream, int slot) {
-    struct Entry {
-        void* ptr = nullptr;
-        size_t bytes = 0;
-    };
-    static std::mutex mu;
-    static std::map<std::tuple<int, hipStream_t, int>, Entry> cache;
+    auto& cache = scratch_cache();
+    auto& mu = scratch_mu;
+    using Entry = ScratchEntry;
     if (bytes == 0) return nullptr;
     int dev = 0;
     AIC_HIP_CHECK(hipGetDevice(&dev));

@@ -68,5 +68,9 @@ private:
 // bytes; callers use it only for the duration of their own launches.  Slots let one call hold
 // several buffers at once.
 void* stream_scratch(size_t bytes, hipStream_t stream, int slot = 0);
+// Returns every scratch buffer cached for `stream` to the pool (stream-ordered on it); called
+// before the stream is destroyed, so that the buffers do not outlive it and a later stream at
+// the same handle address does not inherit them.
+void stream_scratch_release(hipStream_t stream);
 
 }  // namespace aic

@@ -3,6 +3,8 @@
     python -m autonomousaicore_amd.rocprof_summary --stats DIR/run_kernel_stats.csv \
         [--fetch DIR/run_counter_collection.csv --write DIR/run_counter_collection.csv \
          --copy-probe-mib 1024] [--steps N]
+    python -m autonomousaicore_amd.rocprof_summary --pmc DIR1/run_counter_collection.csv \
+        [DIR2/run_counter_collection.csv ...]
 
 Kernel symbols map to the same classes as the library's event profiler (the class a launch
 is timed under inside TransformerLM::train_step), so the per-class average launch time here
@@ -13,6 +15,19 @@ class's dispatch count.  Each counter is scaled by expected/measured on the copy
 `bench.py --copy-probe-mib M` runs before the model (a device-to-device copy of M MiB reads
 and writes exactly M MiB).  The scaled per-launch byte counts are printed as
 `traffic <class> <bytes>` lines, which bench.py reads back for its `roofline.traffic`.
+
+Counters (--pmc, one or more counter-collection files from separate rocprofv3 --pmc passes):
+per kernel symbol of the MFMA classes (GEMMs, attention), the per-dispatch average of every
+counter collected, and from them, with cycles = GRBM_GUI_ACTIVE / XCDs (rocprofv3 sums the
+counter over the 8 XCDs, each counting the same kernel cycles):
+  mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles * SIMDs)   (the matrix pipes' duty)
+  lds_util  = SQ_LDS_IDX_ACTIVE / (cycles * CUs)
+  lds_confl = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT)
+  l2_hit    = TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
+  mfma_flop = SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512 (the bf16 MFMA work executed)
+  clock     = cycles / the kernel's duration (with --stats of the same command)
+with the MI355X's 256 CUs of 4 SIMDs in 8 XCDs (--cus, --xcds).  Passes are run one counter
+set at a time (rocprofv3 collects what one pass can hold), each on the same bench.py command.
 """
 from __future__ import annotations
 
@@ -23,6 +38,9 @@ from collections import defaultdict
 
 # (regex on the demangled or mangled symbol, class); first match wins.
 _RULES = [
+    # gemm_bf16_dma_q4<BM, BN, BK, STAGES, transB, C>: the INT4-operand forward / input gradient
+    (r"gemm_bf16_dma_q4(<(\d+, )+true|I(Li\d+E)+Lb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma_q4(<(\d+, )+false|I(Li\d+E)+Lb0E)", "gemm_dgrad"),
     # gemm_bf16_dma[_grouped|_ragged]<BM, BN, BK, STAGES, transA, transB, C>, demangled or mangled
     (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
     (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
@@ -42,6 +60,7 @@ _RULES = [
     (r"adamw", "adamw"),
     # kernels outside bench.py's event classes (the MoE and QLoRA configurations)
     (r"moe_", "moe_routing"),
+    (r"int4_quantize", "other"),  # the base's one-time quantization at set-up, like the weight init
     (r"int4_", "int4"),
     (r"splitk_reduce", "gemm_splitk_reduce"),
 ]
@@ -96,14 +115,69 @@ def copy_factor(disp, mib):
     return (mib * 1024.0) / max(copies)
 
 
+MFMA_CLASSES = ("gemm_fwd", "gemm_dgrad", "gemm_wgrad", "attn_fwd", "attn_bwd")
+
+
+def pmc_summary(paths, cus, xcds):
+    """Per-kernel per-dispatch counter averages over the MFMA classes, with derived ratios."""
+    vals = defaultdict(lambda: defaultdict(float))
+    disp = defaultdict(lambda: defaultdict(set))
+    for path in paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                k, c = r["Kernel_Name"], r["Counter_Name"]
+                vals[k][c] += float(r["Counter_Value"])
+                disp[k][c].add(r.get("Dispatch_Id", len(disp[k][c])))
+    rows = []
+    for k, cs in vals.items():
+        cls = kernel_class(k)
+        if cls not in MFMA_CLASSES:
+            continue
+        avg = {c: v / max(len(disp[k][c]), 1) for c, v in cs.items()}
+        n = max(len(d) for d in disp[k].values())
+        rows.append((cls, -n, k, n, avg))
+    rows.sort()
+    simds = 4 * cus
+    print("# MFMA-class kernels: per-dispatch counter averages (rocprofv3 --pmc passes)")
+    print(f"{'class':<11} {'disp':>5} {'mfma_busy':>9} {'lds_util':>8} {'lds_confl':>9} {'l2_hit':>6} "
+          f"{'mfma_TFLOP':>10}  kernel")
+    for cls, _, k, n, a in rows:
+        def ratio(num, den):
+            return a[num] / a[den] if num in a and den in a and a[den] > 0 else float("nan")
+        act = a.get("GRBM_GUI_ACTIVE", float("nan")) / xcds
+        mb = a["SQ_VALU_MFMA_BUSY_CYCLES"] / (act * simds) if "SQ_VALU_MFMA_BUSY_CYCLES" in a else float("nan")
+        lu = a["SQ_LDS_IDX_ACTIVE"] / (act * cus) if "SQ_LDS_IDX_ACTIVE" in a else float("nan")
+        lc = (a["SQ_LDS_BANK_CONFLICT"] / (a["SQ_LDS_IDX_ACTIVE"] - a["SQ_LDS_BANK_CONFLICT"])
+              if "SQ_LDS_BANK_CONFLICT" in a and "SQ_LDS_IDX_ACTIVE" in a else float("nan"))
+        hit, miss = a.get("TCC_HIT_sum"), a.get("TCC_MISS_sum")
+        l2 = hit / (hit + miss) if hit is not None and miss is not None and hit + miss > 0 else float("nan")
+        fl = a.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", float("nan")) * 512 / 1e12
+        short = k if len(k) <= 100 else k[:97] + "..."
+        print(f"{cls:<11} {n:>5} {mb:>9.3f} {lu:>8.3f} {lc:>9.3f} {l2:>6.3f} {fl:>10.4f}  {short}")
+    print("\n# raw per-dispatch averages")
+    for cls, _, k, n, a in rows:
+        short = k if len(k) <= 100 else k[:97] + "..."
+        print(f"{cls} {short}")
+        print("    " + ", ".join(f"{c}={v:.4g}" for c, v in sorted(a.items())))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--stats", required=True)
+    ap.add_argument("--stats")
+    ap.add_argument("--pmc", nargs="+", help="counter-collection CSVs of rocprofv3 --pmc passes")
+    ap.add_argument("--cus", type=int, default=256, help="compute units (MI355X: 256, 4 SIMDs each)")
+    ap.add_argument("--xcds", type=int, default=8, help="XCDs the GRBM counter is summed over (MI355X: 8)")
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--copy-probe-mib", type=int, default=0)
     ap.add_argument("--steps", type=int, default=0, help="train steps in the profiled run (for ms/step)")
     args = ap.parse_args(argv)
+    if args.pmc:
+        pmc_summary(args.pmc, args.cus, args.xcds)
+        if not args.stats:
+            return
+    if not args.stats:
+        ap.error("--stats or --pmc is required")
 
     per = defaultdict(lambda: [0, 0.0])
     kernels = []

@@ -202,6 +202,7 @@ def main():
         sys.exit(1)
     c = CONFIGS[args.config]
     B, S = c["B"], c["S"]
+    free0, total = torch.cuda.mem_get_info()
     if args.copy_probe_mib > 0:
         n = args.copy_probe_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -276,6 +277,9 @@ def main():
 
     ms = 1000.0 * elapsed / args.steps
     tokens_per_s = B * S * args.steps / elapsed
+    # device memory the model holds after the steps (parameters, optimiser state, the persistent
+    # step workspace and the library's pool), from hipMemGetInfo around the whole run
+    free1, _ = torch.cuda.mem_get_info()
     flops = step_flops(c)
     classes = timed
     d = class_table(classes, args.steps)[dom_name]
@@ -315,6 +319,7 @@ def main():
         "mfma_peak_frac_step": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "loss": round(float(stats.loss), 5),
         "loss_scale": stats.loss_scale,
+        "hbm_in_use_gib": round((free0 - free1) / 2**30, 2),
         "roofline": roofline,
         "kernel_classes": kc,
         "kernel_classes_pass": "a second run of the same steps after the timed region, every class timed",

@@ -58,6 +58,12 @@ int aic_hip_mem_free_async(void* ptr, aic_stream stream);
 /* Bytes currently allocated through the pool and the high-water mark
  * (replaces MemoryStats, include/memory/allocator.hpp:14-50). */
 int aic_hip_mem_stats(int64_t* allocated_bytes, int64_t* peak_bytes);
+/* Returns the scratch buffers the library keeps cached for `stream` (kernels' partial results,
+ * stream-ordered) to the pool.  Call it before destroying a stream the library has run work on:
+ * the cache is keyed by the stream handle, so its buffers would otherwise stay allocated, and a
+ * later stream created at the same address would inherit them.  The library does this itself
+ * for the streams it creates.  No reference counterpart (the reference allocates per call). */
+int aic_hip_mem_release_stream(aic_stream stream);
 /* Copy of `bytes` between any two of host and device memory, ordered on the stream, returning
  * when it is done (hipMemcpyDefault: the direction comes from the pointers).
  * Replaces: the reference's raw cudaMemcpy calls (e.g. src/tensor/tensor.cpp:266,320,
@@ -338,8 +344,13 @@ int aic_hip_int4_dequantize(const uint8_t* packed, const void* scales, aic_dtype
                             void* out, aic_dtype out_type, aic_stream stream);
 /* C[M,N] = alpha * X[M,K] . op(deq(Wq)) + beta * C + R with Wq an INT4 weight as above:
  * transW = 1: Wq holds W [N,K] and op(W) = W^T (forward y = x W^T); transW = 0: Wq holds W [K,N]
- * (input gradient dx = dy W).  The weight is dequantized into library scratch in ab_type
- * (AIC_BF16 or AIC_F32) and multiplied there; X, C and R as in aic_hip_gemm.
+ * (input gradient dx = dy W).  With bf16 operands (ab_type AIC_BF16) in the shapes the GEMM
+ * kernel takes (K % 64 == 0, group % 64 == 0, the weight's row length % 64 == 0, and for
+ * transW = 0 N % 64 == 0; M, N >= 8; X and Wq 16-byte aligned) the packed values and scales are
+ * read by the GEMM itself and dequantized in its operand load, with no dequantized copy in HBM.
+ * Otherwise (and for AIC_F32) the weight is first dequantized into library scratch in ab_type.
+ * Either way op(W) holds q * scale rounded to ab_type, so both routes give the same product;
+ * X, C and R as in aic_hip_gemm.
  * Replaces: QuantizedLinear::forward (src/nn/quantization.cpp:669-679: dequantize, transpose,
  * matmul) and its MatMulBackward input gradient (src/autograd/functions.cpp:254-273). */
 int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx,

@@ -55,21 +55,27 @@ def test_noalloc_sqnorm_matches_allocating_entry():
     tb, ts = [dev(a) for a in big], [dev(a) for a in small]
     ref_b = float(sum((a.astype(np.float64) ** 2).sum() for a in big))
 
-    s_noalloc, s_alloc = torch.cuda.Stream(), torch.cuda.Stream()  # fresh streams: no cached scratch
+    s_noalloc, s_alloc = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for st in (s_noalloc, s_alloc):  # torch recycles streams: drop what the library cached for them
+        call("aic_hip_mem_release_stream", st.cuda_stream)
     before = _pool_bytes()
     got_b = _sqnorm("aic_hip_grad_sqnorm_multi_noalloc", tb, s_noalloc)
     got_s = _sqnorm("aic_hip_grad_sqnorm_multi_noalloc", ts, s_noalloc)
     assert _pool_bytes() == before, "the no-alloc entry took memory from the library's pool"
 
     exp_b = _sqnorm("aic_hip_grad_sqnorm_multi", tb, s_alloc)
-    assert _pool_bytes() > before  # control: the allocating entry takes its scratch on a new stream
+    assert _pool_bytes() > before  # control: the allocating entry takes its scratch on this stream
     exp_s = _sqnorm("aic_hip_grad_sqnorm_multi", ts, s_alloc)
+    again = _sqnorm("aic_hip_grad_sqnorm_multi_noalloc", tb, s_noalloc)
+    call("aic_hip_mem_release_stream", s_alloc.cuda_stream)
+    assert _pool_bytes() == before  # the released scratch is back in the pool
     assert got_b == exp_b and got_s == exp_s  # bit for bit: the same partials in the same order
     assert got_b[1] == 0 and abs(got_b[0] - ref_b) < 1e-9 * ref_b
     assert got_s[1] == 1
 
     # and again on the first input after the smaller one: stale partials are never read
-    assert _sqnorm("aic_hip_grad_sqnorm_multi_noalloc", tb, s_noalloc) == exp_b
+    assert again == exp_b
 
 
 def test_noalloc_sqnorm_rejects_beyond_its_scratch():
