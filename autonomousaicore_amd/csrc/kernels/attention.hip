@@ -328,16 +328,38 @@ __global__ __launch_bounds__(256) void attn_dot_v8_k(const bf16* __restrict__ o,
 
 // ---------------------------------------------------------------------------------------
 // Backward: dK, dV.  Stage = Q tile, dO tile (64 x HD each), lse and D of the 64 queries.
+//
+// Per query tile a wave (32 keys) runs four groups of MFMAs, each pinned in source order
+// (sched_barrier after every MFMA) together with the work that overlaps it:
+//   A  S^T, dP^T of queries 0..31   (2 KS MFMAs) + fragment reads two k steps ahead
+//   B  S^T, dP^T of queries 32..63  (2 KS)      + the softmax / dS of queries 0..31, one
+//                                                 element per slot, and the transposed reads
+//                                                 of the first dV / dK step
+//   C  dV^T, dK^T over queries 0..31 (4 OB)     + the softmax / dS of queries 32..63 and the
+//                                                 transposed reads one step ahead
+//   D  dV^T, dK^T over queries 32..63 (4 OB)    + the transposed reads one step ahead
+// so the LDS latency of every fragment and the softmax VALU run in the shadow of MFMAs.  The
+// causal mask is one compare per element against a per-lane bound (no branch).
+// head_dim 128 (about 500 registers: one block per CU): three stages, the copy of tile t+2 going
+// out right after the barrier that opens tile t, into the stage tile t-1 used, so one barrier per
+// tile suffices.  head_dim 64: two stages and two blocks per CU (the other block's waves hide
+// what the schedule does not; measured faster than three stages at one block).
 // ---------------------------------------------------------------------------------------
 template <int HD>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
+__global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ldq,
     const bf16* __restrict__ dout, int64_t ldo, const float* __restrict__ lse, const float* __restrict__ Dg,
     bf16* __restrict__ dk, bf16* __restrict__ dv, int64_t ldd, int H, int S, float c, float scale, int causal) {
     constexpr int BQ = 64, BKV = 128, KS = HD / 16, OB = HD / 32, TILE = BQ * HD;
     constexpr int LPT = 2 * (64 * HD / 512 / 4);
+    constexpr int NST = HD == 128 ? 3 : 2;
     constexpr int STAGE = 2 * TILE + 2 * 64 * 2;  // Q, dO, then lse and D as fp32 (2 x 64 x 4 B)
-    __shared__ __attribute__((aligned(16))) bf16 sm[2][STAGE];
+    constexpr int NA = 2 * KS;                    // MFMAs of groups A and B
+    constexpr int NC = 2 * OB * 2;                // MFMAs of groups C and D (two 16-query steps)
+    constexpr int EB = 16 / NA;                   // softmax elements per slot in group B
+    constexpr int EC = 16 / NC;                   // ... in group C
+    static_assert(16 % NA == 0 && 16 % NC == 0, "slot counts");
+    __shared__ __attribute__((aligned(16))) bf16 sm[NST][STAGE];
 
     // 1-D grid, heaviest blocks first (causal: key block 0 sees every query tile)
     const int nkv = (S + BKV - 1) / BKV;
@@ -371,7 +393,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
 
     const int nq = (S + BQ - 1) / BQ;
     const int qt0 = causal ? (k0 / BQ) : 0;
-    // waves 0 and 1 also copy the 64 lse / D values of the tile (4 bytes per lane)
+    // waves 0 and 1 also copy the 64 lse / D values of the tile (4 bytes per lane); rows past S
+    // repeat row S-1 (their lse is replaced by +inf below, so they contribute nothing)
     auto copy = [&](int qt, int st) {
         dma_rows64<HD>(q + tok0 * ldq + hoff, ldq, qt * BQ, S, sm[st]);
         dma_rows64<HD>(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
@@ -384,72 +407,138 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_mfma(
     if (qt0 + 1 < nq) copy(qt0 + 1, 1);
 
     for (int qt = qt0; qt < nq; ++qt) {
-        const int st = (qt - qt0) & 1;
+        const int it = qt - qt0, st = it % NST;
+        // tile qt has landed (tile qt+1's copy may still be in flight) and every wave is done
+        // with tile qt-1, whose stage receives tile qt+2
         if (qt + 1 < nq) {
             if (wave < 2) wait_vmcnt<LPT + 1>();
             else wait_vmcnt<LPT>();
         } else {
             wait_vmcnt<0>();
         }
+        wait_lds();  // this wave's reads of tile qt-1's stage are complete
         __builtin_amdgcn_s_barrier();
+        if (NST == 3 && qt + 2 < nq) copy(qt + 2, (it + 2) % NST);
         const int qs = qt * BQ;
+        // every query of the tile precedes this wave's keys: nothing to do
+        if (!causal || qs + BQ - 1 >= kw) {
         const char* Qb = reinterpret_cast<const char*>(sm[st]);
         const char* Ob = reinterpret_cast<const char*>(sm[st] + TILE);
         const float* Ls = reinterpret_cast<const float*>(sm[st] + 2 * TILE);
         const float* Ds = Ls + 64;
-        if (!causal || qs + BQ - 1 >= kw) {
-            f32x16 s[2], dp[2];
+        // element e of query block jb is query qs + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked
+        // when its offset 32 jb + 8 (e >> 2) + (e & 3) is below lo (causal: key > query)
+        const int lo = causal ? mykey - qs - 4 * hl : -(1 << 30);
+        const bool tail = qs + BQ > S;
+
+        f32x16 sa[2], sd[2];
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                zero(s[mb]);
-                zero(dp[mb]);
+        for (int jb = 0; jb < 2; ++jb) {
+            zero(sa[jb]);
+            zero(sd[jb]);
+        }
+        bf16x8 rq[3], ro[3];  // row fragments, g = jb * KS + kk in slot g % 3
+        auto rd = [&](int g) {
+            rq[g % 3] = F.row(Qb, 32 * (g / KS), g % KS);
+            ro[g % 3] = F.row(Ob, 32 * (g / KS), g % KS);
+        };
+        float nl[2][16], dd[2][16];  // -lse * log2(e) and D per element
+        auto rd_ld = [&](int jb) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int qi = jb * 32 + 8 * g4 + 4 * hl;
+                const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);
+                const float4 d4 = *reinterpret_cast<const float4*>(Ds + qi);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    // queries past S: p = exp2(-inf) = 0
+                    nl[jb][4 * g4 + u] = (tail && qs + qi + u >= S) ? -INFINITY : -lv[u] * kLog2e;
+                    dd[jb][4 * g4 + u] = dv4[u];
+                }
+            }
+        };
+        auto softmax = [&](int jb, int e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, nl[jb][e]));
+            p = (32 * jb + 8 * (e >> 2) + (e & 3) < lo) ? 0.0f : p;
+            sa[jb][e] = p;
+            sd[jb][e] = p * (sd[jb][e] - dd[jb][e]);
+        };
+        bf16x8 pf[4], dsf[4];
+        auto pack = [&](int ks) {
+            pf[ks] = pack_bf16x8(sa[ks >> 1], 8 * (ks & 1));
+            dsf[ks] = pack_bf16x8(sd[ks >> 1], 8 * (ks & 1));
+        };
+        // transposed fragments f = ks * 2 OB + i (i < OB: dO^T block i, else Q^T block i - OB) of
+        // the four 16-query steps, read one step ahead into a ring of 2 OB + 1
+        constexpr int NR = 2 * OB + 1;
+        bf16x8 tr[NR];
+        auto rd_tr = [&](int f) {
+            const int ks = f / (2 * OB), i = f % (2 * OB);
+            tr[f % NR] = i < OB ? F.tr(Ob, i, ks) : F.tr(Qb, i - OB, ks);
+        };
+
+        rd(0);
+        rd(1);
+        rd_ld(0);
+        constexpr int LD1 = NA - 4;  // group B slot from which queries 32..63's lse / D are read
+        // A: S^T, dP^T of queries 0..31
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int kk = i >> 1, g = kk;
+            if ((i & 1) == 0) {
+                sa[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rq[g % 3], kf[kk], sa[0], 0, 0, 0);
+                rd(g + 2);
+            } else {
+                sd[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ro[g % 3], vf[kk], sd[0], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // B: S^T, dP^T of queries 32..63; softmax of queries 0..31; transposed reads of step 0
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int kk = i >> 1, g = KS + kk;
+            if ((i & 1) == 0) {
+                sa[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rq[g % 3], kf[kk], sa[1], 0, 0, 0);
+                if (g + 2 < 2 * KS) rd(g + 2);
+            } else {
+                sd[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ro[g % 3], vf[kk], sd[1], 0, 0, 0);
             }
 #pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
+            for (int e = i * EB; e < (i + 1) * EB; ++e) softmax(0, e);
+            if ((i + 1) * EB == 8) pack(0);
+            if ((i + 1) * EB == 16) pack(1);
+            if (i < 2 * OB) rd_tr(i);
+            if (i == LD1) rd_ld(1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // C, D: dV^T += dO^T P, dK^T += Q^T dS over the four 16-query steps
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Qb, mb * 32, kk), kf[kk], s[mb], 0, 0,
-                                                                     0);
-                    dp[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Ob, mb * 32, kk), vf[kk], dp[mb], 0,
-                                                                      0, 0);
+        for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+            for (int i = 0; i < 2 * OB; ++i) {
+                const int f = ks * 2 * OB + i;
+                if (i < OB)
+                    dvt[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr[f % NR], pf[ks], dvt[i], 0, 0, 0);
+                else
+                    dkt[i - OB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr[f % NR], dsf[ks], dkt[i - OB], 0, 0, 0);
+                if (f + 2 * OB < 8 * OB) rd_tr(f + 2 * OB);
+                if (ks < 2) {  // group C: the softmax of queries 32..63
+                    const int slot = ks * 2 * OB + i;
+#pragma unroll
+                    for (int e = slot * EC; e < (slot + 1) * EC; ++e) softmax(1, e);
+                    if ((slot + 1) * EC == 8) pack(2);
+                    if ((slot + 1) * EC == 16) pack(3);
                 }
-            // s[mb][e]: query qs + 32mb + 8(e/4) + 4hl + e%4, key mykey
-            const bool diag = (causal && qs < kw + 31) || qs + BQ > S || kw + 32 > S;
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int qi = mb * 32 + 8 * g4 + 4 * hl;
-                    const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);
-                    const float4 d4 = *reinterpret_cast<const float4*>(Ds + qi);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int e = 4 * g4 + u;
-                        float p = __builtin_amdgcn_exp2f(fmaf(s[mb][e], c, -lv[u] * kLog2e));
-                        if (diag) {
-                            const int qq = qs + qi + u;
-                            if (qq >= S || mykey >= S || (causal && mykey > qq)) p = 0.0f;
-                        }
-                        s[mb][e] = p;
-                        dp[mb][e] = p * (dp[mb][e] - dvv[u]);
-                    }
-                }
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8 pf = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
-                const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-                for (int ob = 0; ob < OB; ++ob) {
-                    dvt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Ob, ob, ks), pf, dvt[ob], 0, 0, 0);
-                    dkt[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.tr(Qb, ob, ks), dsf, dkt[ob], 0, 0,
-                                                                       0);
-                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        wait_lds();
-        __builtin_amdgcn_s_barrier();
-        if (qt + 2 < nq) copy(qt + 2, st);
+        }
+        if constexpr (NST == 2) {  // every wave is done with stage st before tile qt+2 lands there
+            wait_lds();
+            __builtin_amdgcn_s_barrier();
+            if (qt + 2 < nq) copy(qt + 2, st);
+        }
     }
 
     if (mykey < S) {
