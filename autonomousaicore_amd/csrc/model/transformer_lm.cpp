@@ -871,8 +871,11 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                     s);
     }
     void* dl = logits.get();
-    DeviceBuffer &dx = act(T * d), &dh = act(T * d), &dqkv = act(T * 3 * d), &dgu = act(moe ? 0 : T * 2 * f),
-                 &da = act(moe ? 0 : T * f), &dxa = act(ql ? T * 3 * r : 0);
+    // dx: the residual-stream gradient at a layer's output; dxm: at its attention block's output
+    // (the FFN's RMSNorm backward writes it next to dx, which the dense model's deferred
+    // down-projection weight gradient still reads)
+    DeviceBuffer &dx = act(T * d), &dxm = act(T * d), &dh = act(T * d), &dqkv = act(T * 3 * d),
+                 &dgu = act(moe ? 0 : T * 2 * f), &da = act(moe ? 0 : T * f), &dxa = act(ql ? T * 3 * r : 0);
     // LoRA backward of one projection (LoRALinear, src/nn/lora.cpp:75-93, through autograd):
     // with y += xs B^T and xs = s (x A^T) kept from the forward,
     //   dB = dy^T xs, dxa = s dy B   (then dA = dxa^T x, and dx += dxa A in the base dgrad GEMM)
@@ -908,9 +911,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                 lora_b_bwd(dx.get(), d, d, xad(l), r, ly.bd, dxa.get(), r);
                 gemm(prof_, 1, 0, r, f, T, dxa.get(), r, aml, f, G(ly.ad), f, dt, DType::Float32, s);
                 ld_ = LowRank{dxa.get(), r, W(ly.ad), f, r, 0, 1};
-            } else {
-                gemm(prof_, 1, 0, d, f, T, dx.get(), d, aml, f, G(ly.wd), f, dt, DType::Float32, s);
-            }
+            }  // else: the down-projection weight gradient joins the layer's grouped launch below
             gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s, nullptr, 0,
                  0.0f, 1.0f, ql ? &ld_ : nullptr, wq(ly, 6));
             {
@@ -926,25 +927,24 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                            ly.bu, static_cast<char*>(dxa.get()) + es * r, 2 * r);
                 gemm(prof_, 1, 0, 2 * r, d, T, dxa.get(), 2 * r, h2l, d, G(ly.agu), d, dt, DType::Float32, s);
                 lg = LowRank{dxa.get(), 2 * r, W(ly.agu), d, 2 * r, 0, 1};
-            } else {
-                gemm(prof_, 1, 0, 2 * f, d, T, dgu.get(), 2 * f, h2l, d, G(ly.wgu), d, dt, DType::Float32, s);
-            }
+            }  // else: the gate/up weight gradient joins the layer's grouped launch below (dgu is
+               // not written again before it)
             gemm(prof_, 0, 0, T, d, 2 * f, dgu.get(), 2 * f, wbase(ly, ly.wgu, 4, 5), d, dh.get(), d, dt, dt, s,
                  nullptr, 0, 0.0f, 1.0f, ql ? &lg : nullptr, wq(ly, 4));
         }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x1l, d, PB(ly.n2), atf(r2, l * T), dx.get(), d, dx.get(), d, GB(ly.n2),
+            hip::rmsnorm_bwd(dh.get(), d, x1l, d, PB(ly.n2), atf(r2, l * T), dx.get(), d, dxm.get(), d, GB(ly.n2),
                              false, T, d, dt, s);
         }
         // x1 = x + out_proj(attn(rope(q), rope(k), v))
         LowRank lo_{};
         if (ql) {
-            lora_b_bwd(dx.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
+            lora_b_bwd(dxm.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
             gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
             lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
-        }  // else: the out_proj weight gradient joins the q/k/v one below (dx is unchanged until then)
-        gemm(prof_, 0, 0, T, d, d, dx.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
+        }  // else: the out_proj weight gradient joins the layer's grouped launch below
+        gemm(prof_, 0, 0, T, d, d, dxm.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lo_ : nullptr, wq(ly, 3));
         {
             // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
@@ -966,18 +966,25 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                            static_cast<char*>(dxa.get()) + es * j * r, 3 * r);
             gemm(prof_, 1, 0, 3 * r, d, T, dxa.get(), 3 * r, h1l, d, G(ly.aqkv), d, dt, DType::Float32, s);
             lq = LowRank{dxa.get(), 3 * r, W(ly.aqkv), d, 3 * r, 0, 1};
-        } else {
-            // dWqkv = dqkv^T h1 and dWo = dx^T o in one launch (192 + 64 tiles of 256x256 at the 1B
-            // shape: one round of the chip instead of two partial ones)
-            wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dx.get(), ol, G(ly.wo)}},
+        } else if (moe) {
+            // dWqkv = dqkv^T h1 and dWo = dxm^T o in one launch
+            wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dxm.get(), ol, G(ly.wo)}},
                           {{3 * d, d, T}, {d, d, T}}, dt, s);
+        } else {
+            // the layer's four weight gradients in one launch: dWqkv = dqkv^T h1, dWo = dxm^T o,
+            // dWgu = dgu^T h2 and dWd = dx^T am (at the 1B shape 192 + 64 + 352 + 176 tiles of
+            // 256x256: a little over three full rounds of the chip instead of four partial ones)
+            wgrad_grouped(prof_,
+                          {{dqkv.get(), h1l, G(ly.wqkv)}, {dxm.get(), ol, G(ly.wo)},
+                           {dgu.get(), at(h2, l * T * d), G(ly.wgu)}, {dx.get(), at(am, l * T * f), G(ly.wd)}},
+                          {{3 * d, d, T}, {d, d, T}, {2 * f, d, T}, {d, f, T}}, dt, s);
         }
         gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
              0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dx.get(), d, dx.get(), d, GB(ly.n1), false,
-                             T, d, dt, s);
+            hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dxm.get(), d, dx.get(), d, GB(ly.n1),
+                             false, T, d, dt, s);
         }
     }
     if (!ql) {
