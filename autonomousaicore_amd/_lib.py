@@ -94,6 +94,7 @@ SIGNATURES = {
     "aic_hip_ce_fwd": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, vp, i32, vp]),
     "aic_hip_ce_bwd": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, vp, vp, i64, i32, vp]),
     "aic_hip_ce_bwd_rows": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, i32, f32, vp, i64, i32, vp]),
+    "aic_hip_ce_fwd_bwd": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, vp, vp, i32, vp]),
     "aic_hip_memcpy_sync": (i32, [vp, vp, C.c_size_t, vp]),
     "aic_hip_embed_fwd": (i32, [vp, i64, vp, i64, i64, vp, i32, vp]),
     "aic_hip_embed_bwd": (i32, [vp, i64, vp, i64, i64, vp, i32, i32, vp]),

@@ -267,6 +267,15 @@ int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const
     });
 }
 
+int aic_hip_ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                       float* losses, float* lse, float* loss_mean, int64_t* valid, const float* grad, aic_dtype d,
+                       aic_stream stream) {
+    return guard([&] {
+        aic::hip::ce_fwd_bwd(logits, ld, targets, N, C, ignore_index, losses, lse, loss_mean, valid, grad, dt(d),
+                             st(stream));
+    });
+}
+
 int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N,
                         int64_t C, int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits,
                         int64_t ld_d, aic_dtype d, aic_stream stream) {

@@ -1,9 +1,13 @@
 // Token embedding gather and its deterministic scatter-add backward.
 // Replaces cuda_embedding_forward/backward (src/cuda/cuda_embedding.cu:21-61), whose
 // backward uses fp32 atomicAdd (order-dependent results).  Here the backward sorts the
-// (id, position) pairs once in LDS (bitonic, one block) and then sums each id's rows in
-// token order, so repeated runs are bit-identical and ids that repeat often (Zipf-
-// distributed text) are summed by four waves instead of serialising on one address.
+// (id, position) pairs (chunks of 2048 sorted in LDS by as many blocks, then merged by rank:
+// each key's place is its index in its chunk plus its lower bound in every other chunk) and
+// sums each id's rows in a fixed order (interleaved chains over the token-ordered run, then
+// the chains in order), so repeated runs are bit-identical and ids that repeat often
+// (Zipf-distributed text) are summed by sixteen waves instead of serialising on one address.
+// Rows of ids that do not occur are written as zeros by their own kernel (no separate clear of
+// the whole gradient, and no memset node for a captured graph).
 #include <algorithm>
 
 #include "common.hpp"
@@ -35,28 +39,26 @@ __global__ __launch_bounds__(256) void embed_fwd_v(const int64_t* __restrict__ i
     out[idx] = (t >= 0 && t < V) ? W[t * Dv + d] : make_uint4(0, 0, 0, 0);
 }
 
-constexpr int kSortMax = 16384;  // tokens per step sortable in one block's LDS (128 KB)
+constexpr int kSortChunk = 2048;          // keys sorted per block in LDS (16 KB)
+constexpr int64_t kMaxTokens = 1LL << 20;  // tokens per call (the merge costs log2(2048) probes per other chunk)
 
-// Bitonic sort of keys (id << 32 | position); ids outside [0, V) sort last.
-__global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__ ids, int N, int64_t V,
-                                                     int* __restrict__ sorted_pos, int* __restrict__ sorted_id,
-                                                     int* __restrict__ run_start, int* __restrict__ nruns) {
-    extern __shared__ unsigned long long key[];
-    int P = 1;
-    while (P < N) P <<= 1;
-    for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        unsigned long long k = ~0ull;
-        if (i < N) {
-            const int64_t t = ids[i];
-            const unsigned long long id = (t >= 0 && t < V) ? static_cast<unsigned long long>(t) : 0x7fffffffull;
-            k = (id << 32) | static_cast<unsigned long long>(i);
-        }
-        key[i] = k;
-    }
+// Key of token i: id << 32 | i; ids outside [0, V) sort last (as 0x7fffffff).
+__device__ __forceinline__ unsigned long long embed_key(const int64_t* __restrict__ ids, int i, int64_t V) {
+    const int64_t t = ids[i];
+    const unsigned long long id = (t >= 0 && t < V) ? static_cast<unsigned long long>(t) : 0x7fffffffull;
+    return (id << 32) | static_cast<unsigned long long>(i);
+}
+
+// Block c sorts the keys of tokens [c * 2048, (c + 1) * 2048) ascending (bitonic in LDS).
+__global__ __launch_bounds__(1024) void embed_chunk_sort_k(const int64_t* __restrict__ ids, int N, int64_t V,
+                                                           unsigned long long* __restrict__ sk) {
+    __shared__ unsigned long long key[kSortChunk];
+    const int c0 = static_cast<int>(blockIdx.x) * kSortChunk, n = min(kSortChunk, N - c0);
+    for (int i = threadIdx.x; i < kSortChunk; i += blockDim.x) key[i] = i < n ? embed_key(ids, c0 + i, V) : ~0ull;
     __syncthreads();
-    for (int size = 2; size <= P; size <<= 1) {
+    for (int size = 2; size <= kSortChunk; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < P; i += blockDim.x) {
+            for (int i = threadIdx.x; i < kSortChunk; i += blockDim.x) {
                 const int j = i ^ stride;
                 if (j > i) {
                     const bool up = (i & size) == 0;
@@ -70,21 +72,44 @@ __global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__
             __syncthreads();
         }
     }
-    for (int i = threadIdx.x; i < N; i += blockDim.x) {
-        const unsigned long long k = key[i];
-        sorted_pos[i] = static_cast<int>(k & 0xffffffffull);
-        const int id = static_cast<int>(k >> 32);
-        sorted_id[i] = id;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sk[c0 + i] = key[i];
+}
+
+// The merged order: key g of chunk c lands at its index within c plus, for every other chunk,
+// the number of that chunk's keys below it (keys are unique, so this is a permutation).
+__global__ __launch_bounds__(256) void embed_merge_rank_k(const unsigned long long* __restrict__ sk, int N,
+                                                          int* __restrict__ sorted_pos, int* __restrict__ sorted_id) {
+    const int g = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
+    if (g >= N) return;
+    const unsigned long long k = sk[g];
+    const int c = g / kSortChunk, nchunks = (N + kSortChunk - 1) / kSortChunk;
+    int rank = g - c * kSortChunk;
+    for (int o = 0; o < nchunks; ++o) {
+        if (o == c) continue;
+        const unsigned long long* base = sk + static_cast<int64_t>(o) * kSortChunk;
+        int lo = 0, hi = min(kSortChunk, N - o * kSortChunk);  // lower bound of k in [lo, hi)
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (base[mid] < k) lo = mid + 1;
+            else hi = mid;
+        }
+        rank += lo;
     }
-    if (!run_start) return;
-    // Compact the starts of the runs of equal in-range ids: thread t owns sorted positions
-    // [t * per, (t + 1) * per); an exclusive scan of the per-thread counts gives the offsets.
+    sorted_pos[rank] = static_cast<int>(k & 0xffffffffull);
+    sorted_id[rank] = static_cast<int>(k >> 32);
+}
+
+// Starts of the runs of equal in-range ids in the sorted order, compacted: thread t owns
+// sorted positions [t * per, (t + 1) * per); an exclusive scan of the per-thread counts gives
+// the offsets.
+__global__ __launch_bounds__(1024) void embed_runs_k(const int* __restrict__ sorted_id, int N, int64_t V,
+                                                     int* __restrict__ run_start, int* __restrict__ nruns) {
     __shared__ int cnt[1024];
     const int per = (N + blockDim.x - 1) / blockDim.x;
     const int b0 = threadIdx.x * per, b1 = min(N, b0 + per);
     auto is_start = [&](int i) {
-        const unsigned long long id = key[i] >> 32;
-        return id < static_cast<unsigned long long>(V) && (i == 0 || (key[i - 1] >> 32) != id);
+        const int id = sorted_id[i];
+        return id < V && (i == 0 || sorted_id[i - 1] != id);
     };
     int c = 0;
     for (int i = b0; i < b1; ++i) c += is_start(i);
@@ -100,6 +125,29 @@ __global__ __launch_bounds__(1024) void embed_sort_k(const int64_t* __restrict__
     for (int i = b0; i < b1; ++i)
         if (is_start(i)) run_start[o++] = i;
     if (threadIdx.x == blockDim.x - 1) *nruns = cnt[threadIdx.x];
+}
+
+// Zeros for the rows of ids that occur nowhere in the sorted ids (one wave per row; a lower
+// bound over the sorted ids decides), 16-byte stores when the rows allow them.
+__global__ __launch_bounds__(256) void embed_zero_absent_k(const int* __restrict__ sorted_id, int N, int64_t V,
+                                                           float* __restrict__ dW, int64_t D, int vec) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= V) return;
+    const int lane = threadIdx.x & 63;
+    int lo = 0, hi = N;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sorted_id[mid] < row) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < N && sorted_id[lo] == row) return;
+    float* r = dW + row * D;
+    if (vec) {
+        for (int64_t c = 4 * lane; c < D; c += 256)
+            *reinterpret_cast<float4*>(r + c) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+        for (int64_t c = lane; c < D; c += 64) r[c] = 0.0f;
+    }
 }
 
 // One block of 16 waves per (run of equal ids, chunk of 8 * 64 columns), grid-striding over
@@ -221,27 +269,40 @@ void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t 
 void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, bool accumulate,
                DType dt, hipStream_t s) {
     AIC_CHECK(N >= 0 && V > 0 && D > 0, InvalidArgument, "embed_bwd: bad shape");
-    AIC_CHECK(N <= kSortMax, InvalidArgument, "embed_bwd: at most ", kSortMax, " tokens per call, got ", N);
+    AIC_CHECK(N <= kMaxTokens, InvalidArgument, "embed_bwd: at most ", kMaxTokens, " tokens per call, got ", N);
     AIC_CHECK(V < 0x7fffffffLL, InvalidArgument, "embed_bwd: vocabulary too large");
     AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "embed_bwd: dtype must be f32 or bf16");
-    if (!accumulate) AIC_HIP_CHECK(hipMemsetAsync(dW, 0, sizeof(float) * V * D, s));
-    if (N == 0) return;
+    const int vec = D % 4 == 0 && (reinterpret_cast<uintptr_t>(dW) & 15u) == 0;
+    if (N == 0) {
+        if (!accumulate) {  // every row absent
+            hipLaunchKernelGGL(embed_zero_absent_k, dim3(static_cast<unsigned>((V + 3) / 4)), dim3(256), 0, s, nullptr,
+                               0, V, dW, D, vec);
+            AIC_LAUNCH_CHECK("embed_zero_absent");
+        }
+        return;
+    }
     const size_t es = dtype_size(dt);
     const bool runs = (D * static_cast<int64_t>(es)) % (64 * 16) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15u) == 0;
+    auto* sk = static_cast<unsigned long long*>(stream_scratch(sizeof(unsigned long long) * N, s, 1));
     int* spos = static_cast<int*>(stream_scratch(sizeof(int) * (3 * N + 1), s));
     int* sid = spos + N;
     int* rstart = sid + N;
     int* nruns = rstart + N;
-    int P = 1;
-    while (P < N) P <<= 1;
-    const size_t lds = sizeof(unsigned long long) * P;
-    if (lds > 65536)
-        AIC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&embed_sort_k),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    hipLaunchKernelGGL(embed_sort_k, dim3(1), dim3(1024), lds, s, ids, static_cast<int>(N), V, spos, sid,
-                       runs ? rstart : nullptr, nruns);
-    AIC_LAUNCH_CHECK("embed_sort");
+    const int n = static_cast<int>(N);
+    hipLaunchKernelGGL(embed_chunk_sort_k, dim3(static_cast<unsigned>((N + kSortChunk - 1) / kSortChunk)), dim3(1024),
+                       0, s, ids, n, V, sk);
+    AIC_LAUNCH_CHECK("embed_chunk_sort");
+    hipLaunchKernelGGL(embed_merge_rank_k, dim3(static_cast<unsigned>((N + 255) / 256)), dim3(256), 0, s, sk, n, spos,
+                       sid);
+    AIC_LAUNCH_CHECK("embed_merge_rank");
+    if (!accumulate) {
+        hipLaunchKernelGGL(embed_zero_absent_k, dim3(static_cast<unsigned>((V + 3) / 4)), dim3(256), 0, s, sid, n, V,
+                           dW, D, vec);
+        AIC_LAUNCH_CHECK("embed_zero_absent");
+    }
     if (runs) {
+        hipLaunchKernelGGL(embed_runs_k, dim3(1), dim3(1024), 0, s, sid, n, V, rstart, nruns);
+        AIC_LAUNCH_CHECK("embed_runs");
         // one block of 16 waves per (run, 8 * 64-column chunk), at most 2048 blocks striding
         const unsigned g = static_cast<unsigned>(std::min<int64_t>(2048, N * (D * static_cast<int64_t>(es) / 1024)));
         if (dt == DType::Float32)

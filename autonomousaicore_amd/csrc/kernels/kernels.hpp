@@ -37,6 +37,11 @@ void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float*
 void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
                  int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
                  DType dt, hipStream_t s);
+// Forward and backward in one pass: ce_fwd's outputs (valid required) and the logits overwritten by
+// ce_bwd's gradient with grad (device scalar, null: 1) over the valid rows.
+void ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                float* losses, float* lse, float* loss_mean, int64_t* valid, const float* grad, DType dt,
+                hipStream_t s);
 
 // Embedding (embedding.hip)
 void embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, DType dt, hipStream_t s);

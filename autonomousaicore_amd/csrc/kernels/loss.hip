@@ -178,9 +178,95 @@ __global__ __launch_bounds__(256) void ce_bwd_bf16v(const bf16* logits, int64_t 
             float ga = (__expf(a - l) - (j + 2 * i == t ? 1.0f : 0.0f)) * scale;
             float gb = (__expf(b - l) - (j + 2 * i + 1 == t ? 1.0f : 0.0f)) * scale;
             if (ign) ga = gb = 0.0f;
-            o[i] = static_cast<uint32_t>(f2bf_bits(ga)) | (static_cast<uint32_t>(f2bf_bits(gb)) << 16);
+            o[i] = pack_bf16x2(ga, gb);
         }
         *reinterpret_cast<uint4*>(d + j) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Rows with a target other than ignore_index (single block, fixed order).
+__global__ __launch_bounds__(1024) void ce_count_k(const int64_t* __restrict__ targets, int64_t N,
+                                                   int64_t ignore_index, int64_t* valid) {
+    __shared__ long long sc[1024];
+    long long cnt = 0;
+    for (int64_t i = threadIdx.x; i < N; i += 1024) cnt += (targets[i] != ignore_index) ? 1 : 0;
+    sc[threadIdx.x] = cnt;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if (threadIdx.x < o) sc[threadIdx.x] += sc[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *valid = sc[0];
+}
+
+// Forward and backward of one bf16 row in one pass (C % 8 == 0, C <= 2048 NIT): the row is read
+// once into registers (NIT 16-byte chunks per thread, in ce_fwd_bf16v's order, so the LSE and
+// the row loss are that kernel's), then overwritten by ce_bwd_bf16v's gradient.  The target
+// logit is read before the barrier that precedes every write.
+template <int NIT>
+__global__ __launch_bounds__(256) void ce_fused_bf16v(bf16* logits, int64_t ldl, const int64_t* __restrict__ targets,
+                                                      int C, int64_t ignore_index, float* __restrict__ losses,
+                                                      float* __restrict__ lse_out, RowWeight rw) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    bf16* z = logits + row * ldl;
+    const int64_t t = targets[row];
+    const bool ign = t == ignore_index, tin = t >= 0 && t < C;
+    float zt = 0.0f;
+    if (threadIdx.x == 0 && !ign && tin) zt = bf2f(z[t]);
+    uint4 raw[NIT];
+    float m = -INFINITY, s = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int j = (it * 256 + threadIdx.x) * 8;
+        raw[it] = j < C ? *reinterpret_cast<const uint4*>(z + j) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int j = (it * 256 + threadIdx.x) * 8;
+        if (j >= C) continue;
+        const uint32_t w[4] = {raw[it].x, raw[it].y, raw[it].z, raw[it].w};
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+        float mx = v[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, v[i]);
+        if (mx > m) {
+            s *= __expf(m - mx);
+            m = mx;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += __expf(v[i] - m);
+    }
+    const float M = block_max(m, red);
+    const float part = (m == -INFINITY) ? 0.0f : s * __expf(m - M);
+    const float S = block_sum(part, red);
+    const float lse = M + logf(fmaxf(S, 1e-12f));
+    if (threadIdx.x == 0) {
+        if (lse_out) lse_out[row] = lse;
+        if (losses) losses[row] = ign ? 0.0f : (tin ? lse - zt : NAN);
+    }
+    const float scale = ign ? 0.0f : rw(row);
+    const float l = ign ? 0.0f : lse;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int j = (it * 256 + threadIdx.x) * 8;
+        if (j >= C) continue;
+        const uint32_t w[4] = {raw[it].x, raw[it].y, raw[it].z, raw[it].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xffff0000u);
+            float ga = (__expf(a - l) - (j + 2 * i == t ? 1.0f : 0.0f)) * scale;
+            float gb = (__expf(b - l) - (j + 2 * i + 1 == t ? 1.0f : 0.0f)) * scale;
+            if (ign) ga = gb = 0.0f;
+            o[i] = pack_bf16x2(ga, gb);
+        }
+        *reinterpret_cast<uint4*>(z + j) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -259,6 +345,60 @@ void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const f
     AIC_CHECK(per_row || divisor >= 0.0f, InvalidArgument, "ce_bwd_rows: negative divisor");
     ce_bwd_launch(logits, ld, targets, lse, N, C, ignore_index, RowWeight{grad, nullptr, divisor, per_row ? 1 : 0},
                   dlogits, ld_d, dt, s);
+}
+
+}  // namespace aic::hip
+
+namespace aic::hip {
+
+void ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                float* losses, float* lse, float* loss_mean, int64_t* valid, const float* grad, DType dt,
+                hipStream_t s) {
+    AIC_CHECK(N >= 0 && C > 0 && ld >= C && C < (1LL << 31) && N < (1LL << 31), InvalidArgument,
+              "ce_fwd_bwd: bad shape");
+    AIC_CHECK(valid && (targets || N == 0), InvalidArgument, "ce_fwd_bwd: targets and valid are required");
+    if (N == 0) {
+        ce_fwd(logits, ld, targets, N, C, ignore_index, losses, lse, loss_mean, valid, dt, s);
+        return;
+    }
+    DeviceBuffer hold_l, hold_s;
+    float* lp = losses;
+    float* sp = lse;
+    if (!lp) {
+        hold_l = DeviceBuffer(sizeof(float) * N, s);
+        lp = hold_l.as<float>();
+    }
+    if (!sp) {
+        hold_s = DeviceBuffer(sizeof(float) * N, s);
+        sp = hold_s.as<float>();
+    }
+    hipLaunchKernelGGL(ce_count_k, dim3(1), dim3(1024), 0, s, targets, N, ignore_index, valid);
+    AIC_LAUNCH_CHECK("ce_count");
+    const int64_t nit = (C + 2047) / 2048;
+    if (dt == DType::BFloat16 && C % 8 == 0 && ld % 8 == 0 && a16(logits) && nit <= 32) {
+        const RowWeight rw{grad, valid, 0.0f, 0};
+        const dim3 grid(static_cast<unsigned>(N));
+        bf16* z = static_cast<bf16*>(logits);
+        const int c = static_cast<int>(C);
+#define AIC_CE_FUSED(NIT) \
+    hipLaunchKernelGGL(ce_fused_bf16v<NIT>, grid, dim3(256), 0, s, z, ld, targets, c, ignore_index, lp, sp, rw)
+        if (nit <= 1) AIC_CE_FUSED(1);
+        else if (nit <= 2) AIC_CE_FUSED(2);
+        else if (nit <= 4) AIC_CE_FUSED(4);
+        else if (nit <= 8) AIC_CE_FUSED(8);
+        else if (nit <= 16) AIC_CE_FUSED(16);
+        else AIC_CE_FUSED(32);
+#undef AIC_CE_FUSED
+        AIC_LAUNCH_CHECK("ce_fused");
+    } else {
+        // two passes with the same results: the row losses and LSE, then the gradient in place
+        ce_fwd(logits, ld, targets, N, C, ignore_index, lp, sp, nullptr, nullptr, dt, s);
+        ce_bwd_launch(logits, ld, targets, sp, N, C, ignore_index, RowWeight{grad, valid, 0.0f, 0}, logits, ld, dt, s);
+    }
+    if (loss_mean) {
+        hipLaunchKernelGGL(ce_mean_k, dim3(1), dim3(1024), 0, s, lp, targets, N, ignore_index, loss_mean, valid);
+        AIC_LAUNCH_CHECK("ce_mean");
+    }
 }
 
 }  // namespace aic::hip

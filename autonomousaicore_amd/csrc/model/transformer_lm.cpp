@@ -847,7 +847,15 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     gemm(prof_, 0, 1, T, V, d, hf.get(), d, WB(head_), d, logits.get(), V, dt, dt, s);
 
     // ---- loss (cross_entropy mean, ignore_index -100, src/loss/cross_entropy.cpp:149-290) ----
-    {
+    // A training step fuses the loss's backward into its forward: the logits are read once and
+    // overwritten by their gradient (scaled by the loss scaler's current scale).
+    const float* gscale = opt_.use_loss_scaler ? &dev_->ctl.scale : one_dev_;
+    if (backward) {
+        AIC_HIP_CHECK(hipMemcpyAsync(&dev_->scale_used, &dev_->ctl.scale, sizeof(float), hipMemcpyDeviceToDevice, s));
+        auto _p = prof_.scope(kCeFwdBwd, 0.0, 2.0 * es * T * V + 28.0 * T, s);
+        hip::ce_fwd_bwd(logits.get(), V, targets, T, V, -100, nullptr, lse_ce.as<float>(), &dev_->loss, &dev_->valid,
+                        gscale, dt, s);
+    } else {
         auto _p = prof_.scope(kCeFwd, 0.0, es * T * V + 16.0 * T, s);
         hip::ce_fwd(logits.get(), V, targets, T, V, -100, nullptr, lse_ce.as<float>(), &dev_->loss, &dev_->valid, dt,
                     s);
@@ -863,13 +871,6 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     }
 
     // ---- backward (autograd::backward, src/autograd/engine.cpp:116-189, as a fixed schedule) ----
-    AIC_HIP_CHECK(hipMemcpyAsync(&dev_->scale_used, &dev_->ctl.scale, sizeof(float), hipMemcpyDeviceToDevice, s));
-    const float* gscale = opt_.use_loss_scaler ? &dev_->ctl.scale : one_dev_;
-    {
-        auto _p = prof_.scope(kCeBwd, 0.0, 2.0 * es * T * V + 12.0 * T, s);
-        hip::ce_bwd(logits.get(), V, targets, lse_ce.as<float>(), T, V, -100, gscale, &dev_->valid, logits.get(), V, dt,
-                    s);
-    }
     void* dl = logits.get();
     // dx: the residual-stream gradient at a layer's output; dxm: at its attention block's output
     // (the FFN's RMSNorm backward writes it next to dx, which the dense model's deferred

@@ -9,9 +9,9 @@ namespace aic {
 namespace {
 const char* kNames[kNumKernelClasses] = {"gemm_fwd",   "gemm_dgrad", "gemm_wgrad", "attn_fwd",   "attn_bwd",
                                           "rmsnorm_fwd", "rmsnorm_bwd", "rope",      "swiglu_fwd", "swiglu_bwd",
-                                          "ce_fwd",     "ce_bwd",     "embed_fwd",  "embed_bwd",  "grad_norm",
-                                          "adamw"};
-const bool kMfma[kNumKernelClasses] = {true,  true,  true,  true,  true,  false, false, false,
+                                          "ce_fwd",     "ce_bwd",     "ce_fwd_bwd", "embed_fwd",  "embed_bwd",
+                                          "grad_norm",  "adamw"};
+const bool kMfma[kNumKernelClasses] = {true,  true,  true,  true,  true,  false, false, false, false,
                                        false, false, false, false, false, false, false, false};
 }  // namespace
 

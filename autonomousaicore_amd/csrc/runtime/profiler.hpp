@@ -23,6 +23,7 @@ enum KernelClass : int {
     kSwigluBwd,
     kCeFwd,
     kCeBwd,
+    kCeFwdBwd,     // forward and backward in one pass (training steps)
     kEmbedFwd,
     kEmbedBwd,
     kGradNorm,

@@ -52,10 +52,12 @@ _RULES = [
     (r"rope_k|rope_v", "rope"),
     (r"swiglu_fwd", "swiglu_fwd"),
     (r"swiglu_bwd", "swiglu_bwd"),
-    (r"ce_fwd|ce_mean", "ce_fwd"),
+    # a training step's loss: count, fused forward+backward and the mean in one event scope
+    (r"ce_fused|ce_count|ce_mean", "ce_fwd_bwd"),
+    (r"ce_fwd", "ce_fwd"),
     (r"ce_bwd", "ce_bwd"),
     (r"embed_fwd", "embed_fwd"),
-    (r"embed_sort|embed_seg|embed_run", "embed_bwd"),
+    (r"embed_chunk_sort|embed_merge_rank|embed_seg|embed_run|embed_zero_absent", "embed_bwd"),
     (r"sqnorm|finalize", "grad_norm"),
     (r"adamw", "adamw"),
     # kernels outside bench.py's event classes (the MoE and QLoRA configurations)
@@ -72,8 +74,8 @@ _ANCHOR = {
     "attn_bwd": r"attn_bwd_dq",
     "rmsnorm_bwd": r"rmsnorm_bwd",
     "grad_norm": r"sqnorm_k",
-    "ce_fwd": r"ce_fwd",
-    "embed_bwd": r"embed_sort",
+    "ce_fwd_bwd": r"ce_fused",
+    "embed_bwd": r"embed_chunk_sort",
 }
 
 

@@ -193,15 +193,25 @@ int aic_hip_ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const
 int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N,
                         int64_t C, int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits,
                         int64_t ld_d, aic_dtype dt, aic_stream stream);
+/* Forward and backward of the mean loss in one pass over the logits: losses, lse, *loss_mean and
+ * *valid as aic_hip_ce_fwd (valid required), and the logits overwritten by the gradient of
+ * aic_hip_ce_bwd with grad (device scalar; NULL: 1).  bf16 rows of C % 8 == 0 up to 65536 are
+ * read once into registers and written once; other shapes run the two passes.  Results equal
+ * aic_hip_ce_fwd followed by aic_hip_ce_bwd bit for bit.
+ * Replaces: cuda_cross_entropy_forward + cuda_cross_entropy_backward (src/cuda/cuda_loss.cuh:
+ * 17-52) as CrossEntropyLoss::forward and its backward call them for one loss. */
+int aic_hip_ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
+                       float* losses, float* lse, float* loss_mean, int64_t* valid, const float* grad, aic_dtype dt,
+                       aic_stream stream);
 
 /* ---------------------------------------------------------------- embedding -------- */
 /* out[i,:] = W[ids[i],:] (zero row for ids outside [0, V)); W/out dtype dt.
  * Replaces: cuda_embedding_forward (src/cuda/cuda_embedding.cuh:10-18). */
 int aic_hip_embed_fwd(const int64_t* ids, int64_t N, const void* W, int64_t V, int64_t D, void* out, aic_dtype dt,
                       aic_stream stream);
-/* dW[v,:] (fp32) = sum over i with ids[i] == v of dout[i,:], summed in token order
+/* dW[v,:] (fp32) = sum over i with ids[i] == v of dout[i,:], summed in a fixed order
  * (deterministic; no atomics); overwrite (accumulate = 0: rows of absent ids become 0)
- * or add (accumulate = 1).
+ * or add (accumulate = 1).  N <= 2^20 tokens per call; no memset (safe to capture).
  * Replaces: cuda_embedding_backward (src/cuda/cuda_embedding.cuh:20-28). */
 int aic_hip_embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64_t D, float* dW, int accumulate,
                       aic_dtype dt, aic_stream stream);

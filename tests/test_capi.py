@@ -44,7 +44,7 @@ def test_argument_errors_are_codes():
     assert b"negative" in lib.aic_hip_last_error()
     rc = lib.aic_hip_rope(None, 8, 1, 1, 1, 7, 0, None, None, 0, _lib.AIC_F32, None)
     assert rc == 1 and b"even" in lib.aic_hip_last_error()
-    rc = lib.aic_hip_embed_bwd(None, 20000, None, 10, 4, None, 0, _lib.AIC_F32, None)
+    rc = lib.aic_hip_embed_bwd(None, (1 << 20) + 1, None, 10, 4, None, 0, _lib.AIC_F32, None)
     assert rc == 1 and b"tokens per call" in lib.aic_hip_last_error()
     # an odd INT4 group size over several groups is refused before anything is launched
     rc = lib.aic_hip_int4_quantize(None, 100, 7, None, None, _lib.AIC_F16, None)
