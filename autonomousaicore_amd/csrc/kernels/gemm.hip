@@ -12,6 +12,7 @@
 #include "gemm.hpp"
 
 #include <algorithm>
+#include <vector>
 #include <type_traits>
 
 #include "common.hpp"
@@ -365,6 +366,48 @@ void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
     if (!one_launch) {
         for (int i = 0; i < n; ++i) gemm(a[i], s);
         return;
+    }
+    if (t256 > 256 && t256 % 256 != 0 && t256 % 256 <= 64) {
+        // A few tiles past whole rounds of the chip (the 1B layer's four weight gradients: 784
+        // tiles of 256x256, 3 rounds + 16) would cost most of a fourth round.  One product gives
+        // up whole tile-columns (or tile-rows) making up the excess; they run after the launch
+        // as their own GEMM, which splits them along K over the chip (834 -> 745 us at that
+        // shape).  Taken only when the remaining tiles fall evenly on the 8 XCDs (block b runs
+        // on XCD b % 8; each product's blocks start at a multiple of 8).
+        const int64_t excess = t256 % 256, rounds = t256 / 256;
+        for (int i = n - 1; i >= 0; --i) {
+            const GemmArgs& x = a[i];
+            const int64_t tm = (x.M + 255) / 256, tn = (x.N + 255) / 256;
+            GemmArgs keep = x, cut = x;
+            const size_t es = dtype_size(x.ab), ec = dtype_size(x.c);
+            if (excess % tm == 0 && excess / tm < tn) {  // the rightmost tile-columns
+                const int64_t n0 = 256 * (tn - excess / tm);
+                keep.N = n0;
+                cut.N = x.N - n0;
+                cut.B = static_cast<const char*>(x.B) + es * (x.transB ? n0 * x.ldb : n0);
+                cut.C = static_cast<char*>(x.C) + ec * n0;
+            } else if (excess % tn == 0 && excess / tn < tm) {  // the bottom tile-rows
+                const int64_t m0 = 256 * (tm - excess / tn);
+                keep.M = m0;
+                cut.M = x.M - m0;
+                cut.A = static_cast<const char*>(x.A) + es * (x.transA ? m0 : m0 * x.lda);
+                cut.C = static_cast<char*>(x.C) + ec * m0 * x.ldc;
+            } else {
+                continue;
+            }
+            std::vector<GemmArgs> g(a, a + n);
+            g[i] = keep;
+            int64_t per_xcd[8] = {};
+            for (const GemmArgs& y : g) {
+                const int64_t t = ((y.M + 255) / 256) * ((y.N + 255) / 256);
+                for (int xcd = 0; xcd < 8; ++xcd) per_xcd[xcd] += t / 8 + (xcd < t % 8 ? 1 : 0);
+            }
+            if (*std::max_element(per_xcd, per_xcd + 8) > 32 * rounds) continue;
+            if (g[0].c == DType::Float32) dispatch_grouped<256, 256, 64, 2, float>(g.data(), n, s);
+            else dispatch_grouped<256, 256, 64, 2, bf16>(g.data(), n, s);
+            gemm(cut, s);
+            return;
+        }
     }
     if (a[0].c == DType::Float32) {
         if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, float>(a, n, s);

@@ -603,7 +603,12 @@ GROUPED_CASES = [(0, 1, [(192, 704, 256), (64, 704, 256), (448, 704, 256), (128,
                  (1, 0, [(768, 256, 1024), (256, 256, 1024)]),
                  (0, 0, [(64, 256, 128), (128, 128, 256), (256, 192, 64)]),
                  (1, 0, [(1536, 512, 2048), (512, 512, 2048)]),
-                 (1, 0, [(4096, 2048, 512), (2048, 2048, 512)])]
+                 (1, 0, [(4096, 2048, 512), (2048, 2048, 512)]),
+                 # 272 and 264 tiles of 256x256: the tiles past one round leave the launch as their
+                 # own GEMM (two tile-columns of the third product, one of them partial; the last
+                 # tile-row of the third product with A row-major)
+                 (1, 0, [(2048, 2048, 512), (4096, 2048, 512), (2048, 1800, 512), (2048, 512, 512)]),
+                 (0, 0, [(4096, 2048, 256), (2048, 2048, 256), (2304, 2048, 256)])]
 
 
 @pytest.mark.parametrize("ta,tb,shapes", GROUPED_CASES)
