@@ -100,6 +100,21 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
                  : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(g)
                  : "memory", "m0");
 }
+// The same with the global address as a wave-uniform base (SGPR pair) plus a per-lane 32-bit
+// byte offset.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, const void* lds) {
+    const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    // readfirstlane returns int: each half goes through uint32_t so the low word is not
+    // sign-extended into the high one
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+    const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | lo;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(l)), "v"(voff), "s"(bs)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ void dma4(const void* g, const void* lds) {
     const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"

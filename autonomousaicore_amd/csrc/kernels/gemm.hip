@@ -166,6 +166,7 @@ bool gemm_q4_eligible(const GemmArgs& a) {
 bool gemm_dma_eligible(const GemmArgs& a) {
     if (!gemm_mfma_eligible(a)) return false;
     if (a.K % 64 || a.M < 8 || a.N < 8) return false;
+    if (a.lda >= (int64_t{1} << 23) || a.ldb >= (int64_t{1} << 23)) return false;  // 32-bit copy offsets
     return true;
 }
 
