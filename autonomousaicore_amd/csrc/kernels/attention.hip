@@ -80,6 +80,36 @@ __device__ __forceinline__ void dma_rows64(const bf16* __restrict__ g, int64_t l
     }
 }
 
+// The same copies with the address split into a wave-uniform base (the tile's first row, in
+// SGPRs) and per-lane 32-bit byte offsets computed once per kernel, so a tile's copy costs no
+// per-lane address arithmetic; a tile reaching past nrows takes dma_rows64 (per-lane clamping).
+// Offsets stay below 2^32 for leading dimensions under 2^24 (mfma_ok).
+template <int HD>
+struct Rows64 {
+    static constexpr int NC = HD / 8, RPS = 64 / NC, PER_WAVE = 64 * HD / 512 / 4;
+    uint32_t voff[PER_WAVE];
+    int seg0;
+    __device__ __forceinline__ void init(int64_t ld) {
+        const int lane = threadIdx.x & 63;
+        seg0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * PER_WAVE;
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int row = (seg0 + i) * RPS + lane / NC;
+            const int lc = (lane % NC) ^ swz<HD>(row);
+            voff[i] = static_cast<uint32_t>(2 * (static_cast<int64_t>(row) * ld + lc * 8));
+        }
+    }
+    __device__ __forceinline__ void copy(const bf16* __restrict__ g, int64_t ld, int row0, int nrows, bf16* s) const {
+        if (row0 + 64 > nrows) {
+            dma_rows64<HD>(g, ld, row0, nrows, s);
+            return;
+        }
+        const bf16* base = g + static_cast<int64_t>(row0) * ld;
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) dma16s(base, voff[i], s + (seg0 + i) * 512);
+    }
+};
+
 // MFMA operand fragments of a swizzled [rows][HD] tile, addressed through per-lane byte
 // offsets computed once per kernel (every read is then a register base plus an immediate).
 //   row(t, rb, kk): lane = row rb + lane%32 (rb a multiple of 32), 8 values of k step kk
@@ -206,10 +236,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_pipe(const bf16* __restrict__
     const int nt = (kv_end + BKV - 1) / BKV;  // >= 1
     // tiles from `mask0` on hold keys past some query of the block (causal) or past S
     const int mask0 = min(causal ? q0 / BKV : nt, S / BKV);
-    auto copy_k = [&](int t, int st) { dma_rows64<HD>(kb, ldq, t * BKV, S, sm[st]); };
+    // head_dim 64: per-lane addressing (measured 2% faster there)
+    [[maybe_unused]] Rows64<HD> rows;
+    if constexpr (HD == 128) rows.init(ldq);
+    auto copy_rows = [&](const bf16* g, int t, bf16* dst) {
+        if constexpr (HD == 128) rows.copy(g, ldq, t * BKV, S, dst);
+        else dma_rows64<HD>(g, ldq, t * BKV, S, dst);
+    };
+    auto copy_k = [&](int t, int st) { copy_rows(kb, t, sm[st]); };
     auto unit = [&](int t, int st) {
         if (t + 1 < nt) copy_k(t + 1, st);
-        dma_rows64<HD>(vb, ldq, t * BKV, S, sm[st] + TILE);
+        copy_rows(vb, t, sm[st] + TILE);
     };
     // element e of key block jb is key k0 + 32 jb + 8 (e >> 2) + 4 hl + (e & 3)
     auto masked = [&](int k0, int jb, int e) {
@@ -468,9 +505,21 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
     const int qt0 = causal ? (k0 / BQ) : 0;
     // waves 0 and 1 also copy the 64 lse / D values of the tile (4 bytes per lane); rows past S
     // repeat row S-1 (their lse is replaced by +inf below, so they contribute nothing)
+    // head_dim 64 keeps the per-lane addressing: its two blocks per CU leave no registers for
+    // the offsets
+    [[maybe_unused]] Rows64<HD> rows_q, rows_o;
+    if constexpr (HD == 128) {
+        rows_q.init(ldq);
+        rows_o.init(ldo);
+    }
     auto copy = [&](int qt, int st) {
-        dma_rows64<HD>(q + tok0 * ldq + hoff, ldq, qt * BQ, S, sm[st]);
-        dma_rows64<HD>(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
+        if constexpr (HD == 128) {
+            rows_q.copy(q + tok0 * ldq + hoff, ldq, qt * BQ, S, sm[st]);
+            rows_o.copy(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
+        } else {
+            dma_rows64<HD>(q + tok0 * ldq + hoff, ldq, qt * BQ, S, sm[st]);
+            dma_rows64<HD>(dout + tok0 * ldo + hoff, ldo, qt * BQ, S, sm[st] + TILE);
+        }
         if (wave < 2) {
             const float* src = (wave == 0 ? lse_bh : D_bh) + min(qt * BQ + lane, S - 1);
             dma4(src, sm[st] + 2 * TILE + wave * 128);
@@ -668,9 +717,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
     const int ntiles = (kv_end + BKV - 1) / BKV;
+    Rows64<HD> rows;
+    rows.init(ldq);
     auto copy = [&](int t, int st) {
-        dma_rows64<HD>(k + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st]);
-        dma_rows64<HD>(v + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st] + TILE);
+        rows.copy(k + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st]);
+        rows.copy(v + tok0 * ldq + hoff, ldq, t * BKV, S, sm[st] + TILE);
     };
     if (ntiles > 0) copy(0, 0);
     if (ntiles > 1) copy(1, 1);
@@ -968,7 +1019,8 @@ __global__ __launch_bounds__(256) void attn_cached_k(const T* __restrict__ q, in
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool mfma_ok(const void* q, const void* k, const void* v, int64_t ldq, const void* o, int64_t ldo, int64_t hd) {
-    return (hd == 64 || hd == 128) && ldq % 8 == 0 && ldo % 8 == 0 && a16(q) && a16(k) && a16(v) && a16(o);
+    return (hd == 64 || hd == 128) && ldq % 8 == 0 && ldo % 8 == 0 && a16(q) && a16(k) && a16(v) && a16(o) &&
+           ldq < (int64_t{1} << 24) && ldo < (int64_t{1} << 24);  // 32-bit copy offsets (Rows64)
 }
 
 template <typename T>
