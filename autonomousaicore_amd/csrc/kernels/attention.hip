@@ -543,7 +543,12 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
         if (NST == 3 && qt + 2 < nq) copy(qt + 2, (it + 2) % NST);
         const int qs = qt * BQ;
         // every query of the tile precedes this wave's keys: nothing to do
-        if (!causal || qs + BQ - 1 >= kw) {
+        // EDGE: the tile holds queries before some key of this wave (causal) or past S, so the
+        // mask and the past-S rows are applied; other tiles skip those selects (wave-uniform)
+        const bool tail = qs + BQ > S;
+        const bool edge = (causal && qs < kw + 31) || tail;
+        auto work = [&](auto edge_c) {
+        constexpr bool EDGE = decltype(edge_c)::value;
         const char* Qb = reinterpret_cast<const char*>(sm[st]);
         const char* Ob = reinterpret_cast<const char*>(sm[st] + TILE);
         const float* Ls = reinterpret_cast<const float*>(sm[st] + 2 * TILE);
@@ -551,7 +556,6 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
         // element e of query block jb is query qs + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked
         // when its offset 32 jb + 8 (e >> 2) + (e & 3) is below lo (causal: key > query)
         const int lo = causal ? mykey - qs - 4 * hl : -(1 << 30);
-        const bool tail = qs + BQ > S;
 
         f32x16 sa[2], sd[2];
 #pragma unroll
@@ -575,14 +579,15 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     // queries past S: p = exp2(-inf) = 0
-                    nl[jb][4 * g4 + u] = (tail && qs + qi + u >= S) ? -INFINITY : -lv[u] * kLog2e;
+                    if constexpr (EDGE) nl[jb][4 * g4 + u] = qs + qi + u >= S ? -INFINITY : -lv[u] * kLog2e;
+                    else nl[jb][4 * g4 + u] = -lv[u] * kLog2e;
                     dd[jb][4 * g4 + u] = dv4[u];
                 }
             }
         };
         auto softmax = [&](int jb, int e) {
             float p = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, nl[jb][e]));
-            p = (32 * jb + 8 * (e >> 2) + (e & 3) < lo) ? 0.0f : p;
+            if constexpr (EDGE) p = (32 * jb + 8 * (e >> 2) + (e & 3) < lo) ? 0.0f : p;
             sa[jb][e] = p;
             sd[jb][e] = p * (sd[jb][e] - dd[jb][e]);
         };
@@ -655,6 +660,10 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        };
+        if (!causal || qs + BQ - 1 >= kw) {
+            if (edge) work(std::true_type{});
+            else work(std::false_type{});
         }
         if constexpr (NST == 2) {  // every wave is done with stage st before tile qt+2 lands there
             wait_lds();
@@ -726,8 +735,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
     if (ntiles > 0) copy(0, 0);
     if (ntiles > 1) copy(1, 1);
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int st = t & 1;
+    // one K/V tile; ST: its stage (a compile-time constant in the paired loop below, so the
+    // fragment reads address LDS through immediates)
+    auto tile = [&](int t, auto stc) {
+        constexpr int ST0 = decltype(stc)::value;
+        const int st = ST0 >= 0 ? ST0 : (t & 1);
         if (t + 1 < ntiles) wait_vmcnt<LPT>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
@@ -750,18 +762,30 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
                     dp[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.row(Vb, jb * 32, kk), df[kk], dp[jb], 0,
                                                                       0, 0);
                 }
-            const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S || myq >= S;
+            // wave-uniform: the tile holds keys past some query of the wave (causal) or past S.
+            // Queries past S need no mask: their q, dO, lse and D are 0, so dS = 1 * (0 - 0) = 0.
+            const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S;
+            // element (jb, e) is key k0 + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked when its
+            // offset 32 jb + 8 (e >> 2) + (e & 3) exceeds lim
+            const int lim = min(causal ? myq : S - 1, S - 1) - k0 - 4 * hl;
+            if (diag) {
 #pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
+                for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
-                    if (diag) {
-                        const int key = k0 + jb * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-                        if (key >= S || myq >= S || (causal && key > myq)) p = 0.0f;
+                    for (int e = 0; e < 16; ++e) {
+                        float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
+                        p = (32 * jb + 8 * (e >> 2) + (e & 3) > lim) ? 0.0f : p;
+                        dp[jb][e] = p * (dp[jb][e] - my_D);
                     }
-                    dp[jb][e] = p * (dp[jb][e] - my_D);
-                }
+            } else {
+#pragma unroll
+                for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
+                        dp[jb][e] = p * (dp[jb][e] - my_D);
+                    }
+            }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
@@ -774,7 +798,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
         wait_lds();
         __builtin_amdgcn_s_barrier();
         if (t + 2 < ntiles) copy(t + 2, st);
+    };
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+        tile(t, std::integral_constant<int, 0>{});
+        tile(t + 1, std::integral_constant<int, 1>{});
     }
+    if (t < ntiles) tile(t, std::integral_constant<int, 0>{});
 
     if (myq < S) {
         bf16* dqp = dq + (tok0 + myq) * ldd + hoff;
