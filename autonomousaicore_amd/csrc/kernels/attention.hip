@@ -689,10 +689,10 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                            const bf16* __restrict__ v, int64_t ldq,
-                                                           const bf16* __restrict__ dout, int64_t ldo,
-                                                           const float* __restrict__ lse, const float* __restrict__ Dg,
-                                                           bf16* __restrict__ dq, int64_t ldd, int H, int S, float c,
-                                                           float scale, int causal) {
+                                                           const bf16* __restrict__ o, const bf16* __restrict__ dout,
+                                                           int64_t ldo, const float* __restrict__ lse,
+                                                           float* __restrict__ Dg, bf16* __restrict__ dq, int64_t ldd,
+                                                           int H, int S, float c, float scale, int causal) {
     constexpr int BQ = 128, BKV = 64, KS = HD / 16, OB = HD / 32, TILE = BKV * HD;
     constexpr int LPT = 2 * (64 * HD / 512 / 4);
     __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];
@@ -717,7 +717,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
         }
     }
     const float my_l2 = myq < S ? lse[(static_cast<int64_t>(b) * H + h) * S + myq] * kLog2e : 0.0f;
-    const float my_D = myq < S ? Dg[(static_cast<int64_t>(b) * H + h) * S + myq] : 0.0f;
+    // D = sum over head_dim of dO * O (fp32) for this lane's query: the lane's half of the row
+    // (the chunks its dO fragments hold), then the other half from lane ^ 32.  Written out for
+    // the dK/dV kernel, which runs after this one.
+    float my_D;
+    {
+        const bf16* op = o + (tok0 + myq) * ldo + hoff + 8 * hl;
+        float part = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const uint4 ov = ldg16(op + 16 * kk, myq < S);
+            const uint4 dv = __builtin_bit_cast(uint4, df[kk]);
+            const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                part = fmaf(__uint_as_float(dw[i] << 16), __uint_as_float(ow[i] << 16), part);
+                part = fmaf(__uint_as_float(dw[i] & 0xffff0000u), __uint_as_float(ow[i] & 0xffff0000u), part);
+            }
+        }
+        my_D = part + __shfl_xor(part, 32, 64);
+        if (hl == 0 && myq < S) Dg[(static_cast<int64_t>(b) * H + h) * S + myq] = my_D;
+    }
     Frags<HD> F;
     F.init();
     f32x16 dqt[OB];
@@ -735,8 +755,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
     if (ntiles > 0) copy(0, 0);
     if (ntiles > 1) copy(1, 1);
 
-    // one K/V tile; ST: its stage (a compile-time constant in the paired loop below, so the
-    // fragment reads address LDS through immediates)
+    // one K/V tile (stc: its stage when known at compile time, else -1)
     auto tile = [&](int t, auto stc) {
         constexpr int ST0 = decltype(stc)::value;
         const int st = ST0 >= 0 ? ST0 : (t & 1);
@@ -766,26 +785,16 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
             // Queries past S need no mask: their q, dO, lse and D are 0, so dS = 1 * (0 - 0) = 0.
             const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S;
             // element (jb, e) is key k0 + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked when its
-            // offset 32 jb + 8 (e >> 2) + (e & 3) exceeds lim
-            const int lim = min(causal ? myq : S - 1, S - 1) - k0 - 4 * hl;
-            if (diag) {
+            // offset 32 jb + 8 (e >> 2) + (e & 3) exceeds lim (past every offset off the diagonal)
+            const int lim = diag ? min(causal ? myq : S - 1, S - 1) - k0 - 4 * hl : BKV;
 #pragma unroll
-                for (int jb = 0; jb < 2; ++jb)
+            for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
-                        p = (32 * jb + 8 * (e >> 2) + (e & 3) > lim) ? 0.0f : p;
-                        dp[jb][e] = p * (dp[jb][e] - my_D);
-                    }
-            } else {
-#pragma unroll
-                for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
-                        dp[jb][e] = p * (dp[jb][e] - my_D);
-                    }
-            }
+                for (int e = 0; e < 16; ++e) {
+                    float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
+                    p = (32 * jb + 8 * (e >> 2) + (e & 3) > lim) ? 0.0f : p;
+                    dp[jb][e] = p * (dp[jb][e] - my_D);
+                }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 dsf = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
@@ -799,12 +808,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
         __builtin_amdgcn_s_barrier();
         if (t + 2 < ntiles) copy(t + 2, st);
     };
-    int t = 0;
-    for (; t + 1 < ntiles; t += 2) {
-        tile(t, std::integral_constant<int, 0>{});
-        tile(t + 1, std::integral_constant<int, 1>{});
-    }
-    if (t < ntiles) tile(t, std::integral_constant<int, 0>{});
+    // (a loop over stage pairs, with the stage a compile-time constant, spills here)
+    for (int t = 0; t < ntiles; ++t) tile(t, std::integral_constant<int, -1>{});
 
     if (myq < S) {
         bf16* dqp = dq + (tok0 + myq) * ldd + hoff;
@@ -1134,6 +1139,31 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
               "attn_bwd: sequence too long");
     if (B == 0 || S == 0) return;
     float* D = static_cast<float*>(stream_scratch(sizeof(float) * B * H * S, s));
+    if (dt == DType::BFloat16 && mfma_ok(q, k, v, ld_qkv, dout, ld_o, hd) && ld_d % 8 == 0 && a16(dq) && a16(dk) &&
+        a16(dv) && a16(o)) {
+        // the dQ kernel computes D = rowsum(dO * O) for its queries and writes it for dK/dV
+        const float sl2 = scale * kLog2e;
+        const dim3 grid(static_cast<unsigned>(((S + 127) / 128) * H * B));
+#define AIC_BWD_MFMA(HD_)                                                                                        \
+    do {                                                                                                          \
+        hipLaunchKernelGGL(attn_bwd_dq_mfma<HD_>, grid, dim3(256), 0, s, static_cast<const bf16*>(q),             \
+                           static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
+                           static_cast<const bf16*>(o), static_cast<const bf16*>(dout), ld_o, lse, D,              \
+                           static_cast<bf16*>(dq), ld_d, static_cast<int>(H), static_cast<int>(S), sl2, scale,      \
+                           causal ? 1 : 0);                                                                        \
+        AIC_LAUNCH_CHECK("attn_bwd_dq_mfma");                                                                      \
+        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<HD_>, grid, dim3(256), 0, s, static_cast<const bf16*>(q),           \
+                           static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
+                           static_cast<const bf16*>(dout), ld_o, lse, D, static_cast<bf16*>(dk),                   \
+                           static_cast<bf16*>(dv), ld_d, static_cast<int>(H), static_cast<int>(S), sl2, scale,      \
+                           causal ? 1 : 0);                                                                        \
+        AIC_LAUNCH_CHECK("attn_bwd_dkdv_mfma");                                                                    \
+    } while (0)
+        if (hd == 128) AIC_BWD_MFMA(128);
+        else AIC_BWD_MFMA(64);
+#undef AIC_BWD_MFMA
+        return;
+    }
     const int64_t waves = B * S * H;
     const unsigned dgrid = static_cast<unsigned>((waves * 64 + 255) / 256);
     const bool al16 = (reinterpret_cast<uintptr_t>(o) & 15u) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15u) == 0;
@@ -1163,30 +1193,6 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
         AIC_THROW(DTypeMismatch, "attn_bwd: dtype must be f32 or bf16");
     AIC_LAUNCH_CHECK("attn_dot");
 
-    if (dt == DType::BFloat16 && mfma_ok(q, k, v, ld_qkv, dout, ld_o, hd) && ld_d % 8 == 0 && a16(dq) && a16(dk) &&
-        a16(dv)) {
-        const float sl2 = scale * kLog2e;
-        const dim3 gkv(static_cast<unsigned>(((S + 127) / 128) * H * B));
-        const dim3 gq(static_cast<unsigned>(((S + 127) / 128) * H * B));
-#define AIC_BWD_MFMA(HD_)                                                                                        \
-    do {                                                                                                          \
-        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<HD_>, gkv, dim3(256), 0, s, static_cast<const bf16*>(q),            \
-                           static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
-                           static_cast<const bf16*>(dout), ld_o, lse, D, static_cast<bf16*>(dk),                   \
-                           static_cast<bf16*>(dv), ld_d, static_cast<int>(H), static_cast<int>(S), sl2, scale,      \
-                           causal ? 1 : 0);                                                                        \
-        AIC_LAUNCH_CHECK("attn_bwd_dkdv_mfma");                                                                    \
-        hipLaunchKernelGGL(attn_bwd_dq_mfma<HD_>, gq, dim3(256), 0, s, static_cast<const bf16*>(q),               \
-                           static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
-                           static_cast<const bf16*>(dout), ld_o, lse, D, static_cast<bf16*>(dq), ld_d,             \
-                           static_cast<int>(H), static_cast<int>(S), sl2, scale, causal ? 1 : 0);                  \
-        AIC_LAUNCH_CHECK("attn_bwd_dq_mfma");                                                                      \
-    } while (0)
-        if (hd == 128) AIC_BWD_MFMA(128);
-        else AIC_BWD_MFMA(64);
-#undef AIC_BWD_MFMA
-        return;
-    }
     if (dt == DType::Float32) bwd_simt<float>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
     else bwd_simt<bf16>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
 }
