@@ -242,6 +242,17 @@ int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv
     });
 }
 
+int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
+                          int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B,
+                          int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,
+                          const float* sin_t, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(cos_t && sin_t, InvalidArgument, "attn_bwd_rope: cos_t and sin_t are required");
+        aic::hip::attn_bwd(q, k, v, ld_qkv, o, dout, ld_o, lse, dq, dk, dv, ld_d, B, H, S, hd, causal != 0, scale,
+                           dt(d), st(stream), cos_t, sin_t);
+    });
+}
+
 int aic_hip_swiglu_fwd(const void* g, const void* u, int64_t ld_gu, void* h, int64_t ld_h, int64_t T, int64_t f,
                        aic_dtype d, aic_stream stream) {
     return guard([&] { aic::hip::swiglu_fwd(g, u, ld_gu, h, ld_h, T, f, dt(d), st(stream)); });

@@ -180,6 +180,37 @@ __device__ __forceinline__ void store_t(bf16* row_ptr, const f32x16& acc, int ob
 
 // ---------------------------------------------------------------------------------------
 // Forward
+// store_t of a whole [head_dim] x [lane = token] accumulator with the adjoint of the half-split
+// rotary embedding applied on the way out (RoPEBackward, include/nn/rope.hpp:23-112, as rope_k
+// with INV): for d < head_dim / 2, with a1 = mul acc[d] and a2 = mul acc[d + head_dim / 2],
+// out[d] = a1 cos + a2 sin and out[d + head_dim / 2] = a2 cos - a1 sin, where cos / sin are the
+// token's table rows.  The partner of row d sits in block ob + OB / 2 of the same lane.
+template <int OB>
+__device__ __forceinline__ void store_rot(bf16* row_ptr, const f32x16 (&acc)[OB], float mul, const float* cos_row,
+                                          const float* sin_row) {
+    constexpr int HALF = OB * 16;
+    const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int ob = 0; ob < OB / 2; ++ob)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = ob * 32 + 8 * g + 4 * h;
+            const float4 c4 = *reinterpret_cast<const float4*>(cos_row + d0);
+            const float4 s4 = *reinterpret_cast<const float4*>(sin_row + d0);
+            const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+            float o1[4], o2[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float a1 = acc[ob][4 * g + u] * mul, a2 = acc[ob + OB / 2][4 * g + u] * mul;
+                o1[u] = a1 * cc[u] + a2 * ss[u];
+                o2[u] = a2 * cc[u] - a1 * ss[u];
+            }
+            *reinterpret_cast<uint2*>(row_ptr + d0) = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
+            *reinterpret_cast<uint2*>(row_ptr + HALF + d0) =
+                make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
+        }
+}
+
 // ---------------------------------------------------------------------------------------
 // Forward, software-pipelined.  Copy unit t holds K of tile t+1 and V of tile t, so while a wave
 // multiplies P(t) V(t) it already holds the scores of tile t+1.  Per iteration two MFMA groups,
@@ -459,7 +490,8 @@ template <int HD>
 __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int64_t ldq,
     const bf16* __restrict__ dout, int64_t ldo, const float* __restrict__ lse, const float* __restrict__ Dg,
-    bf16* __restrict__ dk, bf16* __restrict__ dv, int64_t ldd, int H, int S, float c, float scale, int causal) {
+    bf16* __restrict__ dk, bf16* __restrict__ dv, int64_t ldd, int H, int S, float c, float scale, int causal,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
     constexpr int BQ = 64, BKV = 128, KS = HD / 16, OB = HD / 32, TILE = BQ * HD;
     constexpr int LPT = 2 * (64 * HD / 512 / 4);
     constexpr int NST = HD == 128 ? 3 : 2;
@@ -675,11 +707,15 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
     if (mykey < S) {
         bf16* dkp = dk + (tok0 + mykey) * ldd + hoff;
         bf16* dvp = dv + (tok0 + mykey) * ldd + hoff;
+        if (rope_cos) {  // dK leaves with the rotary embedding's adjoint applied
+            store_rot<OB>(dkp, dkt, scale, rope_cos + static_cast<int64_t>(mykey) * (HD / 2),
+                          rope_sin + static_cast<int64_t>(mykey) * (HD / 2));
+        } else {
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob) {
-            store_t(dkp, dkt[ob], ob, scale);
-            store_t(dvp, dvt[ob], ob, 1.0f);
+            for (int ob = 0; ob < OB; ++ob) store_t(dkp, dkt[ob], ob, scale);
         }
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob) store_t(dvp, dvt[ob], ob, 1.0f);
     }
 }
 
@@ -692,7 +728,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
                                                            const bf16* __restrict__ o, const bf16* __restrict__ dout,
                                                            int64_t ldo, const float* __restrict__ lse,
                                                            float* __restrict__ Dg, bf16* __restrict__ dq, int64_t ldd,
-                                                           int H, int S, float c, float scale, int causal) {
+                                                           int H, int S, float c, float scale, int causal,
+                                                           const float* __restrict__ rope_cos,
+                                                           const float* __restrict__ rope_sin) {
     constexpr int BQ = 128, BKV = 64, KS = HD / 16, OB = HD / 32, TILE = BKV * HD;
     constexpr int LPT = 2 * (64 * HD / 512 / 4);
     __shared__ __attribute__((aligned(16))) bf16 sm[2][2 * TILE];
@@ -813,8 +851,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
 
     if (myq < S) {
         bf16* dqp = dq + (tok0 + myq) * ldd + hoff;
+        if (rope_cos) {  // dQ leaves with the rotary embedding's adjoint applied
+            store_rot<OB>(dqp, dqt, scale, rope_cos + static_cast<int64_t>(myq) * (HD / 2),
+                          rope_sin + static_cast<int64_t>(myq) * (HD / 2));
+        } else {
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob) store_t(dqp, dqt[ob], ob, scale);
+            for (int ob = 0; ob < OB; ++ob) store_t(dqp, dqt[ob], ob, scale);
+        }
     }
 }
 
@@ -1132,7 +1175,9 @@ void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void*
 
 void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
               int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
-              int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s) {
+              int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s, const float* rope_cos,
+              const float* rope_sin) {
+    AIC_CHECK((rope_cos == nullptr) == (rope_sin == nullptr), InvalidArgument, "attn_bwd: rope tables come in pairs");
     AIC_CHECK(B >= 0 && H > 0 && S >= 0 && hd > 0 && ld_qkv >= H * hd && ld_o >= H * hd && ld_d >= H * hd,
               InvalidArgument, "attn_bwd: bad shape");
     AIC_CHECK(S < (1LL << 30) && B * S < (1LL << 31) && ((S + 127) / 128) * H * B < (1LL << 31), InvalidArgument,
@@ -1150,13 +1195,13 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
                            static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
                            static_cast<const bf16*>(o), static_cast<const bf16*>(dout), ld_o, lse, D,              \
                            static_cast<bf16*>(dq), ld_d, static_cast<int>(H), static_cast<int>(S), sl2, scale,      \
-                           causal ? 1 : 0);                                                                        \
+                           causal ? 1 : 0, rope_cos, rope_sin);                                                    \
         AIC_LAUNCH_CHECK("attn_bwd_dq_mfma");                                                                      \
         hipLaunchKernelGGL(attn_bwd_dkdv_mfma<HD_>, grid, dim3(256), 0, s, static_cast<const bf16*>(q),           \
                            static_cast<const bf16*>(k), static_cast<const bf16*>(v), ld_qkv,                       \
                            static_cast<const bf16*>(dout), ld_o, lse, D, static_cast<bf16*>(dk),                   \
                            static_cast<bf16*>(dv), ld_d, static_cast<int>(H), static_cast<int>(S), sl2, scale,      \
-                           causal ? 1 : 0);                                                                        \
+                           causal ? 1 : 0, rope_cos, rope_sin);                                                    \
         AIC_LAUNCH_CHECK("attn_bwd_dkdv_mfma");                                                                    \
     } while (0)
         if (hd == 128) AIC_BWD_MFMA(128);
@@ -1195,6 +1240,10 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
 
     if (dt == DType::Float32) bwd_simt<float>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
     else bwd_simt<bf16>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
+    if (rope_cos) {  // the rotary embedding's adjoint as its own pass on these paths
+        rope(dq, ld_d, B, S, H, hd, 0, rope_cos, rope_sin, true, dt, s);
+        rope(dk, ld_d, B, S, H, hd, 0, rope_cos, rope_sin, true, dt, s);
+    }
 }
 
 void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,

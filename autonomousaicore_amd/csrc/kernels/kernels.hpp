@@ -97,9 +97,12 @@ void sum_to_shape(const float* g, int ndim, const int64_t* shape, int tr, const 
 // Attention (attention.hip)
 void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
               int64_t B, int64_t H, int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);
+// rope_cos / rope_sin ([S][hd / 2] tables, positions 0..S-1 of each sequence): dq and dk leave
+// with the half-split rotary embedding's adjoint applied (rope(..., inverse = true) fused).
 void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
               int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
-              int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s);
+              int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s,
+              const float* rope_cos = nullptr, const float* rope_sin = nullptr);
 // Queries of S_new new tokens (rows of q, [B*S_new] x ldq) at positions start_pos.. against a
 // KV cache kc / vc ([B][cache_rows][ldkv], positions 0 .. start_pos+S_new-1 filled), causal.
 void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,

@@ -948,15 +948,13 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         gemm(prof_, 0, 0, T, d, d, dxm.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
              1.0f, ql ? &lo_ : nullptr, wq(ly, 3));
         {
-            // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not
+            // counted as dP, dV, dK, dQ (twice the forward); the recomputed S = Q K^T is not.  The
+            // rotary embedding's backward (RoPEBackward) leaves the kernels with dq and dk.
             auto _p = prof_.scope(kAttnBwd, 2.0 * attn_flops, 8.0 * es * T * d, s);
             hip::attn_bwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,
                           dh.get(), d, atf(lse, l * T * H), dqkv.get(), static_cast<char*>(dqkv.get()) + es * d,
-                          static_cast<char*>(dqkv.get()) + es * 2 * d, 3 * d, B, H, S, hd, true, scale, dt, s);
-        }
-        {
-            auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
-            hip::rope(dqkv.get(), 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, true, dt, s);
+                          static_cast<char*>(dqkv.get()) + es * 2 * d, 3 * d, B, H, S, hd, true, scale, dt, s,
+                          cos_dev_, sin_dev_);
         }
         LowRank lq{};
         if (ql) {

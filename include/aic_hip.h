@@ -158,6 +158,15 @@ int aic_hip_attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv
 int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
                      int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
                      int64_t S, int64_t hd, int causal, float scale, aic_dtype dt, aic_stream stream);
+/* The same with the half-split rotary embedding's backward applied to dq and dk on the way out
+ * (cos_t / sin_t: [S][hd / 2] tables as aic_hip_rope_tables builds them, positions 0..S-1 of
+ * each sequence), as the attention layer's backward runs it right after the attention.
+ * Replaces: launch_flash_attention_backward_gpu followed by RoPEBackward on the q and k
+ * gradients (src/cuda/cuda_flash_attention.cuh:30-46, include/nn/rope.hpp:23-112). */
+int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
+                          int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B,
+                          int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,
+                          const float* sin_t, aic_dtype dt, aic_stream stream);
 
 /* ---------------------------------------------------------------- SwiGLU ----------- */
 /* h = silu(g) * u, silu(x) = x / (1 + exp(-x)); g, u, h [T, f] with leading dims ld_gu, ld_h.

@@ -496,6 +496,53 @@ def test_attention_bf16_mfma(orc, B, S, H, hd, causal):
     np.testing.assert_array_equal(host(dqkv2), g)
 
 
+@pytest.mark.parametrize("B,S,H,hd,causal", [(2, 256, 2, 128, 1), (1, 200, 3, 64, 1), (2, 130, 2, 128, 0),
+                                               (1, 72, 1, 64, 0)])
+def test_attention_bwd_with_rope(orc, B, S, H, hd, causal):
+    """aic_hip_attn_bwd_rope = aic_hip_attn_bwd then the rotary embedding's inverse (RoPEBackward)
+    on dq and dk: dv bit-identical, dq / dk within one bf16 rounding (the fused form rotates the
+    fp32 accumulator instead of its bf16 copy), and both against the oracle's attention backward
+    followed by its RoPE backward."""
+    rng = np.random.default_rng(S + 3 * hd + H + causal)
+    d = H * hd
+    qkv = bf16_round(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+    do = bf16_round(rng.standard_normal((B * S, d)).astype(np.float32))
+    cos_t = np.empty((S, hd // 2), np.float32)
+    sin_t = np.empty_like(cos_t)
+    _lib.check(_lib.load().aic_hip_rope_tables(cos_t.ctypes.data, sin_t.ctypes.data, S, hd, 10000.0))
+    cd, sd = dev(cos_t), dev(sin_t)
+    x = dev(qkv, torch.bfloat16)
+    o = torch.empty((B * S, d), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    sc = 1.0 / np.sqrt(hd)
+    call("aic_hip_attn_fwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), d, ptr(lse), B, H, S, hd, causal,
+         sc, BF16, stream())
+    dod = dev(do, torch.bfloat16)
+    sep = torch.empty_like(x)
+    call("aic_hip_attn_bwd", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
+         ptr(lse), ptr(sep), ptr(sep) + 2 * d, ptr(sep) + 4 * d, 3 * d, B, H, S, hd, causal, sc, BF16, stream())
+    call("aic_hip_rope", ptr(sep), 3 * d, B, S, 2 * H, hd, 0, ptr(cd), ptr(sd), 1, BF16, stream())
+    fused = torch.empty_like(x)
+    call("aic_hip_attn_bwd_rope", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
+         ptr(lse), ptr(fused), ptr(fused) + 2 * d, ptr(fused) + 4 * d, 3 * d, B, H, S, hd, causal, sc,
+         ptr(cd), ptr(sd), BF16, stream())
+    f, g = host(fused), host(sep)
+    np.testing.assert_array_equal(f[:, 2 * d:], g[:, 2 * d:])
+    assert rel(f[:, :2 * d], g[:, :2 * d]) < 4e-3
+    q, k, v = (np.ascontiguousarray(qkv[:, i * d:(i + 1) * d]) for i in range(3))
+    _, E, rs = orc.attention_fwd(q, k, v, B, S, H, hd, causal=bool(causal))
+    dq_ref, dk_ref, _ = orc.attention_bwd(q, k, v, E, rs, do, B, S, H, hd)
+    # the oracle's RoPE backward of the oracle's attention gradients
+    assert rel(f[:, :d], orc.rope_bwd(dq_ref, B, S, H, hd)) < 2e-2
+    assert rel(f[:, d:2 * d], orc.rope_bwd(dk_ref, B, S, H, hd)) < 2e-2
+    # deterministic
+    again = torch.empty_like(x)
+    call("aic_hip_attn_bwd_rope", ptr(x), ptr(x) + 2 * d, ptr(x) + 4 * d, 3 * d, ptr(o), ptr(dod), d,
+         ptr(lse), ptr(again), ptr(again) + 2 * d, ptr(again) + 4 * d, 3 * d, B, H, S, hd, causal, sc,
+         ptr(cd), ptr(sd), BF16, stream())
+    np.testing.assert_array_equal(host(again), f)
+
+
 # ----------------------------------------------------------------------------- optimizer tail
 def test_grad_sqnorm_and_nonfinite():
     rng = np.random.default_rng(41)
