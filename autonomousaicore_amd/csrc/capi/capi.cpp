@@ -242,6 +242,35 @@ int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv
     });
 }
 
+int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
+                      void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq, int64_t start_pos,
+                      const float* cos_t, const float* sin_t, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(cos_t && sin_t, InvalidArgument, "gemm_rope: cos_t and sin_t are required");
+        aic::hip::GemmArgs a;
+        a.transA = 0;
+        a.transB = 1;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.A = A;
+        a.lda = lda;
+        a.B = W;
+        a.ldb = ldw;
+        a.C = C;
+        a.ldc = ldc;
+        a.ab = aic::DType::BFloat16;
+        a.c = aic::DType::BFloat16;
+        a.rope_cos = cos_t;
+        a.rope_sin = sin_t;
+        a.rope_cols = rope_cols;
+        a.rope_hd = hd;
+        a.rope_seq = seq;
+        a.rope_start = start_pos;
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
                           int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B,
                           int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,

@@ -17,6 +17,7 @@
 
 #include "common.hpp"
 #include "gemm_launch.hpp"
+#include "kernels.hpp"
 #include "../runtime/memory_pool.hpp"
 
 namespace aic::hip {
@@ -267,6 +268,24 @@ void gemm(const GemmArgs& a, hipStream_t s) {
                   "low-rank term: leading dimension smaller than the row length");
     }
     if (a.M == 0 || a.N == 0) return;
+    if (a.rope_cos) {
+        AIC_CHECK(a.rope_sin && a.rope_hd > 0 && a.rope_hd % 2 == 0 && a.rope_cols % a.rope_hd == 0 &&
+                      a.rope_cols <= a.N && a.rope_seq > 0 && a.M % a.rope_seq == 0 && a.beta == 0.0f && !a.R,
+                  InvalidArgument, "GEMM rotary epilogue: bad rope arguments");
+        // in the epilogue: bf16 output on full 256x256 tiles of the eight-wave plain path, heads
+        // of 128 that the 64-column wave sub-tiles split in halves
+        const bool fused = !a.Bq && a.c == DType::BFloat16 && a.rope_hd == 128 && gemm_impl::kDmaWaves256 == 8 &&
+                           gemm_dma_eligible(a) && a.M % 256 == 0 && a.N % 256 == 0 && a.rope_cols % 256 == 0 &&
+                           a.ldc % 8 == 0 && aligned16(a.C) && ((a.M / 256) * (a.N / 256) >= 128) && a.r2 == 0;
+        if (!fused) {
+            GemmArgs b = a;
+            b.rope_cos = b.rope_sin = nullptr;
+            gemm(b, s);
+            rope(a.C, a.ldc, a.M / a.rope_seq, a.rope_seq, a.rope_cols / a.rope_hd, a.rope_hd, a.rope_start,
+                 a.rope_cos, a.rope_sin, false, a.c, s);
+            return;
+        }
+    }
     if (a.Bq) {
         gemm_q4(a, s);
         return;

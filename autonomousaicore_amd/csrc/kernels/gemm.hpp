@@ -48,6 +48,14 @@ struct GemmArgs {
     const void* Bscale = nullptr;
     DType scale_t = DType::Float16;
     int64_t group = 0;
+    // Optional rotary embedding of the output (the attention projection's q and k): columns
+    // [0, rope_cols) of C are heads of rope_hd values that leave rotated by the half-split RoPE
+    // (rope(), RotaryPositionEmbedding::forward) at position rope_start + row % rope_seq, with
+    // rope_cos / rope_sin the [positions][rope_hd / 2] tables.  Done in the GEMM's epilogue for
+    // bf16 output on full 256x256 tiles with rope_hd 128; otherwise rope() runs after it.
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    int64_t rope_cols = 0, rope_hd = 0, rope_seq = 0, rope_start = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);

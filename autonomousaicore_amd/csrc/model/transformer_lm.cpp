@@ -52,9 +52,17 @@ struct Q4B {
     int64_t group = 0;
 };
 
+// The rotary embedding of the product's first `cols` columns (the q and k heads; GemmArgs::rope_*).
+struct RopeOut {
+    const float* cos = nullptr;
+    const float* sin = nullptr;
+    int64_t cols = 0, hd = 0, seq = 0, start = 0;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
-          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {}) {
+          int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {},
+          RopeOut rope = {}) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
     // INT4 operand: half a byte per weight plus one fp16 scale per group
@@ -94,6 +102,14 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.Bscale = q4.scales;
         a.scale_t = DType::Float16;
         a.group = q4.group;
+    }
+    if (rope.cos) {
+        a.rope_cos = rope.cos;
+        a.rope_sin = rope.sin;
+        a.rope_cols = rope.cols;
+        a.rope_hd = rope.hd;
+        a.rope_seq = rope.seq;
+        a.rope_start = rope.start;
     }
     hip::gemm(a, s);
 }
@@ -793,12 +809,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xaq(l), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lq = LowRank{xaq(l), 3 * r, W(ly.bq), r, r, d, 0};
         }
+        // q and k leave the projection rotated (RotaryPositionEmbedding::forward in the GEMM's
+        // epilogue where its shape allows, else a rope pass right after it)
         gemm(prof_, 0, 1, T, 3 * d, d, h1l, d, wbase(ly, ly.wqkv, 0, 2), d, qkvl, 3 * d, dt, dt, s, nullptr, 0, 0.0f,
-             1.0f, ql ? &lq : nullptr, wq(ly, 0));
-        {
-            auto _p = prof_.scope(kRope, 0.0, 4.0 * es * T * d, s);
-            hip::rope(qkvl, 3 * d, B, S, 2 * H, hd, 0, cos_dev_, sin_dev_, false, dt, s);
-        }
+             1.0f, ql ? &lq : nullptr, wq(ly, 0), RopeOut{cos_dev_, sin_dev_, 2 * d, hd, S, 0});
         {
             auto _p = prof_.scope(kAttnFwd, attn_flops, 4.0 * es * T * d, s);
             hip::attn_fwd(qkvl, static_cast<char*>(qkvl) + es * d, static_cast<char*>(qkvl) + es * 2 * d, 3 * d, ol,

@@ -96,6 +96,17 @@ int aic_hip_gemm_lowrank(int transA, int transB, int64_t M, int64_t N, int64_t K
                          int64_t ldy2, int64_t r2, int64_t seg_n, int y2_kmajor, float beta, void* C, int64_t ldc,
                          const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type, aic_stream stream);
 
+/* The attention input projection with the rotary embedding applied on the way out: C = A W^T
+ * (bf16 A [M, K], W [N, K], C [M, N]) whose columns [0, rope_cols) are heads of hd values
+ * rotated by the half-split RoPE at position start_pos + row % seq (cos_t / sin_t: [positions]
+ * [hd / 2] tables as aic_hip_rope_tables builds them).  In the GEMM's epilogue for hd 128 on
+ * shapes of at least 128 full 256 x 256 tiles; otherwise the product and then aic_hip_rope.
+ * Replaces: Linear (q, k, v projections) followed by RotaryPositionEmbedding::forward on q and
+ * k (include/nn/rope.hpp:23-112) as CausalSelfAttention::forward runs them. */
+int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
+                      void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq, int64_t start_pos,
+                      const float* cos_t, const float* sin_t, aic_stream stream);
+
 /* Several independent products in one launch (for example every expert's projection of an MoE
  * layer, or two weight gradients whose tiles together fill the chip once).  They must share
  * transA, transB, the dtypes, alpha and beta, and take the MFMA path (bf16, 16-byte aligned

@@ -496,6 +496,44 @@ def test_attention_bf16_mfma(orc, B, S, H, hd, causal):
     np.testing.assert_array_equal(host(dqkv2), g)
 
 
+# (T, d, K, hd, seq, start): 192 tiles of 256x256 with 128-wide heads take the GEMM's rotary
+# epilogue; fewer tiles, head_dim 64, a ragged M or a decode-style start position run the
+# product and then the rope pass
+@pytest.mark.parametrize("T,d,K,hd,seq,start", [(4096, 1024, 256, 128, 2048, 0), (4096, 1024, 256, 128, 1024, 0),
+                                                 (1024, 512, 128, 128, 512, 0), (4096, 1024, 256, 64, 2048, 0),
+                                                 (300, 512, 128, 128, 100, 7)])
+def test_gemm_rope_epilogue(orc, T, d, K, hd, seq, start):
+    """aic_hip_gemm_rope = aic_hip_gemm (x W^T over the q, k, v columns) then aic_hip_rope on the
+    q and k columns: v columns bit-identical, q / k within one bf16 rounding of the rotation of
+    the same bf16 product (the same arithmetic; operation fusing may differ in the last bit), and
+    the oracle's RoPE of the float64 product within the bf16 bound."""
+    rng = np.random.default_rng(T + d + hd + start)
+    N = 3 * d
+    A = bf16_round(rng.standard_normal((T, K)).astype(np.float32))
+    W = bf16_round((rng.standard_normal((N, K)) / 8).astype(np.float32))
+    cos_t = np.empty((start + seq, hd // 2), np.float32)
+    sin_t = np.empty_like(cos_t)
+    _lib.check(_lib.load().aic_hip_rope_tables(cos_t.ctypes.data, sin_t.ctypes.data, start + seq, hd, 10000.0))
+    Ad, Wd, cd, sd = dev(A, torch.bfloat16), dev(W, torch.bfloat16), dev(cos_t), dev(sin_t)
+    fused = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+    call("aic_hip_gemm_rope", T, N, K, ptr(Ad), K, ptr(Wd), K, ptr(fused), N, 2 * d, hd, seq, start, ptr(cd), ptr(sd),
+         stream())
+    sep = _gemm(0, 1, T, N, K, Ad, Wd, BF16, torch.bfloat16)
+    call("aic_hip_rope", ptr(sep), N, T // seq, seq, 2 * d // hd, hd, start, ptr(cd), ptr(sd), 0, BF16, stream())
+    f, g = host(fused), host(sep)
+    np.testing.assert_array_equal(f[:, 2 * d:], g[:, 2 * d:])
+    assert np.max(np.abs(f[:, :2 * d] - g[:, :2 * d]) / (np.abs(g[:, :2 * d]) + 1e-3)) < 1e-2
+    assert rel(f[:, :2 * d], g[:, :2 * d]) < 2e-3
+    ref = A.astype(np.float64) @ W.astype(np.float64).T
+    qk = orc.rope_fwd(ref[:, :2 * d], T // seq, seq, 2 * d // hd, hd, start_pos=start)
+    assert rel(f[:, :2 * d], qk) < 8e-3
+    # deterministic
+    again = torch.empty_like(fused)
+    call("aic_hip_gemm_rope", T, N, K, ptr(Ad), K, ptr(Wd), K, ptr(again), N, 2 * d, hd, seq, start, ptr(cd), ptr(sd),
+         stream())
+    np.testing.assert_array_equal(host(again), f)
+
+
 @pytest.mark.parametrize("B,S,H,hd,causal", [(2, 256, 2, 128, 1), (1, 200, 3, 64, 1), (2, 130, 2, 128, 0),
                                                (1, 72, 1, 64, 0)])
 def test_attention_bwd_with_rope(orc, B, S, H, hd, causal):
