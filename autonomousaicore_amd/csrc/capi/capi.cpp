@@ -271,6 +271,30 @@ int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
     });
 }
 
+int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
+                        void* GU, int64_t ldgu, void* H, int64_t ldh, aic_stream stream) {
+    return guard([&] {
+        aic::hip::GemmArgs a;
+        a.transA = 0;
+        a.transB = 1;
+        a.M = M;
+        a.N = 2 * f;
+        a.K = K;
+        a.A = A;
+        a.lda = lda;
+        a.B = W;
+        a.ldb = ldw;
+        a.C = GU;
+        a.ldc = ldgu;
+        a.ab = aic::DType::BFloat16;
+        a.c = aic::DType::BFloat16;
+        a.glu_f = f;
+        a.glu_out = H;
+        a.ld_glu = ldh;
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
                           int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B,
                           int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,

@@ -56,6 +56,14 @@ struct GemmArgs {
     const float* rope_cos = nullptr;
     const float* rope_sin = nullptr;
     int64_t rope_cols = 0, rope_hd = 0, rope_seq = 0, rope_start = 0;
+    // Optional SwiGLU activation of a gate/up product (N == 2 glu_f: C's columns [0, glu_f) are
+    // the gate, [glu_f, 2 glu_f) the up projection): the product also writes
+    // glu_out[row][j] = silu(C[row][j]) * C[row][glu_f + j] (bf16, leading dimension ld_glu) as
+    // swiglu_fwd does.  In the epilogue for bf16 x W^T on full 256x256 tiles that pair 128 gate
+    // with the matching 128 up columns (glu_f % 128 == 0); otherwise swiglu_fwd runs after it.
+    int64_t glu_f = 0;
+    void* glu_out = nullptr;
+    int64_t ld_glu = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);

@@ -59,10 +59,16 @@ struct RopeOut {
     int64_t cols = 0, hd = 0, seq = 0, start = 0;
 };
 
+// SwiGLU of a gate/up product (GemmArgs::glu_*): out = silu(gate) * up, [M, f] with leading dim ld.
+struct GluOut {
+    void* out = nullptr;
+    int64_t f = 0, ld = 0;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
           int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {},
-          RopeOut rope = {}) {
+          RopeOut rope = {}, GluOut glu = {}) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
     // INT4 operand: half a byte per weight plus one fp16 scale per group
@@ -110,6 +116,11 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.rope_hd = rope.hd;
         a.rope_seq = rope.seq;
         a.rope_start = rope.start;
+    }
+    if (glu.out) {
+        a.glu_f = glu.f;
+        a.glu_out = glu.out;
+        a.ld_glu = glu.ld;
     }
     hip::gemm(a, s);
 }
@@ -839,12 +850,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xagu(l), 2 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
             lg = LowRank{xagu(l), 2 * r, W(ly.bg), r, r, f, 0};
         }
+        // gate/up, with SwiGLU's silu(gate) * up written by the GEMM's epilogue where its shape
+        // allows (else a swiglu pass right after it)
         gemm(prof_, 0, 1, T, 2 * f, d, h2l, d, wbase(ly, ly.wgu, 4, 5), d, gul, 2 * f, dt, dt, s, nullptr, 0, 0.0f,
-             1.0f, ql ? &lg : nullptr, wq(ly, 4));
-        {
-            auto _p = prof_.scope(kSwigluFwd, 0.0, 3.0 * es * T * f, s);
-            hip::swiglu_fwd(gul, static_cast<char*>(gul) + es * f, 2 * f, aml, f, T, f, dt, s);
-        }
+             1.0f, ql ? &lg : nullptr, wq(ly, 4), RopeOut{}, GluOut{aml, f, f});
         LowRank ld_{};
         if (ql) {
             gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);

@@ -107,6 +107,15 @@ int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
                       void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq, int64_t start_pos,
                       const float* cos_t, const float* sin_t, aic_stream stream);
 
+/* The FFN's gate/up projection with SwiGLU applied on the way out: GU = A W^T (bf16 A [M, K],
+ * W [2f, K] = the gate rows then the up rows, GU [M, 2f]) and H[row][j] = silu(GU[row][j]) *
+ * GU[row][f + j] (bf16 [M, f]).  In the GEMM's epilogue on shapes of at least 128 full 256 x 256
+ * tiles with f % 128 == 0; otherwise the product and then aic_hip_swiglu_fwd.
+ * Replaces: the gate and up Linear layers followed by silu * mul (SwiGLU::forward,
+ * include/nn/swiglu.hpp:21-33). */
+int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
+                        void* GU, int64_t ldgu, void* H, int64_t ldh, aic_stream stream);
+
 /* Several independent products in one launch (for example every expert's projection of an MoE
  * layer, or two weight gradients whose tiles together fill the chip once).  They must share
  * transA, transB, the dtypes, alpha and beta, and take the MFMA path (bf16, 16-byte aligned

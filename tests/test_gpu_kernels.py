@@ -496,6 +496,30 @@ def test_attention_bf16_mfma(orc, B, S, H, hd, causal):
     np.testing.assert_array_equal(host(dqkv2), g)
 
 
+# (M, f, K): 32 x 22 = 704 paired tiles (the 1B shape's f over fewer rows) and 256 take the GEMM's
+# SwiGLU epilogue; fewer tiles or f not a multiple of 128 run the product and then swiglu_fwd
+@pytest.mark.parametrize("M,f,K", [(8192, 5632, 128), (4096, 2048, 256), (1024, 1024, 128), (4096, 1088, 128),
+                                   (300, 512, 64)])
+def test_gemm_swiglu_epilogue(orc, M, f, K):
+    """aic_hip_gemm_swiglu = aic_hip_gemm (x W^T over the gate and up rows) then
+    aic_hip_swiglu_fwd: both outputs bit-identical (the same bf16 product, the same activation
+    arithmetic), and against the oracle's SwiGLU of the float64 product within the bf16 bound."""
+    rng = np.random.default_rng(M + f + K)
+    A = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    W = bf16_round((rng.standard_normal((2 * f, K)) / np.sqrt(K)).astype(np.float32))
+    Ad, Wd = dev(A, torch.bfloat16), dev(W, torch.bfloat16)
+    gu = torch.empty((M, 2 * f), dtype=torch.bfloat16, device="cuda")
+    h = torch.empty((M, f), dtype=torch.bfloat16, device="cuda")
+    call("aic_hip_gemm_swiglu", M, f, K, ptr(Ad), K, ptr(Wd), K, ptr(gu), 2 * f, ptr(h), f, stream())
+    gu2 = _gemm(0, 1, M, 2 * f, K, Ad, Wd, BF16, torch.bfloat16)
+    h2 = torch.empty_like(h)
+    call("aic_hip_swiglu_fwd", ptr(gu2), ptr(gu2) + 2 * f, 2 * f, ptr(h2), f, M, f, BF16, stream())
+    np.testing.assert_array_equal(host(gu), host(gu2))
+    np.testing.assert_array_equal(host(h), host(h2))
+    ref = A.astype(np.float64) @ W.astype(np.float64).T
+    assert rel(host(h), orc.swiglu_fwd(ref[:, :f], ref[:, f:])) < 1e-2
+
+
 # (T, d, K, hd, seq, start): 192 tiles of 256x256 with 128-wide heads take the GEMM's rotary
 # epilogue; fewer tiles, head_dim 64, a ragged M or a decode-style start position run the
 # product and then the rope pass
