@@ -295,6 +295,30 @@ int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t 
     });
 }
 
+int aic_hip_gemm_swiglu_bwd(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                            const void* GU, int64_t ldgu, void* DH, int64_t lddh, void* DGU, aic_stream stream) {
+    return guard([&] {
+        aic::hip::GemmArgs a;
+        a.transA = 0;
+        a.transB = 0;
+        a.M = M;
+        a.N = f;
+        a.K = K;
+        a.A = A;
+        a.lda = lda;
+        a.B = B;
+        a.ldb = ldb;
+        a.C = DH;
+        a.ldc = lddh;
+        a.ab = aic::DType::BFloat16;
+        a.c = aic::DType::BFloat16;
+        a.dglu_gu = GU;
+        a.dglu_out = DGU;
+        a.dglu_ld = ldgu;
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, const void* dout,
                           int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B,
                           int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,

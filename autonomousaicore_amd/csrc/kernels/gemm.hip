@@ -188,6 +188,12 @@ void splitk_reduce(const float* part, int splits, const GemmArgs& a, hipStream_t
     AIC_LAUNCH_CHECK("splitk_reduce_k");
 }
 
+// Whether the rank term alpha X2 Y2^T fits the k-loop tail of the DMA kernels with BN-wide tiles.
+bool rank_tail_ok(const GemmArgs& a, int64_t bn) {
+    return a.r2 % 8 == 0 && a.ldx2 % 8 == 0 && aligned16(a.X2) && (a.y2_kmajor || (a.ldy2 % 8 == 0 && aligned16(a.Y2))) &&
+           (a.seg_n == 0 || a.seg_n % bn == 0);
+}
+
 // C = alpha X2 Y2^T + C, per segment, as ordinary GEMMs (the shapes the kernel tail cannot take).
 void rank_term_separately(const GemmArgs& a, hipStream_t s) {
     const size_t es = dtype_size(a.ab), ec = dtype_size(a.c);
@@ -226,9 +232,7 @@ void gemm_q4(const GemmArgs& a, hipStream_t s) {
     const bool big = t256 >= 128;
     if (a.r2 > 0) {
         const int64_t bn = big ? 256 : 128;
-        const bool tail = a.r2 % 8 == 0 && a.ldx2 % 8 == 0 && aligned16(a.X2) &&
-                          (a.y2_kmajor || (a.ldy2 % 8 == 0 && aligned16(a.Y2))) && (a.seg_n == 0 || a.seg_n % bn == 0);
-        if (!tail) {
+        if (!rank_tail_ok(a, bn)) {
             GemmArgs b = a;
             b.r2 = 0;
             gemm_q4(b, s);
@@ -306,6 +310,26 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         if (a.c == DType::BFloat16) dispatch_dma<256, 256, 64, 2, bf16>(a, s);
         return;
     }
+    if (a.dglu_gu) {
+        AIC_CHECK(a.dglu_out && a.dglu_ld >= 2 * a.N && a.beta == 0.0f && !a.R && !a.rope_cos && a.glu_f == 0,
+                  InvalidArgument, "GEMM SwiGLU-backward epilogue: bad arguments");
+        // in the epilogue of the full-tile paths without K split (at least 128 tiles of 256x256)
+        const int64_t es = static_cast<int64_t>(dtype_size(a.c));
+        const bool fused = a.c == DType::BFloat16 && (a.Bq ? gemm_q4_eligible(a) : gemm_dma_eligible(a)) &&
+                           a.M % 256 == 0 && a.N % 256 == 0 &&
+                           (a.M / 256) * (a.N / 256) >= 128 && a.ldc % 8 == 0 && aligned16(a.C) &&
+                           a.dglu_ld % 8 == 0 && aligned16(a.dglu_gu) && aligned16(a.dglu_out) &&
+                           (a.r2 == 0 || rank_tail_ok(a, 256));  // C is not written: no rank term added later
+        if (!fused) {
+            GemmArgs b = a;
+            b.dglu_gu = nullptr;
+            b.dglu_out = nullptr;
+            gemm(b, s);
+            swiglu_bwd(a.dglu_gu, static_cast<const char*>(a.dglu_gu) + es * a.N, a.dglu_ld, a.C, a.ldc, a.dglu_out,
+                       static_cast<char*>(a.dglu_out) + es * a.N, a.dglu_ld, a.M, a.N, a.c, s);
+            return;
+        }
+    }
     if (a.Bq) {
         gemm_q4(a, s);
         return;
@@ -325,10 +349,7 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         }
         if (a.r2 > 0) {
             const int64_t bn = big ? 256 : 128;
-            const bool tail = a.r2 % 8 == 0 && a.ldx2 % 8 == 0 && aligned16(a.X2) &&
-                              (a.y2_kmajor || (a.ldy2 % 8 == 0 && aligned16(a.Y2))) &&
-                              (a.seg_n == 0 || a.seg_n % bn == 0);
-            if (!tail) {
+            if (!rank_tail_ok(a, bn)) {
                 GemmArgs b = a;
                 b.r2 = 0;
                 gemm(b, s);

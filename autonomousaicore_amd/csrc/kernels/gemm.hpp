@@ -64,6 +64,15 @@ struct GemmArgs {
     int64_t glu_f = 0;
     void* glu_out = nullptr;
     int64_t ld_glu = 0;
+    // Optional SwiGLU backward fed by the product (the down projection's input gradient
+    // dh = dy W_d, [M, N = f]): with g = dglu_gu[row][j], u = dglu_gu[row][N + j] (leading
+    // dimension dglu_ld) and dh the bf16 product, dglu_out[row][j] = dh u silu'(g) and
+    // dglu_out[row][N + j] = dh silu(g) (swiglu_bwd's arithmetic).  In the epilogue on full 256x256
+    // tiles of bf16 output, where C is then not written; otherwise the product goes to C and
+    // swiglu_bwd runs after it.
+    const void* dglu_gu = nullptr;
+    void* dglu_out = nullptr;
+    int64_t dglu_ld = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);

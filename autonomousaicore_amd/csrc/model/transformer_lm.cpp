@@ -65,10 +65,17 @@ struct GluOut {
     int64_t f = 0, ld = 0;
 };
 
+// SwiGLU's backward fed by the product dh (GemmArgs::dglu_*): gu [M, 2N] in, dgu [M, 2N] out.
+struct DGlu {
+    const void* gu = nullptr;
+    void* out = nullptr;
+    int64_t ld = 0;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
           int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {},
-          RopeOut rope = {}, GluOut glu = {}) {
+          RopeOut rope = {}, GluOut glu = {}, DGlu dglu = {}) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
     // INT4 operand: half a byte per weight plus one fp16 scale per group
@@ -121,6 +128,11 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.glu_f = glu.f;
         a.glu_out = glu.out;
         a.ld_glu = glu.ld;
+    }
+    if (dglu.gu) {
+        a.dglu_gu = dglu.gu;
+        a.dglu_out = dglu.out;
+        a.dglu_ld = dglu.ld;
     }
     hip::gemm(a, s);
 }
@@ -936,13 +948,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                 gemm(prof_, 1, 0, r, f, T, dxa.get(), r, aml, f, G(ly.ad), f, dt, DType::Float32, s);
                 ld_ = LowRank{dxa.get(), r, W(ly.ad), f, r, 0, 1};
             }  // else: the down-projection weight gradient joins the layer's grouped launch below
+            // da = dx W_d goes straight into SwiGLU's backward in the GEMM's epilogue (dgu from da
+            // and the saved gate/up) where its shape allows, else through da and a swiglu pass
             gemm(prof_, 0, 0, T, f, d, dx.get(), d, wbase(ly, ly.wd, 6, 6), f, da.get(), f, dt, dt, s, nullptr, 0,
-                 0.0f, 1.0f, ql ? &ld_ : nullptr, wq(ly, 6));
-            {
-                auto _p = prof_.scope(kSwigluBwd, 0.0, 5.0 * es * T * f, s);
-                hip::swiglu_bwd(gul, static_cast<char*>(gul) + es * f, 2 * f, da.get(), f, dgu.get(),
-                                static_cast<char*>(dgu.get()) + es * f, 2 * f, T, f, dt, s);
-            }
+                 0.0f, 1.0f, ql ? &ld_ : nullptr, wq(ly, 6), RopeOut{}, GluOut{}, DGlu{gul, dgu.get(), 2 * f});
             LowRank lg{};
             if (ql) {
                 void* xa = xagu(l);

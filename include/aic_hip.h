@@ -116,6 +116,16 @@ int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
 int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
                         void* GU, int64_t ldgu, void* H, int64_t ldh, aic_stream stream);
 
+/* The FFN's down-projection input gradient fed straight into SwiGLU's backward: with
+ * dh = A B (bf16 A [M, K], B [K, f]; dh [M, f] in DH, leading dimension lddh), g = GU[row][j],
+ * u = GU[row][f + j]: DGU[row][j] = dh u silu'(g), DGU[row][f + j] = dh silu(g) (bf16, as
+ * aic_hip_swiglu_bwd).  In the GEMM's epilogue on shapes of at least 128 full 256 x 256 tiles,
+ * where DH is then not written; otherwise the product goes to DH and aic_hip_swiglu_bwd runs.
+ * Replaces: the down Linear layer's input gradient followed by the silu * mul backward
+ * (include/nn/swiglu.hpp:21-33, src/autograd/functions.cpp:60-68,167-175). */
+int aic_hip_gemm_swiglu_bwd(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                            const void* GU, int64_t ldgu, void* DH, int64_t lddh, void* DGU, aic_stream stream);
+
 /* Several independent products in one launch (for example every expert's projection of an MoE
  * layer, or two weight gradients whose tiles together fill the chip once).  They must share
  * transA, transB, the dtypes, alpha and beta, and take the MFMA path (bf16, 16-byte aligned

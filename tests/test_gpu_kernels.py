@@ -520,6 +520,33 @@ def test_gemm_swiglu_epilogue(orc, M, f, K):
     assert rel(host(h), orc.swiglu_fwd(ref[:, :f], ref[:, f:])) < 1e-2
 
 
+# (M, f, K): 32 x 22 = 704 tiles (the 1B down projection's input gradient) and 256 take the GEMM's
+# SwiGLU-backward epilogue; fewer tiles or f not a multiple of 256 go through dh and swiglu_bwd
+@pytest.mark.parametrize("M,f,K", [(8192, 5632, 256), (4096, 2048, 128), (1024, 1024, 128), (4096, 1152, 128),
+                                   (300, 512, 64)])
+def test_gemm_swiglu_bwd_epilogue(orc, M, f, K):
+    """aic_hip_gemm_swiglu_bwd = aic_hip_gemm (dh = dy W) then aic_hip_swiglu_bwd: the gate/up
+    gradients bit-identical, and against the oracle's SwiGLU backward of the float64 product
+    within the bf16 bound."""
+    rng = np.random.default_rng(M + f + K + 1)
+    A = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    Bm = bf16_round((rng.standard_normal((K, f)) / np.sqrt(K)).astype(np.float32))
+    GU = bf16_round(rng.standard_normal((M, 2 * f)).astype(np.float32))
+    Ad, Bd, GUd = dev(A, torch.bfloat16), dev(Bm, torch.bfloat16), dev(GU, torch.bfloat16)
+    dh = torch.empty((M, f), dtype=torch.bfloat16, device="cuda")
+    dgu = torch.empty((M, 2 * f), dtype=torch.bfloat16, device="cuda")
+    call("aic_hip_gemm_swiglu_bwd", M, f, K, ptr(Ad), K, ptr(Bd), f, ptr(GUd), 2 * f, ptr(dh), f, ptr(dgu), stream())
+    dh2 = _gemm(0, 0, M, f, K, Ad, Bd, BF16, torch.bfloat16)
+    dgu2 = torch.empty_like(dgu)
+    call("aic_hip_swiglu_bwd", ptr(GUd), ptr(GUd) + 2 * f, 2 * f, ptr(dh2), f, ptr(dgu2), ptr(dgu2) + 2 * f, 2 * f,
+         M, f, BF16, stream())
+    np.testing.assert_array_equal(host(dgu), host(dgu2))
+    ref = A.astype(np.float64) @ Bm.astype(np.float64)
+    dg_ref, du_ref = orc.swiglu_bwd(GU[:, :f], GU[:, f:], ref)
+    got = host(dgu)
+    assert rel(got[:, :f], dg_ref) < 1e-2 and rel(got[:, f:], du_ref) < 1e-2
+
+
 # (T, d, K, hd, seq, start): 192 tiles of 256x256 with 128-wide heads take the GEMM's rotary
 # epilogue; fewer tiles, head_dim 64, a ragged M or a decode-style start position run the
 # product and then the rope pass
