@@ -182,6 +182,7 @@ SIGNATURES = {
     "aic_lm_synchronize": (i32, [vp]),
     "aic_lm_last_stats": (i32, [vp, C.POINTER(StepStats)]),
     "aic_lm_profile": (i32, [vp, i32]),
+    "aic_lm_fused_grad_norm": (i32, [vp, i32, C.POINTER(i32)]),
     "aic_lm_profile_classes": (i32, [vp, C.c_uint32]),
     "aic_lm_profile_class_index": (i32, [C.c_char_p]),
     "aic_lm_profile_stats": (i32, [vp, C.POINTER(KernelStat), i32, C.POINTER(i32)]),

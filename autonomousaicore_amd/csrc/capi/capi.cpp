@@ -618,6 +618,14 @@ int aic_lm_profile(aic_lm* lm, int enable) {
     });
 }
 
+int aic_lm_fused_grad_norm(aic_lm* lm, int enable, int* used) {
+    return guard([&] {
+        AIC_CHECK(lm, InvalidArgument, "null model");
+        const bool u = lm->model->set_fused_grad_norm(enable != 0);
+        if (used) *used = u ? 1 : 0;
+    });
+}
+
 int aic_lm_profile_classes(aic_lm* lm, uint32_t class_mask) {
     return guard([&] {
         AIC_CHECK(lm, InvalidArgument, "null model");

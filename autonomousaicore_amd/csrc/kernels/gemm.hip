@@ -26,13 +26,42 @@ namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The 256-thread block's sum of every thread's (acc, nf) into *out / *out_nf: a fixed butterfly
+// within each wave, then the four waves in order.  Every thread of the block must call it.
+__device__ __forceinline__ void sq_block256(double acc, int nf, double* out, int* out_nf) {
+    __shared__ double sd[4];
+    __shared__ int sn[4];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        acc += __shfl_xor(acc, o);
+        nf |= __shfl_xor(nf, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sd[threadIdx.x >> 6] = acc;
+        sn[threadIdx.x >> 6] = nf;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        *out = ((sd[0] + sd[1]) + sd[2]) + sd[3];
+        *out_nf = sn[0] | sn[1] | sn[2] | sn[3];
+    }
+}
+
+__device__ __forceinline__ void sq_add1(double& acc, int& nf, float v) {
+    acc += static_cast<double>(v * v);
+    nf |= (__float_as_uint(v) & 0x7f800000u) == 0x7f800000u;
+}
+
 // C = alpha * sum_z P[z] + beta * C + R over the split-K partials P [splits][M][N] (fp32,
-// summed in z order: deterministic).
+// summed in z order: deterministic); with sq, each block also writes the sum of squares of
+// the values it stored (one slot per block).
 template <typename CT>
 __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ P, int splits, int64_t pz, int M, int N,
                                                        float alpha, float beta, CT* C, int64_t ldc, const CT* R,
-                                                       int64_t ldr) {
+                                                       int64_t ldr, double* sq, int* sq_nf) {
     const int64_t total = static_cast<int64_t>(M) * N;
+    double sqa = 0.0;
+    int sqf = 0;
     for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
         const int m = static_cast<int>(i / N), n = static_cast<int>(i % N);
         float acc = P[i];
@@ -42,7 +71,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__
         if (beta != 0.0f) v += beta * ld(C, ci);
         if (R) v += ld(R, static_cast<int64_t>(m) * ldr + n);
         st(C, ci, v);
+        if (sq) sq_add1(sqa, sqf, v);  // fp32 C: the stored value
     }
+    if (sq) sq_block256(sqa, sqf, sq + blockIdx.x, sq_nf + blockIdx.x);
+}
+
+// Sums of squares of the fp32 matrix C [M, N] (leading dimension ldc), one slot per block: the
+// products whose path has no such epilogue.
+__global__ __launch_bounds__(256) void sq_matrix_k(const float* __restrict__ C, int64_t ldc, int M, int N, double* sq,
+                                                   int* sq_nf) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    double sqa = 0.0;
+    int sqf = 0;
+    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256)
+        sq_add1(sqa, sqf, C[(i / N) * ldc + i % N]);
+    sq_block256(sqa, sqf, sq + blockIdx.x, sq_nf + blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -173,19 +216,32 @@ bool gemm_dma_eligible(const GemmArgs& a) {
 
 namespace {
 
-// C = alpha * (sum of the split-K partials) + beta * C + R.
+// C = alpha * (sum of the split-K partials) + beta * C + R (and the sums of squares of C when
+// a.sq_part is set: at most 1024 slots).
 void splitk_reduce(const float* part, int splits, const GemmArgs& a, hipStream_t s) {
     const int64_t total = a.M * a.N;
-    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 4096));
-    if (a.c == DType::Float32)
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, a.sq_part ? 1024 : 4096));
+    if (a.c == DType::Float32) {
+        AIC_CHECK(!a.sq_part || (a.sq_nf && grid <= a.sq_cap), InvalidArgument, "GEMM sums of squares: ", grid,
+                  " slots needed, ", a.sq_cap, " given");
         hipLaunchKernelGGL(splitk_reduce_k<float>, dim3(grid), dim3(256), 0, s, part, splits, total,
                            static_cast<int>(a.M), static_cast<int>(a.N), a.alpha, a.beta, static_cast<float*>(a.C),
-                           a.ldc, static_cast<const float*>(a.R), a.ldr);
-    else
+                           a.ldc, static_cast<const float*>(a.R), a.ldr, a.sq_part, a.sq_nf);
+    } else {
         hipLaunchKernelGGL(splitk_reduce_k<bf16>, dim3(grid), dim3(256), 0, s, part, splits, total,
                            static_cast<int>(a.M), static_cast<int>(a.N), a.alpha, a.beta, static_cast<bf16*>(a.C),
-                           a.ldc, static_cast<const bf16*>(a.R), a.ldr);
+                           a.ldc, static_cast<const bf16*>(a.R), a.ldr, nullptr, nullptr);
+    }
     AIC_LAUNCH_CHECK("splitk_reduce_k");
+}
+
+// The sums of squares of the product already in C, for the paths without them in an epilogue.
+void sq_matrix(const GemmArgs& a, hipStream_t s) {
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>({(a.M * a.N + 1023) / 1024, 256, a.sq_cap}));
+    AIC_CHECK(a.sq_nf && grid >= 1, InvalidArgument, "GEMM sums of squares: no slots given");
+    hipLaunchKernelGGL(sq_matrix_k, dim3(grid), dim3(256), 0, s, static_cast<const float*>(a.C), a.ldc,
+                       static_cast<int>(a.M), static_cast<int>(a.N), a.sq_part, a.sq_nf);
+    AIC_LAUNCH_CHECK("sq_matrix_k");
 }
 
 // Whether the rank term alpha X2 Y2^T fits the k-loop tail of the DMA kernels with BN-wide tiles.
@@ -272,6 +328,21 @@ void gemm(const GemmArgs& a, hipStream_t s) {
                   "low-rank term: leading dimension smaller than the row length");
     }
     if (a.M == 0 || a.N == 0) return;
+    if (a.sq_part) {
+        AIC_CHECK(a.c == DType::Float32 && a.sq_nf && a.sq_cap > 0 && !a.rope_cos && a.glu_f == 0 && !a.dglu_gu,
+                  InvalidArgument, "GEMM sums of squares: fp32 output only, without the RoPE / SwiGLU epilogues");
+        // in the DMA tile kernels' epilogue or split-K reduction; the other paths (INT4 B, a
+        // low-rank term, the non-DMA kernels) read the product back
+        if (a.Bq || a.r2 > 0 || !gemm_dma_eligible(a)) {
+            GemmArgs b = a;
+            b.sq_part = nullptr;
+            b.sq_nf = nullptr;
+            b.sq_cap = 0;
+            gemm(b, s);
+            sq_matrix(a, s);
+            return;
+        }
+    }
     if (a.rope_cos) {
         AIC_CHECK(a.rope_sin && a.rope_hd > 0 && a.rope_hd % 2 == 0 && a.rope_cols % a.rope_hd == 0 &&
                       a.rope_cols <= a.N && a.rope_seq > 0 && a.M % a.rope_seq == 0 && a.beta == 0.0f && !a.R,
@@ -425,7 +496,18 @@ void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
         t256 += ((x.M + 255) / 256) * ((x.N + 255) / 256);
     }
     if (!one_launch) {
-        for (int i = 0; i < n; ++i) gemm(a[i], s);
+        for (int i = 0; i < n; ++i) {
+            GemmArgs b = a[i];
+            if (a[0].sq_part) {  // the launch's slot region in equal shares
+                const int64_t share = a[0].sq_cap / n;
+                b.sq_part = a[0].sq_part + i * share;
+                b.sq_nf = a[0].sq_nf + i * share;
+                b.sq_cap = share;
+            } else {
+                b.sq_part = nullptr;
+            }
+            gemm(b, s);
+        }
         return;
     }
     if (t256 > 256 && t256 % 256 != 0 && t256 % 256 <= 64) {
@@ -466,6 +548,15 @@ void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
             if (*std::max_element(per_xcd, per_xcd + 8) > 32 * rounds) continue;
             if (g[0].c == DType::Float32) dispatch_grouped<256, 256, 64, 2, float>(g.data(), n, s);
             else dispatch_grouped<256, 256, 64, 2, bf16>(g.data(), n, s);
+            cut.sq_part = nullptr;
+            if (a[0].sq_part) {  // the launch's blocks (8-aligned per product), then the cut's slots
+                int64_t blocks = 0;
+                for (const GemmArgs& y : g) blocks += (((y.M + 255) / 256) * ((y.N + 255) / 256) + 7) / 8 * 8;
+                AIC_CHECK(blocks < a[0].sq_cap, InvalidArgument, "grouped GEMM sums of squares: region too small");
+                cut.sq_part = a[0].sq_part + blocks;
+                cut.sq_nf = a[0].sq_nf + blocks;
+                cut.sq_cap = a[0].sq_cap - blocks;
+            }
             gemm(cut, s);
             return;
         }

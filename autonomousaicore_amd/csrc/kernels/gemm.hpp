@@ -73,6 +73,15 @@ struct GemmArgs {
     const void* dglu_gu = nullptr;
     void* dglu_out = nullptr;
     int64_t dglu_ld = 0;
+    // Optional sums of squares of the stored output (fp32 C only), for the gradient norm: the
+    // call writes one fp64 partial and one non-finite flag per slot into sq_part[0..) /
+    // sq_nf[0..) (at most sq_cap slots; how many depends on the path, always the same for the
+    // same shapes) and leaves the rest of the region alone.  Each partial adds double(x0^2 +
+    // x1^2) + double(x2^2 + x3^2) over groups of four stored values, as sqnorm_k does.  The
+    // tile kernels do it in their epilogue (or split-K reduction); other paths read C back.
+    double* sq_part = nullptr;
+    int* sq_nf = nullptr;
+    int64_t sq_cap = 0;
 };
 
 bool gemm_mfma_eligible(const GemmArgs& a);
@@ -86,6 +95,7 @@ void gemm(const GemmArgs& a, hipStream_t stream);
 // Independent products in one launch when they share the kernel configuration (transposes,
 // dtypes, alpha, beta; no residual or low-rank term; up to 8), so that their tiles fill the
 // chip together instead of each product's last partial round; otherwise one gemm() each.
+// Sums of squares (sq_*) of the whole call go to a[0]'s slot region; the others' are ignored.
 void gemm_grouped(const GemmArgs* a, int n, hipStream_t stream);
 
 // The products of E experts over row-ragged operands, one launch, with the row ranges read on

@@ -117,6 +117,16 @@ void grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, 
                                int* nonfinite, hipStream_t s);
 void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s);
 void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipStream_t s);
+// The gradient norm from partial slots written by the gradients' producers (GEMM epilogues,
+// split-K reductions) plus these: sqnorm_partials writes sqnorm_k's partials of the tensors
+// into pd / pn (sqnorm_slots(sizes, count) slots); sqnorm_reduce adds nslots slots in a fixed
+// order (blocks of 4096, then one block over them; tmp_d / tmp_n hold sqnorm_reduce_tmp(nslots)
+// entries) into *sqnorm and the OR of the flags into *nonfinite.
+int64_t sqnorm_slots(const int64_t* sizes, int count);
+void sqnorm_partials(const float* const* grads, const int64_t* sizes, int count, double* pd, int* pn, hipStream_t s);
+int64_t sqnorm_reduce_tmp(int64_t nslots);
+void sqnorm_reduce(const double* pd, const int* pn, int64_t nslots, double* tmp_d, int* tmp_n, double* sqnorm,
+                   int* nonfinite, hipStream_t s);
 void adamw_multi(float* const* p, const float* const* g, float* const* m, float* const* v, void* const* p_bf16,
                  const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps, float wd,
                  int64_t step, const void* ctl, hipStream_t s);

@@ -24,15 +24,17 @@ constexpr int kNormBlocks = 1024;
 
 __device__ __forceinline__ bool finite_(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
-__global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int64_t n, double* part, int* part_nf) {
+// Block `bid` of `nb` blocks over the tensor g[0..n): its partial sum of squares and non-finite flag.
+__device__ __forceinline__ void sqnorm_block(const float* __restrict__ g, int64_t n, int bid, int nb, double* part,
+                                             int* part_nf) {
     __shared__ double sd[256];
     __shared__ int sn[256];
     double acc = 0.0;
     int nf = 0;
     const int64_t n4 = ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) ? n / 4 : 0;
     const float4* g4 = reinterpret_cast<const float4*>(g);
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t stride = static_cast<int64_t>(nb) * 256;
+    int64_t i = static_cast<int64_t>(bid) * 256 + threadIdx.x;
     // four loads in flight per thread; the values are added in the same order as one at a time
     for (; i + 3 * stride < n4; i += 4 * stride) {
         f32x4 v[4];
@@ -50,8 +52,7 @@ __global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int
         nf |= !finite_(v.x) | !finite_(v.y) | !finite_(v.z) | !finite_(v.w);
         acc += static_cast<double>(v.x * v.x + v.y * v.y) + static_cast<double>(v.z * v.z + v.w * v.w);
     }
-    for (int64_t i = n4 * 4 + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
+    for (int64_t i = n4 * 4 + static_cast<int64_t>(bid) * 256 + threadIdx.x; i < n; i += stride) {
         const float v = g[i];
         nf |= !finite_(v);
         acc += static_cast<double>(v) * static_cast<double>(v);
@@ -67,9 +68,30 @@ __global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        part[blockIdx.x] = sd[0];
-        part_nf[blockIdx.x] = sn[0];
+        part[bid] = sd[0];
+        part_nf[bid] = sn[0];
     }
+}
+
+__global__ __launch_bounds__(256) void sqnorm_k(const float* __restrict__ g, int64_t n, double* part, int* part_nf) {
+    sqnorm_block(g, n, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), part, part_nf);
+}
+
+// Several tensors' sqnorm_k blocks in one launch: tensor t owns the blocks [first[t], first[t+1])
+// and its partials land at part + first[t], exactly as one sqnorm_k launch per tensor.
+constexpr int kSqMultiMax = 128;
+struct SqMulti {
+    const float* g[kSqMultiMax];
+    int64_t n[kSqMultiMax];
+    int first[kSqMultiMax + 1];
+    int count;
+};
+__global__ __launch_bounds__(256) void sqnorm_multi_k(const SqMulti m, double* part, int* part_nf) {
+    const int b = static_cast<int>(blockIdx.x);
+    int t = 0;
+    while (t + 1 < m.count && b >= m.first[t + 1]) ++t;
+    const int f0 = m.first[t];
+    sqnorm_block(m.g[t], m.n[t], b - f0, m.first[t + 1] - f0, part + f0, part_nf + f0);
 }
 
 __global__ __launch_bounds__(1024) void sqnorm_final_k(const double* __restrict__ part, const int* __restrict__ part_nf,
@@ -98,6 +120,36 @@ __global__ __launch_bounds__(1024) void sqnorm_final_k(const double* __restrict_
     }
 }
 
+// First level of the sum of many partial slots: block b adds slots [4096 b, 4096 (b + 1)), four
+// per thread in order, then a fixed tree; the second level is sqnorm_final_k over the blocks.
+__global__ __launch_bounds__(1024) void sqsum_level1_k(const double* __restrict__ part, const int* __restrict__ part_nf,
+                                                       int64_t n, double* out, int* out_nf) {
+    __shared__ double sd[1024];
+    __shared__ int sn[1024];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * 4096;
+    double v[4];
+    int f[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t i = base + u * 1024 + threadIdx.x;
+        v[u] = i < n ? part[i] : 0.0;
+        f[u] = i < n ? part_nf[i] : 0;
+    }
+    sd[threadIdx.x] = ((v[0] + v[1]) + v[2]) + v[3];
+    sn[threadIdx.x] = f[0] | f[1] | f[2] | f[3];
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            sd[threadIdx.x] += sd[threadIdx.x + o];
+            sn[threadIdx.x] |= sn[threadIdx.x + o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[blockIdx.x] = sd[0];
+        out_nf[blockIdx.x] = sn[0];
+    }
+}
 __global__ void scale_k(float* g, int64_t n, const float* scale) {
     const float s = *scale;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -339,6 +391,50 @@ void grad_sqnorm_multi_noalloc(const float* const* grads, const int64_t* sizes, 
     double* pd = device_scratch();
     int* pn = reinterpret_cast<int*>(pd + kNoAllocMaxBlocks);
     sqnorm_launch(grads, sizes, count, blocks, static_cast<int>(total), pd, pn, sqnorm, nonfinite, s);
+}
+
+int64_t sqnorm_slots(const int64_t* sizes, int count) {
+    AIC_CHECK(count >= 0 && count <= kMaxNormTensors, InvalidArgument, "sqnorm_slots: 0 to ", kMaxNormTensors,
+              " tensors");
+    int blocks[kMaxNormTensors];
+    return sqnorm_blocks(sizes, count, blocks);
+}
+
+void sqnorm_partials(const float* const* grads, const int64_t* sizes, int count, double* pd, int* pn,
+                     hipStream_t s) {
+    AIC_CHECK(count >= 0 && count <= kMaxNormTensors && pd && pn, InvalidArgument, "sqnorm_partials: bad arguments");
+    int blocks[kMaxNormTensors];
+    sqnorm_blocks(sizes, count, blocks);
+    // kSqMultiMax tensors per launch
+    int64_t off = 0;
+    for (int t0 = 0; t0 < count; t0 += kSqMultiMax) {
+        SqMulti m;
+        m.count = std::min(count - t0, kSqMultiMax);
+        m.first[0] = 0;
+        for (int i = 0; i < m.count; ++i) {
+            m.g[i] = grads[t0 + i];
+            m.n[i] = sizes[t0 + i];
+            m.first[i + 1] = m.first[i] + blocks[t0 + i];
+        }
+        hipLaunchKernelGGL(sqnorm_multi_k, dim3(m.first[m.count]), dim3(256), 0, s, m, pd + off, pn + off);
+        AIC_LAUNCH_CHECK("grad_sqnorm_multi");
+        off += m.first[m.count];
+    }
+}
+
+int64_t sqnorm_reduce_tmp(int64_t nslots) { return std::max<int64_t>(1, (nslots + 4095) / 4096); }
+
+void sqnorm_reduce(const double* pd, const int* pn, int64_t nslots, double* tmp_d, int* tmp_n, double* sqnorm,
+                   int* nonfinite, hipStream_t s) {
+    AIC_CHECK(nslots >= 0 && pd && pn && tmp_d && tmp_n && sqnorm && nonfinite, InvalidArgument,
+              "sqnorm_reduce: bad arguments");
+    const int64_t nb = sqnorm_reduce_tmp(nslots);
+    AIC_CHECK(nb <= (int64_t{1} << 20), InvalidArgument, "sqnorm_reduce: too many slots");
+    hipLaunchKernelGGL(sqsum_level1_k, dim3(static_cast<unsigned>(nb)), dim3(1024), 0, s, pd, pn, nslots, tmp_d, tmp_n);
+    AIC_LAUNCH_CHECK("sqsum_level1");
+    hipLaunchKernelGGL(sqnorm_final_k, dim3(1), dim3(1024), 0, s, tmp_d, tmp_n, static_cast<int>(nb), sqnorm,
+                       nonfinite);
+    AIC_LAUNCH_CHECK("grad_sqnorm_final");
 }
 
 void scale_multi(float* const* grads, const int64_t* sizes, int count, const float* scale, hipStream_t s) {

@@ -72,10 +72,17 @@ struct DGlu {
     int64_t ld = 0;
 };
 
+// Sums of squares of an fp32 product for the gradient norm (GemmArgs::sq_*).
+struct SqOut {
+    double* part = nullptr;
+    int* nf = nullptr;
+    int64_t cap = 0;
+};
+
 void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
           const void* B, int64_t ldb, void* C, int64_t ldc, DType ab, DType c, hipStream_t s, const void* R = nullptr,
           int64_t ldr = 0, float beta = 0.0f, float alpha = 1.0f, const LowRank* lr = nullptr, Q4B q4 = {},
-          RopeOut rope = {}, GluOut glu = {}, DGlu dglu = {}) {
+          RopeOut rope = {}, GluOut glu = {}, DGlu dglu = {}, SqOut sq = {}) {
     const double es = static_cast<double>(dtype_size(ab)), ec = static_cast<double>(dtype_size(c));
     const double kr = lr ? static_cast<double>(lr->r2) : 0.0;
     // INT4 operand: half a byte per weight plus one fp16 scale per group
@@ -134,12 +141,15 @@ void gemm(Profiler& prof, int ta, int tb, int64_t M, int64_t N, int64_t K, const
         a.dglu_out = dglu.out;
         a.dglu_ld = dglu.ld;
     }
+    a.sq_part = sq.part;
+    a.sq_nf = sq.nf;
+    a.sq_cap = sq.cap;
     hip::gemm(a, s);
 }
 
 // Weight gradients dW_i = A_i^T B_i (fp32 out) of independent products in one launch.
 void wgrad_grouped(Profiler& prof, std::initializer_list<std::array<const void*, 3>> ops,
-                   std::initializer_list<std::array<int64_t, 3>> mnk, DType ab, hipStream_t s) {
+                   std::initializer_list<std::array<int64_t, 3>> mnk, DType ab, hipStream_t s, SqOut sq = {}) {
     std::vector<hip::GemmArgs> v;
     double flops = 0.0, bytes = 0.0;
     auto op = ops.begin();
@@ -163,6 +173,9 @@ void wgrad_grouped(Profiler& prof, std::initializer_list<std::array<const void*,
         bytes += static_cast<double>(dtype_size(ab)) * (d[0] * d[2] + d[1] * d[2]) + 4.0 * d[0] * d[1];
         ++op;
     }
+    v[0].sq_part = sq.part;  // the whole launch's sums of squares
+    v[0].sq_nf = sq.nf;
+    v[0].sq_cap = sq.cap;
     auto scope = prof.scope(kGemmWgrad, flops, bytes, s);
     hip::gemm_grouped(v.data(), static_cast<int>(v.size()), s);
 }
@@ -404,6 +417,26 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     const float one = 1.0f;
     AIC_HIP_CHECK(hipMalloc(&one_dev_, sizeof(float)));
     AIC_HIP_CHECK(hipMemcpy(one_dev_, &one, sizeof(float), hipMemcpyHostToDevice));
+    // fused gradient norm: the dense model with an untied head, whose every gradient comes from
+    // the layers' grouped weight-gradient launches, the head's GEMM, the embedding backward and
+    // the norm weights (checked against the tensor list)
+    if (E == 0 && !qlora && !cfg.tie_word_embeddings) {
+        int64_t covered = L * (4 * d * d + 3 * f * d + 2 * d) + 2 * V * d + d, listed = 0;
+        for (const ParamInfo& p : params_) listed += p.numel;
+        sq_fold_ = covered == listed;
+    }
+    if (sq_fold_) {
+        std::vector<int64_t> sizes(1, V * d);
+        sizes.resize(2 * L + 2, d);
+        sq_slots_ = (L + 1) * kSqRegion + hip::sqnorm_slots(sizes.data(), static_cast<int>(sizes.size()));
+        const int64_t nt = hip::sqnorm_reduce_tmp(sq_slots_);
+        AIC_HIP_CHECK(hipMalloc(&sq_part_, sizeof(double) * static_cast<size_t>(sq_slots_)));
+        AIC_HIP_CHECK(hipMalloc(&sq_nf_, sizeof(int) * static_cast<size_t>(sq_slots_)));
+        AIC_HIP_CHECK(hipMalloc(&sq_tmp_, sizeof(double) * static_cast<size_t>(nt)));
+        AIC_HIP_CHECK(hipMalloc(&sq_tmp_nf_, sizeof(int) * static_cast<size_t>(nt)));
+        AIC_HIP_CHECK(hipMemset(sq_part_, 0, sizeof(double) * static_cast<size_t>(sq_slots_)));
+        AIC_HIP_CHECK(hipMemset(sq_nf_, 0, sizeof(int) * static_cast<size_t>(sq_slots_)));
+    }
     if (E > 0) {
         AIC_HIP_CHECK(hipMalloc(&aux_dev_, sizeof(float) * static_cast<size_t>(L)));
         AIC_HIP_CHECK(hipMemset(aux_dev_, 0, sizeof(float) * static_cast<size_t>(L)));
@@ -425,7 +458,9 @@ TransformerLM::~TransformerLM() {
                     static_cast<void*>(v_dev_), low_dev_, static_cast<void*>(cos_dev_), static_cast<void*>(sin_dev_),
                     static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
         if (p) (void)hipFree(p);
-    for (void* p : {static_cast<void*>(hist_), static_cast<void*>(hist_count_), static_cast<void*>(backup_)})
+    for (void* p : {static_cast<void*>(hist_), static_cast<void*>(hist_count_), static_cast<void*>(backup_),
+                    static_cast<void*>(sq_part_), static_cast<void*>(sq_nf_), static_cast<void*>(sq_tmp_),
+                    static_cast<void*>(sq_tmp_nf_)})
         if (p) (void)hipFree(p);
     if (lora())
         for (void* p : {static_cast<void*>(base_dev_), base_low_, static_cast<void*>(q4_), q4s_})
@@ -920,7 +955,14 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         gemm(prof_, 1, 0, n_out, r, T, dy, lddy, xs, ldxs, G(boff), r, dt, DType::Float32, s);
         gemm(prof_, 0, 0, T, r, n_out, dy, lddy, W(boff), r, dxa_out, lddxa, dt, dt, s, nullptr, 0, 0.0f, lsc);
     };
-    if (!ql) gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s);
+    // the gradient norm's partial sums, where the step forms it from the producers (sq_fold)
+    const bool fold = sq_fold_ && sq_fold_on_;
+    auto sq_region = [&](int64_t r) {
+        return fold ? SqOut{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion} : SqOut{};
+    };
+    if (!ql)
+        gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s, nullptr, 0, 0.0f, 1.0f,
+             nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L));
     gemm(prof_, 0, 0, T, d, V, dl, V, WB(head_), d, dh.get(), d, dt, dt, s);
     {
         auto _p = prof_.scope(kNormBwd, 0.0, 3.0 * es * T * d + 4.0 * T, s);
@@ -1008,7 +1050,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             wgrad_grouped(prof_,
                           {{dqkv.get(), h1l, G(ly.wqkv)}, {dxm.get(), ol, G(ly.wo)},
                            {dgu.get(), at(h2, l * T * d), G(ly.wgu)}, {dx.get(), at(am, l * T * f), G(ly.wd)}},
-                          {{3 * d, d, T}, {d, d, T}, {2 * f, d, T}, {d, f, T}}, dt, s);
+                          {{3 * d, d, T}, {d, d, T}, {2 * f, d, T}, {d, f, T}}, dt, s, sq_region(l));
         }
         gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
              0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
@@ -1026,7 +1068,23 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     // ---- optimizer tail: scaler -> clip_grad_norm_ -> AdamW (src/train/trainer.cpp:70-95) ----
     const float* gp[1] = {grads_dev_};
     const int64_t sizes[1] = {arena_};
-    {
+    if (fold) {
+        // the weight gradients' partial sums came from their GEMMs; the embedding's and the
+        // norm weights' are added here, then every slot in a fixed order
+        std::vector<const float*> eg(1, G(emb_));
+        std::vector<int64_t> en(1, V * d);
+        for (const Layer& ly : layers_) {
+            eg.push_back(G(ly.n1));
+            eg.push_back(G(ly.n2));
+        }
+        eg.push_back(G(normf_));
+        en.resize(eg.size(), d);
+        auto _p = prof_.scope(kGradNorm, 0.0, 4.0 * (V * d + (2 * L + 1) * d) + 12.0 * sq_slots_, s);
+        hip::sqnorm_partials(eg.data(), en.data(), static_cast<int>(eg.size()), sq_part_ + (L + 1) * kSqRegion,
+                             sq_nf_ + (L + 1) * kSqRegion, s);
+        hip::sqnorm_reduce(sq_part_, sq_nf_, sq_slots_, sq_tmp_, sq_tmp_nf_, &dev_->sqnorm, &dev_->nonfinite, s);
+        hip::optim_finalize(&dev_->sqnorm, &dev_->nonfinite, &dev_->ctl, s);
+    } else {
         auto _p = prof_.scope(kGradNorm, 0.0, 4.0 * arena_, s);
         hip::grad_sqnorm_multi(gp, sizes, 1, &dev_->sqnorm, &dev_->nonfinite, s);
         hip::optim_finalize(&dev_->sqnorm, &dev_->nonfinite, &dev_->ctl, s);

@@ -167,6 +167,14 @@ public:
     }
     std::vector<KernelClassStats> profile_stats() { return prof_.collect(); }
 
+    // Whether the training step forms the gradient norm from partial sums written by the
+    // gradients' producers (dense models with an untied LM head) instead of a separate pass
+    // over every gradient; on by default where the model allows it.  Returns whether it is used.
+    bool set_fused_grad_norm(bool on) {
+        sq_fold_on_ = on;
+        return sq_fold_ && sq_fold_on_;
+    }
+
 private:
     struct Layer {
         int64_t wqkv, wo, wgu, wd, n1, n2;  // base arena offsets (wgu / wd: dense FFN)
@@ -230,6 +238,17 @@ private:
     int64_t hist_read_ = 0;            // host: records already returned
     float* backup_ = nullptr;          // snapshot: params, m, v (3 arenas) then the device scalars
     int64_t kv_B_ = 0;
+    // Gradient-norm partials (fused gradient norm): a region of kSqRegion slots per layer's
+    // weight-gradient launch, one for the LM head's, then the embedding's and the norm weights'
+    // sqnorm_k partials; fp64 sums and non-finite flags, zero where no producer writes.
+    static constexpr int64_t kSqRegion = 4096;
+    bool sq_fold_ = false;    // the model allows it
+    bool sq_fold_on_ = true;  // switched on
+    double* sq_part_ = nullptr;
+    int* sq_nf_ = nullptr;
+    int64_t sq_slots_ = 0;
+    double* sq_tmp_ = nullptr;
+    int* sq_tmp_nf_ = nullptr;
     Profiler prof_;
 };
 

@@ -288,6 +288,14 @@ class TransformerLM:
         _lib.call("aic_lm_last_stats", self._h, C.byref(st))
         return StepMetrics(st.loss, st.grad_norm, bool(st.found_inf), st.loss_scale, int(st.step), float(st.aux_loss))
 
+    def fused_grad_norm(self, on: bool) -> bool:
+        """Form the step's gradient norm from the producers' partial sums (True, the default
+        where the model allows it) or from a pass over every gradient (False); returns whether
+        the fused form is now used."""
+        used = C.c_int(0)
+        _lib.call("aic_lm_fused_grad_norm", self._h, 1 if on else 0, C.byref(used))
+        return bool(used.value)
+
     def set_profiling(self, on: bool, classes=None) -> None:
         """Time the kernel launches of the following steps with HIP events (resets); `classes`
         (names) restricts the timing to those kernel classes."""

@@ -628,6 +628,15 @@ int aic_lm_profile_class_index(const char* name);
 /* Synchronises, then writes up to cap classes with at least one launch; *n = count. */
 int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n);
 
+/* Whether the training step forms the gradient norm (clip_grad_norm_ and the loss scaler's
+ * non-finite test) from partial sums written by the gradients' producers -- the weight-gradient
+ * GEMMs' epilogues, the split-K reductions, then the embedding and norm weights -- instead of a
+ * separate pass over every gradient.  On by default where the model allows it (dense FFNs, an
+ * untied LM head); enable = 0 selects the pass.  *used (may be null) = whether it is now used.
+ * The norm is the same sum in another order (fp64 partials of fp32 squares).
+ * Replaces: the norm pass of clip_grad_norm_ (src/optim/clip_grad.cpp:11-53). */
+int aic_lm_fused_grad_norm(aic_lm* lm, int enable, int* used);
+
 /* ---------------------------------------------------------------- checkpoints ------- */
 /* The reference's .aic format (save_checkpoint / load_checkpoint, src/train/checkpoint.cpp:30-186;
  * docs/architecture.md:96-117): header (magic 'AIC0', version 1, step, epoch, best_val_loss,

@@ -262,6 +262,45 @@ def test_1b_widths_step_matches_oracle(orc):
     model.close()
 
 
+def test_1b_widths_fused_grad_norm_equals_pass():
+    """The step's gradient norm formed from the producers' partial sums (the weight-gradient
+    GEMMs' epilogues, the split-K reduction of the grouped launch's carved tiles, then the
+    embedding and norm weights) against the pass over every gradient, at configs[2]'s widths with
+    2 layers: the same loss and gradients bit for bit, the norm within 1e-6 (the same fp64 sum of
+    fp32 squares in another order), the same update within 1e-6; a NaN in one weight is flagged
+    by both forms and the step skipped with the parameters unchanged."""
+    c = C1B
+    S = c["S"]
+    ids, tgt = aic.batch(1234, 1, S, c["vocab"], dist="zipf")
+    out = {}
+    for fused in (True, False):
+        model = build_dense(c, L=2)
+        assert model.fused_grad_norm(fused) == fused
+        params = normal_params(model.layout, 5678)
+        model.set_params(params)
+        st = model.train_step(ids, tgt, 1, S)
+        out[fused] = (st, model.get_grads(), model.get_params())
+        model.close()
+    (sf, gf, pf), (sp, gp, pp) = out[True], out[False]
+    print(f"  grad norm fused {sf.grad_norm!r} pass {sp.grad_norm!r}")
+    assert sf.loss == sp.loss and not sf.found_inf and not sp.found_inf
+    np.testing.assert_array_equal(gf, gp)
+    assert abs(sf.grad_norm - sp.grad_norm) <= 1e-6 * sp.grad_norm
+    assert rel(pf, pp) < 1e-6
+
+    bad = params.copy()
+    off = [e for e in model.layout if e[0] == "layers.1.norm2.weight"][0][2]
+    bad[off + 5] = np.nan
+    for fused in (True, False):
+        model = build_dense(c, L=2)
+        model.fused_grad_norm(fused)
+        model.set_params(bad)
+        st = model.train_step(ids, tgt, 1, S)
+        assert st.found_inf and st.step == 0 and st.loss_scale == 65536.0
+        np.testing.assert_array_equal(model.get_params(), bad)
+        model.close()
+
+
 def test_1b_full_config(orc):
     """configs[2] at full size: 16 layers, B 4 x S 2048, N(0, 0.02) weights, bf16 AMP, clip 1.0."""
     c = C1B
