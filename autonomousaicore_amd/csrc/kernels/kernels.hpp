@@ -16,6 +16,15 @@ void rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ld
 void rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
                  const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
                  int64_t dim, DType dt, hipStream_t s);
+// rmsnorm_bwd whose weight gradient is left as rmsnorm_bwd_part_rows(rows) partial rows of dim
+// floats in `part` (dim % 8 == 0); rmsnorm_dw_reduce later overwrites each dws[t] with the sum
+// of parts[t]'s rows in rmsnorm_bwd's own order (bit-identical to it), all norms in one launch.
+int64_t rmsnorm_bwd_part_rows(int64_t rows);
+void rmsnorm_bwd_deferred(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                          const void* dres, int64_t ldres, void* dx, int64_t lddx, float* part, int64_t rows,
+                          int64_t dim, DType dt, hipStream_t s);
+void rmsnorm_dw_reduce(const float* const* parts, float* const* dws, int count, int64_t rows, int64_t dim,
+                       hipStream_t s);
 
 // RoPE (rope.hip)
 void rope(void* x, int64_t ld, int64_t B, int64_t S, int64_t heads, int64_t hd, int64_t start_pos, const float* cos_t,

@@ -3,6 +3,8 @@
 // HBM-bound: one wave per row, 16-byte vector loads; the weight gradient is reduced
 // per block into per-wave LDS slices and then across blocks in a fixed order
 // (deterministic, no atomics).
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "../runtime/memory_pool.hpp"
@@ -260,10 +262,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_r(const T* __restrict__ dy, i
 
 // dw = sum of the per-block partials, 8 columns per block so the whole chip takes part: thread t
 // adds partials t, t + 256, ... of its column pair in order, then a fixed-order block tree.
-__global__ __launch_bounds__(256) void reduce_parts8_k(const float* __restrict__ part, int nparts, int dim,
-                                                       float* dw, int accumulate) {
+__device__ __forceinline__ void reduce_parts8_body(const float* __restrict__ part, int nparts, int dim, float* dw,
+                                                   int accumulate, int c0) {
     __shared__ float red[256][9];
-    const int c0 = blockIdx.x * 8;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -299,6 +300,21 @@ __global__ __launch_bounds__(256) void reduce_parts8_k(const float* __restrict__
         const int j = c0 + threadIdx.x;
         dw[j] = accumulate ? dw[j] + red[0][threadIdx.x] : red[0][threadIdx.x];
     }
+}
+
+__global__ __launch_bounds__(256) void reduce_parts8_k(const float* __restrict__ part, int nparts, int dim,
+                                                       float* dw, int accumulate) {
+    reduce_parts8_body(part, nparts, dim, dw, accumulate, blockIdx.x * 8);
+}
+
+// reduce_parts8_k for several norms at once: blockIdx.y = norm t, with its partial rows and dw.
+constexpr int kDwBatch = 64;
+struct DwBatch {
+    const float* part[kDwBatch];
+    float* dw[kDwBatch];
+};
+__global__ __launch_bounds__(256) void reduce_parts8_batch_k(const DwBatch b, int nparts, int dim) {
+    reduce_parts8_body(b.part[blockIdx.y], nparts, dim, b.dw[blockIdx.y], 0, blockIdx.x * 8);
 }
 
 __global__ __launch_bounds__(1024) void reduce_parts_k(const float* __restrict__ part, int nparts, int dim, float* dw,
@@ -359,7 +375,7 @@ void fwd_t(const void* x, int64_t ldx, const float* w, void* y, int64_t ldy, flo
 template <typename T>
 void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
            const void* dres, int64_t ldres, void* dx, int64_t lddx, float* dw, bool accumulate, int64_t rows,
-           int64_t dim, hipStream_t s) {
+           int64_t dim, hipStream_t s, float* ext_part = nullptr) {
     constexpr int VN = Vec<T>::N;
     const bool vec = vec_ok(dy, lddy, dim, VN, sizeof(T)) && vec_ok(x, ldx, dim, VN, sizeof(T)) &&
                      vec_ok(dx, lddx, dim, VN, sizeof(T)) && (!dres || vec_ok(dres, ldres, dim, VN, sizeof(T)));
@@ -367,8 +383,8 @@ void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float
     const bool reg = vec && ch > 0;
     const int64_t rows_per_block = 4 * (reg ? kBwdRegRowsPerWave : kBwdRowsPerWave);
     const unsigned grid = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
-    float* part = nullptr;
-    if (dw) part = static_cast<float*>(stream_scratch(sizeof(float) * grid * dim, s));
+    float* part = ext_part;  // the caller's partial rows (reduced later), or scratch reduced below
+    if (dw && !part) part = static_cast<float*>(stream_scratch(sizeof(float) * grid * dim, s));
     const size_t lds = dw ? sizeof(float) * 4 * dim : 0;
     AIC_CHECK(lds <= 160 * 1024, InvalidArgument, "rmsnorm_bwd: dim too large for the LDS weight-gradient slices");
 #define AIC_BWD_R(CH)                                                                                         \
@@ -389,7 +405,7 @@ void bwd_t(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float
                            static_cast<const T*>(x), ldx, w, rms, static_cast<const T*>(dres), ldres,
                            static_cast<T*>(dx), lddx, part, rows, static_cast<int>(dim));
     AIC_LAUNCH_CHECK("rmsnorm_bwd");
-    if (dw) {
+    if (dw && !ext_part) {
         if (dim % 8 == 0)
             hipLaunchKernelGGL(reduce_parts8_k, dim3(static_cast<unsigned>(dim / 8)), dim3(256), 0, s, part,
                                static_cast<int>(grid), static_cast<int>(dim), dw, accumulate ? 1 : 0);
@@ -409,6 +425,39 @@ void rmsnorm_fwd(const void* x, int64_t ldx, const float* w, void* y, int64_t ld
     if (dt == DType::Float32) fwd_t<float>(x, ldx, w, y, ldy, rms, rows, dim, eps, s);
     else if (dt == DType::BFloat16) fwd_t<bf16>(x, ldx, w, y, ldy, rms, rows, dim, eps, s);
     else AIC_THROW(DTypeMismatch, "rmsnorm_fwd: dtype must be f32 or bf16");
+}
+
+static_assert(kBwdRowsPerWave == kBwdRegRowsPerWave, "both backward forms take 16 rows per block");
+
+int64_t rmsnorm_bwd_part_rows(int64_t rows) { return (rows + 4 * kBwdRowsPerWave - 1) / (4 * kBwdRowsPerWave); }
+
+void rmsnorm_bwd_deferred(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,
+                          const void* dres, int64_t ldres, void* dx, int64_t lddx, float* part, int64_t rows,
+                          int64_t dim, DType dt, hipStream_t s) {
+    AIC_CHECK(rows > 0 && dim > 0 && dim % 8 == 0 && lddy >= dim && ldx >= dim && lddx >= dim && part,
+              InvalidArgument, "rmsnorm_bwd_deferred: bad shape");
+    if (dt == DType::Float32)
+        bwd_t<float>(dy, lddy, x, ldx, w, rms, dres, ldres, dx, lddx, part, false, rows, dim, s, part);
+    else if (dt == DType::BFloat16)
+        bwd_t<bf16>(dy, lddy, x, ldx, w, rms, dres, ldres, dx, lddx, part, false, rows, dim, s, part);
+    else AIC_THROW(DTypeMismatch, "rmsnorm_bwd_deferred: dtype must be f32 or bf16");
+}
+
+void rmsnorm_dw_reduce(const float* const* parts, float* const* dws, int count, int64_t rows, int64_t dim,
+                       hipStream_t s) {
+    AIC_CHECK(count >= 0 && rows > 0 && dim > 0 && dim % 8 == 0, InvalidArgument, "rmsnorm_dw_reduce: bad shape");
+    const int nparts = static_cast<int>(rmsnorm_bwd_part_rows(rows));
+    for (int t0 = 0; t0 < count; t0 += kDwBatch) {
+        DwBatch b;
+        const int n = std::min(count - t0, kDwBatch);
+        for (int i = 0; i < kDwBatch; ++i) {
+            b.part[i] = parts[t0 + std::min(i, n - 1)];
+            b.dw[i] = dws[t0 + std::min(i, n - 1)];
+        }
+        hipLaunchKernelGGL(reduce_parts8_batch_k, dim3(static_cast<unsigned>(dim / 8), static_cast<unsigned>(n)),
+                           dim3(256), 0, s, b, nparts, static_cast<int>(dim));
+        AIC_LAUNCH_CHECK("rmsnorm_dw_reduce");
+    }
 }
 
 void rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* w, const float* rms,

@@ -964,10 +964,28 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s, nullptr, 0, 0.0f, 1.0f,
              nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L));
     gemm(prof_, 0, 0, T, d, V, dl, V, WB(head_), d, dh.get(), d, dt, dt, s);
+    // The norms' weight gradients: each backward leaves its partial rows in dwp and one launch
+    // after the layer loop reduces them all (the same sums in the same order), where the shape
+    // allows; the optimizer tail is their only reader.
+    const bool defer_dw = !ql && d % 8 == 0;
+    const int64_t prow = hip::rmsnorm_bwd_part_rows(T);
+    float* dwp = defer_dw ? f32((2 * L + 1) * prow * d).as<float>() : nullptr;
+    std::vector<const float*> dw_parts;
+    std::vector<float*> dw_dst;
+    auto norm_bwd = [&](const void* dy, const void* xn, const float* w, const float* rms, const void* dres,
+                        void* out, float* dwt) {
+        if (defer_dw && dwt) {
+            float* part = dwp + static_cast<int64_t>(dw_parts.size()) * prow * d;
+            hip::rmsnorm_bwd_deferred(dy, d, xn, d, w, rms, dres, d, out, d, part, T, d, dt, s);
+            dw_parts.push_back(part);
+            dw_dst.push_back(dwt);
+        } else {
+            hip::rmsnorm_bwd(dy, d, xn, d, w, rms, dres, d, out, d, dwt, false, T, d, dt, s);
+        }
+    };
     {
         auto _p = prof_.scope(kNormBwd, 0.0, 3.0 * es * T * d + 4.0 * T, s);
-        hip::rmsnorm_bwd(dh.get(), d, xL, d, PB(normf_), rf.as<float>(), nullptr, 0, dx.get(), d, GB(normf_), false,
-                         T, d, dt, s);
+        norm_bwd(dh.get(), xL, PB(normf_), rf.as<float>(), nullptr, dx.get(), GB(normf_));
     }
     for (int64_t l = L - 1; l >= 0; --l) {
         const Layer& ly = layers_[l];
@@ -1009,8 +1027,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         }
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x1l, d, PB(ly.n2), atf(r2, l * T), dx.get(), d, dxm.get(), d, GB(ly.n2),
-                             false, T, d, dt, s);
+            norm_bwd(dh.get(), x1l, PB(ly.n2), atf(r2, l * T), dx.get(), dxm.get(), GB(ly.n2));
         }
         // x1 = x + out_proj(attn(rope(q), rope(k), v))
         LowRank lo_{};
@@ -1056,9 +1073,13 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
              0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
         {
             auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * es * T * d + 4.0 * T, s);
-            hip::rmsnorm_bwd(dh.get(), d, x, d, PB(ly.n1), atf(r1, l * T), dxm.get(), d, dx.get(), d, GB(ly.n1),
-                             false, T, d, dt, s);
+            norm_bwd(dh.get(), x, PB(ly.n1), atf(r1, l * T), dxm.get(), dx.get(), GB(ly.n1));
         }
+    }
+    if (!dw_parts.empty()) {
+        const double n = static_cast<double>(dw_parts.size());
+        auto _p = prof_.scope(kNormBwd, 0.0, 4.0 * n * prow * d + 4.0 * n * d, s);
+        hip::rmsnorm_dw_reduce(dw_parts.data(), dw_dst.data(), static_cast<int>(dw_parts.size()), T, d, s);
     }
     if (!ql) {
         auto _p = prof_.scope(kEmbedBwd, 0.0, es * T * d + 4.0 * V * d + 8.0 * T, s);
