@@ -430,12 +430,11 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
         sizes.resize(2 * L + 2, d);
         sq_slots_ = (L + 1) * kSqRegion + hip::sqnorm_slots(sizes.data(), static_cast<int>(sizes.size()));
         const int64_t nt = hip::sqnorm_reduce_tmp(sq_slots_);
-        AIC_HIP_CHECK(hipMalloc(&sq_part_, sizeof(double) * static_cast<size_t>(sq_slots_)));
-        AIC_HIP_CHECK(hipMalloc(&sq_nf_, sizeof(int) * static_cast<size_t>(sq_slots_)));
+        // the partials, then the flags, in one allocation (cleared by one fill per step)
+        AIC_HIP_CHECK(hipMalloc(&sq_part_, (sizeof(double) + sizeof(int)) * static_cast<size_t>(sq_slots_)));
+        sq_nf_ = reinterpret_cast<int*>(sq_part_ + sq_slots_);
         AIC_HIP_CHECK(hipMalloc(&sq_tmp_, sizeof(double) * static_cast<size_t>(nt)));
         AIC_HIP_CHECK(hipMalloc(&sq_tmp_nf_, sizeof(int) * static_cast<size_t>(nt)));
-        AIC_HIP_CHECK(hipMemset(sq_part_, 0, sizeof(double) * static_cast<size_t>(sq_slots_)));
-        AIC_HIP_CHECK(hipMemset(sq_nf_, 0, sizeof(int) * static_cast<size_t>(sq_slots_)));
     }
     if (E > 0) {
         AIC_HIP_CHECK(hipMalloc(&aux_dev_, sizeof(float) * static_cast<size_t>(L)));
@@ -459,8 +458,7 @@ TransformerLM::~TransformerLM() {
                     static_cast<void*>(dev_), static_cast<void*>(one_dev_), static_cast<void*>(aux_dev_)})
         if (p) (void)hipFree(p);
     for (void* p : {static_cast<void*>(hist_), static_cast<void*>(hist_count_), static_cast<void*>(backup_),
-                    static_cast<void*>(sq_part_), static_cast<void*>(sq_nf_), static_cast<void*>(sq_tmp_),
-                    static_cast<void*>(sq_tmp_nf_)})
+                    static_cast<void*>(sq_part_), static_cast<void*>(sq_tmp_), static_cast<void*>(sq_tmp_nf_)})
         if (p) (void)hipFree(p);
     if (lora())
         for (void* p : {static_cast<void*>(base_dev_), base_low_, static_cast<void*>(q4_), q4s_})
@@ -960,6 +958,9 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     auto sq_region = [&](int64_t r) {
         return fold ? SqOut{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion} : SqOut{};
     };
+    // every slot starts at zero: a launch writes only the slots of its path, which can change with
+    // the token count (T not a multiple of 64 leaves the tile kernels)
+    if (fold) hip::fill_const(reinterpret_cast<float*>(sq_part_), sq_slots_ * 3, 0.0f, s);
     if (!ql)
         gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s, nullptr, 0, 0.0f, 1.0f,
              nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L));

@@ -244,7 +244,7 @@ private:
     static constexpr int64_t kSqRegion = 4096;
     bool sq_fold_ = false;    // the model allows it
     bool sq_fold_on_ = true;  // switched on
-    double* sq_part_ = nullptr;
+    double* sq_part_ = nullptr;  // sq_slots_ partials, then sq_slots_ flags (sq_nf_)
     int* sq_nf_ = nullptr;
     int64_t sq_slots_ = 0;
     double* sq_tmp_ = nullptr;

@@ -267,11 +267,14 @@ def test_1b_widths_fused_grad_norm_equals_pass():
     GEMMs' epilogues, the split-K reduction of the grouped launch's carved tiles, then the
     embedding and norm weights) against the pass over every gradient, at configs[2]'s widths with
     2 layers: the same loss and gradients bit for bit, the norm within 1e-6 (the same fp64 sum of
-    fp32 squares in another order), the same update within 1e-6; a NaN in one weight is flagged
-    by both forms and the step skipped with the parameters unchanged."""
+    fp32 squares in another order), the same update within 1e-6 -- then a second step of 1000
+    tokens, where the weight gradients leave the tile kernels (K not a multiple of 64) and other
+    slots are written; a NaN in one weight is flagged by both forms and the step skipped with
+    the parameters unchanged."""
     c = C1B
     S = c["S"]
     ids, tgt = aic.batch(1234, 1, S, c["vocab"], dist="zipf")
+    ids2, tgt2 = aic.batch(4321, 1, 1000, c["vocab"], dist="zipf")
     out = {}
     for fused in (True, False):
         model = build_dense(c, L=2)
@@ -279,14 +282,21 @@ def test_1b_widths_fused_grad_norm_equals_pass():
         params = normal_params(model.layout, 5678)
         model.set_params(params)
         st = model.train_step(ids, tgt, 1, S)
-        out[fused] = (st, model.get_grads(), model.get_params())
+        first = (st, model.get_grads(), model.get_params())
+        st2 = model.train_step(ids2, tgt2, 1, 1000)
+        out[fused] = (first, (st2, model.get_grads(), model.get_params()))
         model.close()
-    (sf, gf, pf), (sp, gp, pp) = out[True], out[False]
-    print(f"  grad norm fused {sf.grad_norm!r} pass {sp.grad_norm!r}")
-    assert sf.loss == sp.loss and not sf.found_inf and not sp.found_inf
-    np.testing.assert_array_equal(gf, gp)
-    assert abs(sf.grad_norm - sp.grad_norm) <= 1e-6 * sp.grad_norm
-    assert rel(pf, pp) < 1e-6
+    for k in range(2):
+        (sf, gf, pf), (sp, gp, pp) = out[True][k], out[False][k]
+        print(f"  step {k + 1}: grad norm fused {sf.grad_norm!r} pass {sp.grad_norm!r}")
+        assert not sf.found_inf and not sp.found_inf
+        if k == 0:
+            assert sf.loss == sp.loss
+            np.testing.assert_array_equal(gf, gp)
+        else:  # the weights differ by the first update's rounding
+            assert abs(sf.loss - sp.loss) <= 1e-5 * abs(sp.loss) and rel(gf, gp) < 1e-4
+        assert abs(sf.grad_norm - sp.grad_norm) <= (1e-6 if k == 0 else 1e-4) * sp.grad_norm
+        assert rel(pf, pp) < 1e-6
 
     bad = params.copy()
     off = [e for e in model.layout if e[0] == "layers.1.norm2.weight"][0][2]
