@@ -133,6 +133,7 @@ void optim_finalize(const double* sqnorm, const int* nonfinite, void* ctl, hipSt
 // entries) into *sqnorm and the OR of the flags into *nonfinite.
 int64_t sqnorm_slots(const int64_t* sizes, int count);
 void sqnorm_partials(const float* const* grads, const int64_t* sizes, int count, double* pd, int* pn, hipStream_t s);
+void sqnorm_clear(double* pd, int* pn, int64_t nslots, hipStream_t s);  // every slot to 0
 int64_t sqnorm_reduce_tmp(int64_t nslots);
 void sqnorm_reduce(const double* pd, const int* pn, int64_t nslots, double* tmp_d, int* tmp_n, double* sqnorm,
                    int* nonfinite, hipStream_t s);

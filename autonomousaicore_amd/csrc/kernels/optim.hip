@@ -150,6 +150,14 @@ __global__ __launch_bounds__(1024) void sqsum_level1_k(const double* __restrict_
         out_nf[blockIdx.x] = sn[0];
     }
 }
+// Zeroes n gradient-norm slots (fp64 partials, then int flags).
+__global__ __launch_bounds__(256) void sqslot_clear_k(double* part, int* part_nf, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        part[i] = 0.0;
+        part_nf[i] = 0;
+    }
+}
 __global__ void scale_k(float* g, int64_t n, const float* scale) {
     const float s = *scale;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -420,6 +428,13 @@ void sqnorm_partials(const float* const* grads, const int64_t* sizes, int count,
         AIC_LAUNCH_CHECK("grad_sqnorm_multi");
         off += m.first[m.count];
     }
+}
+
+void sqnorm_clear(double* pd, int* pn, int64_t nslots, hipStream_t s) {
+    if (nslots <= 0) return;
+    hipLaunchKernelGGL(sqslot_clear_k, dim3(static_cast<unsigned>(std::min<int64_t>((nslots + 255) / 256, 1024))),
+                       dim3(256), 0, s, pd, pn, nslots);
+    AIC_LAUNCH_CHECK("sqslot_clear");
 }
 
 int64_t sqnorm_reduce_tmp(int64_t nslots) { return std::max<int64_t>(1, (nslots + 4095) / 4096); }

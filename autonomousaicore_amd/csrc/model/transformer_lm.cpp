@@ -960,7 +960,10 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     };
     // every slot starts at zero: a launch writes only the slots of its path, which can change with
     // the token count (T not a multiple of 64 leaves the tile kernels)
-    if (fold) hip::fill_const(reinterpret_cast<float*>(sq_part_), sq_slots_ * 3, 0.0f, s);
+    if (fold) {
+        auto _p = prof_.scope(kGradNorm, 0.0, 12.0 * sq_slots_, s);
+        hip::sqnorm_clear(sq_part_, sq_nf_, sq_slots_, s);
+    }
     if (!ql)
         gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s, nullptr, 0, 0.0f, 1.0f,
              nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L));

@@ -58,7 +58,10 @@ _RULES = [
     (r"ce_bwd", "ce_bwd"),
     (r"embed_fwd", "embed_fwd"),
     (r"embed_chunk_sort|embed_merge_rank|embed_seg|embed_run|embed_zero_absent", "embed_bwd"),
-    (r"sqnorm|finalize", "grad_norm"),
+    # the norm pass, or (fused) the slot clear, the embedding / norm-weight partials and the
+    # two-level sum of every slot
+    (r"sqnorm|sqsum|sqslot|finalize", "grad_norm"),
+    (r"sq_matrix", "gemm_wgrad"),
     (r"adamw", "adamw"),
     # kernels outside bench.py's event classes (the MoE and QLoRA configurations)
     (r"moe_", "moe_routing"),
@@ -73,7 +76,7 @@ _RULES = [
 _ANCHOR = {
     "attn_bwd": r"attn_bwd_dq",
     "rmsnorm_bwd": r"rmsnorm_bwd",
-    "grad_norm": r"sqnorm_k",
+    "grad_norm": r"sqnorm_final",
     "ce_fwd_bwd": r"ce_fused",
     "embed_bwd": r"embed_chunk_sort",
 }
