@@ -12,7 +12,7 @@ namespace aic::models {
 namespace {
 
 void gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B, int64_t ldb,
-          void* C, int64_t ldc, DType ab, DType c, hipStream_t s, float beta = 0.0f) {
+          void* C, int64_t ldc, DType ab, DType c, hipStream_t s, float beta = 0.0f, SqSlots sq = {}) {
     hip::GemmArgs a;
     a.transA = ta;
     a.transB = tb;
@@ -28,6 +28,9 @@ void gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_
     a.beta = beta;
     a.ab = ab;
     a.c = c;
+    a.sq_part = sq.part;
+    a.sq_nf = sq.nf;
+    a.sq_cap = sq.cap;
     hip::gemm(a, s);
 }
 
@@ -50,10 +53,19 @@ hip::GemmArgs args(int ta, int tb, int64_t M, int64_t N, int64_t K, const void* 
     return a;
 }
 
-// The experts' products of one kind in launches of up to 8 (hip::gemm_grouped).
-void run_grouped(const std::vector<hip::GemmArgs>& v, hipStream_t s) {
-    for (size_t i = 0; i < v.size(); i += 8)
+// The experts' products of one kind in launches of up to 8 (hip::gemm_grouped); with sq, each
+// launch's sums of squares go to its share of the region.
+void run_grouped(std::vector<hip::GemmArgs> v, hipStream_t s, SqSlots sq = {}) {
+    const size_t launches = (v.size() + 7) / 8;
+    for (size_t i = 0; i < v.size(); i += 8) {
+        if (sq.part) {
+            const int64_t share = sq.cap / static_cast<int64_t>(launches), c = static_cast<int64_t>(i / 8);
+            v[i].sq_part = sq.part + c * share;
+            v[i].sq_nf = sq.nf + c * share;
+            v[i].sq_cap = share;
+        }
         hip::gemm_grouped(v.data() + i, static_cast<int>(std::min<size_t>(8, v.size() - i)), s);
+    }
 }
 
 }  // namespace
@@ -88,9 +100,13 @@ const std::vector<int64_t>& MoEFFN::counts_host() {
 // One kind of expert product: g is expert 0's product at row offset 0 (M or K: the rows).
 // Ragged launch with the device offsets when the layout allows it, else one product per
 // expert from the host offsets.
-void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s) {
+void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s,
+                     SqSlots sq) {
     hip::RaggedArgs r;
     r.g = g;
+    r.g.sq_part = sq.part;
+    r.g.sq_nf = sq.nf;
+    r.g.sq_cap = sq.cap;
     r.offsets = offsets_.as<int64_t>();
     r.E = static_cast<int>(E_);
     r.ragged_k = ragged_k;
@@ -123,9 +139,10 @@ void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int
             a.B = static_cast<const char*>(g.B) + es * e * b_stride;
             a.C = static_cast<char*>(g.C) + ec * o * g.ldc;
         }
+        a.sq_part = nullptr;
         v.push_back(a);
     }
-    run_grouped(v, s);
+    run_grouped(std::move(v), s, sq);
 }
 
 void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* experts_w, const void* R, void* y,
@@ -176,7 +193,8 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
 }
 
 void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s,
-                      const float* daux_scale) {
+                      const float* daux_scale, const SqSlots* sq) {
+    const SqSlots sq_d = sq ? sq[0] : SqSlots{}, sq_gu = sq ? sq[1] : SqSlots{}, sq_r = sq ? sq[2] : SqSlots{};
     AIC_CHECK(T_ > 0 && dy && dh && dwr && dexperts, InvalidArgument, "MoEFFN::backward: forward first, no nulls");
     const size_t es = dtype_size(dt_);
     const int64_t T = T_, f2 = 2 * f_, ex = 3 * f_ * d_, used = used_;
@@ -188,23 +206,23 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
     // down projections: da = dye . Wd and dWd = dye^T . a (fp32, zero for an expert with no rows)
     experts(args(0, 0, used, f_, d_, dye.get(), d_, exb + es * 2 * f_ * d_, f_, da.get(), f_, dt_, dt_), 0, ex, 0, s);
     experts(args(1, 0, d_, f_, 0, dye.get(), d_, a_.get(), f_, dexperts + 2 * f_ * d_, f_, dt_, DType::Float32), 1, 0,
-            ex, s);
+            ex, s, sq_d);
     hip::swiglu_bwd(gu_.get(), static_cast<char*>(gu_.get()) + es * f_, f2, da.get(), f_, dgu.get(),
                     static_cast<char*>(dgu.get()) + es * f_, f2, used, f_, dt_, s);
     // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
     experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s);
-    experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s);
+    experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s, sq_gu);
     hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
     // router: dlogits from the gates and the aux loss, then both router products
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,
                         coef_, daux, daux_scale, dlog.as<float>(), s);
     if (dt_ == DType::Float32) {
-        gemm(1, 0, E_, d_, T, dlog.get(), E_, h_, d_, dwr, d_, DType::Float32, DType::Float32, s);
+        gemm(1, 0, E_, d_, T, dlog.get(), E_, h_, d_, dwr, d_, DType::Float32, DType::Float32, s, 0.0f, sq_r);
         gemm(0, 0, T, d_, E_, dlog.get(), E_, wr_, d_, dh, d_, DType::Float32, DType::Float32, s, 1.0f);
     } else {
         DeviceBuffer dlb(2 * T * E_, s);
         hip::cast_f32_bf16(dlog.as<float>(), dlb.get(), T * E_, s);
-        gemm(1, 0, E_, d_, T, dlb.get(), E_, h_, d_, dwr, d_, DType::BFloat16, DType::Float32, s);
+        gemm(1, 0, E_, d_, T, dlb.get(), E_, h_, d_, dwr, d_, DType::BFloat16, DType::Float32, s, 0.0f, sq_r);
         gemm(0, 0, T, d_, E_, dlb.get(), E_, wr_, d_, dh, d_, DType::BFloat16, DType::BFloat16, s, 1.0f);
     }
 }

@@ -15,6 +15,13 @@
 
 namespace aic::models {
 
+// A slot region for the sums of squares of an fp32 weight gradient (GemmArgs::sq_*).
+struct SqSlots {
+    double* part = nullptr;
+    int* nf = nullptr;
+    int64_t cap = 0;
+};
+
 class MoEFFN {
 public:
     MoEFFN(int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, DType dt);
@@ -26,9 +33,10 @@ public:
                  hipStream_t s);
     // dy [T, d] (dt), daux = dL/daux.  dh [T, d] (dt) is overwritten; dwr [E, d] and dexperts (the
     // experts layout, fp32) are overwritten (zero for an expert that received no token).
-    // daux_scale (device, nullable) multiplies daux (the loss scale of an AMP step).
+    // daux_scale (device, nullable) multiplies daux (the loss scale of an AMP step).  sq (nullable):
+    // slot regions for the sums of squares of the down, gate/up and router weight gradients.
     void backward(const void* dy, float daux, void* dh, float* dwr, float* dexperts, hipStream_t s,
-                  const float* daux_scale = nullptr);
+                  const float* daux_scale = nullptr, const SqSlots* sq = nullptr);
 
     // Routing of the last forward: idx [T, k] and counts [E] (device pointers).
     const int64_t* idx() const { return idx_.as<int64_t>(); }
@@ -45,7 +53,8 @@ private:
     const void* wr_ = nullptr;
     const void* ex_ = nullptr;
     void host_offsets(hipStream_t s);
-    void experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s);
+    void experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s,
+                 SqSlots sq = {});
     int64_t used_ = 0;  // rows of the permuted buffers
     bool host_valid_ = false;
     std::vector<int64_t> counts_h_, offsets_h_;

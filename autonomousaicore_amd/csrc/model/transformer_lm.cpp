@@ -417,18 +417,21 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     const float one = 1.0f;
     AIC_HIP_CHECK(hipMalloc(&one_dev_, sizeof(float)));
     AIC_HIP_CHECK(hipMemcpy(one_dev_, &one, sizeof(float), hipMemcpyHostToDevice));
-    // fused gradient norm: the dense model with an untied head, whose every gradient comes from
-    // the layers' grouped weight-gradient launches, the head's GEMM, the embedding backward and
-    // the norm weights (checked against the tensor list)
-    if (E == 0 && !qlora && !cfg.tie_word_embeddings) {
-        int64_t covered = L * (4 * d * d + 3 * f * d + 2 * d) + 2 * V * d + d, listed = 0;
+    // fused gradient norm: models with an untied head, whose every gradient comes from the
+    // layers' weight-gradient GEMMs (the grouped launch; with MoE FFNs also the experts' and the
+    // router's), the head's GEMM, the embedding backward and the norm weights (checked against
+    // the tensor list)
+    if (!qlora && !cfg.tie_word_embeddings) {
+        const int64_t ffn = E > 0 ? E * d + E * 3 * f * d : 3 * f * d;
+        int64_t covered = L * (4 * d * d + ffn + 2 * d) + 2 * V * d + d, listed = 0;
         for (const ParamInfo& p : params_) listed += p.numel;
         sq_fold_ = covered == listed;
     }
     if (sq_fold_) {
         std::vector<int64_t> sizes(1, V * d);
         sizes.resize(2 * L + 2, d);
-        sq_slots_ = (L + 1) * kSqRegion + hip::sqnorm_slots(sizes.data(), static_cast<int>(sizes.size()));
+        sq_slots_ = (L * sq_regions_per_layer() + 1) * kSqRegion +
+                    hip::sqnorm_slots(sizes.data(), static_cast<int>(sizes.size()));
         const int64_t nt = hip::sqnorm_reduce_tmp(sq_slots_);
         // the partials, then the flags, in one allocation (cleared by one fill per step)
         AIC_HIP_CHECK(hipMalloc(&sq_part_, (sizeof(double) + sizeof(int)) * static_cast<size_t>(sq_slots_)));
@@ -955,9 +958,11 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     };
     // the gradient norm's partial sums, where the step forms it from the producers (sq_fold)
     const bool fold = sq_fold_ && sq_fold_on_;
+    const int64_t RPL = sq_regions_per_layer();
     auto sq_region = [&](int64_t r) {
         return fold ? SqOut{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion} : SqOut{};
     };
+    auto slots = [&](int64_t r) { return SqSlots{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion}; };
     // every slot starts at zero: a launch writes only the slots of its path, which can change with
     // the token count (T not a multiple of 64 leaves the tile kernels)
     if (fold) {
@@ -966,7 +971,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     }
     if (!ql)
         gemm(prof_, 1, 0, V, d, T, dl, V, hf.get(), d, G(head_), d, dt, DType::Float32, s, nullptr, 0, 0.0f, 1.0f,
-             nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L));
+             nullptr, {}, RopeOut{}, GluOut{}, DGlu{}, sq_region(L * RPL));
     gemm(prof_, 0, 0, T, d, V, dl, V, WB(head_), d, dh.get(), d, dt, dt, s);
     // The norms' weight gradients: each backward leaves its partial rows in dwp and one launch
     // after the layer loop reduces them all (the same sums in the same order), where the shape
@@ -1001,7 +1006,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         void* h2l = at(h2, l * T * d);
         if (moe) {
             // x_{l+1} = x1 + moe(h2); d total_loss / d aux_l = 1 (times the loss scale)
-            moe_[l]->backward(dx.get(), 1.0f, dh.get(), G(ly.wr), G(ly.wex), s, gscale);
+            const SqSlots msq[3] = {slots(l * RPL + 1), slots(l * RPL + 2), slots(l * RPL + 3)};
+            moe_[l]->backward(dx.get(), 1.0f, dh.get(), G(ly.wr), G(ly.wex), s, gscale, fold ? msq : nullptr);
         } else {
             void* gul = at(gu, l * T * 2 * f);
             void* aml = at(am, l * T * f);
@@ -1063,7 +1069,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         } else if (moe) {
             // dWqkv = dqkv^T h1 and dWo = dxm^T o in one launch
             wgrad_grouped(prof_, {{dqkv.get(), h1l, G(ly.wqkv)}, {dxm.get(), ol, G(ly.wo)}},
-                          {{3 * d, d, T}, {d, d, T}}, dt, s);
+                          {{3 * d, d, T}, {d, d, T}}, dt, s, sq_region(l * RPL));
         } else {
             // the layer's four weight gradients in one launch: dWqkv = dqkv^T h1, dWo = dxm^T o,
             // dWgu = dgu^T h2 and dWd = dx^T am (at the 1B shape 192 + 64 + 352 + 176 tiles of
@@ -1071,7 +1077,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             wgrad_grouped(prof_,
                           {{dqkv.get(), h1l, G(ly.wqkv)}, {dxm.get(), ol, G(ly.wo)},
                            {dgu.get(), at(h2, l * T * d), G(ly.wgu)}, {dx.get(), at(am, l * T * f), G(ly.wd)}},
-                          {{3 * d, d, T}, {d, d, T}, {2 * f, d, T}, {d, f, T}}, dt, s, sq_region(l));
+                          {{3 * d, d, T}, {d, d, T}, {2 * f, d, T}, {d, f, T}}, dt, s, sq_region(l * RPL));
         }
         gemm(prof_, 0, 0, T, d, 3 * d, dqkv.get(), 3 * d, wbase(ly, ly.wqkv, 0, 2), d, dh.get(), d, dt, dt, s, nullptr,
              0, 0.0f, 1.0f, ql ? &lq : nullptr, wq(ly, 0));
@@ -1105,8 +1111,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         eg.push_back(G(normf_));
         en.resize(eg.size(), d);
         auto _p = prof_.scope(kGradNorm, 0.0, 4.0 * (V * d + (2 * L + 1) * d) + 12.0 * sq_slots_, s);
-        hip::sqnorm_partials(eg.data(), en.data(), static_cast<int>(eg.size()), sq_part_ + (L + 1) * kSqRegion,
-                             sq_nf_ + (L + 1) * kSqRegion, s);
+        const int64_t pass0 = (L * RPL + 1) * kSqRegion;
+        hip::sqnorm_partials(eg.data(), en.data(), static_cast<int>(eg.size()), sq_part_ + pass0, sq_nf_ + pass0, s);
         hip::sqnorm_reduce(sq_part_, sq_nf_, sq_slots_, sq_tmp_, sq_tmp_nf_, &dev_->sqnorm, &dev_->nonfinite, s);
         hip::optim_finalize(&dev_->sqnorm, &dev_->nonfinite, &dev_->ctl, s);
     } else {

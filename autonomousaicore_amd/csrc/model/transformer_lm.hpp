@@ -168,7 +168,7 @@ public:
     std::vector<KernelClassStats> profile_stats() { return prof_.collect(); }
 
     // Whether the training step forms the gradient norm from partial sums written by the
-    // gradients' producers (dense models with an untied LM head) instead of a separate pass
+    // gradients' producers (models with an untied LM head, dense or MoE) instead of a separate pass
     // over every gradient; on by default where the model allows it.  Returns whether it is used.
     bool set_fused_grad_norm(bool on) {
         sq_fold_on_ = on;
@@ -238,10 +238,13 @@ private:
     int64_t hist_read_ = 0;            // host: records already returned
     float* backup_ = nullptr;          // snapshot: params, m, v (3 arenas) then the device scalars
     int64_t kv_B_ = 0;
-    // Gradient-norm partials (fused gradient norm): a region of kSqRegion slots per layer's
-    // weight-gradient launch, one for the LM head's, then the embedding's and the norm weights'
+    // Gradient-norm partials (fused gradient norm): regions of kSqRegion slots for each layer's
+    // weight-gradient launches, one for the LM head's, then the embedding's and the norm weights'
     // sqnorm_k partials; fp64 sums and non-finite flags, zero where no producer writes.
     static constexpr int64_t kSqRegion = 4096;
+    // regions per layer: the grouped launch; with MoE FFNs also the experts' down and gate/up
+    // weight gradients and the router's
+    int64_t sq_regions_per_layer() const { return cfg_.num_experts > 0 ? 4 : 1; }
     bool sq_fold_ = false;    // the model allows it
     bool sq_fold_on_ = true;  // switched on
     double* sq_part_ = nullptr;  // sq_slots_ partials, then sq_slots_ flags (sq_nf_)

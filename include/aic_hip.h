@@ -631,8 +631,8 @@ int aic_lm_profile_stats(aic_lm* lm, aic_kernel_stat* out, int cap, int* n);
 /* Whether the training step forms the gradient norm (clip_grad_norm_ and the loss scaler's
  * non-finite test) from partial sums written by the gradients' producers -- the weight-gradient
  * GEMMs' epilogues, the split-K reductions, then the embedding and norm weights -- instead of a
- * separate pass over every gradient.  On by default where the model allows it (dense FFNs, an
- * untied LM head); enable = 0 selects the pass.  *used (may be null) = whether it is now used.
+ * separate pass over every gradient.  On by default where the model allows it (an untied LM
+ * head, dense or MoE FFNs; not QLoRA); enable = 0 selects the pass.  *used (may be null) = whether it is now used.
  * The norm is the same sum in another order (fp64 partials of fp32 squares).
  * Replaces: the norm pass of clip_grad_norm_ (src/optim/clip_grad.cpp:11-53). */
 int aic_lm_fused_grad_norm(aic_lm* lm, int enable, int* used);

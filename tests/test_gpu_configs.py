@@ -344,6 +344,29 @@ def test_moe_widths_step_matches_oracle(orc):
     model.close()
 
 
+def test_moe_widths_fused_grad_norm_equals_pass():
+    """The fused gradient norm with MoE FFNs (the experts' down and gate/up weight gradients from
+    expert-ragged GEMMs, the router's from a split-K GEMM, each writing its partial sums) against
+    the pass over every gradient, at configs[3]'s widths with 2 layers: the same loss and
+    gradients bit for bit, the norm within 1e-6."""
+    c = CMOE
+    S = c["S"]
+    ids, tgt = aic.batch(99, 1, S, c["vocab"], dist="zipf")
+    out = {}
+    for fused in (True, False):
+        model = build_moe(c, L=2)
+        assert model.fused_grad_norm(fused) == fused
+        model.set_params(normal_params(model.layout, 2024))
+        st = model.train_step(ids, tgt, 1, S)
+        out[fused] = (st, model.get_grads())
+        model.close()
+    (sf, gf), (sp, gp) = out[True], out[False]
+    print(f"  grad norm fused {sf.grad_norm!r} pass {sp.grad_norm!r}")
+    assert sf.loss == sp.loss and not sf.found_inf and not sp.found_inf
+    np.testing.assert_array_equal(gf, gp)
+    assert abs(sf.grad_norm - sp.grad_norm) <= 1e-6 * sp.grad_norm
+
+
 def test_moe_full_config(orc):
     """configs[3] at full size: 12 layers, B 8 x S 1024, every FFN 8 experts top-2."""
     c = CMOE
