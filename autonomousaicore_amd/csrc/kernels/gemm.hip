@@ -587,6 +587,37 @@ bool gemm_ragged_eligible(const RaggedArgs& r) {
 void gemm_ragged(const RaggedArgs& r, hipStream_t s) {
     AIC_CHECK(gemm_ragged_eligible(r), InvalidArgument, "gemm_ragged: unsupported shape, layout or dtype");
     const GemmArgs& a = r.g;
+    bool force256 = false;
+    if (a.glu_f > 0 || a.dglu_gu) {
+        // SwiGLU (forward or backward) of an expert-ragged product: in the epilogue on bf16 outputs
+        // whose columns are whole 256-wide tiles (the forward on 256x256 tiles, whose columns pair
+        // 128 gate with 128 up columns); otherwise the product, then the pass over all rows
+        AIC_CHECK(!r.ragged_k && a.beta == 0.0f && !a.R && !(a.glu_f > 0 && a.dglu_gu), InvalidArgument,
+                  "gemm_ragged: SwiGLU epilogue arguments");
+        const bool cols = a.c == DType::BFloat16 && a.N % 256 == 0 && a.ldc % 8 == 0 && aligned16(a.C);
+        const bool glu = a.glu_f > 0 && cols && a.transB && !a.transA && gemm_impl::kDmaWaves256 == 8 &&
+                         a.N == 2 * a.glu_f && a.glu_f % 128 == 0 && a.ld_glu >= a.glu_f && a.ld_glu % 8 == 0 &&
+                         aligned16(a.glu_out);
+        const bool dglu = a.dglu_gu && cols && a.dglu_ld >= 2 * a.N && a.dglu_ld % 8 == 0 && aligned16(a.dglu_gu) &&
+                          aligned16(a.dglu_out);
+        if (!glu && !dglu) {
+            RaggedArgs b = r;
+            b.g.glu_f = 0;
+            b.g.glu_out = nullptr;
+            b.g.dglu_gu = nullptr;
+            b.g.dglu_out = nullptr;
+            gemm_ragged(b, s);
+            const int64_t es = static_cast<int64_t>(dtype_size(a.c));
+            if (a.glu_f > 0)
+                swiglu_fwd(a.C, static_cast<const char*>(a.C) + es * a.glu_f, a.ldc, a.glu_out, a.ld_glu, a.M, a.glu_f,
+                           a.c, s);
+            else
+                swiglu_bwd(a.dglu_gu, static_cast<const char*>(a.dglu_gu) + es * a.N, a.dglu_ld, a.C, a.ldc,
+                           a.dglu_out, static_cast<char*>(a.dglu_out) + es * a.N, a.dglu_ld, a.M, a.N, a.c, s);
+            return;
+        }
+        force256 = glu;
+    }
     // Tile shape: the grid's tiles (a bound for ragged M) in rounds of 256 CUs; the 256x256
     // tile unless its last round leaves so many CUs idle that 128x128 tiles (taken as 0.8 of
     // its rate) fill the rounds better.
@@ -595,7 +626,7 @@ void gemm_ragged(const RaggedArgs& r, hipStream_t s) {
         return r.ragged_k ? r.E * ((a.M + t - 1) / t) * tn : ((a.M + t - 1) / t + r.E) * tn;
     };
     auto fill = [](int64_t n) { return static_cast<double>(n) / (256.0 * static_cast<double>((n + 255) / 256)); };
-    const bool big = tiles(256) >= 128 && fill(tiles(256)) >= 0.8 * fill(tiles(128));
+    const bool big = force256 || (tiles(256) >= 128 && fill(tiles(256)) >= 0.8 * fill(tiles(128)));
     if (a.c == DType::Float32) {
         if (big) dispatch_ragged<256, 256, 64, 2, float>(r, s);
         else dispatch_ragged<128, 128, 64, 4, float>(r, s);

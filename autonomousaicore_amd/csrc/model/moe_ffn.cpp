@@ -140,9 +140,20 @@ void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int
             a.C = static_cast<char*>(g.C) + ec * o * g.ldc;
         }
         a.sq_part = nullptr;
+        a.glu_f = 0;
+        a.glu_out = nullptr;
+        a.dglu_gu = nullptr;
+        a.dglu_out = nullptr;
         v.push_back(a);
     }
     run_grouped(std::move(v), s, sq);
+    // SwiGLU of the products (the ragged launch does it in the epilogue)
+    if (g.glu_f > 0)
+        hip::swiglu_fwd(g.C, static_cast<const char*>(g.C) + es * g.glu_f, g.ldc, g.glu_out, g.ld_glu, g.M, g.glu_f,
+                        g.c, s);
+    if (g.dglu_gu)
+        hip::swiglu_bwd(g.dglu_gu, static_cast<const char*>(g.dglu_gu) + es * g.N, g.dglu_ld, g.C, g.ldc, g.dglu_out,
+                        static_cast<char*>(g.dglu_out) + es * g.N, g.dglu_ld, g.M, g.N, g.c, s);
 }
 
 void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* experts_w, const void* R, void* y,
@@ -185,8 +196,11 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
     hip::moe_gather(h, d_, src_ent_.as<int>(), k_, used_, d_, xp_.get(), dt_, s);
     const char* exb = static_cast<const char*>(experts_w);
     // gate/up of each expert's rows, SwiGLU, then the down projections
-    experts(args(0, 1, used_, f2, d_, xp_.get(), d_, exb, d_, gu_.get(), f2, dt_, dt_), 0, ex, 0, s);
-    hip::swiglu_fwd(gu_.get(), static_cast<char*>(gu_.get()) + es * f_, f2, a_.get(), f_, used_, f_, dt_, s);
+    hip::GemmArgs gu = args(0, 1, used_, f2, d_, xp_.get(), d_, exb, d_, gu_.get(), f2, dt_, dt_);
+    gu.glu_f = f_;  // a = silu(gate) * up, in the product's epilogue where the shapes allow
+    gu.glu_out = a_.get();
+    gu.ld_glu = f_;
+    experts(gu, 0, ex, 0, s);
     experts(args(0, 1, used_, d_, f_, a_.get(), f_, exb + es * 2 * f_ * d_, f_, ye_.get(), d_, dt_, dt_), 0, ex, 0, s);
     hip::moe_combine(ye_.get(), idx_.as<int64_t>(), dst_row_.as<int>(), gsel_.as<float>(), T, k_, d_, R, d_, y, d_, dt_,
                      s);
@@ -204,11 +218,15 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
                          dgsel.as<float>(), dt_, s);
     const char* exb = static_cast<const char*>(ex_);
     // down projections: da = dye . Wd and dWd = dye^T . a (fp32, zero for an expert with no rows)
-    experts(args(0, 0, used, f_, d_, dye.get(), d_, exb + es * 2 * f_ * d_, f_, da.get(), f_, dt_, dt_), 0, ex, 0, s);
+    // ... and da feeds SwiGLU's backward (dgu from da and the saved gate/up) in the product's
+    // epilogue where the shapes allow
+    hip::GemmArgs dn = args(0, 0, used, f_, d_, dye.get(), d_, exb + es * 2 * f_ * d_, f_, da.get(), f_, dt_, dt_);
+    dn.dglu_gu = gu_.get();
+    dn.dglu_out = dgu.get();
+    dn.dglu_ld = f2;
+    experts(dn, 0, ex, 0, s);
     experts(args(1, 0, d_, f_, 0, dye.get(), d_, a_.get(), f_, dexperts + 2 * f_ * d_, f_, dt_, DType::Float32), 1, 0,
             ex, s, sq_d);
-    hip::swiglu_bwd(gu_.get(), static_cast<char*>(gu_.get()) + es * f_, f2, da.get(), f_, dgu.get(),
-                    static_cast<char*>(dgu.get()) + es * f_, f2, used, f_, dt_, s);
     // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
     experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s);
     experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s, sq_gu);

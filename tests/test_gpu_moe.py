@@ -180,6 +180,42 @@ def test_moe_ffn_bf16_close_to_fp32_oracle(orc):
         assert rel(got, r) < 6e-2, name
 
 
+def test_moe_ffn_bf16_fused_swiglu_rows(orc):
+    """bf16 at widths whose expert products take SwiGLU in their epilogues (2f and f whole
+    256-column tiles, f % 128 == 0: the gate/up product writes silu(gate) * up, the down
+    projection's input gradient feeds SwiGLU's backward), with ragged expert row counts, so experts
+    end in partial row tiles: every token's output and input-gradient row against the fp32 oracle
+    (per-row relative error, so one wrong row at an expert boundary cannot hide in a global norm),
+    the weight gradients within the bf16 tolerance, and two runs bit-identical."""
+    rng = np.random.default_rng(4242)
+    T, d, f, E, k = 1000, 256, 768, 8, 2
+    h, wr, wg, wu, wd, dy = _weights(rng, T, d, f, E, scale=0.05)
+    h, wr, wg, wu, wd, dy = (bf16_round(a) for a in (h, wr, wg, wu, wd, dy))
+    out1 = _ffn_run(h, wr, wg, wu, wd, k, 0.01, dy, 1.0, BF16)
+    out2 = _ffn_run(h, wr, wg, wu, wd, k, 0.01, dy, 1.0, BF16)
+    for a, b in zip(out1[:6], out2[:6]):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(out1[6], out2[6]):
+        np.testing.assert_array_equal(a, b)
+    y, aux, idx, counts, dh, dwr, (dwg, dwu, dwd) = out1
+    assert np.any(counts % 256 != 0)
+    y_ref, aux_ref, idx_ref, _ = orc.moe_ffn_fwd(h, wr, wg, wu, wd, k, 0.01)
+    same = np.all(np.sort(idx, 1) == np.sort(idx_ref, 1), axis=1)
+    assert np.mean(same) > 0.97
+
+    def row_err(got, r):
+        return np.linalg.norm(got - r, axis=1) / np.maximum(np.linalg.norm(r, axis=1), 1e-6)
+
+    ey = row_err(y[same], y_ref[same])
+    ref = orc.moe_ffn_bwd(h, wr, wg, wu, wd, k, 0.01, dy, 1.0)
+    edh = row_err(dh[same], ref[0][same])
+    print(f"  rows: y max {ey.max():.3g} mean {ey.mean():.3g}; dh max {edh.max():.3g} mean {edh.mean():.3g}")
+    assert ey.max() < 6e-2 and ey.mean() < 2e-2
+    assert edh.max() < 1e-1 and edh.mean() < 3e-2
+    for name, got, r in zip(["dwr", "dwg", "dwu", "dwd"], [dwr, dwg, dwu, dwd], ref[1:]):
+        assert rel(got, r) < 6e-2, name
+
+
 @pytest.mark.parametrize("T", [384, 4096])
 def test_moe_ffn_bf16_idle_expert_and_determinism(orc, T):
     """bf16: the expert products read the row offsets on the device (128- and 256-row tiles at
