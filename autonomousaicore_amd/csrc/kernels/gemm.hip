@@ -347,9 +347,11 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         AIC_CHECK(a.rope_sin && a.rope_hd > 0 && a.rope_hd % 2 == 0 && a.rope_cols % a.rope_hd == 0 &&
                       a.rope_cols <= a.N && a.rope_seq > 0 && a.M % a.rope_seq == 0 && a.beta == 0.0f && !a.R,
                   InvalidArgument, "GEMM rotary epilogue: bad rope arguments");
-        // in the epilogue: bf16 output on full 256x256 tiles of the eight-wave plain path, heads
-        // of 128 that the 64-column wave sub-tiles split in halves
-        const bool fused = !a.Bq && a.c == DType::BFloat16 && a.rope_hd == 128 && gemm_impl::kDmaWaves256 == 8 &&
+        // in the epilogue: bf16 output on full 256x256 tiles of the eight-wave plain path, heads of
+        // 128 (split in halves by the 64-column wave sub-tiles, exchanged through LDS) or 64 (one
+        // per wave sub-tile, rotated in registers)
+        const bool fused = !a.Bq && a.c == DType::BFloat16 && (a.rope_hd == 128 || a.rope_hd == 64) &&
+                           gemm_impl::kDmaWaves256 == 8 &&
                            gemm_dma_eligible(a) && a.M % 256 == 0 && a.N % 256 == 0 && a.rope_cols % 256 == 0 &&
                            a.ldc % 8 == 0 && aligned16(a.C) && ((a.M / 256) * (a.N / 256) >= 128) && a.r2 == 0;
         if (!fused) {
