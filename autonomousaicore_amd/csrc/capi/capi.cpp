@@ -783,6 +783,48 @@ int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float
     });
 }
 
+int aic_hip_int4_gemm_rope(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const uint8_t* Wq,
+                           const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2, int64_t ldy2,
+                           int64_t r2, int64_t seg_n, void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq,
+                           int64_t start_pos, const float* cos_t, const float* sin_t, aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(cos_t && sin_t, InvalidArgument, "int4_gemm_rope: cos_t and sin_t are required");
+        AIC_CHECK(r2 >= 0 && (r2 == 0 || (X2 && Y2)), InvalidArgument, "int4_gemm_rope: bad low-rank term");
+        aic::hip::GemmArgs a;
+        a.transA = 0;
+        a.transB = 1;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.A = X;
+        a.lda = ldx;
+        a.ldb = K;
+        a.Bq = Wq;
+        a.Bscale = scales;
+        a.scale_t = aic::DType::Float16;
+        a.group = group;
+        a.C = C;
+        a.ldc = ldc;
+        a.ab = aic::DType::BFloat16;
+        a.c = aic::DType::BFloat16;
+        if (r2 > 0) {
+            a.X2 = X2;
+            a.ldx2 = ldx2;
+            a.Y2 = Y2;
+            a.ldy2 = ldy2;
+            a.r2 = r2;
+            a.seg_n = seg_n;
+        }
+        a.rope_cos = cos_t;
+        a.rope_sin = sin_t;
+        a.rope_cols = rope_cols;
+        a.rope_hd = hd;
+        a.rope_seq = seq;
+        a.rope_start = start_pos;
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_lora_merge(void* W, const void* A, const void* B, int64_t in_features, int64_t out_features, int64_t rank,
                        float scaling, int sign, aic_dtype dtype, aic_stream stream) {
     return guard([&] {

@@ -347,13 +347,16 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         AIC_CHECK(a.rope_sin && a.rope_hd > 0 && a.rope_hd % 2 == 0 && a.rope_cols % a.rope_hd == 0 &&
                       a.rope_cols <= a.N && a.rope_seq > 0 && a.M % a.rope_seq == 0 && a.beta == 0.0f && !a.R,
                   InvalidArgument, "GEMM rotary epilogue: bad rope arguments");
-        // in the epilogue: bf16 output on full 256x256 tiles of the eight-wave plain path, heads of
+        // in the epilogue: bf16 output on full 256x256 tiles, for the eight-wave plain path heads of
         // 128 (split in halves by the 64-column wave sub-tiles, exchanged through LDS) or 64 (one
-        // per wave sub-tile, rotated in registers)
-        const bool fused = !a.Bq && a.c == DType::BFloat16 && (a.rope_hd == 128 || a.rope_hd == 64) &&
-                           gemm_impl::kDmaWaves256 == 8 &&
-                           gemm_dma_eligible(a) && a.M % 256 == 0 && a.N % 256 == 0 && a.rope_cols % 256 == 0 &&
-                           a.ldc % 8 == 0 && aligned16(a.C) && ((a.M / 256) * (a.N / 256) >= 128) && a.r2 == 0;
+        // per wave sub-tile), for the four-wave INT4 path heads of 128 (one per wave sub-tile,
+        // after the kernel's low-rank term)
+        const bool tiles = a.c == DType::BFloat16 && a.M % 256 == 0 && a.N % 256 == 0 && a.rope_cols % 256 == 0 &&
+                           a.ldc % 8 == 0 && aligned16(a.C) && ((a.M / 256) * (a.N / 256) >= 128);
+        const bool fused = tiles && (a.Bq ? a.rope_hd == 128 && a.transB && gemm_q4_eligible(a) &&
+                                                (a.r2 == 0 || rank_tail_ok(a, 256))
+                                          : (a.rope_hd == 128 || a.rope_hd == 64) && gemm_impl::kDmaWaves256 == 8 &&
+                                                gemm_dma_eligible(a) && a.r2 == 0);
         if (!fused) {
             GemmArgs b = a;
             b.rope_cos = b.rope_sin = nullptr;

@@ -406,6 +406,22 @@ int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float
                               const uint8_t* Wq, const void* scales, aic_dtype scale_type, int64_t group, float beta,
                               void* C, int64_t ldc, const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type,
                               aic_stream stream);
+/* The QLoRA attention input projection with the rotary embedding applied on the way out:
+ *   C = X . deq(Wq)^T + X2 . Y2^T
+ * (bf16 X [M, K], INT4 Wq holding W [N, K] with fp16 scales per `group` elements, bf16 C [M, N])
+ * whose columns [0, rope_cols) are heads of hd values rotated as in aic_hip_gemm_rope.  The
+ * low-rank term is optional (r2 0): X2 [M, *] (ldx2) and Y2 [N, r2] (ldy2) bf16, with seg_n > 0
+ * giving output columns [s seg_n, (s+1) seg_n) the X2 columns [s r2, (s+1) r2) (the q, k and v
+ * adapters side by side).  The rotation follows the whole sum.  In the INT4 GEMM's epilogue for
+ * hd 128 on shapes of at least 128 full 256 x 256 tiles (r2 % 8 == 0, seg_n % 256 == 0);
+ * otherwise the product and then aic_hip_rope.
+ * Replaces: the q, k, v LoRALinear::forward over QuantizedLinear::forward (src/nn/lora.cpp:75-93,
+ * src/nn/quantization.cpp:669-679) followed by RotaryPositionEmbedding::forward on q and k
+ * (include/nn/rope.hpp:23-112). */
+int aic_hip_int4_gemm_rope(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const uint8_t* Wq,
+                           const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2, int64_t ldy2,
+                           int64_t r2, int64_t seg_n, void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq,
+                           int64_t start_pos, const float* cos_t, const float* sin_t, aic_stream stream);
 /* W[out,in] += sign * scaling * B[out,rank] . A[rank,in]  (sign >= 0: merge, < 0: unmerge);
  * W, A, B of `dtype` (AIC_F32 or AIC_BF16).
  * Replaces: LoRALinear::merge / unmerge (src/nn/lora.cpp:95-108). */

@@ -113,3 +113,57 @@ def test_int4_gemm_other_shapes_fall_back_to_staging(orc):
     y = _fused(0, M, N, K, 1.0, xd, pd, sd, True, G, 0.0, None, None, F32)
     ref = x.astype(np.float64) @ bf16_round(W).astype(np.float64)
     assert rel(y, ref) < 1e-5
+
+
+# (T, d, K, r, seq, start): the q/k/v projection of 128-wide heads with the rank-r adapters of q, k
+# and v side by side; 192 tiles of 256x256 take the INT4 kernel's rotary epilogue (with and
+# without the adapters, and at a decode-style start position), 24 tiles the product and then
+# the rope pass
+@pytest.mark.parametrize("T,d,K,r,seq,start", [(4096, 1024, 512, 16, 2048, 0), (4096, 1024, 256, 0, 1024, 0),
+                                               (4096, 1024, 256, 16, 4096, 3), (1024, 512, 256, 16, 512, 0)])
+def test_int4_gemm_rope_equals_product_then_rope(orc, T, d, K, r, seq, start):
+    """aic_hip_int4_gemm_rope = the low-rank GEMM over the dequantized weight, then aic_hip_rope on
+    the q and k columns: v columns bit-identical (the same products), q / k within one bf16
+    rounding of the rotation of the same bf16 sum, and the oracle's RoPE of the float64 sum
+    within the bf16 bound."""
+    print(f"int4 gemm rope: T {T} d {d} K {K} r {r} seq {seq} start {start}", flush=True)
+    rng = np.random.default_rng(T + d + K + r + start)
+    hd, N, G = 128, 3 * d, 128
+    packed, scales = _qweight(orc, rng, N, K, G, True)
+    W = bf16_round(orc.int4_dequantize(packed, scales, N * K, G).reshape(N, K))
+    x = bf16_round(rng.standard_normal((T, K)).astype(np.float32))
+    X2 = bf16_round(rng.standard_normal((T, 3 * max(r, 1))).astype(np.float32))
+    Y2 = bf16_round((rng.standard_normal((N, max(r, 1))) / 4).astype(np.float32))
+    cos_t = np.empty((start + seq, hd // 2), np.float32)
+    sin_t = np.empty_like(cos_t)
+    _lib.check(_lib.load().aic_hip_rope_tables(cos_t.ctypes.data, sin_t.ctypes.data, start + seq, hd, 10000.0))
+    xd, pd, sd, Wd = dev(x, torch.bfloat16), dev(packed), dev(scales), dev(W, torch.bfloat16)
+    X2d, Y2d, cd, snd = dev(X2, torch.bfloat16), dev(Y2, torch.bfloat16), dev(cos_t), dev(sin_t)
+    ldx2 = X2.shape[1]
+    fused = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+    call("aic_hip_int4_gemm_rope", T, N, K, ptr(xd), K, ptr(pd), ptr(sd), G, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1], r,
+         d, ptr(fused), N, 2 * d, hd, seq, start, ptr(cd), ptr(snd), stream())
+    sep = torch.empty_like(fused)
+    if r > 0:
+        call("aic_hip_gemm_lowrank", 0, 1, T, N, K, 1.0, ptr(xd), K, ptr(Wd), K, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1],
+             r, d, 0, 0.0, ptr(sep), N, None, 0, BF16, BF16, stream())
+    else:
+        call("aic_hip_gemm", 0, 1, T, N, K, 1.0, ptr(xd), K, ptr(Wd), K, 0.0, ptr(sep), N, None, 0, BF16, BF16,
+             stream())
+    call("aic_hip_rope", ptr(sep), N, T // seq, seq, 2 * d // hd, hd, start, ptr(cd), ptr(snd), 0, BF16, stream())
+    f, g = host(fused), host(sep)
+    np.testing.assert_array_equal(f[:, 2 * d:], g[:, 2 * d:])
+    assert np.max(np.abs(f[:, :2 * d] - g[:, :2 * d]) / (np.abs(g[:, :2 * d]) + 1e-3)) < 1e-2
+    assert rel(f[:, :2 * d], g[:, :2 * d]) < 2e-3
+    ref = x.astype(np.float64) @ W.astype(np.float64).T
+    if r > 0:
+        for s in range(3):
+            ref[:, s * d:(s + 1) * d] += X2[:, s * r:(s + 1) * r].astype(np.float64) @ \
+                Y2[s * d:(s + 1) * d].astype(np.float64).T
+    qk = orc.rope_fwd(ref[:, :2 * d], T // seq, seq, 2 * d // hd, hd, start_pos=start)
+    assert rel(f[:, :2 * d], qk) < 8e-3
+    assert rel(f[:, 2 * d:], ref[:, 2 * d:]) < 8e-3
+    again = torch.empty_like(fused)
+    call("aic_hip_int4_gemm_rope", T, N, K, ptr(xd), K, ptr(pd), ptr(sd), G, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1], r,
+         d, ptr(again), N, 2 * d, hd, seq, start, ptr(cd), ptr(snd), stream())
+    np.testing.assert_array_equal(host(again), f)
