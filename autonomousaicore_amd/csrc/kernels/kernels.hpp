@@ -69,8 +69,11 @@ void moe_combine(const void* ye, const int64_t* idx, const int* dst_row, const f
                  int64_t d, const void* R, int64_t ldr, void* out, int64_t ldo, DType dt, hipStream_t s);
 void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* src_ent, const float* gsel, int64_t rows,
                      int64_t k, int64_t d, void* dye, float* dgsel, DType dt, hipStream_t s);
+// With router_dlogits (fp32 [T, E]) and router_w ([E, d], dtype dt) the router's input gradient
+// dlogits[t] . W_r is added to each token's sum in fp32 before the one rounding to dt.
 void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_t T, int64_t k, int64_t d, void* dx,
-                 int64_t ldx, bool accumulate, DType dt, hipStream_t s);
+                 int64_t ldx, bool accumulate, DType dt, hipStream_t s, const float* router_dlogits = nullptr,
+                 const void* router_w = nullptr, int64_t E = 0);
 // daux_scale (device, nullable) multiplies daux: the loss scale of an AMP step.
 void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, const int64_t* counts, int64_t T,
                     int64_t E, int64_t k, float aux_coef, float daux, const float* daux_scale, float* dlogits,

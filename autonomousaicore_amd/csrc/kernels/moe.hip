@@ -357,7 +357,8 @@ __global__ __launch_bounds__(256) void moe_combine_bwd_k(const T* __restrict__ d
 template <typename T, int VN>
 __global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, const int64_t* __restrict__ idx,
                                                      const int* __restrict__ dst_row, int k, int d, T* __restrict__ dx,
-                                                     int64_t ldx, int accumulate) {
+                                                     int64_t ldx, int accumulate, const float* __restrict__ dlog,
+                                                     const T* __restrict__ wr, int E) {
     const int t = blockIdx.x;
     int ord[kMaxK], row[kMaxK];
     slot_order(idx + static_cast<int64_t>(t) * k, k, ord);
@@ -370,6 +371,15 @@ __global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, 
             ldv<VN>(dxp + static_cast<int64_t>(row[q]) * d + c, v);
 #pragma unroll
             for (int i = 0; i < VN; ++i) sm[i] += v[i];
+        }
+        if (dlog) {
+            // the router's input gradient dlogits[t] . W_r, experts in order
+            for (int e = 0; e < E; ++e) {
+                const float g = dlog[static_cast<int64_t>(t) * E + e];
+                ldv<VN>(wr + static_cast<int64_t>(e) * d + c, v);
+#pragma unroll
+                for (int i = 0; i < VN; ++i) sm[i] = fmaf(g, v[i], sm[i]);
+            }
         }
         T* o = dx + static_cast<int64_t>(t) * ldx + c;
         if (accumulate) {
@@ -540,14 +550,17 @@ void moe_combine_bwd(const void* dout, int64_t ldo, const void* ye, const int* s
 }
 
 void moe_scatter(const void* dxp, const int64_t* idx, const int* dst_row, int64_t T, int64_t k, int64_t d, void* dx,
-                 int64_t ldx, bool accumulate, DType dt, hipStream_t s) {
+                 int64_t ldx, bool accumulate, DType dt, hipStream_t s, const float* router_dlogits,
+                 const void* router_w, int64_t E) {
     AIC_CHECK(T >= 0 && k >= 1 && k <= kMaxK && d > 0 && ldx >= d, InvalidArgument, "moe_scatter: bad shape");
+    AIC_CHECK(!router_dlogits || (router_w && E >= 1 && E <= kMaxE), InvalidArgument, "moe_scatter: bad router term");
     if (T == 0) return;
-    const bool v = d % 8 == 0 && ldx % 8 == 0 && aligned16(dxp) && aligned16(dx);
+    const bool v = d % 8 == 0 && ldx % 8 == 0 && aligned16(dxp) && aligned16(dx) && (!router_w || aligned16(router_w));
     const dim3 g(static_cast<unsigned>(T)), b(v ? 128 : 256);
 #define AIC_SCATTER(TT, VN)                                                                                        \
     hipLaunchKernelGGL((moe_scatter_k<TT, VN>), g, b, 0, s, static_cast<const TT*>(dxp), idx, dst_row,             \
-                       static_cast<int>(k), static_cast<int>(d), static_cast<TT*>(dx), ldx, accumulate ? 1 : 0)
+                       static_cast<int>(k), static_cast<int>(d), static_cast<TT*>(dx), ldx, accumulate ? 1 : 0,    \
+                       router_dlogits, static_cast<const TT*>(router_w), static_cast<int>(E))
     if (dt == DType::BFloat16) {
         if (v) AIC_SCATTER(bf16, 8);
         else AIC_SCATTER(bf16, 1);

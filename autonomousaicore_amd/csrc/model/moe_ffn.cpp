@@ -230,18 +230,20 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
     // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
     experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s);
     experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s, sq_gu);
-    hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
-    // router: dlogits from the gates and the aux loss, then both router products
+    // router: dlogits from the gates and the aux loss, then both router products (for bf16 the
+    // input gradient dlogits . W_r joins the experts' sum in the scatter, in fp32)
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,
                         coef_, daux, daux_scale, dlog.as<float>(), s);
     if (dt_ == DType::Float32) {
+        hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s);
         gemm(1, 0, E_, d_, T, dlog.get(), E_, h_, d_, dwr, d_, DType::Float32, DType::Float32, s, 0.0f, sq_r);
         gemm(0, 0, T, d_, E_, dlog.get(), E_, wr_, d_, dh, d_, DType::Float32, DType::Float32, s, 1.0f);
     } else {
+        hip::moe_scatter(dxp.get(), idx_.as<int64_t>(), dst_row_.as<int>(), T, k_, d_, dh, d_, false, dt_, s,
+                         dlog.as<float>(), wr_, E_);
         DeviceBuffer dlb(2 * T * E_, s);
         hip::cast_f32_bf16(dlog.as<float>(), dlb.get(), T * E_, s);
         gemm(1, 0, E_, d_, T, dlb.get(), E_, h_, d_, dwr, d_, DType::BFloat16, DType::Float32, s, 0.0f, sq_r);
-        gemm(0, 0, T, d_, E_, dlb.get(), E_, wr_, d_, dh, d_, DType::BFloat16, DType::BFloat16, s, 1.0f);
     }
 }
 
