@@ -65,7 +65,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__
     for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
         const int m = static_cast<int>(i / N), n = static_cast<int>(i % N);
         float acc = P[i];
-        for (int z = 1; z < splits; ++z) acc += P[z * pz + i];
+        int z = 1;
+        // eight loads in flight, added in z order
+        for (; z + 8 <= splits; z += 8) {
+            float p[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) p[u] = P[(z + u) * pz + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += p[u];
+        }
+        for (; z < splits; ++z) acc += P[z * pz + i];
         const int64_t ci = static_cast<int64_t>(m) * ldc + n;
         float v = alpha * acc;
         if (beta != 0.0f) v += beta * ld(C, ci);
