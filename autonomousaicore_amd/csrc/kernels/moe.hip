@@ -30,50 +30,75 @@ constexpr int kMaxE = 64;  // experts per layer handled by the per-token kernels
 constexpr int kMaxK = 8;   // experts per token
 
 // One thread per token: softmax over E, top-k selection, normalised gates of the selected.
+// EM >= E bounds the per-token arrays at compile time (every loop unrolled to EM with an e < E
+// guard and no runtime array index), so they stay in registers.
+template <int EM>
 __global__ __launch_bounds__(256) void moe_route_k(const float* __restrict__ logits, int T, int E, int k,
                                                    int64_t* __restrict__ idx, float* __restrict__ gsel,
                                                    float* __restrict__ probs, float* __restrict__ rweights) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
     const float* row = logits + static_cast<int64_t>(t) * E;
-    float x[kMaxE];
+    float x[EM];
     float m = row[0];
-    for (int e = 0; e < E; ++e) {
-        x[e] = row[e];
-        m = fmaxf(m, x[e]);
-    }
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) {
+            x[e] = row[e];
+            m = fmaxf(m, x[e]);
+        }
     double s = 0.0;
-    float p[kMaxE];
-    for (int e = 0; e < E; ++e) {
-        p[e] = expf(x[e] - m);
-        s += static_cast<double>(p[e]);
-    }
+    float p[EM];
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) {
+            p[e] = expf(x[e] - m);
+            s += static_cast<double>(p[e]);
+        }
     const float sf = static_cast<float>(s);
-    for (int e = 0; e < E; ++e) {
-        p[e] = p[e] / sf;
-        probs[static_cast<int64_t>(t) * E + e] = p[e];
-    }
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) {
+            p[e] = p[e] / sf;
+            probs[static_cast<int64_t>(t) * E + e] = p[e];
+        }
     // selection: repeatedly the largest remaining logit, the lowest index among equals
     uint64_t used = 0;
-    int sel[kMaxK];
-    for (int j = 0; j < k; ++j) {
+    float selx[kMaxK], selp[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j >= k) break;
         int best = -1;
-        for (int e = 0; e < E; ++e)
-            if (!((used >> e) & 1) && (best < 0 || x[e] > x[best])) best = e;
+        float bx = 0.0f, bp = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EM; ++e)
+            if (e < E && !((used >> e) & 1) && (best < 0 || x[e] > bx)) {
+                best = e;
+                bx = x[e];
+                bp = p[e];
+            }
         used |= 1ull << best;
-        sel[j] = best;
+        selx[j] = bx;
+        selp[j] = bp;
         idx[static_cast<int64_t>(t) * k + j] = best;
     }
     double den = 0.0;
-    for (int e = 0; e < E; ++e)
-        if ((used >> e) & 1) den += static_cast<double>(p[e]);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E && ((used >> e) & 1)) den += static_cast<double>(p[e]);
     const float denf = static_cast<float>(den) + 1e-9f;
-    for (int j = 0; j < k; ++j) gsel[static_cast<int64_t>(t) * k + j] = p[sel[j]] / denf;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+        if (j < k) gsel[static_cast<int64_t>(t) * k + j] = selp[j] / denf;
     if (rweights) {  // route()'s routing_weights: softmax over the selected logits (moe.cpp:67-77)
-        const float mx = x[sel[0]];
+        const float mx = selx[0];
         float se = 0.0f;
-        for (int j = 0; j < k; ++j) se += expf(x[sel[j]] - mx);
-        for (int j = 0; j < k; ++j) rweights[static_cast<int64_t>(t) * k + j] = expf(x[sel[j]] - mx) / (se + 1e-9f);
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+            if (j < k) se += expf(selx[j] - mx);
+#pragma unroll
+        for (int j = 0; j < kMaxK; ++j)
+            if (j < k) rweights[static_cast<int64_t>(t) * k + j] = expf(selx[j] - mx) / (se + 1e-9f);
     }
 }
 
@@ -392,7 +417,9 @@ __global__ __launch_bounds__(256) void moe_scatter_k(const T* __restrict__ dxp, 
 }
 
 // Router backward, one thread per token: gradient of the gates (normalisation and mask) and of
-// the aux loss through both softmaxes into dlogits [T, E] (overwritten).
+// the aux loss through both softmaxes into dlogits [T, E] (overwritten).  EM >= E as for
+// moe_route_k.
+template <int EM>
 __global__ __launch_bounds__(256) void moe_router_bwd_k(const float* __restrict__ probs, const int64_t* __restrict__ idx,
                                                         const float* __restrict__ dgsel,
                                                         const int64_t* __restrict__ counts, int T, int E, int k,
@@ -401,40 +428,60 @@ __global__ __launch_bounds__(256) void moe_router_bwd_k(const float* __restrict_
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
     if (daux_scale) daux *= *daux_scale;
-    const float* p = probs + static_cast<int64_t>(t) * E;
-    float dg[kMaxE];
+    const float* pp = probs + static_cast<int64_t>(t) * E;
+    float p[EM], dg[EM];
+#pragma unroll
+    for (int e = 0; e < EM; ++e) {
+        p[e] = e < E ? pp[e] : 0.0f;
+        dg[e] = 0.0f;
+    }
     uint64_t used = 0;
-    for (int e = 0; e < E; ++e) dg[e] = 0.0f;
-    for (int j = 0; j < k; ++j) {
-        const int e = static_cast<int>(idx[static_cast<int64_t>(t) * k + j]);
-        used |= 1ull << e;
-        dg[e] = dgsel[static_cast<int64_t>(t) * k + j];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+        if (j >= k) break;
+        const int sel = static_cast<int>(idx[static_cast<int64_t>(t) * k + j]);
+        const float g = dgsel[static_cast<int64_t>(t) * k + j];
+        used |= 1ull << sel;
+#pragma unroll
+        for (int e = 0; e < EM; ++e)
+            if (e == sel) dg[e] = g;
     }
     double den = 0.0;
-    for (int e = 0; e < E; ++e)
-        if ((used >> e) & 1) den += static_cast<double>(p[e]);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E && ((used >> e) & 1)) den += static_cast<double>(p[e]);
     const float denf = static_cast<float>(den) + 1e-9f;
     double sb = 0.0;
-    for (int e = 0; e < E; ++e)
-        if ((used >> e) & 1) sb += static_cast<double>(-dg[e] * p[e] / (denf * denf));
-    float dp[kMaxE];
-    for (int e = 0; e < E; ++e) dp[e] = ((used >> e) & 1) ? (dg[e] / denf + static_cast<float>(sb)) : 0.0f;
-    float dl[kMaxE];
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E && ((used >> e) & 1)) sb += static_cast<double>(-dg[e] * p[e] / (denf * denf));
+    float dp[EM];
+#pragma unroll
+    for (int e = 0; e < EM; ++e) dp[e] = ((used >> e) & 1) ? (dg[e] / denf + static_cast<float>(sb)) : 0.0f;
+    float dl[EM];
     double s = 0.0;
-    for (int e = 0; e < E; ++e) s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
     float sf = static_cast<float>(s);
-    for (int e = 0; e < E; ++e) dl[e] = p[e] * (dp[e] - sf);
+#pragma unroll
+    for (int e = 0; e < EM; ++e) dl[e] = p[e] * (dp[e] - sf);
     if (aux_coef > 0.0f && E > 1) {
         const float fscale = (static_cast<float>(E) * aux_coef) / (static_cast<float>(T) * static_cast<float>(k));
         s = 0.0;
-        for (int e = 0; e < E; ++e) {
-            dp[e] = (daux * (static_cast<float>(counts[e]) * fscale)) / static_cast<float>(T);
-            s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
-        }
+#pragma unroll
+        for (int e = 0; e < EM; ++e)
+            if (e < E) {
+                dp[e] = (daux * (static_cast<float>(counts[e]) * fscale)) / static_cast<float>(T);
+                s += static_cast<double>(dp[e]) * static_cast<double>(p[e]);
+            }
         sf = static_cast<float>(s);
-        for (int e = 0; e < E; ++e) dl[e] += p[e] * (dp[e] - sf);
+#pragma unroll
+        for (int e = 0; e < EM; ++e) dl[e] += p[e] * (dp[e] - sf);
     }
-    for (int e = 0; e < E; ++e) dlogits[static_cast<int64_t>(t) * E + e] = dl[e];
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) dlogits[static_cast<int64_t>(t) * E + e] = dl[e];
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -451,8 +498,14 @@ void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_c
                float* probs, float* rweights, int64_t* counts, float* mean_probs, float* aux, hipStream_t s) {
     check_moe(T, E, k);
     AIC_CHECK(logits && idx && gsel && probs && counts, InvalidArgument, "moe_route: null argument");
-    hipLaunchKernelGGL(moe_route_k, dim3(grid_for(T, 256)), dim3(256), 0, s, logits, static_cast<int>(T),
-                       static_cast<int>(E), static_cast<int>(k), idx, gsel, probs, rweights);
+#define AIC_ROUTE(EM)                                                                                       \
+    hipLaunchKernelGGL(moe_route_k<EM>, dim3(grid_for(T, 256)), dim3(256), 0, s, logits, static_cast<int>(T), \
+                       static_cast<int>(E), static_cast<int>(k), idx, gsel, probs, rweights)
+    if (E <= 8) AIC_ROUTE(8);
+    else if (E <= 16) AIC_ROUTE(16);
+    else if (E <= 32) AIC_ROUTE(32);
+    else AIC_ROUTE(kMaxE);
+#undef AIC_ROUTE
     AIC_LAUNCH_CHECK("moe_route");
     // statistics: 1024 tokens per block, then the partials in block order
     const int nparts = static_cast<int>((T + 1023) / 1024);
@@ -578,9 +631,15 @@ void moe_router_bwd(const float* probs, const int64_t* idx, const float* dgsel, 
                     int64_t E, int64_t k, float aux_coef, float daux, const float* daux_scale, float* dlogits,
                     hipStream_t s) {
     check_moe(T, E, k);
-    hipLaunchKernelGGL(moe_router_bwd_k, dim3(grid_for(T, 256)), dim3(256), 0, s, probs, idx, dgsel, counts,
-                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), aux_coef, daux, daux_scale,
-                       dlogits);
+#define AIC_ROUTER_BWD(EM)                                                                                 \
+    hipLaunchKernelGGL(moe_router_bwd_k<EM>, dim3(grid_for(T, 256)), dim3(256), 0, s, probs, idx, dgsel, counts, \
+                       static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), aux_coef, daux, daux_scale,  \
+                       dlogits)
+    if (E <= 8) AIC_ROUTER_BWD(8);
+    else if (E <= 16) AIC_ROUTER_BWD(16);
+    else if (E <= 32) AIC_ROUTER_BWD(32);
+    else AIC_ROUTER_BWD(kMaxE);
+#undef AIC_ROUTER_BWD
     AIC_LAUNCH_CHECK("moe_router_bwd");
 }
 
