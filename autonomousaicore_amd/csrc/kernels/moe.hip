@@ -102,16 +102,20 @@ __global__ __launch_bounds__(256) void moe_route_k(const float* __restrict__ log
     }
 }
 
-// Per-expert probability sums and counts of the tokens [blockIdx.x * 1024, + 1024): thread t
-// takes one token for 8 experts at a time, the 16 waves reduce with shuffles and their
-// partials are added in wave order; part_p / part_c [block][E] (fixed order: deterministic).
-__global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ idx, const float* __restrict__ probs,
-                                                    int T, int E, int k, double* __restrict__ part_p,
-                                                    long long* __restrict__ part_c) {
-    __shared__ double sp[16][kMaxE];
-    __shared__ long long sc[16][kMaxE];
+// Per-expert probability sums and counts of the tokens [blockIdx.x * kStatsTokens, + kStatsTokens):
+// thread t takes one token for 8 experts at a time, the block's waves reduce with shuffles and
+// their partials are added in wave order; part_p / part_c [block][E] (fixed order:
+// deterministic).  Blocks of 256 tokens spread the pass over T / 256 CUs.
+constexpr int kStatsTokens = 256;
+__global__ __launch_bounds__(kStatsTokens) void moe_stats_k(const int64_t* __restrict__ idx,
+                                                            const float* __restrict__ probs, int T, int E, int k,
+                                                            double* __restrict__ part_p,
+                                                            long long* __restrict__ part_c) {
+    constexpr int NW = kStatsTokens / 64;
+    __shared__ double sp[NW][kMaxE];
+    __shared__ long long sc[NW][kMaxE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t = static_cast<int>(blockIdx.x) * 1024 + static_cast<int>(threadIdx.x);
+    const int t = static_cast<int>(blockIdx.x) * kStatsTokens + static_cast<int>(threadIdx.x);
     for (int e0 = 0; e0 < E; e0 += 8) {
         double a[8];
         long long c[8];
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(1024) void moe_stats_k(const int64_t* __restrict__ 
     if (threadIdx.x < E) {
         double a = 0.0;
         long long c = 0;
-        for (int w = 0; w < 16; ++w) {
+        for (int w = 0; w < NW; ++w) {
             a += sp[w][threadIdx.x];
             c += sc[w][threadIdx.x];
         }
@@ -507,11 +511,11 @@ void moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_c
     else AIC_ROUTE(kMaxE);
 #undef AIC_ROUTE
     AIC_LAUNCH_CHECK("moe_route");
-    // statistics: 1024 tokens per block, then the partials in block order
-    const int nparts = static_cast<int>((T + 1023) / 1024);
+    // statistics: kStatsTokens tokens per block, then the partials in block order
+    const int nparts = static_cast<int>((T + kStatsTokens - 1) / kStatsTokens);
     double* part_p = static_cast<double*>(stream_scratch((sizeof(double) + sizeof(long long)) * nparts * E, s));
     long long* part_c = reinterpret_cast<long long*>(part_p + static_cast<int64_t>(nparts) * E);
-    hipLaunchKernelGGL(moe_stats_k, dim3(static_cast<unsigned>(nparts)), dim3(1024), 0, s, idx, probs,
+    hipLaunchKernelGGL(moe_stats_k, dim3(static_cast<unsigned>(nparts)), dim3(kStatsTokens), 0, s, idx, probs,
                        static_cast<int>(T), static_cast<int>(E), static_cast<int>(k), part_p, part_c);
     AIC_LAUNCH_CHECK("moe_stats");
     hipLaunchKernelGGL(moe_stats_final_k, dim3(1), dim3(64), 0, s, part_p, part_c, nparts, static_cast<int>(T),
