@@ -170,7 +170,23 @@ __global__ __launch_bounds__(64) void moe_stats_final_k(const double* __restrict
     if (threadIdx.x < E) {
         double a = 0.0;
         long long c = 0;
-        for (int b = 0; b < nparts; ++b) {
+        int b = 0;
+        // eight partials' loads in flight, added in block order
+        for (; b + 8 <= nparts; b += 8) {
+            double pa[8];
+            long long pc[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                pa[u] = part_p[static_cast<int64_t>(b + u) * E + threadIdx.x];
+                pc[u] = part_c[static_cast<int64_t>(b + u) * E + threadIdx.x];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                a += pa[u];
+                c += pc[u];
+            }
+        }
+        for (; b < nparts; ++b) {
             a += part_p[static_cast<int64_t>(b) * E + threadIdx.x];
             c += part_c[static_cast<int64_t>(b) * E + threadIdx.x];
         }
@@ -193,6 +209,8 @@ __global__ __launch_bounds__(64) void moe_stats_final_k(const double* __restrict
 constexpr int kRowAlign = 64;  // each expert's row block starts at a multiple of 64 rows
 __device__ __forceinline__ long long align_rows(long long n) { return (n + kRowAlign - 1) / kRowAlign * kRowAlign; }
 
+constexpr int kPermRounds = 16;  // rounds of 1024 entries per pass of moe_permute_k
+
 // One block per expert: stable positions of its (token, slot) entries in token order, in a
 // row block that starts at offsets[e] (a multiple of 64; the block is padded to 64 rows).
 // dst_row[t * k + j] = row of that entry; src_ent[row] = t * k + j, or -1 for a padding row.
@@ -202,8 +220,8 @@ __global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict_
                                                       int* __restrict__ src_ent) {
     const int e = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __shared__ int wsum[16];
-    __shared__ int base_s, start_s;
+    __shared__ int wsum[kPermRounds][16], wpre[kPermRounds][16];
+    __shared__ int base_s, start_s, total_s;
     if (threadIdx.x == 0) {
         long long off = 0;
         for (int i = 0; i < e; ++i) off += align_rows(counts[i]);
@@ -220,27 +238,58 @@ __global__ __launch_bounds__(1024) void moe_permute_k(const int64_t* __restrict_
     }
     __syncthreads();
     const int n = T * k;
-    // 1024 entries per round: a ballot gives each hit its rank within the wave, the 16 wave
-    // totals its wave's offset, so the order stays the entries' (token-major) order
-    for (int c0 = 0; c0 < n; c0 += 1024) {
-        const int i = c0 + static_cast<int>(threadIdx.x);
-        const bool hit = i < n && idx[i] == e;
-        const unsigned long long m = __ballot(hit);
-        if (lane == 0) wsum[wave] = __popcll(m);
-        __syncthreads();
-        int off = base_s;
-        for (int w = 0; w < wave; ++w) off += wsum[w];
-        if (hit) {
-            const int row = off + __popcll(m & ((1ull << lane) - 1ull));
-            dst_row[i] = row;
-            src_ent[row] = i;
+    // passes of kPermRounds rounds of 1024 entries: all the rounds' loads in flight, a ballot
+    // gives each hit its rank within its wave and round, and an exclusive scan of the
+    // (round, wave) hit counts -- in entry order -- its offset, so the order stays the
+    // entries' (token-major) order
+    for (int c0 = 0; c0 < n; c0 += 1024 * kPermRounds) {
+        bool hit[kPermRounds];
+        unsigned long long m[kPermRounds];
+#pragma unroll
+        for (int r = 0; r < kPermRounds; ++r) {
+            const int i = c0 + r * 1024 + static_cast<int>(threadIdx.x);
+            hit[r] = i < n && idx[i] == e;
+        }
+#pragma unroll
+        for (int r = 0; r < kPermRounds; ++r) {
+            m[r] = __ballot(hit[r]);
+            if (lane == 0) wsum[r][wave] = __popcll(m[r]);
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            int t = 0;
-            for (int w = 0; w < 16; ++w) t += wsum[w];
-            base_s += t;
+        if (wave == 0) {  // exclusive scan of the kPermRounds x 16 counts, four per lane
+            constexpr int PL = kPermRounds * 16 / 64;
+            const int* cnt = &wsum[0][0];
+            int v[PL], sum = 0;
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                v[q] = cnt[lane * PL + q];
+                sum += v[q];
+            }
+            int inc = sum;
+#pragma unroll
+            for (int w = 1; w < 64; w <<= 1) {
+                const int t = __shfl_up(inc, w);
+                if (lane >= w) inc += t;
+            }
+            int ex = inc - sum;
+#pragma unroll
+            for (int q = 0; q < PL; ++q) {
+                (&wpre[0][0])[lane * PL + q] = ex;
+                ex += v[q];
+            }
+            if (lane == 63) total_s = inc;
         }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kPermRounds; ++r)
+            if (hit[r]) {
+                const int i = c0 + r * 1024 + static_cast<int>(threadIdx.x);
+                const int row = base_s + wpre[r][wave] + __popcll(m[r] & ((1ull << lane) - 1ull));
+                dst_row[i] = row;
+                src_ent[row] = i;
+            }
+        __syncthreads();
+        if (threadIdx.x == 0) base_s += total_s;
         __syncthreads();
     }
     // padding rows of this expert's block; the last expert also marks the rows after all
