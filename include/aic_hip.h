@@ -413,7 +413,8 @@ int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float
  * low-rank term is optional (r2 0): X2 [M, *] (ldx2) and Y2 [N, r2] (ldy2) bf16, with seg_n > 0
  * giving output columns [s seg_n, (s+1) seg_n) the X2 columns [s r2, (s+1) r2) (the q, k and v
  * adapters side by side).  The rotation follows the whole sum.  In the INT4 GEMM's epilogue for
- * hd 128 on shapes of at least 128 full 256 x 256 tiles (r2 % 8 == 0, seg_n % 256 == 0);
+ * hd 128 on shapes of at least 128 full 256 x 256 tiles whose low-rank term the kernel takes
+ * (r2, ldx2 and ldy2 multiples of 8, X2 and Y2 16-byte aligned, seg_n a multiple of 256);
  * otherwise the product and then aic_hip_rope.
  * Replaces: the q, k, v LoRALinear::forward over QuantizedLinear::forward (src/nn/lora.cpp:75-93,
  * src/nn/quantization.cpp:669-679) followed by RotaryPositionEmbedding::forward on q and k
