@@ -34,6 +34,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     const f32x2_v v = {a, b};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
+// The logistic sigmoid 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, within 1 ulp)
+// instead of an IEEE division: the bf16 SwiGLU paths (GEMM epilogues and the standalone bf16
+// passes, which must agree bit for bit) round the result to bf16 afterwards.
+__device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf2f(bf16 h) {
     return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
 }

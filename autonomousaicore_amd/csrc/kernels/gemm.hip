@@ -369,6 +369,18 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         if (!fused) {
             GemmArgs b = a;
             b.rope_cos = b.rope_sin = nullptr;
+            if (a.Bq && !gemm_q4_eligible(a)) {
+                // an INT4 weight the operand-load dequantization cannot take (group or row length
+                // not a multiple of 64, misaligned scales): dequantized into a scratch copy first
+                const int64_t nw = a.N * a.K;
+                AIC_CHECK(a.transB && a.ldb == a.K && a.Bscale, InvalidArgument,
+                          "INT4 GEMM: the weight must be [N][K] with ld K");
+                void* w = stream_scratch(dtype_size(a.ab) * static_cast<size_t>(nw), s, 5);
+                int4_dequant(a.Bq, a.Bscale, a.scale_t, nw, a.group, w, a.ab, s);
+                b.B = w;
+                b.Bq = nullptr;
+                b.Bscale = nullptr;
+            }
             gemm(b, s);
             rope(a.C, a.ldc, a.M / a.rope_seq, a.rope_seq, a.rope_cols / a.rope_hd, a.rope_hd, a.rope_start,
                  a.rope_cos, a.rope_sin, false, a.c, s);
@@ -582,6 +594,36 @@ void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
         if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, bf16>(a, n, s);
         else dispatch_grouped<128, 128, 64, 4, bf16>(a, n, s);
     }
+}
+
+// One product: the tile kernels write one slot per block (at most its 128x128 tile count,
+// rounded up to a multiple of 8 for the grouped launch's per-product padding), the split-K
+// reduction at most 1024 and the read-back pass at most 256.  Several products: the grouped
+// launch's blocks, or the blocks of all but a cut product plus the cut's own launch, or equal
+// shares of the region per product (one gemm() each) -- all within n + 1 times the largest
+// single bound.
+int64_t gemm_sq_slots(const GemmArgs* a, int n) {
+    AIC_CHECK(a && n >= 1, InvalidArgument, "gemm_sq_slots: no products");
+    int64_t most = 0;
+    for (int i = 0; i < n; ++i) {
+        const int64_t t128 = ((a[i].M + 127) / 128) * ((a[i].N + 127) / 128);
+        most = std::max(most, (std::max<int64_t>(t128, 1024) + 7) / 8 * 8);
+    }
+    return n == 1 ? most : (n + 1) * most;
+}
+
+// The ragged-K launch writes one slot per block: E experts of its tile count rounded up to a
+// multiple of 8 (256x256 or 128x128 tiles); the fallback (one product per expert, in grouped
+// launches of up to 8 sharing the region equally) needs its launches' bounds.
+int64_t gemm_ragged_sq_slots(int64_t M, int64_t N, int E) {
+    AIC_CHECK(M > 0 && N > 0 && E >= 1, InvalidArgument, "gemm_ragged_sq_slots: bad shape");
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    GemmArgs g;
+    g.M = M;
+    g.N = N;
+    std::vector<GemmArgs> eight(8, g);
+    const int64_t launches = (E + 7) / 8;
+    return std::max(E * ((t128 + 7) / 8 * 8), launches * gemm_sq_slots(eight.data(), std::min(E, 8)));
 }
 
 bool gemm_ragged_eligible(const RaggedArgs& r) {

@@ -117,4 +117,11 @@ struct RaggedArgs {
 bool gemm_ragged_eligible(const RaggedArgs& r);
 void gemm_ragged(const RaggedArgs& r, hipStream_t stream);
 
+// Upper bounds of the sum-of-squares slots (GemmArgs::sq_*) that a call writes, whichever of its
+// paths runs, from the products' M and N only: gemm() (n == 1) or gemm_grouped() (n >= 2) over
+// the products a[0..n); gemm_ragged() with ragged K over E experts of an M x N product.  A caller
+// that sizes the slot region from these never meets the launchers' "slots needed" checks.
+int64_t gemm_sq_slots(const GemmArgs* a, int n);
+int64_t gemm_ragged_sq_slots(int64_t M, int64_t N, int E);
+
 }  // namespace aic::hip

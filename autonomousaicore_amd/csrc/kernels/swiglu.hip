@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_v8(const bf16* __restrict__ g,
     unpack8(*reinterpret_cast<const uint4*>(g + t * ld_gu + j), gv);
     unpack8(*reinterpret_cast<const uint4*>(u + t * ld_gu + j), uv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (gv[i] / (1.0f + __expf(-gv[i]))) * uv[i];
+    for (int i = 0; i < 8; ++i) o[i] = (gv[i] * sigmoid_rcp(gv[i])) * uv[i];
     *reinterpret_cast<uint4*>(h + t * ld_h + j) = pack8(o);
 }
 
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_v8(const bf16* __restrict__ g,
     unpack8(*reinterpret_cast<const uint4*>(dh + t * ld_h + j), dv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float sg = 1.0f / (1.0f + __expf(-gv[i]));
+        const float sg = sigmoid_rcp(gv[i]);
         const float a = gv[i] * sg;
         og[i] = (dv[i] * uv[i]) * (sg * (1.0f + gv[i] * (1.0f - sg)));
         ou[i] = dv[i] * a;

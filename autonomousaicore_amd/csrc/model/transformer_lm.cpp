@@ -428,9 +428,28 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
         sq_fold_ = covered == listed;
     }
     if (sq_fold_) {
+        // one region size for all producers: the largest of their slot bounds
+        auto prod = [](int64_t M, int64_t N) {
+            hip::GemmArgs a;
+            a.M = M;
+            a.N = N;
+            return a;
+        };
+        const hip::GemmArgs head = prod(V, d);
+        sq_region_ = hip::gemm_sq_slots(&head, 1);
+        if (E > 0) {
+            const hip::GemmArgs attn[2] = {prod(3 * d, d), prod(d, d)};
+            const hip::GemmArgs router = prod(E, d);
+            sq_region_ = std::max({sq_region_, hip::gemm_sq_slots(attn, 2), hip::gemm_sq_slots(&router, 1),
+                                   hip::gemm_ragged_sq_slots(d, f, static_cast<int>(E)),
+                                   hip::gemm_ragged_sq_slots(2 * f, d, static_cast<int>(E))});
+        } else {
+            const hip::GemmArgs layer[4] = {prod(3 * d, d), prod(d, d), prod(2 * f, d), prod(d, f)};
+            sq_region_ = std::max(sq_region_, hip::gemm_sq_slots(layer, 4));
+        }
         std::vector<int64_t> sizes(1, V * d);
         sizes.resize(2 * L + 2, d);
-        sq_slots_ = (L * sq_regions_per_layer() + 1) * kSqRegion +
+        sq_slots_ = (L * sq_regions_per_layer() + 1) * sq_region_ +
                     hip::sqnorm_slots(sizes.data(), static_cast<int>(sizes.size()));
         const int64_t nt = hip::sqnorm_reduce_tmp(sq_slots_);
         // the partials, then the flags, in one allocation (cleared by one fill per step)
@@ -960,9 +979,9 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     const bool fold = sq_fold_ && sq_fold_on_;
     const int64_t RPL = sq_regions_per_layer();
     auto sq_region = [&](int64_t r) {
-        return fold ? SqOut{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion} : SqOut{};
+        return fold ? SqOut{sq_part_ + r * sq_region_, sq_nf_ + r * sq_region_, sq_region_} : SqOut{};
     };
-    auto slots = [&](int64_t r) { return SqSlots{sq_part_ + r * kSqRegion, sq_nf_ + r * kSqRegion, kSqRegion}; };
+    auto slots = [&](int64_t r) { return SqSlots{sq_part_ + r * sq_region_, sq_nf_ + r * sq_region_, sq_region_}; };
     // every slot starts at zero: a launch writes only the slots of its path, which can change with
     // the token count (T not a multiple of 64 leaves the tile kernels)
     if (fold) {
@@ -1111,7 +1130,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         eg.push_back(G(normf_));
         en.resize(eg.size(), d);
         auto _p = prof_.scope(kGradNorm, 0.0, 4.0 * (V * d + (2 * L + 1) * d) + 12.0 * sq_slots_, s);
-        const int64_t pass0 = (L * RPL + 1) * kSqRegion;
+        const int64_t pass0 = (L * RPL + 1) * sq_region_;
         hip::sqnorm_partials(eg.data(), en.data(), static_cast<int>(eg.size()), sq_part_ + pass0, sq_nf_ + pass0, s);
         hip::sqnorm_reduce(sq_part_, sq_nf_, sq_slots_, sq_tmp_, sq_tmp_nf_, &dev_->sqnorm, &dev_->nonfinite, s);
         hip::optim_finalize(&dev_->sqnorm, &dev_->nonfinite, &dev_->ctl, s);

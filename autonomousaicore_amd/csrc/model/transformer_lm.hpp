@@ -238,10 +238,11 @@ private:
     int64_t hist_read_ = 0;            // host: records already returned
     float* backup_ = nullptr;          // snapshot: params, m, v (3 arenas) then the device scalars
     int64_t kv_B_ = 0;
-    // Gradient-norm partials (fused gradient norm): regions of kSqRegion slots for each layer's
+    // Gradient-norm partials (fused gradient norm): regions of sq_region_ slots for each layer's
     // weight-gradient launches, one for the LM head's, then the embedding's and the norm weights'
-    // sqnorm_k partials; fp64 sums and non-finite flags, zero where no producer writes.
-    static constexpr int64_t kSqRegion = 4096;
+    // sqnorm_k partials; fp64 sums and non-finite flags, zero where no producer writes.  The region
+    // size is the largest slot bound (hip::gemm_sq_slots) over the launches that write one.
+    int64_t sq_region_ = 0;
     // regions per layer: the grouped launch; with MoE FFNs also the experts' down and gate/up
     // weight gradients and the router's
     int64_t sq_regions_per_layer() const { return cfg_.num_experts > 0 ? 4 : 1; }

@@ -311,6 +311,29 @@ def test_1b_widths_fused_grad_norm_equals_pass():
         model.close()
 
 
+def test_large_vocab_head_fused_grad_norm():
+    """A 128k-vocabulary untied head at d_model 3072: its weight-gradient launch has 501 x 12 =
+    6012 blocks of 256x256, each writing one partial-sum slot, more than a fixed 4096-slot region
+    held.  The slot regions are sized from the producers' bounds at construction, so the fused
+    gradient norm runs and equals the pass over every gradient (gradients bit for bit, the norm
+    within 1e-6)."""
+    c = dict(vocab=128256, d=3072, L=1, H=24, f=1024, S=256)
+    ids, tgt = aic.batch(99, 1, c["S"], c["vocab"], dist="zipf")
+    out = {}
+    for fused in (True, False):
+        model = build_dense(c)
+        assert model.fused_grad_norm(fused) == fused
+        model.init_normal(5678, 0.02)
+        st = model.train_step(ids, tgt, 1, c["S"])
+        out[fused] = (st, model.get_grads())
+        model.close()
+    (sf, gf), (sp, gp) = out[True], out[False]
+    print(f"  grad norm fused {sf.grad_norm!r} pass {sp.grad_norm!r}")
+    assert not sf.found_inf and not sp.found_inf and sf.loss == sp.loss
+    np.testing.assert_array_equal(gf, gp)
+    assert abs(sf.grad_norm - sp.grad_norm) <= 1e-6 * sp.grad_norm
+
+
 def test_1b_full_config(orc):
     """configs[2] at full size: 16 layers, B 4 x S 2048, N(0, 0.02) weights, bf16 AMP, clip 1.0."""
     c = C1B

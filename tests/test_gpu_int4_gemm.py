@@ -115,20 +115,22 @@ def test_int4_gemm_other_shapes_fall_back_to_staging(orc):
     assert rel(y, ref) < 1e-5
 
 
-# (T, d, K, r, seq, start): the q/k/v projection of 128-wide heads with the rank-r adapters of q, k
-# and v side by side; 192 tiles of 256x256 take the INT4 kernel's rotary epilogue (with and
+# (T, d, K, r, seq, start, G): the q/k/v projection of 128-wide heads with the rank-r adapters of
+# q, k and v side by side; 192 tiles of 256x256 take the INT4 kernel's rotary epilogue (with and
 # without the adapters, and at a decode-style start position), 24 tiles the product and then
-# the rope pass
-@pytest.mark.parametrize("T,d,K,r,seq,start", [(4096, 1024, 512, 16, 2048, 0), (4096, 1024, 256, 0, 1024, 0),
-                                               (4096, 1024, 256, 16, 4096, 3), (1024, 512, 256, 16, 512, 0)])
-def test_int4_gemm_rope_equals_product_then_rope(orc, T, d, K, r, seq, start):
+# the rope pass; quantization groups of 32 (not a multiple of 64: the operand-load
+# dequantization cannot take them) dequantize the weight into scratch, then the product and rope
+@pytest.mark.parametrize("T,d,K,r,seq,start,G", [(4096, 1024, 512, 16, 2048, 0, 128), (4096, 1024, 256, 0, 1024, 0, 128),
+                                                 (4096, 1024, 256, 16, 4096, 3, 128), (1024, 512, 256, 16, 512, 0, 128),
+                                                 (4096, 1024, 256, 16, 2048, 0, 32)])
+def test_int4_gemm_rope_equals_product_then_rope(orc, T, d, K, r, seq, start, G):
     """aic_hip_int4_gemm_rope = the low-rank GEMM over the dequantized weight, then aic_hip_rope on
     the q and k columns: v columns bit-identical (the same products), q / k within one bf16
     rounding of the rotation of the same bf16 sum, and the oracle's RoPE of the float64 sum
     within the bf16 bound."""
-    print(f"int4 gemm rope: T {T} d {d} K {K} r {r} seq {seq} start {start}", flush=True)
-    rng = np.random.default_rng(T + d + K + r + start)
-    hd, N, G = 128, 3 * d, 128
+    print(f"int4 gemm rope: T {T} d {d} K {K} r {r} seq {seq} start {start} G {G}", flush=True)
+    rng = np.random.default_rng(T + d + K + r + start + G)
+    hd, N = 128, 3 * d
     packed, scales = _qweight(orc, rng, N, K, G, True)
     W = bf16_round(orc.int4_dequantize(packed, scales, N * K, G).reshape(N, K))
     x = bf16_round(rng.standard_normal((T, K)).astype(np.float32))

@@ -547,12 +547,12 @@ def test_gemm_swiglu_bwd_epilogue(orc, M, f, K):
     assert rel(got[:, :f], dg_ref) < 1e-2 and rel(got[:, f:], du_ref) < 1e-2
 
 
-# (T, d, K, hd, seq, start): 192 tiles of 256x256 with 128-wide heads take the GEMM's rotary
-# epilogue; fewer tiles, head_dim 64, a ragged M or a decode-style start position run the
-# product and then the rope pass
+# (T, d, K, hd, seq, start): 192 tiles of 256x256 with heads of 128 or 64 take the GEMM's rotary
+# epilogue, also at a start position past 0 (tables of start + seq rows); fewer tiles or a ragged
+# M run the product and then the rope pass
 @pytest.mark.parametrize("T,d,K,hd,seq,start", [(4096, 1024, 256, 128, 2048, 0), (4096, 1024, 256, 128, 1024, 0),
                                                  (1024, 512, 128, 128, 512, 0), (4096, 1024, 256, 64, 2048, 0),
-                                                 (300, 512, 128, 128, 100, 7)])
+                                                 (4096, 1024, 256, 128, 2048, 5), (300, 512, 128, 128, 100, 7)])
 def test_gemm_rope_epilogue(orc, T, d, K, hd, seq, start):
     """aic_hip_gemm_rope = aic_hip_gemm (x W^T over the q, k, v columns) then aic_hip_rope on the
     q and k columns: v columns bit-identical, q / k within one bf16 rounding of the rotation of
