@@ -176,6 +176,7 @@ SIGNATURES = {
     "aic_checkpoint_module_order": (i32, [i64, C.POINTER(C.c_char_p), i64p]),
     "aic_lm_get_params": (i32, [vp, vp]),
     "aic_lm_get_grads": (i32, [vp, vp]),
+    "aic_lm_moe_routing": (i32, [vp, i64, vp, i64, i64p]),
     "aic_lm_get_adam_state": (i32, [vp, vp, vp, i64p]),
     "aic_lm_init_normal": (i32, [vp, C.c_uint64, f32, i32]),
     "aic_lm_train_step": (i32, [vp, vp, vp, i64, i64, i32, C.POINTER(StepStats)]),

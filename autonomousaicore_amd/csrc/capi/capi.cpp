@@ -543,6 +543,12 @@ int aic_lm_get_base_params(const aic_lm* lm, float* host) {
 int aic_lm_set_params(aic_lm* lm, const float* host) { return guard([&] { lm->model->set_params(host); }); }
 int aic_lm_get_params(const aic_lm* lm, float* host) { return guard([&] { lm->model->get_params(host); }); }
 int aic_lm_get_grads(const aic_lm* lm, float* host) { return guard([&] { lm->model->get_grads(host); }); }
+int aic_lm_moe_routing(const aic_lm* lm, int64_t layer, int64_t* idx_host, int64_t capacity, int64_t* tokens) {
+    return guard([&] {
+        AIC_CHECK(lm && tokens, InvalidArgument, "null argument");
+        *tokens = lm->model->moe_routing(layer, idx_host, capacity);
+    });
+}
 int aic_lm_get_adam_state(const aic_lm* lm, float* m, float* v, int64_t* step) {
     return guard([&] { lm->model->get_adam_state(m, v, step); });
 }

@@ -41,6 +41,8 @@ public:
     // Routing of the last forward: idx [T, k] and counts [E] (device pointers).
     const int64_t* idx() const { return idx_.as<int64_t>(); }
     const int64_t* counts() const { return counts_.as<int64_t>(); }
+    int64_t tokens() const { return T_; }
+    int64_t top_k() const { return k_; }
     // counts on the host (copied from the device, with a stream synchronisation, on first use)
     const std::vector<int64_t>& counts_host();
 

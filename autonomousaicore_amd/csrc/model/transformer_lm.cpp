@@ -599,6 +599,19 @@ void TransformerLM::get_base_params(float* host) const {
 }
 void TransformerLM::get_grads(float* host) const { gather_host(grads_dev_, params_, arena_, host, stream_); }
 
+int64_t TransformerLM::moe_routing(int64_t layer, int64_t* host, int64_t cap) const {
+    AIC_CHECK(!moe_.empty(), InvalidArgument, "moe_routing: not a MoE model");
+    AIC_CHECK(layer >= 0 && layer < static_cast<int64_t>(moe_.size()), OutOfRange, "moe_routing: layer ", layer,
+              " of ", moe_.size());
+    const MoEFFN& m = *moe_[static_cast<size_t>(layer)];
+    const int64_t n = m.tokens() * m.top_k();
+    AIC_CHECK(n > 0, InvalidArgument, "moe_routing: no forward has run");
+    AIC_CHECK(host && cap >= n, OutOfRange, "moe_routing: ", n, " values, room for ", cap);
+    AIC_HIP_CHECK(hipStreamSynchronize(stream_));
+    AIC_HIP_CHECK(hipMemcpy(host, m.idx(), sizeof(int64_t) * static_cast<size_t>(n), hipMemcpyDeviceToHost));
+    return m.tokens();
+}
+
 void TransformerLM::get_adam_state(float* m, float* v, int64_t* step) const {
     if (m) gather_host(m_dev_, params_, arena_, m, stream_);
     if (v) gather_host(v_dev_, params_, arena_, v, stream_);

@@ -119,6 +119,9 @@ public:
     void get_params(float* host) const;
     void get_base_params(float* host) const;
     void get_grads(float* host) const;
+    // MoE: the top-k selection [T, top_k] of layer `layer` in the last forward, to host (at most
+    // cap values; synchronises); returns T.
+    int64_t moe_routing(int64_t layer, int64_t* host, int64_t cap) const;
     void get_adam_state(float* m, float* v, int64_t* step) const;
     void init_normal(uint64_t seed, float std, bool residual_scaling);
 

@@ -184,6 +184,15 @@ class TransformerLM:
         _lib.call("aic_lm_get_grads", self._h, out.ctypes.data)
         return out
 
+    def moe_routing(self, layer: int) -> np.ndarray:
+        """MoE: the top-k selection [T, top_k] (int64) layer `layer` used in the last forward."""
+        k = self.cfg.top_k
+        cap = self.cfg.max_seq_len * 64 * k  # up to 64 sequences of the longest length
+        out = np.empty(cap, np.int64)
+        tokens = C.c_int64()
+        _lib.call("aic_lm_moe_routing", self._h, layer, out.ctypes.data, cap, C.byref(tokens))
+        return out[:tokens.value * k].reshape(tokens.value, k).copy()
+
     def get_adam_state(self):
         m = np.empty(self.num_params, np.float32)
         v = np.empty(self.num_params, np.float32)

@@ -571,6 +571,12 @@ int aic_lm_get_base_params(const aic_lm* lm, float* host);
 int aic_lm_set_params(aic_lm* lm, const float* host);
 int aic_lm_get_params(const aic_lm* lm, float* host);
 int aic_lm_get_grads(const aic_lm* lm, float* host);
+/* MoE models: the top-k expert selection [T, top_k] (int64, each token's experts by falling
+ * logit, lower index on ties) that layer `layer` used in the last forward, copied to idx_host
+ * (capacity values; synchronises); *tokens receives T.  No counterpart in the reference: its
+ * MoERouter::route result is internal (src/nn/moe.cpp:33-129); exposed so that the step can be
+ * checked against the CPU path on the same routing. */
+int aic_lm_moe_routing(const aic_lm* lm, int64_t layer, int64_t* idx_host, int64_t capacity, int64_t* tokens);
 int aic_lm_get_adam_state(const aic_lm* lm, float* m_host, float* v_host, int64_t* step);
 /* Synthetic initialisation on the device: N(0, std) for weight matrices and embeddings,
  * ones for norms; residual projections (out_proj, down_proj) times 1/sqrt(2 L) when

@@ -743,12 +743,22 @@ static void experts_merge_add(float* wex, int64_t E, int64_t d, int64_t f, const
         }
 }
 
-void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
-                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx,
-                     float* gates);
-void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
-                     int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
-                     float* dwr, float* dwg, float* dwu, float* dwd);
+static void moe_ffn_fwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          float* y, float* aux, int64_t* idx_out, float* gates_out);
+static void moe_ffn_bwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          const float* dy, float daux, float* dh, float* dwr, float* dwg, float* dwu, float* dwd);
+
+/* MoE routing of the LM step's layers (test control, orc_moe_set_routing): forced [L][T][k] top-k
+ * selections used instead of each router's own (NULL: the routers decide), and out [L][T][k]
+ * receiving the selections the forward used (NULL: not recorded). */
+static const int64_t* g_moe_forced = NULL;
+static int64_t* g_moe_out = NULL;
+void orc_moe_set_routing(const int64_t* forced, int64_t* out) {
+    g_moe_forced = forced;
+    g_moe_out = out;
+}
 
 /* Forward; returns logits [T, V] (caller frees) and fills acts when non-NULL. */
 static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t* ids, int64_t B, int64_t S,
@@ -801,7 +811,9 @@ static float* lm_forward(const orc_lm_config* c, const lm_ptrs* P, const int64_t
             float* wd = (float*)xcalloc((size_t)(E * f * d), sizeof(float));
             experts_split(L->wex, E, d, f, wg, wu, wd);
             float aux = 0.0f;
-            orc_moe_ffn_fwd(h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef, ffo, &aux, NULL, NULL);
+            const int64_t lk = l * T * c->top_k;
+            moe_ffn_fwd_r(h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef,
+                          g_moe_forced ? g_moe_forced + lk : NULL, ffo, &aux, g_moe_out ? g_moe_out + lk : NULL, NULL);
             aux_sum = have_aux ? aux_sum + aux : aux; /* total_aux_loss: add in layer order */
             have_aux = 1;
             free(wg); free(wu); free(wd);
@@ -944,8 +956,9 @@ static int lm_step_core(const orc_lm_config* c, float* params, float* grads, con
             float* dwd = (float*)xcalloc((size_t)efd, sizeof(float));
             experts_split(L->wex, E, d, f, wg, wu, wd);
             memset(tmp, 0, sizeof(float) * Td);
-            orc_moe_ffn_bwd(A->h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef, dx, gscale, tmp, GL->wr, dwg,
-                            dwu, dwd);
+            moe_ffn_bwd_r(A->h2, L->wr, wg, wu, wd, T, d, f, E, c->top_k, c->aux_coef,
+                          g_moe_forced ? g_moe_forced + l * T * c->top_k : NULL, dx, gscale, tmp, GL->wr, dwg, dwu,
+                          dwd);
             experts_merge_add(GL->wex, E, d, f, dwg, dwu, dwd);
             free(wg); free(wu); free(wd); free(dwg); free(dwu); free(dwd);
         } else {
@@ -1122,8 +1135,20 @@ static void softmax_row_bwd(const float* p, const float* dp, float* dx, int64_t 
  *   with the 1e-9 of moe.cpp:74; counts[e] = tokens routed to e; mean_probs = mean_t probs (double
  *   sum); aux = sum_e mean_probs[e] * counts[e] * E * coef / (T * k) when coef > 0 and E > 1,
  *   else 0; gates = probs * mask / (sum(probs * mask) + 1e-9).  Any output may be NULL. */
+static void moe_route_r(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                        int64_t* idx, float* rweights, float* gates, float* probs, int64_t* counts, float* mean_probs,
+                        float* aux);
 void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, int64_t* idx,
                    float* rweights, float* gates, float* probs, int64_t* counts, float* mean_probs, float* aux) {
+    moe_route_r(logits, T, E, k, aux_coef, NULL, idx, rweights, gates, probs, counts, mean_probs, aux);
+}
+
+/* The same with the selection given: forced [T,k] (k distinct experts per token, in order) when
+ * not NULL -- test control, so that a step can be compared on another implementation's routing;
+ * every other quantity (probabilities, gates, counts, aux) follows from it as above. */
+static void moe_route_r(const float* logits, int64_t T, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                        int64_t* idx, float* rweights, float* gates, float* probs, int64_t* counts, float* mean_probs,
+                        float* aux) {
     float* p = (float*)xcalloc((size_t)(T * E), sizeof(float));
     int64_t* cnt = (int64_t*)xcalloc((size_t)E, sizeof(int64_t));
     int64_t* sel = (int64_t*)xcalloc((size_t)k, sizeof(int64_t));
@@ -1134,8 +1159,12 @@ void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float a
         memset(used, 0, (size_t)E);
         for (int64_t j = 0; j < k; ++j) { /* selection: largest remaining logit, lowest index on ties */
             int64_t best = -1;
-            for (int64_t e = 0; e < E; ++e)
-                if (!used[e] && (best < 0 || row[e] > row[best])) best = e;
+            if (forced) {
+                best = forced[t * k + j];
+            } else {
+                for (int64_t e = 0; e < E; ++e)
+                    if (!used[e] && (best < 0 || row[e] > row[best])) best = e;
+            }
             used[best] = 1;
             sel[j] = best;
             cnt[best]++;
@@ -1188,14 +1217,23 @@ static int64_t moe_rows(const int64_t* idx, int64_t T, int64_t k, int64_t e, int
  * reference evaluates every active expert on all tokens and multiplies by a zero gate for the
  * unrouted ones, which adds exact zeros, so the sparse sum is the same.  Outputs idx [T,k],
  * gates [T,E] and aux may be NULL. */
+static void moe_ffn_fwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          float* y, float* aux, int64_t* idx_out, float* gates_out);
 void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
                      int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx_out,
                      float* gates_out) {
+    moe_ffn_fwd_r(h, wr, wg, wu, wd, T, d, f, E, k, aux_coef, NULL, y, aux, idx_out, gates_out);
+}
+/* forced: the top-k selection to use (moe_route_r), NULL for the router's own. */
+static void moe_ffn_fwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          float* y, float* aux, int64_t* idx_out, float* gates_out) {
     float* logits = (float*)xcalloc((size_t)(T * E), sizeof(float));
     orc_linear_fwd(h, wr, logits, 1, T, d, E);
     int64_t* idx = (int64_t*)xcalloc((size_t)(T * k), sizeof(int64_t));
     float* gates = (float*)xcalloc((size_t)(T * E), sizeof(float));
-    orc_moe_route(logits, T, E, k, aux_coef, idx, NULL, gates, NULL, NULL, NULL, aux);
+    moe_route_r(logits, T, E, k, aux_coef, forced, idx, NULL, gates, NULL, NULL, NULL, aux);
     memset(y, 0, sizeof(float) * (size_t)(T * d));
     int64_t* rows = (int64_t*)xcalloc((size_t)T, sizeof(int64_t));
     float* xe = (float*)xcalloc((size_t)(T * d), sizeof(float));
@@ -1226,16 +1264,24 @@ void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const flo
  * gate normalisation (div / sum / add 1e-9), the mask, both router softmaxes (the one of route()
  * feeding mean_probs and the aux loss, the one of forward() feeding the gates) and both gate
  * Linear applications.  Gradients are added into dh [T,d], dwr [E,d], dwg/dwu [E,f,d], dwd [E,d,f]. */
+static void moe_ffn_bwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          const float* dy, float daux, float* dh, float* dwr, float* dwg, float* dwu, float* dwd);
 void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
                      int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,
                      float* dwr, float* dwg, float* dwu, float* dwd) {
+    moe_ffn_bwd_r(h, wr, wg, wu, wd, T, d, f, E, k, aux_coef, NULL, dy, daux, dh, dwr, dwg, dwu, dwd);
+}
+static void moe_ffn_bwd_r(const float* h, const float* wr, const float* wg, const float* wu, const float* wd,
+                          int64_t T, int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const int64_t* forced,
+                          const float* dy, float daux, float* dh, float* dwr, float* dwg, float* dwu, float* dwd) {
     float* logits = (float*)xcalloc((size_t)(T * E), sizeof(float));
     orc_linear_fwd(h, wr, logits, 1, T, d, E);
     int64_t* idx = (int64_t*)xcalloc((size_t)(T * k), sizeof(int64_t));
     float* gates = (float*)xcalloc((size_t)(T * E), sizeof(float));
     float* probs = (float*)xcalloc((size_t)(T * E), sizeof(float));
     int64_t* counts = (int64_t*)xcalloc((size_t)E, sizeof(int64_t));
-    orc_moe_route(logits, T, E, k, aux_coef, idx, NULL, gates, probs, counts, NULL, NULL);
+    moe_route_r(logits, T, E, k, aux_coef, forced, idx, NULL, gates, probs, counts, NULL, NULL);
     float* dgates = (float*)xcalloc((size_t)(T * E), sizeof(float));
     int64_t* rows = (int64_t*)xcalloc((size_t)T, sizeof(int64_t));
     float* xe = (float*)xcalloc((size_t)(T * d), sizeof(float));

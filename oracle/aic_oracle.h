@@ -209,6 +209,12 @@ void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t k, float a
 void orc_moe_ffn_fwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
                      int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, float* y, float* aux, int64_t* idx,
                      float* gates);
+/* Test control of the MoE LM step's routing (orc_lm_step, orc_lm_loss, orc_lm_logits): with
+ * forced != NULL ([n_layers][T][top_k], k distinct experts per token) every layer uses that top-k
+ * selection instead of its router's (probabilities, gates, counts and aux follow from it); with
+ * out != NULL the selections the forward used are written there.  Stays set until called again
+ * (NULL, NULL). */
+void orc_moe_set_routing(const int64_t* forced, int64_t* out);
 /* Its backward for dL/dy and dL/daux; gradients are added into dh, dwr, dwg, dwu, dwd (E <= 256). */
 void orc_moe_ffn_bwd(const float* h, const float* wr, const float* wg, const float* wu, const float* wd, int64_t T,
                      int64_t d, int64_t f, int64_t E, int64_t k, float aux_coef, const float* dy, float daux, float* dh,

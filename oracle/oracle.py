@@ -324,8 +324,24 @@ def lm_logits(cfg, params, ids, B, S):
 
 
 def lm_step(cfg, params, ids, targets, B, S, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1,
-            max_grad_norm=1.0, m=None, v=None, step=0, scaler: LossScaler | None = None, do_update=True):
-    """One training step in place on `params` (float32 flat).  Returns (result, grads, m, v, step)."""
+            max_grad_norm=1.0, m=None, v=None, step=0, scaler: LossScaler | None = None, do_update=True,
+            moe_forced=None, moe_route_out=None):
+    """One training step in place on `params` (float32 flat).  Returns (result, grads, m, v, step).
+    MoE configurations: moe_forced ([n_layers, T, top_k] int64) makes every layer use that top-k
+    selection instead of its router's; moe_route_out (same shape, int64, written) receives the
+    selections the forward used (orc_moe_set_routing)."""
+    if moe_forced is not None or moe_route_out is not None:
+        shape = (cfg.n_layers, B * S, cfg.top_k)
+        forced = None if moe_forced is None else np.ascontiguousarray(moe_forced, np.int64).reshape(shape)
+        if moe_route_out is not None:
+            assert moe_route_out.dtype == np.int64 and moe_route_out.flags.c_contiguous and moe_route_out.size == np.prod(shape)
+        lib().orc_moe_set_routing(_i(forced) if forced is not None else None,
+                                  _i(moe_route_out) if moe_route_out is not None else None)
+        try:
+            return lm_step(cfg, params, ids, targets, B, S, lr, beta1, beta2, eps, weight_decay, max_grad_norm, m, v,
+                           step, scaler, do_update)
+        finally:
+            lib().orc_moe_set_routing(None, None)
     n = num_params(cfg)
     assert params.size == n and params.dtype == np.float32
     grads = np.zeros(n, np.float32)

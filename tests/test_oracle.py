@@ -760,6 +760,40 @@ def test_moe_lm_step_vs_torch(orc, E, k):
     assert rel(p, new_t) < 1e-4
 
 
+def test_moe_lm_step_forced_routing(orc):
+    """The oracle's forced-routing control (orc_moe_set_routing), used to compare the device's MoE
+    step on the device's own top-k: forcing the routing the routers chose (as the forward records
+    it) reproduces the step bit for bit; forcing another valid routing matches the float64 torch
+    model run on that routing (loss 1e-5, gradients 1e-4) and moves the loss and the aux loss."""
+    vocab, d, L, H, f, B, S, coef, E, k = 64, 32, 2, 2, 48, 2, 16, 0.05, 4, 2
+    rng = np.random.default_rng(77)
+    lay = torch_ref.layout(vocab, d, L, f, False, E)
+    params = np.concatenate([(np.ones(s) if len(s) == 1 else rng.standard_normal(s) * 0.2).ravel()
+                             for _, s in lay]).astype(np.float32)
+    ids = rng.integers(0, vocab, B * S).astype(np.int64)
+    tgt = np.roll(ids, -1)
+    cfg = orc.make_config(vocab, d, L, H, f, S, n_experts=E, top_k=k, aux_coef=coef)
+    own = np.empty((L, B * S, k), np.int64)
+    p0 = params.copy()
+    res0, g0, _, _, _ = orc.lm_step(cfg, p0, ids, tgt, B, S, moe_route_out=own)
+    p1 = params.copy()
+    res1, g1, _, _, _ = orc.lm_step(cfg, p1, ids, tgt, B, S, moe_forced=own)
+    assert res1.loss == res0.loss and res1.aux_loss == res0.aux_loss
+    np.testing.assert_array_equal(g1, g0)
+    np.testing.assert_array_equal(p1, p0)
+    # another valid routing: each token's k experts drawn at random, in random order
+    alt = np.stack([np.stack([rng.permutation(E)[:k] for _ in range(B * S)]) for _ in range(L)]).astype(np.int64)
+    assert (alt != own).any()
+    loss_t, norm_t, grads_t, new_t = torch_ref.lm_step(vocab, d, L, H, f, False, params, ids, tgt, B, S,
+                                                        n_experts=E, top_k=k, aux_coef=coef, moe_forced=alt)
+    p2 = params.copy()
+    res2, g2, _, _, _ = orc.lm_step(cfg, p2, ids, tgt, B, S, moe_forced=alt)
+    assert abs(res2.loss - loss_t) / abs(loss_t) < 1e-5
+    assert abs(res2.grad_norm - norm_t) / norm_t < 1e-4
+    assert rel(g2, grads_t) < 1e-4 and rel(p2, new_t) < 1e-4
+    assert abs(res2.loss - res0.loss) > 1e-4 and res2.aux_loss != res0.aux_loss
+
+
 def _qlora_case(rng, vocab, d, L, f, r, b_std):
     lay = torch_ref.layout(vocab, d, L, f, False)
     base = np.concatenate([(np.ones(s) if len(s) == 1 else rng.standard_normal(s) * 0.2).ravel()

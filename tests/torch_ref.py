@@ -87,10 +87,11 @@ def rope(x, cos, sin):
 
 def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, S, eps=1e-6, lr=3e-4,
             betas=(0.9, 0.95), adam_eps=1e-8, weight_decay=0.1, max_grad_norm=1.0, dtype=torch.float64,
-            n_experts=0, top_k=2, aux_coef=0.01, lora=None):
+            n_experts=0, top_k=2, aux_coef=0.01, lora=None, moe_forced=None):
     """Returns loss (cross-entropy + the MoE aux losses), pre-clip grad norm, grads, updated params.
     lora = (lora_flat, r, alpha, G): params_flat is the frozen base, its projections enter as their
-    INT4 round trip, and the LoRA adapters (y += (x A^T) B^T * alpha / r) are the trained tensors."""
+    INT4 round trip, and the LoRA adapters (y += (x A^T) B^T * alpha / r) are the trained tensors.
+    moe_forced ([n_layers, B*S, top_k]): each MoE layer's top-k selection instead of its router's."""
     lay = layout(vocab, d, n_layers, f, tied, n_experts)
     P = {}
     off = 0
@@ -143,7 +144,8 @@ def lm_step(vocab, d, n_layers, n_heads, f, tied, params_flat, ids, targets, B, 
         if n_experts:
             ex = [(P[p + f"moe.experts.{e}.gate_proj.weight"], P[p + f"moe.experts.{e}.up_proj.weight"],
                    P[p + f"moe.experts.{e}.down_proj.weight"]) for e in range(n_experts)]
-            y, aux = moe_layer(h.reshape(B * S, d), P[p + "moe.router.gate.weight"], ex, top_k, aux_coef)
+            y, aux = moe_layer(h.reshape(B * S, d), P[p + "moe.router.gate.weight"], ex, top_k, aux_coef,
+                               None if moe_forced is None else moe_forced[l])
             x = x + y.reshape(B, S, d)
             aux_total = aux if aux_total is None else aux_total + aux
         else:
@@ -173,14 +175,14 @@ def moe_topk(logits, k):
     return order[:, :k].astype(np.int64)
 
 
-def moe_layer(th, twr, experts, k, aux_coef):
+def moe_layer(th, twr, experts, k, aux_coef, forced=None):
     """The MoE layer as a torch graph (src/nn/moe.cpp:33-253): th [T, d], router twr [E, d],
     experts [(gate, up, down)] -> (y [T, d], aux).  Every active expert runs on all tokens,
     weighted by the normalised masked gate; aux uses route()'s own softmax."""
     T, d = th.shape
     E = twr.shape[0]
     logits = th @ twr.T
-    idx = torch.tensor(moe_topk(logits.detach().numpy(), k))
+    idx = torch.tensor(moe_topk(logits.detach().numpy(), k) if forced is None else np.asarray(forced, np.int64))
     probs_r = torch.softmax(th @ twr.T, dim=-1)
     counts = torch.bincount(idx.reshape(-1), minlength=E).to(th.dtype)
     f_e = counts * (E * aux_coef) / (T * k)
