@@ -2,11 +2,14 @@
 
 Two kinds of check per configuration:
 
-* parity -- the configuration's true d / heads / FFN / vocab with 2 layers and one sequence,
-  one bf16 AMP step against the fp32 CPU oracle on identical weights and ids (the reference's
-  "AMP" computes in fp32, so the bf16 step is judged against the fp32 step): loss within
-  1e-2 relative, the global gradient norm within 5e-2, every gradient
-  tensor within 1e-1 (per-tensor L2; bf16 activations and bf16 operand rounding);
+* parity -- the configuration's true d / heads / FFN / vocab with 2 layers and one sequence
+  (the 1B widths also at the timed B 4 x S 2048), one bf16 AMP step against the fp32 CPU oracle
+  on identical weights and ids (the reference's "AMP" computes in fp32, so the bf16 step is
+  judged against the fp32 step): loss within 1e-2 relative; the global
+  gradient norm and every gradient tensor (per-tensor relative L2) within tolerances set per
+  configuration near twice the errors the GPU shows (both sides are deterministic; bf16
+  activations and operand rounding give worst tensors of 1.3e-2 - 1.6e-2); the MoE step is
+  compared on the device's own top-k selection;
 * full size -- the whole configuration (all layers, the configured batch and sequence) with
   its optimizer (AdamW lr 3e-4, betas 0.9/0.95, wd 0.1, clip 1.0, loss scale 2^16):
   the forward loss of one sequence at full depth against the oracle within 1e-2; the first
@@ -262,7 +265,7 @@ def test_1b_widths_step_matches_oracle(orc):
     st = model.train_step(ids, tgt, 1, S)
     grads = model.get_grads()
     res, g_ref, _, _, _ = orc.lm_step(oracle_cfg(orc, c, L=2), params.copy(), ids, tgt, 1, S)
-    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=1e-1, norm_tol=5e-2, tag="1b-widths B1xS2048")
+    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3.5e-2, norm_tol=4e-4, tag="1b-widths B1xS2048")
     model.close()
 
 
@@ -282,7 +285,7 @@ def test_1b_widths_timed_shape_matches_oracle(orc):
     grads = model.get_grads()
     model.close()
     res, g_ref, _, _, _ = orc.lm_step(oracle_cfg(orc, c, L=2), params.copy(), ids, tgt, B, S)
-    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=1e-1, norm_tol=5e-2, tag="1b-widths B4xS2048")
+    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3e-2, norm_tol=5e-5, tag="1b-widths B4xS2048")
 
 
 def test_1b_widths_fused_grad_norm_equals_pass():
@@ -396,7 +399,7 @@ def test_moe_widths_step_matches_oracle(orc):
                                       moe_forced=routing)
     print(f"  aux {st.aux_loss:.6f} vs oracle {res.aux_loss:.6f}")
     assert abs(st.aux_loss - res.aux_loss) < 3e-2 * abs(res.aux_loss)
-    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=1e-1, norm_tol=5e-2, tag="moe-widths B1xS1024")
+    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3e-2, norm_tol=1e-3, tag="moe-widths B1xS1024")
 
 
 def test_moe_widths_fused_grad_norm_equals_pass():
@@ -453,7 +456,7 @@ def test_qlora_1b_widths_step_matches_oracle(orc):
     grads = model.get_grads()
     res, g_ref, _, _, _ = orc.qlora_step(oracle_cfg(orc, c, L=2), c["r"], c["alpha"], c["G"], base, lora.copy(),
                                          ids, tgt, 1, S)
-    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=1e-1, norm_tol=5e-2, tag="qlora-widths B1xS2048")
+    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3.5e-2, norm_tol=5e-5, tag="qlora-widths B1xS2048")
     model.close()
 
 
