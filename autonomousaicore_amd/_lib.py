@@ -100,6 +100,8 @@ SIGNATURES = {
     "aic_hip_ce_bwd": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, vp, vp, i64, i32, vp]),
     "aic_hip_ce_bwd_rows": (i32, [vp, i64, vp, vp, i64, i64, i64, vp, i32, f32, vp, i64, i32, vp]),
     "aic_hip_ce_fwd_bwd": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, vp, vp, i32, vp]),
+    "aic_hip_ce_fwd_soft": (i32, [vp, i64, vp, i64, i64, i64, vp, vp, vp, i32, vp]),
+    "aic_hip_ce_bwd_soft": (i32, [vp, i64, vp, i64, vp, i64, i64, vp, i32, f32, vp, i64, i32, vp]),
     "aic_hip_memcpy_sync": (i32, [vp, vp, C.c_size_t, vp]),
     "aic_hip_embed_fwd": (i32, [vp, i64, vp, i64, i64, vp, i32, vp]),
     "aic_hip_embed_bwd": (i32, [vp, i64, vp, i64, i64, vp, i32, i32, vp]),
@@ -176,6 +178,9 @@ SIGNATURES = {
     "aic_checkpoint_module_order": (i32, [i64, C.POINTER(C.c_char_p), i64p]),
     "aic_lm_get_params": (i32, [vp, vp]),
     "aic_lm_get_grads": (i32, [vp, vp]),
+    "aic_hip_attn_fwd_qk": (i32, [vp, i64, vp, vp, i64, vp, i64, vp, i64, i64, i64, i64, i64, i32, f32, i32, vp]),
+    "aic_hip_attn_bwd_qk": (i32, [vp, i64, vp, vp, i64, vp, vp, i64, vp, vp, i64, vp, vp, i64, i64, i64, i64, i64, i64,
+                                  i32, f32, i32, vp]),
     "aic_lm_moe_routing": (i32, [vp, i64, vp, i64, i64p]),
     "aic_lm_get_adam_state": (i32, [vp, vp, vp, i64p]),
     "aic_lm_init_normal": (i32, [vp, C.c_uint64, f32, i32]),

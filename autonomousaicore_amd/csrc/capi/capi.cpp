@@ -242,6 +242,25 @@ int aic_hip_attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv
     });
 }
 
+int aic_hip_attn_fwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, void* o, int64_t ld_o,
+                        float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, int causal, float scale,
+                        aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::attn_fwd_qk(q, ld_q, k, v, ld_k, o, ld_o, lse, B, H, Sq, Sk, hd, causal != 0, scale, dt(d),
+                              st(stream));
+    });
+}
+
+int aic_hip_attn_bwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, const void* o,
+                        const void* dout, int64_t ld_o, const float* lse, void* dq, int64_t ld_dq, void* dk, void* dv,
+                        int64_t ld_dkv, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, int causal,
+                        float scale, aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::attn_bwd_qk(q, ld_q, k, v, ld_k, o, dout, ld_o, lse, dq, ld_dq, dk, dv, ld_dkv, B, H, Sq, Sk, hd,
+                              causal != 0, scale, dt(d), st(stream));
+    });
+}
+
 int aic_hip_gemm_rope(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* W, int64_t ldw,
                       void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq, int64_t start_pos,
                       const float* cos_t, const float* sin_t, aic_stream stream) {
@@ -370,6 +389,20 @@ int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, 
     return guard([&] {
         aic::hip::ce_bwd_rows(logits, ld, targets, lse, N, C, ignore_index, grad, per_row, divisor, dlogits, ld_d,
                               dt(d), st(stream));
+    });
+}
+
+int aic_hip_ce_fwd_soft(const void* logits, int64_t ld, const float* y, int64_t ld_y, int64_t N, int64_t C,
+                        float* losses, float* lse, float* loss_mean, aic_dtype d, aic_stream stream) {
+    return guard([&] { aic::hip::ce_fwd_soft(logits, ld, y, ld_y, N, C, losses, lse, loss_mean, dt(d), st(stream)); });
+}
+
+int aic_hip_ce_bwd_soft(const void* logits, int64_t ld, const float* y, int64_t ld_y, const float* lse, int64_t N,
+                        int64_t C, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
+                        aic_dtype d, aic_stream stream) {
+    return guard([&] {
+        aic::hip::ce_bwd_soft(logits, ld, y, ld_y, lse, N, C, grad, per_row, divisor, dlogits, ld_d, dt(d),
+                              st(stream));
     });
 }
 

@@ -869,14 +869,14 @@ constexpr int kSimtTile = 64;
 
 template <typename T, int HD>
 __global__ __launch_bounds__(64) void attn_fwd_simt(const T* __restrict__ q, const T* __restrict__ k,
-                                                    const T* __restrict__ v, int64_t ldq, T* __restrict__ o,
-                                                    int64_t ldo, float* __restrict__ lse, int H, int S, float scale,
-                                                    int causal) {
+                                                    const T* __restrict__ v, int64_t ldq, int64_t ldk,
+                                                    T* __restrict__ o, int64_t ldo, float* __restrict__ lse, int H,
+                                                    int S, int Sk, float scale, int causal) {
     __shared__ float sk[kSimtTile][HD + 1];
     __shared__ float sv[kSimtTile][HD + 1];
     const int h = blockIdx.y, b = blockIdx.z;
     const int qi = blockIdx.x * kSimtTile + threadIdx.x;
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
+    const int64_t tok0 = static_cast<int64_t>(b) * S, tok0k = static_cast<int64_t>(b) * Sk;
     const int64_t hoff = static_cast<int64_t>(h) * HD;
     float qv[HD], acc[HD];
     for (int d = 0; d < HD; ++d) {
@@ -884,20 +884,20 @@ __global__ __launch_bounds__(64) void attn_fwd_simt(const T* __restrict__ q, con
         acc[d] = 0.0f;
     }
     float m = -INFINITY, l = 0.0f;
-    const int kend = causal ? min(S, static_cast<int>((blockIdx.x + 1) * kSimtTile)) : S;
+    const int kend = causal ? min(Sk, static_cast<int>((blockIdx.x + 1) * kSimtTile)) : Sk;
     for (int k0 = 0; k0 < kend; k0 += kSimtTile) {
         __syncthreads();
         for (int e = threadIdx.x; e < kSimtTile * HD; e += 64) {
             const int r = e / HD, d = e % HD;
             const int key = k0 + r;
-            sk[r][d] = key < S ? ld(k, (tok0 + key) * ldq + hoff + d) : 0.0f;
-            sv[r][d] = key < S ? ld(v, (tok0 + key) * ldq + hoff + d) : 0.0f;
+            sk[r][d] = key < Sk ? ld(k, (tok0k + key) * ldk + hoff + d) : 0.0f;
+            sv[r][d] = key < Sk ? ld(v, (tok0k + key) * ldk + hoff + d) : 0.0f;
         }
         __syncthreads();
         if (qi >= S) continue;
         for (int r = 0; r < kSimtTile; ++r) {
             const int key = k0 + r;
-            if (key >= S || (causal && key > qi)) break;
+            if (key >= Sk || (causal && key > qi)) break;
             float sdot = 0.0f;
             for (int d = 0; d < HD; ++d) sdot += qv[d] * sk[r][d];
             const float x = sdot * scale;
@@ -918,23 +918,24 @@ __global__ __launch_bounds__(64) void attn_fwd_simt(const T* __restrict__ q, con
 // dK, dV: one thread per key; loops over queries >= key.
 template <typename T, int HD>
 __global__ __launch_bounds__(64) void attn_bwd_kv_simt(const T* __restrict__ q, const T* __restrict__ k,
-                                                       const T* __restrict__ v, int64_t ldq, const T* __restrict__ dout,
-                                                       int64_t ldo, const float* __restrict__ lse,
-                                                       const float* __restrict__ Dg, T* dk, T* dv, int64_t ldd, int H,
-                                                       int S, float scale, int causal) {
+                                                       const T* __restrict__ v, int64_t ldq, int64_t ldk,
+                                                       const T* __restrict__ dout, int64_t ldo,
+                                                       const float* __restrict__ lse, const float* __restrict__ Dg,
+                                                       T* dk, T* dv, int64_t ldd, int64_t lddk, int H, int S, int Sk,
+                                                       float scale, int causal) {
     __shared__ float sq[kSimtTile][HD + 1];
     __shared__ float sdo[kSimtTile][HD + 1];
     __shared__ float sl[kSimtTile], sD[kSimtTile];
     const int h = blockIdx.y, b = blockIdx.z;
     const int kj = blockIdx.x * kSimtTile + threadIdx.x;
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
+    const int64_t tok0 = static_cast<int64_t>(b) * S, tok0k = static_cast<int64_t>(b) * Sk;
     const int64_t hoff = static_cast<int64_t>(h) * HD;
     const float* lse_bh = lse + (static_cast<int64_t>(b) * H + h) * S;
     const float* D_bh = Dg + (static_cast<int64_t>(b) * H + h) * S;
     float kv_[HD], vv[HD], dka[HD], dva[HD];
     for (int d = 0; d < HD; ++d) {
-        kv_[d] = kj < S ? ld(k, (tok0 + kj) * ldq + hoff + d) : 0.0f;
-        vv[d] = kj < S ? ld(v, (tok0 + kj) * ldq + hoff + d) : 0.0f;
+        kv_[d] = kj < Sk ? ld(k, (tok0k + kj) * ldk + hoff + d) : 0.0f;
+        vv[d] = kj < Sk ? ld(v, (tok0k + kj) * ldk + hoff + d) : 0.0f;
         dka[d] = 0.0f;
         dva[d] = 0.0f;
     }
@@ -953,7 +954,7 @@ __global__ __launch_bounds__(64) void attn_bwd_kv_simt(const T* __restrict__ q, 
             sD[threadIdx.x] = qq < S ? D_bh[qq] : 0.0f;
         }
         __syncthreads();
-        if (kj >= S) continue;
+        if (kj >= Sk) continue;
         for (int r = 0; r < kSimtTile; ++r) {
             const int qq = q0 + r;
             if (qq >= S) break;
@@ -971,24 +972,24 @@ __global__ __launch_bounds__(64) void attn_bwd_kv_simt(const T* __restrict__ q, 
             }
         }
     }
-    if (kj < S)
+    if (kj < Sk)
         for (int d = 0; d < HD; ++d) {
-            st(dk, (tok0 + kj) * ldd + hoff + d, dka[d] * scale);
-            st(dv, (tok0 + kj) * ldd + hoff + d, dva[d]);
+            st(dk, (tok0k + kj) * lddk + hoff + d, dka[d] * scale);
+            st(dv, (tok0k + kj) * lddk + hoff + d, dva[d]);
         }
 }
 
 template <typename T, int HD>
 __global__ __launch_bounds__(64) void attn_bwd_q_simt(const T* __restrict__ q, const T* __restrict__ k,
-                                                      const T* __restrict__ v, int64_t ldq, const T* __restrict__ dout,
-                                                      int64_t ldo, const float* __restrict__ lse,
-                                                      const float* __restrict__ Dg, T* dq, int64_t ldd, int H, int S,
-                                                      float scale, int causal) {
+                                                      const T* __restrict__ v, int64_t ldq, int64_t ldk,
+                                                      const T* __restrict__ dout, int64_t ldo,
+                                                      const float* __restrict__ lse, const float* __restrict__ Dg, T* dq,
+                                                      int64_t ldd, int H, int S, int Sk, float scale, int causal) {
     __shared__ float sk[kSimtTile][HD + 1];
     __shared__ float sv[kSimtTile][HD + 1];
     const int h = blockIdx.y, b = blockIdx.z;
     const int qi = blockIdx.x * kSimtTile + threadIdx.x;
-    const int64_t tok0 = static_cast<int64_t>(b) * S;
+    const int64_t tok0 = static_cast<int64_t>(b) * S, tok0k = static_cast<int64_t>(b) * Sk;
     const int64_t hoff = static_cast<int64_t>(h) * HD;
     float qv[HD], dov[HD], acc[HD];
     for (int d = 0; d < HD; ++d) {
@@ -998,20 +999,20 @@ __global__ __launch_bounds__(64) void attn_bwd_q_simt(const T* __restrict__ q, c
     }
     const float l = qi < S ? lse[(static_cast<int64_t>(b) * H + h) * S + qi] : 0.0f;
     const float Dq = qi < S ? Dg[(static_cast<int64_t>(b) * H + h) * S + qi] : 0.0f;
-    const int kend = causal ? min(S, static_cast<int>((blockIdx.x + 1) * kSimtTile)) : S;
+    const int kend = causal ? min(Sk, static_cast<int>((blockIdx.x + 1) * kSimtTile)) : Sk;
     for (int k0 = 0; k0 < kend; k0 += kSimtTile) {
         __syncthreads();
         for (int e = threadIdx.x; e < kSimtTile * HD; e += 64) {
             const int r = e / HD, d = e % HD;
             const int key = k0 + r;
-            sk[r][d] = key < S ? ld(k, (tok0 + key) * ldq + hoff + d) : 0.0f;
-            sv[r][d] = key < S ? ld(v, (tok0 + key) * ldq + hoff + d) : 0.0f;
+            sk[r][d] = key < Sk ? ld(k, (tok0k + key) * ldk + hoff + d) : 0.0f;
+            sv[r][d] = key < Sk ? ld(v, (tok0k + key) * ldk + hoff + d) : 0.0f;
         }
         __syncthreads();
         if (qi >= S) continue;
         for (int r = 0; r < kSimtTile; ++r) {
             const int key = k0 + r;
-            if (key >= S || (causal && key > qi)) break;
+            if (key >= Sk || (causal && key > qi)) break;
             float sdot = 0.0f, dpd = 0.0f;
             for (int d = 0; d < HD; ++d) {
                 sdot += qv[d] * sk[r][d];
@@ -1102,14 +1103,14 @@ bool mfma_ok(const void* q, const void* k, const void* v, int64_t ldq, const voi
 }
 
 template <typename T>
-void fwd_simt(const void* q, const void* k, const void* v, int64_t ldq, void* o, int64_t ldo, float* lse, int64_t B,
-              int64_t H, int64_t S, int64_t hd, bool causal, float scale, hipStream_t s) {
+void fwd_simt(const void* q, const void* k, const void* v, int64_t ldq, int64_t ldk, void* o, int64_t ldo, float* lse,
+              int64_t B, int64_t H, int64_t S, int64_t Sk, int64_t hd, bool causal, float scale, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + kSimtTile - 1) / kSimtTile), static_cast<unsigned>(H),
                     static_cast<unsigned>(B));
 #define AIC_FWD_SIMT(HD_)                                                                                     \
     hipLaunchKernelGGL((attn_fwd_simt<T, HD_>), grid, dim3(64), 0, s, static_cast<const T*>(q),                \
-                       static_cast<const T*>(k), static_cast<const T*>(v), ldq, static_cast<T*>(o), ldo, lse,     \
-                       static_cast<int>(H), static_cast<int>(S), scale, causal ? 1 : 0)
+                       static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, static_cast<T*>(o), ldo, lse, \
+                       static_cast<int>(H), static_cast<int>(S), static_cast<int>(Sk), scale, causal ? 1 : 0)
     if (hd == 16) AIC_FWD_SIMT(16);
     else if (hd == 32) AIC_FWD_SIMT(32);
     else if (hd == 64) AIC_FWD_SIMT(64);
@@ -1120,21 +1121,26 @@ void fwd_simt(const void* q, const void* k, const void* v, int64_t ldq, void* o,
 }
 
 template <typename T>
-void bwd_simt(const void* q, const void* k, const void* v, int64_t ldq, const void* dout, int64_t ldo, const float* lse,
-              const float* D, void* dq, void* dk, void* dv, int64_t ldd, int64_t B, int64_t H, int64_t S, int64_t hd,
-              bool causal, float scale, hipStream_t s) {
+void bwd_simt(const void* q, const void* k, const void* v, int64_t ldq, int64_t ldk, const void* dout, int64_t ldo,
+              const float* lse, const float* D, void* dq, int64_t ldd, void* dk, void* dv, int64_t lddk, int64_t B,
+              int64_t H, int64_t S, int64_t Sk, int64_t hd, bool causal, float scale, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((S + kSimtTile - 1) / kSimtTile), static_cast<unsigned>(H),
                     static_cast<unsigned>(B));
+    const dim3 gridk(static_cast<unsigned>((Sk + kSimtTile - 1) / kSimtTile), static_cast<unsigned>(H),
+                     static_cast<unsigned>(B));
 #define AIC_BWD_SIMT(HD_)                                                                                      \
     do {                                                                                                        \
-        hipLaunchKernelGGL((attn_bwd_kv_simt<T, HD_>), grid, dim3(64), 0, s, static_cast<const T*>(q),          \
-                           static_cast<const T*>(k), static_cast<const T*>(v), ldq, static_cast<const T*>(dout), \
-                           ldo, lse, D, static_cast<T*>(dk), static_cast<T*>(dv), ldd, static_cast<int>(H),      \
-                           static_cast<int>(S), scale, causal ? 1 : 0);                                          \
-        hipLaunchKernelGGL((attn_bwd_q_simt<T, HD_>), grid, dim3(64), 0, s, static_cast<const T*>(q),           \
-                           static_cast<const T*>(k), static_cast<const T*>(v), ldq, static_cast<const T*>(dout), \
-                           ldo, lse, D, static_cast<T*>(dq), ldd, static_cast<int>(H), static_cast<int>(S),      \
-                           scale, causal ? 1 : 0);                                                               \
+        hipLaunchKernelGGL((attn_bwd_kv_simt<T, HD_>), gridk, dim3(64), 0, s, static_cast<const T*>(q),         \
+                           static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,                        \
+                           static_cast<const T*>(dout), ldo, lse, D, static_cast<T*>(dk), static_cast<T*>(dv),   \
+                           ldd, lddk, static_cast<int>(H), static_cast<int>(S), static_cast<int>(Sk), scale,    \
+                           causal ? 1 : 0);                                                                      \
+        if (S > 0)                                                                                              \
+            hipLaunchKernelGGL((attn_bwd_q_simt<T, HD_>), grid, dim3(64), 0, s, static_cast<const T*>(q),       \
+                               static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,                    \
+                               static_cast<const T*>(dout), ldo, lse, D, static_cast<T*>(dq), ldd,               \
+                               static_cast<int>(H), static_cast<int>(S), static_cast<int>(Sk), scale,           \
+                               causal ? 1 : 0);                                                                  \
     } while (0)
     if (hd == 16) AIC_BWD_SIMT(16);
     else if (hd == 32) AIC_BWD_SIMT(32);
@@ -1168,8 +1174,9 @@ void attn_fwd(const void* q, const void* k, const void* v, int64_t ld_qkv, void*
         AIC_LAUNCH_CHECK("attn_fwd_pipe");
         return;
     }
-    if (dt == DType::Float32) fwd_simt<float>(q, k, v, ld_qkv, o, ld_o, lse, B, H, S, hd, causal, scale, s);
-    else if (dt == DType::BFloat16) fwd_simt<bf16>(q, k, v, ld_qkv, o, ld_o, lse, B, H, S, hd, causal, scale, s);
+    if (dt == DType::Float32) fwd_simt<float>(q, k, v, ld_qkv, ld_qkv, o, ld_o, lse, B, H, S, S, hd, causal, scale, s);
+    else if (dt == DType::BFloat16)
+        fwd_simt<bf16>(q, k, v, ld_qkv, ld_qkv, o, ld_o, lse, B, H, S, S, hd, causal, scale, s);
     else AIC_THROW(DTypeMismatch, "attn_fwd: dtype must be f32 or bf16");
 }
 
@@ -1238,12 +1245,70 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
         AIC_THROW(DTypeMismatch, "attn_bwd: dtype must be f32 or bf16");
     AIC_LAUNCH_CHECK("attn_dot");
 
-    if (dt == DType::Float32) bwd_simt<float>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
-    else bwd_simt<bf16>(q, k, v, ld_qkv, dout, ld_o, lse, D, dq, dk, dv, ld_d, B, H, S, hd, causal, scale, s);
+    if (dt == DType::Float32)
+        bwd_simt<float>(q, k, v, ld_qkv, ld_qkv, dout, ld_o, lse, D, dq, ld_d, dk, dv, ld_d, B, H, S, S, hd, causal,
+                        scale, s);
+    else
+        bwd_simt<bf16>(q, k, v, ld_qkv, ld_qkv, dout, ld_o, lse, D, dq, ld_d, dk, dv, ld_d, B, H, S, S, hd, causal,
+                       scale, s);
     if (rope_cos) {  // the rotary embedding's adjoint as its own pass on these paths
         rope(dq, ld_d, B, S, H, hd, 0, rope_cos, rope_sin, true, dt, s);
         rope(dk, ld_d, B, S, H, hd, 0, rope_cos, rope_sin, true, dt, s);
     }
+}
+
+// Queries and keys of different lengths (launch_flash_attention_forward/backward_gpu take
+// seq_len_q and seq_len_k, src/cuda/cuda_flash_attention.cuh:12-46): q, o, dO [B, Sq] token rows
+// of H heads (leading dimensions ld_q, ld_o), k, v [B, Sk] rows (ld_k); causal as the reference's
+// CPU path (src/ops/flash_attention.cpp:76-89, 170-260): query r sees keys c <= r.  The SIMT
+// kernels (fp32 math) for any dtype; lse [B, H, Sq].
+void attn_fwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, void* o, int64_t ld_o,
+                 float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, bool causal, float scale,
+                 DType dt, hipStream_t s) {
+    AIC_CHECK(B >= 0 && H > 0 && Sq >= 0 && Sk >= 0 && hd > 0 && ld_q >= H * hd && ld_k >= H * hd && ld_o >= H * hd,
+              InvalidArgument, "attn_fwd: bad shape");
+    AIC_CHECK(Sq < (1LL << 30) && Sk < (1LL << 30) && B * std::max(Sq, Sk) < (1LL << 31), InvalidArgument,
+              "attn_fwd: sequence too long");
+    if (B == 0 || Sq == 0) return;
+    AIC_CHECK(Sk > 0, InvalidArgument, "attn_fwd: no keys");
+    if (dt == DType::Float32) fwd_simt<float>(q, k, v, ld_q, ld_k, o, ld_o, lse, B, H, Sq, Sk, hd, causal, scale, s);
+    else if (dt == DType::BFloat16)
+        fwd_simt<bf16>(q, k, v, ld_q, ld_k, o, ld_o, lse, B, H, Sq, Sk, hd, causal, scale, s);
+    else AIC_THROW(DTypeMismatch, "attn_fwd: dtype must be f32 or bf16");
+}
+
+void attn_bwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, const void* o,
+                 const void* dout, int64_t ld_o, const float* lse, void* dq, int64_t ld_dq, void* dk, void* dv,
+                 int64_t ld_dkv, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, bool causal, float scale,
+                 DType dt, hipStream_t s) {
+    AIC_CHECK(B >= 0 && H > 0 && Sq >= 0 && Sk >= 0 && hd > 0 && ld_q >= H * hd && ld_k >= H * hd &&
+                  ld_o >= H * hd && ld_dq >= H * hd && ld_dkv >= H * hd,
+              InvalidArgument, "attn_bwd: bad shape");
+    AIC_CHECK(Sq < (1LL << 30) && Sk < (1LL << 30) && B * std::max(Sq, Sk) < (1LL << 31), InvalidArgument,
+              "attn_bwd: sequence too long");
+    if (B == 0) return;
+    AIC_CHECK(Sk > 0, InvalidArgument, "attn_bwd: no keys");
+    AIC_CHECK(dt == DType::Float32 || dt == DType::BFloat16, DTypeMismatch, "attn_bwd: dtype must be f32 or bf16");
+    // no queries: only the key kernel runs, and its empty query loop writes zero dK and dV
+    float* D = static_cast<float*>(stream_scratch(sizeof(float) * std::max<int64_t>(B * H * Sq, 1), s));
+    if (Sq > 0) {
+        const unsigned dgrid = static_cast<unsigned>((B * Sq * H * 64 + 255) / 256);
+        if (dt == DType::Float32)
+            hipLaunchKernelGGL(attn_dot_k<float>, dim3(dgrid), dim3(256), 0, s, static_cast<const float*>(o),
+                               static_cast<const float*>(dout), ld_o, D, B * Sq, static_cast<int>(H),
+                               static_cast<int>(Sq), static_cast<int>(hd));
+        else
+            hipLaunchKernelGGL(attn_dot_k<bf16>, dim3(dgrid), dim3(256), 0, s, static_cast<const bf16*>(o),
+                               static_cast<const bf16*>(dout), ld_o, D, B * Sq, static_cast<int>(H),
+                               static_cast<int>(Sq), static_cast<int>(hd));
+        AIC_LAUNCH_CHECK("attn_dot");
+    }
+    if (dt == DType::Float32)
+        bwd_simt<float>(q, k, v, ld_q, ld_k, dout, ld_o, lse, D, dq, ld_dq, dk, dv, ld_dkv, B, H, Sq, Sk, hd, causal,
+                        scale, s);
+    else
+        bwd_simt<bf16>(q, k, v, ld_q, ld_k, dout, ld_o, lse, D, dq, ld_dq, dk, dv, ld_dkv, B, H, Sq, Sk, hd, causal,
+                       scale, s);
 }
 
 void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,

@@ -46,6 +46,12 @@ void ce_bwd(const void* logits, int64_t ld, const int64_t* targets, const float*
 void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const float* lse, int64_t N, int64_t C,
                  int64_t ignore_index, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
                  DType dt, hipStream_t s);
+// Soft targets y [N, C] fp32 (leading dimension ldy): row losses lse - sum_j y_j z_j, every row
+// valid (loss_mean over N); the backward writes (softmax - y) times the row weight of ce_bwd_rows.
+void ce_fwd_soft(const void* logits, int64_t ld, const float* y, int64_t ldy, int64_t N, int64_t C, float* losses,
+                 float* lse, float* loss_mean, DType dt, hipStream_t s);
+void ce_bwd_soft(const void* logits, int64_t ld, const float* y, int64_t ldy, const float* lse, int64_t N, int64_t C,
+                 const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d, DType dt, hipStream_t s);
 // Forward and backward in one pass: ce_fwd's outputs (valid required) and the logits overwritten by
 // ce_bwd's gradient with grad (device scalar, null: 1) over the valid rows.
 void ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
@@ -115,6 +121,14 @@ void attn_bwd(const void* q, const void* k, const void* v, int64_t ld_qkv, const
               int64_t ld_o, const float* lse, void* dq, void* dk, void* dv, int64_t ld_d, int64_t B, int64_t H,
               int64_t S, int64_t hd, bool causal, float scale, DType dt, hipStream_t s,
               const float* rope_cos = nullptr, const float* rope_sin = nullptr);
+// Queries and keys of different lengths Sq, Sk (causal: query r sees keys c <= r).
+void attn_fwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, void* o, int64_t ld_o,
+                 float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, bool causal, float scale,
+                 DType dt, hipStream_t s);
+void attn_bwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, const void* o,
+                 const void* dout, int64_t ld_o, const float* lse, void* dq, int64_t ld_dq, void* dk, void* dv,
+                 int64_t ld_dkv, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, bool causal, float scale,
+                 DType dt, hipStream_t s);
 // Queries of S_new new tokens (rows of q, [B*S_new] x ldq) at positions start_pos.. against a
 // KV cache kc / vc ([B][cache_rows][ldkv], positions 0 .. start_pos+S_new-1 filled), causal.
 void attn_cached(const void* q, int64_t ldq, const void* kc, const void* vc, int64_t ldkv, int64_t cache_rows, void* o,

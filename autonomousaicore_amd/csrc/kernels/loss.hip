@@ -1,10 +1,13 @@
-// Fused log-sum-exp cross-entropy with index targets.
+// Fused log-sum-exp cross-entropy with index or soft targets.
 // Replaces cuda_cross_entropy_forward/backward (src/cuda/cuda_loss.cu:68-190) and the CPU
 // path of src/loss/cross_entropy.cpp:149-290.  One block per row; the mean over valid rows
 // is reduced by a single block in a fixed order (deterministic), and the valid-row count
 // stays on the device (the reference synchronises the host for it, cuda_loss.cu:228-234).
-// A target outside [0, C) that is not ignore_index yields a NaN row loss (the reference
-// throws OutOfRange on the host).
+// An index target outside [0, C) that is not ignore_index counts as a valid row with loss
+// lse - 0 and gradient softmax (no one-hot), as the CUDA launcher computes it
+// (cuda_loss.cu:114-121, 170-176; the CPU path throws OutOfRange on the host instead).
+// Soft targets y [N, C] (fp32): row loss lse - sum_j y_j z_j, gradient (softmax - y) * scale,
+// every row valid (cuda_loss.cu:123-131, 177-184).
 #include <cmath>
 
 #include "common.hpp"
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(256) void ce_fwd_k(const T* __restrict__ logits, in
         if (lse_out) lse_out[row] = lse;
         const int64_t t = targets[row];
         float li = 0.0f;
-        if (t != ignore_index) li = (t >= 0 && t < C) ? lse - ld(z, t) : NAN;
+        if (t != ignore_index) li = lse - ((t >= 0 && t < C) ? ld(z, t) : 0.0f);
         if (losses) losses[row] = li;
     }
 }
@@ -61,7 +64,7 @@ __global__ __launch_bounds__(1024) void ce_mean_k(const float* __restrict__ loss
     long long cnt = 0;
     for (int64_t i = threadIdx.x; i < N; i += 1024) {
         acc += static_cast<double>(losses[i]);
-        cnt += (targets[i] != ignore_index) ? 1 : 0;
+        cnt += (!targets || targets[i] != ignore_index) ? 1 : 0;  // no targets: every row (soft targets)
     }
     sd[threadIdx.x] = acc;
     sc[threadIdx.x] = cnt;
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(256) void ce_fwd_bf16v(const bf16* __restrict__ log
         if (lse_out) lse_out[row] = lse;
         const int64_t t = targets[row];
         float li = 0.0f;
-        if (t != ignore_index) li = (t >= 0 && t < C) ? lse - bf2f(z[t]) : NAN;
+        if (t != ignore_index) li = lse - ((t >= 0 && t < C) ? bf2f(z[t]) : 0.0f);
         if (losses) losses[row] = li;
     }
 }
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(256) void ce_fused_bf16v(bf16* logits, int64_t ldl,
     const float lse = M + logf(fmaxf(S, 1e-12f));
     if (threadIdx.x == 0) {
         if (lse_out) lse_out[row] = lse;
-        if (losses) losses[row] = ign ? 0.0f : (tin ? lse - zt : NAN);
+        if (losses) losses[row] = ign ? 0.0f : lse - (tin ? zt : 0.0f);
     }
     const float scale = ign ? 0.0f : rw(row);
     const float l = ign ? 0.0f : lse;
@@ -268,6 +271,50 @@ __global__ __launch_bounds__(256) void ce_fused_bf16v(bf16* logits, int64_t ldl,
         }
         *reinterpret_cast<uint4*>(z + j) = make_uint4(o[0], o[1], o[2], o[3]);
     }
+}
+
+// Soft targets: the row's online log-sum-exp as ce_fwd_k and its dot product with y (block sums).
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(256) void ce_soft_fwd_k(const T* __restrict__ logits, int64_t ldl,
+                                                     const float* __restrict__ y, int64_t ldy, int C,
+                                                     float* __restrict__ losses, float* __restrict__ lse_out) {
+    __shared__ float red[16];
+    const int64_t row = blockIdx.x;
+    const T* z = logits + row * ldl;
+    const float* yr = y + row * ldy;
+    float m = -INFINITY, s = 0.0f, dot = 0.0f;
+    for (int j = threadIdx.x; j < C; j += 256) {
+        const float v = ld(z, j);
+        dot += yr[j] * v;
+        if (v > m) {
+            s = s * ex<PRECISE>(m - v) + 1.0f;
+            m = v;
+        } else {
+            s += ex<PRECISE>(v - m);
+        }
+    }
+    const float M = block_max(m, red);
+    const float part = (m == -INFINITY) ? 0.0f : s * ex<PRECISE>(m - M);
+    const float S = block_sum(part, red);
+    const float D = block_sum(dot, red);
+    if (threadIdx.x == 0) {
+        const float lse = M + logf(fmaxf(S, 1e-12f));
+        if (lse_out) lse_out[row] = lse;
+        if (losses) losses[row] = lse - D;
+    }
+}
+
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(256) void ce_soft_bwd_k(const T* logits, int64_t ldl, const float* __restrict__ y,
+                                                     int64_t ldy, const float* __restrict__ lse, int C, RowWeight rw,
+                                                     T* dl, int64_t ldd) {
+    const int64_t row = blockIdx.x;
+    const T* z = logits + row * ldl;
+    const float* yr = y + row * ldy;
+    T* d = dl + row * ldd;
+    const float scale = rw(row);
+    const float l = lse[row];
+    for (int j = threadIdx.x; j < C; j += 256) st(d, j, (ex<PRECISE>(ld(z, j) - l) - yr[j]) * scale);
 }
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -345,6 +392,55 @@ void ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, const f
     AIC_CHECK(per_row || divisor >= 0.0f, InvalidArgument, "ce_bwd_rows: negative divisor");
     ce_bwd_launch(logits, ld, targets, lse, N, C, ignore_index, RowWeight{grad, nullptr, divisor, per_row ? 1 : 0},
                   dlogits, ld_d, dt, s);
+}
+
+void ce_fwd_soft(const void* logits, int64_t ld, const float* y, int64_t ldy, int64_t N, int64_t C, float* losses,
+                 float* lse, float* loss_mean, DType dt, hipStream_t s) {
+    AIC_CHECK(N >= 0 && C > 0 && ld >= C && ldy >= C && C < (1LL << 31) && N < (1LL << 31), InvalidArgument,
+              "ce_fwd_soft: bad shape");
+    AIC_CHECK(y || N == 0, InvalidArgument, "ce_fwd_soft: targets are required");
+    DeviceBuffer hold;
+    float* lp = losses;
+    if (N > 0 && !lp && loss_mean) {
+        hold = DeviceBuffer(sizeof(float) * N, s);
+        lp = hold.as<float>();
+    }
+    if (N > 0) {
+        const dim3 grid(static_cast<unsigned>(N));
+        if (dt == DType::Float32)
+            hipLaunchKernelGGL((ce_soft_fwd_k<float, true>), grid, dim3(256), 0, s, static_cast<const float*>(logits),
+                               ld, y, ldy, static_cast<int>(C), lp, lse);
+        else if (dt == DType::BFloat16)
+            hipLaunchKernelGGL((ce_soft_fwd_k<bf16, false>), grid, dim3(256), 0, s, static_cast<const bf16*>(logits),
+                               ld, y, ldy, static_cast<int>(C), lp, lse);
+        else
+            AIC_THROW(DTypeMismatch, "ce_fwd_soft: dtype must be f32 or bf16");
+        AIC_LAUNCH_CHECK("ce_soft_fwd");
+    }
+    if (loss_mean) {
+        hipLaunchKernelGGL(ce_mean_k, dim3(1), dim3(1024), 0, s, lp, nullptr, N, int64_t{0}, loss_mean, nullptr);
+        AIC_LAUNCH_CHECK("ce_mean");
+    }
+}
+
+void ce_bwd_soft(const void* logits, int64_t ld, const float* y, int64_t ldy, const float* lse, int64_t N, int64_t C,
+                 const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d, DType dt, hipStream_t s) {
+    AIC_CHECK(N >= 0 && C > 0 && ld >= C && ldy >= C && ld_d >= C && C < (1LL << 31) && N < (1LL << 31),
+              InvalidArgument, "ce_bwd_soft: bad shape");
+    AIC_CHECK((y && lse) || N == 0, InvalidArgument, "ce_bwd_soft: targets and lse are required");
+    AIC_CHECK(per_row || divisor >= 0.0f, InvalidArgument, "ce_bwd_soft: negative divisor");
+    if (N == 0) return;
+    const RowWeight w{grad, nullptr, divisor, per_row ? 1 : 0};
+    const dim3 grid(static_cast<unsigned>(N));
+    if (dt == DType::Float32)
+        hipLaunchKernelGGL((ce_soft_bwd_k<float, true>), grid, dim3(256), 0, s, static_cast<const float*>(logits), ld,
+                           y, ldy, lse, static_cast<int>(C), w, static_cast<float*>(dlogits), ld_d);
+    else if (dt == DType::BFloat16)
+        hipLaunchKernelGGL((ce_soft_bwd_k<bf16, false>), grid, dim3(256), 0, s, static_cast<const bf16*>(logits), ld,
+                           y, ldy, lse, static_cast<int>(C), w, static_cast<bf16*>(dlogits), ld_d);
+    else
+        AIC_THROW(DTypeMismatch, "ce_bwd_soft: dtype must be f32 or bf16");
+    AIC_LAUNCH_CHECK("ce_soft_bwd");
 }
 
 }  // namespace aic::hip

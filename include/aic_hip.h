@@ -198,6 +198,22 @@ int aic_hip_attn_bwd_rope(const void* q, const void* k, const void* v, int64_t l
                           int64_t H, int64_t S, int64_t hd, int causal, float scale, const float* cos_t,
                           const float* sin_t, aic_dtype dt, aic_stream stream);
 
+/* Queries and keys of different lengths (seq_len_q != seq_len_k): q, o, do rows are tokens
+ * b*Sq + s (leading dimensions ld_q, ld_o), k, v rows b*Sk + s (ld_k); dq has leading dimension
+ * ld_dq, dk and dv ld_dkv; lse [B, H, Sq].  Causal as the reference's CPU path: query r sees the
+ * keys c <= r.  fp32 math for F32 and BF16 (any Sq, Sk > 0; Sq == Sk is also accepted; with
+ * Sq == 0 the backward writes zero dk and dv).  head_dim 16, 32, 64 or 128.
+ * Replaces: launch_flash_attention_forward_gpu / launch_flash_attention_backward_gpu with
+ * seq_len_q != seq_len_k (src/cuda/cuda_flash_attention.cuh:12-46; src/ops/flash_attention.cpp:
+ * 32-260 on the CPU). */
+int aic_hip_attn_fwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, void* o, int64_t ld_o,
+                        float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, int causal, float scale,
+                        aic_dtype dt, aic_stream stream);
+int aic_hip_attn_bwd_qk(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_k, const void* o,
+                        const void* dout, int64_t ld_o, const float* lse, void* dq, int64_t ld_dq, void* dk, void* dv,
+                        int64_t ld_dkv, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t hd, int causal,
+                        float scale, aic_dtype dt, aic_stream stream);
+
 /* ---------------------------------------------------------------- SwiGLU ----------- */
 /* h = silu(g) * u, silu(x) = x / (1 + exp(-x)); g, u, h [T, f] with leading dims ld_gu, ld_h.
  * Replaces: silu + mul of SwiGLU::forward (include/nn/swiglu.hpp:21-33). */
@@ -211,7 +227,9 @@ int aic_hip_swiglu_bwd(const void* g, const void* u, int64_t ld_gu, const void* 
 /* ---------------------------------------------------------------- cross-entropy ---- */
 /* Per-row LSE loss with index targets; losses[N], lse[N] (fp32, may be NULL except lse
  * when a backward follows); *loss_mean (device fp32) = sum(losses)/valid, *valid (device
- * int64) = rows with target != ignore_index.  Deterministic.
+ * int64) = rows with target != ignore_index.  Deterministic.  A target outside [0, C) other
+ * than ignore_index is a valid row with loss lse - 0 (and gradient softmax, no one-hot), as the
+ * CUDA launcher computes it (src/cuda/cuda_loss.cu:114-121).
  * Replaces: cuda_cross_entropy_forward (src/cuda/cuda_loss.cuh:17-33). */
 int aic_hip_ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
                    float* losses, float* lse, float* loss_mean, int64_t* valid, aic_dtype dt, aic_stream stream);
@@ -242,6 +260,17 @@ int aic_hip_ce_bwd_rows(const void* logits, int64_t ld, const int64_t* targets, 
 int aic_hip_ce_fwd_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C, int64_t ignore_index,
                        float* losses, float* lse, float* loss_mean, int64_t* valid, const float* grad, aic_dtype dt,
                        aic_stream stream);
+/* Soft (probability) targets y [N, C] fp32 with leading dimension ld_y: losses[i] = lse_i -
+ * sum_j y_ij z_ij, every row valid, *loss_mean = sum(losses) / N (any of losses, lse, loss_mean
+ * may be NULL; lse is needed by the backward).  The backward writes dlogits = (softmax(z) - y) * w_i
+ * with w_i as aic_hip_ce_bwd_rows (per_row, grad, divisor: N for "mean", 1 for "sum").
+ * Replaces: cuda_cross_entropy_forward / cuda_cross_entropy_backward with soft_targets
+ * (src/cuda/cuda_loss.cu:123-131, 177-184; src/loss/cross_entropy.cpp:208-260 on the CPU). */
+int aic_hip_ce_fwd_soft(const void* logits, int64_t ld, const float* y, int64_t ld_y, int64_t N, int64_t C,
+                        float* losses, float* lse, float* loss_mean, aic_dtype dt, aic_stream stream);
+int aic_hip_ce_bwd_soft(const void* logits, int64_t ld, const float* y, int64_t ld_y, const float* lse, int64_t N,
+                        int64_t C, const float* grad, int per_row, float divisor, void* dlogits, int64_t ld_d,
+                        aic_dtype dt, aic_stream stream);
 
 /* ---------------------------------------------------------------- embedding -------- */
 /* out[i,:] = W[ids[i],:] (zero row for ids outside [0, V)); W/out dtype dt.

@@ -351,6 +351,106 @@ void orc_attention_fwd(const float* q, const float* k, const float* v, float* o,
     free(qh); free(kh); free(kt); free(vh); free(oh); free(sc); free(P);
 }
 
+/* Flash attention's CPU forward: per query row, key blocks of 32 with a running max m, sum l
+ * and accumulator rescaled by exp(m_old - m_new); masked scores are -inf and skipped. */
+void orc_flash_fwd(const float* q, const float* k, const float* v, float* o, float* lse, int64_t BH, int64_t Sq,
+                   int64_t Sk, int64_t D, int causal, float scale) {
+    const int64_t Bc = 32;
+    float* acc = (float*)xcalloc((size_t)D, sizeof(float));
+    float sb[32];
+    for (int64_t bh = 0; bh < BH; ++bh) {
+        const float* qb = q + bh * Sq * D;
+        const float* kb = k + bh * Sk * D;
+        const float* vb = v + bh * Sk * D;
+        for (int64_t r = 0; r < Sq; ++r) {
+            const float* qr = qb + r * D;
+            float m = -INFINITY, l = 0.0f;
+            memset(acc, 0, sizeof(float) * (size_t)D);
+            for (int64_t j0 = 0; j0 < Sk; j0 += Bc) {
+                if (causal && j0 > r) break;
+                const int64_t n = (j0 + Bc < Sk ? j0 + Bc : Sk) - j0;
+                float bm = -INFINITY;
+                for (int64_t c = 0; c < n; ++c) {
+                    if (causal && j0 + c > r) {
+                        sb[c] = -INFINITY;
+                        continue;
+                    }
+                    const float* kc = kb + (j0 + c) * D;
+                    float dot = 0.0f;
+                    for (int64_t d = 0; d < D; ++d) dot += qr[d] * kc[d];
+                    dot *= scale;
+                    sb[c] = dot;
+                    if (dot > bm) bm = dot;
+                }
+                if (bm == -INFINITY) continue;
+                const float mn = m > bm ? m : bm;
+                const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
+                for (int64_t d = 0; d < D; ++d) acc[d] *= alpha;
+                float bl = 0.0f;
+                for (int64_t c = 0; c < n; ++c) {
+                    if (!(sb[c] > -1e30f)) continue;
+                    const float p = expf(sb[c] - mn);
+                    bl += p;
+                    const float* vc = vb + (j0 + c) * D;
+                    for (int64_t d = 0; d < D; ++d) acc[d] += p * vc[d];
+                }
+                l = l * alpha + bl;
+                m = mn;
+            }
+            float* orow = o + (bh * Sq + r) * D;
+            if (l > 0.0f) {
+                const float inv = 1.0f / l;
+                for (int64_t d = 0; d < D; ++d) orow[d] = acc[d] * inv;
+                lse[bh * Sq + r] = m + logf(l);
+            } else {
+                memset(orow, 0, sizeof(float) * (size_t)D);
+                lse[bh * Sq + r] = 0.0f;
+            }
+        }
+    }
+    free(acc);
+}
+
+/* Flash attention's CPU backward: D_r = dO_r . O_r; for each visible (r, c): p = exp(s - L_r),
+ * ds = p (dO_r . V_c - D_r) scale, dQ_r += ds K_c, dK_c += ds Q_r, dV_c += p dO_r. */
+void orc_flash_bwd(const float* q, const float* k, const float* v, const float* o, const float* dout,
+                   const float* lse, float* dq, float* dk, float* dv, int64_t BH, int64_t Sq, int64_t Sk, int64_t D,
+                   int causal, float scale) {
+    for (int64_t bh = 0; bh < BH; ++bh) {
+        const float* qb = q + bh * Sq * D;
+        const float* kb = k + bh * Sk * D;
+        const float* vb = v + bh * Sk * D;
+        const float* ob = o + bh * Sq * D;
+        const float* gb = dout + bh * Sq * D;
+        float* dqb = dq + bh * Sq * D;
+        float* dkb = dk + bh * Sk * D;
+        float* dvb = dv + bh * Sk * D;
+        for (int64_t r = 0; r < Sq; ++r) {
+            const float* qr = qb + r * D;
+            const float* gr = gb + r * D;
+            float Dr = 0.0f;
+            for (int64_t d = 0; d < D; ++d) Dr += gr[d] * ob[r * D + d];
+            const float L = lse[bh * Sq + r];
+            const int64_t cmax = causal ? (r + 1 < Sk ? r + 1 : Sk) : Sk;
+            for (int64_t c = 0; c < cmax; ++c) {
+                const float* kc = kb + c * D;
+                const float* vc = vb + c * D;
+                float s = 0.0f, dp = 0.0f;
+                for (int64_t d = 0; d < D; ++d) s += qr[d] * kc[d];
+                s *= scale;
+                const float p = expf(s - L);
+                for (int64_t d = 0; d < D; ++d) dp += gr[d] * vc[d];
+                const float ds = p * (dp - Dr) * scale;
+                for (int64_t d = 0; d < D; ++d) {
+                    dqb[r * D + d] += ds * kc[d];
+                    dkb[c * D + d] += ds * qr[d];
+                    dvb[c * D + d] += p * gr[d];
+                }
+            }
+        }
+    }
+}
+
 /* Backward of the graph above.  For out = e / s (DivBackward then SumBackward then ExpBackward):
  *   t_j = g_j / s ;  c = sum_k(-g_k e_k / (s*s)) in double ;  dscore_j = (t_j + c) * e_j
  * then *scale, and the two MatMulBackwards. */
@@ -508,6 +608,40 @@ void orc_ce_bwd_reduction(const float* logits, const int64_t* targets, const flo
             float ind = (j == t) ? 1.0f : 0.0f;
             gz[j] = (prob - ind) * scale;
         }
+    }
+}
+
+float orc_ce_fwd_soft(const float* logits, const float* y, int64_t N, int64_t C, float* losses, float* lse_out) {
+    double total = 0.0;
+    for (int64_t i = 0; i < N; ++i) {
+        const float* z = logits + i * C;
+        const float* yr = y + i * C;
+        float mx = z[0];
+        for (int64_t j = 1; j < C; ++j)
+            if (z[j] > mx) mx = z[j];
+        double se = 0.0;
+        for (int64_t j = 0; j < C; ++j) se += exp((double)(z[j] - mx));
+        float lse = (float)((double)mx + log(se > 1e-12 ? se : 1e-12));
+        if (lse_out) lse_out[i] = lse;
+        float dot = 0.0f;
+        for (int64_t j = 0; j < C; ++j) dot += yr[j] * z[j];
+        float li = lse - dot;
+        if (losses) losses[i] = li;
+        total += (double)li;
+    }
+    return N > 0 ? (float)total / (float)N : 0.0f;
+}
+
+void orc_ce_bwd_soft(const float* logits, const float* y, const float* lse, int64_t N, int64_t C, const float* g,
+                     int per_row, float divisor, float* dlogits) {
+    for (int64_t i = 0; i < N; ++i) {
+        float scale;
+        if (per_row) scale = g ? g[i] : 1.0f;
+        else scale = divisor > 0.0f ? (g ? g[0] : 1.0f) / divisor : 0.0f;
+        const float* z = logits + i * C;
+        const float* yr = y + i * C;
+        float* gz = dlogits + i * C;
+        for (int64_t j = 0; j < C; ++j) gz[j] = (expf(z[j] - lse[i]) - yr[j]) * scale;
     }
 }
 

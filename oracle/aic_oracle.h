@@ -18,10 +18,14 @@
  *   orc_rope_*            norm preservation + start_pos offset (tests/unit/test_nn.cpp:83-112),
  *                         pos 0 == identity, bwd == inverse rotation, adjoint identity
  *   orc_attention_*       torch scaled_dot_product_attention(is_causal) float64 + autograd
+ *   orc_flash_*           torch SDPA float64 + autograd under the mask of the reference's test
+ *                         (tests/unit/test_flash_attention.cpp:37-60), Sq != Sk both ways,
+ *                         logsumexp, o[0] == v[0], unseen keys get zero gradients
  *   orc_swiglu_*          closed form silu(g)*u + torch autograd float64
  *   orc_ce_*              0.407606 known answer (tests/unit/test_optim.cpp:16-36),
  *                         +-1000 stability (:38-65), ignore_index zero rows (:101-129),
- *                         torch cross_entropy float64 + autograd
+ *                         torch cross_entropy float64 + autograd; soft targets: torch
+ *                         cross_entropy with probabilities, one-hot rows == index targets
  *   orc_embedding_*       gather bit-equal + scatter counts (tests/unit/test_model.cpp:15-48)
  *   orc_adamw             0.989 one-step answer (tests/unit/test_optim.cpp:209-237)
  *                         + torch.optim.AdamW float64
@@ -95,6 +99,16 @@ void orc_attention_bwd(const float* q, const float* k, const float* v, const flo
                        const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t S, int64_t H,
                        int64_t hd);
 
+/* ---- flash attention, CPU path (src/ops/flash_attention.cpp:32-260) ----
+ * q, o [BH, Sq, D], k, v [BH, Sk, D], lse [BH, Sq] (the reference's [B, H, S, D] with BH = B*H).
+ * Online softmax over key blocks of 32; causal: query r sees keys c <= r; a row with no key
+ * gets o = 0 and lse = 0.  The backward accumulates into dq, dk, dv (zero them first). */
+void orc_flash_fwd(const float* q, const float* k, const float* v, float* o, float* lse, int64_t BH, int64_t Sq,
+                   int64_t Sk, int64_t D, int causal, float scale);
+void orc_flash_bwd(const float* q, const float* k, const float* v, const float* o, const float* dout,
+                   const float* lse, float* dq, float* dk, float* dv, int64_t BH, int64_t Sq, int64_t Sk, int64_t D,
+                   int causal, float scale);
+
 /* ---- SwiGLU activation h = silu(g) * u (include/nn/swiglu.hpp:21-33, src/ops/cpu_ops.cpp:143-146) ---- */
 void orc_swiglu_fwd(const float* g, const float* u, float* h, int64_t n);
 /* SiluBackward s*(1+x*(1-s)) (src/autograd/functions.cpp:167-175) and MulBackward. */
@@ -112,6 +126,14 @@ void orc_ce_bwd(const float* logits, const int64_t* targets, const float* lse, i
 enum { ORC_CE_MEAN = 0, ORC_CE_SUM = 1, ORC_CE_NONE = 2 };
 void orc_ce_bwd_reduction(const float* logits, const int64_t* targets, const float* lse, int64_t N, int64_t C,
                           int64_t ignore_index, int reduction, int64_t valid_count, const float* g, float* dlogits);
+
+/* Soft (distribution) targets y [N, C]: losses[i] = lse_i - sum_j y_ij z_ij, every row counted;
+ * returns the "mean" over N (src/loss/cross_entropy.cpp:240-248, 262-270).  The backward writes
+ * (exp(z - lse) - y) * scale_i, scale_i = g[i] when per_row (g NULL: 1), else g[0] / divisor
+ * (src/loss/cross_entropy.cpp:86-105, 120-125). */
+float orc_ce_fwd_soft(const float* logits, const float* y, int64_t N, int64_t C, float* losses, float* lse);
+void orc_ce_bwd_soft(const float* logits, const float* y, const float* lse, int64_t N, int64_t C, const float* g,
+                     int per_row, float divisor, float* dlogits);
 
 /* ---- Embedding (src/nn/embedding.cpp:96-156, :26-82) ---- */
 void orc_embedding_fwd(const int64_t* ids, const float* W, float* out, int64_t N, int64_t D, int64_t V);

@@ -61,6 +61,7 @@ def lib():
             build()
         L = C.CDLL(_LIB_PATH)
         L.orc_ce_fwd.restype = C.c_float
+        L.orc_ce_fwd_soft.restype = C.c_float
         L.orc_clip_grad_norm.restype = C.c_float
         L.orc_lm_loss.restype = C.c_float
         L.orc_lm_num_params.restype = C.c_int64
@@ -223,6 +224,57 @@ def ce_bwd(logits, targets, lse, valid, g=1.0, ignore_index=-100):
 
 
 CE_REDUCTIONS = {"mean": 0, "sum": 1, "none": 2}
+
+
+def flash_fwd(q, k, v, causal=True, scale=None):
+    """orc_flash_fwd on [BH, Sq, D] / [BH, Sk, D] arrays: (o, lse)."""
+    q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    assert k.shape == (BH, Sk, D) and v.shape == k.shape
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    o = np.empty_like(q)
+    lse = np.empty((BH, Sq), np.float32)
+    lib().orc_flash_fwd(_f(q), _f(k), _f(v), _f(o), _f(lse), C.c_int64(BH), C.c_int64(Sq), C.c_int64(Sk),
+                        C.c_int64(D), C.c_int(1 if causal else 0), C.c_float(scale))
+    return o, lse
+
+
+def flash_bwd(q, k, v, o, do, lse, causal=True, scale=None):
+    """orc_flash_bwd: (dq, dk, dv)."""
+    q, k, v, o, do = (np.ascontiguousarray(x, np.float32) for x in (q, k, v, o, do))
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    lib().orc_flash_bwd(_f(q), _f(k), _f(v), _f(o), _f(do), _f(np.ascontiguousarray(lse, np.float32)), _f(dq),
+                        _f(dk), _f(dv), C.c_int64(BH), C.c_int64(Sq), C.c_int64(Sk), C.c_int64(D),
+                        C.c_int(1 if causal else 0), C.c_float(scale))
+    return dq, dk, dv
+
+
+def ce_fwd_soft(logits, y):
+    """orc_ce_fwd_soft: (mean loss, per-row losses, lse) for distribution targets y [N, C]."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    y = np.ascontiguousarray(y, np.float32)
+    N, Cn = logits.shape
+    assert y.shape == logits.shape
+    losses = np.empty(N, np.float32)
+    lse = np.empty(N, np.float32)
+    mean = lib().orc_ce_fwd_soft(_f(logits), _f(y), C.c_int64(N), C.c_int64(Cn), _f(losses), _f(lse))
+    return float(mean), losses, lse
+
+
+def ce_bwd_soft(logits, y, lse, g=None, per_row=False, divisor=1.0):
+    """orc_ce_bwd_soft: (softmax - y) * scale; g None (1), a scalar or per-row values."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    y = np.ascontiguousarray(y, np.float32)
+    N, Cn = logits.shape
+    d = np.empty_like(logits)
+    gp = None if g is None else np.ascontiguousarray(np.atleast_1d(g), np.float32)
+    lib().orc_ce_bwd_soft(_f(logits), _f(y), _f(np.ascontiguousarray(lse, np.float32)), C.c_int64(N), C.c_int64(Cn),
+                          None if gp is None else _f(gp), C.c_int(1 if per_row else 0), C.c_float(divisor), _f(d))
+    return d
 
 
 def ce_bwd_reduction(logits, targets, lse, valid, reduction, g=None, ignore_index=-100):

@@ -271,8 +271,8 @@ def test_cross_entropy(orc, dt, N, Cn):
 def test_cross_entropy_fused(orc, dt, N, Cn):
     """aic_hip_ce_fwd_bwd: equal bit for bit to aic_hip_ce_fwd then aic_hip_ce_bwd in place (row
     widths that take each register-resident variant, one past their limit, odd widths and f32
-    that run the two passes), and to the oracle within the bf16 bound; out-of-range targets give
-    NaN row losses as in aic_hip_ce_fwd."""
+    that run the two passes), and to the oracle within the bf16 bound; out-of-range targets are
+    valid rows of loss lse - 0."""
     rng = np.random.default_rng(N * 7 + Cn)
     z = (3 * rng.standard_normal((N, Cn))).astype(np.float32)
     t = rng.integers(0, Cn, N).astype(np.int64)
@@ -320,15 +320,25 @@ def test_cross_entropy_fused(orc, dt, N, Cn):
         call("aic_hip_ce_fwd_bwd", ptr(z3), Cn, ptr(td), N, Cn, -100, None, None, ptr(mf), ptr(vf), None, dt,
              stream())
         assert rel(host(z3), orc.ce_bwd(z, t, lse_ref, valid_ref, g=1.0)) < (1e-5 if dt == F32 else 4e-3)
-    # a target outside [0, C) gives a NaN row loss (and that row's gradient has no -1 term)
+    # a target outside [0, C) is a valid row of loss lse - 0 whose gradient is the softmax (no -1
+    # term), as the reference's CUDA launcher computes it (cuda_loss.cu:114-121, 170-176)
     if N > 4:
         tb = t.copy()
-        tb[3] = Cn + 5
+        tb[3], tb[4] = Cn + 5, -3
         z4 = dev(z, tdt)
-        call("aic_hip_ce_fwd_bwd", ptr(z4), Cn, ptr(dev(tb)), N, Cn, -100, ptr(lf), None, None, ptr(vf), ptr(g), dt,
-             stream())
-        lo = host(lf)[:N]
-        assert np.isnan(lo[3]) and not np.isnan(np.delete(lo, 3)).any()
+        s4 = torch.empty(N, dtype=torch.float32, device="cuda")
+        call("aic_hip_ce_fwd_bwd", ptr(z4), Cn, ptr(dev(tb)), N, Cn, -100, ptr(lf), ptr(s4), ptr(mf), ptr(vf), ptr(g),
+             dt, stream())
+        lo, s4h = host(lf)[:N], host(s4)
+        np.testing.assert_array_equal(lo[[3, 4]], s4h[[3, 4]])
+        assert int(host(vf)[0]) == valid_ref + (t[3] == -100) + (t[4] == -100)
+        inr = np.where((tb >= 0) & (tb < Cn), tb, 0)
+        losses_ref = orc.ce_fwd(z, inr)[1]
+        keep = (tb != -100) & (tb >= 0) & (tb < Cn)
+        assert rel(lo[keep], losses_ref[keep]) < 1e-6
+        valid4 = int(host(vf)[0])
+        soft = np.exp(z[[3, 4]].astype(np.float64) - lse_ref[[3, 4], None]) * 2.5 / valid4
+        assert rel(host(z4)[[3, 4]], soft) < (1e-5 if dt == F32 else 4e-3)
 
 
 @pytest.mark.parametrize("dt", [F32, BF16])

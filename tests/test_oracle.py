@@ -151,6 +151,35 @@ def test_attention_vs_sdpa(orc, B, S, H, hd):
     assert rel(dv, vt.grad.transpose(1, 2).reshape(B * S, H * hd).numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("BH,Sq,Sk,D,causal", [(3, 5, 70, 16, True), (2, 70, 33, 32, True), (2, 40, 40, 8, True),
+                                                (3, 7, 45, 16, False), (1, 65, 9, 8, False)])
+def test_flash_attention_vs_masked_sdpa(orc, BH, Sq, Sk, D, causal):
+    """The flash-attention CPU path (src/ops/flash_attention.cpp:32-260) with queries and keys of
+    different lengths against torch float64 SDPA + autograd under the mask of the reference's own
+    test (tests/unit/test_flash_attention.cpp:37-60: key j hidden from query i when j > i)."""
+    rng = np.random.default_rng(BH * 1000 + Sq * 10 + Sk)
+    q, do = (rng.standard_normal((BH, Sq, D)).astype(np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((BH, Sk, D)).astype(np.float32) for _ in range(2))
+    qt, kt, vt = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (q, k, v))
+    mask = torch.ones(Sq, Sk, dtype=torch.bool).tril() if causal else None
+    ot = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask)
+    ot.backward(torch.tensor(do, dtype=torch.float64))
+    o, lse = orc.flash_fwd(q, k, v, causal)
+    assert rel(o, ot.detach().numpy()) < 1e-5
+    s = torch.tensor(q, dtype=torch.float64) @ torch.tensor(k, dtype=torch.float64).transpose(1, 2) / np.sqrt(D)
+    if causal:
+        s = s.masked_fill(~mask, -np.inf)
+    assert np.max(np.abs(lse - torch.logsumexp(s, -1).numpy())) < 1e-5
+    dq, dk, dv = orc.flash_bwd(q, k, v, o, do, lse, causal)
+    assert rel(dq, qt.grad.numpy()) < 1e-5
+    assert rel(dk, kt.grad.numpy()) < 1e-5
+    assert rel(dv, vt.grad.numpy()) < 1e-5
+    if causal:
+        np.testing.assert_array_equal(o[:, 0], v[:, 0])  # query 0 sees key 0 only
+        if Sk > Sq:
+            assert np.all(dk[:, Sq:] == 0) and np.all(dv[:, Sq:] == 0)  # keys no query sees
+
+
 def test_attention_first_row_copies_v(orc):
     # causal: query 0 sees only key 0, so o[0] == v[0] exactly
     rng = np.random.default_rng(5)
@@ -235,6 +264,37 @@ def test_ce_reductions_vs_torch(orc, reduction):
     if reduction == "none":
         ones = orc.ce_bwd_reduction(z, t, lse, valid, "none")
         assert rel(ones, orc.ce_bwd(z, t, lse, valid, g=float(valid))) < 1e-6
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_ce_soft_targets_vs_torch(orc, reduction):
+    """Distribution targets (src/loss/cross_entropy.cpp:240-248, 120-125) against torch float64
+    autograd of F.cross_entropy with probability targets; one-hot distributions reduce to the
+    index-target loss and gradient."""
+    rng = np.random.default_rng(13)
+    N, Cn = 29, 61
+    z = (2 * rng.standard_normal((N, Cn))).astype(np.float32)
+    y = rng.random((N, Cn)).astype(np.float32)
+    y /= y.sum(1, keepdims=True)
+    zt = torch.tensor(z, dtype=torch.float64, requires_grad=True)
+    lt = F.cross_entropy(zt, torch.tensor(y, dtype=torch.float64), reduction=reduction)
+    g = rng.standard_normal(N).astype(np.float32) if reduction == "none" else np.float32(0.75)
+    lt.backward(torch.tensor(g, dtype=torch.float64))
+    mean, losses, lse = orc.ce_fwd_soft(z, y)
+    assert rel(losses, F.cross_entropy(torch.tensor(z, dtype=torch.float64), torch.tensor(y, dtype=torch.float64),
+                                       reduction="none").numpy()) < 1e-6
+    assert abs(mean - losses.astype(np.float64).mean()) < 1e-6 * abs(mean)
+    per_row = reduction == "none"
+    d = orc.ce_bwd_soft(z, y, lse, g, per_row=per_row, divisor=float(N) if reduction == "mean" else 1.0)
+    assert rel(d, zt.grad.numpy()) < 1e-6
+    # one-hot rows: the same numbers as index targets
+    t = rng.integers(0, Cn, N)
+    oh = np.eye(Cn, dtype=np.float32)[t]
+    m1, l1, s1 = orc.ce_fwd_soft(z, oh)
+    m0, l0, s0, valid = orc.ce_fwd(z, t)
+    np.testing.assert_array_equal(l1, l0)
+    np.testing.assert_array_equal(s1, s0)
+    np.testing.assert_array_equal(orc.ce_bwd_soft(z, oh, s1, 1.0, divisor=float(N)), orc.ce_bwd(z, t, s0, valid))
 
 
 # --------------------------------------------------------------------------- embedding
