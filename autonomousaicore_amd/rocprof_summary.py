@@ -5,6 +5,10 @@
          --copy-probe-mib 1024] [--steps N]
     python -m autonomousaicore_amd.rocprof_summary --pmc DIR1/run_counter_collection.csv \
         [DIR2/run_counter_collection.csv ...]
+    python -m autonomousaicore_amd.rocprof_summary --bench BENCH_JSON_LINE_FILE
+
+--bench prints the per-class roofline table of a bench.py JSON line (its `kernel_classes`:
+event-timed launches, achieved TFLOP/s or GB/s against the MI355X peak, fraction).
 
 Kernel symbols map to the same classes as the library's event profiler (the class a launch
 is timed under inside TransformerLM::train_step), so the per-class average launch time here
@@ -41,10 +45,11 @@ _RULES = [
     # gemm_bf16_dma_q4<BM, BN, BK, STAGES, transB, C>: the INT4-operand forward / input gradient
     (r"gemm_bf16_dma_q4(<(\d+, )+true|I(Li\d+E)+Lb1E)", "gemm_fwd"),
     (r"gemm_bf16_dma_q4(<(\d+, )+false|I(Li\d+E)+Lb0E)", "gemm_dgrad"),
-    # gemm_bf16_dma[_grouped|_ragged]<BM, BN, BK, STAGES, transA, transB, C>, demangled or mangled
-    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
-    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
-    (r"gemm_bf16_dma(_grouped|_ragged)?(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
+    # gemm_bf16_dma[_grouped|_ragged|_pers]<BM, BN, BK, STAGES, transA, transB, C, ...>, demangled
+    # or mangled
+    (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
+    (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
     (r"attn_fwd", "attn_fwd"),
     (r"attn_bwd|attn_dot", "attn_bwd"),
     (r"rmsnorm_fwd", "rmsnorm_fwd"),
@@ -166,6 +171,30 @@ def pmc_summary(paths, cus, xcds):
         print("    " + ", ".join(f"{c}={v:.4g}" for c, v in sorted(a.items())))
 
 
+def bench_summary(path):
+    """The kernel_classes table of the last bench.py JSON line in a file."""
+    import json
+
+    line = None
+    with open(path) as f:
+        for ln in f:
+            ln = ln.strip()
+            if ln.startswith("{") and '"kernel_classes"' in ln:
+                line = ln
+    if line is None:
+        raise SystemExit(f"{path}: no bench.py JSON line")
+    b = json.loads(line)
+    print(f"# bench.py: {b['value'] / 1e3:.1f} k tokens/s, {b['ms_per_step']:.2f} ms/step, "
+          f"{100 * b['mfma_peak_frac_step']:.1f}% of the bf16 peak over the step ({b['steps']} timed steps)")
+    print("# per-class roofline (bench.py kernel_classes: HIP events on every class; MFMA classes against "
+          "2500 TFLOP/s, HBM classes against 8000 GB/s)")
+    print(f"{'class':<13} {'bound':>5} {'launches':>8} {'avg_ms':>8} {'ms/step':>8} {'achieved':>13} {'frac':>6}")
+    for name, k in sorted(b["kernel_classes"].items(), key=lambda kv: -kv[1]["ms_per_step"]):
+        unit = "TFLOP/s" if k["unit"] == "TFLOP/s" else "GB/s"
+        print(f"{name:<13} {k['bound']:>5} {k['launches']:>8} {k['avg_ms']:>8.4f} {k['ms_per_step']:>8.3f} "
+              f"{k['achieved']:>7.1f} {unit:<5} {k['frac']:>6.3f}")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--stats")
@@ -176,7 +205,13 @@ def main(argv=None):
     ap.add_argument("--write")
     ap.add_argument("--copy-probe-mib", type=int, default=0)
     ap.add_argument("--steps", type=int, default=0, help="train steps in the profiled run (for ms/step)")
+    ap.add_argument("--bench", help="a file holding bench.py's JSON line")
     args = ap.parse_args(argv)
+    if args.bench:
+        bench_summary(args.bench)
+        if not (args.stats or args.pmc):
+            return
+        print()
     if args.pmc:
         pmc_summary(args.pmc, args.cus, args.xcds)
         if not args.stats:
