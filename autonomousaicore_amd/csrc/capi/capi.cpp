@@ -314,6 +314,36 @@ int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t 
     });
 }
 
+int aic_hip_lora_skinny(const void* Y, int64_t ldy, int64_t T, int64_t N, int64_t n_seg, int64_t r_seg, const void* W,
+                        int64_t w_n, int64_t w_j, void* out1, int64_t ldo1, float scale, const void* Z, int64_t ldz,
+                        float* out2, int64_t o2n, int64_t o2j, int accumulate, aic_stream stream) {
+    return guard([&] {
+        aic::hip::LoraSkinny q;
+        q.Y = Y;
+        q.ldy = ldy;
+        q.T = T;
+        q.N = N;
+        q.n_seg = n_seg;
+        q.r_seg = r_seg;
+        q.W = W;
+        q.w_n = w_n;
+        q.w_j = w_j;
+        q.out1 = out1;
+        q.ldo1 = ldo1;
+        q.scale = scale;
+        q.Z = Z;
+        q.ldz = ldz;
+        q.out2 = out2;
+        q.o2n = o2n;
+        q.o2j = o2j;
+        q.accumulate = accumulate != 0;
+        AIC_CHECK(T >= 0 && N >= 0, InvalidArgument, "lora_skinny: negative size");
+        if (T == 0 || N == 0) return;
+        AIC_CHECK(aic::hip::lora_skinny_ok(q), NotImplemented, "lora_skinny: shape or layout outside the kernel's forms");
+        aic::hip::lora_skinny(q, st(stream));
+    });
+}
+
 int aic_hip_gemm_swiglu_bwd(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* B, int64_t ldb,
                             const void* GU, int64_t ldgu, void* DH, int64_t lddh, void* DGU, aic_stream stream) {
     return guard([&] {

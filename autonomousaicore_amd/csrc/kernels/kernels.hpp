@@ -168,4 +168,30 @@ void step_record(const float* loss, const float* aux, const void* ctl, const flo
 void fill_normal(float* dst, int64_t n, uint64_t seed, uint64_t offset, float mean, float std, hipStream_t s);
 void fill_const(float* dst, int64_t n, float v, hipStream_t s);
 
+// LoRA adapter products in one pass over a bf16 operand Y [T, N] (leading dimension ldy) whose
+// columns form N / n_seg segments of n_seg columns (n_seg % 256 == 0), each paired with r_seg
+// (16, 32 or 48) columns of the small operands:
+//   out1[t, g r_seg + j] = bf16(scale * sum_{n in segment g} Y[t, n] W(n, j))   when out1
+//   out2(n, j) (+)= sum_t Y[t, n] Z[t, g(n) r_seg + j]                          when out2
+// W(n, j) = W[n w_n + j w_j] with w_j == 1 (rows of j, w_n % 8 == 0) or w_n == 1 (rows of n,
+// w_j % 8 == 0); out1 [T, ldo1] bf16; Z [T, ldz] bf16; out2 fp32 at out2 + n o2n + j o2j,
+// overwritten or added to (accumulate).  All bf16 pointers 16-byte aligned, ld % 8 == 0.
+// Deterministic: partial sums in a fixed order, no atomics.
+struct LoraSkinny {
+    const void* Y = nullptr;
+    int64_t ldy = 0, T = 0, N = 0, n_seg = 0, r_seg = 0;
+    const void* W = nullptr;
+    int64_t w_n = 0, w_j = 0;
+    void* out1 = nullptr;
+    int64_t ldo1 = 0;
+    float scale = 1.0f;
+    const void* Z = nullptr;
+    int64_t ldz = 0;
+    float* out2 = nullptr;
+    int64_t o2n = 0, o2j = 0;
+    bool accumulate = false;
+};
+bool lora_skinny_ok(const LoraSkinny& q);  // the shapes and layouts the kernel takes
+void lora_skinny(const LoraSkinny& q, hipStream_t s);
+
 }  // namespace aic::hip

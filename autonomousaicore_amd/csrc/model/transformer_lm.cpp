@@ -871,6 +871,34 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
     };
     // the frozen model's gradients are not formed with QLoRA
     auto GB = [&](int64_t off) -> float* { return ql ? nullptr : G(off); };
+    // LoRA's rank-r products (LoRALinear, src/nn/lora.cpp:75-93) in one pass over the large
+    // operand where the kernel takes the shape (bf16, widths % 256), else as GEMMs
+    auto lora_pass = [&](const hip::LoraSkinny& q, double flops) {
+        if (dt != DType::BFloat16 || !hip::lora_skinny_ok(q)) return false;
+        const double big = es * static_cast<double>(q.T) * q.N;  // the operand the pass streams
+        const double small = es * static_cast<double>(q.T) * (q.N / q.n_seg) * q.r_seg;
+        auto _p = prof_.scope(kLora, flops, big + (q.out1 ? small : 0.0) + (q.Z ? small : 0.0), s);
+        hip::lora_skinny(q, s);
+        return true;
+    };
+    // xs = s x A^T, A [R, in] (the adapters' A of a projection stack, stacked)
+    auto lora_xa = [&](const void* x, int64_t in, int64_t a_off, int64_t R, void* out) {
+        hip::LoraSkinny q;
+        q.Y = x;
+        q.ldy = in;
+        q.T = T;
+        q.N = in;
+        q.n_seg = in;
+        q.r_seg = R;
+        q.W = W(a_off);
+        q.w_n = 1;
+        q.w_j = in;
+        q.out1 = out;
+        q.ldo1 = R;
+        q.scale = lsc;
+        if (!lora_pass(q, 2.0 * T * in * R))
+            gemm(prof_, 0, 1, T, R, in, x, in, W(a_off), in, out, R, dt, dt, s, nullptr, 0, 0.0f, lsc);
+    };
 
     // ---- forward (TransformerLM::forward, src/models/transformer_lm.cpp:50-62) ----
     {
@@ -897,7 +925,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         // output column block (q, k, v) with its own r columns of xs and its own B
         LowRank lq{};
         if (ql) {
-            gemm(prof_, 0, 1, T, 3 * r, d, h1l, d, W(ly.aqkv), d, xaq(l), 3 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lora_xa(h1l, d, ly.aqkv, 3 * r, xaq(l));
             lq = LowRank{xaq(l), 3 * r, W(ly.bq), r, r, d, 0};
         }
         // q and k leave the projection rotated (RotaryPositionEmbedding::forward in the GEMM's
@@ -911,7 +939,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         }
         LowRank lo_{};
         if (ql) {
-            gemm(prof_, 0, 1, T, r, d, ol, d, W(ly.ao), d, xao(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lora_xa(ol, d, ly.ao, r, xao(l));
             lo_ = LowRank{xao(l), r, W(ly.bo), r, r, 0, 0};
         }
         gemm(prof_, 0, 1, T, d, d, ol, d, wbase(ly, ly.wo, 3, 3), d, x1l, d, dt, dt, s, x, d, 0.0f, 1.0f,
@@ -927,7 +955,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         }
         LowRank lg{};
         if (ql) {
-            gemm(prof_, 0, 1, T, 2 * r, d, h2l, d, W(ly.agu), d, xagu(l), 2 * r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lora_xa(h2l, d, ly.agu, 2 * r, xagu(l));
             lg = LowRank{xagu(l), 2 * r, W(ly.bg), r, r, f, 0};
         }
         // gate/up, with SwiGLU's silu(gate) * up written by the GEMM's epilogue where its shape
@@ -936,7 +964,7 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
              1.0f, ql ? &lg : nullptr, wq(ly, 4), RopeOut{}, GluOut{aml, f, f});
         LowRank ld_{};
         if (ql) {
-            gemm(prof_, 0, 1, T, r, f, aml, f, W(ly.ad), f, xad(l), r, dt, dt, s, nullptr, 0, 0.0f, lsc);
+            lora_xa(aml, f, ly.ad, r, xad(l));
             ld_ = LowRank{xad(l), r, W(ly.bd), r, r, 0, 0};
         }
         gemm(prof_, 0, 1, T, d, f, aml, f, wbase(ly, ly.wd, 6, 6), f, xn, d, dt, dt, s, x1l, d, 0.0f, 1.0f,
@@ -987,6 +1015,53 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                           void* dxa_out, int64_t lddxa) {
         gemm(prof_, 1, 0, n_out, r, T, dy, lddy, xs, ldxs, G(boff), r, dt, DType::Float32, s);
         gemm(prof_, 0, 0, T, r, n_out, dy, lddy, W(boff), r, dxa_out, lddxa, dt, dt, s, nullptr, 0, 0.0f, lsc);
+    };
+    // The same for a stack of nb projections whose outputs are the n_out-column blocks of dy
+    // [T, nb n_out] and whose B's are stacked in the arena (boffs[j] = boffs[0] + j n_out r):
+    // dB and dxa of all of them from one pass over dy
+    auto lora_bwd = [&](const void* dy, int64_t n_out, int nb, const void* xs, const int64_t* boffs, void* dxa_out) {
+        bool stacked = true;
+        for (int j = 1; j < nb; ++j) stacked = stacked && boffs[j] == boffs[0] + j * n_out * r;
+        hip::LoraSkinny q;
+        q.Y = dy;
+        q.ldy = nb * n_out;
+        q.T = T;
+        q.N = nb * n_out;
+        q.n_seg = n_out;
+        q.r_seg = r;
+        q.W = W(boffs[0]);
+        q.w_n = r;
+        q.w_j = 1;
+        q.out1 = dxa_out;
+        q.ldo1 = nb * r;
+        q.scale = lsc;
+        q.Z = xs;
+        q.ldz = nb * r;
+        q.out2 = G(boffs[0]);
+        q.o2n = r;
+        q.o2j = 1;
+        if (stacked && lora_pass(q, 4.0 * T * nb * n_out * r)) return;
+        for (int j = 0; j < nb; ++j)
+            lora_b_bwd(static_cast<const char*>(dy) + es * j * n_out, nb * n_out, n_out,
+                       static_cast<const char*>(xs) + es * j * r, nb * r, boffs[j],
+                       static_cast<char*>(dxa_out) + es * j * r, nb * r);
+    };
+    // dA = dxa^T x for A [R, in] (stacked A's of a projection stack)
+    auto lora_da = [&](const void* x, int64_t in, const void* dxa_in, int64_t R, int64_t a_off) {
+        hip::LoraSkinny q;
+        q.Y = x;
+        q.ldy = in;
+        q.T = T;
+        q.N = in;
+        q.n_seg = in;
+        q.r_seg = R;
+        q.Z = dxa_in;
+        q.ldz = R;
+        q.out2 = G(a_off);
+        q.o2n = 1;
+        q.o2j = in;
+        if (!lora_pass(q, 2.0 * T * in * R))
+            gemm(prof_, 1, 0, R, in, T, dxa_in, R, x, in, G(a_off), in, dt, DType::Float32, s);
     };
     // the gradient norm's partial sums, where the step forms it from the producers (sq_fold)
     const bool fold = sq_fold_ && sq_fold_on_;
@@ -1046,8 +1121,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
             // x_{l+1} = x1 + down(silu(gate(h2)) * up(h2))
             LowRank ld_{};
             if (ql) {
-                lora_b_bwd(dx.get(), d, d, xad(l), r, ly.bd, dxa.get(), r);
-                gemm(prof_, 1, 0, r, f, T, dxa.get(), r, aml, f, G(ly.ad), f, dt, DType::Float32, s);
+                lora_bwd(dx.get(), d, 1, xad(l), &ly.bd, dxa.get());
+                lora_da(aml, f, dxa.get(), r, ly.ad);
                 ld_ = LowRank{dxa.get(), r, W(ly.ad), f, r, 0, 1};
             }  // else: the down-projection weight gradient joins the layer's grouped launch below
             // da = dx W_d goes straight into SwiGLU's backward in the GEMM's epilogue (dgu from da
@@ -1056,11 +1131,9 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
                  0.0f, 1.0f, ql ? &ld_ : nullptr, wq(ly, 6), RopeOut{}, GluOut{}, DGlu{gul, dgu.get(), 2 * f});
             LowRank lg{};
             if (ql) {
-                void* xa = xagu(l);
-                lora_b_bwd(dgu.get(), 2 * f, f, xa, 2 * r, ly.bg, dxa.get(), 2 * r);
-                lora_b_bwd(static_cast<char*>(dgu.get()) + es * f, 2 * f, f, static_cast<char*>(xa) + es * r, 2 * r,
-                           ly.bu, static_cast<char*>(dxa.get()) + es * r, 2 * r);
-                gemm(prof_, 1, 0, 2 * r, d, T, dxa.get(), 2 * r, h2l, d, G(ly.agu), d, dt, DType::Float32, s);
+                const int64_t bs[2] = {ly.bg, ly.bu};
+                lora_bwd(dgu.get(), f, 2, xagu(l), bs, dxa.get());
+                lora_da(h2l, d, dxa.get(), 2 * r, ly.agu);
                 lg = LowRank{dxa.get(), 2 * r, W(ly.agu), d, 2 * r, 0, 1};
             }  // else: the gate/up weight gradient joins the layer's grouped launch below (dgu is
                // not written again before it)
@@ -1074,8 +1147,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         // x1 = x + out_proj(attn(rope(q), rope(k), v))
         LowRank lo_{};
         if (ql) {
-            lora_b_bwd(dxm.get(), d, d, xao(l), r, ly.bo, dxa.get(), r);
-            gemm(prof_, 1, 0, r, d, T, dxa.get(), r, ol, d, G(ly.ao), d, dt, DType::Float32, s);
+            lora_bwd(dxm.get(), d, 1, xao(l), &ly.bo, dxa.get());
+            lora_da(ol, d, dxa.get(), r, ly.ao);
             lo_ = LowRank{dxa.get(), r, W(ly.ao), d, r, 0, 1};
         }  // else: the out_proj weight gradient joins the layer's grouped launch below
         gemm(prof_, 0, 0, T, d, d, dxm.get(), d, wbase(ly, ly.wo, 3, 3), d, dh.get(), d, dt, dt, s, nullptr, 0, 0.0f,
@@ -1092,11 +1165,8 @@ void TransformerLM::forward_backward(const int64_t* ids, const int64_t* targets,
         LowRank lq{};
         if (ql) {
             const int64_t bs[3] = {ly.bq, ly.bk, ly.bv};
-            for (int j = 0; j < 3; ++j)
-                lora_b_bwd(static_cast<char*>(dqkv.get()) + es * j * d, 3 * d, d,
-                           static_cast<char*>(xaq(l)) + es * j * r, 3 * r, bs[j],
-                           static_cast<char*>(dxa.get()) + es * j * r, 3 * r);
-            gemm(prof_, 1, 0, 3 * r, d, T, dxa.get(), 3 * r, h1l, d, G(ly.aqkv), d, dt, DType::Float32, s);
+            lora_bwd(dqkv.get(), d, 3, xaq(l), bs, dxa.get());
+            lora_da(h1l, d, dxa.get(), 3 * r, ly.aqkv);
             lq = LowRank{dxa.get(), 3 * r, W(ly.aqkv), d, 3 * r, 0, 1};
         } else if (moe) {
             // dWqkv = dqkv^T h1 and dWo = dxm^T o in one launch

@@ -10,9 +10,9 @@ namespace {
 const char* kNames[kNumKernelClasses] = {"gemm_fwd",   "gemm_dgrad", "gemm_wgrad", "attn_fwd",   "attn_bwd",
                                           "rmsnorm_fwd", "rmsnorm_bwd", "rope",      "swiglu_fwd", "swiglu_bwd",
                                           "ce_fwd",     "ce_bwd",     "ce_fwd_bwd", "embed_fwd",  "embed_bwd",
-                                          "grad_norm",  "adamw"};
+                                          "grad_norm",  "adamw",      "lora"};
 const bool kMfma[kNumKernelClasses] = {true,  true,  true,  true,  true,  false, false, false, false,
-                                       false, false, false, false, false, false, false, false};
+                                       false, false, false, false, false, false, false, false, false};
 }  // namespace
 
 int Profiler::class_index(const char* name) {

@@ -28,6 +28,7 @@ enum KernelClass : int {
     kEmbedBwd,
     kGradNorm,
     kAdamW,
+    kLora,         // LoRA adapter products (one pass over the large operand; HBM-bound)
     kNumKernelClasses
 };
 

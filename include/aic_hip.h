@@ -126,6 +126,22 @@ int aic_hip_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* A, int64_t 
 int aic_hip_gemm_swiglu_bwd(int64_t M, int64_t f, int64_t K, const void* A, int64_t lda, const void* B, int64_t ldb,
                             const void* GU, int64_t ldgu, void* DH, int64_t lddh, void* DGU, aic_stream stream);
 
+/* LoRA adapter products in one pass over a bf16 operand Y [T, N] (leading dimension ldy) whose
+ * columns form N / n_seg segments of n_seg columns (n_seg % 256 == 0), segment g paired with
+ * columns [g r_seg, (g+1) r_seg) of the small operands (r_seg 16, 32 or 48):
+ *   out1[t, g r_seg + j] = bf16(scale * sum_{n in segment g} Y[t, n] W(n, j))  (out1 non-NULL)
+ *   out2(n, j) (+)= sum_t Y[t, n] Z[t, g(n) r_seg + j]                         (out2 non-NULL)
+ * W(n, j) = W[n w_n + j w_j] with w_j == 1 (B [out, r] rows) or w_n == 1 (A [r, in] rows);
+ * out1 bf16 [T, ldo1]; Z bf16 [T, ldz]; out2 fp32 at out2 + n o2n + j o2j, overwritten or added
+ * to (accumulate).  bf16 pointers 16-byte aligned, leading dimensions % 8 == 0.  Deterministic.
+ * Other shapes return NotImplemented (the caller runs GEMMs instead).
+ * Replaces (no single reference launcher): the rank-r matmuls of LoRALinear::forward and their
+ * autograd gradients (src/nn/lora.cpp:75-93; MatMulBackward, src/autograd/functions.cpp:254-273):
+ * x A^T (out1 with W = A), dy^T xs and dy B (out2 and out1 in one pass over dy), dxa^T x (out2). */
+int aic_hip_lora_skinny(const void* Y, int64_t ldy, int64_t T, int64_t N, int64_t n_seg, int64_t r_seg, const void* W,
+                        int64_t w_n, int64_t w_j, void* out1, int64_t ldo1, float scale, const void* Z, int64_t ldz,
+                        float* out2, int64_t o2n, int64_t o2j, int accumulate, aic_stream stream);
+
 /* Several independent products in one launch (for example every expert's projection of an MoE
  * layer, or two weight gradients whose tiles together fill the chip once).  They must share
  * transA, transB, the dtypes, alpha and beta, and take the MFMA path (bf16, 16-byte aligned

@@ -456,7 +456,11 @@ def test_qlora_1b_widths_step_matches_oracle(orc):
     grads = model.get_grads()
     res, g_ref, _, _, _ = orc.qlora_step(oracle_cfg(orc, c, L=2), c["r"], c["alpha"], c["G"], base, lora.copy(),
                                          ids, tgt, 1, S)
-    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3.5e-2, norm_tol=5e-5, tag="qlora-widths B1xS2048")
+    # the norm's relative error is second order in the per-element bf16 noise (about half the
+    # squared relative error of the dominant gradient tensors, 1.5e-2 here, so up to ~1.2e-4);
+    # observed 1.8e-5 with GEMM adapter products and 5.2e-5 with the one-pass ones (another,
+    # equally exact summation order)
+    check_step_vs_oracle(st, res, grads, g_ref, model, grad_tol=3.5e-2, norm_tol=1.2e-4, tag="qlora-widths B1xS2048")
     model.close()
 
 
