@@ -175,7 +175,8 @@ void fill_const(float* dst, int64_t n, float v, hipStream_t s);
 //   out2(n, j) (+)= sum_t Y[t, n] Z[t, g(n) r_seg + j]                          when out2
 // W(n, j) = W[n w_n + j w_j] with w_j == 1 (rows of j, w_n % 8 == 0) or w_n == 1 (rows of n,
 // w_j % 8 == 0); out1 [T, ldo1] bf16; Z [T, ldz] bf16; out2 fp32 at out2 + n o2n + j o2j,
-// overwritten or added to (accumulate).  All bf16 pointers 16-byte aligned, ld % 8 == 0.
+// overwritten or added to (accumulate).  bf16 inputs 16-byte aligned with ld % 8 == 0; out1
+// 8-byte aligned with ldo1 % 4 == 0.
 // Deterministic: partial sums in a fixed order, no atomics.
 struct LoraSkinny {
     const void* Y = nullptr;

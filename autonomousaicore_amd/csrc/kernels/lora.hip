@@ -262,30 +262,103 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_k(SkinnyParams p) {
     }
 }
 
-// Fixed-order sums of the partials.  Threads [0, n1): out1[t, g r_seg + j] = bf16(scale *
-// sum over the column groups of segment g); threads [n1, n1 + n2): out2(n, j) = sum over the
-// row blocks.
+// The forward product alone (out1 = bf16(scale * Y W), one segment, W(n, j) = W[j w_j + n]: the
+// adapters' A [R, in]) without partial sums: a block owns 16 rows of Y and the whole width; wave
+// w takes the 256-column chunks w, w + 4, ...  Both MFMA operands come straight from global
+// memory in fragment layout -- a lane's 16 bytes of a Y row are one aligned quarter of a 64-byte
+// segment that the 16 lanes of its row group read together, A's from L2 -- so nothing is staged
+// in LDS; the four waves' partial tiles are added in LDS in wave order at the end.
+template <int RB>
+__global__ __launch_bounds__(256) void lora_xa_k(SkinnyParams p) {
+    constexpr int R = 16 * RB;
+    __shared__ float red[4][16][R];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, i = lane & 15;
+    const int t0 = blockIdx.x * 16;
+    const bool row_ok = t0 + i < p.T;
+    const bf16* yrow = p.Y + (int64_t)(row_ok ? t0 + i : 0) * p.ldy + 8 * g;
+    const bf16* wcol[RB];
+#pragma unroll
+    for (int cb = 0; cb < RB; ++cb) wcol[cb] = p.W + (int64_t)(16 * cb + i) * p.w_j + 8 * g;
+    f32x4 acc[RB];
+#pragma unroll
+    for (int cb = 0; cb < RB; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int chunks = p.N / kChunk;
+    for (int c = w; c < chunks; c += 4) {
+        const int n0 = c * kChunk;
+        bf16x8 a[8], b[8][RB];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            a[ks] = row_ok ? *reinterpret_cast<const bf16x8*>(yrow + n0 + 32 * ks) : bf16x8{};
+#pragma unroll
+            for (int cb = 0; cb < RB; ++cb) b[ks][cb] = *reinterpret_cast<const bf16x8*>(wcol[cb] + n0 + 32 * ks);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+            for (int cb = 0; cb < RB; ++cb) acc[cb] = mfma16(a[ks], b[ks][cb], acc[cb]);
+    }
+    // D of a 16x16 tile: lane (g, i) holds rows 4 g + v, column i
+#pragma unroll
+    for (int cb = 0; cb < RB; ++cb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[w][4 * g + v][16 * cb + i] = acc[cb][v];
+    __syncthreads();
+    for (int e = tid; e < 16 * R; e += 256) {
+        const int row = e / R, j = e % R;
+        if (t0 + row < p.T) {
+            const float sum = ((red[0][row][j] + red[1][row][j]) + red[2][row][j]) + red[3][row][j];
+            p.out1[(int64_t)(t0 + row) * p.ldo1 + j] = f2bf(p.scale * sum);
+        }
+    }
+}
+
+// Fixed-order sums of the partials, four consecutive j per thread (r_seg % 16 == 0).  Threads
+// [0, n1): out1[t, g r_seg + j] = bf16(scale * sum over the column groups of segment g); threads
+// [n1, n1 + n2): out2(n, j) = sum over the row blocks.
 __global__ __launch_bounds__(256) void lora_reduce_k(SkinnyParams p, int groups_per_seg, int segs, int row_blocks) {
-    const int64_t n1 = p.p1 ? (int64_t)p.T * segs * p.r_seg : 0;
-    const int64_t n2 = p.p2 ? (int64_t)p.N * p.r_seg : 0;
+    const int q4 = p.r_seg / 4;
+    const int64_t n1 = p.p1 ? (int64_t)p.T * segs * q4 : 0;
+    const int64_t n2 = p.p2 ? (int64_t)p.N * q4 : 0;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx < n1) {
-        const int j = idx % p.r_seg;
-        const int64_t rest = idx / p.r_seg;
+        const int j = 4 * (idx % q4);
+        const int64_t rest = idx / q4;
         const int sg = rest % segs;
         const int64_t t = rest / segs;
-        float acc = 0.0f;
-        for (int q = 0; q < groups_per_seg; ++q)
-            acc += p.p1[((int64_t)(sg * groups_per_seg + q) * p.T + t) * p.r_seg + j];
-        p.out1[t * p.ldo1 + sg * p.r_seg + j] = f2bf(p.scale * acc);
+        const float* src = p.p1 + ((int64_t)sg * groups_per_seg * p.T + t) * p.r_seg + j;
+        const int64_t stride = (int64_t)p.T * p.r_seg;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int q = 0; q < groups_per_seg; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(src + q * stride);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        *reinterpret_cast<uint2*>(p.out1 + t * p.ldo1 + sg * p.r_seg + j) =
+            make_uint2(pack_bf16x2(p.scale * acc.x, p.scale * acc.y), pack_bf16x2(p.scale * acc.z, p.scale * acc.w));
     } else if (idx < n1 + n2) {
         const int64_t e = idx - n1;
-        const int j = e % p.r_seg;
-        const int64_t n = e / p.r_seg;
-        float acc = 0.0f;
-        for (int q = 0; q < row_blocks; ++q) acc += p.p2[((int64_t)q * p.N + n) * p.r_seg + j];
-        float* o = p.out2 + n * p.o2n + (int64_t)j * p.o2j;
-        *o = p.accumulate ? *o + acc : acc;
+        const int j = 4 * (e % q4);
+        const int64_t n = e / q4;
+        const float* src = p.p2 + n * p.r_seg + j;
+        const int64_t stride = (int64_t)p.N * p.r_seg;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int q = 0; q < row_blocks; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(src + q * stride);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float* o = p.out2 + n * p.o2n + (int64_t)(j + u) * p.o2j;
+            *o = p.accumulate ? *o + a[u] : a[u];
+        }
     }
 }
 
@@ -315,6 +388,7 @@ bool lora_skinny_ok(const LoraSkinny& q) {
     if (q.ldy < q.N || q.ldy % 8 != 0 || !aligned16(q.Y)) return false;
     if (p1) {
         if (!q.W || !aligned16(q.W) || q.ldo1 < (q.N / q.n_seg) * q.r_seg) return false;
+        if (q.ldo1 % 4 != 0 || (reinterpret_cast<uintptr_t>(q.out1) & 7u) != 0) return false;  // 8-byte stores
         const bool nj = q.w_j == 1 && q.w_n >= q.r_seg && q.w_n % 8 == 0;
         const bool jn = q.w_n == 1 && q.w_j >= q.n_seg && q.w_j % 8 == 0;
         if (!nj && !jn) return false;
@@ -351,6 +425,15 @@ void lora_skinny(const LoraSkinny& q, hipStream_t s) {
     p.o2j = q.o2j;
     p.accumulate = q.accumulate ? 1 : 0;
     const int64_t sub_rows = (q.T + kSub - 1) / kSub;
+    if (p1 && !p2 && q.w_n == 1 && q.n_seg == q.N) {
+        // the forward x A^T: 16 rows per block, no partial sums
+        const dim3 grid(static_cast<unsigned>((q.T + 15) / 16));
+        if (RB == 1) hipLaunchKernelGGL((lora_xa_k<1>), grid, dim3(256), 0, s, p);
+        else if (RB == 2) hipLaunchKernelGGL((lora_xa_k<2>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((lora_xa_k<3>), grid, dim3(256), 0, s, p);
+        AIC_LAUNCH_CHECK("lora_xa");
+        return;
+    }
     if (p2) {
         // one chunk per block; rows per block halved from 512 until the grid covers the CUs
         p.cpb = 1;
@@ -387,7 +470,7 @@ void lora_skinny(const LoraSkinny& q, hipStream_t s) {
 #undef AIC_LORA
     AIC_LAUNCH_CHECK("lora_skinny");
     if (p.p1 || p.p2) {
-        const int64_t n = (p.p1 ? q.T * segs * q.r_seg : 0) + (p.p2 ? q.N * q.r_seg : 0);
+        const int64_t n = (p.p1 ? q.T * segs * q.r_seg / 4 : 0) + (p.p2 ? q.N * q.r_seg / 4 : 0);
         hipLaunchKernelGGL(lora_reduce_k, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p,
                            static_cast<int>(gps), static_cast<int>(segs), static_cast<int>(row_blocks));
         AIC_LAUNCH_CHECK("lora_reduce");

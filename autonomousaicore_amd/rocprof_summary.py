@@ -68,7 +68,7 @@ _RULES = [
     (r"sqnorm|sqsum|sqslot|finalize", "grad_norm"),
     (r"sq_matrix", "gemm_wgrad"),
     (r"adamw", "adamw"),
-    (r"lora_skinny|lora_reduce", "lora"),
+    (r"lora_skinny|lora_reduce|lora_xa", "lora"),
     # kernels outside bench.py's event classes (the MoE and QLoRA configurations)
     (r"moe_", "moe_routing"),
     (r"int4_quantize", "other"),  # the base's one-time quantization at set-up, like the weight init

@@ -133,7 +133,8 @@ int aic_hip_gemm_swiglu_bwd(int64_t M, int64_t f, int64_t K, const void* A, int6
  *   out2(n, j) (+)= sum_t Y[t, n] Z[t, g(n) r_seg + j]                         (out2 non-NULL)
  * W(n, j) = W[n w_n + j w_j] with w_j == 1 (B [out, r] rows) or w_n == 1 (A [r, in] rows);
  * out1 bf16 [T, ldo1]; Z bf16 [T, ldz]; out2 fp32 at out2 + n o2n + j o2j, overwritten or added
- * to (accumulate).  bf16 pointers 16-byte aligned, leading dimensions % 8 == 0.  Deterministic.
+ * to (accumulate).  bf16 inputs 16-byte aligned with leading dimensions % 8 == 0, out1 8-byte
+ * aligned with ldo1 % 4 == 0.  Deterministic.
  * Other shapes return NotImplemented (the caller runs GEMMs instead).
  * Replaces (no single reference launcher): the rank-r matmuls of LoRALinear::forward and their
  * autograd gradients (src/nn/lora.cpp:75-93; MatMulBackward, src/autograd/functions.cpp:254-273):

@@ -88,6 +88,23 @@ def test_backward_db_dxa_one_pass(T, n_seg, S, r):
     np.testing.assert_array_equal(host(dB), dB_before + dB_before)
 
 
+@pytest.mark.parametrize("T,n_seg,S", [(8192, 2048, 3), (500, 768, 2)])
+def test_dxa_alone_over_segments(T, n_seg, S):
+    """The out1 product by itself on B-stacked segments (w_j = 1): dxa = s dy B per segment, the
+    general kernel's column-group partial sums."""
+    rng = np.random.default_rng(T + n_seg)
+    N, r = S * n_seg, 16
+    dy, B = _r(rng, T, N), _r(rng, N, r, scale=0.05)
+    dyd, Bd = dev(dy, torch.bfloat16), dev(B, torch.bfloat16)
+    dxa = torch.empty((T, S * r), dtype=torch.bfloat16, device="cuda")
+    _skinny(dyd, T, N, n_seg, r, W=Bd, w_n=r, w_j=1, out1=dxa, ldo1=S * r, scale=0.25)
+    ref = np.concatenate([0.25 * dy[:, g * n_seg:(g + 1) * n_seg].astype(np.float64) @
+                          B[g * n_seg:(g + 1) * n_seg].astype(np.float64) for g in range(S)], axis=1)
+    got = host(dxa)
+    assert rel(got, ref) < 3e-3
+    assert np.max(np.abs(got - ref)) <= 2 ** -7 * np.max(np.abs(ref)) + 1e-6
+
+
 @pytest.mark.parametrize("T,N,R", [(8192, 2048, 48), (8192, 5632, 16), (777, 2048, 32), (64, 256, 16)])
 def test_backward_da(T, N, R):
     """dA = dxa^T x, written transposed into A's [R, in] layout (o2n = 1, o2j = in)."""
