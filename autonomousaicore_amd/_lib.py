@@ -80,6 +80,8 @@ SIGNATURES = {
     "aic_hip_mem_release_stream": (i32, [vp]),
     "aic_hip_gemm": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp, i64, i32, i32, vp]),
     "aic_hip_gemm_grouped": (i32, [i32, C.POINTER(GemmDesc), f32, f32, i32, i32, vp]),
+    "aic_hip_gemm_ragged": (i32, [i32, i64, i64, i64, f32, vp, i64, vp, i64, i64, vp, i64, vp, i32, i64, vp, i64, vp,
+                                  vp, i64, i32, vp]),
     "aic_hip_gemm_lowrank": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32,
                                    f32, vp, i64, vp, i64, i32, i32, vp]),
     "aic_hip_rmsnorm_fwd": (i32, [vp, i64, vp, vp, i64, vp, i64, i64, f32, i32, vp]),

@@ -1289,6 +1289,41 @@ int aic_telemetry_latest_json(const aic_telemetry* t, char* buf, int cap) {
     });
 }
 
+int aic_hip_gemm_ragged(int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                        const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc, const int64_t* offsets,
+                        int E, int64_t glu_f, void* glu_out, int64_t ld_glu, const void* dglu_gu, void* dglu_out,
+                        int64_t dglu_ld, aic_dtype c_type, aic_stream stream) {
+    return guard([&] {
+        aic::hip::RaggedArgs r;
+        aic::hip::GemmArgs& a = r.g;
+        a.transA = 0;
+        a.transB = transB ? 1 : 0;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.alpha = alpha;
+        a.A = A;
+        a.lda = lda;
+        a.B = B;
+        a.ldb = ldb;
+        a.C = C;
+        a.ldc = ldc;
+        a.ab = aic::DType::BFloat16;
+        a.c = dt(c_type);
+        a.glu_f = glu_f;
+        a.glu_out = glu_out;
+        a.ld_glu = ld_glu;
+        a.dglu_gu = dglu_gu;
+        a.dglu_out = dglu_out;
+        a.dglu_ld = dglu_ld;
+        r.offsets = offsets;
+        r.E = E;
+        r.b_stride = b_stride;
+        AIC_CHECK(aic::hip::gemm_ragged_eligible(r), NotImplemented, "gemm_ragged: shape or layout not supported");
+        aic::hip::gemm_ragged(r, st(stream));
+    });
+}
+
 int aic_hip_gemm_grouped(int n, const aic_gemm_desc* descs, float alpha, float beta, aic_dtype ab_type,
                          aic_dtype c_type, aic_stream stream) {
     return guard([&] {

@@ -682,7 +682,12 @@ void gemm_ragged(const RaggedArgs& r, hipStream_t s) {
         return r.ragged_k ? r.E * ((a.M + t - 1) / t) * tn : ((a.M + t - 1) / t + r.E) * tn;
     };
     auto fill = [](int64_t n) { return static_cast<double>(n) / (256.0 * static_cast<double>((n + 255) / 256)); };
-    const bool big = force256 || (tiles(256) >= 128 && fill(tiles(256)) >= 0.8 * fill(tiles(128)));
+    // bf16 rows on whole 256-column tiles run the persistent kernel (gemm_kernels.inc,
+    // launch_dma_ragged), whose blocks take tile after tile: a round of 256 tiles is enough
+    const bool pers = a.c == DType::BFloat16 && !r.ragged_k && r.E <= 63 && a.N % 256 == 0 && a.K % 128 == 0 &&
+                      a.K >= 256 && a.beta == 0.0f;
+    const bool big = force256 || (pers && tiles(256) >= 256) ||
+                     (tiles(256) >= 128 && fill(tiles(256)) >= 0.8 * fill(tiles(128)));
     if (a.c == DType::Float32) {
         if (big) dispatch_ragged<256, 256, 64, 2, float>(r, s);
         else dispatch_ragged<128, 128, 64, 4, float>(r, s);

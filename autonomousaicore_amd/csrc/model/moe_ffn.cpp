@@ -1,6 +1,7 @@
 #include "moe_ffn.hpp"
 
 #include <algorithm>
+#include <optional>
 #include <vector>
 
 #include "../kernels/gemm.hpp"
@@ -101,7 +102,9 @@ const std::vector<int64_t>& MoEFFN::counts_host() {
 // Ragged launch with the device offsets when the layout allows it, else one product per
 // expert from the host offsets.
 void MoEFFN::experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s,
-                     SqSlots sq) {
+                     SqSlots sq, int cls, double flops) {
+    std::optional<Profiler::Scope> scope;
+    if (prof_ && cls >= 0) scope.emplace(prof_, cls, flops, 0.0, s);
     hip::RaggedArgs r;
     r.g = g;
     r.g.sq_part = sq.part;
@@ -200,8 +203,10 @@ void MoEFFN::forward(const void* h, int64_t T, const void* wr, const void* exper
     gu.glu_f = f_;  // a = silu(gate) * up, in the product's epilogue where the shapes allow
     gu.glu_out = a_.get();
     gu.ld_glu = f_;
-    experts(gu, 0, ex, 0, s);
-    experts(args(0, 1, used_, d_, f_, a_.get(), f_, exb + es * 2 * f_ * d_, f_, ye_.get(), d_, dt_, dt_), 0, ex, 0, s);
+    const double routed = static_cast<double>(T) * k_, pf = 2.0 * routed * f_ * d_;  // FLOPs of an f x d product
+    experts(gu, 0, ex, 0, s, {}, kGemmFwd, 2.0 * pf);
+    experts(args(0, 1, used_, d_, f_, a_.get(), f_, exb + es * 2 * f_ * d_, f_, ye_.get(), d_, dt_, dt_), 0, ex, 0, s,
+            {}, kGemmFwd, pf);
     hip::moe_combine(ye_.get(), idx_.as<int64_t>(), dst_row_.as<int>(), gsel_.as<float>(), T, k_, d_, R, d_, y, d_, dt_,
                      s);
 }
@@ -224,12 +229,15 @@ void MoEFFN::backward(const void* dy, float daux, void* dh, float* dwr, float* d
     dn.dglu_gu = gu_.get();
     dn.dglu_out = dgu.get();
     dn.dglu_ld = f2;
-    experts(dn, 0, ex, 0, s);
+    const double pf = 2.0 * static_cast<double>(T) * k_ * f_ * d_;  // FLOPs of an f x d product over the routed rows
+    experts(dn, 0, ex, 0, s, {}, kGemmDgrad, pf);
     experts(args(1, 0, d_, f_, 0, dye.get(), d_, a_.get(), f_, dexperts + 2 * f_ * d_, f_, dt_, DType::Float32), 1, 0,
-            ex, s, sq_d);
+            ex, s, sq_d, kGemmWgrad, pf);
     // gate/up projections: dxp = dgu . Wgu and dWgu = dgu^T . xp
-    experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s);
-    experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s, sq_gu);
+    experts(args(0, 0, used, d_, f2, dgu.get(), f2, exb, d_, dxp.get(), d_, dt_, dt_), 0, ex, 0, s, {}, kGemmDgrad,
+            2.0 * pf);
+    experts(args(1, 0, f2, d_, 0, dgu.get(), f2, xp_.get(), d_, dexperts, d_, dt_, DType::Float32), 1, 0, ex, s, sq_gu,
+            kGemmWgrad, 2.0 * pf);
     // router: dlogits from the gates and the aux loss, then both router products (for bf16 the
     // input gradient dlogits . W_r joins the experts' sum in the scatter, in fp32)
     hip::moe_router_bwd(probs_.as<float>(), idx_.as<int64_t>(), dgsel.as<float>(), counts_.as<int64_t>(), T, E_, k_,

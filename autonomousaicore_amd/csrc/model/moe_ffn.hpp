@@ -12,6 +12,7 @@
 #include "../kernels/gemm.hpp"
 #include "../runtime/dtype.hpp"
 #include "../runtime/memory_pool.hpp"
+#include "../runtime/profiler.hpp"
 
 namespace aic::models {
 
@@ -45,6 +46,9 @@ public:
     int64_t top_k() const { return k_; }
     // counts on the host (copied from the device, with a stream synchronisation, on first use)
     const std::vector<int64_t>& counts_host();
+    // Times the experts' products under the GEMM classes of `p` (nullable), with the FLOPs of the
+    // routed rows (T top_k; the padding rows of the device-offset launches are not counted).
+    void set_profiler(Profiler* p) { prof_ = p; }
 
 private:
     int64_t d_, f_, E_, k_;
@@ -56,7 +60,8 @@ private:
     const void* ex_ = nullptr;
     void host_offsets(hipStream_t s);
     void experts(const hip::GemmArgs& g, int ragged_k, int64_t b_stride, int64_t c_stride, hipStream_t s,
-                 SqSlots sq = {});
+                 SqSlots sq = {}, int cls = -1, double flops = 0.0);
+    Profiler* prof_ = nullptr;
     int64_t used_ = 0;  // rows of the permuted buffers
     bool host_valid_ = false;
     std::vector<int64_t> counts_h_, offsets_h_;

@@ -461,8 +461,10 @@ TransformerLM::TransformerLM(const TransformerLMConfig& cfg, const TrainOptions&
     if (E > 0) {
         AIC_HIP_CHECK(hipMalloc(&aux_dev_, sizeof(float) * static_cast<size_t>(L)));
         AIC_HIP_CHECK(hipMemset(aux_dev_, 0, sizeof(float) * static_cast<size_t>(L)));
-        for (int64_t l = 0; l < L; ++l)
+        for (int64_t l = 0; l < L; ++l) {
             moe_.push_back(std::make_unique<MoEFFN>(d, f, E, cfg.top_k, cfg.aux_loss_coef, cfg.compute));
+            moe_.back()->set_profiler(&prof_);
+        }
     }
     AIC_HIP_CHECK(hipStreamSynchronize(stream_));
 }

@@ -162,6 +162,24 @@ typedef struct {
 int aic_hip_gemm_grouped(int n, const aic_gemm_desc* descs, float alpha, float beta, aic_dtype ab_type,
                          aic_dtype c_type, aic_stream stream);
 
+/* Expert-ragged product: expert e's rows are [offsets[e], offsets[e+1]) of A and C (offsets: E + 1
+ * int64 on the device, read by the kernels -- no host synchronisation), and
+ *   C[rows_e] = alpha * A[rows_e] op(B_e),  B_e = B + e * b_stride elements,
+ * op(B_e) = B_e^T ([N, K] rows, transB = 1) or B_e ([K, N], transB = 0); bf16 A and B, C bf16 or
+ * fp32 [M, ldc] (M: a bound on the rows, the buffers' size).  SwiGLU in the epilogue as
+ * aic_hip_gemm_swiglu / aic_hip_gemm_swiglu_bwd: glu_f > 0 (transB = 1, N = 2 glu_f) also writes
+ * glu_out[row][j] = silu(C[row][j]) C[row][glu_f + j]; dglu_gu non-NULL (transB = 0) writes
+ * dglu_out from the product dh and the saved gate/up rows dglu_gu (C then need not be written).
+ * Where the epilogue does not take the shape (N % 256 != 0, or glu_f % 128 != 0), the product goes
+ * to C and the standalone SwiGLU pass runs over all M rows.  Shapes the kernels do not take
+ * return NotImplemented.
+ * Replaces: the per-expert matmul loop of MoELayer::forward / backward (src/nn/moe.cpp:205-245),
+ * one launch per expert there, with the host reading the expert counts. */
+int aic_hip_gemm_ragged(int transB, int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                        const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc, const int64_t* offsets,
+                        int E, int64_t glu_f, void* glu_out, int64_t ld_glu, const void* dglu_gu, void* dglu_out,
+                        int64_t dglu_ld, aic_dtype c_type, aic_stream stream);
+
 /* ---------------------------------------------------------------- RMSNorm ---------- */
 /* y = x / rms * w with rms = sqrt(mean(x^2) + eps) per row; rms[rows] (fp32) is saved.
  * x/y have dtype dt (F32 or BF16), leading dimensions ldx/ldy; w is fp32 [dim].
