@@ -94,6 +94,8 @@ SIGNATURES = {
     "aic_hip_gemm_rope": (i32, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i64, i64, vp, vp, vp]),
     "aic_hip_gemm_swiglu": (i32, [i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp]),
     "aic_hip_gemm_swiglu_bwd": (i32, [i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, vp]),
+    "aic_hip_int4_gemm_swiglu": (i32, [i64, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp,
+                                       i64, vp]),
     "aic_hip_lora_skinny": (i32, [vp, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, f32, vp, i64, vp, i64, i64, i32,
                                   vp]),
     "aic_hip_attn_bwd_rope": (i32, [vp, vp, vp, i64, vp, vp, i64, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, f32,

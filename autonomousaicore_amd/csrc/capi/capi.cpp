@@ -852,6 +852,49 @@ int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float
     });
 }
 
+int aic_hip_int4_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* X, int64_t ldx, const uint8_t* Wq,
+                             const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2,
+                             int64_t ldy2, int64_t r2, int64_t seg_n, void* GU, int64_t ldgu, void* H, int64_t ldh,
+                             aic_stream stream) {
+    return guard([&] {
+        AIC_CHECK(r2 >= 0 && (r2 == 0 || (X2 && Y2)) && H && f > 0, InvalidArgument,
+                  "int4_gemm_swiglu: bad arguments");
+        aic::hip::GemmArgs a;
+        a.transA = 0;
+        a.transB = 1;
+        a.M = M;
+        a.N = 2 * f;
+        a.K = K;
+        a.A = X;
+        a.lda = ldx;
+        a.ldb = K;
+        a.Bq = Wq;
+        a.Bscale = scales;
+        a.scale_t = aic::DType::Float16;
+        a.group = aic::hip::int4_group(2 * f * K, group);
+        a.C = GU;
+        a.ldc = ldgu;
+        a.ab = aic::DType::BFloat16;
+        a.c = aic::DType::BFloat16;
+        if (r2 > 0) {
+            a.X2 = X2;
+            a.ldx2 = ldx2;
+            a.Y2 = Y2;
+            a.ldy2 = ldy2;
+            a.r2 = r2;
+            a.seg_n = seg_n;
+        }
+        a.glu_f = f;
+        a.glu_out = H;
+        a.ld_glu = ldh;
+        const bool tiles = M % 256 == 0 && (2 * f) % 256 == 0 && f % 128 == 0 && (M / 256) * (2 * f / 256) >= 128;
+        AIC_CHECK(tiles && aic::hip::gemm_q4_eligible(a) &&
+                      (r2 == 0 || (r2 % 8 == 0 && ldx2 % 8 == 0 && ldy2 % 8 == 0 && (seg_n == 0 || seg_n % 256 == 0))),
+                  NotImplemented, "int4_gemm_swiglu: shape outside the INT4 GEMM's SwiGLU epilogue");
+        aic::hip::gemm(a, st(stream));
+    });
+}
+
 int aic_hip_int4_gemm_rope(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const uint8_t* Wq,
                            const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2, int64_t ldy2,
                            int64_t r2, int64_t seg_n, void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq,

@@ -390,11 +390,13 @@ void gemm(const GemmArgs& a, hipStream_t s) {
     if (a.glu_f > 0) {
         AIC_CHECK(a.N == 2 * a.glu_f && a.glu_out && a.ld_glu >= a.glu_f && a.beta == 0.0f && !a.R && !a.rope_cos,
                   InvalidArgument, "GEMM SwiGLU epilogue: bad arguments");
-        // in the epilogue: bf16 x W^T on full 256x256 tiles of the eight-wave plain path
-        const bool fused = !a.Bq && a.transB && !a.transA && a.c == DType::BFloat16 && gemm_impl::kDmaWaves256 == 8 &&
-                           gemm_dma_eligible(a) && a.M % 256 == 0 && a.glu_f % 128 == 0 && a.ldc % 8 == 0 &&
-                           aligned16(a.C) && a.ld_glu % 8 == 0 && aligned16(a.glu_out) &&
-                           ((a.M / 256) * (a.N / 256) >= 128) && a.r2 == 0;
+        // in the epilogue: bf16 x W^T on full 256x256 tiles of the eight-wave plain path, or of the
+        // four-wave INT4 path (also after its low-rank term, whose segments follow the pairing)
+        const bool tiles = a.transB && !a.transA && a.c == DType::BFloat16 && a.M % 256 == 0 && a.glu_f % 128 == 0 &&
+                           a.ldc % 8 == 0 && aligned16(a.C) && a.ld_glu % 8 == 0 && aligned16(a.glu_out) &&
+                           ((a.M / 256) * (a.N / 256) >= 128);
+        const bool fused = tiles && (a.Bq ? gemm_q4_eligible(a) && (a.r2 == 0 || rank_tail_ok(a, 256))
+                                          : gemm_impl::kDmaWaves256 == 8 && gemm_dma_eligible(a) && a.r2 == 0);
         if (!fused) {
             GemmArgs b = a;
             b.glu_f = 0;
@@ -404,7 +406,8 @@ void gemm(const GemmArgs& a, hipStream_t s) {
                        a.M, a.glu_f, a.c, s);
             return;
         }
-        if (a.c == DType::BFloat16) dispatch_dma<256, 256, 64, 2, bf16>(a, s);
+        if (a.Bq) gemm_q4(a, s);
+        else dispatch_dma<256, 256, 64, 2, bf16>(a, s);
         return;
     }
     if (a.dglu_gu) {

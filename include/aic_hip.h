@@ -487,6 +487,20 @@ int aic_hip_int4_gemm_rope(int64_t M, int64_t N, int64_t K, const void* X, int64
                            const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2, int64_t ldy2,
                            int64_t r2, int64_t seg_n, void* C, int64_t ldc, int64_t rope_cols, int64_t hd, int64_t seq,
                            int64_t start_pos, const float* cos_t, const float* sin_t, aic_stream stream);
+/* The QLoRA FFN's gate/up projection with SwiGLU on the way out: GU = X . deq(Wq)^T + X2 . Y2^T
+ * (bf16 X [M, K], INT4 Wq holding W [2f, K] -- gate rows then up rows -- with fp16 scales per
+ * `group` elements; GU [M, 2f] bf16) and H[row][j] = silu(GU[row][j]) GU[row][f + j] (bf16 [M, f]),
+ * as aic_hip_gemm_swiglu.  The low-rank term is optional (r2 0); seg_n > 0 gives the gate and up
+ * columns their own X2 columns (the two adapters side by side, seg_n = f).  In the INT4 GEMM's
+ * epilogue on shapes of at least 128 full 256 x 256 tiles with f % 128 == 0 whose weight the
+ * operand load takes (K, group and the row length multiples of 64) and whose low-rank term the
+ * kernel takes (seg_n a multiple of 256); other shapes return NotImplemented.
+ * Replaces: the gate and up LoRALinear::forward over QuantizedLinear::forward (src/nn/lora.cpp:
+ * 75-93, src/nn/quantization.cpp:669-679) followed by silu * mul (include/nn/swiglu.hpp:21-33). */
+int aic_hip_int4_gemm_swiglu(int64_t M, int64_t f, int64_t K, const void* X, int64_t ldx, const uint8_t* Wq,
+                             const void* scales, int64_t group, const void* X2, int64_t ldx2, const void* Y2,
+                             int64_t ldy2, int64_t r2, int64_t seg_n, void* GU, int64_t ldgu, void* H, int64_t ldh,
+                             aic_stream stream);
 /* W[out,in] += sign * scaling * B[out,rank] . A[rank,in]  (sign >= 0: merge, < 0: unmerge);
  * W, A, B of `dtype` (AIC_F32 or AIC_BF16).
  * Replaces: LoRALinear::merge / unmerge (src/nn/lora.cpp:95-108). */

@@ -169,3 +169,48 @@ def test_int4_gemm_rope_equals_product_then_rope(orc, T, d, K, r, seq, start, G)
     call("aic_hip_int4_gemm_rope", T, N, K, ptr(xd), K, ptr(pd), ptr(sd), G, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1], r,
          d, ptr(again), N, 2 * d, hd, seq, start, ptr(cd), ptr(snd), stream())
     np.testing.assert_array_equal(host(again), f)
+
+
+# (T, f, K, r, G): the gate/up projection of the FFN with the gate and up adapters side by side
+# (seg_n = f); 128 and 176 tiles of 256x256 take the INT4 kernel's SwiGLU epilogue, with and
+# without the adapters
+@pytest.mark.parametrize("T,f,K,r,G", [(4096, 1024, 512, 16, 128), (4096, 1024, 256, 0, 128),
+                                       (2048, 2816, 512, 16, 64)])
+def test_int4_gemm_swiglu_equals_product_then_swiglu(orc, T, f, K, r, G):
+    """aic_hip_int4_gemm_swiglu: GU equal bit for bit to the low-rank GEMM over the dequantized
+    weight (the same bf16 operand values, MFMA sequence and low-rank tail), H equal bit for bit to
+    aic_hip_swiglu_fwd of that GU, and the float64 product within the bf16 bound."""
+    print(f"int4 gemm swiglu: T {T} f {f} K {K} r {r} G {G}", flush=True)
+    rng = np.random.default_rng(T + f + K + r + G)
+    N = 2 * f
+    packed, scales = _qweight(orc, rng, N, K, G, True)
+    W = bf16_round(orc.int4_dequantize(packed, scales, N * K, G).reshape(N, K))
+    x = bf16_round(rng.standard_normal((T, K)).astype(np.float32))
+    X2 = bf16_round(rng.standard_normal((T, 2 * max(r, 1))).astype(np.float32))
+    Y2 = bf16_round((rng.standard_normal((N, max(r, 1))) / 4).astype(np.float32))
+    xd, pd, sd, Wd = dev(x, torch.bfloat16), dev(packed), dev(scales), dev(W, torch.bfloat16)
+    X2d, Y2d = dev(X2, torch.bfloat16), dev(Y2, torch.bfloat16)
+    ldx2 = X2.shape[1]
+    gu = torch.empty((T, N), dtype=torch.bfloat16, device="cuda")
+    h = torch.empty((T, f), dtype=torch.bfloat16, device="cuda")
+    call("aic_hip_int4_gemm_swiglu", T, f, K, ptr(xd), K, ptr(pd), ptr(sd), G, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1],
+         r, f, ptr(gu), N, ptr(h), f, stream())
+    sep = torch.empty_like(gu)
+    if r > 0:
+        call("aic_hip_gemm_lowrank", 0, 1, T, N, K, 1.0, ptr(xd), K, ptr(Wd), K, ptr(X2d), ldx2, ptr(Y2d), Y2.shape[1],
+             r, f, 0, 0.0, ptr(sep), N, None, 0, BF16, BF16, stream())
+    else:
+        call("aic_hip_gemm", 0, 1, T, N, K, 1.0, ptr(xd), K, ptr(Wd), K, 0.0, ptr(sep), N, None, 0, BF16, BF16,
+             stream())
+    h2 = torch.empty_like(h)
+    call("aic_hip_swiglu_fwd", ptr(sep), ptr(sep) + 2 * f, N, ptr(h2), f, T, f, BF16, stream())
+    np.testing.assert_array_equal(host(gu), host(sep))
+    np.testing.assert_array_equal(host(h), host(h2))
+    ref = x.astype(np.float64) @ W.astype(np.float64).T
+    if r > 0:
+        for s in range(2):
+            ref[:, s * f:(s + 1) * f] += X2[:, s * r:(s + 1) * r].astype(np.float64) @ \
+                Y2[s * f:(s + 1) * f].astype(np.float64).T
+    assert rel(host(gu), ref) < 8e-3
+    g, u = ref[:, :f], ref[:, f:]
+    assert rel(host(h), g / (1.0 + np.exp(-g)) * u) < 2e-2
