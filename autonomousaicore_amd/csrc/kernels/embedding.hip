@@ -5,10 +5,12 @@
 // each key's place is its index in its chunk plus its lower bound in every other chunk) and
 // sums each id's rows in a fixed order (interleaved chains over the token-ordered run, then
 // the chains in order), so repeated runs are bit-identical and ids that repeat often
-// (Zipf-distributed text) are summed by sixteen waves instead of serialising on one address.
+// (Zipf-distributed text) are summed by sixteen waves instead of serialising on one address;
+// runs of at most sixteen ids are summed by one wave each, in token order.
 // Rows of ids that do not occur are written as zeros by their own kernel (no separate clear of
 // the whole gradient, and no memset node for a captured graph).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -99,32 +101,58 @@ __global__ __launch_bounds__(256) void embed_merge_rank_k(const unsigned long lo
     sorted_id[rank] = static_cast<int>(k >> 32);
 }
 
-// Starts of the runs of equal in-range ids in the sorted order, compacted: thread t owns
-// sorted positions [t * per, (t + 1) * per); an exclusive scan of the per-thread counts gives
-// the offsets.
+// Runs of at most this many equal ids are summed by one wave in token order; longer ones by a
+// block of sixteen waves.
+constexpr int kShortRun = 16;
+
+// Starts of the runs of equal in-range ids in the sorted order, compacted, with run_start[nruns]
+// = the number of in-range ids (the end of the last run), and the indices of the runs longer than
+// kShortRun in long_runs: thread t owns sorted positions [t * per, (t + 1) * per); exclusive scans
+// of the per-thread counts give the offsets.  counts[0] = nruns, counts[1] = the long runs.
 __global__ __launch_bounds__(1024) void embed_runs_k(const int* __restrict__ sorted_id, int N, int64_t V,
-                                                     int* __restrict__ run_start, int* __restrict__ nruns) {
-    __shared__ int cnt[1024];
+                                                     int* __restrict__ run_start, int* __restrict__ long_runs,
+                                                     int* __restrict__ counts) {
+    __shared__ int cnt[1024], lcnt[1024];
     const int per = (N + blockDim.x - 1) / blockDim.x;
     const int b0 = threadIdx.x * per, b1 = min(N, b0 + per);
     auto is_start = [&](int i) {
         const int id = sorted_id[i];
         return id < V && (i == 0 || sorted_id[i - 1] != id);
     };
-    int c = 0;
-    for (int i = b0; i < b1; ++i) c += is_start(i);
+    // sorted, so a run starting at i is longer than kShortRun iff position i + kShortRun holds its id
+    auto is_long = [&](int i) { return i + kShortRun < N && sorted_id[i + kShortRun] == sorted_id[i]; };
+    int c = 0, l = 0, in_range = 0;
+    for (int i = b0; i < b1; ++i) {
+        const bool st = is_start(i);
+        c += st;
+        l += st && is_long(i);
+        in_range += sorted_id[i] < V;
+    }
     cnt[threadIdx.x] = c;
+    lcnt[threadIdx.x] = l;
     __syncthreads();
-    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {  // inclusive Hillis-Steele scan
-        const int v = threadIdx.x >= static_cast<unsigned>(off) ? cnt[threadIdx.x - off] : 0;
+    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {  // inclusive Hillis-Steele scans
+        const bool has = threadIdx.x >= static_cast<unsigned>(off);
+        const int v = has ? cnt[threadIdx.x - off] : 0, w = has ? lcnt[threadIdx.x - off] : 0;
         __syncthreads();
         cnt[threadIdx.x] += v;
+        lcnt[threadIdx.x] += w;
         __syncthreads();
     }
-    int o = cnt[threadIdx.x] - c;
+    int o = cnt[threadIdx.x] - c, ol = lcnt[threadIdx.x] - l;
     for (int i = b0; i < b1; ++i)
-        if (is_start(i)) run_start[o++] = i;
-    if (threadIdx.x == blockDim.x - 1) *nruns = cnt[threadIdx.x];
+        if (is_start(i)) {
+            if (is_long(i)) long_runs[ol++] = o;
+            run_start[o++] = i;
+        }
+    // the in-range ids sort first: the thread holding the last in-range id (or the first
+    // thread when none is) writes the end of the last run
+    if (in_range > 0 && (b1 == N || sorted_id[b1] >= V)) run_start[cnt[blockDim.x - 1]] = b0 + in_range;
+    if (threadIdx.x == 0 && sorted_id[0] >= V) run_start[0] = 0;
+    if (threadIdx.x == blockDim.x - 1) {
+        counts[0] = cnt[threadIdx.x];
+        counts[1] = lcnt[threadIdx.x];
+    }
 }
 
 // Zeros for the rows of ids that occur nowhere in the sorted ids (one wave per row; a lower
@@ -150,65 +178,123 @@ __global__ __launch_bounds__(256) void embed_zero_absent_k(const int* __restrict
     }
 }
 
-// One block of 16 waves per (run of equal ids, chunk of 8 * 64 columns), grid-striding over
-// all of them.  Wave w adds the rows of tokens p + w, p + w + 16, ... in order, eight rows'
-// 16-byte loads in flight at a time; the 16 partial sums are then added in wave order, so the
-// result is the same on every run.
-template <typename T>
+// LB bytes of a dout row per lane: the row words of LB / 4 32-bit loads.
+template <int LB>
+struct RowLoad {
+    uint32_t w[LB / 4];
+};
+
+template <typename T, int LB>
+__device__ __forceinline__ RowLoad<LB> load_row(const T* __restrict__ p) {
+    RowLoad<LB> r;
+    if constexpr (LB == 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        r.w[0] = v.x, r.w[1] = v.y, r.w[2] = v.z, r.w[3] = v.w;
+    } else if constexpr (LB == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        r.w[0] = v.x, r.w[1] = v.y;
+    } else {
+        r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
+    return r;
+}
+
+template <typename T, int LB>
+__device__ __forceinline__ void add_row(float* acc, const RowLoad<LB>& r) {
+#pragma unroll
+    for (int k = 0; k < LB / 4; ++k) {
+        if constexpr (sizeof(T) == 2) {
+            acc[2 * k] += __uint_as_float(r.w[k] << 16);
+            acc[2 * k + 1] += __uint_as_float(r.w[k] & 0xffff0000u);
+        } else {
+            acc[k] += __uint_as_float(r.w[k]);
+        }
+    }
+}
+
+// Sum of the rows of tokens q0, q0 + step, ... below end, in that order, onto acc: U rows'
+// loads in flight at a time.
+template <typename T, int LB, int U>
+__device__ __forceinline__ void sum_rows(float* acc, const int* __restrict__ sorted_pos, int q0, int end, int step,
+                                         const T* __restrict__ dout, int64_t D, int64_t col) {
+    for (; q0 < end; q0 += step * U) {
+        RowLoad<LB> raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + step * u;
+            if (q < end) raw[u] = load_row<T, LB>(dout + static_cast<int64_t>(sorted_pos[q]) * D + col);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (q0 + step * u >= end) break;
+            add_row<T, LB>(acc, raw[u]);
+        }
+    }
+}
+
+// The column sums of every run of equal ids, per chunk of 64 lanes x LB bytes of the row.
+// Runs longer than kShortRun first: one block of 16 waves per (long run, chunk), wave w adding
+// the rows of tokens p + w, p + w + 16, ... in order, the 16 partial sums then added in wave
+// order.  Then the short runs: one wave per (run, chunk), adding the rows in token order.  Both
+// orders are fixed by the run length alone, so the result is the same on every run.
+template <typename T, int LB>
 __global__ __launch_bounds__(1024) void embed_run_k(const int* __restrict__ sorted_pos, const int* __restrict__ sorted_id,
-                                                    const int* __restrict__ run_start, const int* __restrict__ nruns,
-                                                    int N, const T* __restrict__ dout, int64_t D,
-                                                    float* __restrict__ dW, int accumulate) {
-    constexpr int VE = 16 / sizeof(T);  // elements per 16-byte load
-    constexpr int U = 8;
-    __shared__ float part[16][64 * VE];
+                                                    const int* __restrict__ run_start,
+                                                    const int* __restrict__ long_runs, const int* __restrict__ counts,
+                                                    const T* __restrict__ dout, int64_t D, float* __restrict__ dW,
+                                                    int accumulate) {
+    constexpr int VE = LB / sizeof(T);  // elements per lane
+    constexpr int CE = 64 * VE;         // columns per chunk
+    __shared__ float part[16][CE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunks = static_cast<int>(D / (64 * VE));
-    const int items = *nruns * chunks;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
-        const int r = it / chunks, ch = it % chunks;
-        const int p = run_start[r], id = sorted_id[p];
-        int end = r + 1 < *nruns ? run_start[r + 1] : N;
-        while (end > p + 1 && sorted_id[end - 1] != id) --end;  // trailing out-of-range ids
-        const int64_t col = static_cast<int64_t>(ch) * 64 * VE + lane * VE;
+    const int chunks = static_cast<int>(D / CE);
+    const int nruns = counts[0], nlong = counts[1];
+    for (int it = blockIdx.x; it < nlong * chunks; it += gridDim.x) {
+        const int r = long_runs[it / chunks], ch = it % chunks;
+        const int p = run_start[r], end = run_start[r + 1], id = sorted_id[p];
+        const int64_t col = static_cast<int64_t>(ch) * CE + lane * VE;
         float acc[VE];
 #pragma unroll
         for (int e = 0; e < VE; ++e) acc[e] = 0.0f;
-        for (int q0 = p + wave; q0 < end; q0 += 16 * U) {
-            uint4 raw[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int q = q0 + 16 * u;
-                raw[u] = q < end ? *reinterpret_cast<const uint4*>(dout + static_cast<int64_t>(sorted_pos[q]) * D + col)
-                                 : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (q0 + 16 * u >= end) break;
-                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-                if constexpr (sizeof(T) == 2) {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        acc[2 * k] += __uint_as_float(w[k] << 16);
-                        acc[2 * k + 1] += __uint_as_float(w[k] & 0xffff0000u);
-                    }
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) acc[k] += __uint_as_float(w[k]);
-                }
-            }
-        }
+        sum_rows<T, LB, 8>(acc, sorted_pos, p + wave, end, 16, dout, D, col);
 #pragma unroll
         for (int e = 0; e < VE; ++e) part[wave][lane * VE + e] = acc[e];
         __syncthreads();
-        if (threadIdx.x < 64 * VE) {
+        if (threadIdx.x < CE) {
             float sum = part[0][threadIdx.x];
 #pragma unroll
             for (int w = 1; w < 16; ++w) sum += part[w][threadIdx.x];
-            float* o = dW + static_cast<int64_t>(id) * D + static_cast<int64_t>(ch) * 64 * VE + threadIdx.x;
+            float* o = dW + static_cast<int64_t>(id) * D + static_cast<int64_t>(ch) * CE + threadIdx.x;
             *o = accumulate ? *o + sum : sum;
         }
         __syncthreads();
+    }
+    const int gw = static_cast<int>(blockIdx.x) * 16 + wave, nw = static_cast<int>(gridDim.x) * 16;
+    for (int it = gw; it < nruns * chunks; it += nw) {
+        const int r = it / chunks, ch = it % chunks;
+        const int p = run_start[r], end = run_start[r + 1];
+        if (end - p > kShortRun) continue;
+        const int id = sorted_id[p];
+        const int64_t col = static_cast<int64_t>(ch) * CE + lane * VE;
+        float acc[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[e] = 0.0f;
+        sum_rows<T, LB, 8>(acc, sorted_pos, p, end, 1, dout, D, col);
+        float* o = dW + static_cast<int64_t>(id) * D + col;
+        if constexpr (VE % 4 == 0) {  // 16-byte stores (the caller checks dW's alignment)
+#pragma unroll
+            for (int e = 0; e < VE; e += 4) {
+                float4 v = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
+                if (accumulate) {
+                    const float4 a = *reinterpret_cast<const float4*>(o + e);
+                    v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+                }
+                *reinterpret_cast<float4*>(o + e) = v;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) o[e] = accumulate ? o[e] + acc[e] : acc[e];
+        }
     }
 }
 
@@ -282,12 +368,18 @@ void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64
         return;
     }
     const size_t es = dtype_size(dt);
-    const bool runs = (D * static_cast<int64_t>(es)) % (64 * 16) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15u) == 0;
+    // the run-list path: a chunk of 64 lanes x LB bytes divides the row, LB = 16, 8 or 4
+    const int64_t row_bytes = D * static_cast<int64_t>(es);
+    int lb = 0;
+    for (int b : {16, 8, 4})
+        if (!lb && row_bytes % (64 * b) == 0 && (reinterpret_cast<uintptr_t>(dout) % b) == 0) lb = b;
+    const bool runs = lb > 0 && vec;
     auto* sk = static_cast<unsigned long long*>(stream_scratch(sizeof(unsigned long long) * N, s, 1));
-    int* spos = static_cast<int*>(stream_scratch(sizeof(int) * (3 * N + 1), s));
+    int* spos = static_cast<int*>(stream_scratch(sizeof(int) * (4 * N + 3), s));
     int* sid = spos + N;
-    int* rstart = sid + N;
-    int* nruns = rstart + N;
+    int* rstart = sid + N;      // N + 1 entries
+    int* counts = rstart + N + 1;  // nruns, long runs
+    int* lruns = counts + 2;
     const int n = static_cast<int>(N);
     hipLaunchKernelGGL(embed_chunk_sort_k, dim3(static_cast<unsigned>((N + kSortChunk - 1) / kSortChunk)), dim3(1024),
                        0, s, ids, n, V, sk);
@@ -301,16 +393,25 @@ void embed_bwd(const int64_t* ids, int64_t N, const void* dout, int64_t V, int64
         AIC_LAUNCH_CHECK("embed_zero_absent");
     }
     if (runs) {
-        hipLaunchKernelGGL(embed_runs_k, dim3(1), dim3(1024), 0, s, sid, n, V, rstart, nruns);
+        hipLaunchKernelGGL(embed_runs_k, dim3(1), dim3(1024), 0, s, sid, n, V, rstart, lruns, counts);
         AIC_LAUNCH_CHECK("embed_runs");
-        // one block of 16 waves per (run, 8 * 64-column chunk), at most 2048 blocks striding
-        const unsigned g = static_cast<unsigned>(std::min<int64_t>(2048, N * (D * static_cast<int64_t>(es) / 1024)));
-        if (dt == DType::Float32)
-            hipLaunchKernelGGL(embed_run_k<float>, dim3(g), dim3(1024), 0, s, spos, sid, rstart, nruns,
-                               static_cast<int>(N), static_cast<const float*>(dout), D, dW, accumulate ? 1 : 0);
-        else
-            hipLaunchKernelGGL(embed_run_k<bf16>, dim3(g), dim3(1024), 0, s, spos, sid, rstart, nruns,
-                               static_cast<int>(N), static_cast<const bf16*>(dout), D, dW, accumulate ? 1 : 0);
+        // a wave per (run, chunk) (16 per block), at most 2048 blocks striding
+        const int64_t items = N * (row_bytes / (64 * lb));
+        AIC_CHECK(items < (1LL << 31), InvalidArgument, "embed_bwd: tokens x row chunks exceeds 2^31");
+        const unsigned g = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(2048, (items + 15) / 16)));
+        const int acc = accumulate ? 1 : 0;
+        auto launch = [&](auto tag, auto lbc) {
+            using T = decltype(tag);
+            hipLaunchKernelGGL((embed_run_k<T, decltype(lbc)::value>), dim3(g), dim3(1024), 0, s, spos, sid, rstart,
+                               lruns, counts, static_cast<const T*>(dout), D, dW, acc);
+        };
+        auto by_lb = [&](auto tag) {
+            if (lb == 16) launch(tag, std::integral_constant<int, 16>{});
+            else if (lb == 8) launch(tag, std::integral_constant<int, 8>{});
+            else launch(tag, std::integral_constant<int, 4>{});
+        };
+        if (dt == DType::Float32) by_lb(float{});
+        else by_lb(bf16{});
         AIC_LAUNCH_CHECK("embed_run");
         return;
     }

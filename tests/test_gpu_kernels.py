@@ -379,11 +379,13 @@ def test_cross_entropy_reductions(orc, dt, reduction):
 
 # ----------------------------------------------------------------------------- embedding
 @pytest.mark.parametrize("dt", [F32, BF16])
-@pytest.mark.parametrize("V,D,N", [(1000, 136, 4096), (1500, 1024, 8192), (32000, 2048, 2048), (32000, 1024, 40000)])
+@pytest.mark.parametrize("V,D,N", [(1000, 136, 4096), (1500, 1024, 8192), (32000, 2048, 2048), (32000, 1024, 40000),
+                                   (32000, 768, 8192), (1000, 320, 4096)])
 def test_embedding_gather_bit_exact_and_scatter(orc, dt, V, D, N):
-    # D = 136: the per-column path; D * element size a multiple of 1 KB: the run-list path (the
-    # 1B shape among them), Zipf ids so one id repeats hundreds of times; 40000 tokens: twenty
-    # sorted chunks of 2048 merged, the last one partial
+    # D = 136: the per-column path; D * element size a multiple of 256 bytes: the run-list path
+    # with 16-, 8- or 4-byte loads per lane (the 1B and 125M shapes among them), Zipf ids so one
+    # id repeats hundreds of times; 40000 tokens: twenty sorted chunks of 2048 merged, the last
+    # one partial
     rng = np.random.default_rng(31 + D)
     W = rng.standard_normal((V, D)).astype(np.float32)
     if dt == BF16:
@@ -405,18 +407,24 @@ def test_embedding_gather_bit_exact_and_scatter(orc, dt, V, D, N):
     ref = orc.embedding_bwd(ids, dout, V)
     got = host(dW)
     # The kernels add a run of n equal ids as P interleaved float32 chains (P = 16 waves on the
-    # run-list path, 4 on the per-column path) combined in order: a float32 sum of depth
-    # ceil(n / P) + P, so |got - exact| <= depth * 2^-24 * sum |dout| per element, where a
-    # dropped or doubled row of N(0, 1) gradients would exceed it.
+    # run-list path, 4 on the per-column path) combined in order, or, on the run-list path for
+    # n <= 16, as one chain in token order: a float32 sum of depth at most ceil(n / P) + P, so
+    # |got - exact| <= depth * 2^-24 * sum |dout| per element, where a dropped or doubled row of
+    # N(0, 1) gradients would exceed it.
     ok = (ids >= 0) & (ids < V)
     exact = np.zeros((V, D))
     np.add.at(exact, ids[ok], dout[ok].astype(np.float64))
     mag = np.zeros((V, D))
     np.add.at(mag, ids[ok], np.abs(dout[ok].astype(np.float64)))
-    P = 16 if (D * (4 if dt == F32 else 2)) % 1024 == 0 else 4
+    run_list = (D * (4 if dt == F32 else 2)) % 256 == 0
+    P = 16 if run_list else 4
     n = np.bincount(ids[ok], minlength=V)[:, None]
     bound = (np.ceil(n / P) + P) * 2.0 ** -24 * mag
     assert np.all(np.abs(got - exact) <= bound)
+    if run_list:  # a short run is the reference's own token-order float32 sum, bit for bit
+        short = (n[:, 0] > 0) & (n[:, 0] <= 16)
+        assert short.any()
+        np.testing.assert_array_equal(got[short], ref[short])
     # and the oracle (the reference's token-order float32 sum, depth n) within its own bound
     assert np.all(np.abs(ref - exact) <= n * 2.0 ** -24 * mag)
     assert np.all(got[np.setdiff1d(np.arange(V), ids)] == 0)
