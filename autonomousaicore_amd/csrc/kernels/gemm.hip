@@ -441,9 +441,12 @@ void gemm(const GemmArgs& a, hipStream_t s) {
         // gradient: 80 us against 93 us on 128x128 tiles)
         const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
         const int64_t t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+        const int64_t tw = ((a.M + 127) / 128) * ((a.N + 255) / 256);  // 128x256 tiles
         const bool big = t256 >= 128;
+        // under a round of 256x256 tiles over a long K (a 1024-wide head's input gradient: 128
+        // tiles, K 32000): split K until about one round runs (682 -> 444 us there)
         int splits256 = 1;
-        if (a.r2 == 0 && !big && t256 >= 32 && a.K >= 4096) {
+        if (a.r2 == 0 && t256 < 256 && t256 >= 32 && a.K >= 4096) {
             splits256 = static_cast<int>(std::min<int64_t>(4, 256 / t256));
             while (splits256 > 1 && a.K % (64LL * splits256)) --splits256;
         }
@@ -474,6 +477,16 @@ void gemm(const GemmArgs& a, hipStream_t s) {
             float* part = static_cast<float*>(stream_scratch(sizeof(float) * splits * a.M * a.N, s, 7));
             dispatch_dma<128, 128, 64, 4, float>(a, s, splits, part);
             splitk_reduce(part, splits, a, s);
+            return;
+        }
+        // under a round of 256x256 tiles where 128x256 tiles fill between half the chip and one
+        // round (768- and 1024-wide products over 8192 rows): one round of the four-wave 128x256
+        // kernel beats a partial round of 256x256 tiles and two rounds of 128x128 ones (measured
+        // 3-9% on those shapes); with a residual and at least half a round of 256x256 tiles the
+        // persistent kernel stays ahead (its epilogue overlaps the next tile's copies)
+        if (a.r2 == 0 && !a.rope_cos && !a.dglu_gu && t256 < 256 && tw >= 128 && tw <= 256 && !(a.R && big)) {
+            if (a.c == DType::Float32) dispatch_dma<128, 256, 64, 3, float>(a, s);
+            else dispatch_dma<128, 256, 64, 3, bf16>(a, s);
             return;
         }
         if (a.c == DType::Float32) {

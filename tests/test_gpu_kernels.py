@@ -92,6 +92,38 @@ def test_gemm_long_k_and_epilogues(ta, tb, M, N, K):
     assert rel(host(cb), 0.25 * ref - 1.5 * C0 + R) < 1e-5
 
 
+# Under one round of 256x256 tiles: one round of 128x256 tiles (the 125M / MoE 768- and 1024-wide
+# products; partial tiles in both dimensions), and a long K split in two (128 tiles of 256x256,
+# the 1024-wide head's input gradient).
+WIDE_CASES = [(8192, 768, 768), (2048, 2048, 512), (3000, 1500, 192), (8192, 1024, 4096)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", WIDE_CASES)
+def test_gemm_wide_tiles_and_split(ta, tb, M, N, K):
+    """fp32 output against float64; bf16 output equal to the fp32 output rounded once (the same
+    MFMA sequence per element); residual / alpha / beta epilogue; run-to-run bit-identical."""
+    rng = np.random.default_rng(5 * M + N + K + 2 * ta + tb)
+    A = bf16_round(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = bf16_round(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    ref = _ref_gemm(ta, tb, A, B)
+    Ad, Bd = dev(A, torch.bfloat16), dev(B, torch.bfloat16)
+    c32 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32)
+    assert rel(host(c32), ref) < 1e-5
+    c16 = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.bfloat16)
+    if K < 4096:  # no K split: one rounding of the same fp32 sum
+        np.testing.assert_array_equal(host(c16), bf16_round(host(c32)))
+    else:
+        assert rel(host(c16), ref) < 4e-3
+    R = bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    cb = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32, R=dev(R), alpha=0.25, beta=-1.5, C0=dev(C0))
+    assert rel(host(cb), 0.25 * ref - 1.5 * C0 + R) < 1e-5
+    c16r = _gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.bfloat16, R=dev(R, torch.bfloat16), alpha=0.5)
+    assert rel(host(c16r), 0.5 * ref + R) < 4e-3
+    np.testing.assert_array_equal(host(_gemm(ta, tb, M, N, K, Ad, Bd, BF16, torch.float32)), host(c32))
+
+
 def _gemm_lowrank(ta, tb, M, N, K, A, B, X2, Y2, r2, seg_n, y2k, ab, ct, R=None, alpha=1.0, beta=0.0, C0=None):
     Cout = C0.clone() if C0 is not None else torch.empty((M, N), dtype=ct, device="cuda")
     call("aic_hip_gemm_lowrank", ta, tb, M, N, K, alpha, ptr(A), A.shape[1], ptr(B), B.shape[1], ptr(X2),
