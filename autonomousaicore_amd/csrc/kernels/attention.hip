@@ -821,16 +821,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma(const bf16* __restric
                 }
             // wave-uniform: the tile holds keys past some query of the wave (causal) or past S.
             // Queries past S need no mask: their q, dO, lse and D are 0, so dS = 1 * (0 - 0) = 0.
+            // Only such tiles run the compare and select: their masked scores become -inf, whose
+            // exp2 below is 0 exactly as a select of 0 would be.
             const bool diag = (causal && k0 + BKV - 1 > qw) || k0 + BKV > S;
-            // element (jb, e) is key k0 + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked when its
-            // offset 32 jb + 8 (e >> 2) + (e & 3) exceeds lim (past every offset off the diagonal)
-            const int lim = diag ? min(causal ? myq : S - 1, S - 1) - k0 - 4 * hl : BKV;
+            if (diag) {
+                // element (jb, e) is key k0 + 32 jb + 8 (e >> 2) + 4 hl + (e & 3): masked when its
+                // offset 32 jb + 8 (e >> 2) + (e & 3) exceeds lim
+                const int lim = min(causal ? myq : S - 1, S - 1) - k0 - 4 * hl;
+#pragma unroll
+                for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (32 * jb + 8 * (e >> 2) + (e & 3) > lim) s[jb][e] = -INFINITY;
+            }
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
-                    p = (32 * jb + 8 * (e >> 2) + (e & 3) > lim) ? 0.0f : p;
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[jb][e], c, -my_l2));
                     dp[jb][e] = p * (dp[jb][e] - my_D);
                 }
 #pragma unroll
