@@ -600,28 +600,37 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
             rq[g % 3] = F.row(Qb, 32 * (g / KS), g % KS);
             ro[g % 3] = F.row(Ob, 32 * (g / KS), g % KS);
         };
-        float nl[2][16], dd[2][16];  // -lse * log2(e) and D per element
-        auto rd_ld = [&](int jb) {
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                const int qi = jb * 32 + 8 * g4 + 4 * hl;
-                const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);
-                const float4 d4 = *reinterpret_cast<const float4*>(Ds + qi);
-                const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    // queries past S: p = exp2(-inf) = 0
-                    if constexpr (EDGE) nl[jb][4 * g4 + u] = qs + qi + u >= S ? -INFINITY : -lv[u] * kLog2e;
-                    else nl[jb][4 * g4 + u] = -lv[u] * kLog2e;
-                    dd[jb][4 * g4 + u] = dv4[u];
-                }
-            }
+        // -lse * log2(e) and D of element group G = 4 jb + (e >> 2) (its four queries), in rings
+        // of three float4: read from LDS two groups ahead, lse scaled one group ahead (queries
+        // past S: -inf, so p = exp2(-inf) = 0), so they hold 24 registers instead of 64
+        float4 lr[3], dr[3];
+        auto rd_q = [&](int G) {
+            const int qi = 32 * (G >> 2) + 8 * (G & 3) + 4 * hl;
+            lr[G % 3] = *reinterpret_cast<const float4*>(Ls + qi);
+            dr[G % 3] = *reinterpret_cast<const float4*>(Ds + qi);
         };
+        auto scale_l = [&](int G) {
+            const int qi = 32 * (G >> 2) + 8 * (G & 3) + 4 * hl;
+            float4& l = lr[G % 3];
+            float v[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if constexpr (EDGE) v[u] = qs + qi + u >= S ? -INFINITY : -v[u] * kLog2e;
+                else v[u] = -v[u] * kLog2e;
+            }
+            l = make_float4(v[0], v[1], v[2], v[3]);
+        };
+        auto comp = [](const float4& f, int u) { return u == 0 ? f.x : u == 1 ? f.y : u == 2 ? f.z : f.w; };
         auto softmax = [&](int jb, int e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, nl[jb][e]));
+            const int G = 4 * jb + (e >> 2);
+            if ((e & 3) == 0) {
+                if (G + 2 < 8) rd_q(G + 2);
+                if (G + 1 < 8) scale_l(G + 1);
+            }
+            float p = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, comp(lr[G % 3], e & 3)));
             if constexpr (EDGE) p = (32 * jb + 8 * (e >> 2) + (e & 3) < lo) ? 0.0f : p;
             sa[jb][e] = p;
-            sd[jb][e] = p * (sd[jb][e] - dd[jb][e]);
+            sd[jb][e] = p * (sd[jb][e] - comp(dr[G % 3], e & 3));
         };
         bf16x8 pf[4], dsf[4];
         auto pack = [&](int ks) {
@@ -639,8 +648,8 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
 
         rd(0);
         rd(1);
-        rd_ld(0);
-        constexpr int LD1 = NA - 4;  // group B slot from which queries 32..63's lse / D are read
+        rd_q(0);
+        rd_q(1);
         // A: S^T, dP^T of queries 0..31
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
@@ -653,6 +662,7 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        scale_l(0);
         // B: S^T, dP^T of queries 32..63; softmax of queries 0..31; transposed reads of step 0
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
@@ -668,7 +678,6 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
             if ((i + 1) * EB == 8) pack(0);
             if ((i + 1) * EB == 16) pack(1);
             if (i < 2 * OB) rd_tr(i);
-            if (i == LD1) rd_ld(1);
             __builtin_amdgcn_sched_barrier(0);
         }
         // C, D: dV^T += dO^T P, dK^T += Q^T dS over the four 16-query steps
