@@ -603,11 +603,22 @@ void gemm_grouped(const GemmArgs* a, int n, hipStream_t s) {
             return;
         }
     }
+    // under half a round of 256x256 tiles: 128x128 tiles, or 128x256 ones where those fill one
+    // round and 128x128 tiles would need more (the 125M layer's four weight gradients: 216 tiles
+    // of 128x256 against 432 of 128x128)
+    int64_t t128 = 0, tw = 0;
+    for (int i = 0; i < n; ++i) {
+        t128 += ((a[i].M + 127) / 128) * ((a[i].N + 127) / 128);
+        tw += ((a[i].M + 127) / 128) * ((a[i].N + 255) / 256);
+    }
+    const bool wide = t256 < 128 && t128 > 256 && tw <= 256;
     if (a[0].c == DType::Float32) {
         if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, float>(a, n, s);
+        else if (wide) dispatch_grouped<128, 256, 64, 3, float>(a, n, s);
         else dispatch_grouped<128, 128, 64, 4, float>(a, n, s);
     } else {
         if (t256 >= 128) dispatch_grouped<256, 256, 64, 2, bf16>(a, n, s);
+        else if (wide) dispatch_grouped<128, 256, 64, 3, bf16>(a, n, s);
         else dispatch_grouped<128, 128, 64, 4, bf16>(a, n, s);
     }
 }

@@ -794,7 +794,10 @@ GROUPED_CASES = [(0, 1, [(192, 704, 256), (64, 704, 256), (448, 704, 256), (128,
                  # own GEMM (two tile-columns of the third product, one of them partial; the last
                  # tile-row of the third product with A row-major)
                  (1, 0, [(2048, 2048, 512), (4096, 2048, 512), (2048, 1800, 512), (2048, 512, 512)]),
-                 (0, 0, [(4096, 2048, 256), (2048, 2048, 256), (2304, 2048, 256)])]
+                 (0, 0, [(4096, 2048, 256), (2048, 2048, 256), (2304, 2048, 256)]),
+                 # the 125M layer's four weight gradients (K shortened): 108 tiles of 256x256, 432 of
+                 # 128x128, one round of 216 tiles of 128x256
+                 (1, 0, [(2304, 768, 2048), (768, 768, 2048), (4096, 768, 2048), (768, 2048, 2048)])]
 
 
 @pytest.mark.parametrize("ta,tb,shapes", GROUPED_CASES)
