@@ -621,13 +621,21 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
             l = make_float4(v[0], v[1], v[2], v[3]);
         };
         auto comp = [](const float4& f, int u) { return u == 0 ? f.x : u == 1 ? f.y : u == 2 ? f.z : f.w; };
-        auto softmax = [&](int jb, int e) {
+        // The softmax of element e in two stages a slot apart, so the exponential's latency
+        // passes under the next MFMA instead of holding up its issue: sm1 takes the exponential,
+        // sm2 (the next slot) the mask, P and dS.
+        float pe[2][16];
+        auto sm1 = [&](int jb, int e) {
             const int G = 4 * jb + (e >> 2);
             if ((e & 3) == 0) {
                 if (G + 2 < 8) rd_q(G + 2);
                 if (G + 1 < 8) scale_l(G + 1);
             }
-            float p = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, comp(lr[G % 3], e & 3)));
+            pe[jb][e] = __builtin_amdgcn_exp2f(fmaf(sa[jb][e], c, comp(lr[G % 3], e & 3)));
+        };
+        auto sm2 = [&](int jb, int e) {
+            const int G = 4 * jb + (e >> 2);
+            float p = pe[jb][e];
             if constexpr (EDGE) p = (32 * jb + 8 * (e >> 2) + (e & 3) < lo) ? 0.0f : p;
             sa[jb][e] = p;
             sd[jb][e] = p * (sd[jb][e] - comp(dr[G % 3], e & 3));
@@ -673,10 +681,13 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
             } else {
                 sd[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ro[g % 3], vf[kk], sd[1], 0, 0, 0);
             }
+            if (i > 0) {  // the second stage of the previous slot's elements
 #pragma unroll
-            for (int e = i * EB; e < (i + 1) * EB; ++e) softmax(0, e);
-            if ((i + 1) * EB == 8) pack(0);
-            if ((i + 1) * EB == 16) pack(1);
+                for (int e = (i - 1) * EB; e < i * EB; ++e) sm2(0, e);
+                if (i * EB == 8) pack(0);
+            }
+#pragma unroll
+            for (int e = i * EB; e < (i + 1) * EB; ++e) sm1(0, e);
             if (i < 2 * OB) rd_tr(i);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -691,12 +702,23 @@ __global__ __launch_bounds__(256, HD == 128 ? 1 : 2) void attn_bwd_dkdv_mfma(
                 else
                     dkt[i - OB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr[f % NR], dsf[ks], dkt[i - OB], 0, 0, 0);
                 if (f + 2 * OB < 8 * OB) rd_tr(f + 2 * OB);
-                if (ks < 2) {  // group C: the softmax of queries 32..63
-                    const int slot = ks * 2 * OB + i;
+                if (f == 0) {  // the last slot of group B, second stage
 #pragma unroll
-                    for (int e = slot * EC; e < (slot + 1) * EC; ++e) softmax(1, e);
-                    if ((slot + 1) * EC == 8) pack(2);
-                    if ((slot + 1) * EC == 16) pack(3);
+                    for (int e = (NA - 1) * EB; e < NA * EB; ++e) sm2(0, e);
+                    pack(1);
+                }
+                if (ks < 2 || f == 4 * OB) {  // group C: the softmax of queries 32..63
+                    const int slot = ks * 2 * OB + i;
+                    if (slot > 0) {
+#pragma unroll
+                        for (int e = (slot - 1) * EC; e < slot * EC; ++e) sm2(1, e);
+                        if (slot * EC == 8) pack(2);
+                        if (slot * EC == 16) pack(3);
+                    }
+                    if (ks < 2) {
+#pragma unroll
+                        for (int e = slot * EC; e < (slot + 1) * EC; ++e) sm1(1, e);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
