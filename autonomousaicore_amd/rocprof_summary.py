@@ -165,6 +165,28 @@ def pmc_summary(paths, cus, xcds):
         fl = a.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", float("nan")) * 512 / 1e12
         short = k if len(k) <= 100 else k[:97] + "..."
         print(f"{cls:<11} {n:>5} {mb:>9.3f} {lu:>8.3f} {lc:>9.3f} {l2:>6.3f} {fl:>10.4f}  {short}")
+    issue = [r for r in rows if "SQ_WAVE_CYCLES" in r[4] and "SQ_INSTS_MFMA" in r[4]]
+    if issue:
+        # where a wave's cycles go: issuing (SQ_ACTIVE_INST_ANY), waiting on a counter or barrier
+        # (SQ_WAIT_ANY), waiting for an instruction to be issuable (SQ_WAIT_INST_ANY), as fractions
+        # of SQ_WAVE_CYCLES; and the instructions the waves executed per MFMA
+        print("\n# issue and waits per wave cycle; instructions per MFMA")
+        print(f"{'class':<11} {'issue':>6} {'wait':>6} {'wait_inst':>9} {'valu/mfma':>9} {'trans/mfma':>10} "
+              f"{'lds/mfma':>8}  kernel")
+        for cls, _, k, n, a in issue:
+            wc, mf = a["SQ_WAVE_CYCLES"], max(a["SQ_INSTS_MFMA"], 1.0)
+
+            def frac(c):
+                return a[c] / wc if c in a and wc > 0 else float("nan")
+
+            def per(c):
+                return a[c] / mf if c in a else float("nan")
+
+            valu = (a["SQ_INSTS_VALU"] - a["SQ_INSTS_MFMA"]) / mf if "SQ_INSTS_VALU" in a else float("nan")
+            short = k if len(k) <= 100 else k[:97] + "..."
+            print(f"{cls:<11} {frac('SQ_ACTIVE_INST_ANY'):>6.3f} {frac('SQ_WAIT_ANY'):>6.3f} "
+                  f"{frac('SQ_WAIT_INST_ANY'):>9.3f} {valu:>9.2f} {per('SQ_INSTS_VALU_TRANS_F32'):>10.2f} "
+                  f"{per('SQ_INSTS_LDS'):>8.2f}  {short}")
     print("\n# raw per-dispatch averages")
     for cls, _, k, n, a in rows:
         short = k if len(k) <= 100 else k[:97] + "..."
