@@ -1,4 +1,4 @@
-"""The reference-side shim of INTEGRATION.md (the block marked `shim:compile`) compiles, and the
+"""The reference-side shim of the integration guide (its block marked `shim:compile`) compiles, and the
 library's status codes keep the reference's ErrorCode numbering, so the shim can forward a
 code with a cast.
 
@@ -39,9 +39,10 @@ std::string str_cat(const Args&... args) { std::ostringstream os; (os << ... << 
 
 
 def shim_block():
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    guide = os.path.join(ROOT, "INTEGRATION.md")
+    text = open(guide).read()
     m = re.search(r"<!-- shim:compile -->\s*```cpp\n(.*?)```", text, re.S)
-    assert m, "INTEGRATION.md has no block marked shim:compile"
+    assert m, f"{guide} has no block marked shim:compile"
     return m.group(1)
 
 
