@@ -54,12 +54,15 @@ def _staged(transW, M, N, K, alpha, x, pd, sd, f16, G, beta, c0, R, out_t):
 
 
 # (transW, M, N, K, G, f16 scales, out type, epilogue): the 1B q/k/v forward, down and gate/up
-# input gradients (256x256 tiles), ragged M and N on 128x128 tiles, fp32 outputs, alpha / beta /
-# residual, groups of 64 and 256; fp32 scales take the staged route (the kernel reads fp16 ones)
+# input gradients (256x256 tiles), ragged M and N on 128x128 tiles and on 256x256 tiles (eight
+# waves; with the epilogue, and fp32 output), fp32 outputs, alpha / beta / residual, groups of 64
+# and 256; fp32 scales take the staged route (the kernel reads fp16 ones)
 CASES = [
     (1, 8192, 6144, 2048, 128, True, BF16, False),
     (0, 8192, 5632, 2048, 128, True, BF16, False),
     (0, 8192, 2048, 11264, 128, True, BF16, False),
+    (1, 8000, 4160, 1024, 128, True, BF16, True),
+    (0, 4100, 8192, 1024, 64, True, F32, True),
     (1, 1000, 1000, 512, 64, True, F32, True),
     (0, 520, 384, 640, 256, True, F32, True),
     (1, 2048, 2048, 2048, 128, True, BF16, True),
