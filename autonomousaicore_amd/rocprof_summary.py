@@ -50,6 +50,9 @@ _RULES = [
     (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+false, true|I(Li\d+E)+Lb0ELb1E)", "gemm_fwd"),
     (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+false, false|I(Li\d+E)+Lb0ELb0E)", "gemm_dgrad"),
     (r"gemm_bf16_dma(_grouped|_ragged|_pers)?(<(\d+, )+true, false|I(Li\d+E)+Lb1ELb0E)", "gemm_wgrad"),
+    # the K-split last round of an expert-ragged product, gemm_bf16_dma_rag_tail<transB>
+    (r"gemm_bf16_dma_rag_tail(<true>|ILb1E)", "gemm_fwd"),
+    (r"gemm_bf16_dma_rag_tail(<false>|ILb0E)", "gemm_dgrad"),
     (r"attn_fwd", "attn_fwd"),
     (r"attn_bwd|attn_dot", "attn_bwd"),
     (r"rmsnorm_fwd", "rmsnorm_fwd"),
@@ -73,13 +76,16 @@ _RULES = [
     (r"moe_", "moe_routing"),
     (r"int4_quantize", "other"),  # the base's one-time quantization at set-up, like the weight init
     (r"int4_", "int4"),
-    (r"splitk_reduce", "gemm_splitk_reduce"),
+    (r"splitk_reduce|rag_tail_reduce", "gemm_splitk_reduce"),
 ]
 
 
 # Classes timed as one event scope around several kernels: the kernel launched once per
 # scope, so per-launch figures here are per scope, as in bench.py.
 _ANCHOR = {
+    # an expert-ragged product's split last round runs in the same scope as its persistent launch
+    "gemm_fwd": r"gemm_bf16_dma(?!_rag_tail)",
+    "gemm_dgrad": r"gemm_bf16_dma(?!_rag_tail)",
     "attn_bwd": r"attn_bwd_dq",
     "rmsnorm_bwd": r"rmsnorm_bwd",
     "grad_norm": r"sqnorm_final",

@@ -19,6 +19,9 @@ SYMS = {
     "aic::hip::(anonymous namespace)::sqnorm_k(float const*, long, double*, int*)": "grad_norm",
     "void aic::hip::(anonymous namespace)::adamw_k<true>(float*)": "adamw",
     "aic::hip::(anonymous namespace)::splitk_reduce_k(x)": "gemm_splitk_reduce",
+    "void aic::hip::(anonymous namespace)::gemm_bf16_dma_rag_tail<true>(x)": "gemm_fwd",
+    "_ZN3aic3hip12_GLOBAL__N_122gemm_bf16_dma_rag_tailILb0EEEvNS1_12RaggedParamsEPfi": "gemm_dgrad",
+    "_ZN3aic3hip12_GLOBAL__N_117rag_tail_reduce_kENS1_12RaggedParamsEPKfii": "gemm_splitk_reduce",
     "__amd_rocclr_copyBuffer": "other",
 }
 
