@@ -131,6 +131,7 @@ SIGNATURES = {
     "aic_moe_ffn_routing": (i32, [vp, vp, vp, vp]),
     "aic_hip_int4_quantize": (i32, [vp, i64, i64, vp, vp, i32, vp]),
     "aic_hip_int4_dequantize": (i32, [vp, vp, i32, i64, i64, vp, i32, vp]),
+    "aic_hip_int4_dequantize_zp": (i32, [vp, vp, vp, i32, i64, i64, vp, vp]),
     "aic_hip_int4_gemm_rope": (i32, [i64, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, i64, i64, i64, vp, i64, i64,
                                       i64, i64, i64, vp, vp, vp]),
     "aic_hip_int4_dequant_gemm": (i32, [i32, i64, i64, i64, f32, vp, i64, vp, vp, i32, i64, f32, vp, i64, vp, i64,

@@ -842,6 +842,11 @@ int aic_hip_int4_dequantize(const uint8_t* packed, const void* scales, aic_dtype
     return guard([&] { aic::hip::int4_dequant(packed, scales, dt(scale_type), n, group, out, dt(out_type), st(stream)); });
 }
 
+int aic_hip_int4_dequantize_zp(const uint8_t* packed, const float* scales, const float* zero_points, int is_signed,
+                               int64_t n, int64_t group, float* out, aic_stream stream) {
+    return guard([&] { aic::hip::int4_dequant_zp(packed, scales, zero_points, is_signed != 0, n, group, out, st(stream)); });
+}
+
 int aic_hip_int4_dequant_gemm(int transW, int64_t M, int64_t N, int64_t K, float alpha, const void* X, int64_t ldx,
                               const uint8_t* Wq, const void* scales, aic_dtype scale_type, int64_t group, float beta,
                               void* C, int64_t ldc, const void* R, int64_t ldr, aic_dtype ab_type, aic_dtype c_type,

@@ -94,7 +94,37 @@ __global__ __launch_bounds__(256) void int4_dequant_k(const uint8_t* __restrict_
     }
 }
 
+// The CUDA launcher's general form (zero points, signed or unsigned nibbles; fp32 scales and
+// output): element i = (val - zp[i / G]) * s[i / G], G <= 0 meaning one group, any G (each
+// element finds its own group); eight elements (four bytes) per thread.
+__global__ __launch_bounds__(256) void int4_dequant_zp_k(const uint8_t* __restrict__ packed,
+                                                         const float* __restrict__ scales,
+                                                         const float* __restrict__ zp, bool is_signed, int64_t n,
+                                                         int64_t G, float* __restrict__ out) {
+    const int64_t i0 = 8 * (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x);
+    if (i0 >= n) return;
+    const int64_t e = i0 + 8 < n ? i0 + 8 : n;
+    for (int64_t i = i0; i < e; ++i) {
+        const unsigned b = packed[i / 2], u = (i & 1) ? (b >> 4) : (b & 0x0fu);
+        const float val = is_signed ? nibble_val(u) : static_cast<float>(u);
+        const int64_t g = G > 0 ? i / G : 0;
+        out[i] = (val - (zp ? zp[g] : 0.0f)) * scales[g];
+    }
+}
+
 }  // namespace
+
+void int4_dequant_zp(const uint8_t* packed, const float* scales, const float* zp, bool is_signed, int64_t n,
+                     int64_t G, float* out, hipStream_t s) {
+    AIC_CHECK(n >= 0, InvalidArgument, "int4_dequant_zp: negative element count");
+    if (n == 0) return;
+    AIC_CHECK(packed && scales && out, InvalidArgument, "int4_dequant_zp: null pointer");
+    const int64_t blocks = ((n + 7) / 8 + 255) / 256;
+    AIC_CHECK(blocks < (1LL << 31), InvalidArgument, "int4_dequant_zp: too many elements");
+    hipLaunchKernelGGL(int4_dequant_zp_k, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, packed, scales, zp,
+                       is_signed, n, G, out);
+    AIC_LAUNCH_CHECK("int4_dequant_zp");
+}
 
 int64_t int4_group(int64_t n, int64_t G) {
     AIC_CHECK(n >= 0, InvalidArgument, "int4: negative element count");

@@ -93,6 +93,10 @@ int64_t int4_group(int64_t n, int64_t G);
 void int4_quantize(const float* x, int64_t n, int64_t G, uint8_t* packed, void* scales, DType scale_t, hipStream_t s);
 void int4_dequant(const uint8_t* packed, const void* scales, DType scale_t, int64_t n, int64_t G, void* out, DType out_t,
                   hipStream_t s);
+// The CUDA launcher's general INT4 dequantization: zero points (or none), signed or unsigned
+// nibbles, fp32 scales and output, any group size (<= 0: one group).
+void int4_dequant_zp(const uint8_t* packed, const float* scales, const float* zp, bool is_signed, int64_t n,
+                     int64_t G, float* out, hipStream_t s);
 
 // Tensor primitives (tensor_ops.hip).  Views are (offset, rank <= 8, shape, strides) in elements;
 // binary ops broadcast NumPy-style into a contiguous output.  op codes: binary 0 add, 1 sub,

@@ -455,6 +455,15 @@ int aic_hip_int4_quantize(const float* x, int64_t n, int64_t group, uint8_t* pac
  * launch_dequantize_int4 (src/cuda/cuda_quantize.cuh; src/cuda/cuda_quantize.cu:141-159). */
 int aic_hip_int4_dequantize(const uint8_t* packed, const void* scales, aic_dtype scale_type, int64_t n, int64_t group,
                             void* out, aic_dtype out_type, aic_stream stream);
+/* The general INT4 dequantization of the CUDA launcher, argument for argument: element i is the
+ * low (even i) or high (odd i) nibble u of packed[i/2], read as 4-bit two's complement when
+ * is_signed (u - 16 for u >= 8) or as 0..15 otherwise; g = i / group (group <= 0: 0);
+ * out[i] = (val - zero_points[g]) * scales[g] in fp32 (zero_points NULL: 0).  Any group size,
+ * odd ones included.  fp32 scales, zero points and output.
+ * Replaces: launch_dequantize_int4 (src/cuda/cuda_quantize.cuh; src/cuda/cuda_quantize.cu:54-94,
+ * 141-159) for INT4_ASYMMETRIC and unsigned data (src/nn/quantization.cpp:374-379). */
+int aic_hip_int4_dequantize_zp(const uint8_t* packed, const float* scales, const float* zero_points, int is_signed,
+                               int64_t n, int64_t group, float* out, aic_stream stream);
 /* C[M,N] = alpha * X[M,K] . op(deq(Wq)) + beta * C + R with Wq an INT4 weight as above:
  * transW = 1: Wq holds W [N,K] and op(W) = W^T (forward y = x W^T); transW = 0: Wq holds W [K,N]
  * (input gradient dx = dy W).  With bf16 operands (ab_type AIC_BF16) in the shapes the GEMM

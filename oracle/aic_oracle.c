@@ -1573,6 +1573,23 @@ int orc_int4_dequantize(const uint8_t* packed, const void* scales, int scale_f16
     return 0;
 }
 
+/* The CUDA launcher's general INT4 dequantization (src/cuda/cuda_quantize.cu:54-94, 141-159): per
+ * element i, the nibble u (low nibble of byte i/2 for even i, high for odd), val = u - 16 when
+ * is_signed and u >= 8, else u; g = i / G (G <= 0: group 0); out = (val - zp[g]) * s[g] in fp32,
+ * zp = 0 without zero points.  Any G, odd ones included (each element finds its own group). */
+int orc_int4_dequantize_zp(const uint8_t* packed, const float* scales, const float* zp, int is_signed, int64_t n,
+                           int64_t G, float* out) {
+    if (n < 0) return 1;
+    for (int64_t i = 0; i < n; ++i) {
+        const unsigned b = packed[i / 2], u = (i & 1) ? ((b >> 4) & 0x0fu) : (b & 0x0fu);
+        const float val = (is_signed && u >= 8) ? (float)((int)u - 16) : (float)u;
+        const int64_t g = G > 0 ? i / G : 0;
+        const float z = zp ? zp[g] : 0.0f;
+        out[i] = (val - z) * scales[g];
+    }
+    return 0;
+}
+
 /* ======================================================================================
  * LoRA (src/nn/lora.cpp:31-108)
  * ====================================================================================== */

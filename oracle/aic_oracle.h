@@ -255,6 +255,10 @@ float orc_f16_to_f32(uint16_t h);
 int orc_int4_quantize(const float* x, int64_t n, int64_t G, int scale_f16, uint8_t* packed, void* scales);
 /* QuantizedTensor::dequantize (quantization.cpp:433-443): out[i] = q_i * s_{i/G}. */
 int orc_int4_dequantize(const uint8_t* packed, const void* scales, int scale_f16, int64_t n, int64_t G, float* out);
+/* launch_dequantize_int4 (src/cuda/cuda_quantize.cu:54-94): signed or unsigned nibbles, optional fp32 zero
+ * points, fp32 scales; out = (val - zp[g]) * s[g]. */
+int orc_int4_dequantize_zp(const uint8_t* packed, const float* scales, const float* zp, int is_signed, int64_t n,
+                           int64_t G, float* out);
 
 /* ---- LoRA (src/nn/lora.cpp) ---- */
 /* LoRALinear::forward (lora.cpp:75-93) on base weight W [out,in] (a Linear, or the dequantized

@@ -538,6 +538,20 @@ def int4_dequantize(packed, scales, n, G):
     return out
 
 
+def int4_dequantize_zp(packed, scales, zp, is_signed, n, G):
+    """orc_int4_dequantize_zp: float32 [n]; fp32 scales and zero points (zp None: none)."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zpa = None if zp is None else np.ascontiguousarray(zp, np.float32)
+    out = np.empty(n, np.float32)
+    rc = lib().orc_int4_dequantize_zp(packed.ctypes.data_as(C.c_void_p), _f(scales),
+                                      None if zpa is None else _f(zpa), C.c_int(1 if is_signed else 0),
+                                      C.c_int64(n), C.c_int64(G), _f(out))
+    if rc != 0:
+        raise ValueError(f"orc_int4_dequantize_zp failed with {rc}")
+    return out
+
+
 def lora_fwd(x, W, A, Bm, scaling, Bt, S):
     """orc_lora_fwd: x [Bt*S,in], W [out,in], A [r,in], Bm [out,r] -> y [Bt*S,out], xa [Bt*S,r]."""
     x, W, A, Bm = (np.ascontiguousarray(t, np.float32) for t in (x, W, A, Bm))

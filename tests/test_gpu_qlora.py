@@ -80,6 +80,25 @@ def test_int4_dequant_every_byte(orc):
         np.testing.assert_array_equal(got, orc.int4_dequantize(packed, scales, n, G))
 
 
+@pytest.mark.parametrize("is_signed", [True, False])
+@pytest.mark.parametrize("n,G,zp_kind", [(2047, 3, "int"), (4096, 0, "frac"), (1 << 20, 128, "int"),
+                                         (1001, 2000, "none"), (777, 7, "frac"), (1, 128, "int")])
+def test_int4_dequantize_zp_matches_oracle(orc, is_signed, n, G, zp_kind):
+    """aic_hip_int4_dequantize_zp (launch_dequantize_int4 with zero points or unsigned nibbles):
+    bit-exact against the oracle, odd and <= 0 group sizes, fractional zero points."""
+    print(f"int4 dequantize zp: n {n} G {G} zp {zp_kind} signed {is_signed}", flush=True)
+    rng = np.random.default_rng(n + G + is_signed)
+    packed = rng.integers(0, 256, (n + 1) // 2).astype(np.uint8)
+    ng = (n + G - 1) // G if G > 0 else 1
+    scales = rng.uniform(1e-3, 2.0, ng).astype(np.float32)
+    zp = {"none": None, "int": rng.integers(0, 16, ng).astype(np.float32),
+          "frac": rng.uniform(-2.0, 17.0, ng).astype(np.float32)}[zp_kind]
+    out = torch.full((n,), 7.0, dtype=torch.float32, device="cuda")
+    pd, sd, zd = dev(packed), dev(scales), (dev(zp) if zp is not None else None)  # alive through the call
+    call("aic_hip_int4_dequantize_zp", ptr(pd), ptr(sd), ptr(zd), 1 if is_signed else 0, n, G, ptr(out), stream())
+    np.testing.assert_array_equal(host(out), orc.int4_dequantize_zp(packed, scales, zp, is_signed, n, G))
+
+
 def _qweight(orc, rng, out, inn, G, f16, std=0.02):
     """An INT4 weight [out, in] quantized by the oracle: packed bytes and scales."""
     w = (rng.standard_normal((out, inn)) * std).astype(np.float32)

@@ -517,6 +517,43 @@ def test_int4_every_byte_decodes_to_its_two_nibbles(orc):
     np.testing.assert_array_equal(out[1::2], np.array([_NIBBLE[b >> 4] for b in range(256)], np.float32))
 
 
+def _int4_zp_numpy(packed, scales, zp, is_signed, n, G):
+    """The launcher's formula written independently: nibbles by shifts, sign by the xor-8 trick
+    ((u ^ 8) - 8), groups by integer division, fp32 arithmetic."""
+    b = np.asarray(packed, np.uint8).astype(np.int32)
+    u = np.empty(2 * b.size, np.int32)
+    u[0::2], u[1::2] = b & 15, b >> 4
+    u = u[:n]
+    val = ((u ^ 8) - 8) if is_signed else u
+    g = np.arange(n) // G if G > 0 else np.zeros(n, np.int64)
+    z = np.zeros(n, np.float32) if zp is None else np.asarray(zp, np.float32)[g]
+    return (val.astype(np.float32) - z) * np.asarray(scales, np.float32)[g]
+
+
+@pytest.mark.parametrize("is_signed", [True, False])
+@pytest.mark.parametrize("G,with_zp", [(3, True), (8, True), (0, True), (7, False), (600, True)])
+def test_int4_dequantize_zp_matches_the_launcher_formula(orc, is_signed, G, with_zp):
+    # every byte, an odd element count, odd and <= 0 group sizes (launch_dequantize_int4,
+    # src/cuda/cuda_quantize.cu:54-94: each element finds its own group; G <= 0 is group 0)
+    packed = np.tile(np.arange(256, dtype=np.uint8), 2)
+    n = 2 * packed.size - 1
+    ng = (n + G - 1) // G if G > 0 else 1
+    rng = np.random.default_rng(G + 2 * is_signed)
+    scales = rng.uniform(0.01, 2.0, ng).astype(np.float32)
+    zp = rng.integers(0, 16, ng).astype(np.float32) if with_zp else None
+    got = orc.int4_dequantize_zp(packed, scales, zp, is_signed, n, G)
+    np.testing.assert_array_equal(got, _int4_zp_numpy(packed, scales, zp, is_signed, n, G))
+
+
+def test_int4_dequantize_zp_signed_without_zero_points_is_the_symmetric_form(orc):
+    # INT4_SYMMETRIC goes through the same launcher with zp = nullptr (quantization.cpp:374-376)
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(1000) * 0.1).astype(np.float32)
+    packed, s = orc.int4_quantize(x, 64)
+    np.testing.assert_array_equal(orc.int4_dequantize_zp(packed, s, None, True, 1000, 64),
+                                  orc.int4_dequantize(packed, s, 1000, 64))
+
+
 def test_int4_known_bytes_and_exact_grid(orc):
     # a group whose absmax is 3.5 has s = 0.5 exactly, so x = q*s round-trips for q = -7..7
     q = np.arange(-7, 8, dtype=np.float32)
