@@ -263,50 +263,61 @@ __global__ __launch_bounds__(256, 2) void lora_skinny_k(SkinnyParams p) {
 }
 
 // The forward product alone (out1 = bf16(scale * Y W), one segment, W(n, j) = W[j w_j + n]: the
-// adapters' A [R, in]) without partial sums: a block owns 16 rows of Y and the whole width; wave
-// w takes the 256-column chunks w, w + 4, ...  Both MFMA operands come straight from global
-// memory in fragment layout -- a lane's 16 bytes of a Y row are one aligned quarter of a 64-byte
-// segment that the 16 lanes of its row group read together, A's from L2 -- so nothing is staged
-// in LDS; the four waves' partial tiles are added in LDS in wave order at the end.
+// adapters' A [R, in]) without partial sums: a block owns 32 rows of Y and the whole width; wave
+// w takes the 256-column chunks w, w + 8, ... for all 32 rows, as two 16-row MFMA tiles sharing
+// each A fragment.  Both MFMA operands come straight from global memory in fragment layout -- a
+// lane's 16 bytes of a Y row are one aligned quarter of a 64-byte segment that the 16 lanes of its
+// row group read together, A's from L2 -- so nothing is staged in LDS; the eight waves' partial
+// tiles are added in LDS in wave order at the end.
 template <int RB>
-__global__ __launch_bounds__(256) void lora_xa_k(SkinnyParams p) {
+__global__ __launch_bounds__(512) void lora_xa_k(SkinnyParams p) {
     constexpr int R = 16 * RB;
-    __shared__ float red[4][16][R];
+    __shared__ float red[8][32][R];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, i = lane & 15;
-    const int t0 = blockIdx.x * 16;
-    const bool row_ok = t0 + i < p.T;
-    const bf16* yrow = p.Y + (int64_t)(row_ok ? t0 + i : 0) * p.ldy + 8 * g;
+    const int t0 = blockIdx.x * 32;
+    const bool ok0 = t0 + i < p.T, ok1 = t0 + 16 + i < p.T;
+    const bf16* y0 = p.Y + (int64_t)(ok0 ? t0 + i : 0) * p.ldy + 8 * g;
+    const bf16* y1 = p.Y + (int64_t)(ok1 ? t0 + 16 + i : 0) * p.ldy + 8 * g;
     const bf16* wcol[RB];
 #pragma unroll
     for (int cb = 0; cb < RB; ++cb) wcol[cb] = p.W + (int64_t)(16 * cb + i) * p.w_j + 8 * g;
-    f32x4 acc[RB];
+    f32x4 acc0[RB], acc1[RB];
 #pragma unroll
-    for (int cb = 0; cb < RB; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < RB; ++cb) acc0[cb] = acc1[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int chunks = p.N / kChunk;
-    for (int c = w; c < chunks; c += 4) {
+    for (int c = w; c < chunks; c += 8) {
         const int n0 = c * kChunk;
-        bf16x8 a[8], b[8][RB];
+        bf16x8 a0[8], a1[8], b[8][RB];
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            a[ks] = row_ok ? *reinterpret_cast<const bf16x8*>(yrow + n0 + 32 * ks) : bf16x8{};
+            a0[ks] = ok0 ? *reinterpret_cast<const bf16x8*>(y0 + n0 + 32 * ks) : bf16x8{};
+            a1[ks] = ok1 ? *reinterpret_cast<const bf16x8*>(y1 + n0 + 32 * ks) : bf16x8{};
 #pragma unroll
             for (int cb = 0; cb < RB; ++cb) b[ks][cb] = *reinterpret_cast<const bf16x8*>(wcol[cb] + n0 + 32 * ks);
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-            for (int cb = 0; cb < RB; ++cb) acc[cb] = mfma16(a[ks], b[ks][cb], acc[cb]);
+            for (int cb = 0; cb < RB; ++cb) {
+                acc0[cb] = mfma16(a0[ks], b[ks][cb], acc0[cb]);
+                acc1[cb] = mfma16(a1[ks], b[ks][cb], acc1[cb]);
+            }
     }
     // D of a 16x16 tile: lane (g, i) holds rows 4 g + v, column i
 #pragma unroll
     for (int cb = 0; cb < RB; ++cb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[w][4 * g + v][16 * cb + i] = acc[cb][v];
+        for (int v = 0; v < 4; ++v) {
+            red[w][4 * g + v][16 * cb + i] = acc0[cb][v];
+            red[w][16 + 4 * g + v][16 * cb + i] = acc1[cb][v];
+        }
     __syncthreads();
-    for (int e = tid; e < 16 * R; e += 256) {
+    for (int e = tid; e < 32 * R; e += 512) {
         const int row = e / R, j = e % R;
         if (t0 + row < p.T) {
-            const float sum = ((red[0][row][j] + red[1][row][j]) + red[2][row][j]) + red[3][row][j];
+            float sum = red[0][row][j];
+#pragma unroll
+            for (int k = 1; k < 8; ++k) sum += red[k][row][j];
             p.out1[(int64_t)(t0 + row) * p.ldo1 + j] = f2bf(p.scale * sum);
         }
     }
@@ -426,11 +437,11 @@ void lora_skinny(const LoraSkinny& q, hipStream_t s) {
     p.accumulate = q.accumulate ? 1 : 0;
     const int64_t sub_rows = (q.T + kSub - 1) / kSub;
     if (p1 && !p2 && q.w_n == 1 && q.n_seg == q.N) {
-        // the forward x A^T: 16 rows per block, no partial sums
-        const dim3 grid(static_cast<unsigned>((q.T + 15) / 16));
-        if (RB == 1) hipLaunchKernelGGL((lora_xa_k<1>), grid, dim3(256), 0, s, p);
-        else if (RB == 2) hipLaunchKernelGGL((lora_xa_k<2>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((lora_xa_k<3>), grid, dim3(256), 0, s, p);
+        // the forward x A^T: 32 rows per block, no partial sums
+        const dim3 grid(static_cast<unsigned>((q.T + 31) / 32));
+        if (RB == 1) hipLaunchKernelGGL((lora_xa_k<1>), grid, dim3(512), 0, s, p);
+        else if (RB == 2) hipLaunchKernelGGL((lora_xa_k<2>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((lora_xa_k<3>), grid, dim3(512), 0, s, p);
         AIC_LAUNCH_CHECK("lora_xa");
         return;
     }
