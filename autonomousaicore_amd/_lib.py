@@ -119,6 +119,7 @@ SIGNATURES = {
                                   i32, f32, f32, f32, f32, f32, i64, vp, vp]),
     "aic_hip_adamw_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, vp]),
     "aic_hip_cast_f32_bf16": (i32, [vp, vp, i64, vp]),
+    "aic_hip_stream_probe": (i32, [C.POINTER(vp), i32, C.POINTER(vp), i32, vp, vp, i64, i32, vp]),
     "aic_hip_moe_route": (i32, [vp, i64, i64, i64, f32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "aic_hip_moe_max_rows": (i64, [i64, i64, i64]),
     "aic_hip_moe_permute": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp]),

@@ -495,6 +495,11 @@ int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream str
     return guard([&] { aic::hip::cast_f32_bf16(src, dst, n, st(stream)); });
 }
 
+int aic_hip_stream_probe(const float* const* in, int n_in, float* const* out, int n_out, void* out_bf16, float* sink,
+                         int64_t n, int nontemporal, aic_stream stream) {
+    return guard([&] { aic::hip::stream_probe(in, n_in, out, n_out, out_bf16, sink, n, nontemporal != 0, st(stream)); });
+}
+
 // ------------------------------------------------------------------ TransformerLM
 int aic_lm_create(const aic_lm_config* cfg, const aic_train_config* tcfg, aic_lm** out) {
     return guard([&] {

@@ -165,6 +165,10 @@ void adamw_multi(float* const* p, const float* const* g, float* const* m, float*
 void adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
                 float wd, float bc1, float bc2, hipStream_t s);
 void cast_f32_bf16(const float* src, void* dst, int64_t n, hipStream_t s);
+// Streaming probe (no reference counterpart): out_j = sum(in) + j, out_bf16 = bf16(sum(in)) over
+// n fp32 elements, in the form of adamw_k; mixes: 1r, 1w, 1r1w, 2r1w, 4r3w + bf16.
+void stream_probe(const float* const* in, int n_in, float* const* out, int n_out, void* out_bf16, float* sink,
+                  int64_t n, bool nontemporal, hipStream_t s);
 // Appends {step, loss, aux, grad_norm, loss scale, found_inf} (an aic_step_record) to a device
 // ring of cap records; *count (device) counts all records ever appended.
 void step_record(const float* loss, const float* aux, const void* ctl, const float* scale_used, void* ring,

@@ -14,6 +14,10 @@ The streaming ceiling: torch's own device kernels over 2 GiB buffers -- copy (re
 sum (read), fill (write) and add_ (2 reads + 1 write) -- timed the same way, in GB/s of
 algorithmic bytes.  It is what a plain streaming kernel reaches on this GPU, the practical
 ceiling for the HBM-bound classes (the MI355X's published 8 TB/s is the roofline peak).
+Beside it, the library's own streaming probe (aic_hip_stream_probe: one pass in the AdamW
+kernel's form, plain and non-temporal accesses) over the same buffers for the read, write,
+copy, add and AdamW byte mixes (4 fp32 reads, 3 fp32 writes and a bf16 copy per element), and
+the AdamW kernel itself (aic_hip_adamw_multi with the bf16 copy) over that many elements.
 """
 from __future__ import annotations
 
@@ -131,18 +135,86 @@ def stream_ceiling(reps, rounds, gib=2):
     return out
 
 
+def probe_ceiling(reps, rounds, gib=2):
+    import ctypes as C
+
+    lib = _lib.load()
+    n = gib * (1 << 30) // 4
+    ins = [torch.full((n,), 1.0 + k, dtype=torch.float32, device="cuda") for k in range(4)]
+    outs = [torch.empty(n, dtype=torch.float32, device="cuda") for _ in range(3)]
+    ob = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    sink = torch.empty(1, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    vp = C.c_void_p
+    mixes = [("read", 1, 0, False), ("write", 0, 1, False), ("copy (read + write)", 1, 1, False),
+             ("add (2 reads + 1 write)", 2, 1, False), ("AdamW mix (4r + 3w + bf16)", 4, 3, True)]
+    out = []
+    for name, ni, no, b16 in mixes:
+        for nt in (0, 1):
+            pin = (vp * 4)(*[t.data_ptr() for t in ins])
+            pout = (vp * 3)(*[t.data_ptr() for t in outs])
+
+            def fn(ni=ni, no=no, b16=b16, nt=nt, pin=pin, pout=pout):
+                _lib.check(lib.aic_hip_stream_probe(pin, ni, pout, no, ob.data_ptr() if b16 else None,
+                                                    sink.data_ptr(), n, nt, s.cuda_stream))
+
+            fn()
+            torch.cuda.synchronize()
+            if no:  # the probe's result on a prefix: out_j = sum of the inputs + j
+                want = sum(float(1 + k) for k in range(ni)) + (no - 1)
+                assert bool((outs[no - 1][:1 << 20] == want).all()), name
+            t = min(_time(fn, reps, s) for _ in range(rounds))
+            bytes_ = n * (4 * ni + 4 * no + (2 if b16 else 0))
+            out.append(dict(kernel=f"{name}, {'non-temporal' if nt else 'plain'}", bytes=int(bytes_), ms=round(t, 4),
+                            gbs=round(bytes_ / (t * 1e-3) / 1e9, 1)))
+    # the AdamW kernel itself over the same element count (4 reads, 3 writes, bf16 copy)
+    p, g, m, v = (t.clone() for t in ins)
+    arr = lambda t: (vp * 1)(t.data_ptr())
+    sizes = (C.c_int64 * 1)(n)
+    ap, ag, am, av, ab = arr(p), arr(g), arr(m), arr(v), (vp * 1)(ob.data_ptr())
+
+    def adam():
+        _lib.check(lib.aic_hip_adamw_multi(ap, ag, am, av, ab, sizes, 1, 1e-4, 0.9, 0.95, 1e-8, 0.1, 1, None,
+                                           s.cuda_stream))
+
+    adam()
+    torch.cuda.synchronize()
+    t = min(_time(adam, reps, s) for _ in range(rounds))
+    bytes_ = n * 30
+    out.append(dict(kernel="AdamW kernel (adamw_k)", bytes=int(bytes_), ms=round(t, 4),
+                    gbs=round(bytes_ / (t * 1e-3) / 1e9, 1)))
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", default="1b", choices=sorted(CONFIGS))
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--rounds", type=int, default=3)
     ap.add_argument("--json", help="also write the rows to this file")
+    ap.add_argument("--stream-only", action="store_true", help="only the streaming ceilings (no GEMM table)")
     args = ap.parse_args(argv)
     torch.cuda.set_device(0)
     blas = getattr(torch.backends.cuda, "preferred_blas_library", lambda: "unknown")()
     print(f"# {torch.cuda.get_device_name(0)}, torch {torch.__version__}, preferred BLAS {blas}; "
           f"config {args.config} {CONFIGS[args.config]}; best of {args.rounds} rounds of {args.reps} launches")
-    rows = gemm_table(CONFIGS[args.config], args.reps, args.rounds)
+    rows = [] if args.stream_only else gemm_table(CONFIGS[args.config], args.reps, args.rounds)
+    if rows:
+        print_gemm(rows)
+    st = stream_ceiling(args.reps, args.rounds)
+    print("\n# HBM streaming ceiling (torch device kernels over 2 GiB fp32 buffers; algorithmic bytes)")
+    for r in st:
+        print(f"{r['kernel']:<26} {r['ms']:>8.3f} ms {r['gbs']:>8.1f} GB/s  ({r['gbs'] / 8000:.3f} of 8 TB/s)")
+    pr = probe_ceiling(args.reps, args.rounds)
+    print("\n# the library's streaming probe (aic_hip_stream_probe, 2 GiB per fp32 buffer; algorithmic bytes)")
+    for r in pr:
+        print(f"{r['kernel']:<42} {r['ms']:>8.3f} ms {r['gbs']:>8.1f} GB/s  ({r['gbs'] / 8000:.3f} of 8 TB/s)")
+    if args.json:
+        with open(args.json, "w") as fh:
+            json.dump({"gemm": rows, "stream": st, "probe": pr}, fh)
+
+
+def print_gemm(rows):
     print(f"{'product':<8} {'kind':<6} {'M':>6} {'N':>6} {'K':>6} {'ours_us':>8} {'TFLOP/s':>8} {'frac':>6} "
           f"{'lib_us':>8} {'TFLOP/s':>8} {'frac':>6} {'ours/lib':>8}")
     for r in rows:
@@ -153,13 +225,6 @@ def main(argv=None):
     tot_o = sum(r["ours_us"] for r in rows)
     tot_l = sum(r["lib_us"] for r in rows)
     print(f"sum over the table: ours {tot_o / 1e3:.3f} ms, library {tot_l / 1e3:.3f} ms")
-    st = stream_ceiling(args.reps, args.rounds)
-    print("\n# HBM streaming ceiling (torch device kernels over 2 GiB fp32 buffers; algorithmic bytes)")
-    for r in st:
-        print(f"{r['kernel']:<26} {r['ms']:>8.3f} ms {r['gbs']:>8.1f} GB/s  ({r['gbs'] / 8000:.3f} of 8 TB/s)")
-    if args.json:
-        with open(args.json, "w") as fh:
-            json.dump({"gemm": rows, "stream": st}, fh)
 
 
 if __name__ == "__main__":

@@ -390,6 +390,16 @@ int aic_hip_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, 
 /* fp32 -> bf16 (round to nearest even) copy of n elements. */
 int aic_hip_cast_f32_bf16(const float* src, void* dst, int64_t n, aic_stream stream);
 
+/* Streaming probe over n fp32 elements (n a multiple of 4; fp32 buffers 16-byte aligned):
+ *   out[j][i] = sum_k in[k][i] + j  (j < n_out),  out_bf16[i] = bf16(sum_k in[k][i])  (nullable);
+ * with no output at all, sink[0] may receive 0.  One pass in the form of the AdamW kernel (two
+ * float4 groups per thread, grid-stride), plain or non-temporal accesses.  Mixes: (n_in, n_out,
+ * bf16) = (1,0,no) read, (0,1,no) write, (1,1,no) copy, (2,1,no) add, (4,3,yes) AdamW's bytes.
+ * No counterpart in the reference: it measures the HBM rate the bandwidth-bound kernels are
+ * judged against. */
+int aic_hip_stream_probe(const float* const* in, int n_in, float* const* out, int n_out, void* out_bf16, float* sink,
+                         int64_t n, int nontemporal, aic_stream stream);
+
 /* ---------------------------------------------------------------- mixture of experts */
 /* Routing on fp32 gate logits [T,E] (E <= 64, top_k <= min(E, 8)): probs = softmax(logits)
  * [T,E]; idx [T,k] = the k largest logits per token, descending, ties to the lower expert

@@ -821,3 +821,41 @@ def test_gemm_grouped(ta, tb, shapes):
     call("aic_hip_gemm_grouped", len(descs), arr, 0.5, 0.0, BF16, F32, stream())
     for c, f in zip(outs, first):
         np.testing.assert_array_equal(host(c), f)
+
+
+# ----------------------------------------------------------------------------- streaming probe
+@pytest.mark.parametrize("ni,no,b16", [(1, 0, False), (0, 1, False), (1, 1, False), (2, 1, False), (4, 3, True)])
+@pytest.mark.parametrize("nt", [0, 1])
+def test_stream_probe(ni, no, b16, nt):
+    """The probe computes what it states (out_j = sum of inputs + j, bf16 copy of the sum) over
+    a length that leaves a partial last iteration, so its rates are those of real work."""
+    import ctypes as C
+
+    n = 3 * 256 * 8 + 4 * 37
+    rng = np.random.default_rng(ni * 10 + no + nt)
+    xs = [rng.standard_normal(n).astype(np.float32) for _ in range(ni)]
+    ins = [dev(x, torch.float32) for x in xs]
+    outs = [torch.full((n,), 7.0, device="cuda") for _ in range(3)]
+    ob = torch.zeros(n, dtype=torch.bfloat16, device="cuda") if b16 else None
+    sink = torch.full((1,), 5.0, device="cuda")
+    vp = C.c_void_p
+    pin = (vp * 4)(*([ptr(t) for t in ins] + [None] * (4 - ni)))
+    pout = (vp * 3)(*[ptr(t) for t in outs])
+    call("aic_hip_stream_probe", pin, ni, pout, no, ptr(ob), ptr(sink), n, nt, stream())
+    torch.cuda.synchronize()
+    s = np.zeros(n, np.float32)
+    for x in xs:
+        s = s + x  # the kernel's order: ((x0 + x1) + x2) + x3 in fp32
+    for j in range(3):
+        if j < no:
+            np.testing.assert_array_equal(host(outs[j]), s + np.float32(j))
+        else:
+            assert bool((outs[j] == 7.0).all())
+    if b16:
+        np.testing.assert_array_equal(host(ob.float()), bf16_round(s))
+    if no == 0 and not b16:
+        assert float(sink[0]) == 5.0  # random inputs: no zero sums, so the sink is untouched
+    with pytest.raises(_lib.AicError):  # a length that is not a multiple of 4
+        call("aic_hip_stream_probe", pin, ni, pout, no, ptr(ob), ptr(sink), n - 2, nt, stream())
+    with pytest.raises(_lib.AicError):  # a mix the probe does not provide
+        call("aic_hip_stream_probe", pin, 3, pout, 1, None, ptr(sink), n, nt, stream())
